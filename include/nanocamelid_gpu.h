@@ -1,0 +1,222 @@
+/*
+ * nanocamelid_gpu.h -- C ABI of the MI355X speculative-decoding verify path.
+ *
+ * One shared library, libnanocamelid_hip.so, built with hipcc for gfx950.
+ * Plain pointers and sizes only; opaque handles; every function returns an int
+ * status (NC_OK = 0, negative on error) and never aborts.  nc_last_error()
+ * returns the thread-local message of the last failure.  The library is meant to
+ * be bound from the reference's Rust host through a thin `-sys` crate; every
+ * entry point cites the reference interface it replaces (paths relative to the
+ * reference repository root).
+ *
+ * Ownership: host buffers are borrowed for the duration of a call.  Device
+ * memory (weights, KV cache, workspaces) is owned by model/session handles and
+ * released by the matching *_free.  A model is immutable after load and may be
+ * shared read-only by sessions; a session is used by one host thread at a time
+ * and owns one HIP stream.  Steps allocate nothing.
+ */
+#ifndef NANOCAMELID_GPU_H
+#define NANOCAMELID_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status codes */
+#define NC_OK 0
+#define NC_EINVAL (-1)  /* bad argument (shape, null pointer, unsupported format) */
+#define NC_ENOMEM (-2)  /* device or host allocation failed */
+#define NC_EHIP (-3)    /* a HIP runtime call failed */
+#define NC_EFORMAT (-4) /* malformed or unsupported GGUF */
+#define NC_ERANGE (-5)  /* batch/context bounds (inference.rs:3712-3722 asserts) */
+
+/* GGUF tensor type ids used by this path (gguf.rs:83-115). */
+#define NC_TYPE_F32 0
+#define NC_TYPE_Q4_0 2
+#define NC_TYPE_Q4_K 12
+
+typedef struct nc_ctx nc_ctx;         /* device context: device id, default stream */
+typedef struct nc_qmat nc_qmat;       /* device-resident repacked quantized matrix */
+typedef struct nc_model nc_model;     /* device-resident Llama weights */
+typedef struct nc_session nc_session; /* KV cache + workspaces + stream of one sequence */
+
+/* Thread-local message for the last non-zero status returned on this thread. */
+const char* nc_last_error(void);
+/* Library version string. */
+const char* nc_version(void);
+
+/* ---------------------------------------------------------------- context */
+/* Opens device `device` (HIP ordinal).  No reference counterpart: the reference
+ * is CPU-only; this is the device handle the Rust `-sys` crate holds. */
+int nc_ctx_create(int device, nc_ctx** out);
+void nc_ctx_free(nc_ctx* ctx);
+/* Blocks until all work queued on the context's default stream finished. */
+int nc_ctx_synchronize(nc_ctx* ctx);
+
+/* ---------------------------------------------------------------- operator boundary */
+/* Uploads a row-major GGUF quantized matrix (rows x cols, GGUF dims [cols, rows])
+ * and repacks it into the device layout.  Replaces the load-time matrix
+ * construction load_q4_0_matrix / decode_q4_k_blocks (src/model.rs:1369-1401,
+ * src/model.rs:1270) that feeds QuantizedMatrix (src/model.rs:294-310).
+ * type: NC_TYPE_Q4_0 or NC_TYPE_Q4_K.  cols % 32 == 0 (Q4_K: % 256). */
+int nc_qmat_upload(nc_ctx* ctx, int type, int64_t rows, int64_t cols, const void* gguf_blocks_host,
+                   nc_qmat** out);
+void nc_qmat_free(nc_qmat* w);
+/* Bytes of the repacked device copy (algorithmic bytes of the weight stream). */
+int64_t nc_qmat_device_bytes(const nc_qmat* w);
+
+/* out[t][r] = sum_b ((w_scale[r][b] * x_scales[t][b]) * dot_i32(w[r][b], x[t][b])), the sum
+ * taken in block order b = 0, 1, ... in f32 exactly as the reference's per-row loop.
+ * Replaces matmul_quantized_batch (src/inference.rs:1246-1303) and, for batch_size 1,
+ * matmul_quantized (src/inference.rs:1201-1244).  All pointers are device pointers:
+ * x_i8 [batch][cols] int8, x_scales [batch][cols/32] f32, out [batch][rows] f32
+ * (token-major, as write_batch_out src/inference.rs:1333-1341).  batch_size 1..16.
+ * stream: a hipStream_t or NULL for the context's default stream. */
+int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, const float* x_scales,
+                              float* out, int batch_size, int64_t rows, int64_t cols, void* stream);
+/* Debug/parity variant: writes the int32 per-block dot products (Q4_0:
+ * sum (nib-8)*x per 32-block, q8.rs:2699; Q4_K: W_j = sum nib*x per 32-sub-block,
+ * q8.rs:1339-1376) as dots[t][r][cols/32] (device pointer). */
+int nc_matmul_blockdots(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, int32_t* dots, int batch_size,
+                        int64_t rows, int64_t cols, void* stream);
+/* Per-32-block Q8_0 activation quantiser: scale = amax/127 (f32), q = round-half-away
+ * (x * (1/scale)) clamped to +-127.  Replaces quantize_f32_to_q8_0_batch
+ * (src/inference.rs:967-989, scalar path :991-1029).  Device pointers. */
+int nc_quantize_q8_0_batch(nc_ctx* ctx, const float* x, int8_t* x_i8, float* x_scales, int batch_size,
+                           int64_t dim, void* stream);
+
+/* ---------------------------------------------------------------- model */
+typedef struct nc_model_config {
+    int64_t context_length, embedding_length, block_count, feed_forward_length;
+    int64_t head_count, head_count_kv, head_dim, rope_dimension_count, vocab_size;
+    int64_t attention_output_width, kv_width;
+    int32_t weight_type;  /* NC_TYPE_Q4_0 or NC_TYPE_Q4_K */
+    int32_t tied_head;    /* 1 when the head was requantised from token_embd */
+    float rope_freq_base, rms_norm_epsilon;
+    int64_t device_weight_bytes; /* repacked matrices incl. head */
+    int64_t verify_weight_bytes; /* algorithmic weight bytes streamed by one verify pass */
+} nc_model_config;
+
+typedef struct nc_load_opts {
+    int32_t nthreads;     /* host threads for dequant/requant/repack (0 = all cores) */
+    int32_t reserved[7];
+} nc_load_opts;
+
+/* Parses a GGUF file / in-memory image, builds LlamaModelConfig and uploads the
+ * weights.  Replaces gguf::read_file (src/gguf.rs:454-551),
+ * LlamaModelConfig::from_gguf (src/model.rs:48-186) and LlamaWeights::load
+ * (src/model.rs:461-545), including the tied-head Q4_0 requantisation
+ * (src/q8.rs:2442-2488).  opts may be NULL. */
+int nc_model_load_gguf(nc_ctx* ctx, const char* path, const nc_load_opts* opts, nc_model** out);
+int nc_model_load_gguf_memory(nc_ctx* ctx, const void* data, size_t size, const nc_load_opts* opts,
+                              nc_model** out);
+int nc_model_get_config(const nc_model* m, nc_model_config* out);
+void nc_model_free(nc_model* m);
+
+/* ---------------------------------------------------------------- session */
+/* KV cache [layers][kv_heads][max_ctx][head_dim] f32 plus batch workspaces for up to
+ * max_batch rows.  Replaces LlamaKvCache::new + LlamaWorkspace/LlamaBatchWorkspace
+ * (src/inference.rs:505-695).  max_batch 1..16. */
+int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_session** out);
+void nc_session_free(nc_session* s);
+
+/* Batched forward of n tokens at positions start_pos.. (KV written for every row),
+ * final hidden rows kept for nc_session_logits.  Replaces prefill_pass_batch
+ * (src/inference.rs:3695-3744); n > max_batch is processed in max_batch chunks as
+ * prefill_tokens does (src/main.rs:9415-9485).  Also computes every row's logits
+ * and greedy prediction when want_logits != 0. */
+int nc_prefill(nc_session* s, const uint32_t* toks, int32_t n, int64_t start_pos, int32_t want_logits);
+/* Single-token forward (src/inference.rs:3649-3670 forward_pass).  logits_host may be
+ * NULL; *pred_out (nullable) receives argmax (first max wins, inference.rs:4836-4846). */
+int nc_forward1(nc_session* s, uint32_t tok, int64_t pos, float* logits_host, uint32_t* pred_out);
+
+typedef struct nc_verify_result {
+    int32_t n_accepted; /* drafts accepted (longest matching prefix) */
+    uint32_t next_token; /* the target's token after the accepted prefix */
+    int64_t new_pos;     /* start_pos + n_accepted + 1 */
+} nc_verify_result;
+
+/* k+1 greedy verify: toks[0] = the pending token at start_pos, toks[1..n) = drafts.
+ * One batched forward, per-row head + argmax, and acceptance, all on the device; only
+ * the result struct returns to the host.  KV rows past new_pos are dead (implicit
+ * rollback, src/speculative.rs:184-187).  Semantics of cluster_tcp_smoke.rs:905-979 /
+ * ngram_speculative_step (src/speculative.rs:122-286).  preds_host (nullable) receives
+ * the n per-row predictions. */
+int nc_verify_greedy(nc_session* s, const uint32_t* toks, int32_t n, int64_t start_pos,
+                     nc_verify_result* result, uint32_t* preds_host);
+/* Copies row `row` of the last pass's logits ([vocab] f32) to host
+ * (compute_logits_from_hidden, src/inference.rs:4783-4832). */
+int nc_session_logits(nc_session* s, int32_t row, float* logits_host);
+/* Copies the last pass's final hidden rows ([n][d] f32, before the output norm). */
+int nc_session_hidden(nc_session* s, int32_t n, float* hidden_host);
+
+/* ---------------------------------------------------------------- decode loops */
+typedef struct nc_decode_stats {
+    int64_t steps, drafted, accepted, emitted;
+    double decode_seconds; /* wall time of the decode loop (prefill excluded) */
+    double prefill_seconds;
+} nc_decode_stats;
+
+/* Plain greedy decode: prompt prefill (prefix in max_batch chunks, last token single)
+ * then n_new greedy tokens.  Mirrors the plain loop of src/main.rs:9676-9706. */
+int nc_generate_greedy(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new,
+                       uint32_t* out, nc_decode_stats* stats);
+
+/* k+1 speculative decode with the seeded oracle drafter (no reference counterpart;
+ * the drafter exists only for the benchmark configs): the draft for absolute
+ * position p copies greedy[p - n_prompt] (greedy = the target's recorded greedy
+ * continuation, n_greedy tokens) when philox_u(seed, p) < alpha, else a philox
+ * uniform id.  Emits the target's greedy stream.  Stops after n_new tokens or
+ * max_steps verify steps (max_steps <= 0: no step bound). */
+int nc_generate_speculative_oracle(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new,
+                                   int32_t max_steps, int32_t k, float alpha, uint64_t seed,
+                                   const uint32_t* greedy, int32_t n_greedy, uint32_t* out,
+                                   nc_decode_stats* stats);
+
+/* Draft-model speculative decode, greedy, as speculative_decoding_step
+ * (src/speculative.rs:299-494) driven by the generate loop (src/main.rs:9799-9870):
+ * k draft forwards, one k-row target verify, acceptance against the live target
+ * prediction, then a corrective/bonus single-token forward on both models. */
+int nc_generate_speculative_draft(nc_session* target, nc_session* draft, const uint32_t* prompt,
+                                  int32_t n_prompt, int32_t n_new, int32_t draft_k, uint32_t* out,
+                                  nc_decode_stats* stats);
+
+/* ---------------------------------------------------------------- synthetic models */
+typedef struct nc_synth_spec {
+    int32_t layers, embedding_length, head_count, head_count_kv, feed_forward_length, vocab_size;
+    int32_t context_length;
+    int32_t weight_type; /* NC_TYPE_Q4_0 or NC_TYPE_Q4_K for layer matrices and token_embd */
+    int32_t tied;        /* 1: no output.weight (head requantised at load) */
+    int32_t norm_mode;   /* 0: norm weights 1.0; 1: N(1, 0.1) */
+    float rope_freq_base, rms_norm_epsilon, weight_std;
+    uint64_t seed;
+} nc_synth_spec;
+
+/* Size in bytes of the GGUF v3 image nc_synth_write would produce. */
+int nc_synth_size(const nc_synth_spec* spec, uint64_t* size_out);
+/* Writes a seeded random-init Llama GGUF v3 image (alignment 32): weights drawn from
+ * N(0, weight_std) with a Philox4x32-10 counter stream and Box-Muller, quantised to
+ * Q4_0 (llama.cpp rule: d = max/-8, round-to-nearest-even f16 scale) or Q4_K.
+ * Deterministic for a given spec regardless of nthreads. */
+int nc_synth_write(const nc_synth_spec* spec, void* dst, uint64_t size, int32_t nthreads);
+
+/* Philox4x32-10 helpers shared by the drafter and the synthetic prompt.
+ * ids[i] = philox(seed, i, purpose 4).x mod vocab. */
+int nc_uniform_prompt(uint64_t seed, int64_t n, uint32_t vocab, uint32_t* ids);
+uint32_t nc_oracle_draft(uint64_t seed, int64_t p, float alpha, const uint32_t* greedy, int64_t n_prompt,
+                         int64_t n_greedy, uint32_t vocab);
+
+/* ---------------------------------------------------------------- timing hooks */
+/* Average device time (ms) per launch of the named kernel family recorded with HIP
+ * events on the session stream since the last reset; used by the benchmark's
+ * roofline.  family: "gemm_q4_0" (all verify matmuls).  Returns launches counted. */
+int64_t nc_session_kernel_timing(nc_session* s, const char* family, double* total_ms, int64_t* bytes);
+int nc_session_timing_enable(nc_session* s, int32_t enable);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

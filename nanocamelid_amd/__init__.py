@@ -1,0 +1,273 @@
+"""nanocamelid_amd: MI355X-native speculative-decoding verify path.
+
+Python mirror of the reference's operator and step interface over the C ABI of
+libnanocamelid_hip.so.  Names follow the reference:
+
+* ``matmul_quantized_batch``   -- src/inference.rs:1246 (device tensors in, device tensor out)
+* ``quantize_f32_to_q8_0_batch`` -- src/inference.rs:967
+* ``Model`` / ``Session``       -- LlamaWeights::load (src/model.rs:461) + LlamaKvCache /
+  workspaces (src/inference.rs:505-695)
+* ``Session.prefill_pass_batch`` -- src/inference.rs:3695
+* ``Session.forward_pass``       -- src/inference.rs:3649
+* ``Session.verify_greedy``      -- the k+1 verify of src/speculative.rs:122-286
+* ``generate_speculative_draft`` -- speculative_decoding_step, src/speculative.rs:299-494
+
+Everything runs in the native library on the GPU; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._ffi import (NC_TYPE_Q4_0, NC_TYPE_Q4_K, DecodeStats, LoadOpts, ModelConfig, NcError, SynthSpec,
+                   VerifyResult, check, lib)
+
+__all__ = ["Context", "QMat", "Model", "Session", "matmul_quantized_batch", "matmul_blockdots",
+           "quantize_f32_to_q8_0_batch", "synth_gguf", "uniform_prompt", "oracle_draft",
+           "generate_speculative_draft", "NcError", "NC_TYPE_Q4_0", "NC_TYPE_Q4_K", "SYNTH_CONFIGS"]
+
+
+def _u32(a):
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    return a, a.ctypes.data_as(C.POINTER(C.c_uint32))
+
+
+def _stream_of(t):
+    import torch
+    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+class Context:
+    """Device context (nc_ctx)."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        check(lib().nc_ctx_create(device, C.byref(h)))
+        self.h = h
+        self.device = device
+
+    def synchronize(self):
+        check(lib().nc_ctx_synchronize(self.h))
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().nc_ctx_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class QMat:
+    """Device-resident repacked Q4_0 / Q4_K matrix (QuantizedMatrix, src/model.rs:294-310)."""
+
+    def __init__(self, ctx: Context, qtype: int, rows: int, cols: int, gguf_blocks: np.ndarray):
+        blocks = np.ascontiguousarray(gguf_blocks, dtype=np.uint8)
+        h = C.c_void_p()
+        check(lib().nc_qmat_upload(ctx.h, qtype, rows, cols, blocks.ctypes.data, C.byref(h)))
+        self.h, self.ctx, self.rows, self.cols, self.qtype = h, ctx, rows, cols, qtype
+
+    @property
+    def device_bytes(self) -> int:
+        return int(lib().nc_qmat_device_bytes(self.h))
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().nc_qmat_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def matmul_quantized_batch(ctx: Context, w: QMat, x_i8, x_scales, out=None):
+    """out[t][r] = sum_b (w_scale*x_scale)*dot in block order (src/inference.rs:1246).
+
+    x_i8: torch int8 [batch, cols] on the GPU; x_scales: torch float32 [batch, cols/32]."""
+    import torch
+    n = x_i8.shape[0]
+    if out is None:
+        out = torch.empty((n, w.rows), dtype=torch.float32, device=x_i8.device)
+    check(lib().nc_matmul_quantized_batch(ctx.h, w.h, x_i8.data_ptr(), x_scales.data_ptr(), out.data_ptr(), n,
+                                          w.rows, w.cols, _stream_of(x_i8)))
+    return out
+
+
+def matmul_blockdots(ctx: Context, w: QMat, x_i8):
+    """int32 per-block dot products [batch, rows, cols/32] (q8.rs:2699 per block)."""
+    import torch
+    n = x_i8.shape[0]
+    dots = torch.empty((n, w.rows, w.cols // 32), dtype=torch.int32, device=x_i8.device)
+    check(lib().nc_matmul_blockdots(ctx.h, w.h, x_i8.data_ptr(), dots.data_ptr(), n, w.rows, w.cols,
+                                    _stream_of(x_i8)))
+    return dots
+
+
+def quantize_f32_to_q8_0_batch(ctx: Context, x):
+    """Q8_0 activation quantisation on the GPU (src/inference.rs:967-1029)."""
+    import torch
+    n, dim = x.shape
+    q = torch.empty((n, dim), dtype=torch.int8, device=x.device)
+    s = torch.empty((n, dim // 32), dtype=torch.float32, device=x.device)
+    check(lib().nc_quantize_q8_0_batch(ctx.h, x.data_ptr(), q.data_ptr(), s.data_ptr(), n, dim, _stream_of(x)))
+    return q, s
+
+
+class Model:
+    """Llama weights on the device (LlamaWeights::load, src/model.rs:461-545)."""
+
+    def __init__(self, ctx: Context, path: str | None = None, data: np.ndarray | None = None, nthreads: int = 0):
+        opts = LoadOpts()
+        opts.nthreads = nthreads
+        h = C.c_void_p()
+        if data is not None:
+            buf = np.ascontiguousarray(data, dtype=np.uint8)
+            check(lib().nc_model_load_gguf_memory(ctx.h, buf.ctypes.data, buf.size, C.byref(opts), C.byref(h)))
+        else:
+            check(lib().nc_model_load_gguf(ctx.h, path.encode(), C.byref(opts), C.byref(h)))
+        self.h, self.ctx = h, ctx
+        cfg = ModelConfig()
+        check(lib().nc_model_get_config(h, C.byref(cfg)))
+        self.config = {f: getattr(cfg, f) for f, _ in ModelConfig._fields_}
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().nc_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Session:
+    """One sequence: KV cache, workspaces, stream (LlamaKvCache + workspaces)."""
+
+    def __init__(self, model: Model, max_ctx: int, max_batch: int = 16):
+        h = C.c_void_p()
+        check(lib().nc_session_create(model.h, max_ctx, max_batch, C.byref(h)))
+        self.h, self.model = h, model
+        self.vocab = model.config["vocab_size"]
+        self.d = model.config["embedding_length"]
+
+    def prefill_pass_batch(self, toks, start_pos: int):
+        a, p = _u32(toks)
+        check(lib().nc_prefill(self.h, p, a.size, start_pos, 1))
+
+    def forward_pass(self, tok: int, pos: int, want_logits: bool = True):
+        pred = C.c_uint32()
+        logits = np.empty(self.vocab, np.float32) if want_logits else None
+        lp = logits.ctypes.data_as(C.POINTER(C.c_float)) if want_logits else None
+        check(lib().nc_forward1(self.h, int(tok), pos, lp, C.byref(pred)))
+        return pred.value, logits
+
+    def verify_greedy(self, toks, start_pos: int):
+        a, p = _u32(toks)
+        preds = np.zeros(a.size, np.uint32)
+        r = VerifyResult()
+        check(lib().nc_verify_greedy(self.h, p, a.size, start_pos, C.byref(r),
+                                     preds.ctypes.data_as(C.POINTER(C.c_uint32))))
+        return r.n_accepted, r.next_token, r.new_pos, preds
+
+    def logits(self, row: int) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        check(lib().nc_session_logits(self.h, row, out.ctypes.data_as(C.POINTER(C.c_float))))
+        return out
+
+    def hidden(self, n: int) -> np.ndarray:
+        out = np.empty((n, self.d), np.float32)
+        check(lib().nc_session_hidden(self.h, n, out.ctypes.data_as(C.POINTER(C.c_float))))
+        return out
+
+    def generate_greedy(self, prompt, n_new: int):
+        a, p = _u32(prompt)
+        out = np.zeros(n_new, np.uint32)
+        st = DecodeStats()
+        check(lib().nc_generate_greedy(self.h, p, a.size, n_new, out.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                       C.byref(st)))
+        return out, st
+
+    def generate_speculative_oracle(self, prompt, n_new: int, k: int, alpha: float, seed: int, greedy,
+                                    max_steps: int = 0):
+        a, p = _u32(prompt)
+        g, gp = _u32(greedy)
+        out = np.zeros(n_new, np.uint32)
+        st = DecodeStats()
+        check(lib().nc_generate_speculative_oracle(self.h, p, a.size, n_new, max_steps, k, alpha, seed, gp, g.size,
+                                                   out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
+        return out[:st.emitted], st
+
+    def timing(self, enable: bool):
+        check(lib().nc_session_timing_enable(self.h, 1 if enable else 0))
+
+    def gemm_timing(self):
+        ms = C.c_double()
+        by = C.c_int64()
+        n = lib().nc_session_kernel_timing(self.h, b"gemm_q4_0", C.byref(ms), C.byref(by))
+        return int(n), ms.value, int(by.value)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().nc_session_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def generate_speculative_draft(target: Session, draft: Session, prompt, n_new: int, draft_k: int):
+    a, p = _u32(prompt)
+    out = np.zeros(n_new, np.uint32)
+    st = DecodeStats()
+    check(lib().nc_generate_speculative_draft(target.h, draft.h, p, a.size, n_new, draft_k,
+                                              out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
+    return out[:st.emitted], st
+
+
+# Model shapes of the benchmark configurations.
+SYNTH_CONFIGS = {
+    "llama-3.2-1b": dict(layers=16, embedding_length=2048, head_count=32, head_count_kv=8, feed_forward_length=8192,
+                         vocab_size=128256, tied=1, weight_type=NC_TYPE_Q4_0),
+    "llama-3-8b": dict(layers=32, embedding_length=4096, head_count=32, head_count_kv=8, feed_forward_length=14336,
+                       vocab_size=128256, tied=0, weight_type=NC_TYPE_Q4_0),
+    "llama-3.2-3b-q4k": dict(layers=28, embedding_length=3072, head_count=24, head_count_kv=8,
+                             feed_forward_length=8192, vocab_size=128256, tied=1, weight_type=NC_TYPE_Q4_K),
+    "llama-3-70b": dict(layers=80, embedding_length=8192, head_count=64, head_count_kv=8, feed_forward_length=28672,
+                        vocab_size=128256, tied=0, weight_type=NC_TYPE_Q4_0),
+}
+
+
+def synth_gguf(layers, embedding_length, head_count, head_count_kv, feed_forward_length, vocab_size,
+               context_length=8192, weight_type=NC_TYPE_Q4_0, tied=1, norm_mode=0, rope_freq_base=500000.0,
+               rms_norm_epsilon=1e-5, weight_std=0.02, seed=0, nthreads=0) -> np.ndarray:
+    """Seeded random-init Llama GGUF v3 image (weights N(0, std) -> Q4_0 / Q4_K)."""
+    s = SynthSpec(layers, embedding_length, head_count, head_count_kv, feed_forward_length, vocab_size,
+                  context_length, weight_type, tied, norm_mode, rope_freq_base, rms_norm_epsilon, weight_std, seed)
+    size = C.c_uint64()
+    check(lib().nc_synth_size(C.byref(s), C.byref(size)))
+    buf = np.empty(size.value, np.uint8)
+    check(lib().nc_synth_write(C.byref(s), buf.ctypes.data, size.value, nthreads))
+    return buf
+
+
+def uniform_prompt(seed: int, n: int, vocab: int) -> np.ndarray:
+    out = np.zeros(n, np.uint32)
+    check(lib().nc_uniform_prompt(seed, n, vocab, out.ctypes.data_as(C.POINTER(C.c_uint32))))
+    return out
+
+
+def oracle_draft(seed: int, p: int, alpha: float, greedy, n_prompt: int, vocab: int) -> int:
+    g, gp = _u32(greedy)
+    return int(lib().nc_oracle_draft(seed, p, alpha, gp, n_prompt, g.size, vocab))

@@ -1,0 +1,468 @@
+// Skinny quantized GEMM for the k+1-column verify batch on gfx950.
+//
+//   out[n][r] = sum_b fl( fl(w_scale[r][b] * x_scale[n][b]) * (float)dot_i32(w[r][b], x[n][b]) )
+//
+// with the f32 sum taken strictly in block order b = 0, 1, ... (Q4_0:
+// inference.rs:1553-1573; Q4_K: per super-block partials in order,
+// inference.rs:2083-2130), so results are bit-identical to the reference's
+// portable path.
+//
+// Mapping: one 64-row tile per workgroup, lane = row.  Weight bytes come from a
+// repacked layout where every wave-wide load is 1 KB contiguous; the activation
+// block of a token is wave-uniform and is read with scalar loads into SGPRs, so the
+// int8 dot is v_dot4_i32_i8 with an SGPR operand and needs no LDS or L1 traffic.
+// With S > 1 waves per workgroup the K range is split round-robin in rounds of
+// S*U blocks: each wave writes its per-block terms to LDS and the chain threads
+// (lane = row, wave = token group) add them in block order.  int32 dots are exact,
+// every float op is IEEE with no contraction.
+#include "nc_device.h"
+#include "nc_internal.h"
+
+namespace nc {
+
+typedef const int __attribute__((address_space(4)))* sptr_i32;
+typedef const float __attribute__((address_space(4)))* sptr_f32;
+
+template <typename T>
+__device__ __forceinline__ sptr_i32 as_scalar_i32(const T* p) {
+    return (sptr_i32)(const void __attribute__((address_space(4)))*)(uintptr_t)p;
+}
+template <typename T>
+__device__ __forceinline__ sptr_f32 as_scalar_f32(const T* p) {
+    return (sptr_f32)(const void __attribute__((address_space(4)))*)(uintptr_t)p;
+}
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Scale vector of U consecutive f16 scales of one row.
+template <int U>
+struct ScaleVec;
+template <>
+struct ScaleVec<8> {
+    uint4 v;
+    __device__ __forceinline__ void load(const uint8_t* p) { v = *(const uint4*)p; }
+    __device__ __forceinline__ uint16_t get(int u) const {
+        uint32_t w = u < 2 ? v.x : (u < 4 ? v.y : (u < 6 ? v.z : v.w));
+        return (uint16_t)((u & 1) ? (w >> 16) : (w & 0xffff));
+    }
+};
+template <>
+struct ScaleVec<4> {
+    uint2 v;
+    __device__ __forceinline__ void load(const uint8_t* p) { v = *(const uint2*)p; }
+    __device__ __forceinline__ uint16_t get(int u) const {
+        uint32_t w = u < 2 ? v.x : v.y;
+        return (uint16_t)((u & 1) ? (w >> 16) : (w & 0xffff));
+    }
+};
+template <>
+struct ScaleVec<2> {
+    uint32_t v;
+    __device__ __forceinline__ void load(const uint8_t* p) { v = *(const uint32_t*)p; }
+    __device__ __forceinline__ uint16_t get(int u) const { return (uint16_t)(u ? (v >> 16) : (v & 0xffff)); }
+};
+template <>
+struct ScaleVec<1> {
+    uint16_t v;
+    __device__ __forceinline__ void load(const uint8_t* p) { v = *(const uint16_t*)p; }
+    __device__ __forceinline__ uint16_t get(int) const { return v; }
+};
+
+// ---------------------------------------------------------------- epilogues
+// Thread (wave w, lane l) owns row 64*tile + l and tokens n = w + j*S.
+template <int NMAX, int S>
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const float* acc, int tile, int wave, int lane) {
+    constexpr int TPW = (NMAX + S - 1) / S;
+    const int row = tile * kTileRows + lane;
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        const int n = wave + j * S;
+        if (n >= p.N) break;  // wave-uniform
+        float v = acc[j];
+        switch (p.epi) {
+            case EPI_STORE:
+                if (row < p.M) p.out[(size_t)n * p.ld_out + row] = v;
+                break;
+            case EPI_RESIDUAL:
+                // hidden = matmul; hidden += residual (inference.rs:3985, 4073; add_residual_batch :4122)
+                if (row < p.M) {
+                    float* o = p.out + (size_t)n * p.ld_out + row;
+                    *o = v + *o;
+                }
+                break;
+            case EPI_QKV_ROPE: {
+                // inference.rs:3894-3924: RoPE on q and k rows (NORM pairs 2i, 2i+1 are
+                // adjacent lanes), then q to the q buffer and k, v to the KV cache.
+                const int pos = p.d_pos[0] + n;
+                const int base = tile * kTileRows;  // tiles never straddle q/k/v
+                const bool is_q = base < p.aw;
+                const bool is_k = !is_q && base < p.aw + p.kw;
+                const int rr = is_q ? row : (is_k ? row - p.aw : row - p.aw - p.kw);
+                float partner = __shfl_xor(v, 1, 64);
+                if (is_q || is_k) {
+                    const int i = (rr % p.hd) >> 1;
+                    if (i < p.rope_half) {
+                        const float* sc = p.rope_tab + ((size_t)pos * p.rope_half + i) * 2;
+                        const float s = sc[0], c = sc[1];
+                        const float x0 = (lane & 1) ? partner : v;
+                        const float x1 = (lane & 1) ? v : partner;
+                        v = (lane & 1) ? (x0 * s + x1 * c) : (x0 * c - x1 * s);
+                    }
+                }
+                if (is_q) {
+                    p.q_out[(size_t)n * p.aw + rr] = v;
+                } else {
+                    const int kvh = rr / p.hd, d = rr % p.hd;
+                    float* cache = is_k ? p.kcache : p.vcache;
+                    cache[((size_t)kvh * p.max_ctx + pos) * p.hd + d] = v;
+                }
+                break;
+            }
+            case EPI_SWIGLU_Q8: {
+                // Interleaved tile: lanes 0..31 gate rows f = 32*tile + l, lanes 32..63 the up rows.
+                // fused_silu_mul (inference.rs:3367-3390) then quantize_f32_to_q8_0 of the
+                // 32-wide block f = 32*tile .. +31 (inference.rs:4034-4041).
+                float up = __shfl(v, (lane & 31) + 32, 64);
+                float g = v;
+                float sig = 1.0f / (1.0f + expf_glibc(-g));
+                float y = g * sig * up;
+                float amax = halfwave_amax(y);
+                float scale;
+                int q = quantize_lane_q8(y, amax, &scale);
+                int qs = halfwave_isum(q);
+                if (lane < 32) {
+                    const int f = tile * 32 + lane;
+                    p.xq_out[(size_t)n * p.F + f] = (int8_t)q;
+                    if (lane == 0) {
+                        p.xs_out[(size_t)n * (p.F / 32) + tile] = scale;
+                        p.xsum_out[(size_t)n * (p.F / 32) + tile] = qs;
+                    }
+                }
+                break;
+            }
+            case EPI_HEAD: {
+                // logits row + first-max argmax partial of this tile (inference.rs:4836-4846).
+                if (row < p.M) p.out[(size_t)n * p.ld_out + row] = v;
+                float bv = row < p.M ? v : -__builtin_inff();
+                int bi = row < p.M ? row : 0x7fffffff;
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) {
+                    float ov = __shfl_xor(bv, off, 64);
+                    int oi = __shfl_xor(bi, off, 64);
+                    if (ov > bv || (ov == bv && oi < bi)) {
+                        bv = ov;
+                        bi = oi;
+                    }
+                }
+                if (lane == 0) {
+                    p.part_val[(size_t)n * p.ntiles + tile] = bv;
+                    p.part_idx[(size_t)n * p.ntiles + tile] = bi;
+                }
+                break;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- Q4_0
+template <int NMAX, int S, int U>
+__global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
+    constexpr int RB = S * U;
+    constexpr int TPW = (NMAX + S - 1) / S;
+    extern __shared__ float lds[];  // [RB][NMAX][64] terms when S > 1
+    const int tile = blockIdx.x;
+    const int wave = wave_id_uniform();
+    const int lane = threadIdx.x & 63;
+    const int N = p.N;
+    const int nb = p.units;
+    const uint8_t* wt = p.w + (size_t)tile * p.groups * kQ40ChunkBytes;
+    float acc[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; j++) acc[j] = 0.0f;
+
+    const int nrounds = (nb + RB - 1) / RB;
+    uint4 cur[U], nxt[U];
+    ScaleVec<U> cs, ns;
+    auto load = [&](int r, uint4* nbuf, ScaleVec<U>& sbuf) {
+        const int b0 = r * RB + wave * U;
+        if (b0 < nb) {
+            const uint8_t* chunk = wt + (size_t)(b0 >> 3) * kQ40ChunkBytes;
+            const int u0 = b0 & 7;
+#pragma unroll
+            for (int u = 0; u < U; u++) nbuf[u] = *(const uint4*)(chunk + (u0 + u) * 1024 + lane * 16);
+            sbuf.load(chunk + 8192 + lane * 16 + u0 * 2);
+        }
+    };
+    load(0, cur, cs);
+    for (int r = 0; r < nrounds; r++) {
+        if (r + 1 < nrounds) load(r + 1, nxt, ns);
+        const int b0 = r * RB + wave * U;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int b = b0 + u;
+            if (b < nb) {  // wave-uniform
+                const uint4 v = cur[u];
+                const int lo0 = v.x & 0x0F0F0F0F, hi0 = (v.x >> 4) & 0x0F0F0F0F;
+                const int lo1 = v.y & 0x0F0F0F0F, hi1 = (v.y >> 4) & 0x0F0F0F0F;
+                const int lo2 = v.z & 0x0F0F0F0F, hi2 = (v.z >> 4) & 0x0F0F0F0F;
+                const int lo3 = v.w & 0x0F0F0F0F, hi3 = (v.w >> 4) & 0x0F0F0F0F;
+                const float ws = f16_to_f32(cs.get(u));
+#pragma unroll
+                for (int n = 0; n < NMAX; n++) {
+                    if (n < N) {
+                        sptr_i32 xw = as_scalar_i32(p.x + (size_t)n * p.K + (size_t)b * 32);
+                        const float xsv = as_scalar_f32(p.xs)[(size_t)n * nb + b];
+                        const int xsum = as_scalar_i32(p.xsum)[(size_t)n * nb + b];
+                        // sum (nib - 8) * x == sum nib * x - 8 * sum x (exact in int32)
+                        int d = -8 * xsum;
+                        d = dot4(lo0, xw[0], d);
+                        d = dot4(lo1, xw[1], d);
+                        d = dot4(lo2, xw[2], d);
+                        d = dot4(lo3, xw[3], d);
+                        d = dot4(hi0, xw[4], d);
+                        d = dot4(hi1, xw[5], d);
+                        d = dot4(hi2, xw[6], d);
+                        d = dot4(hi3, xw[7], d);
+                        const float t = (ws * xsv) * (float)d;
+                        if constexpr (S == 1) {
+                            acc[n] = acc[n] + t;
+                        } else {
+                            lds[((wave * U + u) * NMAX + n) * 64 + lane] = t;
+                        }
+                    }
+                }
+            }
+        }
+        if constexpr (S > 1) {
+            __syncthreads();
+            const int nblk = min(RB, nb - r * RB);
+#pragma unroll
+            for (int j = 0; j < TPW; j++) {
+                const int n = wave + j * S;
+                if (n < N) {
+                    float a = acc[j];
+                    for (int bl = 0; bl < nblk; bl++) a = a + lds[(bl * NMAX + n) * 64 + lane];
+                    acc[j] = a;
+                }
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) cur[u] = nxt[u];
+        cs = ns;
+    }
+    gemm_epilogue<NMAX, S>(p, acc, tile, wave, lane);
+}
+
+// ---------------------------------------------------------------- Q4_K
+// q8.rs:2008-2018 q4_k_scale_min on the 12 packed scale bytes held in three words.
+__device__ __forceinline__ uint32_t kbyte(uint32_t w0, uint32_t w1, uint32_t w2, int i) {
+    const uint32_t w = i < 4 ? w0 : (i < 8 ? w1 : w2);
+    return (w >> ((i & 3) * 8)) & 0xff;
+}
+
+template <int NMAX, int S, int U>
+__global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
+    constexpr int RB = S * U;
+    constexpr int TPW = (NMAX + S - 1) / S;
+    extern __shared__ float lds[];
+    const int tile = blockIdx.x;
+    const int wave = wave_id_uniform();
+    const int lane = threadIdx.x & 63;
+    const int N = p.N;
+    const int nsb = p.units;
+    const int nb = nsb * 8;
+    const uint8_t* wt = p.w + (size_t)tile * nsb * kQ4KChunkBytes;
+    float acc[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; j++) acc[j] = 0.0f;
+    const int nrounds = (nsb + RB - 1) / RB;
+    for (int r = 0; r < nrounds; r++) {
+        const int s0 = r * RB + wave * U;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int sb = s0 + u;
+            if (sb < nsb) {
+                const uint8_t* chunk = wt + (size_t)sb * kQ4KChunkBytes + lane * 16;
+                uint4 v[9];
+#pragma unroll
+                for (int i = 0; i < 9; i++) v[i] = *(const uint4*)(chunk + i * 1024);
+                const float d = f16_to_f32((uint16_t)(v[0].x & 0xffff));
+                const float dmin = f16_to_f32((uint16_t)(v[0].x >> 16));
+                float sc[8], mn[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    uint32_t s, m;
+                    if (j < 4) {
+                        s = kbyte(v[0].y, v[0].z, v[0].w, j) & 63;
+                        m = kbyte(v[0].y, v[0].z, v[0].w, j + 4) & 63;
+                    } else {
+                        s = (kbyte(v[0].y, v[0].z, v[0].w, j + 4) & 0x0f) |
+                            ((kbyte(v[0].y, v[0].z, v[0].w, j - 4) >> 6) << 4);
+                        m = (kbyte(v[0].y, v[0].z, v[0].w, j + 4) >> 4) | ((kbyte(v[0].y, v[0].z, v[0].w, j) >> 6) << 4);
+                    }
+                    sc[j] = d * (float)s;
+                    mn[j] = dmin * (float)m;
+                }
+#pragma unroll
+                for (int n = 0; n < NMAX; n++) {
+                    if (n < N) {
+                        sptr_i32 xw = as_scalar_i32(p.x + (size_t)n * p.K + (size_t)sb * 256);
+                        sptr_f32 xsp = as_scalar_f32(p.xs + (size_t)n * nb + (size_t)sb * 8);
+                        sptr_i32 xap = as_scalar_i32(p.xsum + (size_t)n * nb + (size_t)sb * 8);
+                        float part = 0.0f;
+#pragma unroll
+                        for (int pr = 0; pr < 4; pr++) {
+                            const uint4 q0 = v[1 + 2 * pr], q1 = v[2 + 2 * pr];
+                            const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                            int wl = 0, wh = 0;
+#pragma unroll
+                            for (int i = 0; i < 8; i++) {
+                                wl = dot4((int)(qw[i] & 0x0F0F0F0F), xw[pr * 16 + i], wl);
+                                wh = dot4((int)((qw[i] >> 4) & 0x0F0F0F0F), xw[pr * 16 + 8 + i], wh);
+                            }
+                            // q8.rs:1372-1375: sum += xs * (sc*W - mn*A), low then high half
+                            const int jl = 2 * pr, jh = 2 * pr + 1;
+                            part = part + xsp[jl] * (sc[jl] * (float)wl - mn[jl] * (float)xap[jl]);
+                            part = part + xsp[jh] * (sc[jh] * (float)wh - mn[jh] * (float)xap[jh]);
+                        }
+                        if constexpr (S == 1) {
+                            acc[n] = acc[n] + part;
+                        } else {
+                            lds[((wave * U + u) * NMAX + n) * 64 + lane] = part;
+                        }
+                    }
+                }
+            }
+        }
+        if constexpr (S > 1) {
+            __syncthreads();
+            const int nblk = min(RB, nsb - r * RB);
+#pragma unroll
+            for (int j = 0; j < TPW; j++) {
+                const int n = wave + j * S;
+                if (n < N) {
+                    float a = acc[j];
+                    for (int bl = 0; bl < nblk; bl++) a = a + lds[(bl * NMAX + n) * 64 + lane];
+                    acc[j] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    gemm_epilogue<NMAX, S>(p, acc, tile, wave, lane);
+}
+
+// ---------------------------------------------------------------- per-block dots (parity debug)
+__global__ void blockdots_q4_0_kernel(const uint8_t* w, int groups, int M, int K, const int8_t* x, int N, int32_t* dots) {
+    const int nb = K / 32;
+    const int64_t total = (int64_t)N * M * nb;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int b = (int)(i % nb);
+        const int r = (int)((i / nb) % M);
+        const int n = (int)(i / ((int64_t)nb * M));
+        const uint8_t* chunk = w + ((size_t)(r / 64) * groups + b / 8) * kQ40ChunkBytes;
+        const uint8_t* nib = chunk + (b & 7) * 1024 + (r & 63) * 16;
+        const int8_t* xb = x + (size_t)n * K + (size_t)b * 32;
+        int d = 0;
+        for (int j = 0; j < 16; j++) {
+            d += ((int)(nib[j] & 0x0f) - 8) * (int)xb[j];
+            d += ((int)(nib[j] >> 4) - 8) * (int)xb[j + 16];
+        }
+        dots[i] = d;
+    }
+}
+
+__global__ void blockdots_q4_k_kernel(const uint8_t* w, int nsb, int M, int K, const int8_t* x, int N, int32_t* dots) {
+    const int nb = K / 32;
+    const int64_t total = (int64_t)N * M * nb;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int j = (int)(i % nb);
+        const int r = (int)((i / nb) % M);
+        const int n = (int)(i / ((int64_t)nb * M));
+        const int sb = j / 8, sj = j % 8, pr = sj / 2, half = sj % 2;
+        const uint8_t* chunk = w + ((size_t)(r / 64) * nsb + sb) * kQ4KChunkBytes + (r & 63) * 16;
+        const int8_t* xb = x + (size_t)n * K + (size_t)j * 32;
+        int d = 0;
+        for (int l = 0; l < 32; l++) {
+            const uint8_t byte = chunk[(1 + 2 * pr + l / 16) * 1024 + (l % 16)];
+            d += (int)(half ? (byte >> 4) : (byte & 0x0f)) * (int)xb[l];
+        }
+        dots[i] = d;
+    }
+}
+
+// ---------------------------------------------------------------- dispatch
+namespace {
+
+template <int NMAX, int S>
+constexpr int pick_u() {
+    // LDS terms: S*U*NMAX*64*4 bytes <= 64 KB
+    return S == 1 ? 8 : (S * NMAX * 8 <= 256 ? 8 : (S * NMAX * 4 <= 256 ? 4 : (S * NMAX * 2 <= 256 ? 2 : 1)));
+}
+
+template <int NMAX, int S>
+int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st) {
+    constexpr int U = pick_u<NMAX, S>();
+    const size_t lds = S > 1 ? (size_t)S * U * NMAX * 64 * sizeof(float) : 0;
+    if (w.type == NC_TYPE_Q4_0) {
+        hipLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, U>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+    } else {
+        hipLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, (U > 2 ? 2 : U)>), dim3(p.ntiles), dim3(64 * S),
+                           S > 1 ? (size_t)S * (U > 2 ? 2 : U) * NMAX * 64 * sizeof(float) : 0, st, p);
+    }
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+template <int NMAX>
+int launch_s(int S, const QMatDev& w, const GemmParams& p, hipStream_t st) {
+    switch (S) {
+        case 1: return launch_one<NMAX, 1>(w, p, st);
+        case 2: return launch_one<NMAX, 2>(w, p, st);
+        case 4: return launch_one<NMAX, 4>(w, p, st);
+        case 8: return launch_one<NMAX, 8>(w, p, st);
+        default: return launch_one<NMAX, 16>(w, p, st);
+    }
+}
+
+}  // namespace
+
+// Waves per workgroup: enough K-split waves that ~1000+ waves stream the matrix.
+static int pick_waves(int64_t tiles) {
+    int S = 1;
+    while (S < 16 && tiles * S < 1024) S *= 2;
+    return S;
+}
+
+int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st) {
+    GemmParams p = p0;
+    p.w = w.dev;
+    p.ntiles = (int)w.tiles;
+    p.units = (int)w.units;
+    p.groups = (int)w.groups;
+    p.M = (int)w.rows;
+    p.K = (int)w.cols;
+    if (p.N < 1 || p.N > 16) return fail(NC_EINVAL, "gemm: batch must be 1..16");
+    const int S = pick_waves(w.tiles);
+    if (p.N == 1) return launch_s<1>(S, w, p, st);
+    if (p.N == 2) return launch_s<2>(S, w, p, st);
+    if (p.N <= 4) return launch_s<4>(S, w, p, st);
+    if (p.N <= 8) return launch_s<8>(S, w, p, st);
+    return launch_s<16>(S, w, p, st);
+}
+
+int launch_blockdots(const QMatDev& w, const int8_t* x, int32_t* dots, int N, hipStream_t st) {
+    const int64_t total = (int64_t)N * w.rows * (w.cols / 32);
+    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
+    if (w.type == NC_TYPE_Q4_0)
+        hipLaunchKernelGGL(blockdots_q4_0_kernel, dim3(blocks), dim3(256), 0, st, w.dev, (int)w.groups, (int)w.rows,
+                           (int)w.cols, x, N, dots);
+    else
+        hipLaunchKernelGGL(blockdots_q4_k_kernel, dim3(blocks), dim3(256), 0, st, w.dev, (int)w.units, (int)w.rows,
+                           (int)w.cols, x, N, dots);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+}  // namespace nc

@@ -1,0 +1,516 @@
+// GGUF v2/v3 reader and the seeded synthetic-model writer.
+//
+// Reader: same header walk as gguf::read_file (src/gguf.rs:454-551): magic, version
+// 2..3, tensor/metadata counts, metadata key/values, tensor infos, data start
+// aligned to general.alignment (default 32, gguf.rs:10), byte sizes from the type
+// layout table (gguf.rs:154-185, tensor_nbytes gguf.rs:737-763).
+#include "gguf.h"
+
+#include <cmath>
+#include <cstring>
+#include <thread>
+
+namespace nc {
+
+namespace {
+
+struct Cur {
+    const uint8_t* p;
+    size_t n, pos = 0;
+    bool ok = true;
+    uint64_t u(int b) {
+        if (pos + b > n) {
+            ok = false;
+            return 0;
+        }
+        uint64_t v = 0;
+        for (int i = 0; i < b; i++) v |= (uint64_t)p[pos + i] << (8 * i);
+        pos += b;
+        return v;
+    }
+    std::string s() {
+        uint64_t len = u(8);
+        if (!ok || pos + len > n) {
+            ok = false;
+            return "";
+        }
+        std::string r((const char*)p + pos, len);
+        pos += len;
+        return r;
+    }
+};
+
+bool skip_or_read(Cur& c, uint32_t type, GgufValue& v, int depth) {
+    v.type = (int)type;
+    switch (type) {
+        case 0: v.u = c.u(1); return c.ok;
+        case 1: v.i = (int8_t)c.u(1); return c.ok;
+        case 2: v.u = c.u(2); return c.ok;
+        case 3: v.i = (int16_t)c.u(2); return c.ok;
+        case 4: v.u = c.u(4); return c.ok;
+        case 5: v.i = (int32_t)c.u(4); return c.ok;
+        case 6: { uint32_t b = (uint32_t)c.u(4); float f; std::memcpy(&f, &b, 4); v.f = f; return c.ok; }
+        case 7: v.u = c.u(1); return c.ok && v.u <= 1;
+        case 8: v.s = c.s(); return c.ok;
+        case 9: {
+            if (depth) return false;
+            uint32_t it = (uint32_t)c.u(4);
+            uint64_t len = c.u(8);
+            for (uint64_t k = 0; k < len && c.ok; k++) {
+                GgufValue t;
+                if (!skip_or_read(c, it, t, 1)) return false;
+            }
+            return c.ok;
+        }
+        case 10: v.u = c.u(8); return c.ok;
+        case 11: v.i = (int64_t)c.u(8); return c.ok;
+        case 12: { uint64_t b = c.u(8); double d; std::memcpy(&d, &b, 8); v.f = d; return c.ok; }
+        default: return false;
+    }
+}
+
+}  // namespace
+
+bool gguf_type_layout(uint32_t t, uint64_t* block, uint64_t* bytes) {
+    switch (t) {
+        case 0: *block = 1; *bytes = 4; return true;
+        case 1: *block = 1; *bytes = 2; return true;
+        case 2: *block = 32; *bytes = 18; return true;
+        case 8: *block = 32; *bytes = 34; return true;
+        case 12: *block = 256; *bytes = 144; return true;
+        case 30: *block = 1; *bytes = 2; return true;
+        default: return false;
+    }
+}
+
+bool gguf_parse(const uint8_t* data, size_t size, GgufFile& g, std::string& err) {
+    g.data = data;
+    g.size = size;
+    Cur c{data, size};
+    if (size < 8 || std::memcmp(data, "GGUF", 4) != 0) {
+        err = "invalid GGUF magic";
+        return false;
+    }
+    c.pos = 4;
+    uint32_t ver = (uint32_t)c.u(4);
+    if (ver < 2 || ver > 3) {
+        err = "unsupported GGUF version " + std::to_string(ver);
+        return false;
+    }
+    uint64_t nt = c.u(8), nm = c.u(8);
+    for (uint64_t i = 0; i < nm && c.ok; i++) {
+        std::string k = c.s();
+        uint32_t vt = (uint32_t)c.u(4);
+        GgufValue v;
+        if (!skip_or_read(c, vt, v, 0)) {
+            err = "malformed metadata value for key " + k;
+            return false;
+        }
+        g.meta[k] = v;
+    }
+    uint64_t align = 32;
+    auto a = g.meta.find("general.alignment");
+    if (a != g.meta.end()) {
+        if (a->second.type == 4 || a->second.type == 10) align = a->second.u;
+        else if (a->second.type == 5) align = (uint64_t)a->second.i;
+    }
+    if (align == 0 || (align & (align - 1))) {
+        err = "invalid alignment";
+        return false;
+    }
+    struct Raw {
+        std::string name;
+        std::vector<uint64_t> dims;
+        uint32_t type;
+        uint64_t off;
+    };
+    std::vector<Raw> raws;
+    for (uint64_t i = 0; i < nt && c.ok; i++) {
+        Raw r;
+        r.name = c.s();
+        uint32_t nd = (uint32_t)c.u(4);
+        if (nd == 0 || nd > 4) {
+            err = "tensor " + r.name + " has invalid dimension count";
+            return false;
+        }
+        for (uint32_t k = 0; k < nd; k++) r.dims.push_back(c.u(8));
+        r.type = (uint32_t)c.u(4);
+        r.off = c.u(8);
+        raws.push_back(std::move(r));
+    }
+    if (!c.ok) {
+        err = "truncated GGUF header";
+        return false;
+    }
+    const uint64_t start = (c.pos + align - 1) & ~(align - 1);
+    for (auto& r : raws) {
+        uint64_t bs, ts;
+        if (!gguf_type_layout(r.type, &bs, &ts)) {
+            err = "tensor " + r.name + " has an unsupported type " + std::to_string(r.type);
+            return false;
+        }
+        if (r.dims[0] % bs) {
+            err = "tensor " + r.name + " first dimension not divisible by block size";
+            return false;
+        }
+        uint64_t el = 1;
+        for (auto d : r.dims) el *= d;
+        GgufTensor t{r.name, r.dims, r.type, start + r.off, el / bs * ts};
+        if (t.offset + t.nbytes > size) {
+            err = "tensor " + r.name + " exceeds the file";
+            return false;
+        }
+        g.tensors.push_back(std::move(t));
+    }
+    return true;
+}
+
+const GgufTensor* GgufFile::find(const std::string& name) const {
+    for (auto& t : tensors)
+        if (t.name == name) return &t;
+    return nullptr;
+}
+
+bool GgufFile::get_u32(const std::string& k, uint32_t* out) const {  // gguf.rs:230-237
+    auto it = meta.find(k);
+    if (it == meta.end()) return false;
+    const GgufValue& v = it->second;
+    if (v.type == 4) { *out = (uint32_t)v.u; return true; }
+    if (v.type == 10 && v.u <= 0xffffffffull) { *out = (uint32_t)v.u; return true; }
+    if (v.type == 5 && v.i >= 0) { *out = (uint32_t)v.i; return true; }
+    return false;
+}
+
+bool GgufFile::get_f32(const std::string& k, float* out) const {  // gguf.rs:239-245
+    auto it = meta.find(k);
+    if (it == meta.end()) return false;
+    if (it->second.type == 6 || it->second.type == 12) {
+        *out = (float)it->second.f;
+        return true;
+    }
+    return false;
+}
+
+std::string GgufFile::get_str(const std::string& k) const {
+    auto it = meta.find(k);
+    return (it == meta.end() || it->second.type != 8) ? std::string() : it->second.s;
+}
+
+// ---------------------------------------------------------------- Philox4x32-10
+void philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    // Salmon et al., SC'11: multipliers 0xD2511F53 / 0xCD9E8D57, key bumps 0x9E3779B9 / 0xBB67AE85.
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; r++) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)p1;
+        c3 = (uint32_t)p0;
+        c0 = n0;
+        c2 = n2;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0;
+    out[1] = c1;
+    out[2] = c2;
+    out[3] = c3;
+}
+
+uint32_t philox_word(uint64_t seed, uint64_t ctr, uint32_t purpose) {
+    const uint32_t c[4] = {(uint32_t)ctr, (uint32_t)(ctr >> 32), purpose, 0};
+    const uint32_t k[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t o[4];
+    philox4x32_10(c, k, o);
+    return o[0];
+}
+
+float philox_uniform(uint64_t seed, uint64_t ctr, uint32_t purpose) {
+    return (float)(philox_word(seed, ctr, purpose) >> 8) * (1.0f / 16777216.0f);
+}
+
+// ---------------------------------------------------------------- synthetic writer
+namespace {
+
+uint16_t f32_to_f16_rne(float f) {
+    // IEEE round-to-nearest-even binary32 -> binary16 (what llama.cpp's F16C path does).
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+void put_u32(std::vector<uint8_t>& b, uint32_t v) {
+    for (int i = 0; i < 4; i++) b.push_back((uint8_t)(v >> (8 * i)));
+}
+void put_u64(std::vector<uint8_t>& b, uint64_t v) {
+    for (int i = 0; i < 8; i++) b.push_back((uint8_t)(v >> (8 * i)));
+}
+void put_str(std::vector<uint8_t>& b, const std::string& s) {
+    put_u64(b, s.size());
+    b.insert(b.end(), s.begin(), s.end());
+}
+void kv_str(std::vector<uint8_t>& b, const std::string& k, const std::string& v) {
+    put_str(b, k);
+    put_u32(b, 8);
+    put_str(b, v);
+}
+void kv_u32(std::vector<uint8_t>& b, const std::string& k, uint32_t v) {
+    put_str(b, k);
+    put_u32(b, 4);
+    put_u32(b, v);
+}
+void kv_f32(std::vector<uint8_t>& b, const std::string& k, float v) {
+    put_str(b, k);
+    put_u32(b, 6);
+    uint32_t u;
+    std::memcpy(&u, &v, 4);
+    put_u32(b, u);
+}
+
+struct TSpec {
+    std::string name;
+    uint64_t cols, rows;  // rows == 1 for vectors
+    uint32_t type;
+    int kind;             // 0 = weight N(0, std), 1 = norm
+    uint64_t offset = 0, bytes = 0;
+};
+
+std::vector<TSpec> synth_tensors(const nc_synth_spec& s) {
+    const uint64_t d = s.embedding_length, F = s.feed_forward_length, V = s.vocab_size;
+    const uint64_t hd = d / s.head_count, aw = s.head_count * hd, kw = s.head_count_kv * hd;
+    const uint32_t wt = (uint32_t)s.weight_type;
+    std::vector<TSpec> t;
+    t.push_back({"token_embd.weight", d, V, wt, 0});
+    t.push_back({"output_norm.weight", d, 1, 0, 1});
+    if (!s.tied) t.push_back({"output.weight", d, V, NC_TYPE_Q4_0, 0});
+    for (int i = 0; i < s.layers; i++) {
+        const std::string b = "blk." + std::to_string(i) + ".";
+        t.push_back({b + "attn_norm.weight", d, 1, 0, 1});
+        t.push_back({b + "attn_q.weight", d, aw, wt, 0});
+        t.push_back({b + "attn_k.weight", d, kw, wt, 0});
+        t.push_back({b + "attn_v.weight", d, kw, wt, 0});
+        t.push_back({b + "attn_output.weight", aw, d, wt, 0});
+        t.push_back({b + "ffn_norm.weight", d, 1, 0, 1});
+        t.push_back({b + "ffn_gate.weight", d, F, wt, 0});
+        t.push_back({b + "ffn_up.weight", d, F, wt, 0});
+        t.push_back({b + "ffn_down.weight", F, d, wt, 0});
+    }
+    for (auto& x : t) {
+        uint64_t bs, ts;
+        gguf_type_layout(x.type, &bs, &ts);
+        x.bytes = x.cols * x.rows / bs * ts;
+    }
+    return t;
+}
+
+std::vector<uint8_t> synth_header(const nc_synth_spec& s, std::vector<TSpec>& ts, uint64_t* data_start) {
+    std::vector<uint8_t> h = {'G', 'G', 'U', 'F'};
+    put_u32(h, 3);
+    put_u64(h, ts.size());
+    put_u64(h, 13);
+    kv_str(h, "general.architecture", "llama");
+    kv_u32(h, "general.alignment", 32);
+    kv_u32(h, "llama.context_length", (uint32_t)s.context_length);
+    kv_u32(h, "llama.embedding_length", (uint32_t)s.embedding_length);
+    kv_u32(h, "llama.block_count", (uint32_t)s.layers);
+    kv_u32(h, "llama.feed_forward_length", (uint32_t)s.feed_forward_length);
+    kv_u32(h, "llama.attention.head_count", (uint32_t)s.head_count);
+    kv_u32(h, "llama.attention.head_count_kv", (uint32_t)s.head_count_kv);
+    kv_f32(h, "llama.rope.freq_base", s.rope_freq_base);
+    kv_f32(h, "llama.attention.layer_norm_rms_epsilon", s.rms_norm_epsilon);
+    kv_u32(h, "llama.vocab_size", (uint32_t)s.vocab_size);
+    kv_u32(h, "llama.rope.dimension_count", (uint32_t)(s.embedding_length / s.head_count));
+    kv_str(h, "general.name", "nanocamelid-synthetic");
+    uint64_t off = 0;
+    for (auto& t : ts) {
+        put_str(h, t.name);
+        const bool vec = t.rows == 1;
+        put_u32(h, vec ? 1 : 2);
+        put_u64(h, t.cols);
+        if (!vec) put_u64(h, t.rows);
+        put_u32(h, t.type);
+        put_u64(h, off);
+        t.offset = off;
+        off += (t.bytes + 31) & ~31ull;
+    }
+    *data_start = (h.size() + 31) & ~31ull;
+    return h;
+}
+
+constexpr uint32_t kPurposeWeight = 8, kPurposeNorm = 9;
+
+// Two N(0,1) draws per Philox call (Box-Muller on two 53-bit uniforms) for elements
+// 2j and 2j+1 of tensor `tid`.
+inline void normal_pair(uint64_t seed, uint32_t tid, uint64_t j, uint32_t purpose, double* z0, double* z1) {
+    const uint32_t c[4] = {(uint32_t)j, (uint32_t)(j >> 32), tid, purpose};
+    const uint32_t k[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t o[4];
+    philox4x32_10(c, k, o);
+    const double u1 = ((double)(((uint64_t)(o[0] >> 5) << 26) | (o[1] >> 6)) + 1.0) * 0x1p-53;
+    const double u2 = (double)(((uint64_t)(o[2] >> 5) << 26) | (o[3] >> 6)) * 0x1p-53;
+    const double r = std::sqrt(-2.0 * std::log(u1));
+    const double a = 6.283185307179586 * u2;
+    *z0 = r * std::cos(a);
+    *z1 = r * std::sin(a);
+}
+
+void gen_values(uint64_t seed, uint32_t tid, uint64_t start, uint64_t count, float stdv, float mean, uint32_t purpose,
+                float* out) {
+    // start and count are even (blocks of 32/256 values)
+    for (uint64_t e = 0; e < count; e += 2) {
+        double z0, z1;
+        normal_pair(seed, tid, (start + e) / 2, purpose, &z0, &z1);
+        out[e] = (float)(mean + stdv * z0);
+        out[e + 1] = (float)(mean + stdv * z1);
+    }
+}
+
+// llama.cpp quantize_row_q4_0_ref: d = max / -8 (max = signed value of largest |x|),
+// q = min(15, (int8)(x/d + 8.5)), f16 scale rounded to nearest even.
+void quant_q4_0_block(const float* x, uint8_t* out) {
+    float amax = 0.0f, mx = 0.0f;
+    for (int j = 0; j < 32; j++)
+        if (amax < std::fabs(x[j])) {
+            amax = std::fabs(x[j]);
+            mx = x[j];
+        }
+    const float d = mx / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t h = f32_to_f16_rne(d);
+    out[0] = (uint8_t)(h & 0xff);
+    out[1] = (uint8_t)(h >> 8);
+    for (int j = 0; j < 16; j++) {
+        int q0 = (int)(int8_t)(x[j] * id + 8.5f), q1 = (int)(int8_t)(x[16 + j] * id + 8.5f);
+        q0 = q0 > 15 ? 15 : q0;
+        q1 = q1 > 15 ? 15 : q1;
+        out[2 + j] = (uint8_t)(q0 | (q1 << 4));
+    }
+}
+
+// A valid Q4_K encoding: per 32-sub-block affine [min, max] range, 6-bit scales/mins
+// relative to f16 super-block factors d, dmin; packing as llama.cpp's get_scale_min_k4
+// inverse.
+void quant_q4_k_block(const float* x, uint8_t* out) {
+    float scale[8], minv[8];
+    float maxs = 0.0f, maxm = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        float lo = 0.0f, hi = 0.0f;
+        for (int l = 0; l < 32; l++) {
+            lo = std::fmin(lo, x[j * 32 + l]);
+            hi = std::fmax(hi, x[j * 32 + l]);
+        }
+        scale[j] = (hi - lo) / 15.0f;
+        minv[j] = -lo;
+        maxs = std::fmax(maxs, scale[j]);
+        maxm = std::fmax(maxm, minv[j]);
+    }
+    const uint16_t dh = f32_to_f16_rne(maxs / 63.0f), mh = f32_to_f16_rne(maxm / 63.0f);
+    const float d = (float)__builtin_bit_cast(_Float16, dh), dmin = (float)__builtin_bit_cast(_Float16, mh);
+    uint8_t ls[8], lm[8];
+    for (int j = 0; j < 8; j++) {
+        int a = d > 0 ? (int)std::nearbyint(scale[j] / d) : 0;
+        int b = dmin > 0 ? (int)std::nearbyint(minv[j] / dmin) : 0;
+        ls[j] = (uint8_t)(a < 0 ? 0 : (a > 63 ? 63 : a));
+        lm[j] = (uint8_t)(b < 0 ? 0 : (b > 63 ? 63 : b));
+    }
+    uint8_t* sc = out + 4;
+    std::memset(sc, 0, 12);
+    for (int j = 0; j < 8; j++) {
+        if (j < 4) {
+            sc[j] = ls[j];
+            sc[j + 4] = lm[j];
+        } else {
+            sc[j + 4] = (uint8_t)((ls[j] & 0x0f) | ((lm[j] & 0x0f) << 4));
+            sc[j - 4] |= (uint8_t)((ls[j] >> 4) << 6);
+            sc[j] |= (uint8_t)((lm[j] >> 4) << 6);
+        }
+    }
+    out[0] = (uint8_t)(dh & 0xff);
+    out[1] = (uint8_t)(dh >> 8);
+    out[2] = (uint8_t)(mh & 0xff);
+    out[3] = (uint8_t)(mh >> 8);
+    uint8_t* qs = out + 16;
+    std::memset(qs, 0, 128);
+    for (int j = 0; j < 8; j++) {
+        const float sj = d * (float)ls[j], mj = dmin * (float)lm[j];
+        const int pair = j / 2, half = j % 2;
+        for (int l = 0; l < 32; l++) {
+            int q = sj > 0 ? (int)std::nearbyint((x[j * 32 + l] + mj) / sj) : 0;
+            q = q < 0 ? 0 : (q > 15 ? 15 : q);
+            qs[pair * 32 + l] |= (uint8_t)(half ? (q << 4) : q);
+        }
+    }
+}
+
+}  // namespace
+
+int synth_size(const nc_synth_spec& s, uint64_t* size) {
+    auto ts = synth_tensors(s);
+    uint64_t start;
+    synth_header(s, ts, &start);
+    const auto& last = ts.back();
+    *size = start + last.offset + last.bytes;
+    return NC_OK;
+}
+
+int synth_write(const nc_synth_spec& s, uint8_t* dst, uint64_t size, int nthreads) {
+    auto ts = synth_tensors(s);
+    uint64_t start;
+    auto hdr = synth_header(s, ts, &start);
+    const auto& last = ts.back();
+    if (size < start + last.offset + last.bytes) return fail(NC_EINVAL, "synth: destination too small");
+    std::memset(dst, 0, start);
+    std::memcpy(dst, hdr.data(), hdr.size());
+    // Work items: (tensor, block range) chunks, processed by nthreads workers.
+    struct Item {
+        uint32_t tid;
+        uint64_t b0, b1;
+    };
+    std::vector<Item> items;
+    for (uint32_t tid = 0; tid < ts.size(); tid++) {
+        const auto& t = ts[tid];
+        uint64_t bs, tb;
+        gguf_type_layout(t.type, &bs, &tb);
+        const uint64_t nblk = t.cols * t.rows / (t.type == 0 ? 32 : bs);
+        const uint64_t step = 1 << 14;
+        for (uint64_t b = 0; b < nblk; b += step) items.push_back({tid, b, std::min(nblk, b + step)});
+        // zero the alignment padding after the tensor
+        uint8_t* tp = dst + start + t.offset;
+        std::memset(tp + t.bytes, 0, ((t.bytes + 31) & ~31ull) - t.bytes);
+    }
+    std::atomic<size_t> next{0};
+    auto worker = [&]() {
+        std::vector<float> buf(256);
+        for (;;) {
+            const size_t i = next.fetch_add(1);
+            if (i >= items.size()) break;
+            const Item it = items[i];
+            const TSpec& t = ts[it.tid];
+            uint8_t* tp = dst + start + t.offset;
+            if (t.type == 0) {  // f32 norm vector, 32 values per block
+                float* o = (float*)tp;
+                for (uint64_t b = it.b0; b < it.b1; b++) {
+                    if (s.norm_mode == 0) {
+                        for (int j = 0; j < 32; j++) o[b * 32 + j] = 1.0f;
+                    } else {
+                        gen_values(s.seed, it.tid, b * 32, 32, 0.1f, 1.0f, kPurposeNorm, o + b * 32);
+                    }
+                }
+            } else if (t.type == NC_TYPE_Q4_0) {
+                for (uint64_t b = it.b0; b < it.b1; b++) {
+                    gen_values(s.seed, it.tid, b * 32, 32, s.weight_std, 0.0f, kPurposeWeight, buf.data());
+                    quant_q4_0_block(buf.data(), tp + b * 18);
+                }
+            } else {
+                for (uint64_t b = it.b0; b < it.b1; b++) {
+                    gen_values(s.seed, it.tid, b * 256, 256, s.weight_std, 0.0f, kPurposeWeight, buf.data());
+                    quant_q4_k_block(buf.data(), tp + b * 144);
+                }
+            }
+        }
+    };
+    if (nthreads <= 0) nthreads = (int)std::max(1u, std::thread::hardware_concurrency());
+    std::vector<std::thread> th;
+    for (int i = 0; i < nthreads; i++) th.emplace_back(worker);
+    for (auto& t : th) t.join();
+    return NC_OK;
+}
+
+}  // namespace nc

@@ -1,0 +1,56 @@
+// GGUF reader/writer and Philox helpers (host side of libnanocamelid_hip).
+#pragma once
+
+#include <algorithm>
+#include <atomic>
+#include <cstdint>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "nc_internal.h"
+
+namespace nc {
+
+struct GgufValue {
+    int type = -1;
+    uint64_t u = 0;
+    int64_t i = 0;
+    double f = 0;
+    std::string s;
+};
+
+struct GgufTensor {
+    std::string name;
+    std::vector<uint64_t> dims;  // dims[0] = columns (contiguous), dims[1] = rows
+    uint32_t type = 0;
+    uint64_t offset = 0;  // absolute byte offset in the image
+    uint64_t nbytes = 0;
+};
+
+struct GgufFile {
+    const uint8_t* data = nullptr;
+    size_t size = 0;
+    std::map<std::string, GgufValue> meta;
+    std::vector<GgufTensor> tensors;
+    const GgufTensor* find(const std::string& name) const;
+    bool get_u32(const std::string& k, uint32_t* out) const;
+    bool get_f32(const std::string& k, float* out) const;
+    std::string get_str(const std::string& k) const;
+};
+
+bool gguf_type_layout(uint32_t type, uint64_t* block, uint64_t* bytes);
+bool gguf_parse(const uint8_t* data, size_t size, GgufFile& out, std::string& err);
+
+void philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+uint32_t philox_word(uint64_t seed, uint64_t ctr, uint32_t purpose);
+float philox_uniform(uint64_t seed, uint64_t ctr, uint32_t purpose);
+
+// Philox purposes (counter word 2) shared by the drafter, prompts and sampling.
+constexpr uint32_t kPurposeDraft = 1, kPurposeAccept = 2, kPurposeResample = 3, kPurposePrompt = 4;
+constexpr uint32_t kPurposeOracleU = 5, kPurposeOracleId = 6, kPurposeBonus = 7;
+
+int synth_size(const nc_synth_spec& s, uint64_t* size);
+int synth_write(const nc_synth_spec& s, uint8_t* dst, uint64_t size, int nthreads);
+
+}  // namespace nc

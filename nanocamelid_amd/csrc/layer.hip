@@ -1,0 +1,336 @@
+// Row ops of the verify forward on gfx950: fused RMSNorm + Q8_0 quantisation,
+// activation quantisation, embedding gather, causal GQA attention over the
+// HBM-resident f32 KV cache (with the Q8_0 quantisation of its output fused in),
+// the head argmax reduction and greedy acceptance.
+//
+// All f32 chains that the reference evaluates sequentially (the RMSNorm sum of
+// squares, each attention dot product, the softmax denominator, the weighted V
+// sum) are evaluated sequentially here too, so results match the reference's
+// portable path bit for bit; the parallel parts are the order-free ones (max,
+// elementwise maps, integer sums, independent rows/heads/positions).
+#include "nc_device.h"
+#include "nc_internal.h"
+
+namespace nc {
+
+// Writes the Q8_0 block (32 values, one per lane of a half-wave) quantised as
+// inference.rs:1012-1029, plus the block's int8 sum used by the GEMM.
+__device__ __forceinline__ void store_q8_block(float y, int lane32, int8_t* q_dst, float* s_dst, int32_t* sum_dst) {
+    const float amax = halfwave_amax(y);
+    float scale;
+    const int q = quantize_lane_q8(y, amax, &scale);
+    const int qs = halfwave_isum(q);
+    q_dst[lane32] = (int8_t)q;
+    if (lane32 == 0) {
+        *s_dst = scale;
+        *sum_dst = qs;
+    }
+}
+
+// ---------------------------------------------------------------- RMSNorm + Q8_0
+// rms_norm (inference.rs:697-706): sum += x*x sequentially, scale = 1/sqrt(sum/n + eps),
+// y = x*scale*w; then quantize_f32_to_q8_0 of y (inference.rs:3802-3808).
+__global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float* hidden, const float* weight, int d, float eps,
+                                                          int8_t* xq, float* xs, int32_t* xsum) {
+    extern __shared__ float sq[];  // d squares, then the scale
+    const int n = blockIdx.x;
+    const float* x = hidden + (size_t)n * d;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        const float v = x[i];
+        sq[i] = v * v;
+    }
+    __syncthreads();
+    __shared__ float s_scale;
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        const float4* s4 = (const float4*)sq;
+        for (int i = 0; i < d / 4; i++) {
+            const float4 v = s4[i];
+            sum = sum + v.x;
+            sum = sum + v.y;
+            sum = sum + v.z;
+            sum = sum + v.w;
+        }
+        s_scale = 1.0f / __builtin_sqrtf(sum / (float)d + eps);
+    }
+    __syncthreads();
+    const float scale = s_scale;
+    const int lane32 = threadIdx.x & 31;
+    const int half = threadIdx.x >> 5;  // 8 half-waves
+    for (int b = half; b < d / 32; b += blockDim.x / 32) {
+        const int i = b * 32 + lane32;
+        const float y = x[i] * scale * weight[i];
+        store_q8_block(y, lane32, xq + (size_t)n * d + b * 32, xs + (size_t)n * (d / 32) + b,
+                       xsum + (size_t)n * (d / 32) + b);
+    }
+}
+
+int launch_rmsnorm_q8(const float* hidden, const float* weight, int N, int d, float eps, int8_t* xq, float* xs,
+                      int32_t* xsum, hipStream_t st) {
+    if (d % 128) return fail(NC_EINVAL, "rmsnorm: width must be a multiple of 128");
+    hipLaunchKernelGGL(rmsnorm_q8_kernel, dim3(N), dim3(256), (size_t)d * sizeof(float), st, hidden, weight, d, eps,
+                       xq, xs, xsum);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+// ---------------------------------------------------------------- plain Q8_0 quantiser
+__global__ void quantize_q8_kernel(const float* x, int dim, int nblocks_total, int8_t* xq, float* xs, int32_t* xsum) {
+    const int gb = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;  // global block id
+    if (gb >= nblocks_total) return;                               // whole half-wave exits together
+    const int lane32 = threadIdx.x & 31;
+    const float y = x[(size_t)gb * 32 + lane32];
+    store_q8_block(y, lane32, xq + (size_t)gb * 32, xs + gb, xsum + gb);
+}
+
+int launch_quantize_q8(const float* x, int N, int dim, int8_t* xq, float* xs, int32_t* xsum, hipStream_t st) {
+    if (dim % 32) return fail(NC_EINVAL, "quantize: width must be a multiple of 32");
+    const int total = N * (dim / 32);
+    hipLaunchKernelGGL(quantize_q8_kernel, dim3((total * 32 + 255) / 256), dim3(256), 0, st, x, dim, total, xq, xs, xsum);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+__global__ void block_sums_kernel(const int8_t* x, int total_blocks, int32_t* xsum) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= total_blocks) return;
+    const int8_t* p = x + (size_t)b * 32;
+    int s = 0;
+    for (int j = 0; j < 32; j++) s += p[j];
+    xsum[b] = s;
+}
+
+int launch_block_sums(const int8_t* x, int N, int dim, int32_t* xsum, hipStream_t st) {
+    const int total = N * (dim / 32);
+    hipLaunchKernelGGL(block_sums_kernel, dim3((total + 255) / 256), dim3(256), 0, st, x, total, xsum);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+// ---------------------------------------------------------------- pass state
+// Start position and the batch's token ids travel as kernel arguments (copied at
+// launch), so back-to-back passes never race on a host staging buffer.
+__global__ void set_pass_state_kernel(int32_t* d_pos, int32_t pos, uint32_t* d_toks, TokenArgs toks, int n) {
+    const int i = threadIdx.x;
+    if (i == 0) d_pos[0] = pos;
+    if (i < n) d_toks[i] = toks.t[i];
+}
+
+int launch_set_pass_state(int32_t* d_pos, int32_t pos, uint32_t* d_toks, const uint32_t* toks, int n, hipStream_t st) {
+    TokenArgs a{};
+    for (int i = 0; i < n && i < 16; i++) a.t[i] = toks ? toks[i] : 0u;
+    hipLaunchKernelGGL(set_pass_state_kernel, dim3(1), dim3(64), 0, st, d_pos, pos, d_toks, a, toks ? n : 0);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+// ---------------------------------------------------------------- embedding gather
+__global__ void embed_kernel(const float* table, const uint32_t* toks, int d, float* hidden) {
+    const int n = blockIdx.y;
+    const size_t src = (size_t)toks[n] * d;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x)
+        hidden[(size_t)n * d + i] = table[src + i];
+}
+
+int launch_embed(const float* table, const uint32_t* toks, int N, int d, float* hidden, hipStream_t st) {
+    hipLaunchKernelGGL(embed_kernel, dim3((d + 255) / 256, N), dim3(256), 0, st, table, toks, d, hidden);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+// ---------------------------------------------------------------- attention
+// Phase 1: scores[n][h][p] = dot(q[n][h], k[p]) * scale for p <= pos_n
+// (inference.rs:4252-4257; dot_f32_scalar folds a*b from -0.0 in index order).
+// Workgroup = one KV head x 64 positions; wave g = query head kvh*G + g; lane = p.
+template <int HD>
+__global__ __launch_bounds__(1024) void attn_scores_kernel(AttnParams a) {
+    const int kvh = blockIdx.y;
+    const int G = a.H / a.Hkv;
+    const int g = wave_id_uniform();
+    if (g >= G) return;
+    const int h = kvh * G + g;
+    const int lane = threadIdx.x & 63;
+    const int pos0 = a.d_pos[0];
+    const int last = pos0 + a.N - 1;
+    for (int tile = blockIdx.x; tile * 64 <= last; tile += gridDim.x) {
+        const int p = tile * 64 + lane;
+        float k[HD];
+        if (p <= last) {
+            const float4* kp = (const float4*)(a.kcache + ((size_t)kvh * a.max_ctx + p) * HD);
+#pragma unroll
+            for (int i = 0; i < HD / 4; i++) {
+                const float4 v = kp[i];
+                k[4 * i] = v.x;
+                k[4 * i + 1] = v.y;
+                k[4 * i + 2] = v.z;
+                k[4 * i + 3] = v.w;
+            }
+        }
+        for (int n = 0; n < a.N; n++) {
+            if (tile * 64 > pos0 + n) continue;  // uniform: whole tile beyond this row
+            const float __attribute__((address_space(4)))* q =
+                (const float __attribute__((address_space(4)))*)(const void __attribute__((address_space(4)))*)(
+                    uintptr_t)(a.q + (size_t)n * a.H * HD + (size_t)h * HD);
+            float dot = -0.0f;
+#pragma unroll
+            for (int i = 0; i < HD; i++) dot = dot + q[i] * k[i];
+            if (p <= pos0 + n) a.scores[((size_t)n * a.H + h) * a.max_ctx + p] = dot * a.scale;
+        }
+    }
+}
+
+// Phase 2: softmax over 0..=pos (inference.rs:3522-3540): max, e = expf(s - max),
+// sequential sum, probabilities e * (1/sum) written back in place.
+__global__ __launch_bounds__(256) void attn_softmax_kernel(AttnParams a) {
+    extern __shared__ float e[];
+    const int unit = blockIdx.x;  // n * H + h
+    const int n = unit / a.H;
+    const int L = a.d_pos[0] + n + 1;
+    float* s = a.scores + (size_t)unit * a.max_ctx;
+    __shared__ float red[256];
+    float mx = -__builtin_inff();
+    for (int p = threadIdx.x; p < L; p += blockDim.x) {
+        const float v = s[p];
+        mx = v > mx ? v : mx;
+    }
+    red[threadIdx.x] = mx;
+    __syncthreads();
+    for (int off = 128; off >= 1; off >>= 1) {
+        if (threadIdx.x < off) {
+            const float o = red[threadIdx.x + off];
+            red[threadIdx.x] = o > red[threadIdx.x] ? o : red[threadIdx.x];
+        }
+        __syncthreads();
+    }
+    mx = red[0];
+    for (int p = threadIdx.x; p < L; p += blockDim.x) e[p] = expf_glibc(s[p] - mx);
+    __syncthreads();
+    __shared__ float s_inv;
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        int p = 0;
+        const float4* e4 = (const float4*)e;
+        for (; p + 4 <= L; p += 4) {
+            const float4 v = e4[p / 4];
+            sum = sum + v.x;
+            sum = sum + v.y;
+            sum = sum + v.z;
+            sum = sum + v.w;
+        }
+        for (; p < L; p++) sum = sum + e[p];
+        s_inv = 1.0f / sum;
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (int p = threadIdx.x; p < L; p += blockDim.x) s[p] = e[p] * inv;
+}
+
+// Phase 3: out[d] = sum_p prob_p * v_p[d] sequentially in p (add_weighted_f32_scalar,
+// inference.rs:3603-3623, starting from the zero-filled output), then the Q8_0
+// quantisation of the attention output row (inference.rs:3971-3977): each 32-lane
+// group holds exactly one quantisation block of (row n, head h).
+__global__ __launch_bounds__(256) void attn_pv_kernel(AttnParams a) {
+    const int kvh = blockIdx.x;
+    const int dchunk = blockIdx.y;
+    const int G = a.H / a.Hkv;
+    const int unit = blockIdx.z * 8 + (threadIdx.x >> 5);  // (n, g) pair
+    if (unit >= a.N * G) return;                         // whole half-wave exits together
+    const int n = unit / G, g = unit % G;
+    const int h = kvh * G + g;
+    const int lane32 = threadIdx.x & 31;
+    const int d = dchunk * 32 + lane32;
+    const int pos = a.d_pos[0] + n;
+    const float* prob = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
+    const float* v = a.vcache + (size_t)kvh * a.max_ctx * a.hd + d;
+    float acc = 0.0f;
+    for (int p = 0; p <= pos; p++) acc = acc + prob[p] * v[(size_t)p * a.hd];
+    const int aw = a.H * a.hd;
+    const int col = h * a.hd + dchunk * 32;
+    store_q8_block(acc, lane32, a.xq + (size_t)n * aw + col, a.xs + (size_t)n * (aw / 32) + col / 32,
+                   a.xsum + (size_t)n * (aw / 32) + col / 32);
+}
+
+int launch_attention(const AttnParams& a, hipStream_t st) {
+    const int G = a.H / a.Hkv;
+    if (G > 16 || a.H % a.Hkv) return fail(NC_EINVAL, "attention: at most 16 query heads per KV head supported");
+    const int tiles = (a.max_pos + 64) / 64;
+    if (a.hd == 128)
+        hipLaunchKernelGGL(attn_scores_kernel<128>, dim3(tiles, a.Hkv), dim3(64 * G), 0, st, a);
+    else if (a.hd == 64)
+        hipLaunchKernelGGL(attn_scores_kernel<64>, dim3(tiles, a.Hkv), dim3(64 * G), 0, st, a);
+    else
+        return fail(NC_EINVAL, "attention: head_dim must be 64 or 128");
+    NC_HIP(hipGetLastError());
+    const size_t lds = (size_t)(a.max_pos + 1) * sizeof(float);
+    if (lds > 160 * 1024) return fail(NC_ERANGE, "attention: context too long for the softmax kernel");
+    hipLaunchKernelGGL(attn_softmax_kernel, dim3(a.N * a.H), dim3(256), lds, st, a);
+    NC_HIP(hipGetLastError());
+    hipLaunchKernelGGL(attn_pv_kernel, dim3(a.Hkv, a.hd / 32, (a.N * G + 7) / 8), dim3(256), 0, st, a);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+// ---------------------------------------------------------------- head argmax + acceptance
+// First maximum over the per-tile partials (tiles are in row order).
+__global__ void argmax_final_kernel(const float* pv, const int32_t* pi, int ntiles, uint32_t* preds) {
+    const int n = blockIdx.x;
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    for (int t = threadIdx.x; t < ntiles; t += blockDim.x) {
+        const float v = pv[(size_t)n * ntiles + t];
+        const int i = pi[(size_t)n * ntiles + t];
+        if (v > bv || (v == bv && i < bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int off = 128; off >= 1; off >>= 1) {
+        if (threadIdx.x < off) {
+            const float ov = sv[threadIdx.x + off];
+            const int oi = si[threadIdx.x + off];
+            if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
+                sv[threadIdx.x] = ov;
+                si[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) preds[n] = (uint32_t)(si[0] == 0x7fffffff ? 0 : si[0]);
+}
+
+int launch_argmax_final(const float* part_val, const int32_t* part_idx, int N, int ntiles, uint32_t* preds,
+                        hipStream_t st) {
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(N), dim3(256), 0, st, part_val, part_idx, ntiles, preds);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+// cluster_tcp_smoke.rs:954-979: accepted = longest prefix with draft[i] == pred[i],
+// next = pred[accepted], pos += accepted + 1.  result = {accepted, next, new_pos}.
+__global__ void accept_greedy_kernel(const uint32_t* toks, const uint32_t* preds, int n, int32_t* d_pos,
+                                     int32_t* result, uint32_t* next_tok_slot) {
+    if (threadIdx.x != 0) return;
+    int a = 0;
+    while (a < n - 1 && toks[a + 1] == preds[a]) a++;
+    const uint32_t next = preds[a];
+    const int np = d_pos[0] + a + 1;
+    result[0] = a;
+    result[1] = (int32_t)next;
+    result[2] = np;
+    d_pos[0] = np;
+    if (next_tok_slot) next_tok_slot[0] = next;
+}
+
+int launch_accept_greedy(const uint32_t* toks, const uint32_t* preds, int n, int32_t* d_pos, int32_t* result,
+                         uint32_t* next_tok_slot, hipStream_t st) {
+    hipLaunchKernelGGL(accept_greedy_kernel, dim3(1), dim3(64), 0, st, toks, preds, n, d_pos, result, next_tok_slot);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+}  // namespace nc

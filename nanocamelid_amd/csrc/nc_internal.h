@@ -1,0 +1,125 @@
+// Host-side internals of libnanocamelid_hip (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/nanocamelid_gpu.h"
+
+namespace nc {
+
+// ---------------------------------------------------------------- errors
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+
+#define NC_HIP(call)                                                                   \
+    do {                                                                               \
+        hipError_t _e = (call);                                                        \
+        if (_e != hipSuccess)                                                          \
+            return ::nc::fail(NC_EHIP, std::string(#call) + ": " + hipGetErrorString(_e)); \
+    } while (0)
+
+// ---------------------------------------------------------------- weight layouts
+// Q4_0 device layout ("tile-group"): rows padded to 64-row tiles; per (tile, group of 8
+// blocks) a 9216-byte chunk = 8 x [64 lanes x 16 B nibbles] followed by [64 lanes x 8 f16
+// scales].  Lane l of a wave loads row 64*tile + l; every load is 1 KB contiguous.
+constexpr int kTileRows = 64;
+constexpr int kQ40GroupBlocks = 8;
+constexpr int kQ40ChunkBytes = kQ40GroupBlocks * 1024 + 1024;  // 9216
+// Q4_K device layout: per (tile, super-block) 9 x [64 lanes x 16 B]: slot 0 = d, dmin and
+// the 12 packed scale bytes, slots 1..8 = the 128 nibble bytes.
+constexpr int kQ4KChunkBytes = 9 * 1024;
+
+struct QMatDev {
+    int type = NC_TYPE_Q4_0;
+    int64_t rows = 0, cols = 0;
+    int64_t tiles = 0;       // padded rows / 64
+    int64_t units = 0;       // Q4_0: blocks per row; Q4_K: super-blocks per row
+    int64_t groups = 0;      // Q4_0: ceil(blocks / 8)
+    uint8_t* dev = nullptr;  // repacked bytes
+    int64_t dev_bytes = 0;
+    int64_t algo_bytes = 0;  // rows * cols * 18/32 (Q4_0) or 144/256 (Q4_K)
+};
+
+// Repacks row-major GGUF blocks of `rows_src` rows into the device layout, writing tile
+// rows [row_off, row_off + rows_src) of `dst` (host staging buffer of the whole matrix).
+// interleave_pairs: rows_src rows are the gate half (tile lanes 0..31) or up half
+// (lanes 32..63) of an interleaved SwiGLU matrix (half = 0 or 1), else -1.
+void repack_q4_0(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups,
+                 int64_t row_off, int half);
+void repack_q4_k(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t row_off, int half);
+int64_t q40_layout_bytes(int64_t rows, int64_t cols);
+int64_t q4k_layout_bytes(int64_t rows, int64_t cols);
+
+// ---------------------------------------------------------------- GEMM launch
+enum Epi : int {
+    EPI_STORE = 0,      // out[n*ld + row] = acc
+    EPI_RESIDUAL = 1,   // out[n*ld + row] = acc + out[n*ld + row]
+    EPI_QKV_ROPE = 2,   // RoPE on q/k rows, q -> q_out, k/v -> KV cache
+    EPI_SWIGLU_Q8 = 3,  // silu(gate)*up then Q8_0 quantisation -> activations
+    EPI_HEAD = 4,       // logits + per-tile argmax partials
+};
+
+struct GemmParams {
+    const uint8_t* w = nullptr;
+    int ntiles = 0, units = 0, groups = 0, M = 0, K = 0, N = 0;
+    const int8_t* x = nullptr;     // [N][K]
+    const float* xs = nullptr;     // [N][K/32]
+    const int32_t* xsum = nullptr; // [N][K/32] sum of the 32 int8 values of each block
+    int epi = EPI_STORE;
+    float* out = nullptr;
+    int ld_out = 0;
+    // EPI_QKV_ROPE
+    float* q_out = nullptr;
+    int aw = 0, kw = 0, hd = 0, rope_half = 0, max_ctx = 0, kv_heads = 0;
+    const float* rope_tab = nullptr;  // [max_ctx][rope_half][2] = (sin, cos)
+    float* kcache = nullptr;          // layer base of [kv_heads][max_ctx][hd]
+    float* vcache = nullptr;
+    const int32_t* d_pos = nullptr;   // start position of row 0
+    // EPI_SWIGLU_Q8
+    int8_t* xq_out = nullptr;
+    float* xs_out = nullptr;
+    int32_t* xsum_out = nullptr;
+    int F = 0;
+    // EPI_HEAD
+    float* part_val = nullptr;  // [N][ntiles]
+    int32_t* part_idx = nullptr;
+};
+
+int launch_gemm(const QMatDev& w, const GemmParams& p, hipStream_t stream);
+int launch_blockdots(const QMatDev& w, const int8_t* x, int32_t* dots, int N, hipStream_t stream);
+
+// ---------------------------------------------------------------- layer kernels
+int launch_rmsnorm_q8(const float* hidden, const float* weight, int N, int d, float eps, int8_t* xq, float* xs,
+                      int32_t* xsum, hipStream_t stream);
+int launch_quantize_q8(const float* x, int N, int dim, int8_t* xq, float* xs, int32_t* xsum, hipStream_t stream);
+int launch_block_sums(const int8_t* x, int N, int dim, int32_t* xsum, hipStream_t stream);
+struct TokenArgs {
+    uint32_t t[16];
+};
+// Writes d_pos[0] = pos and, when toks != NULL, d_toks[0..n) = toks (n <= 16).
+int launch_set_pass_state(int32_t* d_pos, int32_t pos, uint32_t* d_toks, const uint32_t* toks, int n, hipStream_t st);
+int launch_embed(const float* table, const uint32_t* toks, int N, int d, float* hidden, hipStream_t stream);
+struct AttnParams {
+    const float* q = nullptr;  // [N][H*hd]
+    const float* kcache = nullptr;  // layer base [Hkv][max_ctx][hd]
+    const float* vcache = nullptr;
+    float* scores = nullptr;  // [N][H][max_ctx]
+    int8_t* xq = nullptr;     // [N][H*hd] quantised attention output
+    float* xs = nullptr;
+    int32_t* xsum = nullptr;
+    const int32_t* d_pos = nullptr;
+    int N = 0, H = 0, Hkv = 0, hd = 0, max_ctx = 0, max_pos = 0;
+    float scale = 0.f;
+};
+int launch_attention(const AttnParams& a, hipStream_t stream);
+int launch_argmax_final(const float* part_val, const int32_t* part_idx, int N, int ntiles, uint32_t* preds,
+                        hipStream_t stream);
+int launch_accept_greedy(const uint32_t* toks, const uint32_t* preds, int n, int32_t* d_pos, int32_t* result,
+                         uint32_t* next_tok_slot, hipStream_t stream);
+
+}  // namespace nc

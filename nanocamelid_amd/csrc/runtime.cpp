@@ -1,0 +1,1097 @@
+// Host runtime of libnanocamelid_hip: device context, weight repacking and upload,
+// the Llama model loader, sessions (KV cache + workspaces + stream), the verify pass,
+// the decode loops and the C ABI declared in include/nanocamelid_gpu.h.
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <thread>
+
+#include "gguf.h"
+#include "nc_internal.h"
+
+// ---------------------------------------------------------------- handles
+struct nc_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int32_t* xsum = nullptr;  // grow-only scratch for the operator-level entry points
+    size_t xsum_cap = 0;
+};
+
+struct nc_qmat {
+    nc_ctx* ctx = nullptr;
+    nc::QMatDev m;
+};
+
+namespace {
+
+struct LayerDev {
+    float* attn_norm = nullptr;
+    float* ffn_norm = nullptr;
+    nc::QMatDev qkv, wo, gateup, down;
+};
+
+}  // namespace
+
+struct nc_model {
+    nc_ctx* ctx = nullptr;
+    nc_model_config cfg{};
+    float* tok_emb = nullptr;  // [V][d] f32 (model.rs:467 token_embeddings)
+    float* out_norm = nullptr;
+    nc::QMatDev head;
+    std::vector<LayerDev> layers;
+    std::vector<void*> allocs;
+};
+
+struct nc_session {
+    nc_model* m = nullptr;
+    nc_ctx* ctx = nullptr;
+    hipStream_t stream = nullptr;
+    int64_t max_ctx = 0;
+    int max_batch = 0;
+    int64_t maxw = 0;
+    float *kcache = nullptr, *vcache = nullptr;  // [L][Hkv][max_ctx][hd]
+    float* hidden = nullptr;                     // [B][d]
+    int8_t* xq = nullptr;                        // [B][maxw]
+    float* xs = nullptr;                         // [B][maxw/32]
+    int32_t* xsum = nullptr;
+    float* q = nullptr;       // [B][aw]
+    float* scores = nullptr;  // [B][H][max_ctx]
+    float* logits = nullptr;  // [B][V]
+    float* part_val = nullptr;
+    int32_t* part_idx = nullptr;
+    uint32_t* d_toks = nullptr;
+    uint32_t* d_preds = nullptr;
+    int32_t* d_pos = nullptr;
+    int32_t* d_result = nullptr;
+    float* rope_tab = nullptr;
+    // pinned host mirrors
+    uint32_t* h_toks = nullptr;
+    uint32_t* h_preds = nullptr;
+    int32_t* h_result = nullptr;
+    int32_t* h_pos = nullptr;
+    int last_n = 0;
+    uint32_t staged[16] = {};
+    bool pending_toks = false;
+    // per-kernel timing (HIP events on the session stream)
+    bool timing = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
+    size_t ev_used = 0;
+    double gemm_ms = 0.0;
+    int64_t gemm_launches = 0, gemm_bytes = 0, pending_bytes = 0;
+    std::vector<void*> allocs;
+};
+
+namespace nc {
+
+// ---------------------------------------------------------------- errors
+static thread_local std::string t_err;
+void set_error(const std::string& msg) { t_err = msg; }
+int fail(int code, const std::string& msg) {
+    t_err = msg;
+    return code;
+}
+
+static void parallel_for(int64_t n, int nthreads, const std::function<void(int64_t, int64_t)>& fn) {
+    if (nthreads <= 0) nthreads = (int)std::max(1u, std::thread::hardware_concurrency());
+    if (n < 1024 || nthreads == 1) {
+        fn(0, n);
+        return;
+    }
+    std::vector<std::thread> th;
+    const int64_t chunk = (n + nthreads - 1) / nthreads;
+    for (int t = 0; t < nthreads; t++) {
+        const int64_t lo = t * chunk, hi = std::min(n, lo + chunk);
+        if (lo >= hi) break;
+        th.emplace_back([&fn, lo, hi] { fn(lo, hi); });
+    }
+    for (auto& t : th) t.join();
+}
+
+// ---------------------------------------------------------------- repacking
+int64_t q40_layout_bytes(int64_t rows, int64_t cols) {
+    const int64_t tiles = (rows + 63) / 64, groups = (cols / 32 + 7) / 8;
+    return tiles * groups * kQ40ChunkBytes;
+}
+int64_t q4k_layout_bytes(int64_t rows, int64_t cols) { return (rows + 63) / 64 * (cols / 256) * kQ4KChunkBytes; }
+
+static inline int64_t dst_row(int64_t r, int64_t row_off, int half) {
+    return half < 0 ? row_off + r : (r / 32) * 64 + (r % 32) + 32 * half;
+}
+
+void repack_q4_0(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups, int64_t row_off,
+                 int half) {
+    const int64_t nb = cols / 32;
+    parallel_for(rows_src, 0, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; r++) {
+            const int64_t R = dst_row(r, row_off, half);
+            const int64_t t = R / 64, l = R % 64;
+            for (int64_t b = 0; b < nb; b++) {
+                const uint8_t* blk = src + (r * nb + b) * 18;
+                uint8_t* chunk = dst + (t * groups + b / 8) * kQ40ChunkBytes;
+                std::memcpy(chunk + (b % 8) * 1024 + l * 16, blk + 2, 16);
+                std::memcpy(chunk + 8192 + l * 16 + (b % 8) * 2, blk, 2);
+            }
+        }
+    });
+}
+
+void repack_q4_k(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t row_off, int half) {
+    const int64_t nsb = cols / 256;
+    parallel_for(rows_src, 0, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; r++) {
+            const int64_t R = dst_row(r, row_off, half);
+            const int64_t t = R / 64, l = R % 64;
+            for (int64_t s = 0; s < nsb; s++) {
+                const uint8_t* blk = src + (r * nsb + s) * 144;
+                uint8_t* chunk = dst + (t * nsb + s) * kQ4KChunkBytes;
+                for (int i = 0; i < 9; i++) std::memcpy(chunk + i * 1024 + l * 16, blk + i * 16, 16);
+            }
+        }
+    });
+}
+
+struct Part {
+    const uint8_t* src;
+    int64_t rows;
+    int64_t row_off;
+    int half;
+};
+
+// Builds one device matrix from one or more GGUF row blocks (fused q|k|v, interleaved
+// gate/up, or a single matrix).
+static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector<Part>& parts, QMatDev& out) {
+    if (cols % 32 || (type == NC_TYPE_Q4_K && cols % 256))
+        return fail(NC_EINVAL, "matrix columns must be a multiple of 32 (Q4_K: 256)");
+    out.type = type;
+    out.rows = rows;
+    out.cols = cols;
+    out.tiles = (rows + 63) / 64;
+    out.units = type == NC_TYPE_Q4_0 ? cols / 32 : cols / 256;
+    out.groups = type == NC_TYPE_Q4_0 ? (out.units + 7) / 8 : 0;
+    out.dev_bytes = type == NC_TYPE_Q4_0 ? q40_layout_bytes(rows, cols) : q4k_layout_bytes(rows, cols);
+    out.algo_bytes = type == NC_TYPE_Q4_0 ? rows * cols / 32 * 18 : rows * cols / 256 * 144;
+    std::vector<uint8_t> host(out.dev_bytes, 0);
+    for (const auto& p : parts) {
+        if (type == NC_TYPE_Q4_0) repack_q4_0(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
+        else repack_q4_k(p.src, p.rows, cols, host.data(), p.row_off, p.half);
+    }
+    NC_HIP(hipMalloc((void**)&out.dev, out.dev_bytes));
+    NC_HIP(hipMemcpy(out.dev, host.data(), out.dev_bytes, hipMemcpyHostToDevice));
+    return NC_OK;
+}
+
+// ---------------------------------------------------------------- f16 helpers (host)
+static inline float f16_to_f32_host(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// q8.rs:3644-3673 fast_f32_to_f16 (truncating), used by the tied-head requantisation.
+static uint16_t f32_to_f16_trunc(float value) {
+    uint32_t bits;
+    std::memcpy(&bits, &value, 4);
+    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    const int32_t exponent = (int32_t)((bits >> 23) & 0xffu);
+    const uint32_t fraction = bits & 0x007fffffu;
+    if (exponent == 0) return sign;
+    if (exponent == 0xff) return (uint16_t)(sign | 0x7c00u | (fraction ? ((fraction >> 13) | 1u) : 0u));
+    const int32_t he = exponent - 127 + 15;
+    if (he >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+    if (he <= 0) {
+        if (he < -10) return sign;
+        return (uint16_t)(sign | (uint16_t)((fraction | 0x00800000u) >> (14 - he)));
+    }
+    return (uint16_t)(sign | (uint16_t)(he << 10) | (uint16_t)(fraction >> 13));
+}
+
+// Rust `f32 as i32` (saturating truncation, NaN -> 0).
+static inline int32_t f32_as_i32(float v) {
+    if (v != v) return 0;
+    if (v >= 2147483648.0f) return INT32_MAX;
+    if (v <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)v;
+}
+
+// quantize_f32_matrix_to_q4_0_blocks (q8.rs:2442-2488) for the tied LM head.
+static void requant_tied_head(const float* emb, int64_t rows, int64_t cols, uint8_t* out) {
+    const int64_t bpr = cols / 32;
+    parallel_for(rows, 0, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; r++)
+            for (int64_t b = 0; b < bpr; b++) {
+                const float* c = emb + r * cols + b * 32;
+                float amax = 0.0f, mx = 0.0f;
+                for (int i = 0; i < 32; i++) {
+                    const float a = std::fabs(c[i]);
+                    if (a > amax) {
+                        amax = a;
+                        mx = c[i];
+                    }
+                }
+                const float d = mx / -8.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                uint8_t* blk = out + (r * bpr + b) * 18;
+                const uint16_t sb = f32_to_f16_trunc(d);
+                blk[0] = (uint8_t)(sb & 0xff);
+                blk[1] = (uint8_t)(sb >> 8);
+                for (int j = 0; j < 16; j++) {
+                    const float x0 = c[j] * id + 8.5f, x1 = c[j + 16] * id + 8.5f;
+                    int q0 = f32_as_i32(x0), q1 = f32_as_i32(x1);
+                    q0 = q0 < 0 ? 0 : (q0 > 15 ? 15 : q0);
+                    q1 = q1 < 0 ? 0 : (q1 > 15 ? 15 : q1);
+                    blk[2 + j] = (uint8_t)(q0 | (q1 << 4));
+                }
+            }
+    });
+}
+
+// load_f32_or_f16 (model.rs:1081-1230) for the types this path meets.
+static int tensor_to_f32(const GgufFile& g, const std::string& name, std::vector<float>& out) {
+    const GgufTensor* t = g.find(name);
+    if (!t) return fail(NC_EFORMAT, "missing tensor " + name);
+    uint64_t el = 1;
+    for (auto d : t->dims) el *= d;
+    out.resize(el);
+    const uint8_t* p = g.data + t->offset;
+    if (t->type == NC_TYPE_F32) {
+        std::memcpy(out.data(), p, el * 4);
+    } else if (t->type == 1) {
+        for (uint64_t i = 0; i < el; i++) out[i] = f16_to_f32_host((uint16_t)(p[2 * i] | (p[2 * i + 1] << 8)));
+    } else if (t->type == NC_TYPE_Q4_0) {
+        parallel_for((int64_t)(el / 32), 0, [&](int64_t lo, int64_t hi) {
+            for (int64_t b = lo; b < hi; b++) {
+                const uint8_t* blk = p + b * 18;
+                const float sc = f16_to_f32_host((uint16_t)(blk[0] | (blk[1] << 8)));
+                for (int j = 0; j < 16; j++) {
+                    out[b * 32 + j] = (float)((int)(blk[2 + j] & 0x0f) - 8) * sc;
+                    out[b * 32 + 16 + j] = (float)((int)(blk[2 + j] >> 4) - 8) * sc;
+                }
+            }
+        });
+    } else if (t->type == NC_TYPE_Q4_K) {
+        // Q4KBlock::dequantize (q8.rs:1233-1264)
+        parallel_for((int64_t)(el / 256), 0, [&](int64_t lo, int64_t hi) {
+            for (int64_t b = lo; b < hi; b++) {
+                const uint8_t* blk = p + b * 144;
+                const float d = f16_to_f32_host((uint16_t)(blk[0] | (blk[1] << 8)));
+                const float dmin = f16_to_f32_host((uint16_t)(blk[2] | (blk[3] << 8)));
+                const uint8_t* sc = blk + 4;
+                const uint8_t* qs = blk + 16;
+                auto smin = [&](int j, uint8_t* s, uint8_t* m) {
+                    if (j < 4) {
+                        *s = sc[j] & 63;
+                        *m = sc[j + 4] & 63;
+                    } else {
+                        *s = (uint8_t)((sc[j + 4] & 0x0f) | ((sc[j - 4] >> 6) << 4));
+                        *m = (uint8_t)((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
+                    }
+                };
+                float* o = out.data() + b * 256;
+                for (int pr = 0; pr < 4; pr++) {
+                    uint8_t ls, lm, hs, hm;
+                    smin(2 * pr, &ls, &lm);
+                    smin(2 * pr + 1, &hs, &hm);
+                    const float lsc = d * (float)ls, hsc = d * (float)hs;
+                    const float lmn = dmin * (float)lm, hmn = dmin * (float)hm;
+                    for (int l = 0; l < 32; l++) {
+                        const uint8_t byte = qs[pr * 32 + l];
+                        o[pr * 64 + l] = lsc * (float)(byte & 0x0f) - lmn;
+                        o[pr * 64 + 32 + l] = hsc * (float)(byte >> 4) - hmn;
+                    }
+                }
+            }
+        });
+    } else {
+        return fail(NC_EFORMAT, "tensor " + name + ": unsupported type for an f32 load");
+    }
+    return NC_OK;
+}
+
+template <typename T>
+static int dev_alloc(std::vector<void*>& list, T** p, size_t count) {
+    if (count == 0) count = 1;
+    hipError_t e = hipMalloc((void**)p, count * sizeof(T));
+    if (e != hipSuccess) return fail(NC_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    list.push_back(*p);
+    return NC_OK;
+}
+
+static int upload_f32(std::vector<void*>& list, const std::vector<float>& h, float** d) {
+    int rc = dev_alloc(list, d, h.size());
+    if (rc) return rc;
+    NC_HIP(hipMemcpy(*d, h.data(), h.size() * 4, hipMemcpyHostToDevice));
+    return NC_OK;
+}
+
+static const GgufTensor* matrix_desc(const GgufFile& g, const std::string& name, int64_t rows, int64_t cols, int* err) {
+    const GgufTensor* t = g.find(name);
+    if (!t) {
+        *err = fail(NC_EFORMAT, "missing tensor " + name);
+        return nullptr;
+    }
+    if (t->dims.size() != 2 || (int64_t)t->dims[0] != cols || (int64_t)t->dims[1] != rows) {
+        *err = fail(NC_EFORMAT, "tensor " + name + " has an unexpected shape");
+        return nullptr;
+    }
+    if (t->type != NC_TYPE_Q4_0 && t->type != NC_TYPE_Q4_K) {
+        *err = fail(NC_EFORMAT, "tensor " + name + ": only Q4_0 and Q4_K matrices are supported");
+        return nullptr;
+    }
+    return t;
+}
+
+static void free_model(nc_model* m) {
+    if (!m) return;
+    for (void* p : m->allocs) (void)hipFree(p);
+    if (m->head.dev) (void)hipFree(m->head.dev);
+    for (auto& l : m->layers)
+        for (auto* q : {&l.qkv, &l.wo, &l.gateup, &l.down})
+            if (q->dev) (void)hipFree(q->dev);
+    delete m;
+}
+
+static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_load_opts* opts, nc_model** out) {
+    GgufFile g;
+    std::string err;
+    if (!gguf_parse(data, size, g, err)) return fail(NC_EFORMAT, err);
+    if (g.get_str("general.architecture") != "llama")
+        return fail(NC_EFORMAT, "unsupported architecture: " + g.get_str("general.architecture"));
+    std::unique_ptr<nc_model, void (*)(nc_model*)> m(new nc_model(), free_model);
+    m->ctx = ctx;
+    nc_model_config& c = m->cfg;
+    // LlamaModelConfig::from_gguf (model.rs:48-186)
+    uint32_t v;
+    const std::string P = "llama.";
+    if (!g.get_u32(P + "context_length", &v)) return fail(NC_EFORMAT, "missing llama.context_length");
+    c.context_length = v;
+    if (!g.get_u32(P + "embedding_length", &v)) return fail(NC_EFORMAT, "missing llama.embedding_length");
+    c.embedding_length = v;
+    if (!g.get_u32(P + "block_count", &v)) return fail(NC_EFORMAT, "missing llama.block_count");
+    c.block_count = v;
+    if (!g.get_u32(P + "feed_forward_length", &v)) return fail(NC_EFORMAT, "missing llama.feed_forward_length");
+    c.feed_forward_length = v;
+    if (!g.get_u32(P + "attention.head_count", &v) || v == 0) return fail(NC_EFORMAT, "bad attention.head_count");
+    c.head_count = v;
+    c.head_count_kv = g.get_u32(P + "attention.head_count_kv", &v) ? v : c.head_count;
+    if (c.embedding_length % c.head_count || c.head_count_kv == 0 || c.head_count % c.head_count_kv)
+        return fail(NC_EFORMAT, "inconsistent head geometry");
+    float f;
+    c.rope_freq_base = g.get_f32(P + "rope.freq_base", &f) ? f : 10000.0f;
+    c.rms_norm_epsilon = g.get_f32(P + "attention.layer_norm_rms_epsilon", &f) ? f : 1e-5f;
+    const GgufTensor* te = g.find("token_embd.weight");
+    if (!te || te->dims.size() != 2) return fail(NC_EFORMAT, "missing token_embd.weight");
+    c.vocab_size = g.get_u32(P + "vocab_size", &v) ? v
+                   : ((int64_t)te->dims[0] == c.embedding_length ? (int64_t)te->dims[1] : (int64_t)te->dims[0]);
+    c.head_dim = g.get_u32(P + "attention.key_length", &v) ? v : c.embedding_length / c.head_count;
+    c.rope_dimension_count = g.get_u32(P + "rope.dimension_count", &v) ? v : c.head_dim;
+    if (c.rope_dimension_count == 0 || c.rope_dimension_count > c.head_dim || c.rope_dimension_count % 2)
+        return fail(NC_EFORMAT, "invalid rope.dimension_count");
+    c.attention_output_width = c.head_count * c.head_dim;
+    c.kv_width = c.head_count_kv * c.head_dim;
+    const int64_t d = c.embedding_length, F = c.feed_forward_length, V = c.vocab_size;
+    const int64_t aw = c.attention_output_width, kw = c.kv_width;
+    if (aw % 64 || kw % 64 || F % 32 || d % 256)
+        return fail(NC_EINVAL, "model widths must be multiples of 64 (attention), 32 (ffn), 256 (embedding)");
+    if (c.head_dim != 64 && c.head_dim != 128) return fail(NC_EINVAL, "head_dim must be 64 or 128");
+    // weights (LlamaWeights::load, model.rs:461-545)
+    std::vector<float> emb;
+    int rc = tensor_to_f32(g, "token_embd.weight", emb);
+    if (rc) return rc;
+    if ((int64_t)emb.size() != V * d) return fail(NC_EFORMAT, "token_embd.weight size mismatch");
+    if ((rc = upload_f32(m->allocs, emb, &m->tok_emb))) return rc;
+    std::vector<float> tmp;
+    if ((rc = tensor_to_f32(g, "output_norm.weight", tmp))) return rc;
+    if ((int64_t)tmp.size() != d) return fail(NC_EFORMAT, "output_norm.weight size mismatch");
+    if ((rc = upload_f32(m->allocs, tmp, &m->out_norm))) return rc;
+    if (const GgufTensor* ot = g.find("output.weight")) {
+        int e = 0;
+        if (!matrix_desc(g, "output.weight", V, d, &e)) return e;
+        if ((rc = upload_matrix((int)ot->type, V, d, {{g.data + ot->offset, V, 0, -1}}, m->head))) return rc;
+        c.tied_head = 0;
+    } else {
+        // model.rs:471-532: tied head requantised to Q4_0 from the f32 embeddings
+        std::vector<uint8_t> blocks((size_t)V * (d / 32) * 18);
+        requant_tied_head(emb.data(), V, d, blocks.data());
+        if ((rc = upload_matrix(NC_TYPE_Q4_0, V, d, {{blocks.data(), V, 0, -1}}, m->head))) return rc;
+        c.tied_head = 1;
+    }
+    emb.clear();
+    emb.shrink_to_fit();
+    m->layers.resize(c.block_count);
+    int wtype = -1;
+    for (int64_t i = 0; i < c.block_count; i++) {
+        LayerDev& L = m->layers[i];
+        const std::string b = "blk." + std::to_string(i) + ".";
+        if ((rc = tensor_to_f32(g, b + "attn_norm.weight", tmp))) return rc;
+        if ((rc = upload_f32(m->allocs, tmp, &L.attn_norm))) return rc;
+        if ((rc = tensor_to_f32(g, b + "ffn_norm.weight", tmp))) return rc;
+        if ((rc = upload_f32(m->allocs, tmp, &L.ffn_norm))) return rc;
+        int e = 0;
+        const GgufTensor* tq = matrix_desc(g, b + "attn_q.weight", aw, d, &e);
+        const GgufTensor* tk = tq ? matrix_desc(g, b + "attn_k.weight", kw, d, &e) : nullptr;
+        const GgufTensor* tv = tk ? matrix_desc(g, b + "attn_v.weight", kw, d, &e) : nullptr;
+        const GgufTensor* to = tv ? matrix_desc(g, b + "attn_output.weight", d, aw, &e) : nullptr;
+        const GgufTensor* tg = to ? matrix_desc(g, b + "ffn_gate.weight", F, d, &e) : nullptr;
+        const GgufTensor* tu = tg ? matrix_desc(g, b + "ffn_up.weight", F, d, &e) : nullptr;
+        const GgufTensor* tdn = tu ? matrix_desc(g, b + "ffn_down.weight", d, F, &e) : nullptr;
+        if (!tdn) return e;
+        const int ty = (int)tq->type;
+        if (tk->type != (uint32_t)ty || tv->type != (uint32_t)ty || tg->type != tu->type)
+            return fail(NC_EFORMAT, "q/k/v (and gate/up) must share one quantisation type");
+        if ((rc = upload_matrix(ty, aw + 2 * kw, d,
+                                {{g.data + tq->offset, aw, 0, -1}, {g.data + tk->offset, kw, aw, -1},
+                                 {g.data + tv->offset, kw, aw + kw, -1}},
+                                L.qkv)))
+            return rc;
+        if ((rc = upload_matrix((int)to->type, d, aw, {{g.data + to->offset, d, 0, -1}}, L.wo))) return rc;
+        if ((rc = upload_matrix((int)tg->type, 2 * F, d, {{g.data + tg->offset, F, 0, 0}, {g.data + tu->offset, F, 0, 1}},
+                                L.gateup)))
+            return rc;
+        if ((rc = upload_matrix((int)tdn->type, d, F, {{g.data + tdn->offset, d, 0, -1}}, L.down))) return rc;
+        wtype = ty;
+    }
+    c.weight_type = wtype;
+    int64_t devb = m->head.dev_bytes, algo = m->head.algo_bytes;
+    for (auto& L : m->layers)
+        for (auto* q : {&L.qkv, &L.wo, &L.gateup, &L.down}) {
+            devb += q->dev_bytes;
+            algo += q->algo_bytes;
+        }
+    c.device_weight_bytes = devb;
+    c.verify_weight_bytes = algo;
+    (void)opts;
+    *out = m.release();
+    return NC_OK;
+}
+
+// ---------------------------------------------------------------- session pass
+static int timed_gemm(nc_session* s, const QMatDev& w, const GemmParams& p) {
+    if (!s->timing) return launch_gemm(w, p, s->stream);
+    if (s->ev_used == s->ev.size()) {
+        NC_HIP(hipStreamSynchronize(s->stream));
+        for (auto& e : s->ev) {
+            float ms = 0;
+            NC_HIP(hipEventElapsedTime(&ms, e.first, e.second));
+            s->gemm_ms += ms;
+        }
+        s->gemm_bytes += s->pending_bytes;
+        s->pending_bytes = 0;
+        s->ev_used = 0;
+    }
+    auto& e = s->ev[s->ev_used++];
+    NC_HIP(hipEventRecord(e.first, s->stream));
+    int rc = launch_gemm(w, p, s->stream);
+    NC_HIP(hipEventRecord(e.second, s->stream));
+    s->gemm_launches++;
+    // algorithmic bytes: weights + int8 activations + f32 scales + f32 outputs
+    s->pending_bytes += w.algo_bytes + (int64_t)p.N * w.cols + 4 * (int64_t)p.N * (w.cols / 32) + 4 * (int64_t)p.N * w.rows;
+    return rc;
+}
+
+static int flush_timing(nc_session* s) {
+    if (!s->timing || s->ev_used == 0) return NC_OK;
+    NC_HIP(hipStreamSynchronize(s->stream));
+    for (size_t i = 0; i < s->ev_used; i++) {
+        float ms = 0;
+        NC_HIP(hipEventElapsedTime(&ms, s->ev[i].first, s->ev[i].second));
+        s->gemm_ms += ms;
+    }
+    s->gemm_bytes += s->pending_bytes;
+    s->pending_bytes = 0;
+    s->ev_used = 0;
+    return NC_OK;
+}
+
+// One forward over the n tokens already in d_toks at positions start_pos..: embedding,
+// all layers (run_layer_range_batch, inference.rs:3747-4111), final norm, head and
+// per-row argmax.  Writes d_preds and logits.
+static int run_pass(nc_session* s, int n, int64_t start_pos) {
+    nc_model* m = s->m;
+    const nc_model_config& c = m->cfg;
+    const int d = (int)c.embedding_length, aw = (int)c.attention_output_width, kw = (int)c.kv_width;
+    const int F = (int)c.feed_forward_length, hd = (int)c.head_dim, Hkv = (int)c.head_count_kv;
+    if (n < 1 || n > s->max_batch) return fail(NC_ERANGE, "batch exceeds the session's max_batch");
+    if (start_pos < 0 || start_pos + n > s->max_ctx) return fail(NC_ERANGE, "batch end exceeds the session context");
+    hipStream_t st = s->stream;
+    int rc = launch_set_pass_state(s->d_pos, (int32_t)start_pos, s->d_toks, s->pending_toks ? s->staged : nullptr, n, st);
+    if (rc) return rc;
+    s->pending_toks = false;
+    rc = launch_embed(m->tok_emb, s->d_toks, n, d, s->hidden, st);
+    if (rc) return rc;
+    const size_t layer_kv = (size_t)Hkv * s->max_ctx * hd;
+    for (int64_t li = 0; li < c.block_count; li++) {
+        const LayerDev& L = m->layers[li];
+        if ((rc = launch_rmsnorm_q8(s->hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xsum, st)))
+            return rc;
+        GemmParams p;
+        p.x = s->xq;
+        p.xs = s->xs;
+        p.xsum = s->xsum;
+        p.N = n;
+        p.epi = EPI_QKV_ROPE;
+        p.q_out = s->q;
+        p.aw = aw;
+        p.kw = kw;
+        p.hd = hd;
+        p.rope_half = (int)c.rope_dimension_count / 2;
+        p.max_ctx = (int)s->max_ctx;
+        p.kv_heads = Hkv;
+        p.rope_tab = s->rope_tab;
+        p.kcache = s->kcache + li * layer_kv;
+        p.vcache = s->vcache + li * layer_kv;
+        p.d_pos = s->d_pos;
+        if ((rc = timed_gemm(s, L.qkv, p))) return rc;
+        AttnParams a;
+        a.q = s->q;
+        a.kcache = p.kcache;
+        a.vcache = p.vcache;
+        a.scores = s->scores;
+        a.xq = s->xq;
+        a.xs = s->xs;
+        a.xsum = s->xsum;
+        a.d_pos = s->d_pos;
+        a.N = n;
+        a.H = (int)c.head_count;
+        a.Hkv = Hkv;
+        a.hd = hd;
+        a.max_ctx = (int)s->max_ctx;
+        a.max_pos = (int)(start_pos + n - 1);
+        a.scale = 1.0f / std::sqrt((float)hd);  // inference.rs:3927
+        if ((rc = launch_attention(a, st))) return rc;
+        GemmParams po;
+        po.x = s->xq;
+        po.xs = s->xs;
+        po.xsum = s->xsum;
+        po.N = n;
+        po.epi = EPI_RESIDUAL;
+        po.out = s->hidden;
+        po.ld_out = d;
+        if ((rc = timed_gemm(s, L.wo, po))) return rc;
+        if ((rc = launch_rmsnorm_q8(s->hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xsum, st)))
+            return rc;
+        GemmParams pg;
+        pg.x = s->xq;
+        pg.xs = s->xs;
+        pg.xsum = s->xsum;
+        pg.N = n;
+        pg.epi = EPI_SWIGLU_Q8;
+        pg.xq_out = s->xq;  // gate/up read xq[.][0..d) and write xq[.][0..F): different kernels
+        pg.xs_out = s->xs;
+        pg.xsum_out = s->xsum;
+        pg.F = F;
+        // In-place would race (readers of row n's block b vs writers); use the upper half.
+        pg.xq_out = s->xq + (size_t)s->max_batch * s->maxw;
+        pg.xs_out = s->xs + (size_t)s->max_batch * (s->maxw / 32);
+        pg.xsum_out = s->xsum + (size_t)s->max_batch * (s->maxw / 32);
+        if ((rc = timed_gemm(s, L.gateup, pg))) return rc;
+        GemmParams pd;
+        pd.x = pg.xq_out;
+        pd.xs = pg.xs_out;
+        pd.xsum = pg.xsum_out;
+        pd.N = n;
+        pd.epi = EPI_RESIDUAL;
+        pd.out = s->hidden;
+        pd.ld_out = d;
+        if ((rc = timed_gemm(s, L.down, pd))) return rc;
+    }
+    // compute_logits_from_hidden (inference.rs:4783-4832) for every row + argmax
+    if ((rc = launch_rmsnorm_q8(s->hidden, m->out_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xsum, st))) return rc;
+    GemmParams ph;
+    ph.x = s->xq;
+    ph.xs = s->xs;
+    ph.xsum = s->xsum;
+    ph.N = n;
+    ph.epi = EPI_HEAD;
+    ph.out = s->logits;
+    ph.ld_out = (int)c.vocab_size;
+    ph.part_val = s->part_val;
+    ph.part_idx = s->part_idx;
+    if ((rc = timed_gemm(s, m->head, ph))) return rc;
+    if ((rc = launch_argmax_final(s->part_val, s->part_idx, n, (int)m->head.tiles, s->d_preds, st))) return rc;
+    s->last_n = n;
+    return NC_OK;
+}
+
+// Stages the next pass's tokens; run_pass writes them to the device together with the
+// start position through kernel arguments.
+static int upload_toks(nc_session* s, const uint32_t* toks, int n) {
+    if (n < 1 || n > 16) return fail(NC_ERANGE, "batch must be 1..16 tokens");
+    std::memcpy(s->staged, toks, n * sizeof(uint32_t));
+    s->pending_toks = true;
+    return NC_OK;
+}
+
+static int fetch_preds(nc_session* s, int n, uint32_t* out) {
+    NC_HIP(hipMemcpyAsync(s->h_preds, s->d_preds, n * sizeof(uint32_t), hipMemcpyDeviceToHost, s->stream));
+    NC_HIP(hipStreamSynchronize(s->stream));
+    std::memcpy(out, s->h_preds, n * sizeof(uint32_t));
+    return NC_OK;
+}
+
+// prefill_tokens (main.rs:9415-9485): chunks of max_batch rows.  Returns the last row's
+// greedy prediction in *last_pred.
+static int prefill_chunks(nc_session* s, const uint32_t* toks, int n, int64_t start_pos, uint32_t* last_pred) {
+    int rc;
+    for (int i = 0; i < n; i += s->max_batch) {
+        const int len = std::min(s->max_batch, n - i);
+        if ((rc = upload_toks(s, toks + i, len))) return rc;
+        if ((rc = run_pass(s, len, start_pos + i))) return rc;
+    }
+    if (last_pred) {
+        uint32_t preds[16];
+        if ((rc = fetch_preds(s, s->last_n, preds))) return rc;
+        *last_pred = preds[s->last_n - 1];
+    }
+    return NC_OK;
+}
+
+static int verify_step(nc_session* s, int n, int64_t start_pos, nc_verify_result* r) {
+    int rc = run_pass(s, n, start_pos);
+    if (rc) return rc;
+    if ((rc = launch_accept_greedy(s->d_toks, s->d_preds, n, s->d_pos, s->d_result, nullptr, s->stream))) return rc;
+    NC_HIP(hipMemcpyAsync(s->h_result, s->d_result, 4 * sizeof(int32_t), hipMemcpyDeviceToHost, s->stream));
+    NC_HIP(hipStreamSynchronize(s->stream));
+    r->n_accepted = s->h_result[0];
+    r->next_token = (uint32_t)s->h_result[1];
+    r->new_pos = s->h_result[2];
+    return NC_OK;
+}
+
+static double now_s() {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+}  // namespace nc
+
+using namespace nc;
+
+// ================================================================ C ABI
+extern "C" {
+
+const char* nc_last_error(void) { return t_err.c_str(); }
+const char* nc_version(void) { return "nanocamelid-mi355x 0.1 (gfx950)"; }
+
+int nc_ctx_create(int device, nc_ctx** out) {
+    if (!out) return fail(NC_EINVAL, "out is null");
+    NC_HIP(hipSetDevice(device));
+    auto* c = new nc_ctx();
+    c->device = device;
+    hipError_t e = hipStreamCreate(&c->stream);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(NC_EHIP, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+    }
+    *out = c;
+    return NC_OK;
+}
+
+void nc_ctx_free(nc_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->xsum) (void)hipFree(c->xsum);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int nc_ctx_synchronize(nc_ctx* c) {
+    if (!c) return fail(NC_EINVAL, "ctx is null");
+    NC_HIP(hipSetDevice(c->device));
+    NC_HIP(hipStreamSynchronize(c->stream));
+    return NC_OK;
+}
+
+int nc_qmat_upload(nc_ctx* ctx, int type, int64_t rows, int64_t cols, const void* blocks, nc_qmat** out) {
+    if (!ctx || !blocks || !out || rows <= 0 || cols <= 0) return fail(NC_EINVAL, "nc_qmat_upload: bad arguments");
+    if (type != NC_TYPE_Q4_0 && type != NC_TYPE_Q4_K) return fail(NC_EINVAL, "nc_qmat_upload: type must be Q4_0 or Q4_K");
+    NC_HIP(hipSetDevice(ctx->device));
+    auto* q = new nc_qmat();
+    q->ctx = ctx;
+    int rc = upload_matrix(type, rows, cols, {{(const uint8_t*)blocks, rows, 0, -1}}, q->m);
+    if (rc) {
+        if (q->m.dev) (void)hipFree(q->m.dev);
+        delete q;
+        return rc;
+    }
+    *out = q;
+    return NC_OK;
+}
+
+void nc_qmat_free(nc_qmat* q) {
+    if (!q) return;
+    if (q->m.dev) (void)hipFree(q->m.dev);
+    delete q;
+}
+
+int64_t nc_qmat_device_bytes(const nc_qmat* q) { return q ? q->m.dev_bytes : -1; }
+
+static int ensure_xsum(nc_ctx* ctx, size_t count) {
+    if (ctx->xsum_cap >= count) return NC_OK;
+    if (ctx->xsum) NC_HIP(hipFree(ctx->xsum));
+    ctx->xsum = nullptr;
+    ctx->xsum_cap = 0;
+    NC_HIP(hipMalloc((void**)&ctx->xsum, count * sizeof(int32_t)));
+    ctx->xsum_cap = count;
+    return NC_OK;
+}
+
+int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, const float* x_scales, float* out,
+                              int batch_size, int64_t rows, int64_t cols, void* stream) {
+    if (!ctx || !w || !x_i8 || !x_scales || !out) return fail(NC_EINVAL, "nc_matmul_quantized_batch: null argument");
+    if (rows != w->m.rows || cols != w->m.cols) return fail(NC_EINVAL, "nc_matmul_quantized_batch: shape mismatch");
+    if (batch_size < 1 || batch_size > 16) return fail(NC_EINVAL, "nc_matmul_quantized_batch: batch must be 1..16");
+    NC_HIP(hipSetDevice(ctx->device));
+    hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+    int rc = ensure_xsum(ctx, (size_t)batch_size * (cols / 32));
+    if (rc) return rc;
+    if ((rc = launch_block_sums(x_i8, batch_size, (int)cols, ctx->xsum, st))) return rc;
+    GemmParams p;
+    p.x = x_i8;
+    p.xs = x_scales;
+    p.xsum = ctx->xsum;
+    p.N = batch_size;
+    p.epi = EPI_STORE;
+    p.out = out;
+    p.ld_out = (int)rows;
+    return launch_gemm(w->m, p, st);
+}
+
+int nc_matmul_blockdots(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, int32_t* dots, int batch_size, int64_t rows,
+                        int64_t cols, void* stream) {
+    if (!ctx || !w || !x_i8 || !dots) return fail(NC_EINVAL, "nc_matmul_blockdots: null argument");
+    if (rows != w->m.rows || cols != w->m.cols) return fail(NC_EINVAL, "nc_matmul_blockdots: shape mismatch");
+    NC_HIP(hipSetDevice(ctx->device));
+    return launch_blockdots(w->m, x_i8, dots, batch_size, stream ? (hipStream_t)stream : ctx->stream);
+}
+
+int nc_quantize_q8_0_batch(nc_ctx* ctx, const float* x, int8_t* x_i8, float* x_scales, int batch_size, int64_t dim,
+                           void* stream) {
+    if (!ctx || !x || !x_i8 || !x_scales || dim % 32) return fail(NC_EINVAL, "nc_quantize_q8_0_batch: bad arguments");
+    NC_HIP(hipSetDevice(ctx->device));
+    int rc = ensure_xsum(ctx, (size_t)batch_size * (dim / 32));
+    if (rc) return rc;
+    return launch_quantize_q8(x, batch_size, (int)dim, x_i8, x_scales, ctx->xsum, stream ? (hipStream_t)stream : ctx->stream);
+}
+
+int nc_model_load_gguf_memory(nc_ctx* ctx, const void* data, size_t size, const nc_load_opts* opts, nc_model** out) {
+    if (!ctx || !data || !out) return fail(NC_EINVAL, "nc_model_load_gguf_memory: null argument");
+    NC_HIP(hipSetDevice(ctx->device));
+    return load_model(ctx, (const uint8_t*)data, size, opts, out);
+}
+
+int nc_model_load_gguf(nc_ctx* ctx, const char* path, const nc_load_opts* opts, nc_model** out) {
+    if (!ctx || !path || !out) return fail(NC_EINVAL, "nc_model_load_gguf: null argument");
+    FILE* fp = std::fopen(path, "rb");
+    if (!fp) return fail(NC_EINVAL, std::string("cannot open ") + path);
+    std::fseek(fp, 0, SEEK_END);
+    const long sz = std::ftell(fp);
+    std::fseek(fp, 0, SEEK_SET);
+    std::vector<uint8_t> buf((size_t)sz);
+    const size_t got = std::fread(buf.data(), 1, buf.size(), fp);
+    std::fclose(fp);
+    if (got != buf.size()) return fail(NC_EFORMAT, "short read");
+    return nc_model_load_gguf_memory(ctx, buf.data(), buf.size(), opts, out);
+}
+
+int nc_model_get_config(const nc_model* m, nc_model_config* out) {
+    if (!m || !out) return fail(NC_EINVAL, "null argument");
+    *out = m->cfg;
+    return NC_OK;
+}
+
+void nc_model_free(nc_model* m) { free_model(m); }
+
+void nc_session_free(nc_session* s) {
+    if (!s) return;
+    (void)hipSetDevice(s->ctx->device);
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    for (auto& e : s->ev) {
+        (void)hipEventDestroy(e.first);
+        (void)hipEventDestroy(e.second);
+    }
+    for (void* p : s->allocs) (void)hipFree(p);
+    for (void* p : {(void*)s->h_toks, (void*)s->h_preds, (void*)s->h_result, (void*)s->h_pos})
+        if (p) (void)hipHostFree(p);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    delete s;
+}
+
+int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_session** out) {
+    if (!m || !out) return fail(NC_EINVAL, "null argument");
+    if (max_batch < 1 || max_batch > 16) return fail(NC_EINVAL, "max_batch must be 1..16");
+    if (max_ctx < 1 || max_ctx > m->cfg.context_length)
+        return fail(NC_ERANGE, "max_ctx must be in 1..context_length");
+    NC_HIP(hipSetDevice(m->ctx->device));
+    std::unique_ptr<nc_session, void (*)(nc_session*)> s(new nc_session(), nc_session_free);
+    s->m = m;
+    s->ctx = m->ctx;
+    s->max_ctx = max_ctx;
+    s->max_batch = max_batch;
+    NC_HIP(hipStreamCreate(&s->stream));
+    const nc_model_config& c = m->cfg;
+    const int64_t B = max_batch;
+    s->maxw = std::max({c.embedding_length, c.feed_forward_length, c.attention_output_width});
+    const size_t kv = (size_t)c.block_count * c.head_count_kv * max_ctx * c.head_dim;
+    int rc;
+    if ((rc = dev_alloc(s->allocs, &s->kcache, kv)) || (rc = dev_alloc(s->allocs, &s->vcache, kv)) ||
+        (rc = dev_alloc(s->allocs, &s->hidden, B * c.embedding_length)) ||
+        (rc = dev_alloc(s->allocs, &s->xq, 2 * B * s->maxw)) ||
+        (rc = dev_alloc(s->allocs, &s->xs, 2 * B * (s->maxw / 32))) ||
+        (rc = dev_alloc(s->allocs, &s->xsum, 2 * B * (s->maxw / 32))) ||
+        (rc = dev_alloc(s->allocs, &s->q, B * c.attention_output_width)) ||
+        (rc = dev_alloc(s->allocs, &s->scores, (size_t)B * c.head_count * max_ctx)) ||
+        (rc = dev_alloc(s->allocs, &s->logits, (size_t)B * c.vocab_size)) ||
+        (rc = dev_alloc(s->allocs, &s->part_val, B * m->head.tiles)) ||
+        (rc = dev_alloc(s->allocs, &s->part_idx, B * m->head.tiles)) ||
+        (rc = dev_alloc(s->allocs, &s->d_toks, B)) || (rc = dev_alloc(s->allocs, &s->d_preds, B)) ||
+        (rc = dev_alloc(s->allocs, &s->d_pos, 4)) || (rc = dev_alloc(s->allocs, &s->d_result, 4)))
+        return rc;
+    NC_HIP(hipMemset(s->kcache, 0, kv * 4));
+    NC_HIP(hipMemset(s->vcache, 0, kv * 4));
+    NC_HIP(hipHostMalloc((void**)&s->h_toks, 64 * sizeof(uint32_t), hipHostMallocDefault));
+    NC_HIP(hipHostMalloc((void**)&s->h_preds, 64 * sizeof(uint32_t), hipHostMallocDefault));
+    NC_HIP(hipHostMalloc((void**)&s->h_result, 16 * sizeof(int32_t), hipHostMallocDefault));
+    NC_HIP(hipHostMalloc((void**)&s->h_pos, 16 * sizeof(int32_t), hipHostMallocDefault));
+    // RoPE (sin, cos) table, cached_rope_angles (inference.rs:880-901), from glibc on the
+    // host: theta = base.powf(-(2i)/rope_dim), (sin, cos) = (pos*theta).sin_cos().
+    const int64_t half = c.rope_dimension_count / 2;
+    std::vector<float> tab((size_t)max_ctx * half * 2);
+    static float (*volatile p_sinf)(float) = sinf;
+    static float (*volatile p_cosf)(float) = cosf;
+    static float (*volatile p_powf)(float, float) = powf;
+    std::vector<float> theta(half);
+    for (int64_t i = 0; i < half; i++)
+        theta[i] = p_powf(c.rope_freq_base, -((float)(i * 2)) / (float)c.rope_dimension_count);
+    for (int64_t pos = 0; pos < max_ctx; pos++)
+        for (int64_t i = 0; i < half; i++) {
+            const float angle = (float)pos * theta[i];
+            tab[(pos * half + i) * 2] = p_sinf(angle);
+            tab[(pos * half + i) * 2 + 1] = p_cosf(angle);
+        }
+    if ((rc = upload_f32(s->allocs, tab, &s->rope_tab))) return rc;
+    s->ev.resize(4096);
+    for (auto& e : s->ev) {
+        NC_HIP(hipEventCreate(&e.first));
+        NC_HIP(hipEventCreate(&e.second));
+    }
+    *out = s.release();
+    return NC_OK;
+}
+
+int nc_prefill(nc_session* s, const uint32_t* toks, int32_t n, int64_t start_pos, int32_t want_logits) {
+    if (!s || !toks || n < 1) return fail(NC_EINVAL, "nc_prefill: bad arguments");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    (void)want_logits;
+    int rc = prefill_chunks(s, toks, n, start_pos, nullptr);
+    if (rc) return rc;
+    NC_HIP(hipStreamSynchronize(s->stream));
+    return flush_timing(s);
+}
+
+int nc_forward1(nc_session* s, uint32_t tok, int64_t pos, float* logits_host, uint32_t* pred_out) {
+    if (!s) return fail(NC_EINVAL, "null session");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    int rc = upload_toks(s, &tok, 1);
+    if (rc || (rc = run_pass(s, 1, pos))) return rc;
+    if (logits_host) {
+        NC_HIP(hipMemcpyAsync(logits_host, s->logits, s->m->cfg.vocab_size * 4, hipMemcpyDeviceToHost, s->stream));
+    }
+    uint32_t pred;
+    if ((rc = fetch_preds(s, 1, &pred))) return rc;
+    if (pred_out) *pred_out = pred;
+    return flush_timing(s);
+}
+
+int nc_verify_greedy(nc_session* s, const uint32_t* toks, int32_t n, int64_t start_pos, nc_verify_result* result,
+                     uint32_t* preds_host) {
+    if (!s || !toks || !result || n < 1) return fail(NC_EINVAL, "nc_verify_greedy: bad arguments");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    int rc = upload_toks(s, toks, n);
+    if (rc || (rc = verify_step(s, n, start_pos, result))) return rc;
+    if (preds_host && (rc = fetch_preds(s, n, preds_host))) return rc;
+    return flush_timing(s);
+}
+
+int nc_session_logits(nc_session* s, int32_t row, float* logits_host) {
+    if (!s || !logits_host || row < 0 || row >= s->last_n) return fail(NC_EINVAL, "nc_session_logits: bad row");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    NC_HIP(hipMemcpyAsync(logits_host, s->logits + (size_t)row * s->m->cfg.vocab_size, s->m->cfg.vocab_size * 4,
+                          hipMemcpyDeviceToHost, s->stream));
+    NC_HIP(hipStreamSynchronize(s->stream));
+    return NC_OK;
+}
+
+int nc_session_hidden(nc_session* s, int32_t n, float* hidden_host) {
+    if (!s || !hidden_host || n < 1 || n > s->max_batch) return fail(NC_EINVAL, "nc_session_hidden: bad arguments");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    NC_HIP(hipMemcpyAsync(hidden_host, s->hidden, (size_t)n * s->m->cfg.embedding_length * 4, hipMemcpyDeviceToHost,
+                          s->stream));
+    NC_HIP(hipStreamSynchronize(s->stream));
+    return NC_OK;
+}
+
+int nc_generate_greedy(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new, uint32_t* out,
+                       nc_decode_stats* stats) {
+    if (!s || !prompt || !out || n_prompt < 1 || n_new < 1) return fail(NC_EINVAL, "nc_generate_greedy: bad arguments");
+    if (n_prompt + n_new > s->max_ctx) return fail(NC_ERANGE, "prompt + new tokens exceed the session context");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    const double t0 = now_s();
+    uint32_t pending;
+    int rc = prefill_chunks(s, prompt, n_prompt, 0, &pending);
+    if (rc) return rc;
+    const double t1 = now_s();
+    int64_t pos = n_prompt, steps = 0;
+    out[0] = pending;
+    for (int i = 1; i < n_new; i++) {
+        nc_verify_result r;
+        if ((rc = upload_toks(s, &pending, 1)) || (rc = verify_step(s, 1, pos, &r))) return rc;
+        pending = r.next_token;
+        out[i] = pending;
+        pos = r.new_pos;
+        steps++;
+    }
+    const double t2 = now_s();
+    if (stats) {
+        *stats = nc_decode_stats{steps, 0, 0, n_new, t2 - t1, t1 - t0};
+    }
+    return flush_timing(s);
+}
+
+int nc_generate_speculative_oracle(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new,
+                                   int32_t max_steps, int32_t k, float alpha, uint64_t seed, const uint32_t* greedy,
+                                   int32_t n_greedy, uint32_t* out, nc_decode_stats* stats) {
+    if (!s || !prompt || !out || !greedy || n_prompt < 1 || n_new < 1 || k < 0)
+        return fail(NC_EINVAL, "nc_generate_speculative_oracle: bad arguments");
+    if (n_prompt + n_new > s->max_ctx) return fail(NC_ERANGE, "prompt + new tokens exceed the session context");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    const uint32_t V = (uint32_t)s->m->cfg.vocab_size;
+    const double t0 = now_s();
+    uint32_t pending;
+    int rc = prefill_chunks(s, prompt, n_prompt, 0, &pending);
+    if (rc) return rc;
+    const double t1 = now_s();
+    int64_t pos = n_prompt, produced = 0, steps = 0, drafted = 0, accepted = 0;
+    out[produced++] = pending;
+    uint32_t batch[16];
+    while (produced < n_new && (max_steps <= 0 || steps < max_steps)) {
+        int64_t kk = std::min<int64_t>(k, s->max_batch - 1);
+        kk = std::min<int64_t>(kk, s->max_ctx - pos - 1);
+        if (kk < 0) break;
+        batch[0] = pending;
+        for (int64_t i = 1; i <= kk; i++) batch[i] = nc_oracle_draft(seed, pos + i, alpha, greedy, n_prompt, n_greedy, V);
+        nc_verify_result r;
+        if ((rc = upload_toks(s, batch, (int)kk + 1)) || (rc = verify_step(s, (int)kk + 1, pos, &r))) return rc;
+        drafted += kk;
+        accepted += r.n_accepted;
+        for (int i = 1; i <= r.n_accepted && produced < n_new; i++) out[produced++] = batch[i];
+        pending = r.next_token;
+        if (produced < n_new) out[produced++] = pending;
+        pos = r.new_pos;
+        steps++;
+    }
+    const double t2 = now_s();
+    if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};
+    return flush_timing(s);
+}
+
+int nc_generate_speculative_draft(nc_session* tg, nc_session* dr, const uint32_t* prompt, int32_t n_prompt,
+                                  int32_t n_new, int32_t draft_k, uint32_t* out, nc_decode_stats* stats) {
+    if (!tg || !dr || !prompt || !out || n_prompt < 1 || n_new < 1 || draft_k < 1)
+        return fail(NC_EINVAL, "nc_generate_speculative_draft: bad arguments");
+    NC_HIP(hipSetDevice(tg->ctx->device));
+    const double t0 = now_s();
+    uint32_t tlive, dlive;
+    // main.rs:9643-9706: prefill both models; live predictions for position n_prompt
+    int rc = prefill_chunks(dr, prompt, n_prompt, 0, &dlive);
+    if (rc || (rc = prefill_chunks(tg, prompt, n_prompt, 0, &tlive))) return rc;
+    const double t1 = now_s();
+    int64_t pos = n_prompt, produced = 0, steps = 0, drafted = 0, accepted = 0;
+    uint32_t drafts[16], preds[16];
+    while (produced < n_new && pos < tg->max_ctx) {
+        // speculative.rs:318-321 clamp
+        int64_t k = std::min<int64_t>(draft_k, n_new - produced);
+        k = std::min<int64_t>(k, tg->max_batch);
+        k = std::min<int64_t>(k, tg->max_ctx - (pos + 1));
+        k = std::min<int64_t>(k, dr->max_ctx - (pos + 1));
+        if (k <= 0) break;
+        // 1. drafting: sample from the draft's live prediction, then a draft forward
+        for (int64_t i = 0; i < k; i++) {
+            drafts[i] = dlive;
+            if ((rc = nc_forward1(dr, drafts[i], pos + i, nullptr, &dlive))) return rc;
+        }
+        // 2. batched target pass over the drafts
+        if ((rc = upload_toks(tg, drafts, (int)k)) || (rc = run_pass(tg, (int)k, pos)) ||
+            (rc = fetch_preds(tg, (int)k, preds)))
+            return rc;
+        // 3. verification (speculative.rs:384-447)
+        drafted += k;
+        int64_t i = 0;
+        for (; i < k; i++) {
+            const uint32_t tt = i == 0 ? tlive : preds[i - 1];
+            if (drafts[i] != tt) break;
+            accepted++;
+            if (produced < n_new) out[produced++] = drafts[i];
+        }
+        uint32_t fix;
+        int64_t at;
+        if (i < k) {
+            fix = i == 0 ? tlive : preds[i - 1];  // corrective token
+            at = pos + i;
+        } else {
+            fix = preds[k - 1];  // 4. trailing verified token
+            at = pos + k;
+        }
+        if (produced < n_new) out[produced++] = fix;
+        if ((rc = nc_forward1(tg, fix, at, nullptr, &tlive)) || (rc = nc_forward1(dr, fix, at, nullptr, &dlive))) return rc;
+        pos = at + 1;
+        steps++;
+    }
+    const double t2 = now_s();
+    if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};
+    return flush_timing(tg);
+}
+
+int nc_synth_size(const nc_synth_spec* spec, uint64_t* size_out) {
+    if (!spec || !size_out) return fail(NC_EINVAL, "null argument");
+    return synth_size(*spec, size_out);
+}
+
+int nc_synth_write(const nc_synth_spec* spec, void* dst, uint64_t size, int32_t nthreads) {
+    if (!spec || !dst) return fail(NC_EINVAL, "null argument");
+    if (spec->embedding_length % spec->head_count || spec->embedding_length % 256 || spec->feed_forward_length % 256)
+        return fail(NC_EINVAL, "synth: widths must be multiples of 256");
+    return synth_write(*spec, (uint8_t*)dst, size, nthreads);
+}
+
+int nc_uniform_prompt(uint64_t seed, int64_t n, uint32_t vocab, uint32_t* ids) {
+    if (!ids || vocab == 0) return fail(NC_EINVAL, "bad arguments");
+    for (int64_t i = 0; i < n; i++) ids[i] = philox_word(seed, (uint64_t)i, kPurposePrompt) % vocab;
+    return NC_OK;
+}
+
+uint32_t nc_oracle_draft(uint64_t seed, int64_t p, float alpha, const uint32_t* greedy, int64_t n_prompt,
+                         int64_t n_greedy, uint32_t vocab) {
+    const float u = philox_uniform(seed, (uint64_t)p, kPurposeOracleU);
+    const int64_t gi = p - n_prompt;
+    if (u < alpha && gi >= 0 && gi < n_greedy) return greedy[gi];
+    return philox_word(seed, (uint64_t)p, kPurposeOracleId) % vocab;
+}
+
+int nc_session_timing_enable(nc_session* s, int32_t enable) {
+    if (!s) return fail(NC_EINVAL, "null session");
+    int rc = flush_timing(s);
+    if (rc) return rc;
+    s->timing = enable != 0;
+    s->gemm_ms = 0.0;
+    s->gemm_launches = 0;
+    s->gemm_bytes = 0;
+    s->pending_bytes = 0;
+    return NC_OK;
+}
+
+int64_t nc_session_kernel_timing(nc_session* s, const char* family, double* total_ms, int64_t* bytes) {
+    if (!s || !family) return fail(NC_EINVAL, "bad arguments");
+    if (flush_timing(s)) return -1;
+    if (std::strcmp(family, "gemm_q4_0") != 0) return fail(NC_EINVAL, "unknown kernel family");
+    if (total_ms) *total_ms = s->gemm_ms;
+    if (bytes) *bytes = s->gemm_bytes;
+    return s->gemm_launches;
+}
+
+}  // extern "C"

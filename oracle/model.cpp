@@ -1,0 +1,767 @@
+// Oracle: GGUF reader, Llama model, f32 KV cache, single/batched forward and the
+// speculative decode loops.  TEST INFRASTRUCTURE ONLY (see nc_oracle.h).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "oracle_internal.h"
+
+namespace {
+
+// ---------------------------------------------------------------- GGUF (gguf.rs:454-763)
+struct MetaVal {
+    int type = -1;  // gguf.rs:652-668 value type ids
+    uint64_t u = 0;
+    int64_t i = 0;
+    double f = 0;
+    std::string s;
+};
+
+struct Tensor {
+    std::string name;
+    std::vector<uint64_t> dims;
+    uint32_t type = 0;
+    uint64_t offset = 0;  // absolute
+    uint64_t nbytes = 0;
+};
+
+struct Gguf {
+    const uint8_t* data = nullptr;
+    size_t size = 0;
+    std::map<std::string, MetaVal> meta;
+    std::vector<Tensor> tensors;
+    const Tensor* find(const std::string& n) const {
+        for (auto& t : tensors)
+            if (t.name == n) return &t;
+        return nullptr;
+    }
+};
+
+struct Cursor {
+    const uint8_t* p;
+    size_t n, pos = 0;
+    bool ok = true;
+    bool need(size_t k) {
+        if (pos + k > n) ok = false;
+        return ok;
+    }
+    uint64_t u(int bytes) {
+        if (!need(bytes)) return 0;
+        uint64_t v = 0;
+        for (int i = 0; i < bytes; i++) v |= (uint64_t)p[pos + i] << (8 * i);
+        pos += bytes;
+        return v;
+    }
+    std::string str() {
+        uint64_t len = u(8);
+        if (!need(len)) return "";
+        std::string s((const char*)p + pos, len);
+        pos += len;
+        return s;
+    }
+};
+
+// gguf.rs:154-185 GgufTensorType::layout (block size, type size) for the types used here.
+bool type_layout(uint32_t t, uint64_t* bs, uint64_t* ts) {
+    switch (t) {
+        case 0: *bs = 1; *ts = 4; return true;      // F32
+        case 1: *bs = 1; *ts = 2; return true;      // F16
+        case 2: *bs = 32; *ts = 18; return true;    // Q4_0
+        case 8: *bs = 32; *ts = 34; return true;    // Q8_0
+        case 12: *bs = 256; *ts = 144; return true; // Q4_K
+        case 30: *bs = 1; *ts = 2; return true;     // BF16
+        default: return false;
+    }
+}
+
+bool read_value(Cursor& c, uint32_t type, MetaVal& v, int depth = 0) {
+    v.type = (int)type;
+    switch (type) {
+        case 0: v.u = c.u(1); break;
+        case 1: v.i = (int8_t)c.u(1); break;
+        case 2: v.u = c.u(2); break;
+        case 3: v.i = (int16_t)c.u(2); break;
+        case 4: v.u = c.u(4); break;
+        case 5: v.i = (int32_t)c.u(4); break;
+        case 6: { uint32_t b = (uint32_t)c.u(4); v.f = bits_f32(b); break; }
+        case 7: v.u = c.u(1); if (v.u > 1) return false; break;
+        case 8: v.s = c.str(); break;
+        case 9: {
+            if (depth > 0) return false;
+            uint32_t it = (uint32_t)c.u(4);
+            uint64_t len = c.u(8);
+            for (uint64_t k = 0; k < len && c.ok; k++) {
+                MetaVal tmp;
+                if (!read_value(c, it, tmp, depth + 1)) return false;
+            }
+            break;
+        }
+        case 10: v.u = c.u(8); break;
+        case 11: v.i = (int64_t)c.u(8); break;
+        case 12: { uint64_t b = c.u(8); double d; std::memcpy(&d, &b, 8); v.f = d; break; }
+        default: return false;
+    }
+    return c.ok;
+}
+
+bool parse_gguf(const uint8_t* data, size_t size, Gguf& g, std::string& err) {
+    g.data = data;
+    g.size = size;
+    Cursor c{data, size};
+    if (size < 4 || std::memcmp(data, "GGUF", 4) != 0) { err = "invalid GGUF magic"; return false; }
+    c.pos = 4;
+    uint32_t version = (uint32_t)c.u(4);
+    if (version < 2 || version > 3) { err = "unsupported GGUF version"; return false; }
+    uint64_t tcount = c.u(8), mcount = c.u(8);
+    for (uint64_t i = 0; i < mcount && c.ok; i++) {
+        std::string key = c.str();
+        uint32_t vt = (uint32_t)c.u(4);
+        MetaVal v;
+        if (!read_value(c, vt, v)) { err = "bad metadata value for " + key; return false; }
+        g.meta[key] = v;
+    }
+    uint64_t alignment = 32;  // gguf.rs:10
+    auto it = g.meta.find("general.alignment");
+    if (it != g.meta.end()) {
+        if (it->second.type == 4 || it->second.type == 10) alignment = it->second.u;
+        else if (it->second.type == 5) alignment = (uint64_t)it->second.i;
+    }
+    if (alignment == 0 || (alignment & (alignment - 1))) { err = "invalid alignment"; return false; }
+    struct Raw { std::string n; std::vector<uint64_t> d; uint32_t t; uint64_t off; };
+    std::vector<Raw> raws;
+    for (uint64_t i = 0; i < tcount && c.ok; i++) {
+        Raw r;
+        r.n = c.str();
+        uint32_t nd = (uint32_t)c.u(4);
+        if (nd == 0 || nd > 4) { err = "invalid dimension count"; return false; }
+        for (uint32_t k = 0; k < nd; k++) r.d.push_back(c.u(8));
+        r.t = (uint32_t)c.u(4);
+        r.off = c.u(8);
+        raws.push_back(r);
+    }
+    if (!c.ok) { err = "truncated GGUF header"; return false; }
+    uint64_t start = (c.pos + alignment - 1) & ~(alignment - 1);
+    for (auto& r : raws) {
+        uint64_t bs, ts;
+        if (!type_layout(r.t, &bs, &ts)) { err = "unsupported tensor type in " + r.n; return false; }
+        if (r.d[0] % bs) { err = "first dim not divisible by block size: " + r.n; return false; }
+        uint64_t el = 1;
+        for (auto d : r.d) el *= d;
+        Tensor t{r.n, r.d, r.t, start + r.off, el / bs * ts};
+        if (t.offset + t.nbytes > size) { err = "tensor out of file bounds: " + r.n; return false; }
+        g.tensors.push_back(t);
+    }
+    return true;
+}
+
+bool meta_u32(const Gguf& g, const std::string& k, uint32_t* out) {  // gguf.rs:230-237
+    auto it = g.meta.find(k);
+    if (it == g.meta.end()) return false;
+    const MetaVal& v = it->second;
+    if (v.type == 4) { *out = (uint32_t)v.u; return true; }
+    if (v.type == 10 && v.u <= 0xffffffffull) { *out = (uint32_t)v.u; return true; }
+    if (v.type == 5 && v.i >= 0) { *out = (uint32_t)v.i; return true; }
+    return false;
+}
+bool meta_f32(const Gguf& g, const std::string& k, float* out) {  // gguf.rs:239-245
+    auto it = g.meta.find(k);
+    if (it == g.meta.end()) return false;
+    if (it->second.type == 6 || it->second.type == 12) { *out = (float)it->second.f; return true; }
+    return false;
+}
+
+// ---------------------------------------------------------------- model (model.rs)
+struct QMat {
+    uint32_t type = 2;  // 2 = Q4_0 (GGUF blocks [rows][cols/32][18]), 12 = Q4_K
+    int64_t rows = 0, cols = 0;
+    std::vector<uint8_t> blocks;
+};
+
+struct Layer {
+    std::vector<float> attn_norm, ffn_norm;
+    QMat wq, wk, wv, wo, w1, w3, w2;
+};
+
+}  // namespace
+
+struct or_model {
+    std::vector<uint8_t> owned;  // memory image copy (or empty when mmapped)
+    void* map = nullptr;
+    size_t map_size = 0;
+    int nthreads = 1;
+    // config (model.rs:26-186)
+    int64_t ctx = 0, d = 0, L = 0, F = 0, H = 0, Hkv = 0, hd = 0, rope_dim = 0, V = 0;
+    int64_t attn_w = 0, kv_w = 0;
+    float rope_base = 10000.0f, eps = 1e-5f;
+    bool has_output = false;
+    uint32_t wtype = 2;
+    std::vector<float> tok_emb, out_norm;
+    QMat head;
+    std::vector<Layer> layers;
+    ~or_model() {
+        if (map) munmap(map, map_size);
+    }
+};
+
+struct or_session {
+    or_model* m;
+    int64_t max_ctx, max_batch;
+    std::vector<float> kc, vc;  // [L][max_ctx][kv_w]
+    // batch workspace (inference.rs:624-695)
+    std::vector<float> hidden, residual, norm_x, q, k, v, attn, gate, up, gu, scores;
+    std::vector<int8_t> xq;
+    std::vector<float> xs;
+    std::vector<float> logits;  // single-token workspace logits [V]
+    std::vector<float> row_hidden;
+};
+
+namespace {
+
+bool load_f32_tensor(const Gguf& g, const std::string& name, std::vector<float>& out, std::string& err) {
+    // model.rs:1081-1230 load_f32_or_f16 (F32, F16, Q4_0, Q4_K used here)
+    const Tensor* t = g.find(name);
+    if (!t) { err = "missing tensor " + name; return false; }
+    const uint8_t* p = g.data + t->offset;
+    uint64_t el = 1;
+    for (auto dd : t->dims) el *= dd;
+    out.resize(el);
+    if (t->type == 0) {
+        std::memcpy(out.data(), p, el * 4);
+    } else if (t->type == 1) {
+        for (uint64_t i = 0; i < el; i++) out[i] = or_f16_to_f32(load_u16(p + 2 * i));
+    } else if (t->type == 2) {
+        for (uint64_t b = 0; b < el / 32; b++) {
+            const uint8_t* blk = p + b * 18;
+            float sc = or_f16_to_f32(load_u16(blk));
+            for (int j = 0; j < 16; j++) {
+                out[b * 32 + j] = (float)((int)(blk[2 + j] & 0x0f) - 8) * sc;
+                out[b * 32 + 16 + j] = (float)((int)(blk[2 + j] >> 4) - 8) * sc;
+            }
+        }
+    } else if (t->type == 12) {
+        for (uint64_t b = 0; b < el / 256; b++) or_q4_k_dequantize(p + b * 144, out.data() + b * 256);
+    } else {
+        err = "unsupported f32 source type for " + name;
+        return false;
+    }
+    return true;
+}
+
+bool load_qmat(const Gguf& g, const std::string& name, int64_t rows, int64_t cols, QMat& q, std::string& err) {
+    const Tensor* t = g.find(name);
+    if (!t) { err = "missing tensor " + name; return false; }
+    if (t->dims.size() != 2 || (int64_t)t->dims[0] != cols || (int64_t)t->dims[1] != rows) {
+        err = "bad shape for " + name;
+        return false;
+    }
+    if (t->type != 2 && t->type != 12) { err = "unsupported matrix type for " + name; return false; }
+    q.type = t->type;
+    q.rows = rows;
+    q.cols = cols;
+    q.blocks.assign(g.data + t->offset, g.data + t->offset + t->nbytes);
+    return true;
+}
+
+bool build_model(or_model* m, const uint8_t* data, size_t size, std::string& err) {
+    Gguf g;
+    if (!parse_gguf(data, size, g, err)) return false;
+    auto it = g.meta.find("general.architecture");
+    if (it == g.meta.end() || it->second.s != "llama") { err = "unsupported architecture"; return false; }
+    const std::string P = "llama.";
+    uint32_t v32;
+    if (!meta_u32(g, P + "context_length", &v32)) { err = "missing llama.context_length"; return false; }
+    m->ctx = v32;
+    if (!meta_u32(g, P + "embedding_length", &v32)) { err = "missing embedding_length"; return false; }
+    m->d = v32;
+    if (!meta_u32(g, P + "block_count", &v32)) { err = "missing block_count"; return false; }
+    m->L = v32;
+    if (!meta_u32(g, P + "feed_forward_length", &v32)) { err = "missing feed_forward_length"; return false; }
+    m->F = v32;
+    if (!meta_u32(g, P + "attention.head_count", &v32) || v32 == 0) { err = "bad head_count"; return false; }
+    m->H = v32;
+    m->Hkv = meta_u32(g, P + "attention.head_count_kv", &v32) ? v32 : m->H;
+    if (m->d % m->H || m->Hkv == 0 || m->H % m->Hkv) { err = "bad head geometry"; return false; }
+    float f;
+    m->rope_base = meta_f32(g, P + "rope.freq_base", &f) ? f : 10000.0f;
+    m->eps = meta_f32(g, P + "attention.layer_norm_rms_epsilon", &f) ? f : 1e-5f;
+    const Tensor* te = g.find("token_embd.weight");
+    if (!te) { err = "missing token_embd.weight"; return false; }
+    if (meta_u32(g, P + "vocab_size", &v32)) m->V = v32;
+    else m->V = (int64_t)(te->dims[0] == (uint64_t)m->d ? te->dims[1] : te->dims[0]);
+    m->hd = meta_u32(g, P + "attention.key_length", &v32) ? v32 : m->d / m->H;
+    m->rope_dim = meta_u32(g, P + "rope.dimension_count", &v32) ? v32 : m->hd;
+    m->attn_w = m->H * m->hd;
+    m->kv_w = m->Hkv * m->hd;
+    if (!load_f32_tensor(g, "token_embd.weight", m->tok_emb, err)) return false;
+    if (!load_f32_tensor(g, "output_norm.weight", m->out_norm, err)) return false;
+    m->has_output = g.find("output.weight") != nullptr;
+    if (m->has_output) {
+        if (!load_qmat(g, "output.weight", m->V, m->d, m->head, err)) return false;
+    } else {
+        // model.rs:471-532 tied head -> Q4_0 requantisation of the f32 embeddings.
+        m->head.type = 2;
+        m->head.rows = m->V;
+        m->head.cols = m->d;
+        m->head.blocks.resize((size_t)m->V * (m->d / 32) * 18);
+        parallel_rows(m->V, m->nthreads, [&](int64_t lo, int64_t hi) {
+            or_quantize_q4_0_tied(m->tok_emb.data() + lo * m->d, hi - lo, m->d,
+                                  m->head.blocks.data() + (size_t)lo * (m->d / 32) * 18);
+        });
+    }
+    m->layers.resize(m->L);
+    for (int64_t i = 0; i < m->L; i++) {
+        Layer& ly = m->layers[i];
+        std::string b = "blk." + std::to_string(i) + ".";
+        if (!load_f32_tensor(g, b + "attn_norm.weight", ly.attn_norm, err)) return false;
+        if (!load_f32_tensor(g, b + "ffn_norm.weight", ly.ffn_norm, err)) return false;
+        if (!load_qmat(g, b + "attn_q.weight", m->attn_w, m->d, ly.wq, err)) return false;
+        if (!load_qmat(g, b + "attn_k.weight", m->kv_w, m->d, ly.wk, err)) return false;
+        if (!load_qmat(g, b + "attn_v.weight", m->kv_w, m->d, ly.wv, err)) return false;
+        if (!load_qmat(g, b + "attn_output.weight", m->d, m->attn_w, ly.wo, err)) return false;
+        if (!load_qmat(g, b + "ffn_gate.weight", m->F, m->d, ly.w1, err)) return false;
+        if (!load_qmat(g, b + "ffn_up.weight", m->F, m->d, ly.w3, err)) return false;
+        if (!load_qmat(g, b + "ffn_down.weight", m->d, m->F, ly.w2, err)) return false;
+        m->wtype = ly.wq.type;
+    }
+    return true;
+}
+
+void matmul(const or_model* m, float* out, const int8_t* x, const float* xs, const QMat& w, int64_t N) {
+    // inference.rs:1246-1303 matmul_quantized_batch dispatch
+    if (w.type == 2) or_matmul_q4_0(out, x, xs, w.blocks.data(), N, w.rows, w.cols, m->nthreads);
+    else or_matmul_q4_k(out, x, xs, w.blocks.data(), N, w.rows, w.cols, m->nthreads);
+}
+
+void quantize_rows(const float* x, int64_t N, int64_t dim, int8_t* q, float* s) {
+    // inference.rs:967-989 quantize_f32_to_q8_0_batch
+    for (int64_t t = 0; t < N; t++) or_quantize_q8_0(x + t * dim, dim, q + t * dim, s + t * (dim / 32));
+}
+
+// inference.rs:3747-4111 run_layer_range_batch (dense llama layers).  N == 1 is the
+// single-token run_layer_range (inference.rs:4505-4781), identical per row.
+void run_layers(or_session* s, int64_t N, int64_t start_pos) {
+    or_model* m = s->m;
+    const int64_t d = m->d, aw = m->attn_w, kw = m->kv_w, F = m->F;
+    const float scale = 1.0f / std::sqrt((float)m->hd);
+    const int64_t kv_mul = m->H / m->Hkv;
+    for (int64_t li = 0; li < m->L; li++) {
+        const Layer& ly = m->layers[li];
+        std::copy(s->hidden.begin(), s->hidden.begin() + N * d, s->residual.begin());
+        for (int64_t t = 0; t < N; t++)
+            or_rms_norm(&s->norm_x[t * d], &s->hidden[t * d], ly.attn_norm.data(), d, m->eps);
+        quantize_rows(s->norm_x.data(), N, d, s->xq.data(), s->xs.data());
+        matmul(m, s->q.data(), s->xq.data(), s->xs.data(), ly.wq, N);
+        matmul(m, s->k.data(), s->xq.data(), s->xs.data(), ly.wk, N);
+        matmul(m, s->v.data(), s->xq.data(), s->xs.data(), ly.wv, N);
+        for (int64_t t = 0; t < N; t++) {
+            int64_t pos = start_pos + t;
+            or_rope(&s->q[t * aw], pos, m->H, m->hd, m->rope_dim, m->rope_base, 0);
+            or_rope(&s->k[t * kw], pos, m->Hkv, m->hd, m->rope_dim, m->rope_base, 0);
+            size_t off = ((size_t)li * s->max_ctx + pos) * kw;  // inference.rs:539-548
+            std::copy(&s->k[t * kw], &s->k[t * kw] + kw, &s->kc[off]);
+            std::copy(&s->v[t * kw], &s->v[t * kw] + kw, &s->vc[off]);
+        }
+        std::fill(s->attn.begin(), s->attn.begin() + N * aw, 0.0f);
+        const float* kc = &s->kc[(size_t)li * s->max_ctx * kw];
+        const float* vc = &s->vc[(size_t)li * s->max_ctx * kw];
+        for (int64_t t = 0; t < N; t++) {
+            int64_t pos = start_pos + t;
+            parallel_rows(m->H, m->H >= 8 ? std::min<int>(m->nthreads, 8) : 1, [&](int64_t lo, int64_t hi) {
+                std::vector<float> sc(pos + 1);
+                for (int64_t h = lo; h < hi; h++)
+                    or_attention_head(&s->attn[t * aw + h * m->hd], sc.data(), &s->q[t * aw + h * m->hd],
+                                      kc, vc, pos, kw, h / kv_mul, m->hd, scale);
+            });
+        }
+        quantize_rows(s->attn.data(), N, aw, s->xq.data(), s->xs.data());
+        matmul(m, s->hidden.data(), s->xq.data(), s->xs.data(), ly.wo, N);
+        for (int64_t i = 0; i < N * d; i++) s->hidden[i] += s->residual[i];
+        std::copy(s->hidden.begin(), s->hidden.begin() + N * d, s->residual.begin());
+        for (int64_t t = 0; t < N; t++)
+            or_rms_norm(&s->norm_x[t * d], &s->hidden[t * d], ly.ffn_norm.data(), d, m->eps);
+        quantize_rows(s->norm_x.data(), N, d, s->xq.data(), s->xs.data());
+        matmul(m, s->gate.data(), s->xq.data(), s->xs.data(), ly.w1, N);
+        matmul(m, s->up.data(), s->xq.data(), s->xs.data(), ly.w3, N);
+        or_silu_mul(s->gu.data(), s->gate.data(), s->up.data(), N * F);
+        quantize_rows(s->gu.data(), N, F, s->xq.data(), s->xs.data());
+        matmul(m, s->hidden.data(), s->xq.data(), s->xs.data(), ly.w2, N);
+        for (int64_t i = 0; i < N * d; i++) s->hidden[i] += s->residual[i];
+    }
+}
+
+void embed(or_session* s, const uint32_t* toks, int64_t N) {
+    const or_model* m = s->m;
+    for (int64_t t = 0; t < N; t++)
+        std::copy(&m->tok_emb[(size_t)toks[t] * m->d], &m->tok_emb[(size_t)toks[t] * m->d] + m->d,
+                  &s->hidden[t * m->d]);
+}
+
+// inference.rs:4783-4832 compute_logits_from_hidden on one hidden row.
+void logits_from_hidden(or_session* s, const float* h, float* out) {
+    const or_model* m = s->m;
+    std::vector<float> nx(m->d);
+    std::vector<int8_t> q(m->d);
+    std::vector<float> xs(m->d / 32);
+    or_rms_norm(nx.data(), h, m->out_norm.data(), m->d, m->eps);
+    or_quantize_q8_0(nx.data(), m->d, q.data(), xs.data());
+    matmul(m, out, q.data(), xs.data(), m->head, 1);
+}
+
+// ---------------------------------------------------------------- spec helpers
+constexpr uint32_t PURPOSE_DRAFT = 1, PURPOSE_ACCEPT = 2, PURPOSE_RESAMPLE = 3, PURPOSE_BONUS = 7;
+constexpr uint32_t PURPOSE_PROMPT = 4, PURPOSE_ORACLE_U = 5, PURPOSE_ORACLE_ID = 6;
+
+uint32_t philox_word(uint64_t seed, uint64_t pos, uint32_t purpose) {
+    uint32_t ctr[4] = {(uint32_t)pos, (uint32_t)(pos >> 32), purpose, 0};
+    uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t out[4];
+    or_philox4x32_10(ctr, key, out);
+    return out[0];
+}
+// u in [0,1) from the top 24 bits.
+float philox_uniform(uint64_t seed, uint64_t pos, uint32_t purpose) {
+    return (float)(philox_word(seed, pos, purpose) >> 8) * (1.0f / 16777216.0f);
+}
+
+void prefill(or_session* s, const uint32_t* toks, int64_t n, int64_t start_pos, int64_t chunk) {
+    // main.rs:9415-9485 prefill_tokens: chunks of the batch width; a lone token takes the
+    // single-token path.  Per-row numerics are identical either way.
+    int64_t pos = start_pos;
+    for (int64_t i = 0; i < n; i += chunk) {
+        int64_t len = std::min(chunk, n - i);
+        or_prefill_pass_batch(s, toks + i, len, pos);
+        pos += len;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+static or_model* finish_load(or_model* m, const uint8_t* data, size_t size, char* err, int errlen) {
+    std::string e;
+    if (!build_model(m, data, size, e)) {
+        if (err && errlen > 0) std::snprintf(err, errlen, "%s", e.c_str());
+        delete m;
+        return nullptr;
+    }
+    return m;
+}
+
+or_model* or_model_load(const char* path, int nthreads, char* err, int errlen) {
+    int fd = open(path, O_RDONLY);
+    if (fd < 0) {
+        if (err) std::snprintf(err, errlen, "cannot open %s", path);
+        return nullptr;
+    }
+    struct stat st;
+    fstat(fd, &st);
+    void* p = mmap(nullptr, st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (p == MAP_FAILED) {
+        if (err) std::snprintf(err, errlen, "mmap failed");
+        return nullptr;
+    }
+    or_model* m = new or_model();
+    m->nthreads = nthreads;
+    m->map = p;
+    m->map_size = st.st_size;
+    return finish_load(m, (const uint8_t*)p, st.st_size, err, errlen);
+}
+
+or_model* or_model_load_memory(const void* data, size_t size, int nthreads, char* err, int errlen) {
+    or_model* m = new or_model();
+    m->nthreads = nthreads;
+    return finish_load(m, (const uint8_t*)data, size, err, errlen);
+}
+
+void or_model_free(or_model* m) { delete m; }
+
+void or_model_info(const or_model* m, int64_t* o) {
+    int64_t v[16] = {m->ctx, m->d, m->L, m->F, m->H, m->Hkv, m->hd, m->rope_dim, m->V, m->attn_w,
+                     m->kv_w, m->has_output ? 1 : 0, (int64_t)m->wtype, 0, 0, 0};
+    std::memcpy(o, v, sizeof(v));
+}
+void or_model_info_f(const or_model* m, float* o) {
+    o[0] = m->rope_base;
+    o[1] = m->eps;
+}
+
+int64_t or_model_head_q4_0(const or_model* m, uint8_t* out, int64_t cap) {
+    if (m->head.type != 2 || (int64_t)m->head.blocks.size() > cap) return -1;
+    std::memcpy(out, m->head.blocks.data(), m->head.blocks.size());
+    return (int64_t)m->head.blocks.size();
+}
+
+or_session* or_session_create(or_model* m, int64_t max_ctx, int64_t max_batch) {
+    or_session* s = new or_session();
+    s->m = m;
+    s->max_ctx = max_ctx;
+    s->max_batch = max_batch;
+    s->kc.assign((size_t)m->L * max_ctx * m->kv_w, 0.0f);
+    s->vc.assign((size_t)m->L * max_ctx * m->kv_w, 0.0f);
+    int64_t B = max_batch;
+    s->hidden.resize(B * m->d);
+    s->residual.resize(B * m->d);
+    s->norm_x.resize(B * m->d);
+    s->q.resize(B * m->attn_w);
+    s->k.resize(B * m->kv_w);
+    s->v.resize(B * m->kv_w);
+    s->attn.resize(B * m->attn_w);
+    s->gate.resize(B * m->F);
+    s->up.resize(B * m->F);
+    s->gu.resize(B * m->F);
+    int64_t mx = std::max({m->d, m->F, m->attn_w});
+    s->xq.resize(B * mx);
+    s->xs.resize(B * (mx / 32 + 1));
+    s->logits.resize(m->V);
+    return s;
+}
+
+void or_session_free(or_session* s) { delete s; }
+
+void or_prefill_pass_batch(or_session* s, const uint32_t* toks, int64_t n, int64_t start_pos) {
+    if (n <= 0) return;
+    if (n > s->max_batch || start_pos + n > s->max_ctx) {  // inference.rs:3712-3722
+        std::fprintf(stderr, "oracle: batch out of bounds\n");
+        std::abort();
+    }
+    embed(s, toks, n);
+    run_layers(s, n, start_pos);
+}
+
+void or_forward_pass(or_session* s, uint32_t tok, int64_t pos) {
+    or_prefill_pass_batch(s, &tok, 1, pos);
+    logits_from_hidden(s, s->hidden.data(), s->logits.data());
+}
+
+void or_batch_row_logits(or_session* s, int64_t row, float* out) {
+    logits_from_hidden(s, &s->hidden[row * s->m->d], out);
+}
+
+const float* or_session_logits(const or_session* s) { return s->logits.data(); }
+const float* or_session_batch_hidden(const or_session* s) { return s->hidden.data(); }
+
+static float top2_margin(const float* l, int64_t V, int64_t best) {
+    float second = -INFINITY;
+    for (int64_t i = 0; i < V; i++)
+        if (i != best && l[i] > second) second = l[i];
+    return l[best] - second;
+}
+
+void or_verify_greedy(or_session* s, const uint32_t* toks, int64_t n, int64_t start_pos,
+                      uint32_t* preds, float* margins, float* logits_out) {
+    or_prefill_pass_batch(s, toks, n, start_pos);
+    std::vector<float> lg(s->m->V);
+    for (int64_t i = 0; i < n; i++) {
+        float* dst = logits_out ? logits_out + i * s->m->V : lg.data();
+        or_batch_row_logits(s, i, dst);
+        int64_t a = or_argmax(dst, s->m->V);
+        preds[i] = (uint32_t)a;
+        if (margins) margins[i] = top2_margin(dst, s->m->V, a);
+    }
+}
+
+int or_generate_greedy(or_session* s, const uint32_t* prompt, int64_t n_prompt, int64_t n_new,
+                       int64_t prefill_batch, uint32_t* out) {
+    // main.rs:9676-9706: prefix via prefill_tokens, last prompt token via forward_pass,
+    // then the plain greedy loop (sample, emit, forward).
+    prefill(s, prompt, n_prompt - 1, 0, prefill_batch);
+    int64_t pos = n_prompt - 1;
+    or_forward_pass(s, prompt[n_prompt - 1], pos);
+    pos++;
+    for (int64_t i = 0; i < n_new; i++) {
+        uint32_t t = (uint32_t)or_argmax(s->logits.data(), s->m->V);
+        out[i] = t;
+        if (i + 1 < n_new) {
+            or_forward_pass(s, t, pos);
+            pos++;
+        }
+    }
+    return 0;
+}
+
+int64_t or_generate_speculative_draft(or_session* tg, or_session* dr, const uint32_t* prompt,
+                                      int64_t n_prompt, int64_t n_new, int64_t draft_k,
+                                      int64_t prefill_batch, uint32_t* out, int64_t* stats,
+                                      int64_t* steps_out) {
+    // main.rs:9643-9706 prefill of both models, then speculative.rs:299-494 per step
+    // (greedy, temp 0, no stop tokens).
+    const int64_t V = tg->m->V;
+    prefill(dr, prompt, n_prompt - 1, 0, std::min(prefill_batch, dr->max_batch));
+    or_forward_pass(dr, prompt[n_prompt - 1], n_prompt - 1);
+    prefill(tg, prompt, n_prompt - 1, 0, prefill_batch);
+    or_forward_pass(tg, prompt[n_prompt - 1], n_prompt - 1);
+    int64_t pos = n_prompt, dpos = n_prompt, produced = 0, steps = 0;
+    stats[0] = stats[1] = 0;
+    std::vector<float> lg(V);
+    while (produced < n_new && pos < tg->max_ctx) {
+        int64_t k = std::min(draft_k, n_new - produced);
+        k = std::min(k, tg->max_batch);
+        k = std::min(k, tg->max_ctx - (pos + 1));
+        k = std::min(k, dr->max_ctx - (pos + 1));
+        if (k <= 0) break;
+        std::vector<uint32_t> drafts;
+        int64_t cdp = pos;
+        while ((int64_t)drafts.size() < k) {
+            uint32_t t = (uint32_t)or_argmax(dr->logits.data(), V);
+            drafts.push_back(t);
+            or_forward_pass(dr, t, cdp);
+            cdp++;
+        }
+        or_prefill_pass_batch(tg, drafts.data(), k, pos);
+        std::vector<uint32_t> acc;
+        bool rejected = false;
+        stats[0] += k;
+        for (int64_t i = 0; i < k; i++) {
+            const float* l;
+            if (i > 0) {
+                or_batch_row_logits(tg, i - 1, lg.data());
+                l = lg.data();
+            } else {
+                l = tg->logits.data();
+            }
+            uint32_t tt = (uint32_t)or_argmax(l, V);
+            if (drafts[i] == tt) {
+                acc.push_back(tt);
+                stats[1]++;
+            } else {
+                rejected = true;
+                acc.push_back(tt);
+                or_forward_pass(tg, tt, pos + i);
+                or_forward_pass(dr, tt, pos + i);
+                pos = dpos = pos + i + 1;
+                break;
+            }
+        }
+        if (!rejected) {
+            or_batch_row_logits(tg, k - 1, lg.data());
+            uint32_t tt = (uint32_t)or_argmax(lg.data(), V);
+            acc.push_back(tt);
+            or_forward_pass(tg, tt, pos + k);
+            or_forward_pass(dr, tt, pos + k);
+            pos = dpos = pos + k + 1;
+        }
+        for (auto t : acc)
+            if (produced < n_new) out[produced++] = t;
+        steps++;
+    }
+    (void)dpos;
+    if (steps_out) *steps_out = steps;
+    return produced;
+}
+
+uint32_t or_oracle_draft(uint64_t seed, int64_t p, float alpha, const uint32_t* greedy,
+                         int64_t n_prompt, int64_t n_greedy, uint32_t vocab) {
+    float u = philox_uniform(seed, (uint64_t)p, PURPOSE_ORACLE_U);
+    int64_t gi = p - n_prompt;
+    if (u < alpha && gi >= 0 && gi < n_greedy) return greedy[gi];
+    return philox_word(seed, (uint64_t)p, PURPOSE_ORACLE_ID) % vocab;
+}
+
+void or_uniform_prompt(uint64_t seed, int64_t n, uint32_t vocab, uint32_t* ids) {
+    for (int64_t i = 0; i < n; i++) ids[i] = philox_word(seed, (uint64_t)i, PURPOSE_PROMPT) % vocab;
+}
+
+int64_t or_generate_speculative_oracle(or_session* s, const uint32_t* prompt, int64_t n_prompt,
+                                       int64_t n_new, int64_t k, float alpha, uint64_t seed,
+                                       const uint32_t* greedy, int64_t prefill_batch, uint32_t* out,
+                                       int64_t* stats, int64_t* steps_out) {
+    // k+1 form (cluster_tcp_smoke.rs:905-979): batch = [pending] + drafts, preds after
+    // every row, accepted = longest prefix with draft[i] == pred[i], next = pred[accepted].
+    const int64_t V = s->m->V;
+    prefill(s, prompt, n_prompt - 1, 0, prefill_batch);
+    or_forward_pass(s, prompt[n_prompt - 1], n_prompt - 1);
+    uint32_t pending = (uint32_t)or_argmax(s->logits.data(), V);
+    int64_t pos = n_prompt, produced = 0, steps = 0;
+    stats[0] = stats[1] = 0;
+    out[produced++] = pending;
+    std::vector<uint32_t> batch, preds;
+    while (produced < n_new) {
+        int64_t kk = std::min(k, s->max_batch - 1);
+        kk = std::min(kk, s->max_ctx - pos - 1);
+        if (kk < 0) break;
+        batch.assign(1, pending);
+        for (int64_t i = 1; i <= kk; i++)
+            batch.push_back(or_oracle_draft(seed, pos + i, alpha, greedy, n_prompt, n_new, (uint32_t)V));
+        preds.resize(kk + 1);
+        or_verify_greedy(s, batch.data(), kk + 1, pos, preds.data(), nullptr, nullptr);
+        int64_t a = 0;
+        while (a < kk && batch[a + 1] == preds[a]) a++;
+        stats[0] += kk;
+        stats[1] += a;
+        for (int64_t i = 1; i <= a && produced < n_new; i++) out[produced++] = batch[i];
+        pending = preds[a];
+        if (produced < n_new) out[produced++] = pending;
+        pos += a + 1;
+        steps++;
+    }
+    if (steps_out) *steps_out = steps;
+    return produced;
+}
+
+void or_temperature_probs(const float* logits, int64_t V, float temp, float* probs) {
+    // Max, exp((l - max) / T) (as inference.rs:4857-4862), sequential sum, then the
+    // softmax normalisation (inference.rs:3535-3539): p = e * (1 / sum).
+    float mx = logits[0];
+    for (int64_t i = 0; i < V; i++)
+        if (logits[i] > mx) mx = logits[i];
+    float sum = 0.0f;
+    for (int64_t i = 0; i < V; i++) {
+        probs[i] = expf((logits[i] - mx) / temp);
+        sum += probs[i];
+    }
+    float inv = 1.0f / sum;
+    for (int64_t i = 0; i < V; i++) probs[i] *= inv;
+}
+
+uint32_t or_sample_inverse_cdf(const float* probs, int64_t V, float u) {
+    // inference.rs:4865-4872 style: r = u * total, subtract in id order, first r <= 0 wins.
+    float total = 0.0f;
+    for (int64_t i = 0; i < V; i++) total += probs[i];
+    float r = u * total;
+    int64_t last_pos = V - 1;
+    for (int64_t i = 0; i < V; i++) {
+        if (probs[i] > 0.0f) last_pos = i;
+        r -= probs[i];
+        if (r <= 0.0f && probs[i] > 0.0f) return (uint32_t)i;
+    }
+    return (uint32_t)last_pos;
+}
+
+void or_stochastic_accept(const float* p_logits, const float* q_probs, const uint32_t* drafts,
+                          int64_t k, int64_t V, float temp, uint64_t seed, int64_t start_pos,
+                          int64_t* n_accepted, uint32_t* next_token) {
+    std::vector<float> p(V), r(V);
+    for (int64_t i = 0; i < k; i++) {
+        or_temperature_probs(p_logits + i * V, V, temp, p.data());
+        const float* q = q_probs + i * V;
+        uint32_t x = drafts[i];
+        float u = philox_uniform(seed, (uint64_t)(start_pos + i), PURPOSE_ACCEPT);
+        if (u * q[x] < p[x]) continue;  // accept with probability min(1, p/q)
+        for (int64_t j = 0; j < V; j++) {
+            float dlt = p[j] - q[j];
+            r[j] = dlt > 0.0f ? dlt : 0.0f;
+        }
+        float ur = philox_uniform(seed, (uint64_t)(start_pos + i), PURPOSE_RESAMPLE);
+        float tot = 0.0f;
+        for (int64_t j = 0; j < V; j++) tot += r[j];
+        *n_accepted = i;
+        *next_token = tot > 0.0f ? or_sample_inverse_cdf(r.data(), V, ur) : or_sample_inverse_cdf(p.data(), V, ur);
+        return;
+    }
+    or_temperature_probs(p_logits + k * V, V, temp, p.data());
+    *n_accepted = k;
+    *next_token = or_sample_inverse_cdf(p.data(), V, philox_uniform(seed, (uint64_t)(start_pos + k), PURPOSE_BONUS));
+}
+
+}  // extern "C"

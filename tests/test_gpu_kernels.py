@@ -1,0 +1,128 @@
+"""GPU parity of the quantized GEMM and the activation quantiser against the CPU oracle.
+
+Bar: int32 per-block dots bit-exact; fp32 outputs within 1e-3
+relative (they are in fact bit-identical, which is asserted too).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.gpu_util import q8_activations, random_q4_0, random_q4_k
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import nanocamelid_amd as nc
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    return nc.Context(0)
+
+
+def _run_gemm(ctx, qtype, blocks, M, K, xq, xs):
+    import nanocamelid_amd as nc
+    w = nc.QMat(ctx, qtype, M, K, blocks)
+    xt = torch.from_numpy(xq).cuda()
+    st = torch.from_numpy(xs).cuda()
+    out = nc.matmul_quantized_batch(ctx, w, xt, st)
+    dots = nc.matmul_blockdots(ctx, w, xt)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), dots.cpu().numpy()
+
+
+@pytest.mark.parametrize("N", [1, 2, 5, 9, 16])
+def test_q4_0_small_bit_exact(ctx, N):
+    import nanocamelid_amd as nc
+    M, K = 320, 768  # 5 tiles, 24 blocks (3 groups)
+    w = random_q4_0(M, K, seed=N)
+    _, xq, xs = q8_activations(N, K, seed=100 + N)
+    out, dots = _run_gemm(ctx, nc.NC_TYPE_Q4_0, w, M, K, xq, xs)
+    ref = O.matmul_q4_0(xq, xs, w, N, M, K)
+    ref_dots = O.matmul_q4_0_blockdots(xq, w, N, M, K)
+    assert np.array_equal(dots, ref_dots)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_q4_0_partial_group_and_tile(ctx):
+    # K/32 = 13 blocks (last group partial), M = 100 rows (last tile partial)
+    import nanocamelid_amd as nc
+    M, K, N = 100, 416, 3
+    w = random_q4_0(M, K, seed=7)
+    _, xq, xs = q8_activations(N, K, seed=8)
+    out, dots = _run_gemm(ctx, nc.NC_TYPE_Q4_0, w, M, K, xq, xs)
+    assert np.array_equal(dots, O.matmul_q4_0_blockdots(xq, w, N, M, K))
+    assert np.array_equal(out, O.matmul_q4_0(xq, xs, w, N, M, K))
+
+
+CONFIG1 = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
+
+
+@pytest.mark.parametrize("shape", CONFIG1, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_q4_0_config1_shapes(ctx, shape):
+    """Config 1: Llama-3-8B projection shapes, N = 1, 2, 5, 9, 16, weights N(0,0.02)->Q4_0,
+    activations N(0,1)->Q8_0.  Every output and every block dot is compared."""
+    import nanocamelid_amd as nc
+    M, K = shape
+    w = random_q4_0(M, K, seed=M + K)
+    q = nc.QMat(ctx, nc.NC_TYPE_Q4_0, M, K, w)
+    for N in (1, 2, 5, 9, 16):
+        x, xq, xs = q8_activations(N, K, seed=N * 31 + M)
+        xt, st = torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda()
+        out = nc.matmul_quantized_batch(ctx, q, xt, st).cpu().numpy()
+        ref = O.matmul_q4_0(xq, xs, w, N, M, K, nthreads=16)
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), N
+        # fp32 within 1e-3 relative of a float64 evaluation of the same quantized product
+        if M * K <= 4096 * 14336:
+            wf = _dequant(w).astype(np.float64)
+            xf = xq.astype(np.float64) * np.repeat(xs.astype(np.float64), 32, axis=1)
+            r64 = xf @ wf.T
+            err = np.abs(out - r64) / (np.abs(r64) + 1e-3 * np.abs(r64).max())
+            assert err.max() < 1e-3
+        if N in (1, 5, 16):
+            rows = np.random.default_rng(N).choice(M, size=min(M, 512), replace=False)
+            dots = nc.matmul_blockdots(ctx, q, xt).cpu().numpy()[:, rows]
+            ref_dots = O.matmul_q4_0_blockdots(xq, w.reshape(M, -1)[rows], N, len(rows), K, nthreads=16)
+            assert np.array_equal(dots, ref_dots)
+
+
+def _dequant(w):
+    M, nb, _ = w.shape
+    sc = (w[:, :, 0].astype(np.uint16) | (w[:, :, 1].astype(np.uint16) << 8)).view(np.float16).astype(np.float32)
+    lo = (w[:, :, 2:] & 15).astype(np.float32) - 8
+    hi = (w[:, :, 2:] >> 4).astype(np.float32) - 8
+    return (np.concatenate([lo, hi], 2) * sc[:, :, None]).reshape(M, nb * 32)
+
+
+@pytest.mark.parametrize("N", [1, 5, 9, 16])
+def test_q4_k_bit_exact(ctx, N):
+    import nanocamelid_amd as nc
+    M, K = 192, 1024
+    w = random_q4_k(M, K, seed=N)
+    _, xq, xs = q8_activations(N, K, seed=200 + N)
+    out, dots = _run_gemm(ctx, nc.NC_TYPE_Q4_K, w, M, K, xq, xs)
+    ref = O.matmul_q4_k(xq, xs, w, N, M, K)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    # per 32-sub-block W_j = sum nib * x (q8.rs:1339-1376)
+    for r in (0, 7, 100, 191):
+        for n in range(N):
+            for sb in range(K // 256):
+                W, _ = O.q4_k_subblock_ints(w[r, sb], xq[n, sb * 256:(sb + 1) * 256])
+                assert np.array_equal(dots[n, r, sb * 8:(sb + 1) * 8], W)
+
+
+def test_quantize_q8_0_matches_oracle(ctx):
+    import nanocamelid_amd as nc
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 1, (4, 4096)).astype(np.float32)
+    x[0, :32] = 0.0                    # zero block
+    x[1, :32] = np.arange(32) * 0.5   # exact .5 ties -> away from zero
+    x[1, 31] = 127 * 0.5
+    x[2, 64:96] = 1e-30                # tiny scale
+    q, s = nc.quantize_f32_to_q8_0_batch(ctx, torch.from_numpy(x).cuda())
+    q, s = q.cpu().numpy(), s.cpu().numpy()
+    for n in range(4):
+        rq, rs = O.quantize_q8_0(x[n])
+        assert np.array_equal(q[n], rq)
+        assert np.array_equal(s[n].view(np.uint32), rs.view(np.uint32))
