@@ -8,13 +8,17 @@
 // portable path.
 //
 // Mapping: one 64-row tile per workgroup, lane = row.  Weight bytes come from a
-// repacked layout where every wave-wide load is 1 KB contiguous; the activation
-// block of a token is wave-uniform and is read with scalar loads into SGPRs, so the
-// int8 dot is v_dot4_i32_i8 with an SGPR operand and needs no LDS or L1 traffic.
+// repacked layout where every wave-wide load is 1 KB contiguous.  Q4_0: the activation
+// block of a token is wave-uniform; each 16-lane row loads it once (one dword per lane)
+// and v_dot4c_i32_i8 with a DPP row broadcast feeds it to every lane, so activations
+// cost no LDS traffic and no extra VALU moves.  Q4_K reads activations with scalar loads.
 // With S > 1 waves per workgroup the K range is split round-robin in rounds of
 // S*U blocks: each wave writes its per-block terms to LDS and the chain threads
 // (lane = row, wave = token group) add them in block order.  int32 dots are exact,
 // every float op is IEEE with no contraction.
+#include <cstdlib>
+#include <utility>
+
 #include "nc_device.h"
 #include "nc_internal.h"
 
@@ -33,40 +37,6 @@ __device__ __forceinline__ sptr_f32 as_scalar_f32(const T* p) {
 }
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
-
-// Scale vector of U consecutive f16 scales of one row.
-template <int U>
-struct ScaleVec;
-template <>
-struct ScaleVec<8> {
-    uint4 v;
-    __device__ __forceinline__ void load(const uint8_t* p) { v = *(const uint4*)p; }
-    __device__ __forceinline__ uint16_t get(int u) const {
-        uint32_t w = u < 2 ? v.x : (u < 4 ? v.y : (u < 6 ? v.z : v.w));
-        return (uint16_t)((u & 1) ? (w >> 16) : (w & 0xffff));
-    }
-};
-template <>
-struct ScaleVec<4> {
-    uint2 v;
-    __device__ __forceinline__ void load(const uint8_t* p) { v = *(const uint2*)p; }
-    __device__ __forceinline__ uint16_t get(int u) const {
-        uint32_t w = u < 2 ? v.x : v.y;
-        return (uint16_t)((u & 1) ? (w >> 16) : (w & 0xffff));
-    }
-};
-template <>
-struct ScaleVec<2> {
-    uint32_t v;
-    __device__ __forceinline__ void load(const uint8_t* p) { v = *(const uint32_t*)p; }
-    __device__ __forceinline__ uint16_t get(int u) const { return (uint16_t)(u ? (v >> 16) : (v & 0xffff)); }
-};
-template <>
-struct ScaleVec<1> {
-    uint16_t v;
-    __device__ __forceinline__ void load(const uint8_t* p) { v = *(const uint16_t*)p; }
-    __device__ __forceinline__ uint16_t get(int) const { return v; }
-};
 
 // ---------------------------------------------------------------- epilogues
 // Thread (wave w, lane l) owns row 64*tile + l and tokens n = w + j*S.
@@ -135,7 +105,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const float* 
                     p.xq_out[(size_t)n * p.F + f] = (int8_t)q;
                     if (lane == 0) {
                         p.xs_out[(size_t)n * (p.F / 32) + tile] = scale;
-                        p.xsum_out[(size_t)n * (p.F / 32) + tile] = qs;
+                        p.xs8_out[(size_t)n * (p.F / 32) + tile] = -8 * qs;
                     }
                 }
                 break;
@@ -165,69 +135,134 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const float* 
 }
 
 // ---------------------------------------------------------------- Q4_0
-template <int NMAX, int S, int U>
+// Activation delivery by DPP row broadcast.  For block b, each row of 16 lanes loads the
+// 16 dwords {x[2p][b] (8 dwords), x[2p+1][b] (8 dwords)} of token pair p (every row holds
+// the same 64 bytes, one global_load_dword per lane), and one "meta" dword per lane:
+// lane j < 8 holds x_scale[j][b], lane 8 + j holds -8 * sum(x[j][b]) (tokens 8q..8q+7).
+// v_dot4c_i32_i8 with DPP row_newbcast:j reads lane j of each row as its src0, so the
+// activation dword reaches every lane without scalar loads, LDS, or extra VALU moves.
+
+// 8 int8 dot4 steps of one (block, token): acc += sum_i dot4(x dword (J0 + i), w_i).
+// The leading s_nop covers the VALU-write -> DPP-read hazard in case the compiler
+// materialised the activation register with a VALU move.  The trailing s_nop 2 covers
+// the DOT-write -> other-VALU-read hazard (3 wait states on gfx950): the compiler's
+// hazard recognizer cannot see inside the asm, and without it the first consumer of the
+// result reads the accumulator as it was two dot4c steps earlier.
+template <int J0>
+__device__ __forceinline__ int dot32_bcast(int acc, int xp, int w0, int w1, int w2, int w3, int w4, int w5, int w6,
+                                           int w7) {
+    asm("s_nop 1\n\t"
+        "v_dot4c_i32_i8_dpp %0, %1, %2 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %1, %3 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %1, %4 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %1, %5 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %1, %6 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %1, %7 row_newbcast:%15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %1, %8 row_newbcast:%16 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %1, %9 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 2"
+        : "+v"(acc)
+        : "v"(xp), "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(w4), "v"(w5), "v"(w6), "v"(w7), "n"(J0), "n"(J0 + 1),
+          "n"(J0 + 2), "n"(J0 + 3), "n"(J0 + 4), "n"(J0 + 5), "n"(J0 + 6), "n"(J0 + 7));
+    return acc;
+}
+
+template <int J>
+__device__ __forceinline__ int bcast_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, 0x150 + J, 0xf, 0xf, false);
+}
+template <int J>
+__device__ __forceinline__ float bcast_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xf, 0xf, false));
+}
+
+// Term of token n (compile-time) for one block: t = (ws * xs) * (float)sum (nib - 8) * x.
+template <int n>
+__device__ __forceinline__ float term_q40(const int* xp, const int* meta, const int (&lo)[4], const int (&hi)[4],
+                                          float ws) {
+    int d = bcast_i<8 + (n & 7)>(meta[n >> 3]);  // -8 * sum x: sum (nib-8)*x = sum nib*x - 8 sum x
+    d = dot32_bcast<8 * (n & 1)>(d, xp[n >> 1], lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]);
+    const float xs = bcast_f<n & 7>(__int_as_float(meta[n >> 3]));
+    return (xs * ws) * (float)d;  // IEEE multiplication is commutative: == (ws * xs) * d
+}
+
+template <int NMAX, int S>
 __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
-    constexpr int RB = S * U;
-    constexpr int TPW = (NMAX + S - 1) / S;
-    extern __shared__ float lds[];  // [RB][NMAX][64] terms when S > 1
+    constexpr int U = 4;                       // blocks per wave per round
+    constexpr int RB = S * U;                  // blocks per round
+    constexpr int TPW = (NMAX + S - 1) / S;    // chain tokens per thread
+    constexpr int NP = (NMAX + 1) / 2;         // token-pair activation dwords per block
+    constexpr int NM = (NMAX + 7) / 8;         // meta dwords per block
+    extern __shared__ float lds[];             // [RB][NMAX][64] terms when S > 1
     const int tile = blockIdx.x;
     const int wave = wave_id_uniform();
     const int lane = threadIdx.x & 63;
+    const int j16 = lane & 15;
     const int N = p.N;
     const int nb = p.units;
     const uint8_t* wt = p.w + (size_t)tile * p.groups * kQ40ChunkBytes;
     float acc[TPW];
 #pragma unroll
     for (int j = 0; j < TPW; j++) acc[j] = 0.0f;
+    // per-lane activation addresses: pair q -> token 2q + (j16 >> 3), dword j16 & 7;
+    // meta: lanes 0..7 read x_scale, lanes 8..15 read -8*sum(x) of token 8q + (j16 & 7)
+    const int* xbase = (const int*)p.x + (j16 & 7);
+    const int xtok = j16 >> 3;
+    const int mtok = j16 & 7;
+    const int* mbase = j16 >= 8 ? p.xs8 : (const int*)p.xs;
 
     const int nrounds = (nb + RB - 1) / RB;
-    uint4 cur[U], nxt[U];
-    ScaleVec<U> cs, ns;
-    auto load = [&](int r, uint4* nbuf, ScaleVec<U>& sbuf) {
+    uint4 cw[U], nw[U];
+    uint2 cs, ns;
+    int cx[U][NP], nx[U][NP], cm[U][NM], nm[U][NM];
+    auto load_round = [&](int r, uint4* wbuf, uint2& sbuf, int (*xbuf)[NP], int (*mbuf)[NM]) {
         const int b0 = r * RB + wave * U;
         if (b0 < nb) {
             const uint8_t* chunk = wt + (size_t)(b0 >> 3) * kQ40ChunkBytes;
             const int u0 = b0 & 7;
 #pragma unroll
-            for (int u = 0; u < U; u++) nbuf[u] = *(const uint4*)(chunk + (u0 + u) * 1024 + lane * 16);
-            sbuf.load(chunk + 8192 + lane * 16 + u0 * 2);
+            for (int u = 0; u < U; u++) wbuf[u] = *(const uint4*)(chunk + (u0 + u) * 1024 + lane * 16);
+            sbuf = *(const uint2*)(chunk + 8192 + lane * 16 + u0 * 2);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int b = min(b0 + u, nb - 1);
+#pragma unroll
+                for (int q = 0; q < NP; q++) {
+                    const int t = min(2 * q + xtok, N - 1);
+                    xbuf[u][q] = xbase[((size_t)t * p.K + (size_t)b * 32) / 4];
+                }
+#pragma unroll
+                for (int q = 0; q < NM; q++) {
+                    const int t = min(8 * q + mtok, N - 1);
+                    mbuf[u][q] = mbase[(size_t)t * nb + b];
+                }
+            }
         }
     };
-    load(0, cur, cs);
+    load_round(0, cw, cs, cx, cm);
     for (int r = 0; r < nrounds; r++) {
-        if (r + 1 < nrounds) load(r + 1, nxt, ns);
+        if (r + 1 < nrounds) load_round(r + 1, nw, ns, nx, nm);
         const int b0 = r * RB + wave * U;
+        if (b0 < nb) {  // wave-uniform
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int b = b0 + u;
-            if (b < nb) {  // wave-uniform
-                const uint4 v = cur[u];
-                const int lo0 = v.x & 0x0F0F0F0F, hi0 = (v.x >> 4) & 0x0F0F0F0F;
-                const int lo1 = v.y & 0x0F0F0F0F, hi1 = (v.y >> 4) & 0x0F0F0F0F;
-                const int lo2 = v.z & 0x0F0F0F0F, hi2 = (v.z >> 4) & 0x0F0F0F0F;
-                const int lo3 = v.w & 0x0F0F0F0F, hi3 = (v.w >> 4) & 0x0F0F0F0F;
-                const float ws = f16_to_f32(cs.get(u));
+            for (int u = 0; u < U; u++) {
+                if (b0 + u < nb) {
+                    const uint4 v = cw[u];
+                    const int lo[4] = {(int)(v.x & 0x0F0F0F0Fu), (int)(v.y & 0x0F0F0F0Fu), (int)(v.z & 0x0F0F0F0Fu),
+                                       (int)(v.w & 0x0F0F0F0Fu)};
+                    const int hi[4] = {(int)((v.x >> 4) & 0x0F0F0F0Fu), (int)((v.y >> 4) & 0x0F0F0F0Fu),
+                                       (int)((v.z >> 4) & 0x0F0F0F0Fu), (int)((v.w >> 4) & 0x0F0F0F0Fu)};
+                    const uint32_t sw = u < 2 ? cs.x : cs.y;
+                    const float ws = f16_to_f32((uint16_t)((u & 1) ? (sw >> 16) : (sw & 0xffff)));
+                    float t[NMAX];
+                    [&]<int... I>(std::integer_sequence<int, I...>) {
+                        ((t[I] = I < NMAX ? term_q40<I>(cx[u], cm[u], lo, hi, ws) : 0.0f), ...);
+                    }(std::make_integer_sequence<int, NMAX>{});
 #pragma unroll
-                for (int n = 0; n < NMAX; n++) {
-                    if (n < N) {
-                        sptr_i32 xw = as_scalar_i32(p.x + (size_t)n * p.K + (size_t)b * 32);
-                        const float xsv = as_scalar_f32(p.xs)[(size_t)n * nb + b];
-                        const int xsum = as_scalar_i32(p.xsum)[(size_t)n * nb + b];
-                        // sum (nib - 8) * x == sum nib * x - 8 * sum x (exact in int32)
-                        int d = -8 * xsum;
-                        d = dot4(lo0, xw[0], d);
-                        d = dot4(lo1, xw[1], d);
-                        d = dot4(lo2, xw[2], d);
-                        d = dot4(lo3, xw[3], d);
-                        d = dot4(hi0, xw[4], d);
-                        d = dot4(hi1, xw[5], d);
-                        d = dot4(hi2, xw[6], d);
-                        d = dot4(hi3, xw[7], d);
-                        const float t = (ws * xsv) * (float)d;
-                        if constexpr (S == 1) {
-                            acc[n] = acc[n] + t;
-                        } else {
-                            lds[((wave * U + u) * NMAX + n) * 64 + lane] = t;
+                    for (int n = 0; n < NMAX; n++) {
+                        if (n < N) {
+                            if constexpr (S == 1) acc[n] = acc[n] + t[n];
+                            else lds[((wave * U + u) * NMAX + n) * 64 + lane] = t[n];
                         }
                     }
                 }
@@ -248,7 +283,13 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
             __syncthreads();
         }
 #pragma unroll
-        for (int u = 0; u < U; u++) cur[u] = nxt[u];
+        for (int u = 0; u < U; u++) {
+            cw[u] = nw[u];
+#pragma unroll
+            for (int q = 0; q < NP; q++) cx[u][q] = nx[u][q];
+#pragma unroll
+            for (int q = 0; q < NM; q++) cm[u][q] = nm[u][q];
+        }
         cs = ns;
     }
     gemm_epilogue<NMAX, S>(p, acc, tile, wave, lane);
@@ -309,7 +350,7 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
                     if (n < N) {
                         sptr_i32 xw = as_scalar_i32(p.x + (size_t)n * p.K + (size_t)sb * 256);
                         sptr_f32 xsp = as_scalar_f32(p.xs + (size_t)n * nb + (size_t)sb * 8);
-                        sptr_i32 xap = as_scalar_i32(p.xsum + (size_t)n * nb + (size_t)sb * 8);
+                        sptr_i32 xap = as_scalar_i32(p.xs8 + (size_t)n * nb + (size_t)sb * 8);
                         float part = 0.0f;
 #pragma unroll
                         for (int pr = 0; pr < 4; pr++) {
@@ -323,8 +364,8 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
                             }
                             // q8.rs:1372-1375: sum += xs * (sc*W - mn*A), low then high half
                             const int jl = 2 * pr, jh = 2 * pr + 1;
-                            part = part + xsp[jl] * (sc[jl] * (float)wl - mn[jl] * (float)xap[jl]);
-                            part = part + xsp[jh] * (sc[jh] * (float)wh - mn[jh] * (float)xap[jh]);
+                            part = part + xsp[jl] * (sc[jl] * (float)wl - mn[jl] * (float)(xap[jl] / -8));
+                            part = part + xsp[jh] * (sc[jh] * (float)wh - mn[jh] * (float)(xap[jh] / -8));
                         }
                         if constexpr (S == 1) {
                             acc[n] = acc[n] + part;
@@ -396,20 +437,20 @@ __global__ void blockdots_q4_k_kernel(const uint8_t* w, int nsb, int M, int K, c
 namespace {
 
 template <int NMAX, int S>
-constexpr int pick_u() {
-    // LDS terms: S*U*NMAX*64*4 bytes <= 64 KB
-    return S == 1 ? 8 : (S * NMAX * 8 <= 256 ? 8 : (S * NMAX * 4 <= 256 ? 4 : (S * NMAX * 2 <= 256 ? 2 : 1)));
+constexpr int pick_u_k() {
+    // Q4_K LDS terms: S*U*NMAX*64*4 bytes <= 64 KB, U <= 2 super-blocks per wave
+    return S == 1 ? 2 : (S * NMAX * 2 <= 256 ? 2 : 1);
 }
 
 template <int NMAX, int S>
 int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st) {
-    constexpr int U = pick_u<NMAX, S>();
-    const size_t lds = S > 1 ? (size_t)S * U * NMAX * 64 * sizeof(float) : 0;
     if (w.type == NC_TYPE_Q4_0) {
-        hipLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, U>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+        const size_t lds = S > 1 ? (size_t)S * 4 * NMAX * 64 * sizeof(float) : 0;
+        hipLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
     } else {
-        hipLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, (U > 2 ? 2 : U)>), dim3(p.ntiles), dim3(64 * S),
-                           S > 1 ? (size_t)S * (U > 2 ? 2 : U) * NMAX * 64 * sizeof(float) : 0, st, p);
+        constexpr int U = pick_u_k<NMAX, S>();
+        hipLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, U>), dim3(p.ntiles), dim3(64 * S),
+                           S > 1 ? (size_t)S * U * NMAX * 64 * sizeof(float) : 0, st, p);
     }
     NC_HIP(hipGetLastError());
     return NC_OK;
@@ -429,9 +470,9 @@ int launch_s(int S, const QMatDev& w, const GemmParams& p, hipStream_t st) {
 }  // namespace
 
 // Waves per workgroup: enough K-split waves that ~1000+ waves stream the matrix.
-static int pick_waves(int64_t tiles) {
+static int pick_waves(int64_t tiles, int nmax) {
     int S = 1;
-    while (S < 16 && tiles * S < 1024) S *= 2;
+    while (S < 16 && tiles * S < 1024 && (2 * S) * 4 * nmax <= 256) S *= 2;
     return S;
 }
 
@@ -444,7 +485,15 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st) {
     p.M = (int)w.rows;
     p.K = (int)w.cols;
     if (p.N < 1 || p.N > 16) return fail(NC_EINVAL, "gemm: batch must be 1..16");
-    const int S = pick_waves(w.tiles);
+    const int nmax = p.N == 1 ? 1 : (p.N == 2 ? 2 : (p.N <= 4 ? 4 : (p.N <= 8 ? 8 : 16)));
+    int S = pick_waves(w.tiles, nmax);
+    // NC_GEMM_WAVES=<1|2|4|8|16>: tuning override of the K-split width (LDS limit still applies)
+    static const int forced = [] {
+        const char* e = getenv("NC_GEMM_WAVES");
+        return e ? atoi(e) : 0;
+    }();
+    if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16)
+        S = (forced * 4 * nmax <= 256 || forced == 1) ? forced : S;
     if (p.N == 1) return launch_s<1>(S, w, p, st);
     if (p.N == 2) return launch_s<2>(S, w, p, st);
     if (p.N <= 4) return launch_s<4>(S, w, p, st);

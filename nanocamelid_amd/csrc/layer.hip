@@ -14,8 +14,8 @@
 namespace nc {
 
 // Writes the Q8_0 block (32 values, one per lane of a half-wave) quantised as
-// inference.rs:1012-1029, plus the block's int8 sum used by the GEMM.
-__device__ __forceinline__ void store_q8_block(float y, int lane32, int8_t* q_dst, float* s_dst, int32_t* sum_dst) {
+// inference.rs:1012-1029, plus -8 * (the block's int8 sum) used by the Q4_0 GEMM.
+__device__ __forceinline__ void store_q8_block(float y, int lane32, int8_t* q_dst, float* s_dst, int32_t* s8_dst) {
     const float amax = halfwave_amax(y);
     float scale;
     const int q = quantize_lane_q8(y, amax, &scale);
@@ -23,7 +23,7 @@ __device__ __forceinline__ void store_q8_block(float y, int lane32, int8_t* q_ds
     q_dst[lane32] = (int8_t)q;
     if (lane32 == 0) {
         *s_dst = scale;
-        *sum_dst = qs;
+        *s8_dst = -8 * qs;
     }
 }
 
@@ -42,14 +42,21 @@ __global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float* hidden, co
     __syncthreads();
     __shared__ float s_scale;
     if (threadIdx.x == 0) {
+        // One dependent add per element; the LDS reads of a 64-element chunk are issued
+        // before the chunk's adds so only the add chain is on the critical path.
         float sum = 0.0f;
         const float4* s4 = (const float4*)sq;
-        for (int i = 0; i < d / 4; i++) {
-            const float4 v = s4[i];
-            sum = sum + v.x;
-            sum = sum + v.y;
-            sum = sum + v.z;
-            sum = sum + v.w;
+        for (int i = 0; i < d / 4; i += 16) {
+            float4 v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = s4[i + j];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                sum = sum + v[j].x;
+                sum = sum + v[j].y;
+                sum = sum + v[j].z;
+                sum = sum + v[j].w;
+            }
         }
         s_scale = 1.0f / __builtin_sqrtf(sum / (float)d + eps);
     }
@@ -67,7 +74,7 @@ __global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float* hidden, co
 
 int launch_rmsnorm_q8(const float* hidden, const float* weight, int N, int d, float eps, int8_t* xq, float* xs,
                       int32_t* xsum, hipStream_t st) {
-    if (d % 128) return fail(NC_EINVAL, "rmsnorm: width must be a multiple of 128");
+    if (d % 256) return fail(NC_EINVAL, "rmsnorm: width must be a multiple of 256");
     hipLaunchKernelGGL(rmsnorm_q8_kernel, dim3(N), dim3(256), (size_t)d * sizeof(float), st, hidden, weight, d, eps,
                        xq, xs, xsum);
     NC_HIP(hipGetLastError());
@@ -97,7 +104,7 @@ __global__ void block_sums_kernel(const int8_t* x, int total_blocks, int32_t* xs
     const int8_t* p = x + (size_t)b * 32;
     int s = 0;
     for (int j = 0; j < 32; j++) s += p[j];
-    xsum[b] = s;
+    xsum[b] = -8 * s;
 }
 
 int launch_block_sums(const int8_t* x, int N, int dim, int32_t* xsum, hipStream_t st) {
@@ -141,25 +148,35 @@ int launch_embed(const float* table, const uint32_t* toks, int N, int d, float* 
 // ---------------------------------------------------------------- attention
 // Phase 1: scores[n][h][p] = dot(q[n][h], k[p]) * scale for p <= pos_n
 // (inference.rs:4252-4257; dot_f32_scalar folds a*b from -0.0 in index order).
-// Workgroup = one KV head x 64 positions; wave g = query head kvh*G + g; lane = p.
+// Workgroup = one KV head x 64 positions: the K tile is staged once in LDS (rows padded
+// to HD+4 floats so the per-lane row reads are bank-conflict free) and shared by the
+// G query-head waves; lane = position p, each lane keeps k_p in VGPRs across rows n.
 template <int HD>
 __global__ __launch_bounds__(1024) void attn_scores_kernel(AttnParams a) {
+    constexpr int RS = HD + 4;
+    __shared__ float kt[64 * RS];
     const int kvh = blockIdx.y;
     const int G = a.H / a.Hkv;
     const int g = wave_id_uniform();
-    if (g >= G) return;
     const int h = kvh * G + g;
     const int lane = threadIdx.x & 63;
     const int pos0 = a.d_pos[0];
     const int last = pos0 + a.N - 1;
     for (int tile = blockIdx.x; tile * 64 <= last; tile += gridDim.x) {
+        __syncthreads();  // previous tile's readers are done with kt
+        const int rows = min(64, last + 1 - tile * 64);
+        const float4* src = (const float4*)(a.kcache + ((size_t)kvh * a.max_ctx + (size_t)tile * 64) * HD);
+        for (int i = threadIdx.x; i < rows * (HD / 4); i += blockDim.x) {
+            const int r = i / (HD / 4), c = i % (HD / 4);
+            *(float4*)&kt[r * RS + c * 4] = src[(size_t)r * (HD / 4) + c];
+        }
+        __syncthreads();
         const int p = tile * 64 + lane;
         float k[HD];
         if (p <= last) {
-            const float4* kp = (const float4*)(a.kcache + ((size_t)kvh * a.max_ctx + p) * HD);
 #pragma unroll
             for (int i = 0; i < HD / 4; i++) {
-                const float4 v = kp[i];
+                const float4 v = *(const float4*)&kt[lane * RS + i * 4];
                 k[4 * i] = v.x;
                 k[4 * i + 1] = v.y;
                 k[4 * i + 2] = v.z;
@@ -179,75 +196,80 @@ __global__ __launch_bounds__(1024) void attn_scores_kernel(AttnParams a) {
     }
 }
 
-// Phase 2: softmax over 0..=pos (inference.rs:3522-3540): max, e = expf(s - max),
-// sequential sum, probabilities e * (1/sum) written back in place.
-__global__ __launch_bounds__(256) void attn_softmax_kernel(AttnParams a) {
-    extern __shared__ float e[];
-    const int unit = blockIdx.x;  // n * H + h
-    const int n = unit / a.H;
-    const int L = a.d_pos[0] + n + 1;
-    float* s = a.scores + (size_t)unit * a.max_ctx;
-    __shared__ float red[256];
-    float mx = -__builtin_inff();
-    for (int p = threadIdx.x; p < L; p += blockDim.x) {
-        const float v = s[p];
-        mx = v > mx ? v : mx;
-    }
-    red[threadIdx.x] = mx;
-    __syncthreads();
-    for (int off = 128; off >= 1; off >>= 1) {
-        if (threadIdx.x < off) {
-            const float o = red[threadIdx.x + off];
-            red[threadIdx.x] = o > red[threadIdx.x] ? o : red[threadIdx.x];
-        }
-        __syncthreads();
-    }
-    mx = red[0];
-    for (int p = threadIdx.x; p < L; p += blockDim.x) e[p] = expf_glibc(s[p] - mx);
-    __syncthreads();
-    __shared__ float s_inv;
-    if (threadIdx.x == 0) {
-        float sum = 0.0f;
-        int p = 0;
-        const float4* e4 = (const float4*)e;
-        for (; p + 4 <= L; p += 4) {
-            const float4 v = e4[p / 4];
-            sum = sum + v.x;
-            sum = sum + v.y;
-            sum = sum + v.z;
-            sum = sum + v.w;
-        }
-        for (; p < L; p++) sum = sum + e[p];
-        s_inv = 1.0f / sum;
-    }
-    __syncthreads();
-    const float inv = s_inv;
-    for (int p = threadIdx.x; p < L; p += blockDim.x) s[p] = e[p] * inv;
-}
-
-// Phase 3: out[d] = sum_p prob_p * v_p[d] sequentially in p (add_weighted_f32_scalar,
-// inference.rs:3603-3623, starting from the zero-filled output), then the Q8_0
-// quantisation of the attention output row (inference.rs:3971-3977): each 32-lane
-// group holds exactly one quantisation block of (row n, head h).
-__global__ __launch_bounds__(256) void attn_pv_kernel(AttnParams a) {
+// Phase 2 (fused): softmax over 0..=pos (inference.rs:3522-3540) and the weighted V sum
+// (add_weighted_f32_scalar, inference.rs:3603-3623) for two (row, head) units per
+// workgroup; half-wave u owns unit u and 32 output dims.  max is order free; e_p =
+// expf(s_p - max) goes to LDS; lane 0 of the half-wave adds e_0, e_1, ... in order;
+// prob_p = e_p * (1/sum); out[d] = ((0 + prob_0*v_0[d]) + prob_1*v_1[d]) + ... in order.
+// The output block of 32 dims is then quantised to Q8_0 for the wo matmul.
+__global__ __launch_bounds__(64) void attn_softmax_pv_kernel(AttnParams a) {
+    extern __shared__ float e[];  // [2][a.max_pos + 1 rounded up to 4]
     const int kvh = blockIdx.x;
     const int dchunk = blockIdx.y;
     const int G = a.H / a.Hkv;
-    const int unit = blockIdx.z * 8 + (threadIdx.x >> 5);  // (n, g) pair
-    if (unit >= a.N * G) return;                         // whole half-wave exits together
-    const int n = unit / G, g = unit % G;
+    const int lane = threadIdx.x & 63;
+    const int u = lane >> 5, lane32 = lane & 31;
+    const int unit = blockIdx.z * 2 + u;  // (n, g) pair
+    const bool active = unit < a.N * G;  // half-wave uniform
+    const int n = active ? unit / G : 0, g = active ? unit % G : 0;
     const int h = kvh * G + g;
-    const int lane32 = threadIdx.x & 31;
+    const int L = a.d_pos[0] + n + 1;
+    const int stride = ((a.max_pos + 1) + 3) & ~3;
+    float* eu = e + u * stride;
+    const float* s = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
+    float mx = -__builtin_inff();
+    if (active)
+        for (int p = lane32; p < L; p += 32) {
+            const float v = s[p];
+            mx = v > mx ? v : mx;
+        }
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(mx, off, 64);
+        mx = o > mx ? o : mx;
+    }
+    if (active)
+        for (int p = lane32; p < L; p += 32) eu[p] = expf_glibc(s[p] - mx);
+    __syncthreads();
+    float inv = 0.0f;
+    if (active && lane32 == 0) {
+        float sum = 0.0f;
+        int p = 0;
+        for (; p + 32 <= L; p += 32) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = *(const float4*)&eu[p + 4 * j];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                sum = sum + v[j].x;
+                sum = sum + v[j].y;
+                sum = sum + v[j].z;
+                sum = sum + v[j].w;
+            }
+        }
+        for (; p < L; p++) sum = sum + eu[p];
+        inv = 1.0f / sum;
+    }
+    inv = __shfl(inv, u * 32, 64);
+    if (!active) return;  // no barriers below
     const int d = dchunk * 32 + lane32;
-    const int pos = a.d_pos[0] + n;
-    const float* prob = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
     const float* v = a.vcache + (size_t)kvh * a.max_ctx * a.hd + d;
     float acc = 0.0f;
-    for (int p = 0; p <= pos; p++) acc = acc + prob[p] * v[(size_t)p * a.hd];
+    int p = 0;
+    for (; p + 16 <= L; p += 16) {
+        float vv[16], pr[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) vv[j] = v[(size_t)(p + j) * a.hd];
+#pragma unroll
+        for (int j = 0; j < 16; j++) pr[j] = eu[p + j] * inv;
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc = acc + pr[j] * vv[j];
+    }
+    for (; p < L; p++) acc = acc + (eu[p] * inv) * v[(size_t)p * a.hd];
     const int aw = a.H * a.hd;
     const int col = h * a.hd + dchunk * 32;
     store_q8_block(acc, lane32, a.xq + (size_t)n * aw + col, a.xs + (size_t)n * (aw / 32) + col / 32,
-                   a.xsum + (size_t)n * (aw / 32) + col / 32);
+                   a.xs8 + (size_t)n * (aw / 32) + col / 32);
 }
 
 int launch_attention(const AttnParams& a, hipStream_t st) {
@@ -261,11 +283,9 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
     else
         return fail(NC_EINVAL, "attention: head_dim must be 64 or 128");
     NC_HIP(hipGetLastError());
-    const size_t lds = (size_t)(a.max_pos + 1) * sizeof(float);
-    if (lds > 160 * 1024) return fail(NC_ERANGE, "attention: context too long for the softmax kernel");
-    hipLaunchKernelGGL(attn_softmax_kernel, dim3(a.N * a.H), dim3(256), lds, st, a);
-    NC_HIP(hipGetLastError());
-    hipLaunchKernelGGL(attn_pv_kernel, dim3(a.Hkv, a.hd / 32, (a.N * G + 7) / 8), dim3(256), 0, st, a);
+    const size_t lds = 2 * (size_t)(((a.max_pos + 1) + 3) & ~3) * sizeof(float);
+    if (lds > 160 * 1024) return fail(NC_ERANGE, "attention: context too long for the fused softmax kernel");
+    hipLaunchKernelGGL(attn_softmax_pv_kernel, dim3(a.Hkv, a.hd / 32, (a.N * G + 1) / 2), dim3(64), lds, st, a);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }

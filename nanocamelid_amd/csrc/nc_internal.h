@@ -69,7 +69,7 @@ struct GemmParams {
     int ntiles = 0, units = 0, groups = 0, M = 0, K = 0, N = 0;
     const int8_t* x = nullptr;     // [N][K]
     const float* xs = nullptr;     // [N][K/32]
-    const int32_t* xsum = nullptr; // [N][K/32] sum of the 32 int8 values of each block
+    const int32_t* xs8 = nullptr;  // [N][K/32] -8 * (sum of the 32 int8 values of each block)
     int epi = EPI_STORE;
     float* out = nullptr;
     int ld_out = 0;
@@ -83,7 +83,7 @@ struct GemmParams {
     // EPI_SWIGLU_Q8
     int8_t* xq_out = nullptr;
     float* xs_out = nullptr;
-    int32_t* xsum_out = nullptr;
+    int32_t* xs8_out = nullptr;
     int F = 0;
     // EPI_HEAD
     float* part_val = nullptr;  // [N][ntiles]
@@ -95,9 +95,10 @@ int launch_blockdots(const QMatDev& w, const int8_t* x, int32_t* dots, int N, hi
 
 // ---------------------------------------------------------------- layer kernels
 int launch_rmsnorm_q8(const float* hidden, const float* weight, int N, int d, float eps, int8_t* xq, float* xs,
-                      int32_t* xsum, hipStream_t stream);
-int launch_quantize_q8(const float* x, int N, int dim, int8_t* xq, float* xs, int32_t* xsum, hipStream_t stream);
-int launch_block_sums(const int8_t* x, int N, int dim, int32_t* xsum, hipStream_t stream);
+                      int32_t* xs8, hipStream_t stream);
+// Activation side buffers: xs = per-block f32 scale, xs8 = -8 * per-block int8 sum.
+int launch_quantize_q8(const float* x, int N, int dim, int8_t* xq, float* xs, int32_t* xs8, hipStream_t stream);
+int launch_block_sums(const int8_t* x, int N, int dim, int32_t* xs8, hipStream_t stream);
 struct TokenArgs {
     uint32_t t[16];
 };
@@ -111,7 +112,7 @@ struct AttnParams {
     float* scores = nullptr;  // [N][H][max_ctx]
     int8_t* xq = nullptr;     // [N][H*hd] quantised attention output
     float* xs = nullptr;
-    int32_t* xsum = nullptr;
+    int32_t* xs8 = nullptr;
     const int32_t* d_pos = nullptr;
     int N = 0, H = 0, Hkv = 0, hd = 0, max_ctx = 0, max_pos = 0;
     float scale = 0.f;

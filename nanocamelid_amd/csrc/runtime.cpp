@@ -54,7 +54,7 @@ struct nc_session {
     float* hidden = nullptr;                     // [B][d]
     int8_t* xq = nullptr;                        // [B][maxw]
     float* xs = nullptr;                         // [B][maxw/32]
-    int32_t* xsum = nullptr;
+    int32_t* xs8 = nullptr;  // -8 * per-block int8 sums
     float* q = nullptr;       // [B][aw]
     float* scores = nullptr;  // [B][H][max_ctx]
     float* logits = nullptr;  // [B][V]
@@ -518,12 +518,12 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
     const size_t layer_kv = (size_t)Hkv * s->max_ctx * hd;
     for (int64_t li = 0; li < c.block_count; li++) {
         const LayerDev& L = m->layers[li];
-        if ((rc = launch_rmsnorm_q8(s->hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xsum, st)))
+        if ((rc = launch_rmsnorm_q8(s->hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
             return rc;
         GemmParams p;
         p.x = s->xq;
         p.xs = s->xs;
-        p.xsum = s->xsum;
+        p.xs8 = s->xs8;
         p.N = n;
         p.epi = EPI_QKV_ROPE;
         p.q_out = s->q;
@@ -545,7 +545,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
         a.scores = s->scores;
         a.xq = s->xq;
         a.xs = s->xs;
-        a.xsum = s->xsum;
+        a.xs8 = s->xs8;
         a.d_pos = s->d_pos;
         a.N = n;
         a.H = (int)c.head_count;
@@ -558,33 +558,32 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
         GemmParams po;
         po.x = s->xq;
         po.xs = s->xs;
-        po.xsum = s->xsum;
+        po.xs8 = s->xs8;
         po.N = n;
         po.epi = EPI_RESIDUAL;
         po.out = s->hidden;
         po.ld_out = d;
         if ((rc = timed_gemm(s, L.wo, po))) return rc;
-        if ((rc = launch_rmsnorm_q8(s->hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xsum, st)))
+        if ((rc = launch_rmsnorm_q8(s->hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
             return rc;
         GemmParams pg;
         pg.x = s->xq;
         pg.xs = s->xs;
-        pg.xsum = s->xsum;
+        pg.xs8 = s->xs8;
         pg.N = n;
         pg.epi = EPI_SWIGLU_Q8;
         pg.xq_out = s->xq;  // gate/up read xq[.][0..d) and write xq[.][0..F): different kernels
         pg.xs_out = s->xs;
-        pg.xsum_out = s->xsum;
-        pg.F = F;
+                pg.F = F;
         // In-place would race (readers of row n's block b vs writers); use the upper half.
         pg.xq_out = s->xq + (size_t)s->max_batch * s->maxw;
         pg.xs_out = s->xs + (size_t)s->max_batch * (s->maxw / 32);
-        pg.xsum_out = s->xsum + (size_t)s->max_batch * (s->maxw / 32);
+        pg.xs8_out = s->xs8 + (size_t)s->max_batch * (s->maxw / 32);
         if ((rc = timed_gemm(s, L.gateup, pg))) return rc;
         GemmParams pd;
         pd.x = pg.xq_out;
         pd.xs = pg.xs_out;
-        pd.xsum = pg.xsum_out;
+        pd.xs8 = pg.xs8_out;
         pd.N = n;
         pd.epi = EPI_RESIDUAL;
         pd.out = s->hidden;
@@ -592,11 +591,11 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
         if ((rc = timed_gemm(s, L.down, pd))) return rc;
     }
     // compute_logits_from_hidden (inference.rs:4783-4832) for every row + argmax
-    if ((rc = launch_rmsnorm_q8(s->hidden, m->out_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xsum, st))) return rc;
+    if ((rc = launch_rmsnorm_q8(s->hidden, m->out_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st))) return rc;
     GemmParams ph;
     ph.x = s->xq;
     ph.xs = s->xs;
-    ph.xsum = s->xsum;
+    ph.xs8 = s->xs8;
     ph.N = n;
     ph.epi = EPI_HEAD;
     ph.out = s->logits;
@@ -744,7 +743,7 @@ int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8,
     GemmParams p;
     p.x = x_i8;
     p.xs = x_scales;
-    p.xsum = ctx->xsum;
+    p.xs8 = ctx->xsum;
     p.N = batch_size;
     p.epi = EPI_STORE;
     p.out = out;
@@ -833,7 +832,7 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
         (rc = dev_alloc(s->allocs, &s->hidden, B * c.embedding_length)) ||
         (rc = dev_alloc(s->allocs, &s->xq, 2 * B * s->maxw)) ||
         (rc = dev_alloc(s->allocs, &s->xs, 2 * B * (s->maxw / 32))) ||
-        (rc = dev_alloc(s->allocs, &s->xsum, 2 * B * (s->maxw / 32))) ||
+        (rc = dev_alloc(s->allocs, &s->xs8, 2 * B * (s->maxw / 32))) ||
         (rc = dev_alloc(s->allocs, &s->q, B * c.attention_output_width)) ||
         (rc = dev_alloc(s->allocs, &s->scores, (size_t)B * c.head_count * max_ctx)) ||
         (rc = dev_alloc(s->allocs, &s->logits, (size_t)B * c.vocab_size)) ||
