@@ -212,7 +212,8 @@ uint32_t nc_oracle_draft(uint64_t seed, int64_t p, float alpha, const uint32_t* 
 /* ---------------------------------------------------------------- timing hooks */
 /* Average device time (ms) per launch of the named kernel family recorded with HIP
  * events on the session stream since the last reset; used by the benchmark's
- * roofline.  family: "gemm_q4_0" (all verify matmuls).  Returns launches counted. */
+ * roofline.  family: "gemm_q4_0" (all verify matmuls).  Prompt prefill passes are
+ * never timed: only decode and verify passes count.  Returns launches counted. */
 int64_t nc_session_kernel_timing(nc_session* s, const char* family, double* total_ms, int64_t* bytes);
 int nc_session_timing_enable(nc_session* s, int32_t enable);
 

@@ -19,6 +19,8 @@
 #include <cstdlib>
 #include <utility>
 
+#include <hip/hip_ext.h>
+
 #include "nc_device.h"
 #include "nc_internal.h"
 
@@ -442,28 +444,37 @@ constexpr int pick_u_k() {
     return S == 1 ? 2 : (S * NMAX * 2 <= 256 ? 2 : 1);
 }
 
+// ev0/ev1 (optional): events stamped by the dispatch itself at kernel start and end
+// (hipExtLaunchKernelGGL), so their elapsed time is the kernel's own duration.
 template <int NMAX, int S>
-int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st) {
+int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     if (w.type == NC_TYPE_Q4_0) {
         const size_t lds = S > 1 ? (size_t)S * 4 * NMAX * 64 * sizeof(float) : 0;
-        hipLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+        if (ev0)
+            hipExtLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0, p);
+        else
+            hipLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
     } else {
         constexpr int U = pick_u_k<NMAX, S>();
-        hipLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, U>), dim3(p.ntiles), dim3(64 * S),
-                           S > 1 ? (size_t)S * U * NMAX * 64 * sizeof(float) : 0, st, p);
+        const size_t lds = S > 1 ? (size_t)S * U * NMAX * 64 * sizeof(float) : 0;
+        if (ev0)
+            hipExtLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, U>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0,
+                                  p);
+        else
+            hipLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, U>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
     }
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
 
 template <int NMAX>
-int launch_s(int S, const QMatDev& w, const GemmParams& p, hipStream_t st) {
+int launch_s(int S, const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     switch (S) {
-        case 1: return launch_one<NMAX, 1>(w, p, st);
-        case 2: return launch_one<NMAX, 2>(w, p, st);
-        case 4: return launch_one<NMAX, 4>(w, p, st);
-        case 8: return launch_one<NMAX, 8>(w, p, st);
-        default: return launch_one<NMAX, 16>(w, p, st);
+        case 1: return launch_one<NMAX, 1>(w, p, st, ev0, ev1);
+        case 2: return launch_one<NMAX, 2>(w, p, st, ev0, ev1);
+        case 4: return launch_one<NMAX, 4>(w, p, st, ev0, ev1);
+        case 8: return launch_one<NMAX, 8>(w, p, st, ev0, ev1);
+        default: return launch_one<NMAX, 16>(w, p, st, ev0, ev1);
     }
 }
 
@@ -476,7 +487,7 @@ static int pick_waves(int64_t tiles, int nmax) {
     return S;
 }
 
-int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st) {
+int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     GemmParams p = p0;
     p.w = w.dev;
     p.ntiles = (int)w.tiles;
@@ -494,11 +505,11 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st) {
     }();
     if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16)
         S = (forced * 4 * nmax <= 256 || forced == 1) ? forced : S;
-    if (p.N == 1) return launch_s<1>(S, w, p, st);
-    if (p.N == 2) return launch_s<2>(S, w, p, st);
-    if (p.N <= 4) return launch_s<4>(S, w, p, st);
-    if (p.N <= 8) return launch_s<8>(S, w, p, st);
-    return launch_s<16>(S, w, p, st);
+    if (p.N == 1) return launch_s<1>(S, w, p, st, ev0, ev1);
+    if (p.N == 2) return launch_s<2>(S, w, p, st, ev0, ev1);
+    if (p.N <= 4) return launch_s<4>(S, w, p, st, ev0, ev1);
+    if (p.N <= 8) return launch_s<8>(S, w, p, st, ev0, ev1);
+    return launch_s<16>(S, w, p, st, ev0, ev1);
 }
 
 int launch_blockdots(const QMatDev& w, const int8_t* x, int32_t* dots, int N, hipStream_t st) {

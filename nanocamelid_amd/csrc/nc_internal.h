@@ -90,7 +90,9 @@ struct GemmParams {
     int32_t* part_idx = nullptr;
 };
 
-int launch_gemm(const QMatDev& w, const GemmParams& p, hipStream_t stream);
+// ev0/ev1: optional events stamped at the kernel's own start and end (timing).
+int launch_gemm(const QMatDev& w, const GemmParams& p, hipStream_t stream, hipEvent_t ev0 = nullptr,
+                hipEvent_t ev1 = nullptr);
 int launch_blockdots(const QMatDev& w, const int8_t* x, int32_t* dots, int N, hipStream_t stream);
 
 // ---------------------------------------------------------------- layer kernels

@@ -476,9 +476,7 @@ static int timed_gemm(nc_session* s, const QMatDev& w, const GemmParams& p) {
         s->ev_used = 0;
     }
     auto& e = s->ev[s->ev_used++];
-    NC_HIP(hipEventRecord(e.first, s->stream));
-    int rc = launch_gemm(w, p, s->stream);
-    NC_HIP(hipEventRecord(e.second, s->stream));
+    int rc = launch_gemm(w, p, s->stream, e.first, e.second);
     s->gemm_launches++;
     // algorithmic bytes: weights + int8 activations + f32 scales + f32 outputs
     s->pending_bytes += w.algo_bytes + (int64_t)p.N * w.cols + 4 * (int64_t)p.N * (w.cols / 32) + 4 * (int64_t)p.N * w.rows;
@@ -627,6 +625,13 @@ static int fetch_preds(nc_session* s, int n, uint32_t* out) {
 // prefill_tokens (main.rs:9415-9485): chunks of max_batch rows.  Returns the last row's
 // greedy prediction in *last_pred.
 static int prefill_chunks(nc_session* s, const uint32_t* toks, int n, int64_t start_pos, uint32_t* last_pred) {
+    // per-kernel timing covers decode and verify passes only, never the prompt
+    struct TimingOff {
+        nc_session* s;
+        bool was;
+        ~TimingOff() { s->timing = was; }
+    } guard{s, s->timing};
+    s->timing = false;
     int rc;
     for (int i = 0; i < n; i += s->max_batch) {
         const int len = std::min(s->max_batch, n - i);
