@@ -88,6 +88,15 @@ int nc_matmul_blockdots(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, int32
 int nc_quantize_q8_0_batch(nc_ctx* ctx, const float* x, int8_t* x_i8, float* x_scales, int batch_size,
                            int64_t dim, void* stream);
 
+/* RMSNorm then Q8_0 quantisation of each row: scale = 1/sqrt(sum/dim + eps) with the sum of
+ * squares taken left to right in f32 (bit-identical), y = x*scale*w, then the per-32-block
+ * quantiser above.  Replaces rms_norm_batch (src/inference.rs:949-967, row op :697-706)
+ * followed by quantize_f32_to_q8_0_batch (:967-989), as run_layer_range_batch does at
+ * :3802-3808.  Device pointers: x [batch][dim], w [dim], x_i8 [batch][dim],
+ * x_scales [batch][dim/32].  dim = 256 * {1,2,3,4,6,8,12,16,20,24,32}. */
+int nc_rms_norm_q8_0_batch(nc_ctx* ctx, const float* x, const float* w, float eps, int8_t* x_i8, float* x_scales,
+                           int batch_size, int64_t dim, void* stream);
+
 /* ---------------------------------------------------------------- model */
 typedef struct nc_model_config {
     int64_t context_length, embedding_length, block_count, feed_forward_length;

@@ -120,6 +120,18 @@ def quantize_f32_to_q8_0_batch(ctx: Context, x):
     return q, s
 
 
+def rms_norm_q8_0_batch(ctx: Context, x, w, eps: float):
+    """RMSNorm (sequential f32 sum of squares, bit-identical) then Q8_0 quantisation on the
+    GPU (src/inference.rs:949-967 and :967-1029, as run at :3802-3808)."""
+    import torch
+    n, dim = x.shape
+    q = torch.empty((n, dim), dtype=torch.int8, device=x.device)
+    s = torch.empty((n, dim // 32), dtype=torch.float32, device=x.device)
+    check(lib().nc_rms_norm_q8_0_batch(ctx.h, x.data_ptr(), w.data_ptr(), float(eps), q.data_ptr(), s.data_ptr(), n,
+                                       dim, _stream_of(x)))
+    return q, s
+
+
 class Model:
     """Llama weights on the device (LlamaWeights::load, src/model.rs:461-545)."""
 

@@ -66,6 +66,7 @@ SIGNATURES = {
     "nc_matmul_quantized_batch": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _vp]),
     "nc_matmul_blockdots": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _vp]),
     "nc_quantize_q8_0_batch": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _vp]),
+    "nc_rms_norm_q8_0_batch": (C.c_int, [_vp, _vp, _vp, C.c_float, _vp, _vp, C.c_int, _i64, _vp]),
     "nc_model_load_gguf": (C.c_int, [_vp, C.c_char_p, C.POINTER(LoadOpts), C.POINTER(_vp)]),
     "nc_model_load_gguf_memory": (C.c_int, [_vp, _vp, C.c_size_t, C.POINTER(LoadOpts), C.POINTER(_vp)]),
     "nc_model_get_config": (C.c_int, [_vp, C.POINTER(ModelConfig)]),

@@ -3,12 +3,14 @@
 // HBM-resident f32 KV cache (with the Q8_0 quantisation of its output fused in),
 // the head argmax reduction and greedy acceptance.
 //
-// All f32 chains that the reference evaluates sequentially (the RMSNorm sum of
-// squares, each attention dot product, the softmax denominator, the weighted V
-// sum) are evaluated sequentially here too, so results match the reference's
-// portable path bit for bit; the parallel parts are the order-free ones (max,
-// elementwise maps, integer sums, independent rows/heads/positions).
+// Every f32 chain that the reference evaluates sequentially gives the same bits here:
+// the RMSNorm sum of squares goes through exact_chain_sum (a parallel evaluation that is
+// verified step by step against the sequential recurrence); each attention dot product,
+// the softmax denominator and the weighted V sum are evaluated in order.  The parallel
+// parts are the order-free ones (max, elementwise maps, integer sums, independent
+// rows/heads/positions).
 #include "nc_device.h"
+#include "nc_chain.h"
 #include "nc_internal.h"
 
 namespace nc {
@@ -29,42 +31,28 @@ __device__ __forceinline__ void store_q8_block(float y, int lane32, int8_t* q_ds
 
 // ---------------------------------------------------------------- RMSNorm + Q8_0
 // rms_norm (inference.rs:697-706): sum += x*x sequentially, scale = 1/sqrt(sum/n + eps),
-// y = x*scale*w; then quantize_f32_to_q8_0 of y (inference.rs:3802-3808).
-__global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float* hidden, const float* weight, int d, float eps,
+// y = x*scale*w; then quantize_f32_to_q8_0 of y (inference.rs:3802-3808).  The sequential
+// sum is evaluated by exact_chain_sum (bit-identical to the left-to-right loop).  One
+// workgroup of 256 threads per row; thread t owns elements [t*E, t*E + E).
+template <int E>
+__global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float* hidden, const float* weight, float eps,
                                                           int8_t* xq, float* xs, int32_t* xsum) {
-    extern __shared__ float sq[];  // d squares, then the scale
+    constexpr int T = 256, d = T * E;
+    __shared__ ChainScratch<T> sc;
+    __shared__ float a_lds[d];
     const int n = blockIdx.x;
     const float* x = hidden + (size_t)n * d;
-    for (int i = threadIdx.x; i < d; i += blockDim.x) {
-        const float v = x[i];
-        sq[i] = v * v;
-    }
-    __syncthreads();
-    __shared__ float s_scale;
-    if (threadIdx.x == 0) {
-        // One dependent add per element; the LDS reads of a 64-element chunk are issued
-        // before the chunk's adds so only the add chain is on the critical path.
-        float sum = 0.0f;
-        const float4* s4 = (const float4*)sq;
-        for (int i = 0; i < d / 4; i += 16) {
-            float4 v[16];
+    float a[E];
 #pragma unroll
-            for (int j = 0; j < 16; j++) v[j] = s4[i + j];
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                sum = sum + v[j].x;
-                sum = sum + v[j].y;
-                sum = sum + v[j].z;
-                sum = sum + v[j].w;
-            }
-        }
-        s_scale = 1.0f / __builtin_sqrtf(sum / (float)d + eps);
+    for (int j = 0; j < E; j++) {
+        const float v = x[threadIdx.x * E + j];
+        a[j] = v * v;
     }
-    __syncthreads();
-    const float scale = s_scale;
+    const float sum = exact_chain_sum<E, T>(a, sc, a_lds);
+    const float scale = 1.0f / __builtin_sqrtf(sum / (float)d + eps);
     const int lane32 = threadIdx.x & 31;
     const int half = threadIdx.x >> 5;  // 8 half-waves
-    for (int b = half; b < d / 32; b += blockDim.x / 32) {
+    for (int b = half; b < d / 32; b += T / 32) {
         const int i = b * 32 + lane32;
         const float y = x[i] * scale * weight[i];
         store_q8_block(y, lane32, xq + (size_t)n * d + b * 32, xs + (size_t)n * (d / 32) + b,
@@ -74,9 +62,26 @@ __global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float* hidden, co
 
 int launch_rmsnorm_q8(const float* hidden, const float* weight, int N, int d, float eps, int8_t* xq, float* xs,
                       int32_t* xsum, hipStream_t st) {
-    if (d % 256) return fail(NC_EINVAL, "rmsnorm: width must be a multiple of 256");
-    hipLaunchKernelGGL(rmsnorm_q8_kernel, dim3(N), dim3(256), (size_t)d * sizeof(float), st, hidden, weight, d, eps,
-                       xq, xs, xsum);
+#define NC_RMS_CASE(E)                                                                                      \
+    case E:                                                                                                 \
+        hipLaunchKernelGGL(rmsnorm_q8_kernel<E>, dim3(N), dim3(256), 0, st, hidden, weight, eps, xq, xs, xsum); \
+        break;
+    switch (d % 256 ? 0 : d / 256) {
+        NC_RMS_CASE(1)
+        NC_RMS_CASE(2)
+        NC_RMS_CASE(3)
+        NC_RMS_CASE(4)
+        NC_RMS_CASE(6)
+        NC_RMS_CASE(8)
+        NC_RMS_CASE(12)
+        NC_RMS_CASE(16)
+        NC_RMS_CASE(20)
+        NC_RMS_CASE(24)
+        NC_RMS_CASE(32)
+        default:
+            return fail(NC_EINVAL, "rmsnorm: width must be 256 * {1,2,3,4,6,8,12,16,20,24,32}");
+    }
+#undef NC_RMS_CASE
     NC_HIP(hipGetLastError());
     return NC_OK;
 }

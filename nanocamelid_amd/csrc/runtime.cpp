@@ -773,6 +773,17 @@ int nc_quantize_q8_0_batch(nc_ctx* ctx, const float* x, int8_t* x_i8, float* x_s
     return launch_quantize_q8(x, batch_size, (int)dim, x_i8, x_scales, ctx->xsum, stream ? (hipStream_t)stream : ctx->stream);
 }
 
+int nc_rms_norm_q8_0_batch(nc_ctx* ctx, const float* x, const float* w, float eps, int8_t* x_i8, float* x_scales,
+                           int batch_size, int64_t dim, void* stream) {
+    if (!ctx || !x || !w || !x_i8 || !x_scales || batch_size < 1 || dim < 256)
+        return fail(NC_EINVAL, "nc_rms_norm_q8_0_batch: bad arguments");
+    NC_HIP(hipSetDevice(ctx->device));
+    int rc = ensure_xsum(ctx, (size_t)batch_size * (dim / 32));
+    if (rc) return rc;
+    return launch_rmsnorm_q8(x, w, batch_size, (int)dim, eps, x_i8, x_scales, ctx->xsum,
+                             stream ? (hipStream_t)stream : ctx->stream);
+}
+
 int nc_model_load_gguf_memory(nc_ctx* ctx, const void* data, size_t size, const nc_load_opts* opts, nc_model** out) {
     if (!ctx || !data || !out) return fail(NC_EINVAL, "nc_model_load_gguf_memory: null argument");
     NC_HIP(hipSetDevice(ctx->device));
