@@ -34,29 +34,133 @@ __device__ __forceinline__ void store_q8_block(float y, int lane32, int8_t* q_ds
 // y = x*scale*w; then quantize_f32_to_q8_0 of y (inference.rs:3802-3808).  The sequential
 // sum is evaluated by exact_chain_sum (bit-identical to the left-to-right loop).  One
 // workgroup of 256 threads per row; thread t owns elements [t*E, t*E + E).
+// Q8_0 quantisation of a row held in LDS (quantize_f32_to_q8_0, inference.rs:1012-1029):
+// 8 lanes per 32-block, 4 values per lane, all blocks of the row in one pass.
+template <int T>
+__device__ __forceinline__ void quantize_row_lds_q8(const float* y, int d, int8_t* q, float* s, int32_t* s8) {
+    for (int g = threadIdx.x; g < d / 4; g += T) {  // d % 32 == 0: 8-lane groups stay whole
+        const float4 v = *(const float4*)(y + 4 * g);
+        float amax = __builtin_fabsf(v.x);
+        amax = __builtin_fabsf(v.y) > amax ? __builtin_fabsf(v.y) : amax;
+        amax = __builtin_fabsf(v.z) > amax ? __builtin_fabsf(v.z) : amax;
+        amax = __builtin_fabsf(v.w) > amax ? __builtin_fabsf(v.w) : amax;
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            const float o = __shfl_xor(amax, off, 8);
+            amax = o > amax ? o : amax;
+        }
+        float scale;
+        const int q0 = quantize_lane_q8(v.x, amax, &scale);
+        const int q1 = quantize_lane_q8(v.y, amax, &scale);
+        const int q2 = quantize_lane_q8(v.z, amax, &scale);
+        const int q3 = quantize_lane_q8(v.w, amax, &scale);
+        int qs = q0 + q1 + q2 + q3;
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) qs += __shfl_xor(qs, off, 8);
+        *(int*)(q + 4 * g) = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((q3 & 0xff) << 24);
+        if ((g & 7) == 0) {
+            s[g >> 3] = scale;
+            s8[g >> 3] = -8 * qs;
+        }
+    }
+}
+
+// Exact max / sum over aligned groups of W lanes (W = 1, 2, 4, ..., 32).
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (W >= 2) {
+        const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));
+        v = o > v ? o : v;
+    }
+    if constexpr (W >= 4) {
+        const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));
+        v = o > v ? o : v;
+    }
+#pragma unroll
+    for (int off = 4; off < W; off <<= 1) {
+        const float o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+template <int W>
+__device__ __forceinline__ int group_sum(int v) {
+    if constexpr (W >= 2) v += __builtin_amdgcn_mov_dpp(v, 0xb1, 0xf, 0xf, false);
+    if constexpr (W >= 4) v += __builtin_amdgcn_mov_dpp(v, 0x4e, 0xf, 0xf, false);
+#pragma unroll
+    for (int off = 4; off < W; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Q8_0 quantisation (inference.rs:1012-1029) of a row whose 32-blocks are split across
+// 32/E consecutive lanes holding E values each (register resident, no LDS).
+template <int E>
+__device__ __forceinline__ void quantize_regs_q8(const float (&y)[E], int8_t* q_row, float* s_row, int32_t* s8_row) {
+    constexpr int W = 32 / E;
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < E; j++) amax = __builtin_fabsf(y[j]) > amax ? __builtin_fabsf(y[j]) : amax;
+    amax = group_max<W>(amax);
+    const float scale = amax / 127.0f;
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    int qv[E];
+    int qs = 0;
+#pragma unroll
+    for (int j = 0; j < E; j++) {
+        float r = round_half_away(y[j] * inv);
+        r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+        qv[j] = scale > 0.0f ? (int)r : 0;
+        qs += qv[j];
+    }
+    qs = group_sum<W>(qs);
+    int8_t* dst = q_row + threadIdx.x * E;
+    if constexpr (E >= 4) {
+#pragma unroll
+        for (int j = 0; j < E; j += 4)
+            *(int*)(dst + j) = (qv[j] & 0xff) | ((qv[j + 1] & 0xff) << 8) | ((qv[j + 2] & 0xff) << 16) |
+                               ((qv[j + 3] & 0xff) << 24);
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; j++) dst[j] = (int8_t)qv[j];
+    }
+    if (threadIdx.x % W == 0) {
+        const int b = threadIdx.x / W;
+        s_row[b] = scale;
+        s8_row[b] = -8 * qs;
+    }
+}
+
 template <int E>
 __global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float* hidden, const float* weight, float eps,
                                                           int8_t* xq, float* xs, int32_t* xsum) {
     constexpr int T = 256, d = T * E;
     __shared__ ChainScratch<T> sc;
-    __shared__ float a_lds[d];
+    __shared__ __align__(16) float a_lds[d];
     const int n = blockIdx.x;
     const float* x = hidden + (size_t)n * d;
-    float a[E];
+    float xv[E], wv[E], a[E];
 #pragma unroll
     for (int j = 0; j < E; j++) {
-        const float v = x[threadIdx.x * E + j];
-        a[j] = v * v;
+        xv[j] = x[threadIdx.x * E + j];
+        wv[j] = weight[threadIdx.x * E + j];
     }
+#pragma unroll
+    for (int j = 0; j < E; j++) a[j] = xv[j] * xv[j];
     const float sum = exact_chain_sum<E, T>(a, sc, a_lds);
     const float scale = 1.0f / __builtin_sqrtf(sum / (float)d + eps);
-    const int lane32 = threadIdx.x & 31;
-    const int half = threadIdx.x >> 5;  // 8 half-waves
-    for (int b = half; b < d / 32; b += T / 32) {
-        const int i = b * 32 + lane32;
-        const float y = x[i] * scale * weight[i];
-        store_q8_block(y, lane32, xq + (size_t)n * d + b * 32, xs + (size_t)n * (d / 32) + b,
-                       xsum + (size_t)n * (d / 32) + b);
+    float y[E];
+#pragma unroll
+    for (int j = 0; j < E; j++) y[j] = xv[j] * scale * wv[j];
+    int8_t* q_row = xq + (size_t)n * d;
+    float* s_row = xs + (size_t)n * (d / 32);
+    int32_t* s8_row = xsum + (size_t)n * (d / 32);
+    if constexpr (32 % E == 0) {
+        quantize_regs_q8<E>(y, q_row, s_row, s8_row);
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; j++) a_lds[threadIdx.x * E + j] = y[j];
+        __syncthreads();
+        quantize_row_lds_q8<T>(a_lds, d, q_row, s_row, s8_row);
     }
 }
 
@@ -155,11 +259,14 @@ int launch_embed(const float* table, const uint32_t* toks, int N, int d, float* 
 // (inference.rs:4252-4257; dot_f32_scalar folds a*b from -0.0 in index order).
 // Workgroup = one KV head x 64 positions: the K tile is staged once in LDS (rows padded
 // to HD+4 floats so the per-lane row reads are bank-conflict free) and shared by the
-// G query-head waves; lane = position p, each lane keeps k_p in VGPRs across rows n.
-template <int HD>
-__global__ __launch_bounds__(1024) void attn_scores_kernel(AttnParams a) {
+// G query-head waves; lane = position p reads its key row from LDS (4 floats a step).
+// RB rows' dot chains are interleaved (each chain is sequential in i, the rows are
+// independent); their q vectors sit in LDS and are read as wave-wide broadcasts.
+template <int HD, int RB>
+__global__ __launch_bounds__(512) void attn_scores_kernel(AttnParams a) {
     constexpr int RS = HD + 4;
     __shared__ float kt[64 * RS];
+    __shared__ __align__(16) float qs[8][RB][HD];  // [head in group][row][dim]
     const int kvh = blockIdx.y;
     const int G = a.H / a.Hkv;
     const int g = wave_id_uniform();
@@ -177,120 +284,180 @@ __global__ __launch_bounds__(1024) void attn_scores_kernel(AttnParams a) {
         }
         __syncthreads();
         const int p = tile * 64 + lane;
-        float k[HD];
-        if (p <= last) {
+        const float* krow = &kt[lane * RS];  // this lane's key row (stale for p > last: unused)
+        // rows whose window reaches this tile: n >= tile*64 - pos0 (uniform over the block)
+        const int n_first = max(0, tile * 64 - pos0);
+        for (int n0 = n_first; n0 < a.N; n0 += RB) {
+            // this wave's head: q rows n0 .. n0+RB-1 into LDS (each wave owns its slice)
 #pragma unroll
-            for (int i = 0; i < HD / 4; i++) {
-                const float4 v = *(const float4*)&kt[lane * RS + i * 4];
-                k[4 * i] = v.x;
-                k[4 * i + 1] = v.y;
-                k[4 * i + 2] = v.z;
-                k[4 * i + 3] = v.w;
+            for (int r = 0; r < RB; r++) {
+                const int n = min(n0 + r, a.N - 1);
+                const float* qrow = a.q + (size_t)n * a.H * HD + (size_t)h * HD;
+                for (int i = lane; i < HD; i += 64) qs[g][r][i] = qrow[i];
             }
-        }
-        for (int n = 0; n < a.N; n++) {
-            if (tile * 64 > pos0 + n) continue;  // uniform: whole tile beyond this row
-            const float __attribute__((address_space(4)))* q =
-                (const float __attribute__((address_space(4)))*)(const void __attribute__((address_space(4)))*)(
-                    uintptr_t)(a.q + (size_t)n * a.H * HD + (size_t)h * HD);
-            float dot = -0.0f;
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            float dot[RB];
 #pragma unroll
-            for (int i = 0; i < HD; i++) dot = dot + q[i] * k[i];
-            if (p <= pos0 + n) a.scores[((size_t)n * a.H + h) * a.max_ctx + p] = dot * a.scale;
+            for (int r = 0; r < RB; r++) dot[r] = -0.0f;
+#pragma unroll 4
+            for (int i = 0; i < HD; i += 4) {
+                const float4 kv = *(const float4*)&krow[i];
+#pragma unroll
+                for (int r = 0; r < RB; r++) {
+                    const float4 qv = *(const float4*)&qs[g][r][i];
+                    dot[r] = dot[r] + qv.x * kv.x;
+                    dot[r] = dot[r] + qv.y * kv.y;
+                    dot[r] = dot[r] + qv.z * kv.z;
+                    dot[r] = dot[r] + qv.w * kv.w;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RB; r++) {
+                const int n = n0 + r;
+                if (n < a.N && p <= pos0 + n) a.scores[((size_t)n * a.H + h) * a.max_ctx + p] = dot[r] * a.scale;
+            }
+            __builtin_amdgcn_wave_barrier();  // readers done before the next group overwrites qs
         }
     }
 }
 
-// Phase 2 (fused): softmax over 0..=pos (inference.rs:3522-3540) and the weighted V sum
-// (add_weighted_f32_scalar, inference.rs:3603-3623) for two (row, head) units per
-// workgroup; half-wave u owns unit u and 32 output dims.  max is order free; e_p =
-// expf(s_p - max) goes to LDS; lane 0 of the half-wave adds e_0, e_1, ... in order;
-// prob_p = e_p * (1/sum); out[d] = ((0 + prob_0*v_0[d]) + prob_1*v_1[d]) + ... in order.
-// The output block of 32 dims is then quantised to Q8_0 for the wo matmul.
-__global__ __launch_bounds__(64) void attn_softmax_pv_kernel(AttnParams a) {
-    extern __shared__ float e[];  // [2][a.max_pos + 1 rounded up to 4]
-    const int kvh = blockIdx.x;
-    const int dchunk = blockIdx.y;
-    const int G = a.H / a.Hkv;
-    const int lane = threadIdx.x & 63;
-    const int u = lane >> 5, lane32 = lane & 31;
-    const int unit = blockIdx.z * 2 + u;  // (n, g) pair
-    const bool active = unit < a.N * G;  // half-wave uniform
-    const int n = active ? unit / G : 0, g = active ? unit % G : 0;
-    const int h = kvh * G + g;
+// Phase 2 (fused), one workgroup of T threads per (row n, head h) unit: softmax over
+// 0..=pos (inference.rs:3522-3540) then the weighted V sum (add_weighted_f32_scalar,
+// inference.rs:3603-3623) and the Q8_0 quantisation of the output for the wo matmul.
+//   max: order free (block reduction); e_p = expf(s_p - max) in parallel;
+//   sum = e_0 + e_1 + ... left to right: exact_chain_sum (bit-identical);
+//   prob_p = e_p * (1/sum);  out[d] = ((0 + prob_0*v_0[d]) + prob_1*v_1[d]) + ... in order,
+//   one lane per output dim d, V rows streamed with a software-pipelined prefetch.
+// Thread t owns positions [t*E, t*E + E) of the score row (zeros past the row's end).
+template <int E, int T>
+__global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
+    __shared__ ChainScratch<T> sc;
+    __shared__ __align__(16) float probs[T * E];
+    __shared__ float red[T / 64];
+    const int unit = blockIdx.x;
+    const int n = unit / a.H, h = unit % a.H;
+    const int kvh = h / (a.H / a.Hkv);
     const int L = a.d_pos[0] + n + 1;
-    const int stride = ((a.max_pos + 1) + 3) & ~3;
-    float* eu = e + u * stride;
-    const float* s = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
-    float mx = -__builtin_inff();
-    if (active)
-        for (int p = lane32; p < L; p += 32) {
-            const float v = s[p];
-            mx = v > mx ? v : mx;
-        }
+    const int t = threadIdx.x;
+    const float* srow = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
+    float sv[E];
 #pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) {
+    for (int j = 0; j < E; j++) {
+        const int p = t * E + j;
+        sv[j] = p < L ? srow[p] : -__builtin_inff();
+    }
+    float mx = sv[0];
+#pragma unroll
+    for (int j = 1; j < E; j++) mx = sv[j] > mx ? sv[j] : mx;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
         const float o = __shfl_xor(mx, off, 64);
         mx = o > mx ? o : mx;
     }
-    if (active)
-        for (int p = lane32; p < L; p += 32) eu[p] = expf_glibc(s[p] - mx);
+    if ((t & 63) == 0) red[t >> 6] = mx;
     __syncthreads();
-    float inv = 0.0f;
-    if (active && lane32 == 0) {
-        float sum = 0.0f;
-        int p = 0;
-        for (; p + 32 <= L; p += 32) {
-            float4 v[8];
+    mx = red[0];
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = *(const float4*)&eu[p + 4 * j];
+    for (int w = 1; w < T / 64; w++) mx = red[w] > mx ? red[w] : mx;
+    float e[E];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                sum = sum + v[j].x;
-                sum = sum + v[j].y;
-                sum = sum + v[j].z;
-                sum = sum + v[j].w;
-            }
+    for (int j = 0; j < E; j++) e[j] = t * E + j < L ? expf_glibc(sv[j] - mx) : 0.0f;
+    const float sum = exact_chain_sum<E, T>(e, sc, probs);
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int j = 0; j < E; j++) probs[t * E + j] = e[j] * inv;
+    __syncthreads();
+    if (t >= a.hd) return;  // no barriers below
+    const int HDv = a.hd;
+    const float* v = a.vcache + (size_t)kvh * a.max_ctx * HDv + t;
+    // V rows stream from HBM: a ring of D batches of B positions keeps (D-1)*B rows in
+    // flight ahead of the add chain (registers are plentiful at one wave per SIMD).
+    constexpr int B = 32, D = T >= 512 ? 2 : 4;
+    float ring[D][B];
+    const int nb = L / B;
+#pragma unroll
+    for (int k = 0; k < D - 1; k++)
+        if (k < nb) {
+#pragma unroll
+            for (int j = 0; j < B; j++) ring[k][j] = v[(size_t)(k * B + j) * HDv];
         }
-        for (; p < L; p++) sum = sum + eu[p];
-        inv = 1.0f / sum;
-    }
-    inv = __shfl(inv, u * 32, 64);
-    if (!active) return;  // no barriers below
-    const int d = dchunk * 32 + lane32;
-    const float* v = a.vcache + (size_t)kvh * a.max_ctx * a.hd + d;
     float acc = 0.0f;
-    int p = 0;
-    for (; p + 16 <= L; p += 16) {
-        float vv[16], pr[16];
+    int b = 0;
+    for (; b + D <= nb; b += D) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) vv[j] = v[(size_t)(p + j) * a.hd];
+        for (int k = 0; k < D; k++) {
+            const int nxt = b + k + D - 1;  // batch loaded into slot (k + D - 1) % D
+            if (nxt < nb) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) pr[j] = eu[p + j] * inv;
+                for (int j = 0; j < B; j++) ring[(k + D - 1) % D][j] = v[(size_t)(nxt * B + j) * HDv];
+            }
 #pragma unroll
-        for (int j = 0; j < 16; j++) acc = acc + pr[j] * vv[j];
+            for (int j = 0; j < B; j++) acc = acc + probs[(b + k) * B + j] * ring[k][j];
+        }
     }
-    for (; p < L; p++) acc = acc + (eu[p] * inv) * v[(size_t)p * a.hd];
-    const int aw = a.H * a.hd;
-    const int col = h * a.hd + dchunk * 32;
-    store_q8_block(acc, lane32, a.xq + (size_t)n * aw + col, a.xs + (size_t)n * (aw / 32) + col / 32,
+#pragma unroll
+    for (int k = 0; k < D; k++) {  // remaining whole batches (fewer than D), already in flight
+        if (b + k < nb) {
+#pragma unroll
+            for (int j = 0; j < B; j++) acc = acc + probs[(b + k) * B + j] * ring[k][j];
+        }
+    }
+    for (int p = nb * B; p < L; p++) acc = acc + probs[p] * v[(size_t)p * HDv];
+    const int aw = a.H * HDv;
+    const int col = h * HDv + (t & ~31);
+    store_q8_block(acc, t & 31, a.xq + (size_t)n * aw + col, a.xs + (size_t)n * (aw / 32) + col / 32,
                    a.xs8 + (size_t)n * (aw / 32) + col / 32);
 }
 
 int launch_attention(const AttnParams& a, hipStream_t st) {
     const int G = a.H / a.Hkv;
-    if (G > 16 || a.H % a.Hkv) return fail(NC_EINVAL, "attention: at most 16 query heads per KV head supported");
+    if (G > 8 || a.H % a.Hkv) return fail(NC_EINVAL, "attention: at most 8 query heads per KV head supported");
     const int tiles = (a.max_pos + 64) / 64;
-    if (a.hd == 128)
-        hipLaunchKernelGGL(attn_scores_kernel<128>, dim3(tiles, a.Hkv), dim3(64 * G), 0, st, a);
-    else if (a.hd == 64)
-        hipLaunchKernelGGL(attn_scores_kernel<64>, dim3(tiles, a.Hkv), dim3(64 * G), 0, st, a);
-    else
-        return fail(NC_EINVAL, "attention: head_dim must be 64 or 128");
+    if (a.hd != 64 && a.hd != 128) return fail(NC_EINVAL, "attention: head_dim must be 64 or 128");
+    const int rb = a.N >= 8 ? 8 : a.N;  // rows interleaved per pass of the scores kernel
+#define NC_SCORES(HD, RB)                                                                       \
+    hipLaunchKernelGGL((attn_scores_kernel<HD, RB>), dim3(tiles, a.Hkv), dim3(64 * G), 0, st, a); \
+    break;
+#define NC_SCORES_HD(HD)            \
+    switch (rb) {                   \
+        case 1: NC_SCORES(HD, 1)    \
+        case 2: NC_SCORES(HD, 2)    \
+        case 3: NC_SCORES(HD, 3)    \
+        case 4: NC_SCORES(HD, 4)    \
+        case 5: NC_SCORES(HD, 5)    \
+        case 6: NC_SCORES(HD, 6)    \
+        case 7: NC_SCORES(HD, 7)    \
+        default: NC_SCORES(HD, 8)   \
+    }
+    if (a.hd == 128) {
+        NC_SCORES_HD(128)
+    } else {
+        NC_SCORES_HD(64)
+    }
+#undef NC_SCORES_HD
+#undef NC_SCORES
     NC_HIP(hipGetLastError());
-    const size_t lds = 2 * (size_t)(((a.max_pos + 1) + 3) & ~3) * sizeof(float);
-    if (lds > 160 * 1024) return fail(NC_ERANGE, "attention: context too long for the fused softmax kernel");
-    hipLaunchKernelGGL(attn_softmax_pv_kernel, dim3(a.Hkv, a.hd / 32, (a.N * G + 1) / 2), dim3(64), lds, st, a);
+    // max_pos + 1 is the longest score row of the pass
+    const int len = a.max_pos + 1;
+    const dim3 grid(a.N * a.H);
+    if (len <= 256)
+        hipLaunchKernelGGL((attn_softmax_pv_kernel<1, 256>), grid, dim3(256), 0, st, a);
+    else if (len <= 512)
+        hipLaunchKernelGGL((attn_softmax_pv_kernel<2, 256>), grid, dim3(256), 0, st, a);
+    else if (len <= 1024)
+        hipLaunchKernelGGL((attn_softmax_pv_kernel<4, 256>), grid, dim3(256), 0, st, a);
+    else if (len <= 2048)
+        hipLaunchKernelGGL((attn_softmax_pv_kernel<8, 256>), grid, dim3(256), 0, st, a);
+    else if (len <= 4096)
+        hipLaunchKernelGGL((attn_softmax_pv_kernel<16, 256>), grid, dim3(256), 0, st, a);
+    else if (len <= 8192)
+        hipLaunchKernelGGL((attn_softmax_pv_kernel<32, 256>), grid, dim3(256), 0, st, a);
+    else if (len <= 16384)
+        hipLaunchKernelGGL((attn_softmax_pv_kernel<32, 512>), grid, dim3(512), 0, st, a);
+    else
+        return fail(NC_ERANGE, "attention: context longer than 16384 positions");
     NC_HIP(hipGetLastError());
     return NC_OK;
 }

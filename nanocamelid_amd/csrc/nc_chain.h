@@ -9,31 +9,31 @@
 // when evaluated literally.  This routine returns the bit-identical s_{n-1} from a
 // workgroup of T threads in a few parallel passes:
 //
-//  1. Guess.  P_i = sum_{j<=i} a_j in double (a block scan) and G_{i-1} = fl32(P_{i-1})
+//  1. Guess.  P_i = sum_{j<=i} a_j in double (a block scan) and g_i = fl32(P_{i-1})
 //     approximates the chain value before step i (it differs from s_{i-1} only by the
 //     chain's accumulated rounding, a few ulps).
-//  2. Increments.  If s_{i-1} and G_{i-1} lie in the same binade, the step neither
-//     crosses into the next binade nor rounds a tie, then
-//         fl32(s_{i-1} + a_i) - s_{i-1} = fl32(G_{i-1} + a_i) - G_{i-1} =: d_i,
+//  2. Increments.  If s_{i-1} lies within 256 ulps of g_i, in the same binade, and the
+//     step neither reaches the next binade nor rounds an exact tie, then
+//         fl32(s_{i-1} + a_i) - s_{i-1} = fl32(g_i + a_i) - g_i =: d_i,
 //     because both states are multiples of the binade's ulp.  Steps where that can fail
-//     (a binade boundary within a margin of 256 ulps of G, or a tie) are flagged
-//     "sensitive"; there are ~20 of them in 4096 terms (most binade crossings happen
-//     in the first few dozen terms, where the sum grows fastest).
-//  3. c_i = sum_{j<=i} d_j (block scan in double; exact, since partial sums are
-//     differences of f32 values).
+//     are flagged "sensitive" by integer tests on the f32 bits; there are ~20 of them in
+//     4096 terms of smooth data (binade crossings cluster in the first few dozen terms,
+//     where the sum grows fastest).
+//  3. c_i = sum_{j<=i} d_j (block scan in double).
 //  4. Sensitive walk.  One wave visits the sensitive steps in order and computes their
-//     true result from the corrected chain value before them, keeping the running
-//     correction shift_k = s_k - c_k.  Every other step inherits the shift of the last
-//     sensitive step before it.
-//  5. Verify.  Every step is checked locally, in parallel: the corrected value must be an
-//     f32 and equal fl32(previous corrected value + a_i).  If every step holds, the
-//     corrected sequence IS the sequential chain (induction from s_{-1} = 0), whatever
-//     the guesses were.  If any step fails (never seen on test data; it needs the chain
-//     to drift > 256 ulps from the exact prefix), thread 0 recomputes the chain
-//     sequentially.
+//     true result from the corrected chain value before them (carried in f32, two
+//     dependent adds per step), giving the correction shift_k = s_k - c_k.  Every other
+//     step inherits the shift of the last sensitive step before it.
+//  5. Verify.  With cn_i = fl32(c_i + shift), every step is checked locally and in
+//     parallel: cn_i == fl32(cn_{i-1} + a_i), cn_{-1} = 0.  If all hold, cn IS the
+//     sequential chain (induction), whatever the guesses were.  If any fails (it needs the
+//     chain to drift > 256 ulps from the exact prefix, or more than kChainMaxSensitive
+//     sensitive steps), thread 0 recomputes the chain sequentially.
 //
 // The result is therefore always bit-identical to the sequential loop; the guesses only
 // decide how fast it is found.  Terms must be >= 0 (sums of squares, exponentials).
+//
+// Wave-level scans use gfx9 DPP (row_shr, row_bcast, wave_shr): no LDS round trips.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -49,7 +49,6 @@ struct ChainEntry {
     double cold;   // c_k (uncorrected)
     double shift;  // s_k - c_k after the walk
     float a;       // a_k
-    int idx;       // k
 };
 
 template <int T>
@@ -61,17 +60,48 @@ struct ChainScratch {
     float result;
 };
 
-// Binade class of a non-negative value at f32 resolution: the unbiased binary exponent,
-// with zero and the f32 subnormal range (one ulp, 2^-149) collapsed into one class.
-__device__ __forceinline__ int chain_binade(double v) {
-    if (!(v >= 1.1754943508222875e-38)) return -127;
-    return (int)((__double_as_longlong(v) >> 52) & 0x7ff) - 1023;
+// ---------------------------------------------------------------- DPP helpers (wave64)
+enum : int {
+    kDppRowShr1 = 0x111,
+    kDppRowShr2 = 0x112,
+    kDppRowShr4 = 0x114,
+    kDppRowShr8 = 0x118,
+    kDppWaveShr1 = 0x138,
+    kDppRowBcast15 = 0x142,
+    kDppRowBcast31 = 0x143,
+};
+
+// Lanes whose DPP source is invalid or whose row is masked off read 0.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ int dpp0_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xf, false);
+}
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ double dpp0_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(b & 0xffffffff), CTRL, ROWS, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, ROWS, 0xf, false);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
-// ulp of a non-negative f32 value (2^-149 in the subnormal range).
-__device__ __forceinline__ double chain_ulp(float x) {
-    const int e = (int)((__float_as_uint(x) >> 23) & 0xff);
-    return __longlong_as_double((long long)(e > 0 ? e - 23 + 1023 - 127 : 1023 - 149) << 52);
+// Inclusive scans over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan_i32(int v) {
+    v += dpp0_i<kDppRowShr1>(v);
+    v += dpp0_i<kDppRowShr2>(v);
+    v += dpp0_i<kDppRowShr4>(v);
+    v += dpp0_i<kDppRowShr8>(v);
+    v += dpp0_i<kDppRowBcast15, 0xa>(v);
+    v += dpp0_i<kDppRowBcast31, 0xc>(v);
+    return v;
+}
+__device__ __forceinline__ double wave_incl_scan_f64(double v) {
+    v += dpp0_d<kDppRowShr1>(v);
+    v += dpp0_d<kDppRowShr2>(v);
+    v += dpp0_d<kDppRowShr4>(v);
+    v += dpp0_d<kDppRowShr8>(v);
+    v += dpp0_d<kDppRowBcast15, 0xa>(v);
+    v += dpp0_d<kDppRowBcast31, 0xc>(v);
+    return v;
 }
 
 __device__ __forceinline__ double chain_readlane(double v, int lane) {
@@ -81,52 +111,73 @@ __device__ __forceinline__ double chain_readlane(double v, int lane) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
+// Block-wide exclusive scan of a double (and optionally of an int in the same pass).
 template <int T>
-__device__ __forceinline__ double chain_excl_scan_f64(double v, double* tot, double* total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    double incl = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const double o = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += o;
-    }
-    double excl = __shfl_up(incl, 1, 64);
-    if (lane == 0) excl = 0.0;
-    if (lane == 63) tot[w] = incl;
+__device__ __forceinline__ double block_excl_scan_f64(double v, double* tot) {
+    const int w = threadIdx.x >> 6;
+    const double incl = wave_incl_scan_f64(v);
+    const double excl = dpp0_d<kDppWaveShr1>(incl);
+    if ((threadIdx.x & 63) == 63) tot[w] = incl;
     __syncthreads();
-    double base = 0.0, all = 0.0;
+    double base = 0.0;
+#pragma unroll
+    for (int i = 0; i < T / 64; i++)
+        if (i < w) base += tot[i];
+    __syncthreads();
+    return base + excl;
+}
+template <int T>
+__device__ __forceinline__ double block_excl_scan_f64_i32(double v, int k, double* tot, int* itot, int* kexcl,
+                                                           int* ktotal) {
+    const int w = threadIdx.x >> 6;
+    const double incl = wave_incl_scan_f64(v);
+    const double excl = dpp0_d<kDppWaveShr1>(incl);
+    const int kincl = wave_incl_scan_i32(k);
+    if ((threadIdx.x & 63) == 63) {
+        tot[w] = incl;
+        itot[w] = kincl;
+    }
+    __syncthreads();
+    double base = 0.0;
+    int kbase = 0, kall = 0;
 #pragma unroll
     for (int i = 0; i < T / 64; i++) {
-        const double t = tot[i];
-        if (i < w) base += t;
-        all += t;
+        const int ki = itot[i];
+        if (i < w) {
+            base += tot[i];
+            kbase += ki;
+        }
+        kall += ki;
     }
     __syncthreads();
-    *total = all;
+    *kexcl = kbase + kincl - k;
+    *ktotal = kall;
     return base + excl;
 }
 
-template <int T>
-__device__ __forceinline__ int chain_excl_scan_i32(int v, int* tot, int* total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int incl = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int o = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += o;
-    }
-    if (lane == 63) tot[w] = incl;
-    __syncthreads();
-    int base = 0, all = 0;
-#pragma unroll
-    for (int i = 0; i < T / 64; i++) {
-        const int t = tot[i];
-        if (i < w) base += t;
-        all += t;
-    }
-    __syncthreads();
-    *total = all;
-    return base + incl - v;
+// Step i with guess g (the chain value before the step, approximately) and term a >= 0:
+// returns d = fl32(g + a) - g exactly and whether the step is sensitive (see above).
+// Branch free (selects only): every lane evaluates every test.
+__device__ __forceinline__ double chain_increment(float g, float a, bool* sensitive) {
+    const float r = g + a;
+    const double d = (double)r - (double)g;
+    const uint32_t bg = __float_as_uint(g), ba = __float_as_uint(a);
+    const int eg = (int)(bg >> 23), ea = (int)(ba >> 23);
+    const int mg = (int)(bg & 0x7fffff);
+    const int sh = eg - (ea > 0 ? ea : 1);  // a's binary exponent below g's
+    const uint32_t ma = (ba & 0x7fffffu) | (ea > 0 ? 0x800000u : 0u);
+    const int shc = sh < 1 ? 1 : (sh > 31 ? 31 : sh);
+    const uint32_t low = ma & ((1u << shc) - 1u);
+    // exact tie of g + a at g's ulp (only possible for 2 <= sh <= 24)
+    const bool tie = (sh >= 2) & (sh <= 24) & (low == (1u << (shc - 1)));
+    const int a_ulps = sh > 24 ? 1 : (int)(ma >> shc) + 1;  // >= a / ulp(g)
+    // sh < 2: a comparable to the running sum, the binade may change; eg == 0: subnormal
+    // running sum; the margin tests: s may sit in the binade below, or s + a may reach the
+    // next binade.
+    const bool s = (sh < 2) | tie | (mg + a_ulps + 256 >= (1 << 23)) | (mg < 256) | (eg == 0);
+    // g == 0: every earlier term is 0, the chain is exactly 0 and d = a.  a == 0: d = 0.
+    *sensitive = s & (bg != 0) & (ba != 0);
+    return d;
 }
 
 // Thread t holds terms a[0..E) = a_{tE} .. a_{tE+E-1} (n = T*E terms; pad with zeros, which
@@ -139,7 +190,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
 #pragma unroll
     for (int j = 0; j < E; j++) a_lds[t * E + j] = a[j];
 
-    // 1. guesses from the exact-ish double prefix
+    // 1. guesses from the double prefix
     double w[E];
     double run = 0.0;
 #pragma unroll
@@ -147,46 +198,33 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
         run += (double)a[j];
         w[j] = run;
     }
-    double totp;
-    const double exclp = chain_excl_scan_f64<T>(run, sc.dtot, &totp);
+    const double exclp = block_excl_scan_f64<T>(run, sc.dtot);
 
     // 2. speculative increments and sensitivity (w[] becomes d[])
     uint32_t sens = 0;
-    double prevp = exclp;
+    float g = (float)exclp;
 #pragma unroll
     for (int j = 0; j < E; j++) {
-        const double pj = exclp + w[j];
-        const float g = (float)prevp;
-        const float r = g + a[j];
-        const double dj = (double)r - (double)g;
-        bool s = false;
-        if (g != 0.0f) {  // g == 0 means every earlier term is 0, so the chain is exactly 0
-            const double rem = ((double)g + (double)a[j]) - (double)r;
-            s = __builtin_fabs(rem) == 0.5 * chain_ulp(r);
-            const double m = 256.0 * chain_ulp(g);
-            const double lo = (double)g - m, hi = (double)g + m + (double)a[j];
-            s = s || chain_binade(lo) != chain_binade(hi);
-        }
+        const float gnext = (float)(exclp + w[j]);
+        bool s;
+        w[j] = chain_increment(g, a[j], &s);
         if (s) sens |= 1u << j;
-        w[j] = dj;
-        prevp = pj;
+        g = gnext;
     }
 
-    // 3. uncorrected chain c = prefix of d
+    // 3. uncorrected chain c = prefix of d, with the sensitive count scanned in the same pass
     run = 0.0;
 #pragma unroll
     for (int j = 0; j < E; j++) {
         run += w[j];
         w[j] = run;
     }
-    double totc;
-    const double exclc = chain_excl_scan_f64<T>(run, sc.dtot, &totc);
+    int off, total_s;
+    const double exclc = block_excl_scan_f64_i32<T>(run, __popc(sens), sc.dtot, sc.itot, &off, &total_s);
 
     // 4. sensitive list in ascending order, then the walk
-    int total_s;
-    const int off = chain_excl_scan_i32<T>(__popc(sens), sc.itot, &total_s);
     const bool listed = total_s <= kChainMaxSensitive;
-    if (listed) {
+    if (listed && sens) {
         int e = off;
 #pragma unroll
         for (int j = 0; j < E; j++) {
@@ -195,36 +233,43 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
                 ce.cprev = j == 0 ? exclc : exclc + w[j - 1];
                 ce.cold = exclc + w[j];
                 ce.a = a[j];
-                ce.idx = t * E + j;
             }
         }
     }
     __syncthreads();
     if (listed && t < 64) {
-        double acc = 0.0;
+        // s_{k-1} = s_j + (c_{k-1} - c_j) with j the previous sensitive step (the advance is
+        // exact: nothing between j and k changes binade or ties), then s_k = fl32(s_{k-1} + a_k).
+        float s_run = 0.0f;    // s_j (s_{-1} = 0 = c_{-1} before the first entry)
+        double co_last = 0.0;  // c_j
         for (int e0 = 0; e0 < total_s; e0 += 64) {
             const int me = e0 + t;
             double cp = 0.0, co = 0.0;
             float av = 0.0f;
-            int ix = 0;
             if (me < total_s) {
                 cp = sc.ent[me].cprev;
                 co = sc.ent[me].cold;
                 av = sc.ent[me].a;
-                ix = sc.ent[me].idx;
             }
-            double mine = 0.0;
+            double co_prev = dpp0_d<kDppWaveShr1>(co);
+            if (t == 0) co_prev = co_last;
+            const float adv = (float)(cp - co_prev);
+            float mine = 0.0f;
             const int cnt = min(64, total_s - e0);
-            for (int q = 0; q < cnt; q++) {  // q is wave-uniform: v_readlane, no LDS
-                const double cpq = chain_readlane(cp, q), coq = chain_readlane(co, q);
-                const float aq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(av), q));
-                const int iq = __builtin_amdgcn_readlane(ix, q);
-                const double prev = iq == 0 ? 0.0 : cpq + acc;
-                const float tr = (float)prev + aq;
-                acc = (double)tr - coq;
-                if (t == q) mine = acc;
+            for (int q0 = 0; q0 < cnt; q0 += 8) {  // q is wave-uniform: v_readlane, no LDS
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int q = q0 + u;
+                    if (q < cnt) {
+                        const float advq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(adv), q));
+                        const float aq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(av), q));
+                        s_run = (s_run + advq) + aq;
+                        mine = t == q ? s_run : mine;
+                    }
+                }
             }
-            if (me < total_s) sc.ent[me].shift = mine;
+            if (me < total_s) sc.ent[me].shift = (double)mine - co;
+            co_last = chain_readlane(co, cnt - 1);
         }
     }
     __syncthreads();
@@ -238,9 +283,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
 #pragma unroll
         for (int j = 0; j < E; j++) {
             if (sens >> j & 1) cur = sc.ent[e++].shift;
-            const double v = exclc + w[j] + cur;
-            cn[j] = (float)v;
-            bad = bad || (double)cn[j] != v;
+            cn[j] = (float)(exclc + w[j] + cur);
         }
         sc.last[t] = cn[E - 1];
     }
@@ -249,7 +292,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
         float prev = t == 0 ? 0.0f : sc.last[t - 1];
 #pragma unroll
         for (int j = 0; j < E; j++) {
-            bad = bad || (prev + a[j]) != cn[j];
+            bad |= (prev + a[j]) != cn[j];
             prev = cn[j];
         }
     }
