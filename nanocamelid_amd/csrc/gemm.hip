@@ -188,14 +188,17 @@ __device__ __forceinline__ float term_q40(const int* xp, const int* meta, const 
     return (xs * ws) * (float)d;  // IEEE multiplication is commutative: == (ws * xs) * d
 }
 
-template <int NMAX, int S>
+// R64: a ring of D rounds of weights, scales and activations is kept in flight per wave;
+// tokens n >= N are skipped (wave-uniform branch).  With S > 1 the terms go to a double-
+// buffered LDS array, one barrier per round, and the chain threads add them in block order.
+template <int NMAX, int S, int D>
 __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
     constexpr int U = 4;                       // blocks per wave per round
     constexpr int RB = S * U;                  // blocks per round
     constexpr int TPW = (NMAX + S - 1) / S;    // chain tokens per thread
     constexpr int NP = (NMAX + 1) / 2;         // token-pair activation dwords per block
     constexpr int NM = (NMAX + 7) / 8;         // meta dwords per block
-    extern __shared__ float lds[];             // [RB][NMAX][64] terms when S > 1
+    extern __shared__ float lds[];             // [2][RB][NMAX][64] terms when S > 1
     const int tile = blockIdx.x;
     const int wave = wave_id_uniform();
     const int lane = threadIdx.x & 63;
@@ -205,96 +208,261 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
     const uint8_t* wt = p.w + (size_t)tile * p.groups * kQ40ChunkBytes;
     float acc[TPW];
 #pragma unroll
-    for (int j = 0; j < TPW; j++) acc[j] = 0.0f;
+    for (int t = 0; t < TPW; t++) acc[t] = 0.0f;
     // per-lane activation addresses: pair q -> token 2q + (j16 >> 3), dword j16 & 7;
     // meta: lanes 0..7 read x_scale, lanes 8..15 read -8*sum(x) of token 8q + (j16 & 7)
     const int* xbase = (const int*)p.x + (j16 & 7);
     const int xtok = j16 >> 3;
     const int mtok = j16 & 7;
     const int* mbase = j16 >= 8 ? p.xs8 : (const int*)p.xs;
-
     const int nrounds = (nb + RB - 1) / RB;
-    uint4 cw[U], nw[U];
-    uint2 cs, ns;
-    int cx[U][NP], nx[U][NP], cm[U][NM], nm[U][NM];
-    auto load_round = [&](int r, uint4* wbuf, uint2& sbuf, int (*xbuf)[NP], int (*mbuf)[NM]) {
-        const int b0 = r * RB + wave * U;
-        if (b0 < nb) {
-            const uint8_t* chunk = wt + (size_t)(b0 >> 3) * kQ40ChunkBytes;
-            const int u0 = b0 & 7;
+
+    uint4 rw[D][U];
+    uint2 rs[D];
+    int rx[D][U][NP], rm[D][U][NM];
+#define NC_R64_LOAD(R, SLOT)                                                                        \
+    do {                                                                                            \
+        const int b0_ = (R) * RB + wave * U;                                                        \
+        if ((R) < nrounds && b0_ < nb) {                                                            \
+            const uint8_t* chunk_ = wt + (size_t)(b0_ >> 3) * kQ40ChunkBytes;                       \
+            const int u0_ = b0_ & 7;                                                                \
+            _Pragma("unroll") for (int u = 0; u < U; u++) rw[SLOT][u] =                             \
+                *(const uint4*)(chunk_ + (u0_ + u) * 1024 + lane * 16);                             \
+            rs[SLOT] = *(const uint2*)(chunk_ + 8192 + lane * 16 + u0_ * 2);                        \
+            _Pragma("unroll") for (int u = 0; u < U; u++) {                                         \
+                const int b_ = min(b0_ + u, nb - 1);                                                \
+                _Pragma("unroll") for (int q = 0; q < NP; q++) {                                    \
+                    const int t_ = min(2 * q + xtok, N - 1);                                        \
+                    rx[SLOT][u][q] = xbase[((size_t)t_ * p.K + (size_t)b_ * 32) / 4];               \
+                }                                                                                   \
+                _Pragma("unroll") for (int q = 0; q < NM; q++) {                                    \
+                    const int t_ = min(8 * q + mtok, N - 1);                                        \
+                    rm[SLOT][u][q] = mbase[(size_t)t_ * nb + b_];                                   \
+                }                                                                                   \
+            }                                                                                       \
+        }                                                                                           \
+    } while (0)
+
 #pragma unroll
-            for (int u = 0; u < U; u++) wbuf[u] = *(const uint4*)(chunk + (u0 + u) * 1024 + lane * 16);
-            sbuf = *(const uint2*)(chunk + 8192 + lane * 16 + u0 * 2);
+    for (int k = 0; k < D - 1; k++) NC_R64_LOAD(k, k);
+    for (int r0 = 0; r0 < nrounds; r0 += D) {
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int b = min(b0 + u, nb - 1);
+        for (int k = 0; k < D; k++) {
+            const int r = r0 + k;
+            if (r < nrounds) {  // uniform
+                NC_R64_LOAD(r + D - 1, (k + D - 1) % D);
+                float* buf = lds + (size_t)(r & 1) * RB * NMAX * 64;
+                const int b0 = r * RB + wave * U;
 #pragma unroll
-                for (int q = 0; q < NP; q++) {
-                    const int t = min(2 * q + xtok, N - 1);
-                    xbuf[u][q] = xbase[((size_t)t * p.K + (size_t)b * 32) / 4];
+                for (int u = 0; u < U; u++) {
+                    if (b0 + u < nb) {  // uniform
+                        const uint4 v = rw[k][u];
+                        const int lo[4] = {(int)(v.x & 0x0F0F0F0Fu), (int)(v.y & 0x0F0F0F0Fu),
+                                           (int)(v.z & 0x0F0F0F0Fu), (int)(v.w & 0x0F0F0F0Fu)};
+                        const int hi[4] = {(int)((v.x >> 4) & 0x0F0F0F0Fu), (int)((v.y >> 4) & 0x0F0F0F0Fu),
+                                           (int)((v.z >> 4) & 0x0F0F0F0Fu), (int)((v.w >> 4) & 0x0F0F0F0Fu)};
+                        const uint32_t sw = u < 2 ? rs[k].x : rs[k].y;
+                        const float ws = f16_to_f32((uint16_t)((u & 1) ? (sw >> 16) : (sw & 0xffff)));
+                        [&]<int... I>(std::integer_sequence<int, I...>) {
+                            ((I < N ? (void)([&] {
+                                 const float t = term_q40<I>(rx[k][u], rm[k][u], lo, hi, ws);
+                                 if constexpr (S == 1) acc[I] = acc[I] + t;
+                                 else buf[((wave * U + u) * NMAX + I) * 64 + lane] = t;
+                             }())
+                                    : (void)0),
+                             ...);
+                        }(std::make_integer_sequence<int, NMAX>{});
+                    }
                 }
+                if constexpr (S > 1) {
+                    __syncthreads();
+                    const int nblk = min(RB, nb - r * RB);
 #pragma unroll
-                for (int q = 0; q < NM; q++) {
-                    const int t = min(8 * q + mtok, N - 1);
-                    mbuf[u][q] = mbase[(size_t)t * nb + b];
-                }
-            }
-        }
-    };
-    load_round(0, cw, cs, cx, cm);
-    for (int r = 0; r < nrounds; r++) {
-        if (r + 1 < nrounds) load_round(r + 1, nw, ns, nx, nm);
-        const int b0 = r * RB + wave * U;
-        if (b0 < nb) {  // wave-uniform
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                if (b0 + u < nb) {
-                    const uint4 v = cw[u];
-                    const int lo[4] = {(int)(v.x & 0x0F0F0F0Fu), (int)(v.y & 0x0F0F0F0Fu), (int)(v.z & 0x0F0F0F0Fu),
-                                       (int)(v.w & 0x0F0F0F0Fu)};
-                    const int hi[4] = {(int)((v.x >> 4) & 0x0F0F0F0Fu), (int)((v.y >> 4) & 0x0F0F0F0Fu),
-                                       (int)((v.z >> 4) & 0x0F0F0F0Fu), (int)((v.w >> 4) & 0x0F0F0F0Fu)};
-                    const uint32_t sw = u < 2 ? cs.x : cs.y;
-                    const float ws = f16_to_f32((uint16_t)((u & 1) ? (sw >> 16) : (sw & 0xffff)));
-                    float t[NMAX];
-                    [&]<int... I>(std::integer_sequence<int, I...>) {
-                        ((t[I] = I < NMAX ? term_q40<I>(cx[u], cm[u], lo, hi, ws) : 0.0f), ...);
-                    }(std::make_integer_sequence<int, NMAX>{});
-#pragma unroll
-                    for (int n = 0; n < NMAX; n++) {
+                    for (int t = 0; t < TPW; t++) {
+                        const int n = wave + t * S;
                         if (n < N) {
-                            if constexpr (S == 1) acc[n] = acc[n] + t[n];
-                            else lds[((wave * U + u) * NMAX + n) * 64 + lane] = t[n];
+                            float a = acc[t];
+                            for (int bl = 0; bl < nblk; bl++) a = a + buf[(bl * NMAX + n) * 64 + lane];
+                            acc[t] = a;
                         }
                     }
                 }
             }
         }
-        if constexpr (S > 1) {
-            __syncthreads();
-            const int nblk = min(RB, nb - r * RB);
-#pragma unroll
-            for (int j = 0; j < TPW; j++) {
-                const int n = wave + j * S;
-                if (n < N) {
-                    float a = acc[j];
-                    for (int bl = 0; bl < nblk; bl++) a = a + lds[(bl * NMAX + n) * 64 + lane];
-                    acc[j] = a;
+    }
+#undef NC_R64_LOAD
+    gemm_epilogue<NMAX, S>(p, acc, tile, wave, lane);
+}
+
+// ---------------------------------------------------------------- Q4_0, 16-row tiles (R16)
+// Workgroup = one 16-row tile, S waves.  A wave instruction covers one quad of blocks:
+// lane = 16*j + r holds block 4*qd + j of row r, so each DPP row of 16 lanes is one block
+// and its activation dwords / meta are broadcast inside the row exactly as above.  Rounds
+// of S*U quads: wave w takes quads w*U .. w*U+U-1 of the round; a ring of D rounds of
+// weights, scales and activations is kept in flight per wave.  Terms go to a double-
+// buffered LDS array [round block][token][row]; after the round's barrier the chain
+// threads (thread c: token c/16, row c%16) add them in block order.
+template <int NMAX>
+__device__ __forceinline__ void gemm_epilogue_r16(const GemmParams& p, float v, int n, int tile, int r) {
+    const int row = tile * kTileRowsR16 + r;
+    switch (p.epi) {
+        case EPI_STORE:
+            if (row < p.M) p.out[(size_t)n * p.ld_out + row] = v;
+            break;
+        case EPI_RESIDUAL:
+            if (row < p.M) {
+                float* o = p.out + (size_t)n * p.ld_out + row;
+                *o = v + *o;
+            }
+            break;
+        case EPI_QKV_ROPE: {
+            // inference.rs:3894-3924 (see gemm_epilogue): pair rows 2i, 2i+1 are lanes r, r^1
+            const int pos = p.d_pos[0] + n;
+            const int base = tile * kTileRowsR16;
+            const bool is_q = base < p.aw;
+            const bool is_k = !is_q && base < p.aw + p.kw;
+            const int rr = is_q ? row : (is_k ? row - p.aw : row - p.aw - p.kw);
+            const float partner = __shfl_xor(v, 1, 64);
+            if (is_q || is_k) {
+                const int i = (rr % p.hd) >> 1;
+                if (i < p.rope_half) {
+                    const float* sc = p.rope_tab + ((size_t)pos * p.rope_half + i) * 2;
+                    const float sn = sc[0], cs = sc[1];
+                    const float x0 = (r & 1) ? partner : v;
+                    const float x1 = (r & 1) ? v : partner;
+                    v = (r & 1) ? (x0 * sn + x1 * cs) : (x0 * cs - x1 * sn);
                 }
             }
-            __syncthreads();
+            if (is_q) {
+                p.q_out[(size_t)n * p.aw + rr] = v;
+            } else {
+                const int kvh = rr / p.hd, d = rr % p.hd;
+                float* cache = is_k ? p.kcache : p.vcache;
+                cache[((size_t)kvh * p.max_ctx + pos) * p.hd + d] = v;
+            }
+            break;
         }
+        case EPI_HEAD: {
+            // logits row + first-max argmax partial of this 16-row tile (inference.rs:4836-4846)
+            if (row < p.M) p.out[(size_t)n * p.ld_out + row] = v;
+            float bv = row < p.M ? v : -__builtin_inff();
+            int bi = row < p.M ? row : 0x7fffffff;
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            cw[u] = nw[u];
-#pragma unroll
-            for (int q = 0; q < NP; q++) cx[u][q] = nx[u][q];
-#pragma unroll
-            for (int q = 0; q < NM; q++) cm[u][q] = nm[u][q];
+            for (int off = 8; off >= 1; off >>= 1) {
+                const float ov = __shfl_xor(bv, off, 64);
+                const int oi = __shfl_xor(bi, off, 64);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            if (r == 0) {
+                p.part_val[(size_t)n * p.ntiles + tile] = bv;
+                p.part_idx[(size_t)n * p.ntiles + tile] = bi;
+            }
+            break;
         }
-        cs = ns;
+        default:
+            break;  // EPI_SWIGLU_Q8 never uses R16 (interleaved gate/up stays R64)
     }
-    gemm_epilogue<NMAX, S>(p, acc, tile, wave, lane);
+}
+
+template <int NMAX, int S, int U, int D>
+__global__ __launch_bounds__(64 * S) void gemm_q4_0_r16_kernel(GemmParams p) {
+    static_assert(16 * NMAX <= 64 * S, "chain threads must fit the workgroup");
+    static_assert(U == 1 || U == 2 || U == 4, "quads per wave per round");
+    constexpr int QR = S * U;                // quads per round
+    constexpr int BR = 4 * QR;               // blocks per round
+    constexpr int NP = (NMAX + 1) / 2;       // token-pair activation dwords per block
+    constexpr int NM = (NMAX + 7) / 8;       // meta dwords per block
+    constexpr int SW = U == 4 ? 2 : 1;       // scale dwords per wave round
+    extern __shared__ float lds[];           // [2][BR][NMAX][16]
+    const int tile = blockIdx.x;
+    const int wave = wave_id_uniform();
+    const int lane = threadIdx.x & 63;
+    const int j = lane >> 4, i16 = lane & 15;
+    const int N = p.N, nb = p.units;
+    const int nq = (nb + 3) / 4;
+    const uint8_t* wt = p.w + (size_t)tile * p.groups * kQ40ChunkBytes;
+    const int* xbase = (const int*)p.x + (i16 & 7);
+    const int xtok = i16 >> 3, mtok = i16 & 7;
+    const int* mbase = i16 >= 8 ? p.xs8 : (const int*)p.xs;
+    const int nrounds = (nq + QR - 1) / QR;
+
+    uint4 rw[D][U];
+    uint32_t rs[D][SW];
+    int rx[D][U][NP], rm[D][U][NM];
+#define NC_R16_LOAD(R, SLOT)                                                                         \
+    do {                                                                                             \
+        const int qd0_ = (R) * QR + wave * U;                                                        \
+        if ((R) < nrounds && qd0_ < nq) {                                                            \
+            const uint8_t* chunk_ = wt + (size_t)(qd0_ >> 3) * kQ40ChunkBytes;                       \
+            _Pragma("unroll") for (int u = 0; u < U; u++) rw[SLOT][u] =                              \
+                *(const uint4*)(chunk_ + ((qd0_ + u) & 7) * 1024 + lane * 16);                       \
+            const uint8_t* sp_ = chunk_ + 8192 + lane * 16 + (qd0_ & 7) * 2;                         \
+            if constexpr (SW == 2) {                                                                 \
+                const uint2 s2_ = *(const uint2*)sp_;                                                \
+                rs[SLOT][0] = s2_.x;                                                                 \
+                rs[SLOT][SW - 1] = s2_.y;                                                            \
+            } else if constexpr (U == 2) {                                                           \
+                rs[SLOT][0] = *(const uint32_t*)sp_;                                                 \
+            } else {                                                                                 \
+                rs[SLOT][0] = *(const uint16_t*)sp_;                                                 \
+            }                                                                                        \
+            _Pragma("unroll") for (int u = 0; u < U; u++) {                                          \
+                const int b_ = min(4 * (qd0_ + u) + j, nb - 1);                                      \
+                _Pragma("unroll") for (int q = 0; q < NP; q++) {                                     \
+                    const int t_ = min(2 * q + xtok, N - 1);                                         \
+                    rx[SLOT][u][q] = xbase[((size_t)t_ * p.K + (size_t)b_ * 32) / 4];                \
+                }                                                                                    \
+                _Pragma("unroll") for (int q = 0; q < NM; q++) {                                     \
+                    const int t_ = min(8 * q + mtok, N - 1);                                         \
+                    rm[SLOT][u][q] = mbase[(size_t)t_ * nb + b_];                                    \
+                }                                                                                    \
+            }                                                                                        \
+        }                                                                                            \
+    } while (0)
+
+#pragma unroll
+    for (int k = 0; k < D - 1; k++) NC_R16_LOAD(k, k);
+    float acc = 0.0f;
+    const int cn = threadIdx.x >> 4, cr = threadIdx.x & 15;  // chain thread: token, row
+    for (int r0 = 0; r0 < nrounds; r0 += D) {
+#pragma unroll
+        for (int k = 0; k < D; k++) {
+            const int r = r0 + k;
+            if (r < nrounds) {  // uniform
+                NC_R16_LOAD(r + D - 1, (k + D - 1) % D);
+                float* buf = lds + (size_t)(r & 1) * BR * NMAX * 16;
+                const int qd0 = r * QR + wave * U;
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    if (qd0 + u < nq) {  // uniform
+                        const uint4 v = rw[k][u];
+                        const int lo[4] = {(int)(v.x & 0x0F0F0F0Fu), (int)(v.y & 0x0F0F0F0Fu),
+                                           (int)(v.z & 0x0F0F0F0Fu), (int)(v.w & 0x0F0F0F0Fu)};
+                        const int hi[4] = {(int)((v.x >> 4) & 0x0F0F0F0Fu), (int)((v.y >> 4) & 0x0F0F0F0Fu),
+                                           (int)((v.z >> 4) & 0x0F0F0F0Fu), (int)((v.w >> 4) & 0x0F0F0F0Fu)};
+                        const uint32_t sw = rs[k][(u >> 1) & (SW - 1)];
+                        const float ws = f16_to_f32((uint16_t)((u & 1) ? (sw >> 16) : (sw & 0xffff)));
+                        float* dst = buf + ((size_t)((wave * U + u) * 4 + j) * NMAX) * 16 + i16;
+                        [&]<int... I>(std::integer_sequence<int, I...>) {
+                            ((I < N ? (void)(dst[I * 16] = term_q40<I>(rx[k][u], rm[k][u], lo, hi, ws)) : (void)0),
+                             ...);
+                        }(std::make_integer_sequence<int, NMAX>{});
+                    }
+                }
+                __syncthreads();
+                if (threadIdx.x < 16 * NMAX && cn < N) {
+                    const int nblk = min(BR, nb - r * BR);
+                    const float* src = buf + cn * 16 + cr;
+                    for (int bl = 0; bl < nblk; bl++) acc = acc + src[bl * NMAX * 16];
+                }
+            }
+        }
+    }
+#undef NC_R16_LOAD
+    if (threadIdx.x < 16 * NMAX && cn < N) gemm_epilogue_r16<NMAX>(p, acc, cn, tile, cr);
 }
 
 // ---------------------------------------------------------------- Q4_K
@@ -397,15 +565,21 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------- per-block dots (parity debug)
-__global__ void blockdots_q4_0_kernel(const uint8_t* w, int groups, int M, int K, const int8_t* x, int N, int32_t* dots) {
+__global__ void blockdots_q4_0_kernel(const uint8_t* w, int groups, int r16, int M, int K, const int8_t* x, int N,
+                                      int32_t* dots) {
     const int nb = K / 32;
     const int64_t total = (int64_t)N * M * nb;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
         const int b = (int)(i % nb);
         const int r = (int)((i / nb) % M);
         const int n = (int)(i / ((int64_t)nb * M));
-        const uint8_t* chunk = w + ((size_t)(r / 64) * groups + b / 8) * kQ40ChunkBytes;
-        const uint8_t* nib = chunk + (b & 7) * 1024 + (r & 63) * 16;
+        const uint8_t* nib;
+        if (r16) {
+            const int qd = b / 4, lane = 16 * (b & 3) + (r & 15);
+            nib = w + ((size_t)(r / 16) * groups + qd / 8) * kQ40ChunkBytes + (qd & 7) * 1024 + lane * 16;
+        } else {
+            nib = w + ((size_t)(r / 64) * groups + b / 8) * kQ40ChunkBytes + (b & 7) * 1024 + (r & 63) * 16;
+        }
         const int8_t* xb = x + (size_t)n * K + (size_t)b * 32;
         int d = 0;
         for (int j = 0; j < 16; j++) {
@@ -449,11 +623,13 @@ constexpr int pick_u_k() {
 template <int NMAX, int S>
 int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     if (w.type == NC_TYPE_Q4_0) {
-        const size_t lds = S > 1 ? (size_t)S * 4 * NMAX * 64 * sizeof(float) : 0;
+        constexpr int D = 3;
+        const size_t lds = S > 1 ? (size_t)2 * S * 4 * NMAX * 64 * sizeof(float) : 0;
         if (ev0)
-            hipExtLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0, p);
+            hipExtLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0,
+                                  p);
         else
-            hipLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+            hipLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
     } else {
         constexpr int U = pick_u_k<NMAX, S>();
         const size_t lds = S > 1 ? (size_t)S * U * NMAX * 64 * sizeof(float) : 0;
@@ -467,6 +643,22 @@ int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
     return NC_OK;
 }
 
+// R16: S waves so that the chain threads (16 per token) fit; U = 2 quads per wave-round,
+// a ring of 3 rounds in flight.
+template <int NMAX>
+int launch_r16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    constexpr int S = 4;  // 16 chain threads per token: 4 waves hold up to 16 tokens
+    constexpr int U = 4, D = 4;
+    const size_t lds = (size_t)2 * 4 * S * U * NMAX * 16 * sizeof(float);
+    if (ev0)
+        hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1,
+                              0, p);
+    else
+        hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
 template <int NMAX>
 int launch_s(int S, const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     switch (S) {
@@ -474,7 +666,9 @@ int launch_s(int S, const QMatDev& w, const GemmParams& p, hipStream_t st, hipEv
         case 2: return launch_one<NMAX, 2>(w, p, st, ev0, ev1);
         case 4: return launch_one<NMAX, 4>(w, p, st, ev0, ev1);
         case 8: return launch_one<NMAX, 8>(w, p, st, ev0, ev1);
-        default: return launch_one<NMAX, 16>(w, p, st, ev0, ev1);
+        default:  // 16 waves only where their registers suffice (a 1024-thread block caps VGPRs at 128)
+            if constexpr (NMAX <= 4) return launch_one<NMAX, 16>(w, p, st, ev0, ev1);
+            else return launch_one<NMAX, 8>(w, p, st, ev0, ev1);
     }
 }
 
@@ -496,6 +690,14 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent
     p.M = (int)w.rows;
     p.K = (int)w.cols;
     if (p.N < 1 || p.N > 16) return fail(NC_EINVAL, "gemm: batch must be 1..16");
+    if (w.layout == LAYOUT_R16) {
+        if (p.epi == EPI_SWIGLU_Q8) return fail(NC_EINVAL, "gemm: the SwiGLU epilogue needs the R64 layout");
+        if (p.N == 1) return launch_r16<1>(w, p, st, ev0, ev1);
+        if (p.N == 2) return launch_r16<2>(w, p, st, ev0, ev1);
+        if (p.N <= 4) return launch_r16<4>(w, p, st, ev0, ev1);
+        if (p.N <= 8) return launch_r16<8>(w, p, st, ev0, ev1);
+        return launch_r16<16>(w, p, st, ev0, ev1);
+    }
     const int nmax = p.N == 1 ? 1 : (p.N == 2 ? 2 : (p.N <= 4 ? 4 : (p.N <= 8 ? 8 : 16)));
     int S = pick_waves(w.tiles, nmax);
     // NC_GEMM_WAVES=<1|2|4|8|16>: tuning override of the K-split width (LDS limit still applies)
@@ -516,7 +718,8 @@ int launch_blockdots(const QMatDev& w, const int8_t* x, int32_t* dots, int N, hi
     const int64_t total = (int64_t)N * w.rows * (w.cols / 32);
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
     if (w.type == NC_TYPE_Q4_0)
-        hipLaunchKernelGGL(blockdots_q4_0_kernel, dim3(blocks), dim3(256), 0, st, w.dev, (int)w.groups, (int)w.rows,
+        hipLaunchKernelGGL(blockdots_q4_0_kernel, dim3(blocks), dim3(256), 0, st, w.dev, (int)w.groups,
+                           (int)(w.layout == LAYOUT_R16), (int)w.rows,
                            (int)w.cols, x, N, dots);
     else
         hipLaunchKernelGGL(blockdots_q4_k_kernel, dim3(blocks), dim3(256), 0, st, w.dev, (int)w.units, (int)w.rows,

@@ -34,12 +34,21 @@ constexpr int kQ40ChunkBytes = kQ40GroupBlocks * 1024 + 1024;  // 9216
 // the 12 packed scale bytes, slots 1..8 = the 128 nibble bytes.
 constexpr int kQ4KChunkBytes = 9 * 1024;
 
+// Q4_0 "R16" layout (matrices with fewer than 512 64-row tiles, so that a launch still
+// spans every CU): rows padded to 16-row tiles; blocks taken in quads (block b = 4*qd + j)
+// and groups of 8 quads.  Per (tile16, group) a 9216-byte chunk: 8 x [64 lanes x 16 B
+// nibbles] with lane = 16*j + r holding block 4*qd + j of row 16*tile + r, then [64 lanes x
+// 8 f16 scales] (one per quad of the group).  One wave load covers 4 blocks x 16 rows.
+constexpr int kTileRowsR16 = 16;
+enum Layout : int { LAYOUT_R64 = 0, LAYOUT_R16 = 1 };
+
 struct QMatDev {
     int type = NC_TYPE_Q4_0;
+    int layout = LAYOUT_R64;
     int64_t rows = 0, cols = 0;
-    int64_t tiles = 0;       // padded rows / 64
+    int64_t tiles = 0;       // padded rows / 64 (R16: / 16)
     int64_t units = 0;       // Q4_0: blocks per row; Q4_K: super-blocks per row
-    int64_t groups = 0;      // Q4_0: ceil(blocks / 8)
+    int64_t groups = 0;      // Q4_0: ceil(blocks / 8) (R16: ceil(blocks / 32))
     uint8_t* dev = nullptr;  // repacked bytes
     int64_t dev_bytes = 0;
     int64_t algo_bytes = 0;  // rows * cols * 18/32 (Q4_0) or 144/256 (Q4_K)
@@ -52,6 +61,8 @@ struct QMatDev {
 void repack_q4_0(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups,
                  int64_t row_off, int half);
 void repack_q4_k(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t row_off, int half);
+void repack_q4_0_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups, int64_t row_off);
+int64_t q40_r16_layout_bytes(int64_t rows, int64_t cols);
 int64_t q40_layout_bytes(int64_t rows, int64_t cols);
 int64_t q4k_layout_bytes(int64_t rows, int64_t cols);
 

@@ -136,6 +136,29 @@ void repack_q4_0(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* ds
     });
 }
 
+int64_t q40_r16_layout_bytes(int64_t rows, int64_t cols) {
+    const int64_t tiles = (rows + 15) / 16, groups = (cols / 32 + 31) / 32;
+    return tiles * groups * kQ40ChunkBytes;
+}
+
+void repack_q4_0_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups,
+                     int64_t row_off) {
+    const int64_t nb = cols / 32;
+    parallel_for(rows_src, 0, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; r++) {
+            const int64_t R = row_off + r;
+            const int64_t t = R / 16, rr = R % 16;
+            for (int64_t b = 0; b < nb; b++) {
+                const uint8_t* blk = src + (r * nb + b) * 18;
+                const int64_t qd = b / 4, j = b % 4, lane = 16 * j + rr;
+                uint8_t* chunk = dst + (t * groups + qd / 8) * kQ40ChunkBytes;
+                std::memcpy(chunk + (qd % 8) * 1024 + lane * 16, blk + 2, 16);
+                std::memcpy(chunk + 8192 + lane * 16 + (qd % 8) * 2, blk, 2);
+            }
+        }
+    });
+}
+
 void repack_q4_k(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t row_off, int half) {
     const int64_t nsb = cols / 256;
     parallel_for(rows_src, 0, [&](int64_t lo, int64_t hi) {
@@ -166,14 +189,26 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
     out.type = type;
     out.rows = rows;
     out.cols = cols;
-    out.tiles = (rows + 63) / 64;
+    // R16 for Q4_0 matrices too small to fill the chip with 64-row tiles (an interleaved
+    // gate/up pair keeps R64: its SwiGLU epilogue pairs lanes within a 64-row tile)
+    bool interleaved = false;
+    for (const auto& p : parts) interleaved = interleaved || p.half >= 0;
+    out.layout = type == NC_TYPE_Q4_0 && !interleaved && (rows + 63) / 64 < 512 ? LAYOUT_R16 : LAYOUT_R64;
     out.units = type == NC_TYPE_Q4_0 ? cols / 32 : cols / 256;
-    out.groups = type == NC_TYPE_Q4_0 ? (out.units + 7) / 8 : 0;
-    out.dev_bytes = type == NC_TYPE_Q4_0 ? q40_layout_bytes(rows, cols) : q4k_layout_bytes(rows, cols);
+    if (out.layout == LAYOUT_R16) {
+        out.tiles = (rows + 15) / 16;
+        out.groups = (out.units + 31) / 32;
+        out.dev_bytes = q40_r16_layout_bytes(rows, cols);
+    } else {
+        out.tiles = (rows + 63) / 64;
+        out.groups = type == NC_TYPE_Q4_0 ? (out.units + 7) / 8 : 0;
+        out.dev_bytes = type == NC_TYPE_Q4_0 ? q40_layout_bytes(rows, cols) : q4k_layout_bytes(rows, cols);
+    }
     out.algo_bytes = type == NC_TYPE_Q4_0 ? rows * cols / 32 * 18 : rows * cols / 256 * 144;
     std::vector<uint8_t> host(out.dev_bytes, 0);
     for (const auto& p : parts) {
-        if (type == NC_TYPE_Q4_0) repack_q4_0(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
+        if (out.layout == LAYOUT_R16) repack_q4_0_r16(p.src, p.rows, cols, host.data(), out.groups, p.row_off);
+        else if (type == NC_TYPE_Q4_0) repack_q4_0(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
         else repack_q4_k(p.src, p.rows, cols, host.data(), p.row_off, p.half);
     }
     NC_HIP(hipMalloc((void**)&out.dev, out.dev_bytes));

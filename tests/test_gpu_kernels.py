@@ -56,6 +56,20 @@ def test_q4_0_partial_group_and_tile(ctx):
     assert np.array_equal(out, O.matmul_q4_0(xq, xs, w, N, M, K))
 
 
+@pytest.mark.parametrize("N", [1, 2, 5, 8, 9, 16])
+@pytest.mark.parametrize("shape", [(100, 416), (32800, 416)], ids=["r16-partial", "r64-partial"])
+def test_q4_0_layouts_partial(ctx, shape, N):
+    """Both device layouts (16-row tiles below 512 64-row tiles, 64-row tiles above) with a
+    partial last tile, a partial last quad of blocks (13 blocks) and every batch width."""
+    import nanocamelid_amd as nc
+    M, K = shape
+    w = random_q4_0(M, K, seed=M + N)
+    _, xq, xs = q8_activations(N, K, seed=9 * N + M)
+    out, dots = _run_gemm(ctx, nc.NC_TYPE_Q4_0, w, M, K, xq, xs)
+    assert np.array_equal(dots, O.matmul_q4_0_blockdots(xq, w, N, M, K, nthreads=16))
+    assert np.array_equal(out.view(np.uint32), O.matmul_q4_0(xq, xs, w, N, M, K, nthreads=16).view(np.uint32))
+
+
 CONFIG1 = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
 
 
