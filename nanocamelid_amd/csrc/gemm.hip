@@ -169,6 +169,33 @@ __device__ __forceinline__ int dot32_bcast(int acc, int xp, int w0, int w1, int 
     return acc;
 }
 
+// Two tokens of a pair (2p, 2p+1) share the activation register xp: their 8-step chains
+// are interleaved (acc0 reads lanes 0..7 of each row, acc1 lanes 8..15) so that each
+// dot4c's dependency on its own accumulator is hidden behind the other chain.
+__device__ __forceinline__ void dot32_bcast_pair(int& acc0, int& acc1, int xp, int w0, int w1, int w2, int w3, int w4,
+                                                 int w5, int w6, int w7) {
+    asm("s_nop 1\n\t"
+        "v_dot4c_i32_i8_dpp %0, %2, %3 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %2, %3 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %2, %4 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %2, %4 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %2, %5 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %2, %5 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %2, %6 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %2, %6 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %2, %7 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %2, %7 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %2, %8 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %2, %8 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %2, %9 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %2, %9 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %2, %10 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %2, %10 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 2"
+        : "+v"(acc0), "+v"(acc1)
+        : "v"(xp), "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(w4), "v"(w5), "v"(w6), "v"(w7));
+}
+
 template <int J>
 __device__ __forceinline__ int bcast_i(int v) {
     return __builtin_amdgcn_mov_dpp(v, 0x150 + J, 0xf, 0xf, false);
@@ -188,9 +215,30 @@ __device__ __forceinline__ float term_q40(const int* xp, const int* meta, const 
     return (xs * ws) * (float)d;  // IEEE multiplication is commutative: == (ws * xs) * d
 }
 
-// R64: a ring of D rounds of weights, scales and activations is kept in flight per wave;
-// tokens n >= N are skipped (wave-uniform branch).  With S > 1 the terms go to a double-
+// R64: a ring of D rounds of weights, scales and activations is kept in flight per wave.
+// NMAX is the batch width itself for N <= 9.  With S > 1 the terms go to a double-
 // buffered LDS array, one barrier per round, and the chain threads add them in block order.
+// Terms of all NMAX tokens of one block (token pairs through dot32_bcast_pair).
+template <int NMAX>
+__device__ __forceinline__ void terms_q40(float (&t)[NMAX], const int* xp, const int* meta, const int (&lo)[4],
+                                          const int (&hi)[4], float ws) {
+    [&]<int... P>(std::integer_sequence<int, P...>) {
+        (([&] {
+             constexpr int n0 = 2 * P, n1 = 2 * P + 1;
+             if constexpr (n1 < NMAX) {
+                 int d0 = bcast_i<8 + (n0 & 7)>(meta[n0 >> 3]);
+                 int d1 = bcast_i<8 + (n1 & 7)>(meta[n1 >> 3]);
+                 dot32_bcast_pair(d0, d1, xp[P], lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]);
+                 t[n0] = (bcast_f<n0 & 7>(__int_as_float(meta[n0 >> 3])) * ws) * (float)d0;
+                 t[n1] = (bcast_f<n1 & 7>(__int_as_float(meta[n1 >> 3])) * ws) * (float)d1;
+             } else {
+                 t[n0] = term_q40<n0>(xp, meta, lo, hi, ws);
+             }
+         }()),
+         ...);
+    }(std::make_integer_sequence<int, (NMAX + 1) / 2>{});
+}
+
 template <int NMAX, int S, int D>
 __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
     constexpr int U = 4;                       // blocks per wave per round
@@ -220,25 +268,27 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
     uint4 rw[D][U];
     uint2 rs[D];
     int rx[D][U][NP], rm[D][U][NM];
+    // Loads are issued unconditionally (indices clamped into the padded matrix, data past the
+    // end is never used): straight-line load sequences keep the compiler's wait counts exact,
+    // so consuming one ring slot never drains the slots still in flight.
+    const int bmax = 8 * p.groups - U;  // last round start inside the padded groups (U | 8)
 #define NC_R64_LOAD(R, SLOT)                                                                        \
     do {                                                                                            \
-        const int b0_ = (R) * RB + wave * U;                                                        \
-        if ((R) < nrounds && b0_ < nb) {                                                            \
-            const uint8_t* chunk_ = wt + (size_t)(b0_ >> 3) * kQ40ChunkBytes;                       \
-            const int u0_ = b0_ & 7;                                                                \
-            _Pragma("unroll") for (int u = 0; u < U; u++) rw[SLOT][u] =                             \
-                *(const uint4*)(chunk_ + (u0_ + u) * 1024 + lane * 16);                             \
-            rs[SLOT] = *(const uint2*)(chunk_ + 8192 + lane * 16 + u0_ * 2);                        \
-            _Pragma("unroll") for (int u = 0; u < U; u++) {                                         \
-                const int b_ = min(b0_ + u, nb - 1);                                                \
-                _Pragma("unroll") for (int q = 0; q < NP; q++) {                                    \
-                    const int t_ = min(2 * q + xtok, N - 1);                                        \
-                    rx[SLOT][u][q] = xbase[((size_t)t_ * p.K + (size_t)b_ * 32) / 4];               \
-                }                                                                                   \
-                _Pragma("unroll") for (int q = 0; q < NM; q++) {                                    \
-                    const int t_ = min(8 * q + mtok, N - 1);                                        \
-                    rm[SLOT][u][q] = mbase[(size_t)t_ * nb + b_];                                   \
-                }                                                                                   \
+        const int b0_ = min(min((R), nrounds - 1) * RB + wave * U, bmax);                           \
+        const uint8_t* chunk_ = wt + (size_t)(b0_ >> 3) * kQ40ChunkBytes;                           \
+        const int u0_ = b0_ & 7;                                                                    \
+        _Pragma("unroll") for (int u = 0; u < U; u++) rw[SLOT][u] =                                 \
+            *(const uint4*)(chunk_ + (u0_ + u) * 1024 + lane * 16);                                 \
+        rs[SLOT] = *(const uint2*)(chunk_ + 8192 + lane * 16 + u0_ * 2);                            \
+        _Pragma("unroll") for (int u = 0; u < U; u++) {                                             \
+            const int b_ = min(b0_ + u, nb - 1);                                                    \
+            _Pragma("unroll") for (int q = 0; q < NP; q++) {                                        \
+                const int t_ = min(2 * q + xtok, N - 1);                                            \
+                rx[SLOT][u][q] = xbase[((size_t)t_ * p.K + (size_t)b_ * 32) / 4];                   \
+            }                                                                                       \
+            _Pragma("unroll") for (int q = 0; q < NM; q++) {                                        \
+                const int t_ = min(8 * q + mtok, N - 1);                                            \
+                rm[SLOT][u][q] = mbase[(size_t)t_ * nb + b_];                                       \
             }                                                                                       \
         }                                                                                           \
     } while (0)
@@ -249,8 +299,8 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
 #pragma unroll
         for (int k = 0; k < D; k++) {
             const int r = r0 + k;
+            NC_R64_LOAD(r + D - 1, (k + D - 1) % D);
             if (r < nrounds) {  // uniform
-                NC_R64_LOAD(r + D - 1, (k + D - 1) % D);
                 float* buf = lds + (size_t)(r & 1) * RB * NMAX * 64;
                 const int b0 = r * RB + wave * U;
 #pragma unroll
@@ -263,15 +313,16 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
                                            (int)((v.z >> 4) & 0x0F0F0F0Fu), (int)((v.w >> 4) & 0x0F0F0F0Fu)};
                         const uint32_t sw = u < 2 ? rs[k].x : rs[k].y;
                         const float ws = f16_to_f32((uint16_t)((u & 1) ? (sw >> 16) : (sw & 0xffff)));
-                        [&]<int... I>(std::integer_sequence<int, I...>) {
-                            ((I < N ? (void)([&] {
-                                 const float t = term_q40<I>(rx[k][u], rm[k][u], lo, hi, ws);
-                                 if constexpr (S == 1) acc[I] = acc[I] + t;
-                                 else buf[((wave * U + u) * NMAX + I) * 64 + lane] = t;
-                             }())
-                                    : (void)0),
-                             ...);
-                        }(std::make_integer_sequence<int, NMAX>{});
+                        // every token of the instantiation, without branches (tokens >= N read
+                        // clamped activations and are never stored): straight-line code keeps
+                        // the load wait counts precise
+                        float t[NMAX];
+                        terms_q40<NMAX>(t, rx[k][u], rm[k][u], lo, hi, ws);
+#pragma unroll
+                        for (int n = 0; n < NMAX; n++) {
+                            if constexpr (S == 1) acc[n] = acc[n] + t[n];
+                            else buf[((wave * U + u) * NMAX + n) * 64 + lane] = t[n];
+                        }
                     }
                 }
                 if constexpr (S > 1) {
@@ -282,7 +333,16 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
                         const int n = wave + t * S;
                         if (n < N) {
                             float a = acc[t];
-                            for (int bl = 0; bl < nblk; bl++) a = a + buf[(bl * NMAX + n) * 64 + lane];
+                            const float* src = buf + n * 64 + lane;
+                            int bl = 0;
+                            for (; bl + 8 <= nblk; bl += 8) {
+                                float v[8];
+#pragma unroll
+                                for (int i = 0; i < 8; i++) v[i] = src[(bl + i) * NMAX * 64];
+#pragma unroll
+                                for (int i = 0; i < 8; i++) a = a + v[i];
+                            }
+                            for (; bl < nblk; bl++) a = a + src[bl * NMAX * 64];
                             acc[t] = a;
                         }
                     }
@@ -392,33 +452,33 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_r16_kernel(GemmParams p) {
     uint4 rw[D][U];
     uint32_t rs[D][SW];
     int rx[D][U][NP], rm[D][U][NM];
+    // Unconditional, clamped loads (see the R64 kernel): exact wait counts across the ring.
+    const int qmax = 8 * p.groups - U;  // last wave-round start inside the padded groups (U | 8)
 #define NC_R16_LOAD(R, SLOT)                                                                         \
     do {                                                                                             \
-        const int qd0_ = (R) * QR + wave * U;                                                        \
-        if ((R) < nrounds && qd0_ < nq) {                                                            \
-            const uint8_t* chunk_ = wt + (size_t)(qd0_ >> 3) * kQ40ChunkBytes;                       \
-            _Pragma("unroll") for (int u = 0; u < U; u++) rw[SLOT][u] =                              \
-                *(const uint4*)(chunk_ + ((qd0_ + u) & 7) * 1024 + lane * 16);                       \
-            const uint8_t* sp_ = chunk_ + 8192 + lane * 16 + (qd0_ & 7) * 2;                         \
-            if constexpr (SW == 2) {                                                                 \
-                const uint2 s2_ = *(const uint2*)sp_;                                                \
-                rs[SLOT][0] = s2_.x;                                                                 \
-                rs[SLOT][SW - 1] = s2_.y;                                                            \
-            } else if constexpr (U == 2) {                                                           \
-                rs[SLOT][0] = *(const uint32_t*)sp_;                                                 \
-            } else {                                                                                 \
-                rs[SLOT][0] = *(const uint16_t*)sp_;                                                 \
+        const int qd0_ = min(min((R), nrounds - 1) * QR + wave * U, qmax);                           \
+        const uint8_t* chunk_ = wt + (size_t)(qd0_ >> 3) * kQ40ChunkBytes;                           \
+        _Pragma("unroll") for (int u = 0; u < U; u++) rw[SLOT][u] =                                  \
+            *(const uint4*)(chunk_ + ((qd0_ + u) & 7) * 1024 + lane * 16);                           \
+        const uint8_t* sp_ = chunk_ + 8192 + lane * 16 + (qd0_ & 7) * 2;                             \
+        if constexpr (SW == 2) {                                                                     \
+            const uint2 s2_ = *(const uint2*)sp_;                                                    \
+            rs[SLOT][0] = s2_.x;                                                                     \
+            rs[SLOT][SW - 1] = s2_.y;                                                                \
+        } else if constexpr (U == 2) {                                                               \
+            rs[SLOT][0] = *(const uint32_t*)sp_;                                                     \
+        } else {                                                                                     \
+            rs[SLOT][0] = *(const uint16_t*)sp_;                                                     \
+        }                                                                                            \
+        _Pragma("unroll") for (int u = 0; u < U; u++) {                                              \
+            const int b_ = min(4 * (qd0_ + u) + j, nb - 1);                                          \
+            _Pragma("unroll") for (int q = 0; q < NP; q++) {                                         \
+                const int t_ = min(2 * q + xtok, N - 1);                                             \
+                rx[SLOT][u][q] = xbase[((size_t)t_ * p.K + (size_t)b_ * 32) / 4];                    \
             }                                                                                        \
-            _Pragma("unroll") for (int u = 0; u < U; u++) {                                          \
-                const int b_ = min(4 * (qd0_ + u) + j, nb - 1);                                      \
-                _Pragma("unroll") for (int q = 0; q < NP; q++) {                                     \
-                    const int t_ = min(2 * q + xtok, N - 1);                                         \
-                    rx[SLOT][u][q] = xbase[((size_t)t_ * p.K + (size_t)b_ * 32) / 4];                \
-                }                                                                                    \
-                _Pragma("unroll") for (int q = 0; q < NM; q++) {                                     \
-                    const int t_ = min(8 * q + mtok, N - 1);                                         \
-                    rm[SLOT][u][q] = mbase[(size_t)t_ * nb + b_];                                    \
-                }                                                                                    \
+            _Pragma("unroll") for (int q = 0; q < NM; q++) {                                         \
+                const int t_ = min(8 * q + mtok, N - 1);                                             \
+                rm[SLOT][u][q] = mbase[(size_t)t_ * nb + b_];                                        \
             }                                                                                        \
         }                                                                                            \
     } while (0)
@@ -431,8 +491,8 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_r16_kernel(GemmParams p) {
 #pragma unroll
         for (int k = 0; k < D; k++) {
             const int r = r0 + k;
+            NC_R16_LOAD(r + D - 1, (k + D - 1) % D);
             if (r < nrounds) {  // uniform
-                NC_R16_LOAD(r + D - 1, (k + D - 1) % D);
                 float* buf = lds + (size_t)(r & 1) * BR * NMAX * 16;
                 const int qd0 = r * QR + wave * U;
 #pragma unroll
@@ -446,17 +506,26 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_r16_kernel(GemmParams p) {
                         const uint32_t sw = rs[k][(u >> 1) & (SW - 1)];
                         const float ws = f16_to_f32((uint16_t)((u & 1) ? (sw >> 16) : (sw & 0xffff)));
                         float* dst = buf + ((size_t)((wave * U + u) * 4 + j) * NMAX) * 16 + i16;
-                        [&]<int... I>(std::integer_sequence<int, I...>) {
-                            ((I < N ? (void)(dst[I * 16] = term_q40<I>(rx[k][u], rm[k][u], lo, hi, ws)) : (void)0),
-                             ...);
-                        }(std::make_integer_sequence<int, NMAX>{});
+                        float t[NMAX];
+                        terms_q40<NMAX>(t, rx[k][u], rm[k][u], lo, hi, ws);
+#pragma unroll
+                        for (int n = 0; n < NMAX; n++) dst[n * 16] = t[n];
                     }
                 }
                 __syncthreads();
                 if (threadIdx.x < 16 * NMAX && cn < N) {
                     const int nblk = min(BR, nb - r * BR);
                     const float* src = buf + cn * 16 + cr;
-                    for (int bl = 0; bl < nblk; bl++) acc = acc + src[bl * NMAX * 16];
+                    // groups of 16 terms read ahead of their dependent adds
+                    int bl = 0;
+                    for (; bl + 16 <= nblk; bl += 16) {
+                        float v[16];
+#pragma unroll
+                        for (int i = 0; i < 16; i++) v[i] = src[(bl + i) * NMAX * 16];
+#pragma unroll
+                        for (int i = 0; i < 16; i++) acc = acc + v[i];
+                    }
+                    for (; bl < nblk; bl++) acc = acc + src[bl * NMAX * 16];
                 }
             }
         }
@@ -647,8 +716,8 @@ int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
 // a ring of 3 rounds in flight.
 template <int NMAX>
 int launch_r16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    constexpr int S = 4;  // 16 chain threads per token: 4 waves hold up to 16 tokens
-    constexpr int U = 4, D = 4;
+    constexpr int S = 8;  // two waves per SIMD hide each other's dependency latency
+    constexpr int U = 2, D = 4;
     const size_t lds = (size_t)2 * 4 * S * U * NMAX * 16 * sizeof(float);
     if (ev0)
         hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1,
@@ -664,22 +733,34 @@ int launch_s(int S, const QMatDev& w, const GemmParams& p, hipStream_t st, hipEv
     switch (S) {
         case 1: return launch_one<NMAX, 1>(w, p, st, ev0, ev1);
         case 2: return launch_one<NMAX, 2>(w, p, st, ev0, ev1);
-        case 4: return launch_one<NMAX, 4>(w, p, st, ev0, ev1);
-        case 8: return launch_one<NMAX, 8>(w, p, st, ev0, ev1);
-        default:  // 16 waves only where their registers suffice (a 1024-thread block caps VGPRs at 128)
-            if constexpr (NMAX <= 4) return launch_one<NMAX, 16>(w, p, st, ev0, ev1);
-            else return launch_one<NMAX, 8>(w, p, st, ev0, ev1);
+        default: return launch_one<NMAX, 4>(w, p, st, ev0, ev1);
     }
 }
 
 }  // namespace
 
-// Waves per workgroup: enough K-split waves that ~1000+ waves stream the matrix.
-static int pick_waves(int64_t tiles, int nmax) {
+// R64 waves per workgroup: enough K-split waves that ~1000+ waves stream the matrix
+// (1, 2 or 4; LDS terms double-buffered: 2 * S * 4 * NMAX * 64 floats).
+static int pick_waves(int64_t tiles) {
     int S = 1;
-    while (S < 16 && tiles * S < 1024 && (2 * S) * 4 * nmax <= 256) S *= 2;
+    while (S < 4 && tiles * S < 1024) S *= 2;
     return S;
 }
+
+// Instantiated batch widths: exact for 1..9 (k <= 8 verify widths, decode), 16 above.
+#define NC_GEMM_FOR_NMAX(F, N_, ...)                  \
+    switch ((N_) <= 9 ? (N_) : 16) {                  \
+        case 1: return F<1>(__VA_ARGS__);             \
+        case 2: return F<2>(__VA_ARGS__);             \
+        case 3: return F<3>(__VA_ARGS__);             \
+        case 4: return F<4>(__VA_ARGS__);             \
+        case 5: return F<5>(__VA_ARGS__);             \
+        case 6: return F<6>(__VA_ARGS__);             \
+        case 7: return F<7>(__VA_ARGS__);             \
+        case 8: return F<8>(__VA_ARGS__);             \
+        case 9: return F<9>(__VA_ARGS__);             \
+        default: return F<16>(__VA_ARGS__);           \
+    }
 
 int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     GemmParams p = p0;
@@ -692,26 +773,16 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent
     if (p.N < 1 || p.N > 16) return fail(NC_EINVAL, "gemm: batch must be 1..16");
     if (w.layout == LAYOUT_R16) {
         if (p.epi == EPI_SWIGLU_Q8) return fail(NC_EINVAL, "gemm: the SwiGLU epilogue needs the R64 layout");
-        if (p.N == 1) return launch_r16<1>(w, p, st, ev0, ev1);
-        if (p.N == 2) return launch_r16<2>(w, p, st, ev0, ev1);
-        if (p.N <= 4) return launch_r16<4>(w, p, st, ev0, ev1);
-        if (p.N <= 8) return launch_r16<8>(w, p, st, ev0, ev1);
-        return launch_r16<16>(w, p, st, ev0, ev1);
+        NC_GEMM_FOR_NMAX(launch_r16, p.N, w, p, st, ev0, ev1)
     }
-    const int nmax = p.N == 1 ? 1 : (p.N == 2 ? 2 : (p.N <= 4 ? 4 : (p.N <= 8 ? 8 : 16)));
-    int S = pick_waves(w.tiles, nmax);
-    // NC_GEMM_WAVES=<1|2|4|8|16>: tuning override of the K-split width (LDS limit still applies)
+    int S = pick_waves(w.tiles);
+    // NC_GEMM_WAVES=<1|2|4>: tuning override of the R64 K-split width
     static const int forced = [] {
         const char* e = getenv("NC_GEMM_WAVES");
         return e ? atoi(e) : 0;
     }();
-    if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16)
-        S = (forced * 4 * nmax <= 256 || forced == 1) ? forced : S;
-    if (p.N == 1) return launch_s<1>(S, w, p, st, ev0, ev1);
-    if (p.N == 2) return launch_s<2>(S, w, p, st, ev0, ev1);
-    if (p.N <= 4) return launch_s<4>(S, w, p, st, ev0, ev1);
-    if (p.N <= 8) return launch_s<8>(S, w, p, st, ev0, ev1);
-    return launch_s<16>(S, w, p, st, ev0, ev1);
+    if (forced == 1 || forced == 2 || forced == 4) S = forced;
+    NC_GEMM_FOR_NMAX(launch_s, p.N, S, w, p, st, ev0, ev1)
 }
 
 int launch_blockdots(const QMatDev& w, const int8_t* x, int32_t* dots, int N, hipStream_t st) {
