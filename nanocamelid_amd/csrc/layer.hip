@@ -370,41 +370,57 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
     for (int j = 0; j < E; j++) probs[t * E + j] = e[j] * inv;
     __syncthreads();
     if (t >= a.hd) return;  // no barriers below
+    // Weighted V sum, lane = output dim t.  V is stored in position quads: one 16-byte load
+    // brings positions 4q..4q+3 of this lane's dim (consecutive lanes read consecutive 16
+    // bytes).  A ring of D batches of B quads keeps (D-1)*B*4 positions in flight; loads are
+    // unconditional with clamped indices so the wait counts stay exact.
     const int HDv = a.hd;
-    const float* v = a.vcache + (size_t)kvh * a.max_ctx * HDv + t;
-    // V rows stream from HBM: a ring of D batches of B positions keeps (D-1)*B rows in
-    // flight ahead of the add chain (registers are plentiful at one wave per SIMD).
-    constexpr int B = 32, D = T >= 512 ? 2 : 4;
-    float ring[D][B];
-    const int nb = L / B;
-#pragma unroll
-    for (int k = 0; k < D - 1; k++)
-        if (k < nb) {
-#pragma unroll
-            for (int j = 0; j < B; j++) ring[k][j] = v[(size_t)(k * B + j) * HDv];
-        }
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v* vq = (const f4v*)(a.vcache + (size_t)kvh * a.max_ctx * HDv) + t;  // [quad][dim]
+    constexpr int B = 8, D = 6;
+    const int nq = L >> 2;    // whole position quads
+    const int nbt = nq / B;   // whole batches
     float acc = 0.0f;
-    int b = 0;
-    for (; b + D <= nb; b += D) {
+    if (nbt > 0) {
+        f4v ring[D][B];
+#define NC_PV_LOAD(BT, SLOT)                                                                 \
+        _Pragma("unroll") for (int j = 0; j < B; j++) ring[SLOT][j] =                        \
+            vq[(size_t)(min((BT), nbt - 1) * B + j) * HDv];
 #pragma unroll
-        for (int k = 0; k < D; k++) {
-            const int nxt = b + k + D - 1;  // batch loaded into slot (k + D - 1) % D
-            if (nxt < nb) {
+        for (int k = 0; k < D - 1; k++) NC_PV_LOAD(k, k)
+        for (int b0 = 0; b0 < nbt; b0 += D) {
 #pragma unroll
-                for (int j = 0; j < B; j++) ring[(k + D - 1) % D][j] = v[(size_t)(nxt * B + j) * HDv];
+            for (int k = 0; k < D; k++) {
+                const int b = b0 + k;
+                NC_PV_LOAD(b + D - 1, (k + D - 1) % D)
+                if (b < nbt) {
+#pragma unroll
+                    for (int j = 0; j < B; j++) {
+                        const float4 p4 = *(const float4*)&probs[(b * B + j) * 4];
+                        const f4v v = ring[k][j];
+                        acc = acc + p4.x * v.x;
+                        acc = acc + p4.y * v.y;
+                        acc = acc + p4.z * v.z;
+                        acc = acc + p4.w * v.w;
+                    }
+                }
             }
-#pragma unroll
-            for (int j = 0; j < B; j++) acc = acc + probs[(b + k) * B + j] * ring[k][j];
         }
+#undef NC_PV_LOAD
     }
-#pragma unroll
-    for (int k = 0; k < D; k++) {  // remaining whole batches (fewer than D), already in flight
-        if (b + k < nb) {
-#pragma unroll
-            for (int j = 0; j < B; j++) acc = acc + probs[(b + k) * B + j] * ring[k][j];
-        }
+    for (int q = nbt * B; q < nq; q++) {
+        const f4v v = vq[(size_t)q * HDv];
+        acc = acc + probs[4 * q] * v.x;
+        acc = acc + probs[4 * q + 1] * v.y;
+        acc = acc + probs[4 * q + 2] * v.z;
+        acc = acc + probs[4 * q + 3] * v.w;
     }
-    for (int p = nb * B; p < L; p++) acc = acc + probs[p] * v[(size_t)p * HDv];
+    if (nq * 4 < L) {  // 1..3 positions of a last partial quad, each added only if it exists
+        const f4v v = vq[(size_t)nq * HDv];
+        acc = acc + probs[4 * nq] * v.x;
+        if (nq * 4 + 1 < L) acc = acc + probs[4 * nq + 1] * v.y;
+        if (nq * 4 + 2 < L) acc = acc + probs[4 * nq + 2] * v.z;
+    }
     const int aw = a.H * HDv;
     const int col = h * HDv + (t & ~31);
     store_q8_block(acc, t & 31, a.xq + (size_t)n * aw + col, a.xs + (size_t)n * (aw / 32) + col / 32,

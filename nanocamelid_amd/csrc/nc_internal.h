@@ -89,7 +89,7 @@ struct GemmParams {
     int aw = 0, kw = 0, hd = 0, rope_half = 0, max_ctx = 0, kv_heads = 0;
     const float* rope_tab = nullptr;  // [max_ctx][rope_half][2] = (sin, cos)
     float* kcache = nullptr;          // layer base of [kv_heads][max_ctx][hd]
-    float* vcache = nullptr;
+    float* vcache = nullptr;          // layer base of [kv_heads][max_ctx/4][hd][4] (position quads)
     const int32_t* d_pos = nullptr;   // start position of row 0
     // EPI_SWIGLU_Q8
     int8_t* xq_out = nullptr;
@@ -121,7 +121,7 @@ int launch_embed(const float* table, const uint32_t* toks, int N, int d, float* 
 struct AttnParams {
     const float* q = nullptr;  // [N][H*hd]
     const float* kcache = nullptr;  // layer base [Hkv][max_ctx][hd]
-    const float* vcache = nullptr;
+    const float* vcache = nullptr;  // layer base [Hkv][max_ctx/4][hd][4]: 4 positions of a dim per 16 B
     float* scores = nullptr;  // [N][H][max_ctx]
     int8_t* xq = nullptr;     // [N][H*hd] quantised attention output
     float* xs = nullptr;

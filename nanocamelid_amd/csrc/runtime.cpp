@@ -48,15 +48,16 @@ struct nc_session {
     nc_ctx* ctx = nullptr;
     hipStream_t stream = nullptr;
     int64_t max_ctx = 0;
+    int64_t ctx_stride = 0;  // max_ctx rounded up to 4: KV rows, V position quads, score rows
     int max_batch = 0;
     int64_t maxw = 0;
-    float *kcache = nullptr, *vcache = nullptr;  // [L][Hkv][max_ctx][hd]
+    float *kcache = nullptr, *vcache = nullptr;  // K [L][Hkv][ctx_stride][hd], V [L][Hkv][ctx_stride/4][hd][4]
     float* hidden = nullptr;                     // [B][d]
     int8_t* xq = nullptr;                        // [B][maxw]
     float* xs = nullptr;                         // [B][maxw/32]
     int32_t* xs8 = nullptr;  // -8 * per-block int8 sums
     float* q = nullptr;       // [B][aw]
-    float* scores = nullptr;  // [B][H][max_ctx]
+    float* scores = nullptr;  // [B][H][ctx_stride]
     float* logits = nullptr;  // [B][V]
     float* part_val = nullptr;
     int32_t* part_idx = nullptr;
@@ -548,7 +549,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
     s->pending_toks = false;
     rc = launch_embed(m->tok_emb, s->d_toks, n, d, s->hidden, st);
     if (rc) return rc;
-    const size_t layer_kv = (size_t)Hkv * s->max_ctx * hd;
+    const size_t layer_kv = (size_t)Hkv * s->ctx_stride * hd;
     for (int64_t li = 0; li < c.block_count; li++) {
         const LayerDev& L = m->layers[li];
         if ((rc = launch_rmsnorm_q8(s->hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
@@ -564,7 +565,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
         p.kw = kw;
         p.hd = hd;
         p.rope_half = (int)c.rope_dimension_count / 2;
-        p.max_ctx = (int)s->max_ctx;
+        p.max_ctx = (int)s->ctx_stride;
         p.kv_heads = Hkv;
         p.rope_tab = s->rope_tab;
         p.kcache = s->kcache + li * layer_kv;
@@ -584,7 +585,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
         a.H = (int)c.head_count;
         a.Hkv = Hkv;
         a.hd = hd;
-        a.max_ctx = (int)s->max_ctx;
+        a.max_ctx = (int)s->ctx_stride;
         a.max_pos = (int)(start_pos + n - 1);
         a.scale = 1.0f / std::sqrt((float)hd);  // inference.rs:3927
         if ((rc = launch_attention(a, st))) return rc;
@@ -872,12 +873,13 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
     s->m = m;
     s->ctx = m->ctx;
     s->max_ctx = max_ctx;
+    s->ctx_stride = (max_ctx + 3) / 4 * 4;
     s->max_batch = max_batch;
     NC_HIP(hipStreamCreate(&s->stream));
     const nc_model_config& c = m->cfg;
     const int64_t B = max_batch;
     s->maxw = std::max({c.embedding_length, c.feed_forward_length, c.attention_output_width});
-    const size_t kv = (size_t)c.block_count * c.head_count_kv * max_ctx * c.head_dim;
+    const size_t kv = (size_t)c.block_count * c.head_count_kv * s->ctx_stride * c.head_dim;
     int rc;
     if ((rc = dev_alloc(s->allocs, &s->kcache, kv)) || (rc = dev_alloc(s->allocs, &s->vcache, kv)) ||
         (rc = dev_alloc(s->allocs, &s->hidden, B * c.embedding_length)) ||
@@ -885,7 +887,7 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
         (rc = dev_alloc(s->allocs, &s->xs, 2 * B * (s->maxw / 32))) ||
         (rc = dev_alloc(s->allocs, &s->xs8, 2 * B * (s->maxw / 32))) ||
         (rc = dev_alloc(s->allocs, &s->q, B * c.attention_output_width)) ||
-        (rc = dev_alloc(s->allocs, &s->scores, (size_t)B * c.head_count * max_ctx)) ||
+        (rc = dev_alloc(s->allocs, &s->scores, (size_t)B * c.head_count * s->ctx_stride)) ||
         (rc = dev_alloc(s->allocs, &s->logits, (size_t)B * c.vocab_size)) ||
         (rc = dev_alloc(s->allocs, &s->part_val, B * m->head.tiles)) ||
         (rc = dev_alloc(s->allocs, &s->part_idx, B * m->head.tiles)) ||
