@@ -276,6 +276,7 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(AttnParams a) {
     const int last = pos0 + a.N - 1;
     for (int tile = blockIdx.x; tile * 64 <= last; tile += gridDim.x) {
         __syncthreads();  // previous tile's readers are done with kt
+        if (tile * 64 > pos0 + min(a.N, ((int)blockIdx.z + 1) * RB) - 1) break;  // no row of this block reaches it
         const int rows = min(64, last + 1 - tile * 64);
         const float4* src = (const float4*)(a.kcache + ((size_t)kvh * a.max_ctx + (size_t)tile * 64) * HD);
         for (int i = threadIdx.x; i < rows * (HD / 4); i += blockDim.x) {
@@ -285,9 +286,10 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(AttnParams a) {
         __syncthreads();
         const int p = tile * 64 + lane;
         const float* krow = &kt[lane * RS];  // this lane's key row (stale for p > last: unused)
-        // rows whose window reaches this tile: n >= tile*64 - pos0 (uniform over the block)
-        const int n_first = max(0, tile * 64 - pos0);
-        for (int n0 = n_first; n0 < a.N; n0 += RB) {
+        // this block's rows: n = blockIdx.z*RB .. +RB-1 whose window reaches this tile
+        // (n >= tile*64 - pos0; uniform over the block)
+        const int n_first = max((int)blockIdx.z * RB, tile * 64 - pos0);
+        for (int n0 = n_first; n0 < min(a.N, ((int)blockIdx.z + 1) * RB); n0 += RB) {
             // this wave's head: q rows n0 .. n0+RB-1 into LDS (each wave owns its slice)
 #pragma unroll
             for (int r = 0; r < RB; r++) {
@@ -432,20 +434,17 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
     if (G > 8 || a.H % a.Hkv) return fail(NC_EINVAL, "attention: at most 8 query heads per KV head supported");
     const int tiles = (a.max_pos + 64) / 64;
     if (a.hd != 64 && a.hd != 128) return fail(NC_EINVAL, "attention: head_dim must be 64 or 128");
-    const int rb = a.N >= 8 ? 8 : a.N;  // rows interleaved per pass of the scores kernel
-#define NC_SCORES(HD, RB)                                                                       \
-    hipLaunchKernelGGL((attn_scores_kernel<HD, RB>), dim3(tiles, a.Hkv), dim3(64 * G), 0, st, a); \
+    // rows per block: one or two interleaved dot chains per lane; row groups are spread over
+    // blockIdx.z so that every SIMD gets a short chain instead of a few SIMDs getting long ones
+    const int rb = a.N >= 2 ? 2 : 1;
+#define NC_SCORES(HD, RB)                                                                         \
+    hipLaunchKernelGGL((attn_scores_kernel<HD, RB>), dim3(tiles, a.Hkv, (a.N + (RB)-1) / (RB)), dim3(64 * G), 0, \
+                       st, a);                                                                    \
     break;
 #define NC_SCORES_HD(HD)            \
     switch (rb) {                   \
         case 1: NC_SCORES(HD, 1)    \
-        case 2: NC_SCORES(HD, 2)    \
-        case 3: NC_SCORES(HD, 3)    \
-        case 4: NC_SCORES(HD, 4)    \
-        case 5: NC_SCORES(HD, 5)    \
-        case 6: NC_SCORES(HD, 6)    \
-        case 7: NC_SCORES(HD, 7)    \
-        default: NC_SCORES(HD, 8)   \
+        default: NC_SCORES(HD, 2)   \
     }
     if (a.hd == 128) {
         NC_SCORES_HD(128)
