@@ -93,7 +93,8 @@ int nc_quantize_q8_0_batch(nc_ctx* ctx, const float* x, int8_t* x_i8, float* x_s
  * quantiser above.  Replaces rms_norm_batch (src/inference.rs:949-967, row op :697-706)
  * followed by quantize_f32_to_q8_0_batch (:967-989), as run_layer_range_batch does at
  * :3802-3808.  Device pointers: x [batch][dim], w [dim], x_i8 [batch][dim],
- * x_scales [batch][dim/32].  dim = 256 * {1,2,3,4,6,8,12,16,20,24,32}. */
+ * x_scales [batch][dim/32].  dim one of 256, 512, 768, 1024, 1536, 2048, 3072, 4096, 5120, 6144,
+ * 8192. */
 int nc_rms_norm_q8_0_batch(nc_ctx* ctx, const float* x, const float* w, float eps, int8_t* x_i8, float* x_scales,
                            int batch_size, int64_t dim, void* stream);
 

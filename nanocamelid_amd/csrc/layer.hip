@@ -130,10 +130,10 @@ __device__ __forceinline__ void quantize_regs_q8(const float (&y)[E], int8_t* q_
     }
 }
 
-template <int E>
-__global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float* hidden, const float* weight, float eps,
-                                                          int8_t* xq, float* xs, int32_t* xsum) {
-    constexpr int T = 256, d = T * E;
+template <int E, int T>
+__global__ __launch_bounds__(T) void rmsnorm_q8_kernel(const float* hidden, const float* weight, float eps,
+                                                        int8_t* xq, float* xs, int32_t* xsum) {
+    constexpr int d = T * E;
     __shared__ ChainScratch<T> sc;
     __shared__ __align__(16) float a_lds[d];
     const int n = blockIdx.x;
@@ -166,26 +166,28 @@ __global__ __launch_bounds__(256) void rmsnorm_q8_kernel(const float* hidden, co
 
 int launch_rmsnorm_q8(const float* hidden, const float* weight, int N, int d, float eps, int8_t* xq, float* xs,
                       int32_t* xsum, hipStream_t st) {
-#define NC_RMS_CASE(E)                                                                                      \
-    case E:                                                                                                 \
-        hipLaunchKernelGGL(rmsnorm_q8_kernel<E>, dim3(N), dim3(256), 0, st, hidden, weight, eps, xq, xs, xsum); \
-        break;
-    switch (d % 256 ? 0 : d / 256) {
-        NC_RMS_CASE(1)
-        NC_RMS_CASE(2)
-        NC_RMS_CASE(3)
-        NC_RMS_CASE(4)
-        NC_RMS_CASE(6)
-        NC_RMS_CASE(8)
-        NC_RMS_CASE(12)
-        NC_RMS_CASE(16)
-        NC_RMS_CASE(20)
-        NC_RMS_CASE(24)
-        NC_RMS_CASE(32)
+    // One workgroup per row.  Wide rows use 1024 threads (4 waves per SIMD hide the latency
+    // of the chain's per-term work), small ones 256.
+#define NC_RMS(E, T)                                                                                     \
+    hipLaunchKernelGGL((rmsnorm_q8_kernel<E, T>), dim3(N), dim3(T), 0, st, hidden, weight, eps, xq, xs, xsum); \
+    break;
+    switch (d) {
+        case 256: NC_RMS(1, 256)
+        case 512: NC_RMS(2, 256)
+        case 768: NC_RMS(3, 256)
+        case 1024: NC_RMS(4, 256)
+        case 1536: NC_RMS(6, 256)
+        case 2048: NC_RMS(2, 1024)
+        case 3072: NC_RMS(3, 1024)
+        case 4096: NC_RMS(4, 1024)
+        case 5120: NC_RMS(5, 1024)
+        case 6144: NC_RMS(6, 1024)
+        case 8192: NC_RMS(8, 1024)
         default:
-            return fail(NC_EINVAL, "rmsnorm: width must be 256 * {1,2,3,4,6,8,12,16,20,24,32}");
+            return fail(NC_EINVAL, "rmsnorm: width must be one of 256, 512, 768, 1024, 1536, 2048, 3072, 4096, "
+                                   "5120, 6144, 8192");
     }
-#undef NC_RMS_CASE
+#undef NC_RMS
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
@@ -333,7 +335,7 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(AttnParams a) {
 //   prob_p = e_p * (1/sum);  out[d] = ((0 + prob_0*v_0[d]) + prob_1*v_1[d]) + ... in order,
 //   one lane per output dim d, V rows streamed with a software-pipelined prefetch.
 // Thread t owns positions [t*E, t*E + E) of the score row (zeros past the row's end).
-template <int E, int T>
+template <int E, int T, int HD>
 __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
     __shared__ ChainScratch<T> sc;
     __shared__ __align__(16) float probs[T * E];
@@ -371,23 +373,26 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
 #pragma unroll
     for (int j = 0; j < E; j++) probs[t * E + j] = e[j] * inv;
     __syncthreads();
-    if (t >= a.hd) return;  // no barriers below
+    if (t >= HD) return;  // no barriers below
     // Weighted V sum, lane = output dim t.  V is stored in position quads: one 16-byte load
     // brings positions 4q..4q+3 of this lane's dim (consecutive lanes read consecutive 16
     // bytes).  A ring of D batches of B quads keeps (D-1)*B*4 positions in flight; loads are
     // unconditional with clamped indices so the wait counts stay exact.
-    const int HDv = a.hd;
+    constexpr int HDv = HD;
     typedef float f4v __attribute__((ext_vector_type(4)));
-    const f4v* vq = (const f4v*)(a.vcache + (size_t)kvh * a.max_ctx * HDv) + t;  // [quad][dim]
+    // this lane's dim in quad 0; quad q is q * HD * 16 bytes further (compile-time strides)
+    const char* vlane = (const char*)(a.vcache + (size_t)kvh * a.max_ctx * HD) + t * 16;
     constexpr int B = 8, D = 6;
     const int nq = L >> 2;    // whole position quads
     const int nbt = nq / B;   // whole batches
     float acc = 0.0f;
     if (nbt > 0) {
         f4v ring[D][B];
-#define NC_PV_LOAD(BT, SLOT)                                                                 \
-        _Pragma("unroll") for (int j = 0; j < B; j++) ring[SLOT][j] =                        \
-            vq[(size_t)(min((BT), nbt - 1) * B + j) * HDv];
+#define NC_PV_LOAD(BT, SLOT)                                                                        \
+        {                                                                                           \
+            const char* bp_ = vlane + (size_t)min((BT), nbt - 1) * (B * HD * 16);                   \
+            _Pragma("unroll") for (int j = 0; j < B; j++) ring[SLOT][j] = *(const f4v*)(bp_ + j * HD * 16); \
+        }
 #pragma unroll
         for (int k = 0; k < D - 1; k++) NC_PV_LOAD(k, k)
         for (int b0 = 0; b0 < nbt; b0 += D) {
@@ -410,6 +415,7 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
         }
 #undef NC_PV_LOAD
     }
+    const f4v* vq = (const f4v*)vlane;  // [quad] stride HD f4v
     for (int q = nbt * B; q < nq; q++) {
         const f4v v = vq[(size_t)q * HDv];
         acc = acc + probs[4 * q] * v.x;
@@ -457,22 +463,27 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
     // max_pos + 1 is the longest score row of the pass
     const int len = a.max_pos + 1;
     const dim3 grid(a.N * a.H);
-    if (len <= 256)
-        hipLaunchKernelGGL((attn_softmax_pv_kernel<1, 256>), grid, dim3(256), 0, st, a);
-    else if (len <= 512)
-        hipLaunchKernelGGL((attn_softmax_pv_kernel<2, 256>), grid, dim3(256), 0, st, a);
-    else if (len <= 1024)
-        hipLaunchKernelGGL((attn_softmax_pv_kernel<4, 256>), grid, dim3(256), 0, st, a);
-    else if (len <= 2048)
-        hipLaunchKernelGGL((attn_softmax_pv_kernel<8, 256>), grid, dim3(256), 0, st, a);
-    else if (len <= 4096)
-        hipLaunchKernelGGL((attn_softmax_pv_kernel<16, 256>), grid, dim3(256), 0, st, a);
-    else if (len <= 8192)
-        hipLaunchKernelGGL((attn_softmax_pv_kernel<32, 256>), grid, dim3(256), 0, st, a);
-    else if (len <= 16384)
-        hipLaunchKernelGGL((attn_softmax_pv_kernel<32, 512>), grid, dim3(512), 0, st, a);
-    else
+#define NC_PV(E, T)                                                                              \
+    if (a.hd == 128) hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 128>), grid, dim3(T), 0, st, a); \
+    else hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 64>), grid, dim3(T), 0, st, a);
+    if (len <= 256) {
+        NC_PV(1, 256)
+    } else if (len <= 512) {
+        NC_PV(2, 256)
+    } else if (len <= 1024) {
+        NC_PV(4, 256)
+    } else if (len <= 2048) {
+        NC_PV(8, 256)
+    } else if (len <= 4096) {
+        NC_PV(16, 256)
+    } else if (len <= 8192) {
+        NC_PV(32, 256)
+    } else if (len <= 16384) {
+        NC_PV(32, 512)
+    } else {
         return fail(NC_ERANGE, "attention: context longer than 16384 positions");
+    }
+#undef NC_PV
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
