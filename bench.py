@@ -243,7 +243,7 @@ def main():
                    "verify_weight_bytes": int(cfg["verify_weight_bytes"])},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": measured_traffic(args),
-                     "kernel": "gemm_q4_0_kernel (all verify matmuls)",
+                     "kernel": "gemm_q4_0_r16_kernel + gemm_q4_0_kernel (all verify matmuls)",
                      "launches": int(launches), "avg_us": round(gemm_ms / max(launches, 1) * 1e3, 3),
                      "avg_algorithmic_bytes": int(gemm_bytes // max(launches, 1))},
         "cpu_baseline": cpu,
