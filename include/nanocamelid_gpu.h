@@ -98,6 +98,29 @@ int nc_quantize_q8_0_batch(nc_ctx* ctx, const float* x, int8_t* x_i8, float* x_s
 int nc_rms_norm_q8_0_batch(nc_ctx* ctx, const float* x, const float* w, float eps, int8_t* x_i8, float* x_scales,
                            int batch_size, int64_t dim, void* stream);
 
+/* ---------------------------------------------------------------- stochastic acceptance
+ * No reference counterpart: the reference's temperature path matches sampled tokens
+ * (src/speculative.rs:403) and samples with a global LCG (src/inference.rs:4834-4883).
+ * This library's specification (restated by the CPU oracle, checked bit for bit):
+ *   probs    p_j = e_j * (1/S), e_j = expf((l_j - max)/temp), S = sum e_j left to right in
+ *            f32 (the reference's softmax formula, src/inference.rs:3522-3540, 4857-4862);
+ *   uniform  u = (philox4x32_10(ctr = {pos, pos >> 32, purpose, 0}, key = seed).x >> 8) / 2^24,
+ *            purposes: draft sample 1, accept 2, resample 3, bonus 7;
+ *   accept   draft i (row at start_pos + i) iff u_accept * q_i(x) < p_i(x);
+ *   sample   W_j = floor(w_j * 2^40), first j whose inclusive prefix of W exceeds
+ *            floor(k24 * sum W / 2^24), k24 = u * 2^24.  At the first rejection the next
+ *            token is drawn from w = max(0, p_i - q_i) (from p_i if that has no mass) with
+ *            the resample uniform; after k acceptances from p_k with the bonus uniform. */
+/* probs[r][j] for rows x vocab (device pointers, row stride vocab); temp > 0. */
+int nc_temperature_probs_batch(nc_ctx* ctx, const float* logits, float* probs, int32_t rows, int64_t vocab, float temp,
+                               void* stream);
+/* k+1 acceptance over device buffers: p_probs [k+1][vocab] target probabilities of the rows
+ * at start_pos .. start_pos+k, q_probs [k][vocab] draft probabilities, drafts [k] ids.
+ * result (device, 3 x int32) = {n_accepted, next_token, start_pos + n_accepted + 1}.
+ * k 0..15; a draft id >= vocab counts as rejected. */
+int nc_stochastic_accept(nc_ctx* ctx, const float* p_probs, const float* q_probs, const uint32_t* drafts, int32_t k,
+                         int64_t vocab, uint64_t seed, int64_t start_pos, int32_t* result, void* stream);
+
 /* ---------------------------------------------------------------- model */
 typedef struct nc_model_config {
     int64_t context_length, embedding_length, block_count, feed_forward_length;
@@ -157,6 +180,12 @@ typedef struct nc_verify_result {
  * the n per-row predictions. */
 int nc_verify_greedy(nc_session* s, const uint32_t* toks, int32_t n, int64_t start_pos,
                      nc_verify_result* result, uint32_t* preds_host);
+/* k+1 stochastic verify: toks[0] = the pending token at start_pos, toks[1..n) = drafts
+ * sampled from q_probs (device, [n-1][vocab] draft probabilities at temperature temp).  One
+ * batched forward, then temperature probabilities and the acceptance above on the device;
+ * only the result struct returns.  The stochastic counterpart of nc_verify_greedy. */
+int nc_verify_stochastic(nc_session* s, const uint32_t* toks, int32_t n, int64_t start_pos, const float* q_probs,
+                         float temp, uint64_t seed, nc_verify_result* result);
 /* Copies row `row` of the last pass's logits ([vocab] f32) to host
  * (compute_logits_from_hidden, src/inference.rs:4783-4832). */
 int nc_session_logits(nc_session* s, int32_t row, float* logits_host);
@@ -193,6 +222,19 @@ int nc_generate_speculative_oracle(nc_session* s, const uint32_t* prompt, int32_
 int nc_generate_speculative_draft(nc_session* target, nc_session* draft, const uint32_t* prompt,
                                   int32_t n_prompt, int32_t n_new, int32_t draft_k, uint32_t* out,
                                   nc_decode_stats* stats);
+
+/* Draft-model speculative sampling at temperature temp > 0, k+1 form (no reference
+ * counterpart; the draft-model loop shape follows src/speculative.rs:299-494).  Both models
+ * prefill the prompt; the first token is drawn from the target's last prompt row with the
+ * bonus uniform at position n_prompt-1.  Per step at position pos with pending token t0:
+ * the draft runs t0, d_0 .. d_{k-2} at pos .. pos+k-1 and samples d_i from its temperature
+ * probabilities with u(seed, pos+i, draft); the target verifies [t0, d_0 .. d_{k-1}]; the
+ * acceptance above emits d_0 .. d_{a-1} and the next token.  After a full acceptance the
+ * draft first runs d_{k-1}.  k is clamped to max_batch-1 and the context of both sessions.
+ * Drafts stay on the device; one 16-byte result and the step's ids return per step. */
+int nc_generate_speculative_stochastic(nc_session* target, nc_session* draft, const uint32_t* prompt,
+                                       int32_t n_prompt, int32_t n_new, int32_t k, float temp, uint64_t seed,
+                                       uint32_t* out, nc_decode_stats* stats);
 
 /* ---------------------------------------------------------------- synthetic models */
 typedef struct nc_synth_spec {

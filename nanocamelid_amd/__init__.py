@@ -132,6 +132,32 @@ def rms_norm_q8_0_batch(ctx: Context, x, w, eps: float):
     return q, s
 
 
+def temperature_probs_batch(ctx: Context, logits, temp: float, out=None):
+    """Temperature softmax of each row on the GPU: p = expf((l - max)/temp) * (1/sum), the sum
+    left to right in f32 (the reference's softmax formula, src/inference.rs:3522-3540,
+    4857-4862).  logits: [rows][vocab] f32 device tensor."""
+    import torch
+    rows, vocab = logits.shape
+    out = torch.empty_like(logits) if out is None else out
+    check(lib().nc_temperature_probs_batch(ctx.h, logits.data_ptr(), out.data_ptr(), rows, vocab, float(temp),
+                                           _stream_of(logits)))
+    return out
+
+
+def stochastic_accept(ctx: Context, p_probs, q_probs, drafts, seed: int, start_pos: int):
+    """k+1 stochastic acceptance on the GPU (no reference counterpart; the library's Philox /
+    min(1, p/q) / fixed-point resampling specification).  p_probs [k+1][V], q_probs [k][V]
+    f32 and drafts [k] int32/uint32 device tensors.  Returns (n_accepted, next_token, new_pos)."""
+    import torch
+    k = p_probs.shape[0] - 1
+    res = torch.zeros(4, dtype=torch.int32, device=p_probs.device)
+    check(lib().nc_stochastic_accept(ctx.h, p_probs.data_ptr(), q_probs.data_ptr() if k else None,
+                                     drafts.data_ptr() if k else None, k, p_probs.shape[1], seed, start_pos,
+                                     res.data_ptr(), _stream_of(p_probs)))
+    r = res.cpu().tolist()
+    return r[0], r[1], r[2]
+
+
 class Model:
     """Llama weights on the device (LlamaWeights::load, src/model.rs:461-545)."""
 
@@ -190,6 +216,14 @@ class Session:
                                      preds.ctypes.data_as(C.POINTER(C.c_uint32))))
         return r.n_accepted, r.next_token, r.new_pos, preds
 
+    def verify_stochastic(self, toks, start_pos: int, q_probs, temp: float, seed: int):
+        """toks = [pending] + drafts; q_probs: [len(drafts)][vocab] f32 device tensor."""
+        a, p = _u32(toks)
+        r = VerifyResult()
+        check(lib().nc_verify_stochastic(self.h, p, a.size, start_pos, q_probs.data_ptr() if a.size > 1 else None,
+                                         float(temp), seed, C.byref(r)))
+        return r.n_accepted, r.next_token, r.new_pos
+
     def logits(self, row: int) -> np.ndarray:
         out = np.empty(self.vocab, np.float32)
         check(lib().nc_session_logits(self.h, row, out.ctypes.data_as(C.POINTER(C.c_float))))
@@ -245,6 +279,17 @@ def generate_speculative_draft(target: Session, draft: Session, prompt, n_new: i
     st = DecodeStats()
     check(lib().nc_generate_speculative_draft(target.h, draft.h, p, a.size, n_new, draft_k,
                                               out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
+    return out[:st.emitted], st
+
+
+def generate_speculative_stochastic(target: Session, draft: Session, prompt, n_new: int, k: int, temp: float,
+                                    seed: int):
+    """Draft-model speculative sampling at temperature temp (Philox acceptance), k+1 form."""
+    a, p = _u32(prompt)
+    out = np.zeros(n_new, np.uint32)
+    st = DecodeStats()
+    check(lib().nc_generate_speculative_stochastic(target.h, draft.h, p, a.size, n_new, k, float(temp), seed,
+                                                   out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
     return out[:st.emitted], st
 
 

@@ -67,6 +67,8 @@ SIGNATURES = {
     "nc_matmul_blockdots": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _vp]),
     "nc_quantize_q8_0_batch": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _vp]),
     "nc_rms_norm_q8_0_batch": (C.c_int, [_vp, _vp, _vp, C.c_float, _vp, _vp, C.c_int, _i64, _vp]),
+    "nc_temperature_probs_batch": (C.c_int, [_vp, _vp, _vp, _i32, _i64, C.c_float, _vp]),
+    "nc_stochastic_accept": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _i64, C.c_uint64, _i64, _vp, _vp]),
     "nc_model_load_gguf": (C.c_int, [_vp, C.c_char_p, C.POINTER(LoadOpts), C.POINTER(_vp)]),
     "nc_model_load_gguf_memory": (C.c_int, [_vp, _vp, C.c_size_t, C.POINTER(LoadOpts), C.POINTER(_vp)]),
     "nc_model_get_config": (C.c_int, [_vp, C.POINTER(ModelConfig)]),
@@ -76,12 +78,15 @@ SIGNATURES = {
     "nc_prefill": (C.c_int, [_vp, _u32p, _i32, _i64, _i32]),
     "nc_forward1": (C.c_int, [_vp, C.c_uint32, _i64, _f32p, _u32p]),
     "nc_verify_greedy": (C.c_int, [_vp, _u32p, _i32, _i64, C.POINTER(VerifyResult), _u32p]),
+    "nc_verify_stochastic": (C.c_int, [_vp, _u32p, _i32, _i64, _vp, C.c_float, C.c_uint64, C.POINTER(VerifyResult)]),
     "nc_session_logits": (C.c_int, [_vp, _i32, _f32p]),
     "nc_session_hidden": (C.c_int, [_vp, _i32, _f32p]),
     "nc_generate_greedy": (C.c_int, [_vp, _u32p, _i32, _i32, _u32p, C.POINTER(DecodeStats)]),
     "nc_generate_speculative_oracle": (C.c_int, [_vp, _u32p, _i32, _i32, _i32, _i32, C.c_float, C.c_uint64, _u32p,
                                                  _i32, _u32p, C.POINTER(DecodeStats)]),
     "nc_generate_speculative_draft": (C.c_int, [_vp, _vp, _u32p, _i32, _i32, _i32, _u32p, C.POINTER(DecodeStats)]),
+    "nc_generate_speculative_stochastic": (C.c_int, [_vp, _vp, _u32p, _i32, _i32, _i32, C.c_float, C.c_uint64, _u32p,
+                                                     C.POINTER(DecodeStats)]),
     "nc_synth_size": (C.c_int, [C.POINTER(SynthSpec), C.POINTER(C.c_uint64)]),
     "nc_synth_write": (C.c_int, [C.POINTER(SynthSpec), _vp, C.c_uint64, _i32]),
     "nc_uniform_prompt": (C.c_int, [C.c_uint64, _i64, C.c_uint32, _u32p]),

@@ -3,7 +3,7 @@
 // The reference accumulates several sums strictly left to right in f32 (the RMSNorm
 // sum of squares, inference.rs:697-706; the softmax denominator, inference.rs:3522-3540):
 //
-//     s_{-1} = 0,   s_i = fl32(s_{i-1} + a_i),   i = 0 .. n-1.
+//     s_{-1} = s0 (0 unless a carry-in is given),   s_i = fl32(s_{i-1} + a_i),   i = 0 .. n-1.
 //
 // On gfx950 one dependent v_add_f32 costs ~10 cycles, so a 4096-term chain is ~21 us
 // when evaluated literally.  This routine returns the bit-identical s_{n-1} from a
@@ -181,10 +181,12 @@ __device__ __forceinline__ double chain_increment(float g, float a, bool* sensit
 }
 
 // Thread t holds terms a[0..E) = a_{tE} .. a_{tE+E-1} (n = T*E terms; pad with zeros, which
-// leave the chain unchanged).  a_lds: n floats of LDS used by the fallback.  Every thread
-// of the block must call it; returns s_{n-1} to all threads.
+// leave the chain unchanged).  The chain starts from s_{-1} = s0 >= 0, so a long sum can be
+// evaluated as consecutive segments, each starting from the previous segment's result.
+// a_lds: n floats of LDS used by the fallback.  Every thread of the block must call it;
+// returns s_{n-1} to all threads.
 template <int E, int T>
-__device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float* a_lds) {
+__device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float* a_lds, float s0 = 0.0f) {
     static_assert(E >= 1 && E <= 32, "terms per thread");
     const int t = threadIdx.x;
 #pragma unroll
@@ -198,7 +200,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
         run += (double)a[j];
         w[j] = run;
     }
-    const double exclp = block_excl_scan_f64<T>(run, sc.dtot);
+    const double exclp = (double)s0 + block_excl_scan_f64<T>(run, sc.dtot);
 
     // 2. speculative increments and sensitivity (w[] becomes d[])
     uint32_t sens = 0;
@@ -240,7 +242,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
     if (listed && t < 64) {
         // s_{k-1} = s_j + (c_{k-1} - c_j) with j the previous sensitive step (the advance is
         // exact: nothing between j and k changes binade or ties), then s_k = fl32(s_{k-1} + a_k).
-        float s_run = 0.0f;    // s_j (s_{-1} = 0 = c_{-1} before the first entry)
+        float s_run = s0;      // s_j (s_{-1} = s0, c_{-1} = 0 before the first entry)
         double co_last = 0.0;  // c_j
         for (int e0 = 0; e0 < total_s; e0 += 64) {
             const int me = e0 + t;
@@ -278,7 +280,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
     bool bad = !listed;
     float cn[E];
     if (listed) {
-        double cur = off == 0 ? 0.0 : sc.ent[off - 1].shift;
+        double cur = off == 0 ? (double)s0 : sc.ent[off - 1].shift;
         int e = off;
 #pragma unroll
         for (int j = 0; j < E; j++) {
@@ -289,7 +291,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
     }
     __syncthreads();
     if (listed) {
-        float prev = t == 0 ? 0.0f : sc.last[t - 1];
+        float prev = t == 0 ? s0 : sc.last[t - 1];
 #pragma unroll
         for (int j = 0; j < E; j++) {
             bad |= (prev + a[j]) != cn[j];
@@ -300,7 +302,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
     if (!any_bad) {
         if (t == T - 1) sc.result = cn[E - 1];
     } else if (t == 0) {
-        float s = 0.0f;
+        float s = s0;
         for (int i = 0; i < T * E; i++) s = s + a_lds[i];
         sc.result = s;
     }

@@ -136,4 +136,16 @@ int launch_argmax_final(const float* part_val, const int32_t* part_idx, int N, i
 int launch_accept_greedy(const uint32_t* toks, const uint32_t* preds, int n, int32_t* d_pos, int32_t* result,
                          uint32_t* next_tok_slot, hipStream_t stream);
 
+// ---------------------------------------------------------------- stochastic acceptance
+// probs[r][j] = expf((l_j - max)/temp) * (1 / sum), the sum exact left to right (rows x V).
+int launch_temperature_probs(const float* logits, int64_t ld_in, float* probs, int64_t ld_out, int rows, int V,
+                             float temp, hipStream_t st);
+// p [k+1][ld] target probs, q [k][ld] draft probs, drafts[k] (device); result = {n_accepted,
+// next_token, start_pos + n_accepted + 1}; d_pos (nullable) receives the new position.
+int launch_accept_stochastic(const float* p, const float* q, int64_t ld, const uint32_t* drafts, int k, int V,
+                             uint64_t seed, int64_t start_pos, int32_t* result, int32_t* d_pos, hipStream_t st);
+// One fixed-point inverse-CDF sample of probs[V] with the Philox uniform (seed, pos, purpose).
+int launch_sample_probs(const float* probs, int V, uint64_t seed, int64_t pos, uint32_t purpose, uint32_t* out0,
+                        uint32_t* out1, hipStream_t st);
+
 }  // namespace nc

@@ -59,6 +59,8 @@ struct nc_session {
     float* q = nullptr;       // [B][aw]
     float* scores = nullptr;  // [B][H][ctx_stride]
     float* logits = nullptr;  // [B][V]
+    float* probs = nullptr;   // [B][V] temperature probabilities of the last pass's rows
+    float* qbuf = nullptr;    // [B][V] draft probabilities of the current speculative step
     float* part_val = nullptr;
     int32_t* part_idx = nullptr;
     uint32_t* d_toks = nullptr;
@@ -73,6 +75,7 @@ struct nc_session {
     int32_t* h_pos = nullptr;
     int last_n = 0;
     uint32_t staged[16] = {};
+    int n_staged = 0;  // staged tokens land in d_toks[0..n_staged); the rest stay as they are
     bool pending_toks = false;
     // per-kernel timing (HIP events on the session stream)
     bool timing = false;
@@ -544,7 +547,8 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
     if (n < 1 || n > s->max_batch) return fail(NC_ERANGE, "batch exceeds the session's max_batch");
     if (start_pos < 0 || start_pos + n > s->max_ctx) return fail(NC_ERANGE, "batch end exceeds the session context");
     hipStream_t st = s->stream;
-    int rc = launch_set_pass_state(s->d_pos, (int32_t)start_pos, s->d_toks, s->pending_toks ? s->staged : nullptr, n, st);
+    int rc = launch_set_pass_state(s->d_pos, (int32_t)start_pos, s->d_toks, s->pending_toks ? s->staged : nullptr,
+                                   s->pending_toks ? s->n_staged : 0, st);
     if (rc) return rc;
     s->pending_toks = false;
     rc = launch_embed(m->tok_emb, s->d_toks, n, d, s->hidden, st);
@@ -647,6 +651,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
 static int upload_toks(nc_session* s, const uint32_t* toks, int n) {
     if (n < 1 || n > 16) return fail(NC_ERANGE, "batch must be 1..16 tokens");
     std::memcpy(s->staged, toks, n * sizeof(uint32_t));
+    s->n_staged = n;
     s->pending_toks = true;
     return NC_OK;
 }
@@ -691,6 +696,28 @@ static int verify_step(nc_session* s, int n, int64_t start_pos, nc_verify_result
     r->n_accepted = s->h_result[0];
     r->next_token = (uint32_t)s->h_result[1];
     r->new_pos = s->h_result[2];
+    return NC_OK;
+}
+
+// Stochastic k+1 acceptance of the pass just run (rows 0..n-1 at start_pos): temperature
+// probabilities of every row, then the accept/resample kernel.  q: [n-1][V] draft probs.
+static int accept_stochastic_step(nc_session* s, int n, int64_t start_pos, const float* q, float temp, uint64_t seed) {
+    const int V = (int)s->m->cfg.vocab_size;
+    int rc = launch_temperature_probs(s->logits, V, s->probs, V, n, V, temp, s->stream);
+    if (rc) return rc;
+    return launch_accept_stochastic(s->probs, q, V, s->d_toks + 1, n - 1, V, seed, start_pos, s->d_result, s->d_pos,
+                                    s->stream);
+}
+
+static int fetch_result(nc_session* s, int n_toks, nc_verify_result* r, uint32_t* toks_out) {
+    NC_HIP(hipMemcpyAsync(s->h_result, s->d_result, 4 * sizeof(int32_t), hipMemcpyDeviceToHost, s->stream));
+    if (toks_out)
+        NC_HIP(hipMemcpyAsync(s->h_toks, s->d_toks, n_toks * sizeof(uint32_t), hipMemcpyDeviceToHost, s->stream));
+    NC_HIP(hipStreamSynchronize(s->stream));
+    r->n_accepted = s->h_result[0];
+    r->next_token = (uint32_t)s->h_result[1];
+    r->new_pos = s->h_result[2];
+    if (toks_out) std::memcpy(toks_out, s->h_toks, n_toks * sizeof(uint32_t));
     return NC_OK;
 }
 
@@ -820,6 +847,25 @@ int nc_rms_norm_q8_0_batch(nc_ctx* ctx, const float* x, const float* w, float ep
                              stream ? (hipStream_t)stream : ctx->stream);
 }
 
+int nc_temperature_probs_batch(nc_ctx* ctx, const float* logits, float* probs, int32_t rows, int64_t vocab, float temp,
+                               void* stream) {
+    if (!ctx || !logits || !probs || rows < 1 || vocab < 1 || vocab > INT32_MAX || !(temp > 0.0f))
+        return fail(NC_EINVAL, "nc_temperature_probs_batch: bad arguments");
+    NC_HIP(hipSetDevice(ctx->device));
+    return launch_temperature_probs(logits, vocab, probs, vocab, rows, (int)vocab, temp,
+                                    stream ? (hipStream_t)stream : ctx->stream);
+}
+
+int nc_stochastic_accept(nc_ctx* ctx, const float* p_probs, const float* q_probs, const uint32_t* drafts, int32_t k,
+                         int64_t vocab, uint64_t seed, int64_t start_pos, int32_t* result, void* stream) {
+    if (!ctx || !p_probs || !result || k < 0 || k > 15 || (k > 0 && (!q_probs || !drafts)) || vocab < 1 ||
+        vocab > INT32_MAX || start_pos < 0)
+        return fail(NC_EINVAL, "nc_stochastic_accept: bad arguments");
+    NC_HIP(hipSetDevice(ctx->device));
+    return launch_accept_stochastic(p_probs, q_probs, vocab, drafts, k, (int)vocab, seed, start_pos, result, nullptr,
+                                    stream ? (hipStream_t)stream : ctx->stream);
+}
+
 int nc_model_load_gguf_memory(nc_ctx* ctx, const void* data, size_t size, const nc_load_opts* opts, nc_model** out) {
     if (!ctx || !data || !out) return fail(NC_EINVAL, "nc_model_load_gguf_memory: null argument");
     NC_HIP(hipSetDevice(ctx->device));
@@ -889,6 +935,8 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
         (rc = dev_alloc(s->allocs, &s->q, B * c.attention_output_width)) ||
         (rc = dev_alloc(s->allocs, &s->scores, (size_t)B * c.head_count * s->ctx_stride)) ||
         (rc = dev_alloc(s->allocs, &s->logits, (size_t)B * c.vocab_size)) ||
+        (rc = dev_alloc(s->allocs, &s->probs, (size_t)B * c.vocab_size)) ||
+        (rc = dev_alloc(s->allocs, &s->qbuf, (size_t)B * c.vocab_size)) ||
         (rc = dev_alloc(s->allocs, &s->part_val, B * m->head.tiles)) ||
         (rc = dev_alloc(s->allocs, &s->part_idx, B * m->head.tiles)) ||
         (rc = dev_alloc(s->allocs, &s->d_toks, B)) || (rc = dev_alloc(s->allocs, &s->d_preds, B)) ||
@@ -957,6 +1005,18 @@ int nc_verify_greedy(nc_session* s, const uint32_t* toks, int32_t n, int64_t sta
     int rc = upload_toks(s, toks, n);
     if (rc || (rc = verify_step(s, n, start_pos, result))) return rc;
     if (preds_host && (rc = fetch_preds(s, n, preds_host))) return rc;
+    return flush_timing(s);
+}
+
+int nc_verify_stochastic(nc_session* s, const uint32_t* toks, int32_t n, int64_t start_pos, const float* q_probs,
+                         float temp, uint64_t seed, nc_verify_result* result) {
+    if (!s || !toks || !result || n < 1 || (n > 1 && !q_probs) || !(temp > 0.0f))
+        return fail(NC_EINVAL, "nc_verify_stochastic: bad arguments");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    int rc = upload_toks(s, toks, n);
+    if (rc || (rc = run_pass(s, n, start_pos)) || (rc = accept_stochastic_step(s, n, start_pos, q_probs, temp, seed)) ||
+        (rc = fetch_result(s, n, result, nullptr)))
+        return rc;
     return flush_timing(s);
 }
 
@@ -1092,6 +1152,80 @@ int nc_generate_speculative_draft(nc_session* tg, nc_session* dr, const uint32_t
         if (produced < n_new) out[produced++] = fix;
         if ((rc = nc_forward1(tg, fix, at, nullptr, &tlive)) || (rc = nc_forward1(dr, fix, at, nullptr, &dlive))) return rc;
         pos = at + 1;
+        steps++;
+    }
+    const double t2 = now_s();
+    if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};
+    return flush_timing(tg);
+}
+
+int nc_generate_speculative_stochastic(nc_session* tg, nc_session* dr, const uint32_t* prompt, int32_t n_prompt,
+                                       int32_t n_new, int32_t k, float temp, uint64_t seed, uint32_t* out,
+                                       nc_decode_stats* stats) {
+    if (!tg || !dr || tg == dr || !prompt || !out || n_prompt < 1 || n_new < 1 || k < 0 || !(temp > 0.0f))
+        return fail(NC_EINVAL, "nc_generate_speculative_stochastic: bad arguments");
+    if (tg->m->cfg.vocab_size != dr->m->cfg.vocab_size) return fail(NC_EINVAL, "target and draft vocabularies differ");
+    if (tg->ctx->device != dr->ctx->device) return fail(NC_EINVAL, "target and draft must share a device");
+    if (n_prompt >= tg->max_ctx || n_prompt >= dr->max_ctx) return fail(NC_ERANGE, "prompt fills the session context");
+    NC_HIP(hipSetDevice(tg->ctx->device));
+    const int V = (int)tg->m->cfg.vocab_size;
+    const double t0 = now_s();
+    int rc = prefill_chunks(dr, prompt, n_prompt, 0, nullptr);
+    if (rc || (rc = prefill_chunks(tg, prompt, n_prompt, 0, nullptr))) return rc;
+    NC_HIP(hipStreamSynchronize(dr->stream));
+    // The draft's kernels run on the target's stream for the decode loop: the draft samples
+    // feed the target's token buffer and probability rows without cross-stream waits.
+    struct StreamShare {
+        nc_session* d;
+        hipStream_t own;
+        ~StreamShare() { d->stream = own; }
+    } share{dr, dr->stream};
+    dr->stream = tg->stream;
+    hipStream_t st = tg->stream;
+    // first token: the target's last prompt row, u(seed, n_prompt - 1, bonus)
+    if ((rc = launch_temperature_probs(tg->logits + (size_t)(tg->last_n - 1) * V, V, tg->probs, V, 1, V, temp, st)) ||
+        (rc = launch_sample_probs(tg->probs, V, seed, n_prompt - 1, kPurposeBonus, (uint32_t*)(tg->d_result + 1),
+                                         nullptr, st)))
+        return rc;
+    NC_HIP(hipMemcpyAsync(tg->h_result, tg->d_result, 4 * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    NC_HIP(hipStreamSynchronize(st));
+    uint32_t pending = (uint32_t)tg->h_result[1];
+    const double t1 = now_s();
+    int64_t pos = n_prompt, dvalid = n_prompt, produced = 0, steps = 0, drafted = 0, accepted = 0;
+    uint32_t last_draft = 0, toks[16];
+    out[produced++] = pending;
+    while (produced < n_new) {
+        int64_t kk = std::min<int64_t>(k, tg->max_batch - 1);
+        kk = std::min<int64_t>(kk, tg->max_ctx - pos - 1);
+        kk = std::min<int64_t>(kk, dr->max_ctx - pos - 1);
+        if (kk < 0) break;
+        if (dvalid < pos) {  // full acceptance last step: the draft has not seen d_{k-1}
+            if ((rc = upload_toks(dr, &last_draft, 1)) || (rc = run_pass(dr, 1, dvalid))) return rc;
+            dvalid++;
+        }
+        // k draft forwards; draft i's sample becomes the next draft input and target row i+1
+        for (int64_t i = 0; i < kk; i++) {
+            if (i == 0 && (rc = upload_toks(dr, &pending, 1))) return rc;
+            if ((rc = run_pass(dr, 1, pos + i)) ||
+                (rc = launch_temperature_probs(dr->logits, V, tg->qbuf + (size_t)i * V, V, 1, V, temp, st)) ||
+                (rc = launch_sample_probs(tg->qbuf + (size_t)i * V, V, seed, pos + i, kPurposeDraft, tg->d_toks + 1 + i,
+                                          dr->d_toks, st)))
+                return rc;
+        }
+        if (kk > 0) dvalid = pos + kk;
+        // target verify of [pending, d_0 .. d_{kk-1}]: only row 0 comes from the host
+        nc_verify_result r;
+        if ((rc = upload_toks(tg, &pending, 1)) || (rc = run_pass(tg, (int)kk + 1, pos)) ||
+            (rc = accept_stochastic_step(tg, (int)kk + 1, pos, tg->qbuf, temp, seed)) ||
+            (rc = fetch_result(tg, (int)kk + 1, &r, toks)))
+            return rc;
+        drafted += kk;
+        accepted += r.n_accepted;
+        for (int i = 1; i <= r.n_accepted && produced < n_new; i++) out[produced++] = toks[i];
+        if (produced < n_new) out[produced++] = r.next_token;
+        if (kk > 0) last_draft = toks[kk];
+        pending = r.next_token;
+        pos = r.new_pos;
         steps++;
     }
     const double t2 = now_s();

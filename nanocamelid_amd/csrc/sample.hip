@@ -1,0 +1,242 @@
+// Stochastic speculative acceptance on the device.
+//
+// Temperature softmax over the vocabulary, the min(1, p/q) acceptance test and
+// fixed-point inverse-CDF sampling driven by Philox4x32-10 uniforms.  The reference has
+// no speculative sampler (its temperature path matches tokens, speculative.rs:403, and
+// samples with an LCG, inference.rs:4834-4883); this specification is the library's own:
+//
+//   probs     p_j = e_j * (1 / S),  e_j = expf((l_j - max) / T),  S = sum_j e_j taken left
+//             to right in f32 (the reference's softmax formula, inference.rs:3522-3540,
+//             4857-4862), evaluated exactly with the segmented parallel chain;
+//   uniforms  u = (philox(seed, position, purpose).x >> 8) / 2^24, counter = (position,
+//             purpose), key = seed;
+//   accept    draft x of row i (position start+i) iff u_accept * q_i(x) < p_i(x);
+//   sample    weights W_j = floor(w_j * 2^40) (exact integers), target =
+//             floor(k24 * sum W / 2^24), result = first j whose inclusive prefix of W
+//             exceeds target.  Integer prefix sums do not depend on evaluation order,
+//             so one workgroup scans the vocabulary in parallel.
+//
+// The CPU oracle restates the same specification; the tests compare the two bit for bit.
+#include <hip/hip_runtime.h>
+
+#include "gguf.h"
+#include "nc_chain.h"
+#include "nc_device.h"
+#include "nc_internal.h"
+
+namespace nc {
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): round multipliers 0xD2511F53 and
+// 0xCD9E8D57, Weyl key increments 0x9E3779B9 and 0xBB67AE85, ten rounds.  Returns word 0.
+__device__ inline uint32_t philox_word_dev(uint64_t seed, uint64_t pos, uint32_t purpose) {
+    uint32_t c0 = (uint32_t)pos, c1 = (uint32_t)(pos >> 32), c2 = purpose, c3 = 0;
+    uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+    for (int r = 0; r < 10; r++) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)p1;
+        c3 = (uint32_t)p0;
+        c0 = n0;
+        c2 = n2;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    return c0;
+}
+
+__device__ inline uint32_t philox_u24(uint64_t seed, int64_t pos, uint32_t purpose) {
+    return philox_word_dev(seed, (uint64_t)pos, purpose) >> 8;
+}
+
+__device__ inline uint64_t fixed_weight(float w) { return w > 0.0f ? (uint64_t)(w * 1099511627776.0f) : 0ull; }
+
+// ---------------------------------------------------------------- temperature softmax
+constexpr int kSmT = 1024;             // threads per row
+constexpr int kSmE = 16;               // chain terms per thread per segment
+constexpr int kSmSeg = kSmT * kSmE;    // terms per exact-chain segment
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// One workgroup per row: probs[row][j] = p_j for j < V.
+__global__ __launch_bounds__(kSmT) void temperature_probs_kernel(const float* logits, int64_t ld_in, float* probs,
+                                                                 int64_t ld_out, int V, float temp) {
+    __shared__ ChainScratch<kSmT> sc;
+    __shared__ __align__(16) float a_lds[kSmSeg];
+    __shared__ float wmax[kSmT / 64];
+    const float* l = logits + (size_t)blockIdx.x * ld_in;
+    float* out = probs + (size_t)blockIdx.x * ld_out;
+    const int t = threadIdx.x;
+    // max is independent of evaluation order (finite logits; +-0 give identical terms)
+    float mx = -INFINITY;
+    for (int i = t; i < V; i += kSmT) mx = fmaxf(mx, l[i]);
+    mx = wave_max(mx);
+    if ((t & 63) == 0) wmax[t >> 6] = mx;
+    __syncthreads();
+    mx = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kSmT / 64; w++) mx = fmaxf(mx, wmax[w]);
+    // S = sum e_j left to right, one exact segment of kSmSeg terms at a time
+    float sum = 0.0f;
+    for (int base = 0; base < V; base += kSmSeg) {
+        float a[kSmE];
+#pragma unroll
+        for (int j = 0; j < kSmE; j++) {
+            const int i = base + t * kSmE + j;
+            a[j] = i < V ? expf_glibc((l[i] - mx) / temp) : 0.0f;
+        }
+        sum = exact_chain_sum<kSmE, kSmT>(a, sc, a_lds, sum);
+    }
+    const float inv = 1.0f / sum;
+    for (int i = t; i < V; i += kSmT) out[i] = expf_glibc((l[i] - mx) / temp) * inv;
+}
+
+// ---------------------------------------------------------------- fixed-point sampler
+constexpr int kSpT = 1024;
+
+struct SampleScratch {
+    uint64_t wtot[kSpT / 64];
+    int found;
+};
+
+// Inclusive scan of a uint64 over the 64 lanes of a wave (shuffle based).
+__device__ inline uint64_t wave_incl_scan_u64(uint64_t v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t n = __shfl_up(v, o);
+        if (lane >= o) v += n;
+    }
+    return v;
+}
+
+// Weight of id i: residual max(0, p_i - q_i) when q is given, else p_i.
+__device__ inline uint64_t sample_weight(const float* p, const float* q, int i) {
+    if (q) {
+        const float d = p[i] - q[i];
+        return fixed_weight(d > 0.0f ? d : 0.0f);
+    }
+    return fixed_weight(p[i]);
+}
+
+// Every thread of the block calls it; returns the sampled id, or -1 when all weights are 0.
+// Thread t owns the contiguous ids [t*C, t*C + C).
+__device__ int sample_fixed_block(const float* p, const float* q, int V, uint32_t k24, SampleScratch& ss) {
+    const int t = threadIdx.x;
+    const int C = (V + kSpT - 1) / kSpT;
+    const int lo = min(t * C, V), hi = min(lo + C, V);
+    uint64_t mine = 0;
+    for (int i = lo; i < hi; i++) mine += sample_weight(p, q, i);
+    const uint64_t incl = wave_incl_scan_u64(mine);
+    if ((t & 63) == 63) ss.wtot[t >> 6] = incl;
+    if (t == 0) ss.found = -1;
+    __syncthreads();
+    uint64_t base = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kSpT / 64; w++) {
+        const uint64_t v = ss.wtot[w];
+        if (w < (t >> 6)) base += v;
+        total += v;
+    }
+    const uint64_t excl = base + incl - mine;
+    // target = floor(k24 * total / 2^24) < total, split so every product fits in 64 bits
+    const uint64_t target = (((uint64_t)k24 * (total >> 32)) << 8) + (((uint64_t)k24 * (total & 0xffffffffull)) >> 24);
+    if (total != 0 && excl <= target && target < excl + mine) {
+        uint64_t c = excl;
+        for (int i = lo; i < hi; i++) {
+            c += sample_weight(p, q, i);
+            if (c > target) {
+                ss.found = i;
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    const int r = ss.found;
+    __syncthreads();  // ss is reused by the caller's next call
+    return r;
+}
+
+// k+1 acceptance.  p: [k+1][ld] target probs of rows at start_pos .. start_pos+k; q: [k][ld]
+// draft probs; drafts[k].  result = {n_accepted, next_token, start_pos + n_accepted + 1}.
+__global__ __launch_bounds__(kSpT) void accept_stochastic_kernel(const float* p, const float* q, int64_t ld,
+                                                                 const uint32_t* drafts, int k, int V, uint64_t seed,
+                                                                 int64_t start_pos, int32_t* result, int32_t* d_pos) {
+    __shared__ SampleScratch ss;
+    __shared__ int s_a;
+    const int t = threadIdx.x;
+    if (t < 64) {
+        bool reject = false;
+        if (t < k) {
+            const uint32_t x = drafts[t];
+            const float u = (float)philox_u24(seed, start_pos + t, kPurposeAccept) * (1.0f / 16777216.0f);
+            // an id outside the vocabulary has no probability under p: rejected
+            reject = x >= (uint32_t)V || !(u * q[(size_t)t * ld + x] < p[(size_t)t * ld + x]);
+        }
+        const uint64_t m = __ballot(reject);
+        if (t == 0) s_a = m ? __ffsll((unsigned long long)m) - 1 : k;
+    }
+    __syncthreads();
+    const int a = s_a;
+    int next;
+    if (a < k) {
+        const uint32_t k24 = philox_u24(seed, start_pos + a, kPurposeResample);
+        const float* pa = p + (size_t)a * ld;
+        next = sample_fixed_block(pa, q + (size_t)a * ld, V, k24, ss);
+        if (next < 0) next = sample_fixed_block(pa, nullptr, V, k24, ss);
+    } else {
+        next = sample_fixed_block(p + (size_t)k * ld, nullptr, V, philox_u24(seed, start_pos + k, kPurposeBonus), ss);
+    }
+    if (t == 0) {
+        const int np = (int)(start_pos + a + 1);
+        result[0] = a;
+        result[1] = next;
+        result[2] = np;
+        if (d_pos) d_pos[0] = np;
+    }
+}
+
+// One sample from probs[V] with u(seed, pos, purpose); the id goes to out0 (and out1).
+__global__ __launch_bounds__(kSpT) void sample_probs_kernel(const float* probs, int V, uint64_t seed, int64_t pos,
+                                                            uint32_t purpose, uint32_t* out0, uint32_t* out1) {
+    __shared__ SampleScratch ss;
+    const int id = sample_fixed_block(probs, nullptr, V, philox_u24(seed, pos, purpose), ss);
+    if (threadIdx.x == 0) {
+        const uint32_t v = id < 0 ? 0u : (uint32_t)id;
+        out0[0] = v;
+        if (out1) out1[0] = v;
+    }
+}
+
+int launch_temperature_probs(const float* logits, int64_t ld_in, float* probs, int64_t ld_out, int rows, int V,
+                             float temp, hipStream_t st) {
+    if (rows < 1 || V < 1 || !(temp > 0.0f)) return fail(NC_EINVAL, "temperature probs: rows, vocab and temp must be > 0");
+    hipLaunchKernelGGL(temperature_probs_kernel, dim3(rows), dim3(kSmT), 0, st, logits, ld_in, probs, ld_out, V, temp);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+int launch_accept_stochastic(const float* p, const float* q, int64_t ld, const uint32_t* drafts, int k, int V,
+                             uint64_t seed, int64_t start_pos, int32_t* result, int32_t* d_pos, hipStream_t st) {
+    if (k < 0 || k > 63 || V < 1) return fail(NC_EINVAL, "stochastic accept: k must be 0..63");
+    hipLaunchKernelGGL(accept_stochastic_kernel, dim3(1), dim3(kSpT), 0, st, p, q, ld, drafts, k, V, seed, start_pos,
+                       result, d_pos);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+int launch_sample_probs(const float* probs, int V, uint64_t seed, int64_t pos, uint32_t purpose, uint32_t* out0,
+                        uint32_t* out1, hipStream_t st) {
+    if (V < 1) return fail(NC_EINVAL, "sample: vocab must be > 0");
+    hipLaunchKernelGGL(sample_probs_kernel, dim3(1), dim3(kSpT), 0, st, probs, V, seed, pos, purpose, out0, out1);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+}  // namespace nc

@@ -724,44 +724,133 @@ void or_temperature_probs(const float* logits, int64_t V, float temp, float* pro
     for (int64_t i = 0; i < V; i++) probs[i] *= inv;
 }
 
-uint32_t or_sample_inverse_cdf(const float* probs, int64_t V, float u) {
-    // inference.rs:4865-4872 style: r = u * total, subtract in id order, first r <= 0 wins.
-    float total = 0.0f;
-    for (int64_t i = 0; i < V; i++) total += probs[i];
-    float r = u * total;
-    int64_t last_pos = V - 1;
+// Fixed-point inverse CDF (this build's stochastic specification; the reference samples with
+// a sequential f32 walk, inference.rs:4865-4872, and has no speculative sampler).  Weights
+// W_j = floor(w_j * 2^40) are exact integers, so their prefix sums do not depend on the
+// summation order: the GPU evaluates the same sampler with a parallel scan.  With
+// total = sum W_j and u = k24 / 2^24, the sample is the first j whose inclusive prefix
+// exceeds target = floor(k24 * total / 2^24) (< total, so such a j exists and W_j > 0).
+// Returns false when every weight is zero.
+static inline uint64_t fixed_weight(float w) { return w > 0.0f ? (uint64_t)(w * 1099511627776.0f) : 0u; }
+
+static bool sample_fixed(const float* w, int64_t V, uint32_t k24, uint32_t* out) {
+    uint64_t total = 0;
+    for (int64_t i = 0; i < V; i++) total += fixed_weight(w[i]);
+    if (total == 0) return false;
+    const uint64_t th = total >> 32, tl = total & 0xffffffffu;
+    const uint64_t target = ((k24 * th) << 8) + ((k24 * tl) >> 24);
+    uint64_t c = 0;
     for (int64_t i = 0; i < V; i++) {
-        if (probs[i] > 0.0f) last_pos = i;
-        r -= probs[i];
-        if (r <= 0.0f && probs[i] > 0.0f) return (uint32_t)i;
+        c += fixed_weight(w[i]);
+        if (c > target) {
+            *out = (uint32_t)i;
+            return true;
+        }
     }
-    return (uint32_t)last_pos;
+    return false;  // unreachable: target < total
+}
+
+static uint32_t philox_u24(uint64_t seed, uint64_t pos, uint32_t purpose) { return philox_word(seed, pos, purpose) >> 8; }
+
+uint32_t or_sample_inverse_cdf(const float* probs, int64_t V, float u) {
+    uint32_t k24 = (uint32_t)((double)u * 16777216.0), out = 0;
+    if (k24 > 0xffffffu) k24 = 0xffffffu;
+    return sample_fixed(probs, V, k24, &out) ? out : 0u;
 }
 
 void or_stochastic_accept(const float* p_logits, const float* q_probs, const uint32_t* drafts,
                           int64_t k, int64_t V, float temp, uint64_t seed, int64_t start_pos,
                           int64_t* n_accepted, uint32_t* next_token) {
+    // Row i of the k+1 verify batch sits at position start_pos + i and scores draft i.
+    // Draft i is accepted iff u * q_i(x) < p_i(x) (probability min(1, p/q)); at the first
+    // rejection the next token is drawn from max(0, p_i - q_i) (from p_i if that residual
+    // has no fixed-point mass); after k acceptances the bonus token is drawn from p_k.
     std::vector<float> p(V), r(V);
     for (int64_t i = 0; i < k; i++) {
         or_temperature_probs(p_logits + i * V, V, temp, p.data());
         const float* q = q_probs + i * V;
-        uint32_t x = drafts[i];
-        float u = philox_uniform(seed, (uint64_t)(start_pos + i), PURPOSE_ACCEPT);
-        if (u * q[x] < p[x]) continue;  // accept with probability min(1, p/q)
+        const uint32_t x = drafts[i];
+        const float u = philox_uniform(seed, (uint64_t)(start_pos + i), PURPOSE_ACCEPT);
+        if (u * q[x] < p[x]) continue;
         for (int64_t j = 0; j < V; j++) {
-            float dlt = p[j] - q[j];
+            const float dlt = p[j] - q[j];
             r[j] = dlt > 0.0f ? dlt : 0.0f;
         }
-        float ur = philox_uniform(seed, (uint64_t)(start_pos + i), PURPOSE_RESAMPLE);
-        float tot = 0.0f;
-        for (int64_t j = 0; j < V; j++) tot += r[j];
+        const uint32_t k24 = philox_u24(seed, (uint64_t)(start_pos + i), PURPOSE_RESAMPLE);
+        uint32_t t = 0;
+        if (!sample_fixed(r.data(), V, k24, &t)) sample_fixed(p.data(), V, k24, &t);
         *n_accepted = i;
-        *next_token = tot > 0.0f ? or_sample_inverse_cdf(r.data(), V, ur) : or_sample_inverse_cdf(p.data(), V, ur);
+        *next_token = t;
         return;
     }
     or_temperature_probs(p_logits + k * V, V, temp, p.data());
+    uint32_t t = 0;
+    sample_fixed(p.data(), V, philox_u24(seed, (uint64_t)(start_pos + k), PURPOSE_BONUS), &t);
     *n_accepted = k;
-    *next_token = or_sample_inverse_cdf(p.data(), V, philox_uniform(seed, (uint64_t)(start_pos + k), PURPOSE_BONUS));
+    *next_token = t;
+}
+
+int64_t or_generate_speculative_stochastic(or_session* tg, or_session* dr, const uint32_t* prompt,
+                                           int64_t n_prompt, int64_t n_new, int64_t k, float temp,
+                                           uint64_t seed, int64_t prefill_batch, uint32_t* out,
+                                           int64_t* stats, int64_t* steps_out) {
+    // Draft-model speculative sampling in the k+1 form (no reference counterpart: the
+    // reference's temperature path matches tokens, speculative.rs:403).  Per step at
+    // position pos with the pending token t0: the draft runs t0, d_0, .., d_{k-2} at
+    // pos .. pos+k-1 and samples d_i from q_i = softmax(draft logits / T) with
+    // u(seed, pos+i, draft); the target verifies [t0, d_0 .. d_{k-1}] at pos .. pos+k;
+    // or_stochastic_accept decides.  After a full acceptance the draft first catches up
+    // on d_{k-1}.  The first token is drawn from the target's last prompt row with
+    // u(seed, n_prompt-1, bonus).
+    const int64_t V = tg->m->V;
+    prefill(dr, prompt, n_prompt, 0, std::min(prefill_batch, dr->max_batch));
+    prefill(tg, prompt, n_prompt - 1, 0, prefill_batch);
+    or_forward_pass(tg, prompt[n_prompt - 1], n_prompt - 1);
+    std::vector<float> p(V), q, lg;
+    or_temperature_probs(tg->logits.data(), V, temp, p.data());
+    uint32_t pending = 0;
+    sample_fixed(p.data(), V, philox_u24(seed, (uint64_t)(n_prompt - 1), PURPOSE_BONUS), &pending);
+    int64_t pos = n_prompt, dvalid = n_prompt, produced = 0, steps = 0;
+    uint32_t last_draft = 0;
+    stats[0] = stats[1] = 0;
+    out[produced++] = pending;
+    std::vector<uint32_t> batch;
+    while (produced < n_new) {
+        int64_t kk = std::min(k, tg->max_batch - 1);
+        kk = std::min(kk, tg->max_ctx - pos - 1);
+        kk = std::min(kk, dr->max_ctx - pos - 1);
+        if (kk < 0) break;
+        if (dvalid < pos) {  // full acceptance last step: the draft has not seen d_{k-1}
+            or_forward_pass(dr, last_draft, dvalid);
+            dvalid++;
+        }
+        batch.assign(1, pending);
+        q.resize((size_t)kk * V);
+        uint32_t x = pending;
+        for (int64_t i = 0; i < kk; i++) {
+            or_forward_pass(dr, x, pos + i);
+            or_temperature_probs(dr->logits.data(), V, temp, &q[(size_t)i * V]);
+            sample_fixed(&q[(size_t)i * V], V, philox_u24(seed, (uint64_t)(pos + i), PURPOSE_DRAFT), &x);
+            batch.push_back(x);
+        }
+        dvalid = pos + kk;
+        or_prefill_pass_batch(tg, batch.data(), kk + 1, pos);
+        lg.resize((size_t)(kk + 1) * V);
+        for (int64_t i = 0; i <= kk; i++) or_batch_row_logits(tg, i, &lg[(size_t)i * V]);
+        int64_t a = 0;
+        uint32_t next = 0;
+        or_stochastic_accept(lg.data(), q.data(), batch.data() + 1, kk, V, temp, seed, pos, &a, &next);
+        stats[0] += kk;
+        stats[1] += a;
+        for (int64_t i = 1; i <= a && produced < n_new; i++) out[produced++] = batch[i];
+        if (produced < n_new) out[produced++] = next;
+        if (kk > 0) last_draft = batch[kk];
+        pos += a + 1;
+        pending = next;
+        steps++;
+    }
+    if (steps_out) *steps_out = steps;
+    return produced;
 }
 
 }  // extern "C"

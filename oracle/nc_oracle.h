@@ -161,8 +161,17 @@ void or_stochastic_accept(const float* p_logits, const float* q_probs, const uin
                           int64_t* n_accepted, uint32_t* next_token);
 /* Softmax with temperature used by the stochastic spec: probs[V]. */
 void or_temperature_probs(const float* logits, int64_t V, float temp, float* probs);
-/* Inverse-CDF sample with uniform u over probs (sequential sum over ids). */
+/* Fixed-point inverse-CDF sample: weights W_j = floor(probs_j * 2^40), u = k24 / 2^24
+ * (k24 = floor(u * 2^24)); returns the first j whose inclusive prefix of W exceeds
+ * floor(k24 * sum(W) / 2^24); 0 when every weight is zero. */
 uint32_t or_sample_inverse_cdf(const float* probs, int64_t V, float u);
+/* Draft-model speculative sampling at temperature temp in the k+1 form (draft and
+ * target sessions share the vocabulary).  out[n_new]; stats[2] = drafted, accepted.
+ * Returns tokens written. */
+int64_t or_generate_speculative_stochastic(or_session* target, or_session* draft, const uint32_t* prompt,
+                                           int64_t n_prompt, int64_t n_new, int64_t k, float temp,
+                                           uint64_t seed, int64_t prefill_batch, uint32_t* out,
+                                           int64_t* stats, int64_t* steps_out);
 
 #ifdef __cplusplus
 }

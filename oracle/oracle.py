@@ -76,6 +76,7 @@ def lib():
         "or_verify_greedy": (None, [C.c_void_p, _u32p, _i64, _i64, _u32p, C.c_void_p, C.c_void_p]),
         "or_generate_greedy": (C.c_int, [C.c_void_p, _u32p, _i64, _i64, _i64, _u32p]),
         "or_generate_speculative_draft": (_i64, [C.c_void_p, C.c_void_p, _u32p, _i64, _i64, _i64, _i64, _u32p, _i64p, _i64p]),
+        "or_generate_speculative_stochastic": (_i64, [C.c_void_p, C.c_void_p, _u32p, _i64, _i64, _i64, C.c_float, C.c_uint64, _i64, _u32p, _i64p, _i64p]),
         "or_generate_speculative_oracle": (_i64, [C.c_void_p, _u32p, _i64, _i64, _i64, C.c_float, C.c_uint64, _u32p, _i64, _u32p, _i64p, _i64p]),
         "or_oracle_draft": (C.c_uint32, [C.c_uint64, _i64, C.c_float, _u32p, _i64, _i64, C.c_uint32]),
         "or_uniform_prompt": (None, [C.c_uint64, _i64, C.c_uint32, _u32p]),
@@ -359,4 +360,16 @@ def generate_speculative_draft(target: Session, draft: Session, prompt, n_new, d
     steps = np.zeros(1, np.int64)
     n = lib().or_generate_speculative_draft(target.h, draft.h, p, p.size, n_new, draft_k, prefill_batch,
                                             out, stats, steps)
+    return out[:n], int(stats[0]), int(stats[1]), int(steps[0])
+
+
+def generate_speculative_stochastic(target: Session, draft: Session, prompt, n_new, k, temp, seed, prefill_batch=16):
+    """Draft-model speculative sampling (k+1 form, Philox acceptance); returns
+    (tokens, drafted, accepted, steps)."""
+    p = _c(prompt, np.uint32)
+    out = np.zeros(n_new, np.uint32)
+    stats = np.zeros(2, np.int64)
+    steps = np.zeros(1, np.int64)
+    n = lib().or_generate_speculative_stochastic(target.h, draft.h, p, p.size, n_new, k, temp, seed, prefill_batch,
+                                                 out, stats, steps)
     return out[:n], int(stats[0]), int(stats[1]), int(steps[0])

@@ -1,0 +1,169 @@
+"""GPU parity of the stochastic (temperature) speculative path against the CPU oracle.
+
+The specification has no reference counterpart (the reference's temperature path matches
+tokens, speculative.rs:403); the oracle restates the library's own: temperature softmax
+with the reference's formula and a left-to-right f32 sum (inference.rs:3522-3540,
+4857-4862), Philox4x32-10 uniforms, min(1, p/q) acceptance and fixed-point inverse-CDF
+sampling.  Every probability must be bit-identical and every sampled token identical.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+TINY = dict(layers=2, embedding_length=256, head_count=4, head_count_kv=2, feed_forward_length=512, vocab_size=1000,
+            context_length=512, tied=1, norm_mode=1)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import nanocamelid_amd as nc
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    return nc.Context(0)
+
+
+def _rows(V, rng):
+    rows = {
+        "normal": rng.normal(0, 2, V),
+        "flat": np.zeros(V),                               # every term exactly 1
+        "peaked": np.concatenate([[40.0], rng.normal(0, 1, V - 1)]),
+        "wide": rng.normal(0, 30, V),                      # most terms underflow to 0
+        "ties": np.round(rng.normal(0, 1, V) * 4) / 4,     # many equal logits
+        "ramp": np.linspace(-20, 5, V),
+    }
+    return {k: v.astype(np.float32) for k, v in rows.items()}
+
+
+@pytest.mark.parametrize("V", [7, 1000, 16384, 128256])
+@pytest.mark.parametrize("temp", [1.0, 0.7, 2.5])
+def test_temperature_probs_bit_exact(ctx, V, temp):
+    import nanocamelid_amd as nc
+    rows = _rows(V, np.random.default_rng(V))
+    names = list(rows)
+    x = np.stack([rows[k] for k in names])
+    print(f"temperature probs V={V} T={temp}", flush=True)
+    got = nc.temperature_probs_batch(ctx, torch.from_numpy(x).cuda(), temp).cpu().numpy()
+    for r, name in enumerate(names):
+        ref = O.temperature_probs(x[r], temp)
+        assert np.array_equal(got[r].view(np.uint32), ref.view(np.uint32)), f"{name} V={V} T={temp}"
+
+
+def _accept_case(ctx, p_logits, q, drafts, temp, seed, start):
+    import nanocamelid_amd as nc
+    k = len(drafts)
+    pt = nc.temperature_probs_batch(ctx, torch.from_numpy(p_logits).cuda(), temp)
+    qt = torch.from_numpy(np.ascontiguousarray(q, np.float32)).cuda()
+    dt = torch.from_numpy(np.asarray(drafts, np.int32)).cuda()
+    a, nxt, newpos = nc.stochastic_accept(ctx, pt, qt, dt, seed, start)
+    oa, onxt = O.stochastic_accept(p_logits, q, np.asarray(drafts, np.uint32), temp, seed, start)
+    assert (a, nxt, newpos) == (oa, onxt, start + oa + 1), (seed, start)
+    return a
+
+
+@pytest.mark.parametrize("V", [1000, 128256])
+def test_stochastic_accept_matches_oracle(ctx, V):
+    rng = np.random.default_rng(V + 1)
+    seen = set()
+    for trial in range(12):
+        k = (0, 1, 4, 8)[trial % 4]
+        temp = (1.0, 0.8)[trial % 2]
+        p_logits = rng.normal(0, 2, (k + 1, V)).astype(np.float32)
+        # draft distribution: a perturbed copy of the target rows, drafts sampled from it
+        q_logits = p_logits[:k] + rng.normal(0, 1.0, (k, V)).astype(np.float32)
+        q = np.stack([O.temperature_probs(q_logits[i], temp) for i in range(k)]) if k else np.zeros((0, V), np.float32)
+        drafts = [O.sample_inverse_cdf(q[i], np.float32(rng.integers(0, 2**24) / 2**24)) for i in range(k)]
+        print(f"accept V={V} trial={trial} k={k}", flush=True)
+        seen.add(_accept_case(ctx, p_logits, q, drafts, temp, 1000 + trial, 50 + 7 * trial) == k)
+    assert seen == {True, False}  # both the bonus and the resample branch ran
+
+
+def test_stochastic_accept_edge_cases(ctx):
+    rng = np.random.default_rng(8)
+    V, k = 1000, 4
+    p_logits = rng.normal(0, 1, (k + 1, V)).astype(np.float32)
+    p = np.stack([O.temperature_probs(p_logits[i], 1.0) for i in range(k + 1)])
+    # q == p: every draft accepted, bonus sample from row k
+    drafts = [int(np.argmax(p[i])) for i in range(k)]
+    assert _accept_case(ctx, p_logits, p[:k], drafts, 1.0, 5, 10) == k
+    # q concentrated on a token p gives zero mass: rejected at row 0, resampled elsewhere
+    p0 = p_logits.copy()
+    p0[0, 7] = -1e30
+    q0 = np.zeros((k, V), np.float32)
+    q0[:, 7] = 1.0
+    assert _accept_case(ctx, p0, q0, [7] * k, 1.0, 5, 10) == 0
+    # q = p except q(x) = 2 p(x): the residual max(0, p - q) is empty, so a rejection
+    # resamples from p; find seeds (by the oracle) where row 0 rejects
+    q2 = p[:k].copy()
+    x = int(np.argmax(p[0]))
+    q2[0, x] = 2 * p[0, x]
+    hit = 0
+    for seed in range(40):
+        oa, _ = O.stochastic_accept(p_logits, q2, np.array([x] + [0] * (k - 1), np.uint32), 1.0, seed, 3)
+        if oa == 0:
+            assert _accept_case(ctx, p_logits, q2, [x] + [0] * (k - 1), 1.0, seed, 3) == 0
+            hit += 1
+    assert hit >= 3
+    # an id outside the vocabulary is rejected without reading past the rows
+    import nanocamelid_amd as nc
+    pt = nc.temperature_probs_batch(ctx, torch.from_numpy(p_logits).cuda(), 1.0)
+    a, nxt, _ = nc.stochastic_accept(ctx, pt, torch.from_numpy(p[:k]).cuda(),
+                                     torch.tensor([V + 5, 0, 0, 0], dtype=torch.int32, device="cuda"), 9, 0)
+    assert a == 0 and nxt < V
+
+
+def _models(ctx, spec, seed):
+    import nanocamelid_amd as nc
+    img = nc.synth_gguf(**spec, seed=seed)
+    return nc.Model(ctx, data=img), O.Model(data=img.tobytes(), nthreads=16)
+
+
+def test_verify_stochastic_session(ctx):
+    import nanocamelid_amd as nc
+    gm, om = _models(ctx, TINY, seed=12)
+    gs = nc.Session(gm, 256, 16)
+    os_ = O.Session(om, 256, 16)
+    rng = np.random.default_rng(2)
+    pos = 0
+    prompt = nc.uniform_prompt(3, 20, 1000)
+    gs.prefill_pass_batch(prompt, 0)
+    for i in range(0, 20, 16):  # the oracle's batch pass takes at most max_batch rows
+        os_.prefill_pass_batch(prompt[i:i + 16], i)
+    pos = 20
+    for step, k in enumerate((4, 2, 8, 0, 4)):
+        toks = nc.uniform_prompt(100 + step, k + 1, 1000)
+        q_logits = rng.normal(0, 2, (k, 1000)).astype(np.float32)
+        q = np.stack([O.temperature_probs(q_logits[i], 0.9) for i in range(k)]) if k else np.zeros((1, 1000), np.float32)
+        print(f"verify_stochastic step={step} k={k} pos={pos}", flush=True)
+        a, nxt, newpos = gs.verify_stochastic(toks, pos, torch.from_numpy(q).cuda(), 0.9, 42)
+        _, _, lg = os_.verify_greedy(toks, pos, want_logits=True)
+        oa, onxt = O.stochastic_accept(lg, q[:k], toks[1:], 0.9, 42, pos)
+        assert (a, nxt, newpos) == (oa, onxt, pos + oa + 1)
+        pos += k + 1
+
+
+def test_generate_speculative_stochastic(ctx):
+    import nanocamelid_amd as nc
+    gm, om = _models(ctx, TINY, seed=31)
+    dspec = dict(TINY, layers=1, feed_forward_length=256, head_count=2, head_count_kv=1)
+    dgm, dom = _models(ctx, dspec, seed=5)
+    prompt = nc.uniform_prompt(77, 24, 1000)
+    for k, temp, seed in ((4, 1.0, 7), (2, 0.6, 8), (8, 1.3, 9)):
+        print(f"stochastic stream k={k} T={temp}", flush=True)
+        g_out, st = nc.generate_speculative_stochastic(nc.Session(gm, 400, 16), nc.Session(dgm, 400, 16), prompt, 80,
+                                                       k, temp, seed)
+        o_out, drafted, accepted, steps = O.generate_speculative_stochastic(
+            O.Session(om, 400, 16), O.Session(dom, 400, 16), prompt, 80, k, temp, seed)
+        assert np.array_equal(g_out, o_out), (k, temp)
+        assert (st.drafted, st.accepted, st.steps) == (drafted, accepted, steps)
+        assert 0 < accepted < drafted
+    # draft identical to the target: every draft is accepted
+    g_out, st = nc.generate_speculative_stochastic(nc.Session(gm, 400, 16), nc.Session(gm, 400, 16), prompt, 60, 4,
+                                                   1.0, 3)
+    o_out, drafted, accepted, steps = O.generate_speculative_stochastic(O.Session(om, 400, 16), O.Session(om, 400, 16),
+                                                                        prompt, 60, 4, 1.0, 3)
+    assert np.array_equal(g_out, o_out)
+    assert st.accepted == st.drafted > 0

@@ -71,3 +71,23 @@ def test_q4_k_model_batch_equals_single(tmp_path):
     s = O.Session(m, 32, 1)
     for i, t in enumerate(toks):
         assert np.array_equal(s.forward_pass(t, i), logits[i])
+
+
+def test_stochastic_speculation(tiny):
+    img, m = tiny
+    prompt = nc.uniform_prompt(5, 16, 1000)
+    # draft identical to the target: q == p bit for bit, so every draft is accepted
+    out, drafted, accepted, steps = O.generate_speculative_stochastic(O.Session(m, 256, 16), O.Session(m, 256, 4),
+                                                                      prompt, 40, 4, 1.0, 77)
+    assert len(out) == 40 and accepted == drafted and drafted > 0
+    # a different draft model over the same vocabulary: deterministic, partial acceptance,
+    # and independent of how the prompt is chunked
+    dimg = nc.synth_gguf(layers=1, embedding_length=256, head_count=2, head_count_kv=1, feed_forward_length=256,
+                         vocab_size=1000, context_length=512, tied=1, seed=5)
+    dm = O.Model(data=dimg.tobytes())
+    a = O.generate_speculative_stochastic(O.Session(m, 256, 16), O.Session(dm, 256, 8), prompt, 40, 4, 1.0, 77)
+    b = O.generate_speculative_stochastic(O.Session(m, 256, 16), O.Session(dm, 256, 8), prompt, 40, 4, 1.0, 77,
+                                          prefill_batch=5)
+    assert np.array_equal(a[0], b[0]) and a[1:] == b[1:]
+    assert 0 < a[2] < a[1]
+    assert np.all(a[0] < 1000)

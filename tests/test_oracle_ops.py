@@ -136,6 +136,55 @@ def test_inverse_cdf_and_temperature_probs():
     assert np.allclose(pr, e / e.sum(), rtol=1e-6)
 
 
+def test_fixed_point_sampler_boundaries():
+    # weights 1:2:3:4 (exact in 2^-40 fixed point): u in [0, .1) -> 0, [.1, .3) -> 1,
+    # [.3, .6) -> 2, [.6, 1) -> 3; u = k/2^24 on either side of each boundary
+    w = np.array([1, 2, 3, 4], np.float32) / np.float32(16)
+    for lo, hi, idx in ((0.0, 0.1, 0), (0.1, 0.3, 1), (0.3, 0.6, 2), (0.6, 1.0, 3)):
+        first = int(np.ceil(lo * 2**24))
+        last = int(np.ceil(hi * 2**24)) - 1
+        assert O.sample_inverse_cdf(w, np.float32(first / 2**24)) == idx, (lo, idx)
+        assert O.sample_inverse_cdf(w, np.float32(last / 2**24)) == idx, (hi, idx)
+    # weights below 2^-40 carry no mass; zero-mass ids are never returned
+    w2 = np.array([1e-13, 0.5, 0.0, 1e-13, 0.5], np.float32)
+    got = {O.sample_inverse_cdf(w2, np.float32(k / 64)) for k in range(64)}
+    assert got == {1, 4}
+    # mass is additive: a distribution split across duplicated ids samples the same ranges
+    rng = np.random.default_rng(3)
+    v = rng.random(50).astype(np.float32)
+    v /= v.sum()
+    us = rng.integers(0, 2**24, 300) / 2**24
+    for u in us:
+        i = O.sample_inverse_cdf(v, np.float32(u))
+        assert v[i] > 0
+        cum = np.cumsum(np.floor(v.astype(np.float64) * 2**40))
+        # the chosen id's fixed-point interval contains u * total (integer arithmetic)
+        target = (int(u * 2**24) * int(cum[-1])) >> 24
+        assert (cum[i - 1] if i else 0) <= target < cum[i]
+
+
+def test_speculative_sampling_preserves_target_distribution():
+    # The defining property of speculative sampling: whatever the draft distribution q,
+    # the first emitted token (the draft if accepted, else the residual resample) is
+    # distributed as p.  Chi-square over 20000 seeds on a 6-token vocabulary.
+    from scipy.stats import chisquare
+    V, N = 6, 20000
+    p_logits = np.array([[0.3, -1.0, 1.2, 0.0, -0.4, 0.8], [0.0] * 6], np.float32)
+    q = O.temperature_probs(np.array([1.5, 0.2, -0.5, 0.9, 0.0, -1.2], np.float32), 1.0)[None, :]
+    p0 = O.temperature_probs(p_logits[0], 1.0).astype(np.float64)
+    rng = np.random.default_rng(11)
+    counts = np.zeros(V)
+    acc = 0
+    for s in range(N):
+        d = O.sample_inverse_cdf(q[0], np.float32(rng.integers(0, 2**24) / 2**24))
+        na, nt = O.stochastic_accept(p_logits, q, np.array([d], np.uint32), 1.0, s, 10)
+        counts[d if na == 1 else nt] += 1
+        acc += na
+    assert chisquare(counts, p0 / p0.sum() * N).pvalue > 1e-4
+    # acceptance rate = sum_x min(p, q)
+    assert abs(acc / N - np.minimum(p0, q[0]).sum()) < 0.02
+
+
 def test_stochastic_accept_invariants():
     rng = np.random.default_rng(4)
     V, k = 50, 4
