@@ -131,6 +131,88 @@ def run_gemm_sweep(args):
             m.close()
 
 
+def run_config3(args):
+    """Config 3: Llama-3.2-3B-shape Q4_K target (tied head requantised to Q4_0), Llama-3.2-1B-shape
+    Q4_0 draft, temperature 1.0, k=4, Philox min(1, p/q) acceptance, 4096-position context.
+    One timed call of the device decode loop after a short warmup call; prints one JSON line."""
+    import numpy as np
+    import torch
+
+    import nanocamelid_amd as nc
+    t0 = time.time()
+    timg = nc.synth_gguf(**nc.SYNTH_CONFIGS["llama-3.2-3b-q4k"], context_length=8192, seed=args.seed,
+                         nthreads=HOST_THREADS)
+    dimg = nc.synth_gguf(**nc.SYNTH_CONFIGS["llama-3.2-1b"], context_length=8192, seed=args.seed + 1,
+                         nthreads=HOST_THREADS)
+    log(f"synthetic target {timg.nbytes / 1e9:.2f} GB + draft {dimg.nbytes / 1e9:.2f} GB in {time.time() - t0:.1f}s")
+    ctx = nc.Context(0)
+    tm = nc.Model(ctx, data=timg, nthreads=HOST_THREADS)
+    dm = nc.Model(ctx, data=dimg, nthreads=HOST_THREADS)
+    V = tm.config["vocab_size"]
+    n_prompt, max_ctx = args.c3_prompt, 4096
+    n_new = min(args.c3_new, max_ctx - n_prompt - args.k - 2)
+    prompt = nc.uniform_prompt(args.seed, n_prompt, V)
+    temp = 1.0
+
+    def run(n, timing=False):
+        ts, ds = nc.Session(tm, max_ctx, 16), nc.Session(dm, max_ctx, 16)
+        ts.timing(timing)
+        out, st = nc.generate_speculative_stochastic(ts, ds, prompt, n, args.k, temp, args.seed)
+        gt = ts.gemm_timing() if timing else (0, 0.0, 0)
+        ts.close()
+        ds.close()
+        return out, st, gt
+
+    run(64)  # warmup
+    torch.cuda.synchronize()
+    out, st, _ = run(n_new)
+    tok = st.emitted - 1  # the first token comes from the prompt pass
+    tok_s = tok / st.decode_seconds
+    log(f"config 3: {st.steps} steps, {tok} tokens in {st.decode_seconds:.3f}s = {tok_s:.1f} tok/s, acceptance "
+        f"{st.accepted}/{st.drafted}, prefill {st.prefill_seconds:.2f}s")
+    _, _, (launches, gemm_ms, gemm_bytes) = run(min(n_new, 256), timing=True)
+    achieved = gemm_bytes / (gemm_ms / 1e3) / 1e9 if launches else 0.0
+    log(f"target gemm: {launches} launches, {gemm_ms / max(launches, 1) * 1e3:.2f} us avg -> {achieved:.0f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+        tmo, dmo = O.Model(data=timg.tobytes(), nthreads=HOST_THREADS), O.Model(data=dimg.tobytes(), nthreads=HOST_THREADS)
+        cp = prompt[:16]
+        tp = time.time()
+        O.generate_speculative_stochastic(O.Session(tmo, 256, 16), O.Session(dmo, 256, 16), cp, 1, args.k, temp, args.seed)
+        t_prefill = time.time() - tp
+        td = time.time()
+        o, drafted, accepted, nsteps = O.generate_speculative_stochastic(O.Session(tmo, 256, 16), O.Session(dmo, 256, 16),
+                                                                         cp, 1 + args.cpu_steps * (args.k + 1), args.k,
+                                                                         temp, args.seed)
+        t_dec = time.time() - td - t_prefill
+        cpu = {"value": round((len(o) - 1) / t_dec, 4), "unit": "tok/s", "cores": HOST_THREADS, "kind": "port",
+               "sample": f"same models on the host: 16-token prompt, {nsteps} stochastic steps (k={args.k}, T=1.0, "
+                         f"{len(o) - 1} tokens, {accepted}/{drafted} accepted) in {t_dec:.1f}s"}
+        log(f"cpu baseline: {cpu}")
+    line = {
+        "metric": "verified tok/s (config 3: Llama-3.2-3B-shape Q4_K target, 1B-shape Q4_0 draft, T=1.0, k=4, "
+                  "Philox acceptance)",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": int(st.steps), "warmup": 1,
+        "ms_per_step": round(st.decode_seconds / max(st.steps, 1) * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8 dot -> int32, f32 accumulate",
+        "data": "synthetic (random-init weights N(0,0.02) -> Q4_K / Q4_0, seeded uniform prompt)",
+        "config": {"workload": f"llama-3.2-3b-q4k target + llama-3.2-1b draft, stochastic speculative sampling k={args.k} "
+                               f"T=1.0, {n_prompt}-token prompt, {int(tok)} new tokens, 4096-position KV",
+                   "k": args.k, "temperature": temp, "prompt_tokens": n_prompt, "tokens_emitted": int(tok),
+                   "drafted": int(st.drafted), "accepted": int(st.accepted),
+                   "target_verify_weight_bytes": int(tm.config["verify_weight_bytes"]),
+                   "draft_weight_bytes": int(dm.config["verify_weight_bytes"])},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "target verify matmuls (gemm_q4_k_kernel layers + gemm_q4_0_kernel head)",
+                     "launches": int(launches), "avg_us": round(gemm_ms / max(launches, 1) * 1e3, 3),
+                     "avg_algorithmic_bytes": int(gemm_bytes // max(launches, 1))},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -146,6 +228,10 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gemm-sweep", action="store_true", help="config 1: isolated GEMM bandwidth table")
+    ap.add_argument("--config3", action="store_true",
+                    help="config 3: 3B Q4_K target + 1B Q4_0 draft, stochastic acceptance (T=1, k=4)")
+    ap.add_argument("--c3-prompt", type=int, default=3072)
+    ap.add_argument("--c3-new", type=int, default=768)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy (known HBM bytes) to scale rocprofv3 --pmc byte counters")
     args = ap.parse_args()
@@ -162,6 +248,9 @@ def main():
     assert torch.cuda.is_available(), "bench needs the MI355X"
     if args.gemm_sweep:
         run_gemm_sweep(args)
+        return
+    if args.config3:
+        run_config3(args)
         return
     spec = dict(nc.SYNTH_CONFIGS[args.config])
     t0 = time.time()
