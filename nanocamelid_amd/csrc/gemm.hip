@@ -692,7 +692,9 @@ constexpr int pick_u_k() {
 template <int NMAX, int S>
 int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     if (w.type == NC_TYPE_Q4_0) {
-        constexpr int D = 3;
+        // ring depth: one round ahead when K is split over waves (deeper rings measured slower:
+        // the extra loads issued up front delay every wave's first round), two for S = 1
+        constexpr int D = S == 1 ? 3 : 2;
         const size_t lds = S > 1 ? (size_t)2 * S * 4 * NMAX * 64 * sizeof(float) : 0;
         if (ev0)
             hipExtLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0,
@@ -712,12 +714,13 @@ int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
     return NC_OK;
 }
 
-// R16: S waves so that the chain threads (16 per token) fit; U = 2 quads per wave-round,
-// a ring of 3 rounds in flight.
+// R16: S waves so that the chain threads (16 per token) fit; U = 1 quad per wave-round and
+// one round in flight ahead of the one being computed (the fastest of the measured
+// S x U x D shapes on every layer matrix of the 8B model).
 template <int NMAX>
 int launch_r16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     constexpr int S = 8;  // two waves per SIMD hide each other's dependency latency
-    constexpr int U = 2, D = 4;
+    constexpr int U = 1, D = 2;
     const size_t lds = (size_t)2 * 4 * S * U * NMAX * 16 * sizeof(float);
     if (ev0)
         hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1,
