@@ -4,9 +4,9 @@
 // the head argmax reduction and greedy acceptance.
 //
 // Every f32 chain that the reference evaluates sequentially gives the same bits here:
-// the RMSNorm sum of squares goes through exact_chain_sum (a parallel evaluation that is
-// verified step by step against the sequential recurrence); each attention dot product,
-// the softmax denominator and the weighted V sum are evaluated in order.  The parallel
+// the RMSNorm sum of squares and the softmax denominator go through exact_chain_sum (a
+// parallel evaluation that is verified step by step against the sequential recurrence);
+// each attention dot product and the weighted V sum are evaluated in order.  The parallel
 // parts are the order-free ones (max, elementwise maps, integer sums, independent
 // rows/heads/positions).
 #include "nc_device.h"
@@ -30,10 +30,6 @@ __device__ __forceinline__ void store_q8_block(float y, int lane32, int8_t* q_ds
 }
 
 // ---------------------------------------------------------------- RMSNorm + Q8_0
-// rms_norm (inference.rs:697-706): sum += x*x sequentially, scale = 1/sqrt(sum/n + eps),
-// y = x*scale*w; then quantize_f32_to_q8_0 of y (inference.rs:3802-3808).  The sequential
-// sum is evaluated by exact_chain_sum (bit-identical to the left-to-right loop).  One
-// workgroup of 256 threads per row; thread t owns elements [t*E, t*E + E).
 // Q8_0 quantisation of a row held in LDS (quantize_f32_to_q8_0, inference.rs:1012-1029):
 // 8 lanes per 32-block, 4 values per lane, all blocks of the row in one pass.
 template <int T>
@@ -130,6 +126,10 @@ __device__ __forceinline__ void quantize_regs_q8(const float (&y)[E], int8_t* q_
     }
 }
 
+// rms_norm (inference.rs:697-706): sum += x*x sequentially, scale = 1/sqrt(sum/n + eps),
+// y = x*scale*w; then quantize_f32_to_q8_0 of y (inference.rs:3802-3808).  The sequential
+// sum is evaluated by exact_chain_sum (bit-identical to the left-to-right loop).  One
+// workgroup of T threads (256 or 1024) per row; thread t owns elements [t*E, t*E + E).
 template <int E, int T>
 __global__ __launch_bounds__(T) void rmsnorm_q8_kernel(const float* hidden, const float* weight, float eps,
                                                         int8_t* xq, float* xs, int32_t* xsum) {
