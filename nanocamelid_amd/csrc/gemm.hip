@@ -541,32 +541,42 @@ __device__ __forceinline__ uint32_t kbyte(uint32_t w0, uint32_t w1, uint32_t w2,
     return (w >> ((i & 3) * 8)) & 0xff;
 }
 
-template <int NMAX, int S, int U>
+template <int NMAX, int S, int D>
 __global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
-    constexpr int RB = S * U;
-    constexpr int TPW = (NMAX + S - 1) / S;
-    extern __shared__ float lds[];
+    constexpr int TPW = (NMAX + S - 1) / S;  // chain tokens per thread
+    extern __shared__ float lds[];           // [2][S][NMAX][64] super-block terms when S > 1
     const int tile = blockIdx.x;
     const int wave = wave_id_uniform();
     const int lane = threadIdx.x & 63;
     const int N = p.N;
     const int nsb = p.units;
     const int nb = nsb * 8;
-    const uint8_t* wt = p.w + (size_t)tile * nsb * kQ4KChunkBytes;
+    const uint8_t* wt = p.w + (size_t)tile * nsb * kQ4KChunkBytes + lane * 16;
     float acc[TPW];
 #pragma unroll
     for (int j = 0; j < TPW; j++) acc[j] = 0.0f;
-    const int nrounds = (nsb + RB - 1) / RB;
-    for (int r = 0; r < nrounds; r++) {
-        const int s0 = r * RB + wave * U;
+    // round r: wave w takes super-block r*S + w; a ring of D super-blocks (9 x 16 B per lane)
+    // is in flight.  Loads are unconditional with clamped indices (straight-line load code
+    // keeps the wait counts exact); a clamped super-block's term is never added.
+    const int nrounds = (nsb + S - 1) / S;
+    uint4 rw[D][9];
+#define NC_K_LOAD(R, SLOT)                                                                           \
+    do {                                                                                             \
+        const int sb_ = min(min((R), nrounds - 1) * S + wave, nsb - 1);                              \
+        const uint8_t* c_ = wt + (size_t)sb_ * kQ4KChunkBytes;                                       \
+        _Pragma("unroll") for (int i = 0; i < 9; i++) rw[SLOT][i] = *(const uint4*)(c_ + i * 1024); \
+    } while (0)
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int sb = s0 + u;
-            if (sb < nsb) {
-                const uint8_t* chunk = wt + (size_t)sb * kQ4KChunkBytes + lane * 16;
-                uint4 v[9];
+    for (int k = 0; k < D - 1; k++) NC_K_LOAD(k, k);
+    for (int r0 = 0; r0 < nrounds; r0 += D) {
 #pragma unroll
-                for (int i = 0; i < 9; i++) v[i] = *(const uint4*)(chunk + i * 1024);
+        for (int k = 0; k < D; k++) {
+            const int r = r0 + k;
+            NC_K_LOAD(r + D - 1, (k + D - 1) % D);
+            if (r < nrounds) {  // uniform
+                const int sb = r * S + wave;
+                const int sbc = min(sb, nsb - 1);
+                const uint4* v = rw[k];
                 const float d = f16_to_f32((uint16_t)(v[0].x & 0xffff));
                 const float dmin = f16_to_f32((uint16_t)(v[0].x >> 16));
                 float sc[8], mn[8];
@@ -584,52 +594,60 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
                     sc[j] = d * (float)s;
                     mn[j] = dmin * (float)m;
                 }
+                // every token of the instantiation, without branches (tokens >= N read clamped
+                // activations and are never stored)
+                float t[NMAX];
 #pragma unroll
                 for (int n = 0; n < NMAX; n++) {
-                    if (n < N) {
-                        sptr_i32 xw = as_scalar_i32(p.x + (size_t)n * p.K + (size_t)sb * 256);
-                        sptr_f32 xsp = as_scalar_f32(p.xs + (size_t)n * nb + (size_t)sb * 8);
-                        sptr_i32 xap = as_scalar_i32(p.xs8 + (size_t)n * nb + (size_t)sb * 8);
-                        float part = 0.0f;
+                    const int nn = min(n, N - 1);
+                    sptr_i32 xw = as_scalar_i32(p.x + (size_t)nn * p.K + (size_t)sbc * 256);
+                    sptr_f32 xsp = as_scalar_f32(p.xs + (size_t)nn * nb + (size_t)sbc * 8);
+                    sptr_i32 xap = as_scalar_i32(p.xs8 + (size_t)nn * nb + (size_t)sbc * 8);
+                    float part = 0.0f;
 #pragma unroll
-                        for (int pr = 0; pr < 4; pr++) {
-                            const uint4 q0 = v[1 + 2 * pr], q1 = v[2 + 2 * pr];
-                            const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-                            int wl = 0, wh = 0;
+                    for (int pr = 0; pr < 4; pr++) {
+                        const uint4 q0 = v[1 + 2 * pr], q1 = v[2 + 2 * pr];
+                        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                        int wl = 0, wh = 0;
 #pragma unroll
-                            for (int i = 0; i < 8; i++) {
-                                wl = dot4((int)(qw[i] & 0x0F0F0F0F), xw[pr * 16 + i], wl);
-                                wh = dot4((int)((qw[i] >> 4) & 0x0F0F0F0F), xw[pr * 16 + 8 + i], wh);
-                            }
-                            // q8.rs:1372-1375: sum += xs * (sc*W - mn*A), low then high half
-                            const int jl = 2 * pr, jh = 2 * pr + 1;
-                            part = part + xsp[jl] * (sc[jl] * (float)wl - mn[jl] * (float)(xap[jl] / -8));
-                            part = part + xsp[jh] * (sc[jh] * (float)wh - mn[jh] * (float)(xap[jh] / -8));
+                        for (int i = 0; i < 8; i++) {
+                            wl = dot4((int)(qw[i] & 0x0F0F0F0F), xw[pr * 16 + i], wl);
+                            wh = dot4((int)((qw[i] >> 4) & 0x0F0F0F0F), xw[pr * 16 + 8 + i], wh);
                         }
-                        if constexpr (S == 1) {
-                            acc[n] = acc[n] + part;
-                        } else {
-                            lds[((wave * U + u) * NMAX + n) * 64 + lane] = part;
+                        // q8.rs:1372-1375: sum += xs * (sc*W - mn*A), low then high half
+                        const int jl = 2 * pr, jh = 2 * pr + 1;
+                        part = part + xsp[jl] * (sc[jl] * (float)wl - mn[jl] * (float)(xap[jl] / -8));
+                        part = part + xsp[jh] * (sc[jh] * (float)wh - mn[jh] * (float)(xap[jh] / -8));
+                    }
+                    t[n] = part;
+                }
+                if constexpr (S == 1) {
+                    if (sb < nsb) {  // uniform
+#pragma unroll
+                        for (int n = 0; n < NMAX; n++) acc[n] = acc[n] + t[n];
+                    }
+                } else {
+                    // double-buffered terms: one barrier per round (round r+2 rewrites this
+                    // buffer only after every thread passed round r+1's barrier)
+                    float* buf = lds + (size_t)(r & 1) * S * NMAX * 64;
+#pragma unroll
+                    for (int n = 0; n < NMAX; n++) buf[(wave * NMAX + n) * 64 + lane] = t[n];
+                    __syncthreads();
+                    const int nblk = min(S, nsb - r * S);
+#pragma unroll
+                    for (int j = 0; j < TPW; j++) {
+                        const int n = wave + j * S;
+                        if (n < N) {
+                            float a = acc[j];
+                            for (int bl = 0; bl < nblk; bl++) a = a + buf[(bl * NMAX + n) * 64 + lane];
+                            acc[j] = a;
                         }
                     }
                 }
             }
         }
-        if constexpr (S > 1) {
-            __syncthreads();
-            const int nblk = min(RB, nsb - r * RB);
-#pragma unroll
-            for (int j = 0; j < TPW; j++) {
-                const int n = wave + j * S;
-                if (n < N) {
-                    float a = acc[j];
-                    for (int bl = 0; bl < nblk; bl++) a = a + lds[(bl * NMAX + n) * 64 + lane];
-                    acc[j] = a;
-                }
-            }
-            __syncthreads();
-        }
     }
+#undef NC_K_LOAD
     gemm_epilogue<NMAX, S>(p, acc, tile, wave, lane);
 }
 
@@ -681,34 +699,33 @@ __global__ void blockdots_q4_k_kernel(const uint8_t* w, int nsb, int M, int K, c
 // ---------------------------------------------------------------- dispatch
 namespace {
 
-template <int NMAX, int S>
-constexpr int pick_u_k() {
-    // Q4_K LDS terms: S*U*NMAX*64*4 bytes <= 64 KB, U <= 2 super-blocks per wave
-    return S == 1 ? 2 : (S * NMAX * 2 <= 256 ? 2 : 1);
-}
 
 // ev0/ev1 (optional): events stamped by the dispatch itself at kernel start and end
 // (hipExtLaunchKernelGGL), so their elapsed time is the kernel's own duration.
 template <int NMAX, int S>
 int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     if (w.type == NC_TYPE_Q4_0) {
-        // ring depth: one round ahead when K is split over waves (deeper rings measured slower:
-        // the extra loads issued up front delay every wave's first round), two for S = 1
-        constexpr int D = S == 1 ? 3 : 2;
-        const size_t lds = S > 1 ? (size_t)2 * S * 4 * NMAX * 64 * sizeof(float) : 0;
-        if (ev0)
-            hipExtLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0,
-                                  p);
-        else
-            hipLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+        if constexpr (S > 4) {
+            return fail(NC_EINVAL, "gemm: Q4_0 uses at most 4 K-split waves");
+        } else {
+            // ring depth: one round ahead when K is split over waves (deeper rings measured
+            // slower: the extra loads issued up front delay every wave's first round), two for S = 1
+            constexpr int D = S == 1 ? 3 : 2;
+            const size_t lds = S > 1 ? (size_t)2 * S * 4 * NMAX * 64 * sizeof(float) : 0;
+            if (ev0)
+                hipExtLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0,
+                                      ev1, 0, p);
+            else
+                hipLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+        }
     } else {
-        constexpr int U = pick_u_k<NMAX, S>();
-        const size_t lds = S > 1 ? (size_t)S * U * NMAX * 64 * sizeof(float) : 0;
+        constexpr int D = 2;  // one super-block ahead
+        const size_t lds = S > 1 ? (size_t)2 * S * NMAX * 64 * sizeof(float) : 0;
         if (ev0)
-            hipExtLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, U>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0,
+            hipExtLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0,
                                   p);
         else
-            hipLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, U>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+            hipLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
     }
     NC_HIP(hipGetLastError());
     return NC_OK;
@@ -737,6 +754,20 @@ int launch_s(int S, const QMatDev& w, const GemmParams& p, hipStream_t st, hipEv
         case 1: return launch_one<NMAX, 1>(w, p, st, ev0, ev1);
         case 2: return launch_one<NMAX, 2>(w, p, st, ev0, ev1);
         default: return launch_one<NMAX, 4>(w, p, st, ev0, ev1);
+    }
+}
+
+// Q4_K: more K-split waves than the Q4_0 path (a super-block is 9 KB per wave and the 3B/8B
+// Q4_K matrices have few 64-row tiles): 12 waves when K is 12 super-blocks (one round),
+// else 8, else 4.
+template <int NMAX>
+int launch_k(int S, const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    switch (S) {
+        case 1: return launch_one<NMAX, 1>(w, p, st, ev0, ev1);
+        case 2: return launch_one<NMAX, 2>(w, p, st, ev0, ev1);
+        case 4: return launch_one<NMAX, 4>(w, p, st, ev0, ev1);
+        case 8: return launch_one<NMAX, 8>(w, p, st, ev0, ev1);
+        default: return launch_one<NMAX, 12>(w, p, st, ev0, ev1);
     }
 }
 
@@ -777,6 +808,12 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent
     if (w.layout == LAYOUT_R16) {
         if (p.epi == EPI_SWIGLU_Q8) return fail(NC_EINVAL, "gemm: the SwiGLU epilogue needs the R64 layout");
         NC_GEMM_FOR_NMAX(launch_r16, p.N, w, p, st, ev0, ev1)
+    }
+    if (w.type == NC_TYPE_Q4_K) {
+        const int nsb = (int)w.units;
+        int S = nsb == 12 ? 12 : (nsb >= 8 ? 8 : 4);
+        if (w.tiles * S > 4096) S = pick_waves(w.tiles);
+        NC_GEMM_FOR_NMAX(launch_k, p.N, S, w, p, st, ev0, ev1)
     }
     int S = pick_waves(w.tiles);
     // NC_GEMM_WAVES=<1|2|4>: tuning override of the R64 K-split width

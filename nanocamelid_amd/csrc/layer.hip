@@ -335,17 +335,14 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(AttnParams a) {
 //   prob_p = e_p * (1/sum);  out[d] = ((0 + prob_0*v_0[d]) + prob_1*v_1[d]) + ... in order,
 //   one lane per output dim d, V rows streamed with a software-pipelined prefetch.
 // Thread t owns positions [t*E, t*E + E) of the score row (zeros past the row's end).
-template <int E, int T, int HD>
-__global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
-    __shared__ ChainScratch<T> sc;
-    __shared__ __align__(16) float probs[T * E];
-    __shared__ float red[T / 64];
-    const int unit = blockIdx.x;
-    const int n = unit / a.H, h = unit % a.H;
-    const int kvh = h / (a.H / a.Hkv);
-    const int L = a.d_pos[0] + n + 1;
+// softmax (inference.rs:3522-3540) of the score row srow[0 .. L): max, e = expf(s - max),
+// the sum of e left to right (exact_chain_sum), p = e * (1 / sum).  Thread t returns the
+// probabilities of positions t*E .. t*E + E - 1 (0 past L).  Every thread of the block calls
+// it; lds_terms: T*E floats used by the chain.
+template <int E, int T>
+__device__ __forceinline__ void softmax_row(const float* srow, int L, float (&pr)[E], ChainScratch<T>& sc,
+                                            float* lds_terms, float* red) {
     const int t = threadIdx.x;
-    const float* srow = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
     float sv[E];
 #pragma unroll
     for (int j = 0; j < E; j++) {
@@ -368,10 +365,27 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
     float e[E];
 #pragma unroll
     for (int j = 0; j < E; j++) e[j] = t * E + j < L ? expf_glibc(sv[j] - mx) : 0.0f;
-    const float sum = exact_chain_sum<E, T>(e, sc, probs);
+    const float sum = exact_chain_sum<E, T>(e, sc, lds_terms);
     const float inv = 1.0f / sum;
 #pragma unroll
-    for (int j = 0; j < E; j++) probs[t * E + j] = e[j] * inv;
+    for (int j = 0; j < E; j++) pr[j] = e[j] * inv;
+}
+
+template <int E, int T, int HD>
+__global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
+    __shared__ ChainScratch<T> sc;
+    __shared__ __align__(16) float probs[T * E];
+    __shared__ float red[T / 64];
+    const int unit = blockIdx.x;
+    const int n = unit / a.H, h = unit % a.H;
+    const int kvh = h / (a.H / a.Hkv);
+    const int L = a.d_pos[0] + n + 1;
+    const int t = threadIdx.x;
+    const float* srow = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
+    float pr[E];
+    softmax_row<E, T>(srow, L, pr, sc, probs, red);
+#pragma unroll
+    for (int j = 0; j < E; j++) probs[t * E + j] = pr[j];
     __syncthreads();
     if (t >= HD) return;  // no barriers below
     // Weighted V sum, lane = output dim t.  V is stored in position quads: one 16-byte load

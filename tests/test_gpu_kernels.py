@@ -126,6 +126,20 @@ def test_q4_k_bit_exact(ctx, N):
                 assert np.array_equal(dots[n, r, sb * 8:(sb + 1) * 8], W)
 
 
+@pytest.mark.parametrize("shape", [(130, 2048), (192, 3072), (64, 8192)], ids=["S8", "S12", "S8x4"])
+@pytest.mark.parametrize("N", [1, 5, 9, 16])
+def test_q4_k_wave_splits(ctx, shape, N):
+    """Q4_K K-split widths: 8 super-blocks (8 waves, one round), 12 (12 waves), 32 (8 waves,
+    four rounds), with a partial 64-row tile."""
+    import nanocamelid_amd as nc
+    M, K = shape
+    w = random_q4_k(M, K, seed=M + K + N)
+    _, xq, xs = q8_activations(N, K, seed=300 + N)
+    out, _ = _run_gemm(ctx, nc.NC_TYPE_Q4_K, w, M, K, xq, xs)
+    ref = O.matmul_q4_k(xq, xs, w, N, M, K, nthreads=16)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
 def test_quantize_q8_0_matches_oracle(ctx):
     import nanocamelid_amd as nc
     rng = np.random.default_rng(5)
