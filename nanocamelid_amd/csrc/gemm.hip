@@ -423,22 +423,31 @@ __device__ __forceinline__ void gemm_epilogue_r16(const GemmParams& p, float v, 
             break;
         }
         default:
-            break;  // EPI_SWIGLU_Q8 never uses R16 (interleaved gate/up stays R64)
+            break;  // EPI_SWIGLU_Q8: the four-tile variant finishes it in its own epilogue
     }
 }
 
-template <int NMAX, int S, int U, int D>
-__global__ __launch_bounds__(64 * S) void gemm_q4_0_r16_kernel(GemmParams p) {
+// TPG = 4: one workgroup covers four consecutive tiles (64 rows) with a group of S waves
+// each, sharing the per-round barrier; used for the interleaved gate,up matrix, whose 64-row
+// groups hold 32 gate rows and the 32 matching up rows, so that SwiGLU and the Q8_0
+// quantisation of the 32-wide output block finish inside the workgroup.
+template <int NMAX, int S, int U, int D, int TPG>
+__global__ __launch_bounds__(64 * S * TPG) void gemm_q4_0_r16_kernel(GemmParams p) {
     static_assert(16 * NMAX <= 64 * S, "chain threads must fit the workgroup");
     static_assert(U == 1 || U == 2 || U == 4, "quads per wave per round");
+    static_assert(TPG == 1 || TPG == 4, "tiles per workgroup");
     constexpr int QR = S * U;                // quads per round
     constexpr int BR = 4 * QR;               // blocks per round
     constexpr int NP = (NMAX + 1) / 2;       // token-pair activation dwords per block
     constexpr int NM = (NMAX + 7) / 8;       // meta dwords per block
     constexpr int SW = U == 4 ? 2 : 1;       // scale dwords per wave round
-    extern __shared__ float lds[];           // [2][BR][NMAX][16]
-    const int tile = blockIdx.x;
-    const int wave = wave_id_uniform();
+    extern __shared__ float lds_all[];       // per tile group: [2][BR][NMAX][16]
+    const int wave_all = wave_id_uniform();
+    const int sub = wave_all / S;            // tile of the group (TPG = 4)
+    const int wave = wave_all % S;
+    const int tile = blockIdx.x * TPG + sub;
+    float* lds = lds_all + (size_t)sub * 2 * BR * NMAX * 16;
+    const int tig = threadIdx.x - sub * 64 * S;  // thread index within the tile's group
     const int lane = threadIdx.x & 63;
     const int j = lane >> 4, i16 = lane & 15;
     const int N = p.N, nb = p.units;
@@ -486,7 +495,7 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_r16_kernel(GemmParams p) {
 #pragma unroll
     for (int k = 0; k < D - 1; k++) NC_R16_LOAD(k, k);
     float acc = 0.0f;
-    const int cn = threadIdx.x >> 4, cr = threadIdx.x & 15;  // chain thread: token, row
+    const int cn = tig >> 4, cr = tig & 15;  // chain thread: token, row
     for (int r0 = 0; r0 < nrounds; r0 += D) {
 #pragma unroll
         for (int k = 0; k < D; k++) {
@@ -513,7 +522,7 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_r16_kernel(GemmParams p) {
                     }
                 }
                 __syncthreads();
-                if (threadIdx.x < 16 * NMAX && cn < N) {
+                if (tig < 16 * NMAX && cn < N) {
                     const int nblk = min(BR, nb - r * BR);
                     const float* src = buf + cn * 16 + cr;
                     // groups of 16 terms read ahead of their dependent adds
@@ -531,7 +540,38 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_r16_kernel(GemmParams p) {
         }
     }
 #undef NC_R16_LOAD
-    if (threadIdx.x < 16 * NMAX && cn < N) gemm_epilogue_r16<NMAX>(p, acc, cn, tile, cr);
+    if constexpr (TPG == 1) {
+        if (tig < 16 * NMAX && cn < N) gemm_epilogue_r16<NMAX>(p, acc, cn, tile, cr);
+    } else {
+        // EPI_SWIGLU_Q8 over the group's 64 rows: rows 0-31 gate, 32-63 up of output block
+        // blockIdx.x (fused_silu_mul inference.rs:3367-3390, then quantize_f32_to_q8_0 of the
+        // 32-wide block, inference.rs:4034-4041); the same expressions as the 64-row kernel.
+        float* outv = lds_all;  // [64 rows][NMAX]
+        __syncthreads();        // every chain has read its last round's terms
+        if (tig < 16 * NMAX && cn < N) outv[(sub * 16 + cr) * NMAX + cn] = acc;
+        __syncthreads();
+        const int lane = threadIdx.x & 63;
+        const int n = wave_all;  // one wave per token, lanes 0-31 = the 32 outputs
+        if (n < N) {
+            const int l = lane & 31;
+            const float g = outv[l * NMAX + n];
+            const float up = outv[(32 + l) * NMAX + n];
+            const float sig = 1.0f / (1.0f + expf_glibc(-g));
+            const float y = g * sig * up;
+            const float amax = halfwave_amax(y);
+            float scale;
+            const int q = quantize_lane_q8(y, amax, &scale);
+            const int qs = halfwave_isum(q);
+            if (lane < 32) {
+                const int blk = blockIdx.x;
+                p.xq_out[(size_t)n * p.F + blk * 32 + lane] = (int8_t)q;
+                if (lane == 0) {
+                    p.xs_out[(size_t)n * (p.F / 32) + blk] = scale;
+                    p.xs8_out[(size_t)n * (p.F / 32) + blk] = -8 * qs;
+                }
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------- Q4_K
@@ -736,14 +776,28 @@ int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
 // S x U x D shapes on every layer matrix of the 8B model).
 template <int NMAX>
 int launch_r16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
-    constexpr int S = 8;  // two waves per SIMD hide each other's dependency latency
     constexpr int U = 1, D = 2;
-    const size_t lds = (size_t)2 * 4 * S * U * NMAX * 16 * sizeof(float);
-    if (ev0)
-        hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1,
-                              0, p);
-    else
-        hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+    if (p.epi == EPI_SWIGLU_Q8) {
+        // four 16-row tiles per workgroup, 4 waves each (the fastest 16-row shape measured on
+        // the 28672 x 4096 gate,up matrix)
+        constexpr int S = 4, TPG = 4;
+        if (p.ntiles % TPG) return fail(NC_EINVAL, "gemm: SwiGLU rows must fill whole 64-row groups");
+        const size_t lds = (size_t)TPG * 2 * 4 * S * U * NMAX * 16 * sizeof(float);
+        if (ev0)
+            hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, TPG>), dim3(p.ntiles / TPG),
+                                  dim3(64 * S * TPG), lds, st, ev0, ev1, 0, p);
+        else
+            hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, TPG>), dim3(p.ntiles / TPG), dim3(64 * S * TPG),
+                               lds, st, p);
+    } else {
+        constexpr int S = 8;  // two waves per SIMD hide each other's dependency latency
+        const size_t lds = (size_t)2 * 4 * S * U * NMAX * 16 * sizeof(float);
+        if (ev0)
+            hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1>), dim3(p.ntiles), dim3(64 * S), lds, st,
+                                  ev0, ev1, 0, p);
+        else
+            hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+    }
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
@@ -806,7 +860,6 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent
     p.K = (int)w.cols;
     if (p.N < 1 || p.N > 16) return fail(NC_EINVAL, "gemm: batch must be 1..16");
     if (w.layout == LAYOUT_R16) {
-        if (p.epi == EPI_SWIGLU_Q8) return fail(NC_EINVAL, "gemm: the SwiGLU epilogue needs the R64 layout");
         NC_GEMM_FOR_NMAX(launch_r16, p.N, w, p, st, ev0, ev1)
     }
     if (w.type == NC_TYPE_Q4_K) {

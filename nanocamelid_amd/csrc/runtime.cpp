@@ -146,11 +146,11 @@ int64_t q40_r16_layout_bytes(int64_t rows, int64_t cols) {
 }
 
 void repack_q4_0_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups,
-                     int64_t row_off) {
+                     int64_t row_off, int half) {
     const int64_t nb = cols / 32;
     parallel_for(rows_src, 0, [&](int64_t lo, int64_t hi) {
         for (int64_t r = lo; r < hi; r++) {
-            const int64_t R = row_off + r;
+            const int64_t R = dst_row(r, row_off, half);
             const int64_t t = R / 16, rr = R % 16;
             for (int64_t b = 0; b < nb; b++) {
                 const uint8_t* blk = src + (r * nb + b) * 18;
@@ -193,11 +193,10 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
     out.type = type;
     out.rows = rows;
     out.cols = cols;
-    // R16 for Q4_0 matrices too small to fill the chip with 64-row tiles (an interleaved
-    // gate/up pair keeps R64: its SwiGLU epilogue pairs lanes within a 64-row tile)
-    bool interleaved = false;
-    for (const auto& p : parts) interleaved = interleaved || p.half >= 0;
-    out.layout = type == NC_TYPE_Q4_0 && !interleaved && (rows + 63) / 64 < 512 ? LAYOUT_R16 : LAYOUT_R64;
+    // R16 for Q4_0 matrices too small to fill the chip with 64-row tiles.  An interleaved
+    // gate/up pair keeps its 64-row groups (gate rows 32t.. in rows 0-31 of group t, up rows in
+    // 32-63): with R16 those are four consecutive 16-row tiles, which one workgroup covers.
+    out.layout = type == NC_TYPE_Q4_0 && (rows + 63) / 64 < 512 ? LAYOUT_R16 : LAYOUT_R64;
     out.units = type == NC_TYPE_Q4_0 ? cols / 32 : cols / 256;
     if (out.layout == LAYOUT_R16) {
         out.tiles = (rows + 15) / 16;
@@ -211,7 +210,7 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
     out.algo_bytes = type == NC_TYPE_Q4_0 ? rows * cols / 32 * 18 : rows * cols / 256 * 144;
     std::vector<uint8_t> host(out.dev_bytes, 0);
     for (const auto& p : parts) {
-        if (out.layout == LAYOUT_R16) repack_q4_0_r16(p.src, p.rows, cols, host.data(), out.groups, p.row_off);
+        if (out.layout == LAYOUT_R16) repack_q4_0_r16(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
         else if (type == NC_TYPE_Q4_0) repack_q4_0(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
         else repack_q4_k(p.src, p.rows, cols, host.data(), p.row_off, p.half);
     }
