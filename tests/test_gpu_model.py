@@ -108,6 +108,33 @@ def test_q4_k_model_logits(ctx):
             assert _same(gs.logits(i), ologits[i])
 
 
+@pytest.mark.parametrize("hd,checks", [(128, (2045, 4093)), (64, (8190,))], ids=["hd128-4k", "hd64-8k"])
+def test_long_context_logits(ctx, hd, checks):
+    """Verify logits bit-exact at long contexts: 5-row passes that straddle the softmax
+    instantiation boundaries at 2048, 4096 and 8192 positions (the 8192 one switches the
+    softmax to 512 threads)."""
+    import nanocamelid_amd as nc
+    upto = checks[-1] + 5
+    spec = dict(layers=1, embedding_length=2 * hd * 2, head_count=4, head_count_kv=2, feed_forward_length=512,
+                vocab_size=1000, context_length=upto + 64, tied=1, norm_mode=1)
+    _, gm, om = _models(ctx, spec, seed=hd)
+    prompt = nc.uniform_prompt(hd, upto, 1000)
+    gs, os_ = nc.Session(gm, upto + 16, 16), O.Session(om, upto + 16, 16)
+    pos = 0
+    for c in checks:
+        print(f"long context hd={hd}: prefill to {c}, verify 5 rows", flush=True)
+        gs.prefill_pass_batch(prompt[pos:c], pos)
+        for i in range(pos, c, 16):
+            os_.prefill_pass_batch(prompt[i:min(i + 16, c)], i)
+        batch = nc.uniform_prompt(c, 5, 1000)
+        _, _, _, preds = gs.verify_greedy(batch, c)
+        opreds, _, ologits = os_.verify_greedy(batch, c, want_logits=True)
+        assert np.array_equal(preds, opreds)
+        for i in range(5):
+            assert _same(gs.logits(i), ologits[i]), (c, i)
+        pos = c
+
+
 @pytest.mark.slow
 def test_config0_plumbing_run(ctx):
     """Config 0: Llama-3.2-1B shape, tied Q4_0 head, 32-token seeded prompt, greedy, k=4,
