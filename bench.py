@@ -95,6 +95,10 @@ def _q4_0_random_blocks(M, K, seed):
 
 
 def run_gemm_sweep(args):
+    """Config 1: per-shape median kernel time (dispatch-stamped events around each of >= 60
+    back-to-back launches) rotating >= 1 GB of distinct weight copies."""
+    import ctypes as C
+
     import numpy as np
     import torch
 
@@ -109,23 +113,22 @@ def run_gemm_sweep(args):
         copies = max(2, int(np.ceil(1.0e9 / wbytes)))
         mats = [nc.QMat(ctx, nc.NC_TYPE_Q4_0, M, K, blocks) for _ in range(copies)]
         res = {"shape": f"{M}x{K}", "role": name, "weight_bytes": wbytes, "copies": copies}
+        handles = (C.c_void_p * copies)(*[m.h for m in mats])
         for N in (1, 2, 5, 9, 16):
             rng = np.random.default_rng(N)
             xq = torch.from_numpy(rng.integers(-127, 128, (N, K), dtype=np.int8)).cuda()
             xs = torch.from_numpy(rng.uniform(0.005, 0.02, (N, K // 32)).astype(np.float32)).cuda()
             out = torch.empty((N, M), dtype=torch.float32, device="cuda")
-            for i in range(copies):
-                nc.matmul_quantized_batch(ctx, mats[i], xq, xs, out)
-            iters = max(50, copies * 4)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for i in range(iters):
-                nc.matmul_quantized_batch(ctx, mats[i % copies], xq, xs, out)
-            e1.record(stream)
             torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / iters
+            iters = max(60, 2 * copies)
+            us = np.zeros(copies + iters, np.float32)
+            # the first round over the copies is warmup; the median is over the next iters launches
+            nc.check(nc.lib().nc_bench_matmul(ctx.h, handles, copies, xq.data_ptr(), xs.data_ptr(), out.data_ptr(), N,
+                                              copies + iters, us.ctypes.data))
+            med = float(np.median(us[copies:]))
             algo = wbytes + N * K + 4 * N * (K // 32) + 4 * N * M
-            res[f"N{N}"] = {"us": round(us, 2), "GBps": round(algo / us / 1e3, 1)}
+            res[f"N{N}"] = {"us_median": round(med, 2), "GBps": round(algo / med / 1e3, 1),
+                            "us_mean": round(float(np.mean(us[copies:])), 2)}
         print(json.dumps(res), flush=True)
         for m in mats:
             m.close()

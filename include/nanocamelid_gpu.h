@@ -255,6 +255,14 @@ int nc_synth_size(const nc_synth_spec* spec, uint64_t* size_out);
  * Deterministic for a given spec regardless of nthreads. */
 int nc_synth_write(const nc_synth_spec* spec, void* dst, uint64_t size, int32_t nthreads);
 
+/* Benchmark helper (config 1; no reference counterpart): launches the quantized matmul
+ * `iters` times back to back on the context stream, round robin over `ncopies` weight copies
+ * of one shape (so the weights stream from HBM, not the 256 MB last-level cache), each launch
+ * bracketed by events stamped by its own dispatch; us_out[iters] receives every launch's kernel
+ * duration in microseconds.  Device pointers as nc_matmul_quantized_batch. */
+int nc_bench_matmul(nc_ctx* ctx, const nc_qmat* const* w, int32_t ncopies, const int8_t* x_i8, const float* x_scales,
+                    float* out, int32_t batch_size, int32_t iters, float* us_out);
+
 /* Philox4x32-10 helpers shared by the drafter and the synthetic prompt.
  * ids[i] = philox(seed, i, purpose 4).x mod vocab. */
 int nc_uniform_prompt(uint64_t seed, int64_t n, uint32_t vocab, uint32_t* ids);

@@ -67,6 +67,7 @@ SIGNATURES = {
     "nc_matmul_blockdots": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _vp]),
     "nc_quantize_q8_0_batch": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _vp]),
     "nc_rms_norm_q8_0_batch": (C.c_int, [_vp, _vp, _vp, C.c_float, _vp, _vp, C.c_int, _i64, _vp]),
+    "nc_bench_matmul": (C.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _vp]),
     "nc_temperature_probs_batch": (C.c_int, [_vp, _vp, _vp, _i32, _i64, C.c_float, _vp]),
     "nc_stochastic_accept": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _i64, C.c_uint64, _i64, _vp, _vp]),
     "nc_model_load_gguf": (C.c_int, [_vp, C.c_char_p, C.POINTER(LoadOpts), C.POINTER(_vp)]),

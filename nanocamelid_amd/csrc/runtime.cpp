@@ -818,6 +818,40 @@ int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8,
     return launch_gemm(w->m, p, st);
 }
 
+int nc_bench_matmul(nc_ctx* ctx, const nc_qmat* const* w, int32_t ncopies, const int8_t* x_i8, const float* x_scales,
+                    float* out, int32_t batch_size, int32_t iters, float* us_out) {
+    if (!ctx || !w || ncopies < 1 || !x_i8 || !x_scales || !out || !us_out || iters < 1)
+        return fail(NC_EINVAL, "nc_bench_matmul: bad arguments");
+    if (batch_size < 1 || batch_size > 16) return fail(NC_EINVAL, "nc_bench_matmul: batch must be 1..16");
+    for (int i = 0; i < ncopies; i++)
+        if (!w[i] || w[i]->m.rows != w[0]->m.rows || w[i]->m.cols != w[0]->m.cols)
+            return fail(NC_EINVAL, "nc_bench_matmul: weight copies differ in shape");
+    NC_HIP(hipSetDevice(ctx->device));
+    hipStream_t st = ctx->stream;
+    const int64_t cols = w[0]->m.cols, rows = w[0]->m.rows;
+    int rc = ensure_xsum(ctx, (size_t)batch_size * (cols / 32));
+    if (rc || (rc = launch_block_sums(x_i8, batch_size, (int)cols, ctx->xsum, st))) return rc;
+    GemmParams p;
+    p.x = x_i8;
+    p.xs = x_scales;
+    p.xs8 = ctx->xsum;
+    p.N = batch_size;
+    p.epi = EPI_STORE;
+    p.out = out;
+    p.ld_out = (int)rows;
+    std::vector<hipEvent_t> ev(2 * (size_t)iters, nullptr);
+    for (auto& e : ev) NC_HIP(hipEventCreate(&e));
+    for (int i = 0; i < iters && !rc; i++) rc = launch_gemm(w[i % ncopies]->m, p, st, ev[2 * i], ev[2 * i + 1]);
+    if (!rc && hipStreamSynchronize(st) != hipSuccess) rc = fail(NC_EHIP, "nc_bench_matmul: stream failed");
+    for (int i = 0; i < iters && !rc; i++) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]) != hipSuccess) rc = fail(NC_EHIP, "nc_bench_matmul: event");
+        us_out[i] = ms * 1000.0f;
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    return rc;
+}
+
 int nc_matmul_blockdots(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, int32_t* dots, int batch_size, int64_t rows,
                         int64_t cols, void* stream) {
     if (!ctx || !w || !x_i8 || !dots) return fail(NC_EINVAL, "nc_matmul_blockdots: null argument");
