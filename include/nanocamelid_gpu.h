@@ -215,6 +215,24 @@ int nc_generate_speculative_oracle(nc_session* s, const uint32_t* prompt, int32_
                                    const uint32_t* greedy, int32_t n_greedy, uint32_t* out,
                                    nc_decode_stats* stats);
 
+/* Prompt-lookup drafting, NGramDrafter::draft (src/speculative.rs:81-103): the longest
+ * suffix n-gram of history (max_ngram down to min_ngram; the reference defaults are 4 and 3)
+ * with an earlier occurrence, most recent occurrence first, proposes the tokens that followed
+ * it: at most max_tokens, never past the end of the history.  Writes them to out and returns
+ * how many (0: no proposal).  Host only; needs no device. */
+int32_t nc_ngram_draft(const uint32_t* history, int64_t len, int32_t min_ngram, int32_t max_ngram, int32_t max_tokens,
+                       uint32_t* out);
+
+/* n-gram speculative decode, greedy: ngram_speculative_step (src/speculative.rs:122-286)
+ * in the k+1 verify form (src/bin/cluster_tcp_smoke.rs:905-979).  Each step verifies the
+ * pending token plus up to k drafts that nc_ngram_draft proposes from prompt + emitted
+ * tokens; no proposal means a one-row pass.  The emitted stream is the target's greedy
+ * stream, cut before the first of the n_stop stop tokens (a stop token is neither emitted
+ * nor consumed).  stats->emitted (<= n_new) is the number of tokens written to out. */
+int nc_generate_speculative_ngram(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new, int32_t k,
+                                  int32_t min_ngram, int32_t max_ngram, const uint32_t* stop, int32_t n_stop,
+                                  uint32_t* out, nc_decode_stats* stats);
+
 /* Draft-model speculative decode, greedy, as speculative_decoding_step
  * (src/speculative.rs:299-494) driven by the generate loop (src/main.rs:9799-9870):
  * k draft forwards, one k-row target verify, acceptance against the live target

@@ -252,6 +252,18 @@ class Session:
                                                    out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
         return out[:st.emitted], st
 
+    def generate_speculative_ngram(self, prompt, n_new: int, k: int, min_ngram: int = 3, max_ngram: int = 4,
+                                   stop=()):
+        """ngram_speculative_step (speculative.rs:122-286), greedy, k+1 verify form; returns
+        (tokens, stats).  The stream ends before the first stop token."""
+        a, p = _u32(prompt)
+        so, sp = _u32(np.asarray(stop, np.uint32).reshape(-1) if len(stop) else np.zeros(1, np.uint32))
+        out = np.zeros(n_new, np.uint32)
+        st = DecodeStats()
+        check(lib().nc_generate_speculative_ngram(self.h, p, a.size, n_new, k, min_ngram, max_ngram, sp, len(stop),
+                                                  out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
+        return out[:st.emitted], st
+
     def timing(self, enable: bool):
         check(lib().nc_session_timing_enable(self.h, 1 if enable else 0))
 
@@ -323,6 +335,15 @@ def uniform_prompt(seed: int, n: int, vocab: int) -> np.ndarray:
     out = np.zeros(n, np.uint32)
     check(lib().nc_uniform_prompt(seed, n, vocab, out.ctypes.data_as(C.POINTER(C.c_uint32))))
     return out
+
+
+def ngram_draft(history, max_tokens: int, min_ngram: int = 3, max_ngram: int = 4):
+    """NGramDrafter::draft (speculative.rs:81-103); defaults as NGramDrafter::default."""
+    h, hp = _u32(history if len(history) else np.zeros(1, np.uint32))
+    out = np.zeros(max(int(max_tokens), 1), np.uint32)
+    n = lib().nc_ngram_draft(hp, len(history), min_ngram, max_ngram, max_tokens,
+                             out.ctypes.data_as(C.POINTER(C.c_uint32)))
+    return out[:n]
 
 
 def oracle_draft(seed: int, p: int, alpha: float, greedy, n_prompt: int, vocab: int) -> int:

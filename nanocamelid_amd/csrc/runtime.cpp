@@ -1,6 +1,7 @@
 // Host runtime of libnanocamelid_hip: device context, weight repacking and upload,
 // the Llama model loader, sessions (KV cache + workspaces + stream), the verify pass,
 // the decode loops and the C ABI declared in include/nanocamelid_gpu.h.
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstring>
@@ -1129,6 +1130,80 @@ int nc_generate_speculative_oracle(nc_session* s, const uint32_t* prompt, int32_
         if (produced < n_new) out[produced++] = pending;
         pos = r.new_pos;
         steps++;
+    }
+    const double t2 = now_s();
+    if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};
+    return flush_timing(s);
+}
+
+int32_t nc_ngram_draft(const uint32_t* history, int64_t len, int32_t min_ngram, int32_t max_ngram, int32_t max_tokens,
+                       uint32_t* out) {
+    // NGramDrafter::draft (speculative.rs:81-103): the longest suffix n-gram, max_ngram down
+    // to min_ngram, that occurred earlier in the history (the most recent earlier occurrence
+    // wins) proposes the tokens that followed it, at most max_tokens and never past the end.
+    if (max_tokens <= 0 || min_ngram <= 0 || len <= min_ngram || !history || !out) return 0;
+    const int64_t max_n = std::min<int64_t>(max_ngram, len - 1);
+    for (int64_t n = max_n; n >= min_ngram; n--) {
+        const uint32_t* pat = history + len - n;
+        for (int64_t start = len - n - 1; start >= 0; start--) {
+            if (!std::equal(pat, pat + n, history + start)) continue;
+            const int64_t from = start + n, to = std::min<int64_t>(from + max_tokens, len);
+            std::copy(history + from, history + to, out);
+            return (int32_t)(to - from);  // from < len, so at least one token
+        }
+    }
+    return 0;
+}
+
+int nc_generate_speculative_ngram(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new, int32_t k,
+                                  int32_t min_ngram, int32_t max_ngram, const uint32_t* stop, int32_t n_stop,
+                                  uint32_t* out, nc_decode_stats* stats) {
+    if (!s || !prompt || !out || n_prompt < 1 || n_new < 1 || k < 0 || min_ngram < 1 || max_ngram < min_ngram ||
+        n_stop < 0 || (n_stop > 0 && !stop))
+        return fail(NC_EINVAL, "nc_generate_speculative_ngram: bad arguments");
+    if (n_prompt >= s->max_ctx) return fail(NC_ERANGE, "prompt fills the session context");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    auto is_stop = [&](uint32_t t) { return std::find(stop, stop + n_stop, t) != stop + n_stop; };
+    const double t0 = now_s();
+    uint32_t pending;
+    int rc = prefill_chunks(s, prompt, n_prompt, 0, &pending);
+    if (rc) return rc;
+    const double t1 = now_s();
+    // ngram_speculative_step (speculative.rs:122-286) in the k+1 verify form
+    // (cluster_tcp_smoke.rs:905-979): [pending] + drafts from the history ending in pending;
+    // accepted = matching prefix; next pending = pred[accepted].  The emitted stream is the
+    // target's greedy stream cut before the first stop token (never emitted nor consumed).
+    std::vector<uint32_t> history(prompt, prompt + n_prompt);
+    history.reserve((size_t)n_prompt + n_new);
+    int64_t pos = n_prompt, produced = 0, steps = 0, drafted = 0, accepted = 0;
+    uint32_t batch[16];
+    while (produced < n_new && !is_stop(pending)) {
+        out[produced++] = pending;
+        history.push_back(pending);
+        if (produced >= n_new || pos + 1 >= s->max_ctx) break;
+        int64_t kk = std::min<int64_t>(k, s->max_batch - 1);
+        kk = std::min<int64_t>(kk, s->max_ctx - pos - 1);
+        batch[0] = pending;
+        const int nd = kk > 0 ? nc_ngram_draft(history.data(), (int64_t)history.size(), min_ngram, max_ngram, (int)kk,
+                                               batch + 1)
+                              : 0;
+        nc_verify_result r;
+        if ((rc = upload_toks(s, batch, nd + 1)) || (rc = verify_step(s, nd + 1, pos, &r))) return rc;
+        drafted += nd;
+        accepted += r.n_accepted;
+        bool stopped = false;
+        for (int i = 1; i <= r.n_accepted && produced < n_new; i++) {
+            if (is_stop(batch[i])) {
+                stopped = true;
+                break;
+            }
+            out[produced++] = batch[i];
+            history.push_back(batch[i]);
+        }
+        pending = r.next_token;
+        pos = r.new_pos;
+        steps++;
+        if (stopped) break;
     }
     const double t2 = now_s();
     if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};

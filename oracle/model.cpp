@@ -709,6 +709,81 @@ int64_t or_generate_speculative_oracle(or_session* s, const uint32_t* prompt, in
     return produced;
 }
 
+int64_t or_ngram_draft(const uint32_t* history, int64_t len, int64_t min_ngram, int64_t max_ngram,
+                       int64_t max_tokens, uint32_t* out) {
+    // NGramDrafter::draft (speculative.rs:81-103): longest suffix n-gram (max_ngram down to
+    // min_ngram) with an earlier occurrence, most recent occurrence first; propose what
+    // followed it, at most max_tokens and never past the end of the history.
+    if (max_tokens <= 0 || min_ngram <= 0 || len <= min_ngram) return 0;
+    const int64_t max_n = std::min(max_ngram, len - 1);
+    for (int64_t n = max_n; n >= min_ngram; n--) {
+        const uint32_t* pat = history + len - n;
+        for (int64_t start = len - n - 1; start >= 0; start--) {
+            if (std::equal(pat, pat + n, history + start)) {
+                const int64_t cs = start + n, ce = std::min(cs + max_tokens, len);
+                if (cs < ce) {
+                    std::copy(history + cs, history + ce, out);
+                    return ce - cs;
+                }
+                break;
+            }
+        }
+    }
+    return 0;
+}
+
+int64_t or_generate_speculative_ngram(or_session* s, const uint32_t* prompt, int64_t n_prompt, int64_t n_new,
+                                      int64_t k, int64_t min_ngram, int64_t max_ngram, const uint32_t* stop,
+                                      int64_t n_stop, int64_t prefill_batch, uint32_t* out, int64_t* stats,
+                                      int64_t* steps_out) {
+    // ngram_speculative_step (speculative.rs:122-286) in the k+1 verify form
+    // (cluster_tcp_smoke.rs:905-979): each step verifies [pending] + drafts drawn from the
+    // history that ends with pending; the emitted stream is the target's greedy stream,
+    // cut before the first stop token (stop tokens are neither emitted nor consumed).
+    const int64_t V = s->m->V;
+    auto is_stop = [&](uint32_t t) { return std::find(stop, stop + n_stop, t) != stop + n_stop; };
+    prefill(s, prompt, n_prompt - 1, 0, prefill_batch);
+    or_forward_pass(s, prompt[n_prompt - 1], n_prompt - 1);
+    uint32_t pending = (uint32_t)or_argmax(s->logits.data(), V);
+    std::vector<uint32_t> history(prompt, prompt + n_prompt), batch, preds, drafts(std::max<int64_t>(k, 1));
+    int64_t pos = n_prompt, produced = 0, steps = 0;
+    stats[0] = stats[1] = 0;
+    bool stopped = false;
+    while (produced < n_new && !stopped) {
+        if (is_stop(pending)) break;
+        out[produced++] = pending;
+        history.push_back(pending);
+        if (produced >= n_new) break;
+        int64_t kk = std::min(k, s->max_batch - 1);
+        kk = std::min(kk, s->max_ctx - pos - 1);
+        if (kk < 0) break;
+        const int64_t nd = kk > 0 ? or_ngram_draft(history.data(), (int64_t)history.size(), min_ngram, max_ngram,
+                                                   kk, drafts.data())
+                                  : 0;
+        batch.assign(1, pending);
+        batch.insert(batch.end(), drafts.begin(), drafts.begin() + nd);
+        preds.resize(nd + 1);
+        or_verify_greedy(s, batch.data(), nd + 1, pos, preds.data(), nullptr, nullptr);
+        int64_t a = 0;
+        while (a < nd && batch[a + 1] == preds[a]) a++;
+        stats[0] += nd;
+        stats[1] += a;
+        for (int64_t i = 1; i <= a && produced < n_new; i++) {
+            if (is_stop(batch[i])) {
+                stopped = true;
+                break;
+            }
+            out[produced++] = batch[i];
+            history.push_back(batch[i]);
+        }
+        pending = preds[a];
+        pos += a + 1;
+        steps++;
+    }
+    if (steps_out) *steps_out = steps;
+    return produced;
+}
+
 void or_temperature_probs(const float* logits, int64_t V, float temp, float* probs) {
     // Max, exp((l - max) / T) (as inference.rs:4857-4862), sequential sum, then the
     // softmax normalisation (inference.rs:3535-3539): p = e * (1 / sum).

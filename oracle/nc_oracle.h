@@ -146,6 +146,18 @@ int64_t or_generate_speculative_oracle(or_session* target, const uint32_t* promp
                                        const uint32_t* greedy, int64_t prefill_batch,
                                        uint32_t* out, int64_t* stats, int64_t* steps_out);
 
+/* NGramDrafter::draft (speculative.rs:81-103): writes up to max_tokens proposals to out,
+ * returns how many. */
+int64_t or_ngram_draft(const uint32_t* history, int64_t len, int64_t min_ngram, int64_t max_ngram,
+                       int64_t max_tokens, uint32_t* out);
+/* n-gram prompt-lookup speculation (speculative.rs:122-286) in the k+1 verify form; the
+ * stream stops before the first of the n_stop stop tokens.  stats[2] = drafted, accepted.
+ * Returns tokens written (<= n_new). */
+int64_t or_generate_speculative_ngram(or_session* target, const uint32_t* prompt, int64_t n_prompt,
+                                      int64_t n_new, int64_t k, int64_t min_ngram, int64_t max_ngram,
+                                      const uint32_t* stop, int64_t n_stop, int64_t prefill_batch,
+                                      uint32_t* out, int64_t* stats, int64_t* steps_out);
+
 /* Oracle-drafter proposal for absolute position p (shared spec with the product). */
 uint32_t or_oracle_draft(uint64_t seed, int64_t p, float alpha, const uint32_t* greedy,
                          int64_t n_prompt, int64_t n_greedy, uint32_t vocab);

@@ -79,6 +79,9 @@ def lib():
         "or_generate_speculative_stochastic": (_i64, [C.c_void_p, C.c_void_p, _u32p, _i64, _i64, _i64, C.c_float, C.c_uint64, _i64, _u32p, _i64p, _i64p]),
         "or_generate_speculative_oracle": (_i64, [C.c_void_p, _u32p, _i64, _i64, _i64, C.c_float, C.c_uint64, _u32p, _i64, _u32p, _i64p, _i64p]),
         "or_oracle_draft": (C.c_uint32, [C.c_uint64, _i64, C.c_float, _u32p, _i64, _i64, C.c_uint32]),
+        "or_ngram_draft": (_i64, [_u32p, _i64, _i64, _i64, _i64, _u32p]),
+        "or_generate_speculative_ngram": (_i64, [C.c_void_p, _u32p, _i64, _i64, _i64, _i64, _i64, _u32p, _i64, _i64,
+                                                 _u32p, _i64p, _i64p]),
         "or_uniform_prompt": (None, [C.c_uint64, _i64, C.c_uint32, _u32p]),
         "or_stochastic_accept": (None, [_f32p, _f32p, _u32p, _i64, _i64, C.c_float, C.c_uint64, _i64, C.POINTER(_i64), C.POINTER(C.c_uint32)]),
         "or_temperature_probs": (None, [_f32p, _i64, C.c_float, _f32p]),
@@ -227,6 +230,14 @@ def oracle_draft(seed, p, alpha, greedy, n_prompt, vocab):
     return lib().or_oracle_draft(seed, p, alpha, g, n_prompt, g.size, vocab)
 
 
+def ngram_draft(history, max_tokens, min_ngram=3, max_ngram=4):
+    """NGramDrafter::draft (speculative.rs:81-103); defaults as NGramDrafter::default."""
+    h = _c(history, np.uint32)
+    out = np.zeros(max(int(max_tokens), 1), np.uint32)
+    n = lib().or_ngram_draft(h, h.size, min_ngram, max_ngram, max_tokens, out)
+    return out[:n]
+
+
 def temperature_probs(logits, temp):
     logits = _c(logits, np.float32)
     out = np.zeros_like(logits)
@@ -339,6 +350,16 @@ class Session:
         steps = np.zeros(1, np.int64)
         n = lib().or_generate_speculative_oracle(self.h, p, p.size, n_new, k, alpha, seed,
                                                  _c(greedy, np.uint32), prefill_batch, out, stats, steps)
+        return out[:n], int(stats[0]), int(stats[1]), int(steps[0])
+
+    def generate_speculative_ngram(self, prompt, n_new, k, min_ngram=3, max_ngram=4, stop=(), prefill_batch=16):
+        p = _c(prompt, np.uint32)
+        st = _c(np.asarray(stop, np.uint32).reshape(-1) if len(stop) else np.zeros(1, np.uint32), np.uint32)
+        out = np.zeros(n_new, np.uint32)
+        stats = np.zeros(2, np.int64)
+        steps = np.zeros(1, np.int64)
+        n = lib().or_generate_speculative_ngram(self.h, p, p.size, n_new, k, min_ngram, max_ngram, st, len(stop),
+                                                prefill_batch, out, stats, steps)
         return out[:n], int(stats[0]), int(stats[1]), int(steps[0])
 
     def close(self):

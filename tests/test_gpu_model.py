@@ -83,6 +83,28 @@ def test_greedy_and_speculative_streams(ctx):
         assert (st.drafted, st.accepted, st.steps) == (drafted, accepted, steps)
 
 
+def test_ngram_speculation_streams(ctx):
+    # ngram_speculative_step (speculative.rs:122-286), k+1 form: same stream, drafts, acceptances
+    # and steps as the oracle; the stream is the greedy stream cut before the first stop token
+    import nanocamelid_amd as nc
+    _, gm, om = _models(ctx, TINY, seed=21)
+    base = nc.uniform_prompt(9, 6, 1000)
+    prompt = np.concatenate([base, base, base, nc.uniform_prompt(10, 4, 1000), base[:4]]).astype(np.uint32)
+    ref = O.Session(om, 256, 16).generate_greedy(prompt, 64)
+    for k, mn, mx in ((1, 3, 4), (4, 3, 4), (8, 2, 5), (15, 3, 4)):
+        print(f"ngram k={k} n={mn}..{mx}", flush=True)
+        g_out, st = nc.Session(gm, 256, 16).generate_speculative_ngram(prompt, 64, k, mn, mx)
+        o_out, drafted, accepted, steps = O.Session(om, 256, 16).generate_speculative_ngram(prompt, 64, k, mn, mx)
+        assert np.array_equal(g_out, ref) and np.array_equal(o_out, ref), k
+        assert (st.drafted, st.accepted, st.steps) == (drafted, accepted, steps), k
+        assert drafted > 0 and accepted > 0
+    stop = [int(ref[20]), 999999]
+    g_out, _ = nc.Session(gm, 256, 16).generate_speculative_ngram(prompt, 64, 4, stop=stop)
+    o_out, _, _, _ = O.Session(om, 256, 16).generate_speculative_ngram(prompt, 64, 4, stop=stop)
+    assert np.array_equal(g_out, o_out)
+    assert np.array_equal(g_out, ref[:int(np.where(ref == ref[20])[0][0])])
+
+
 def test_draft_model_speculation(ctx):
     import nanocamelid_amd as nc
     _, gm, om = _models(ctx, TINY, seed=32)
