@@ -453,41 +453,68 @@ __global__ __launch_bounds__(64 * S * TPG) void gemm_q4_0_r16_kernel(GemmParams 
     const int N = p.N, nb = p.units;
     const int nq = (nb + 3) / 4;
     const uint8_t* wt = p.w + (size_t)tile * p.groups * kQ40ChunkBytes;
-    const int* xbase = (const int*)p.x + (i16 & 7);
     const int xtok = i16 >> 3, mtok = i16 & 7;
-    const int* mbase = i16 >= 8 ? p.xs8 : (const int*)p.xs;
     const int nrounds = (nq + QR - 1) / QR;
 
     uint4 rw[D][U];
     uint32_t rs[D][SW];
     int rx[D][U][NP], rm[D][U][NM];
-    // Unconditional, clamped loads (see the R64 kernel): exact wait counts across the ring.
+    // Unconditional loads (see the R64 kernel): exact wait counts across the ring.  Weights
+    // and activations are buffer loads.  The weight chunk offset is wave-uniform (scalar) and
+    // clamped to the padded groups; activations (and block scales on the buffer path) take a
+    // per-lane 32-bit offset that is range-checked against the real [N][K] / [N][K/32]
+    // extents, so a token past N or a block past the last row reads 0 instead of being
+    // clamped (those terms are never added).
     const int qmax = 8 * p.groups - U;  // last wave-round start inside the padded groups (U | 8)
+    const __amdgpu_buffer_rsrc_t wres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)wt, 0, p.groups * kQ40ChunkBytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, 0, N * p.K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs, 0, N * nb * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t s8res = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs8, 0, N * nb * 4, 0x00020000);
+    const int wvo = lane * 16;
+    int xvo[NP], mvo[NM], mt[NM];
+#pragma unroll
+    for (int q = 0; q < NP; q++) xvo[q] = (2 * q + xtok) * p.K + 32 * j + 4 * (i16 & 7);
+#pragma unroll
+    for (int q = 0; q < NM; q++) {
+        mvo[q] = ((8 * q + mtok) * nb + j) * 4;
+        mt[q] = min(8 * q + mtok, N - 1);
+    }
+    // Block scales: lanes 0-7 of a row take xs, lanes 8-15 xs8.  For 3..8 rows two buffer
+    // loads and a select measured faster than one load through a per-lane pointer; for
+    // other widths the single clamped load is faster.
+    constexpr bool kMetaBuf = NMAX >= 3 && NMAX <= 8;
+    const bool meta_s = i16 < 8;
+    const int* mbase = meta_s ? (const int*)p.xs : p.xs8;
 #define NC_R16_LOAD(R, SLOT)                                                                         \
     do {                                                                                             \
         const int qd0_ = min(min((R), nrounds - 1) * QR + wave * U, qmax);                           \
-        const uint8_t* chunk_ = wt + (size_t)(qd0_ >> 3) * kQ40ChunkBytes;                           \
-        _Pragma("unroll") for (int u = 0; u < U; u++) rw[SLOT][u] =                                  \
-            *(const uint4*)(chunk_ + ((qd0_ + u) & 7) * 1024 + lane * 16);                           \
-        const uint8_t* sp_ = chunk_ + 8192 + lane * 16 + (qd0_ & 7) * 2;                             \
+        const int cb_ = (qd0_ >> 3) * kQ40ChunkBytes;                                                \
+        _Pragma("unroll") for (int u = 0; u < U; u++) rw[SLOT][u] = __builtin_bit_cast(               \
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wvo, cb_ + ((qd0_ + u) & 7) * 1024, 0)); \
+        const int so_ = cb_ + 8192 + (qd0_ & 7) * 2;                                                 \
         if constexpr (SW == 2) {                                                                     \
-            const uint2 s2_ = *(const uint2*)sp_;                                                    \
+            const uint2 s2_ = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wres, wvo, so_, 0)); \
             rs[SLOT][0] = s2_.x;                                                                     \
             rs[SLOT][SW - 1] = s2_.y;                                                                \
         } else if constexpr (U == 2) {                                                               \
-            rs[SLOT][0] = *(const uint32_t*)sp_;                                                     \
+            rs[SLOT][0] = __builtin_amdgcn_raw_buffer_load_b32(wres, wvo, so_, 0);                   \
         } else {                                                                                     \
-            rs[SLOT][0] = *(const uint16_t*)sp_;                                                     \
+            rs[SLOT][0] = __builtin_amdgcn_raw_buffer_load_b16(wres, wvo, so_, 0);                   \
         }                                                                                            \
         _Pragma("unroll") for (int u = 0; u < U; u++) {                                              \
-            const int b_ = min(4 * (qd0_ + u) + j, nb - 1);                                          \
-            _Pragma("unroll") for (int q = 0; q < NP; q++) {                                         \
-                const int t_ = min(2 * q + xtok, N - 1);                                             \
-                rx[SLOT][u][q] = xbase[((size_t)t_ * p.K + (size_t)b_ * 32) / 4];                    \
-            }                                                                                        \
+            _Pragma("unroll") for (int q = 0; q < NP; q++) rx[SLOT][u][q] = (int)                     \
+                __builtin_amdgcn_raw_buffer_load_b32(xres, xvo[q] + 128 * (qd0_ + u), 0, 0);         \
             _Pragma("unroll") for (int q = 0; q < NM; q++) {                                         \
-                const int t_ = min(8 * q + mtok, N - 1);                                             \
-                rm[SLOT][u][q] = mbase[(size_t)t_ * nb + b_];                                        \
+                if constexpr (kMetaBuf) {                                                            \
+                    const int mo_ = mvo[q] + 16 * (qd0_ + u);                                        \
+                    const int ms_ = (int)__builtin_amdgcn_raw_buffer_load_b32(sres, mo_, 0, 0);      \
+                    const int m8_ = (int)__builtin_amdgcn_raw_buffer_load_b32(s8res, mo_, 0, 0);     \
+                    rm[SLOT][u][q] = meta_s ? ms_ : m8_;                                             \
+                } else {                                                                             \
+                    const int b_ = min(4 * (qd0_ + u) + j, nb - 1);                                  \
+                    rm[SLOT][u][q] = mbase[(size_t)mt[q] * nb + b_];                                 \
+                }                                                                                    \
             }                                                                                        \
         }                                                                                            \
     } while (0)
