@@ -5,30 +5,33 @@
 //
 //     s_{-1} = s0 (0 unless a carry-in is given),   s_i = fl32(s_{i-1} + a_i),   i = 0 .. n-1.
 //
-// On gfx950 one dependent v_add_f32 costs ~10 cycles, so a 4096-term chain is ~21 us
+// On gfx950 one dependent v_add_f32 costs ~10 cycles, so a 4096-term chain is ~17 us
 // when evaluated literally.  This routine returns the bit-identical s_{n-1} from a
-// workgroup of T threads in a few parallel passes:
+// workgroup of T threads; thread t owns the segment of terms a_{tE} .. a_{tE+E-1}:
 //
-//  1. Guess.  P_i = sum_{j<=i} a_j in double (a block scan) and g_i = fl32(P_{i-1})
-//     approximates the chain value before step i (it differs from s_{i-1} only by the
-//     chain's accumulated rounding, a few ulps).
-//  2. Increments.  If s_{i-1} lies within 256 ulps of g_i, in the same binade, and the
-//     step neither reaches the next binade nor rounds an exact tie, then
-//         fl32(s_{i-1} + a_i) - s_{i-1} = fl32(g_i + a_i) - g_i =: d_i,
-//     because both states are multiples of the binade's ulp.  Steps where that can fail
-//     are flagged "sensitive" by integer tests on the f32 bits; there are ~20 of them in
-//     4096 terms of smooth data (binade crossings cluster in the first few dozen terms,
-//     where the sum grows fastest).
-//  3. c_i = sum_{j<=i} d_j (block scan in double).
-//  4. Sensitive walk.  One wave visits the sensitive steps in order and computes their
-//     true result from the corrected chain value before them (carried in f32, two
-//     dependent adds per step), giving the correction shift_k = s_k - c_k.  Every other
-//     step inherits the shift of the last sensitive step before it.
-//  5. Verify.  With cn_i = fl32(c_i + shift), every step is checked locally and in
-//     parallel: cn_i == fl32(cn_{i-1} + a_i), cn_{-1} = 0.  If all hold, cn IS the
-//     sequential chain (induction), whatever the guesses were.  If any fails (it needs the
-//     chain to drift > 256 ulps from the exact prefix, or more than kChainMaxSensitive
-//     sensitive steps), thread 0 recomputes the chain sequentially.
+//  1. Guess.  G_t = fl32(s0 + sum of all earlier terms), the prefix taken in double (a
+//     block scan): it differs from the true chain value at the segment start only by the
+//     chain's accumulated rounding, a few ulps.
+//  2. Segment from the guess.  Each thread runs its E additions sequentially from G_t,
+//     giving the end value X_t and the increment D_t = X_t - G_t (exact in double).  If the
+//     true start S_t lies within 256 ulps of G_t in the same binade, and the run neither
+//     leaves that binade (start and end in the same binade, both 256 ulps from its edges)
+//     nor rounds an exact tie (the Fast2Sum error of a step equals half an ulp), then
+//     every step rounds the same way from S_t as from G_t, so the true end is S_t + D_t:
+//     both states are multiples of the binade's ulp.  Segments where that can fail are
+//     "sensitive" (typically the ~12 that contain a binade crossing of the growing sum).
+//  3. C_t = s0 + sum of the earlier D (block scan in double): the start of segment t if no
+//     earlier segment were sensitive.
+//  4. Walk.  One thread visits the sensitive segments in order: it advances the true chain
+//     value over the insensitive segments in between (their increments add exactly),
+//     evaluates the sensitive segment term by term, and records the correction
+//     shift_k = (true end) - (C_k + D_k).  A segment's start is then C_t + shift of the last
+//     sensitive segment before it.
+//  5. Verify.  Every thread recomputes its segment sequentially from that start; if each
+//     start equals the previous segment's recomputed end (and the first equals s0), the
+//     last end IS the sequential chain, by induction, whatever the guesses were.  If any
+//     check fails (the chain drifted > 256 ulps from the exact prefix, or more than
+//     kChainMaxSensitive segments are sensitive), thread 0 recomputes the chain sequentially.
 //
 // The result is therefore always bit-identical to the sequential loop; the guesses only
 // decide how fast it is found.  Terms must be >= 0 (sums of squares, exponentials).
@@ -45,10 +48,10 @@ namespace nc {
 constexpr int kChainMaxSensitive = 256;
 
 struct ChainEntry {
-    double cprev;  // c_{k-1} (uncorrected)
-    double cold;   // c_k (uncorrected)
-    double shift;  // s_k - c_k after the walk
-    float a;       // a_k
+    double cstart;  // C_k: uncorrected start of sensitive segment k
+    double cend;    // C_k + D_k: its uncorrected end
+    double shift;   // true end - cend, after the walk
+    int seg;        // segment (thread) index
 };
 
 template <int T>
@@ -155,36 +158,13 @@ __device__ __forceinline__ double block_excl_scan_f64_i32(double v, int k, doubl
     return base + excl;
 }
 
-// Step i with guess g (the chain value before the step, approximately) and term a >= 0:
-// returns d = fl32(g + a) - g exactly and whether the step is sensitive (see above).
-// Branch free (selects only): every lane evaluates every test.
-__device__ __forceinline__ double chain_increment(float g, float a, bool* sensitive) {
-    const float r = g + a;
-    const double d = (double)r - (double)g;
-    const uint32_t bg = __float_as_uint(g), ba = __float_as_uint(a);
-    const int eg = (int)(bg >> 23), ea = (int)(ba >> 23);
-    const int mg = (int)(bg & 0x7fffff);
-    const int sh = eg - (ea > 0 ? ea : 1);  // a's binary exponent below g's
-    const uint32_t ma = (ba & 0x7fffffu) | (ea > 0 ? 0x800000u : 0u);
-    const int shc = sh < 1 ? 1 : (sh > 31 ? 31 : sh);
-    const uint32_t low = ma & ((1u << shc) - 1u);
-    // exact tie of g + a at g's ulp (only possible for 2 <= sh <= 24)
-    const bool tie = (sh >= 2) & (sh <= 24) & (low == (1u << (shc - 1)));
-    const int a_ulps = sh > 24 ? 1 : (int)(ma >> shc) + 1;  // >= a / ulp(g)
-    // sh < 2: a comparable to the running sum, the binade may change; eg == 0: subnormal
-    // running sum; the margin tests: s may sit in the binade below, or s + a may reach the
-    // next binade.
-    const bool s = (sh < 2) | tie | (mg + a_ulps + 256 >= (1 << 23)) | (mg < 256) | (eg == 0);
-    // g == 0: every earlier term is 0, the chain is exactly 0 and d = a.  a == 0: d = 0.
-    *sensitive = s & (bg != 0) & (ba != 0);
-    return d;
-}
+constexpr int kChainMargin = 256;  // ulps between a guess and the true state that are tolerated
 
 // Thread t holds terms a[0..E) = a_{tE} .. a_{tE+E-1} (n = T*E terms; pad with zeros, which
 // leave the chain unchanged).  The chain starts from s_{-1} = s0 >= 0, so a long sum can be
 // evaluated as consecutive segments, each starting from the previous segment's result.
-// a_lds: n floats of LDS used by the fallback.  Every thread of the block must call it;
-// returns s_{n-1} to all threads.
+// a_lds: n floats of LDS used by the walk and the fallback.  Every thread of the block must
+// call it; returns s_{n-1} to all threads.
 template <int E, int T>
 __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float* a_lds, float s0 = 0.0f) {
     static_assert(E >= 1 && E <= 32, "terms per thread");
@@ -192,119 +172,86 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
 #pragma unroll
     for (int j = 0; j < E; j++) a_lds[t * E + j] = a[j];
 
-    // 1. guesses from the double prefix
-    double w[E];
+    // 1. guess of the segment's start from the double prefix
     double run = 0.0;
 #pragma unroll
-    for (int j = 0; j < E; j++) {
-        run += (double)a[j];
-        w[j] = run;
-    }
+    for (int j = 0; j < E; j++) run += (double)a[j];
     const double exclp = (double)s0 + block_excl_scan_f64<T>(run, sc.dtot);
+    const float g = (float)exclp;  // segment 0: exactly s0
 
-    // 2. speculative increments and sensitivity (w[] becomes d[])
-    uint32_t sens = 0;
-    float g = (float)exclp;
+    // 2. the segment evaluated from the guess, with the tie and binade tests
+    const uint32_t bg = __float_as_uint(g);
+    const int eg = (int)(bg >> 23);
+    // half an ulp of g's binade, 2^(eg - 151); only used when eg >= 25 (else sensitive anyway)
+    const float half = __uint_as_float((uint32_t)(eg > 25 ? eg - 24 : 1) << 23);
+    float x = g;
+    bool tie = false;
 #pragma unroll
     for (int j = 0; j < E; j++) {
-        const float gnext = (float)(exclp + w[j]);
-        bool s;
-        w[j] = chain_increment(g, a[j], &s);
-        if (s) sens |= 1u << j;
-        g = gnext;
+        const float r = x + a[j];
+        // Fast2Sum error of the step (exact while x >= a[j], i.e. whenever the binade holds)
+        tie |= __builtin_fabsf(a[j] - (r - x)) == half;
+        x = r;
     }
+    const uint32_t bx = __float_as_uint(x);
+    const int mg = (int)(bg & 0x7fffff), mx = (int)(bx & 0x7fffff);
+    // g == 0: every earlier term and s0 are 0, so the start is exact and the run is the truth
+    const bool sens = (bg != 0) & ((eg < 25) | ((int)(bx >> 23) != eg) | (mg < kChainMargin) |
+                                   (mx + kChainMargin >= (1 << 23)) | tie);
+    const double d = (double)x - (double)g;
 
-    // 3. uncorrected chain c = prefix of d, with the sensitive count scanned in the same pass
-    run = 0.0;
-#pragma unroll
-    for (int j = 0; j < E; j++) {
-        run += w[j];
-        w[j] = run;
-    }
+    // 3. uncorrected starts C_t, with the sensitive count scanned in the same pass
     int off, total_s;
-    const double exclc = block_excl_scan_f64_i32<T>(run, __popc(sens), sc.dtot, sc.itot, &off, &total_s);
+    const double cstart = (double)s0 + block_excl_scan_f64_i32<T>(d, sens ? 1 : 0, sc.dtot, sc.itot, &off, &total_s);
 
-    // 4. sensitive list in ascending order, then the walk
+    // 4. sensitive list in ascending order, then the walk (one thread)
     const bool listed = total_s <= kChainMaxSensitive;
     if (listed && sens) {
-        int e = off;
-#pragma unroll
-        for (int j = 0; j < E; j++) {
-            if (sens >> j & 1) {
-                ChainEntry& ce = sc.ent[e++];
-                ce.cprev = j == 0 ? exclc : exclc + w[j - 1];
-                ce.cold = exclc + w[j];
-                ce.a = a[j];
-            }
-        }
+        ChainEntry& ce = sc.ent[off];
+        ce.cstart = cstart;
+        ce.cend = cstart + d;
+        ce.seg = t;
     }
     __syncthreads();
-    if (listed && t < 64) {
-        // s_{k-1} = s_j + (c_{k-1} - c_j) with j the previous sensitive step (the advance is
-        // exact: nothing between j and k changes binade or ties), then s_k = fl32(s_{k-1} + a_k).
-        float s_run = s0;      // s_j (s_{-1} = s0, c_{-1} = 0 before the first entry)
-        double co_last = 0.0;  // c_j
-        for (int e0 = 0; e0 < total_s; e0 += 64) {
-            const int me = e0 + t;
-            double cp = 0.0, co = 0.0;
-            float av = 0.0f;
-            if (me < total_s) {
-                cp = sc.ent[me].cprev;
-                co = sc.ent[me].cold;
-                av = sc.ent[me].a;
-            }
-            double co_prev = dpp0_d<kDppWaveShr1>(co);
-            if (t == 0) co_prev = co_last;
-            const float adv = (float)(cp - co_prev);
-            float mine = 0.0f;
-            const int cnt = min(64, total_s - e0);
-            for (int q0 = 0; q0 < cnt; q0 += 8) {  // q is wave-uniform: v_readlane, no LDS
+    if (listed && t == 0) {
+        float S = s0;         // true chain value at the end of the last walked segment
+        double cl = (double)s0;  // its uncorrected counterpart
+        for (int e = 0; e < total_s; e++) {
+            const double cs = sc.ent[e].cstart, ce = sc.ent[e].cend;
+            const float* ap = a_lds + sc.ent[e].seg * E;
+            // insensitive segments in between keep their shift: the advance is exact
+            S = S + (float)(cs - cl);
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const int q = q0 + u;
-                    if (q < cnt) {
-                        const float advq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(adv), q));
-                        const float aq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(av), q));
-                        s_run = (s_run + advq) + aq;
-                        mine = t == q ? s_run : mine;
-                    }
-                }
-            }
-            if (me < total_s) sc.ent[me].shift = (double)mine - co;
-            co_last = chain_readlane(co, cnt - 1);
+            for (int j = 0; j < E; j++) S = S + ap[j];
+            sc.ent[e].shift = (double)S - ce;
+            cl = ce;
         }
     }
     __syncthreads();
 
-    // 5. corrected values and the local check of every step
+    // 5. corrected start, sequential recomputation, and the check of every boundary
     bool bad = !listed;
-    float cn[E];
+    float y = 0.0f;
     if (listed) {
-        double cur = off == 0 ? (double)s0 : sc.ent[off - 1].shift;
-        int e = off;
+        const double sh = off == 0 ? 0.0 : sc.ent[off - 1].shift;
+        const float start = (float)(cstart + sh);
+        y = start;
 #pragma unroll
-        for (int j = 0; j < E; j++) {
-            if (sens >> j & 1) cur = sc.ent[e++].shift;
-            cn[j] = (float)(exclc + w[j] + cur);
-        }
-        sc.last[t] = cn[E - 1];
+        for (int j = 0; j < E; j++) y = y + a[j];
+        sc.last[t] = y;
+        bad = t == 0 ? start != s0 : false;
+        // the start is compared with the previous segment's end after the barrier
+        run = (double)start;  // reuse a register for the start
     }
     __syncthreads();
-    if (listed) {
-        float prev = t == 0 ? s0 : sc.last[t - 1];
-#pragma unroll
-        for (int j = 0; j < E; j++) {
-            bad |= (prev + a[j]) != cn[j];
-            prev = cn[j];
-        }
-    }
+    if (listed && t > 0) bad |= (float)run != sc.last[t - 1];
     const bool any_bad = __syncthreads_or(bad);
     if (!any_bad) {
-        if (t == T - 1) sc.result = cn[E - 1];
+        if (t == T - 1) sc.result = y;
     } else if (t == 0) {
-        float s = s0;
-        for (int i = 0; i < T * E; i++) s = s + a_lds[i];
-        sc.result = s;
+        float v = s0;
+        for (int i = 0; i < T * E; i++) v = v + a_lds[i];
+        sc.result = v;
     }
     __syncthreads();
     return sc.result;
