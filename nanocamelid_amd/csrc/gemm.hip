@@ -718,6 +718,136 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
     gemm_epilogue<NMAX, S>(p, acc, tile, wave, lane);
 }
 
+// ---------------------------------------------------------------- Q4_K, 16-row tiles (R16)
+// Workgroup = one 16-row tile, S waves.  A wave instruction covers a quad of 4 super-blocks:
+// lane = 16*q + r holds super-block 4*g + q of row r (9 x 16 bytes: slot 0 = d, dmin and the
+// 12 packed scale bytes, slots 1..8 the 128 nibble bytes).  Round: wave w takes quad
+// r*S + w.  Each DPP row of 16 lanes is one super-block, so its activations are broadcast
+// inside the row: for token n, dword c*16 + j of the super-block's 256 int8 activations sits
+// in lane 16*q + j of register ax[n][c], and one meta dword per lane carries the sub-block
+// scales (lanes j < 8: x_scale of sub-block j) and sums (lanes 8 + j: -8 * sum of x).  Per
+// token the super-block term follows q8.rs:1372-1375 sub-block by sub-block (low half then
+// high half of each nibble pair); the terms go through LDS and the chain threads (token n,
+// row r) add them in super-block order.  Loads are unconditional buffer loads: weights at a
+// scalar chunk offset (clamped to the padded quads), activations and meta at per-lane offsets
+// range-checked against [N][K] and [N][K/32] (a token past N reads 0 and is never stored).
+template <int NMAX, int S, int D>
+__global__ __launch_bounds__(64 * S) void gemm_q4_k_r16_kernel(GemmParams p) {
+    static_assert(16 * NMAX <= 64 * S, "chain threads must fit the workgroup");
+    extern __shared__ float lds[];  // [2][4*S][NMAX][16] super-block terms
+    const int tile = blockIdx.x;
+    const int wave = wave_id_uniform();
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 4, j = lane & 15;
+    const int N = p.N, nsb = p.units, nb = nsb * 8;
+    const int nquads = (nsb + 3) / 4;    // padded to p.groups quads per tile
+    const int nrounds = (nquads + S - 1) / S;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.w + (size_t)tile * p.groups * kQ4KChunkBytes), 0, p.groups * kQ4KChunkBytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, 0, N * p.K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs, 0, N * nb * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t s8res = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs8, 0, N * nb * 4, 0x00020000);
+    const int wvo = lane * 16;
+    const int xvo = q * 256 + j * 4;          // + n*K + c*64 + quad*1024
+    const int mvo = q * 32 + (j & 7) * 4;     // + n*nb*4 + quad*128
+    const bool meta_s = j < 8;
+    uint4 rw[D][9];
+    int ax[D][NMAX][4], am[D][NMAX];
+#define NC_K16_LOAD(R, SLOT)                                                                         \
+    do {                                                                                             \
+        const int g_ = min(min((R), nrounds - 1) * S + wave, p.groups - 1);                          \
+        _Pragma("unroll") for (int i = 0; i < 9; i++) rw[SLOT][i] = __builtin_bit_cast(               \
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wvo, g_ * kQ4KChunkBytes + i * 1024, 0)); \
+        _Pragma("unroll") for (int n = 0; n < NMAX; n++) {                                           \
+            _Pragma("unroll") for (int c = 0; c < 4; c++) ax[SLOT][n][c] = (int)                      \
+                __builtin_amdgcn_raw_buffer_load_b32(xres, xvo + n * p.K + c * 64 + g_ * 1024, 0, 0); \
+            const int mo_ = mvo + n * nb * 4 + g_ * 128;                                             \
+            const int ms_ = (int)__builtin_amdgcn_raw_buffer_load_b32(sres, mo_, 0, 0);              \
+            const int m8_ = (int)__builtin_amdgcn_raw_buffer_load_b32(s8res, mo_, 0, 0);             \
+            am[SLOT][n] = meta_s ? ms_ : m8_;                                                        \
+        }                                                                                            \
+    } while (0)
+#pragma unroll
+    for (int k = 0; k < D - 1; k++) NC_K16_LOAD(k, k);
+    float acc = 0.0f;
+    const int cn = threadIdx.x >> 4, cr = threadIdx.x & 15;  // chain thread: token, row
+    for (int r0 = 0; r0 < nrounds; r0 += D) {
+#pragma unroll
+        for (int k = 0; k < D; k++) {
+            const int r = r0 + k;
+            NC_K16_LOAD(r + D - 1, (k + D - 1) % D);
+            if (r < nrounds) {  // uniform
+                float* buf = lds + (size_t)(r & 1) * 4 * S * NMAX * 16;
+                const uint4* v = rw[k];
+                const float d = f16_to_f32((uint16_t)(v[0].x & 0xffff));
+                const float dmin = f16_to_f32((uint16_t)(v[0].x >> 16));
+                float sc[8], mn[8];
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) {  // q8.rs:2008-2018 q4_k_scale_min
+                    uint32_t sv, mv;
+                    if (jj < 4) {
+                        sv = kbyte(v[0].y, v[0].z, v[0].w, jj) & 63;
+                        mv = kbyte(v[0].y, v[0].z, v[0].w, jj + 4) & 63;
+                    } else {
+                        sv = (kbyte(v[0].y, v[0].z, v[0].w, jj + 4) & 0x0f) |
+                             ((kbyte(v[0].y, v[0].z, v[0].w, jj - 4) >> 6) << 4);
+                        mv = (kbyte(v[0].y, v[0].z, v[0].w, jj + 4) >> 4) |
+                             ((kbyte(v[0].y, v[0].z, v[0].w, jj) >> 6) << 4);
+                    }
+                    sc[jj] = d * (float)sv;
+                    mn[jj] = dmin * (float)mv;
+                }
+                float part[NMAX];
+#pragma unroll
+                for (int n = 0; n < NMAX; n++) part[n] = 0.0f;
+                auto pair_step = [&]<int PR>() {
+                    const uint4 q0 = v[1 + 2 * PR], q1 = v[2 + 2 * PR];
+                    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                    int lo[8], hi[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        lo[i] = (int)(qw[i] & 0x0F0F0F0Fu);
+                        hi[i] = (int)((qw[i] >> 4) & 0x0F0F0F0Fu);
+                    }
+                    constexpr int jl = 2 * PR, jh = 2 * PR + 1;
+                    [&]<int... Ns>(std::integer_sequence<int, Ns...>) {
+                        (([&] {
+                             constexpr int n = Ns;
+                             // W = sum(nib * x) over the pair's low / high 32 elements: x dwords
+                             // 16*PR + i (lanes i) and 16*PR + 8 + i (lanes 8 + i) of ax[.][n][PR]
+                             const int wl = dot32_bcast<0>(0, ax[k][n][PR], lo[0], lo[1], lo[2], lo[3], lo[4], lo[5],
+                                                           lo[6], lo[7]);
+                             const int wh = dot32_bcast<8>(0, ax[k][n][PR], hi[0], hi[1], hi[2], hi[3], hi[4], hi[5],
+                                                           hi[6], hi[7]);
+                             const float xl = bcast_f<jl>(__int_as_float(am[k][n]));
+                             const float xh = bcast_f<jh>(__int_as_float(am[k][n]));
+                             const int al = bcast_i<8 + jl>(am[k][n]) / -8;  // A_j = sum of x
+                             const int ah = bcast_i<8 + jh>(am[k][n]) / -8;
+                             // q8.rs:1372-1375: sum += xs * (sc*W - mn*A), low then high half
+                             part[n] = part[n] + xl * (sc[jl] * (float)wl - mn[jl] * (float)al);
+                             part[n] = part[n] + xh * (sc[jh] * (float)wh - mn[jh] * (float)ah);
+                         }()),
+                         ...);
+                    }(std::make_integer_sequence<int, NMAX>{});
+                };
+                pair_step.template operator()<0>();
+                pair_step.template operator()<1>();
+                pair_step.template operator()<2>();
+                pair_step.template operator()<3>();
+#pragma unroll
+                for (int n = 0; n < NMAX; n++) buf[((wave * 4 + q) * NMAX + n) * 16 + j] = part[n];
+                __syncthreads();
+                if (threadIdx.x < 16 * NMAX && cn < N) {
+                    const int nblk = min(4 * S, nsb - r * 4 * S);
+                    for (int bl = 0; bl < nblk; bl++) acc = acc + buf[(bl * NMAX + cn) * 16 + cr];
+                }
+            }
+        }
+    }
+#undef NC_K16_LOAD
+    if (threadIdx.x < 16 * NMAX && cn < N) gemm_epilogue_r16<NMAX>(p, acc, cn, tile, cr);
+}
+
 // ---------------------------------------------------------------- per-block dots (parity debug)
 __global__ void blockdots_q4_0_kernel(const uint8_t* w, int groups, int r16, int M, int K, const int8_t* x, int N,
                                       int32_t* dots) {
@@ -744,7 +874,8 @@ __global__ void blockdots_q4_0_kernel(const uint8_t* w, int groups, int r16, int
     }
 }
 
-__global__ void blockdots_q4_k_kernel(const uint8_t* w, int nsb, int M, int K, const int8_t* x, int N, int32_t* dots) {
+__global__ void blockdots_q4_k_kernel(const uint8_t* w, int nsb, int groups, int r16, int M, int K, const int8_t* x,
+                                      int N, int32_t* dots) {
     const int nb = K / 32;
     const int64_t total = (int64_t)N * M * nb;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
@@ -752,7 +883,9 @@ __global__ void blockdots_q4_k_kernel(const uint8_t* w, int nsb, int M, int K, c
         const int r = (int)((i / nb) % M);
         const int n = (int)(i / ((int64_t)nb * M));
         const int sb = j / 8, sj = j % 8, pr = sj / 2, half = sj % 2;
-        const uint8_t* chunk = w + ((size_t)(r / 64) * nsb + sb) * kQ4KChunkBytes + (r & 63) * 16;
+        const uint8_t* chunk = r16 ? w + ((size_t)(r / 16) * groups + sb / 4) * kQ4KChunkBytes +
+                                         (16 * (sb % 4) + (r & 15)) * 16
+                                   : w + ((size_t)(r / 64) * nsb + sb) * kQ4KChunkBytes + (r & 63) * 16;
         const int8_t* xb = x + (size_t)n * K + (size_t)j * 32;
         int d = 0;
         for (int l = 0; l < 32; l++) {
@@ -852,6 +985,27 @@ int launch_k(int S, const QMatDev& w, const GemmParams& p, hipStream_t st, hipEv
     }
 }
 
+// Q4_K on 16-row tiles: 8 waves (one quad of super-blocks each per round) when K has at least
+// 8 quads, else 4 (enough chain threads for 16 tokens); a ring of 2 rounds, 1 at 16 rows
+// (registers).
+template <int NMAX>
+int launch_k16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    constexpr int D = NMAX <= 9 ? 2 : 1;
+    auto go = [&]<int S>() {
+        const size_t lds = (size_t)2 * 4 * S * NMAX * 16 * sizeof(float);
+        if (ev0)
+            hipExtLaunchKernelGGL((gemm_q4_k_r16_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0,
+                                  p);
+        else
+            hipLaunchKernelGGL((gemm_q4_k_r16_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+    };
+    if (p.epi == EPI_SWIGLU_Q8) return fail(NC_EINVAL, "gemm: the 16-row Q4_K layout has no SwiGLU epilogue");
+    if (w.groups >= 8) go.template operator()<8>();
+    else go.template operator()<4>();
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
 }  // namespace
 
 // R64 waves per workgroup: enough K-split waves that ~1000+ waves stream the matrix
@@ -889,6 +1043,9 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent
     if (w.layout == LAYOUT_R16) {
         NC_GEMM_FOR_NMAX(launch_r16, p.N, w, p, st, ev0, ev1)
     }
+    if (w.layout == LAYOUT_R16K) {
+        NC_GEMM_FOR_NMAX(launch_k16, p.N, w, p, st, ev0, ev1)
+    }
     if (w.type == NC_TYPE_Q4_K) {
         const int nsb = (int)w.units;
         int S = nsb == 12 ? 12 : (nsb >= 8 ? 8 : 4);
@@ -913,8 +1070,8 @@ int launch_blockdots(const QMatDev& w, const int8_t* x, int32_t* dots, int N, hi
                            (int)(w.layout == LAYOUT_R16), (int)w.rows,
                            (int)w.cols, x, N, dots);
     else
-        hipLaunchKernelGGL(blockdots_q4_k_kernel, dim3(blocks), dim3(256), 0, st, w.dev, (int)w.units, (int)w.rows,
-                           (int)w.cols, x, N, dots);
+        hipLaunchKernelGGL(blockdots_q4_k_kernel, dim3(blocks), dim3(256), 0, st, w.dev, (int)w.units, (int)w.groups,
+                           (int)(w.layout == LAYOUT_R16K), (int)w.rows, (int)w.cols, x, N, dots);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }

@@ -40,7 +40,7 @@ constexpr int kQ4KChunkBytes = 9 * 1024;
 // nibbles] with lane = 16*j + r holding block 4*qd + j of row 16*tile + r, then [64 lanes x
 // 8 f16 scales] (one per quad of the group).  One wave load covers 4 blocks x 16 rows.
 constexpr int kTileRowsR16 = 16;
-enum Layout : int { LAYOUT_R64 = 0, LAYOUT_R16 = 1 };
+enum Layout : int { LAYOUT_R64 = 0, LAYOUT_R16 = 1, LAYOUT_R16K = 2 };  // R16K: Q4_K on 16-row tiles
 
 struct QMatDev {
     int type = NC_TYPE_Q4_0;
@@ -66,6 +66,11 @@ void repack_q4_0_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t
 int64_t q40_r16_layout_bytes(int64_t rows, int64_t cols);
 int64_t q40_layout_bytes(int64_t rows, int64_t cols);
 int64_t q4k_layout_bytes(int64_t rows, int64_t cols);
+int64_t q4k_r16_layout_bytes(int64_t rows, int64_t cols);
+// Q4_K on 16-row tiles: per (tile, quad of 4 super-blocks) 9 x [64 lanes x 16 B], lane
+// 16*q + r = super-block 4*quad + q of row r.
+void repack_q4_k_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups,
+                     int64_t row_off);
 
 // ---------------------------------------------------------------- GEMM launch
 enum Epi : int {

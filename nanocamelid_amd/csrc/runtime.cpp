@@ -119,6 +119,9 @@ int64_t q40_layout_bytes(int64_t rows, int64_t cols) {
     return tiles * groups * kQ40ChunkBytes;
 }
 int64_t q4k_layout_bytes(int64_t rows, int64_t cols) { return (rows + 63) / 64 * (cols / 256) * kQ4KChunkBytes; }
+int64_t q4k_r16_layout_bytes(int64_t rows, int64_t cols) {
+    return (rows + 15) / 16 * ((cols / 256 + 3) / 4) * kQ4KChunkBytes;
+}
 
 static inline int64_t dst_row(int64_t r, int64_t row_off, int half) {
     return half < 0 ? row_off + r : (r / 32) * 64 + (r % 32) + 32 * half;
@@ -179,6 +182,21 @@ void repack_q4_k(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* ds
     });
 }
 
+void repack_q4_k_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups,
+                     int64_t row_off) {
+    const int64_t nsb = cols / 256;
+    parallel_for(rows_src, 0, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; r++) {
+            const int64_t R = r + row_off, t = R / 16, rr = R % 16;
+            for (int64_t s = 0; s < nsb; s++) {
+                const uint8_t* blk = src + (r * nsb + s) * 144;
+                uint8_t* chunk = dst + (t * groups + s / 4) * kQ4KChunkBytes + (16 * (s % 4) + rr) * 16;
+                for (int i = 0; i < 9; i++) std::memcpy(chunk + i * 1024, blk + i * 16, 16);
+            }
+        }
+    });
+}
+
 struct Part {
     const uint8_t* src;
     int64_t rows;
@@ -197,12 +215,20 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
     // R16 for Q4_0 matrices too small to fill the chip with 64-row tiles.  An interleaved
     // gate/up pair keeps its 64-row groups (gate rows 32t.. in rows 0-31 of group t, up rows in
     // 32-63): with R16 those are four consecutive 16-row tiles, which one workgroup covers.
+    // Q4_K likewise on 16-row tiles below 256 64-row tiles, except an interleaved gate/up pair
+    // (its SwiGLU epilogue needs the 64-row groups; those matrices are large anyway).
+    const bool single = std::all_of(parts.begin(), parts.end(), [](const Part& q) { return q.half < 0; });
     out.layout = type == NC_TYPE_Q4_0 && (rows + 63) / 64 < 512 ? LAYOUT_R16 : LAYOUT_R64;
+    if (type == NC_TYPE_Q4_K && single && (rows + 63) / 64 < 256) out.layout = LAYOUT_R16K;
     out.units = type == NC_TYPE_Q4_0 ? cols / 32 : cols / 256;
     if (out.layout == LAYOUT_R16) {
         out.tiles = (rows + 15) / 16;
         out.groups = (out.units + 31) / 32;
         out.dev_bytes = q40_r16_layout_bytes(rows, cols);
+    } else if (out.layout == LAYOUT_R16K) {
+        out.tiles = (rows + 15) / 16;
+        out.groups = (out.units + 3) / 4;
+        out.dev_bytes = q4k_r16_layout_bytes(rows, cols);
     } else {
         out.tiles = (rows + 63) / 64;
         out.groups = type == NC_TYPE_Q4_0 ? (out.units + 7) / 8 : 0;
@@ -212,6 +238,7 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
     std::vector<uint8_t> host(out.dev_bytes, 0);
     for (const auto& p : parts) {
         if (out.layout == LAYOUT_R16) repack_q4_0_r16(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
+        else if (out.layout == LAYOUT_R16K) repack_q4_k_r16(p.src, p.rows, cols, host.data(), out.groups, p.row_off);
         else if (type == NC_TYPE_Q4_0) repack_q4_0(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
         else repack_q4_k(p.src, p.rows, cols, host.data(), p.row_off, p.half);
     }

@@ -140,6 +140,26 @@ def test_q4_k_wave_splits(ctx, shape, N):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("shape", [(130, 1280), (16400, 1024)], ids=["r16k-partial-quad", "r64-large"])
+@pytest.mark.parametrize("N", [1, 5, 16])
+def test_q4_k_layouts(ctx, shape, N):
+    """Q4_K matrices below 256 64-row tiles use 16-row tiles (4 super-blocks per wave
+    instruction; 1280 columns leave the last quad one super-block); larger ones keep 64-row
+    tiles.  Outputs and per-sub-block ints bit-exact either way."""
+    import nanocamelid_amd as nc
+    M, K = shape
+    w = random_q4_k(M, K, seed=M + K + N)
+    _, xq, xs = q8_activations(N, K, seed=400 + N)
+    out, dots = _run_gemm(ctx, nc.NC_TYPE_Q4_K, w, M, K, xq, xs)
+    ref = O.matmul_q4_k(xq, xs, w, N, M, K, nthreads=16)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    for r in (0, 15, 16, M - 1):
+        for n in (0, N - 1):
+            for sb in range(K // 256):
+                W, _ = O.q4_k_subblock_ints(w[r, sb], xq[n, sb * 256:(sb + 1) * 256])
+                assert np.array_equal(dots[n, r, sb * 8:(sb + 1) * 8], W)
+
+
 def test_quantize_q8_0_matches_oracle(ctx):
     import nanocamelid_amd as nc
     rng = np.random.default_rng(5)
