@@ -126,35 +126,45 @@ __device__ inline uint64_t sample_weight(const float* p, const float* q, int i) 
 }
 
 // Every thread of the block calls it; returns the sampled id, or -1 when all weights are 0.
-// Thread t owns the contiguous ids [t*C, t*C + C).
+// Wave w owns the contiguous ids [w*C, w*C + C) and reads them 64 at a time (lane l takes id
+// base + 64*i + l: coalesced).  Phase 1: the wave totals (order-free integer sums) and their
+// block scan fix the target and the wave whose range holds it.  Phase 2: that wave walks its
+// range in 64-id tiles, an inclusive 64-bit scan per tile on top of the running prefix, and
+// the first lane whose prefix exceeds the target is the answer.
 __device__ int sample_fixed_block(const float* p, const float* q, int V, uint32_t k24, SampleScratch& ss) {
-    const int t = threadIdx.x;
-    const int C = (V + kSpT - 1) / kSpT;
-    const int lo = min(t * C, V), hi = min(lo + C, V);
+    constexpr int NW = kSpT / 64;
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int C = (V + NW - 1) / NW;
+    const int lo = min(w * C, V), hi = min(lo + C, V);
     uint64_t mine = 0;
-    for (int i = lo; i < hi; i++) mine += sample_weight(p, q, i);
-    const uint64_t incl = wave_incl_scan_u64(mine);
-    if ((t & 63) == 63) ss.wtot[t >> 6] = incl;
+    for (int i = lo + lane; i < hi; i += 64) mine += sample_weight(p, q, i);
+    // wave total (order-free)
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mine += __shfl_xor(mine, o);
+    if (lane == 0) ss.wtot[w] = mine;
     if (t == 0) ss.found = -1;
     __syncthreads();
     uint64_t base = 0, total = 0;
 #pragma unroll
-    for (int w = 0; w < kSpT / 64; w++) {
-        const uint64_t v = ss.wtot[w];
-        if (w < (t >> 6)) base += v;
+    for (int i = 0; i < NW; i++) {
+        const uint64_t v = ss.wtot[i];
+        if (i < w) base += v;
         total += v;
     }
-    const uint64_t excl = base + incl - mine;
     // target = floor(k24 * total / 2^24) < total, split so every product fits in 64 bits
     const uint64_t target = (((uint64_t)k24 * (total >> 32)) << 8) + (((uint64_t)k24 * (total & 0xffffffffull)) >> 24);
-    if (total != 0 && excl <= target && target < excl + mine) {
-        uint64_t c = excl;
-        for (int i = lo; i < hi; i++) {
-            c += sample_weight(p, q, i);
-            if (c > target) {
-                ss.found = i;
+    if (total != 0 && base <= target && target < base + mine) {  // wave-uniform
+        uint64_t run = base;  // inclusive prefix before this tile
+        for (int t0 = lo; t0 < hi; t0 += 64) {
+            const int i = t0 + lane;
+            const uint64_t wv = i < hi ? sample_weight(p, q, i) : 0ull;
+            const uint64_t incl = run + wave_incl_scan_u64(wv);
+            const uint64_t hit = __ballot(i < hi && incl > target);
+            if (hit) {
+                if (lane == 0) ss.found = t0 + __ffsll((unsigned long long)hit) - 1;
                 break;
             }
+            run = __shfl(incl, 63);
         }
     }
     __syncthreads();
