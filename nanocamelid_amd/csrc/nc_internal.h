@@ -144,8 +144,11 @@ int launch_accept_greedy(const uint32_t* toks, const uint32_t* preds, int n, int
 
 // ---------------------------------------------------------------- stochastic acceptance
 // probs[r][j] = expf((l_j - max)/temp) * (1 / sum), the sum exact left to right (rows x V).
+// Temperature probabilities of `rows` rows; scratch: temperature_scratch_floats(rows) floats of
+// device memory owned by the caller (stream-ordered reuse).
+size_t temperature_scratch_floats(int rows);
 int launch_temperature_probs(const float* logits, int64_t ld_in, float* probs, int64_t ld_out, int rows, int V,
-                             float temp, hipStream_t st);
+                             float temp, float* scratch, hipStream_t st);
 // p [k+1][ld] target probs, q [k][ld] draft probs, drafts[k] (device); result = {n_accepted,
 // next_token, start_pos + n_accepted + 1}; d_pos (nullable) receives the new position.
 int launch_accept_stochastic(const float* p, const float* q, int64_t ld, const uint32_t* drafts, int k, int V,

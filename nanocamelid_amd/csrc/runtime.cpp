@@ -17,6 +17,8 @@ struct nc_ctx {
     hipStream_t stream = nullptr;
     int32_t* xsum = nullptr;  // grow-only scratch for the operator-level entry points
     size_t xsum_cap = 0;
+    float* tp_scratch = nullptr;  // grow-only scratch of the temperature softmax
+    size_t tp_cap = 0;
 };
 
 struct nc_qmat {
@@ -62,6 +64,7 @@ struct nc_session {
     float* logits = nullptr;  // [B][V]
     float* probs = nullptr;   // [B][V] temperature probabilities of the last pass's rows
     float* qbuf = nullptr;    // [B][V] draft probabilities of the current speculative step
+    float* tp_scratch = nullptr;  // temperature softmax scratch for B rows
     float* part_val = nullptr;
     int32_t* part_idx = nullptr;
     uint32_t* d_toks = nullptr;
@@ -730,7 +733,7 @@ static int verify_step(nc_session* s, int n, int64_t start_pos, nc_verify_result
 // probabilities of every row, then the accept/resample kernel.  q: [n-1][V] draft probs.
 static int accept_stochastic_step(nc_session* s, int n, int64_t start_pos, const float* q, float temp, uint64_t seed) {
     const int V = (int)s->m->cfg.vocab_size;
-    int rc = launch_temperature_probs(s->logits, V, s->probs, V, n, V, temp, s->stream);
+    int rc = launch_temperature_probs(s->logits, V, s->probs, V, n, V, temp, s->tp_scratch, s->stream);
     if (rc) return rc;
     return launch_accept_stochastic(s->probs, q, V, s->d_toks + 1, n - 1, V, seed, start_pos, s->d_result, s->d_pos,
                                     s->stream);
@@ -780,6 +783,7 @@ void nc_ctx_free(nc_ctx* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     if (c->xsum) (void)hipFree(c->xsum);
+    if (c->tp_scratch) (void)hipFree(c->tp_scratch);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -913,7 +917,15 @@ int nc_temperature_probs_batch(nc_ctx* ctx, const float* logits, float* probs, i
     if (!ctx || !logits || !probs || rows < 1 || vocab < 1 || vocab > INT32_MAX || !(temp > 0.0f))
         return fail(NC_EINVAL, "nc_temperature_probs_batch: bad arguments");
     NC_HIP(hipSetDevice(ctx->device));
-    return launch_temperature_probs(logits, vocab, probs, vocab, rows, (int)vocab, temp,
+    const size_t need = temperature_scratch_floats(rows);
+    if (ctx->tp_cap < need) {
+        if (ctx->tp_scratch) NC_HIP(hipFree(ctx->tp_scratch));
+        ctx->tp_scratch = nullptr;
+        ctx->tp_cap = 0;
+        NC_HIP(hipMalloc((void**)&ctx->tp_scratch, need * sizeof(float)));
+        ctx->tp_cap = need;
+    }
+    return launch_temperature_probs(logits, vocab, probs, vocab, rows, (int)vocab, temp, ctx->tp_scratch,
                                     stream ? (hipStream_t)stream : ctx->stream);
 }
 
@@ -998,6 +1010,7 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
         (rc = dev_alloc(s->allocs, &s->logits, (size_t)B * c.vocab_size)) ||
         (rc = dev_alloc(s->allocs, &s->probs, (size_t)B * c.vocab_size)) ||
         (rc = dev_alloc(s->allocs, &s->qbuf, (size_t)B * c.vocab_size)) ||
+        (rc = dev_alloc(s->allocs, &s->tp_scratch, temperature_scratch_floats(B))) ||
         (rc = dev_alloc(s->allocs, &s->part_val, B * m->head.tiles)) ||
         (rc = dev_alloc(s->allocs, &s->part_idx, B * m->head.tiles)) ||
         (rc = dev_alloc(s->allocs, &s->d_toks, B)) || (rc = dev_alloc(s->allocs, &s->d_preds, B)) ||
@@ -1318,7 +1331,8 @@ int nc_generate_speculative_stochastic(nc_session* tg, nc_session* dr, const uin
     dr->stream = tg->stream;
     hipStream_t st = tg->stream;
     // first token: the target's last prompt row, u(seed, n_prompt - 1, bonus)
-    if ((rc = launch_temperature_probs(tg->logits + (size_t)(tg->last_n - 1) * V, V, tg->probs, V, 1, V, temp, st)) ||
+    if ((rc = launch_temperature_probs(tg->logits + (size_t)(tg->last_n - 1) * V, V, tg->probs, V, 1, V, temp,
+                                       tg->tp_scratch, st)) ||
         (rc = launch_sample_probs(tg->probs, V, seed, n_prompt - 1, kPurposeBonus, (uint32_t*)(tg->d_result + 1),
                                          nullptr, st)))
         return rc;
@@ -1342,7 +1356,8 @@ int nc_generate_speculative_stochastic(nc_session* tg, nc_session* dr, const uin
         for (int64_t i = 0; i < kk; i++) {
             if (i == 0 && (rc = upload_toks(dr, &pending, 1))) return rc;
             if ((rc = run_pass(dr, 1, pos + i)) ||
-                (rc = launch_temperature_probs(dr->logits, V, tg->qbuf + (size_t)i * V, V, 1, V, temp, st)) ||
+                (rc = launch_temperature_probs(dr->logits, V, tg->qbuf + (size_t)i * V, V, 1, V, temp,
+                                               tg->tp_scratch, st)) ||
                 (rc = launch_sample_probs(tg->qbuf + (size_t)i * V, V, seed, pos + i, kPurposeDraft, tg->d_toks + 1 + i,
                                           dr->d_toks, st)))
                 return rc;

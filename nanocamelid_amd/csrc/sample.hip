@@ -64,37 +64,72 @@ __device__ inline float wave_max(float v) {
     return v;
 }
 
-// One workgroup per row: probs[row][j] = p_j for j < V.
-__global__ __launch_bounds__(kSmT) void temperature_probs_kernel(const float* logits, int64_t ld_in, float* probs,
-                                                                 int64_t ld_out, int V, float temp) {
+// The order-free passes (max, e_j, p_j = e_j * (1/S)) run on kTpCh workgroups per row; only
+// the exact sequential sum S runs on one workgroup per row.  e_j is kept in the output row
+// between the passes.  scratch: per row kTpCh chunk maxima, then 1/S.
+constexpr int kTpCh = 64;
+constexpr int kTpT = 256;
+
+__device__ inline int tp_chunk(int V) { return (V + kTpCh - 1) / kTpCh; }
+
+__global__ __launch_bounds__(kTpT) void tp_max_kernel(const float* logits, int64_t ld_in, int V, float* scratch) {
+    __shared__ float wm[kTpT / 64];
+    const int row = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+    const float* l = logits + (size_t)row * ld_in;
+    const int lo = min(c * tp_chunk(V), V), hi = min(lo + tp_chunk(V), V);
+    float mx = -INFINITY;
+    for (int i = lo + t; i < hi; i += kTpT) mx = fmaxf(mx, l[i]);
+    mx = wave_max(mx);
+    if ((t & 63) == 0) wm[t >> 6] = mx;
+    __syncthreads();
+    if (t == 0) {
+#pragma unroll
+        for (int w = 1; w < kTpT / 64; w++) mx = fmaxf(mx, wm[w]);
+        scratch[(size_t)row * (kTpCh + 1) + c] = mx;
+    }
+}
+
+// e_j = expf((l_j - max) / T) (inference.rs:4857-4862), written to the output row.  The max
+// does not depend on evaluation order (finite logits; +-0 give identical terms).
+__global__ __launch_bounds__(kTpT) void tp_exp_kernel(const float* logits, int64_t ld_in, float* probs, int64_t ld_out,
+                                                      int V, float temp, const float* scratch) {
+    const int row = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+    const float* pm = scratch + (size_t)row * (kTpCh + 1);
+    static_assert(kTpCh == 64, "one chunk maximum per lane");
+    float mx = pm[t & 63];
+    mx = wave_max(mx);  // every wave reduces all kTpCh chunk maxima
+    const float* l = logits + (size_t)row * ld_in;
+    float* e = probs + (size_t)row * ld_out;
+    const int lo = min(c * tp_chunk(V), V), hi = min(lo + tp_chunk(V), V);
+    for (int i = lo + t; i < hi; i += kTpT) e[i] = expf_glibc((l[i] - mx) / temp);
+}
+
+// S = sum e_j left to right, one exact segment of kSmSeg terms at a time; scratch gets 1/S.
+__global__ __launch_bounds__(kSmT) void tp_sum_kernel(const float* probs, int64_t ld_out, int V, float* scratch) {
     __shared__ ChainScratch<kSmT> sc;
     __shared__ __align__(16) float a_lds[kSmSeg];
-    __shared__ float wmax[kSmT / 64];
-    const float* l = logits + (size_t)blockIdx.x * ld_in;
-    float* out = probs + (size_t)blockIdx.x * ld_out;
+    const float* e = probs + (size_t)blockIdx.x * ld_out;
     const int t = threadIdx.x;
-    // max is independent of evaluation order (finite logits; +-0 give identical terms)
-    float mx = -INFINITY;
-    for (int i = t; i < V; i += kSmT) mx = fmaxf(mx, l[i]);
-    mx = wave_max(mx);
-    if ((t & 63) == 0) wmax[t >> 6] = mx;
-    __syncthreads();
-    mx = wmax[0];
-#pragma unroll
-    for (int w = 1; w < kSmT / 64; w++) mx = fmaxf(mx, wmax[w]);
-    // S = sum e_j left to right, one exact segment of kSmSeg terms at a time
     float sum = 0.0f;
     for (int base = 0; base < V; base += kSmSeg) {
         float a[kSmE];
 #pragma unroll
         for (int j = 0; j < kSmE; j++) {
             const int i = base + t * kSmE + j;
-            a[j] = i < V ? expf_glibc((l[i] - mx) / temp) : 0.0f;
+            a[j] = i < V ? e[i] : 0.0f;
         }
         sum = exact_chain_sum<kSmE, kSmT>(a, sc, a_lds, sum);
     }
-    const float inv = 1.0f / sum;
-    for (int i = t; i < V; i += kSmT) out[i] = expf_glibc((l[i] - mx) / temp) * inv;
+    if (t == 0) scratch[(size_t)blockIdx.x * (kTpCh + 1) + kTpCh] = 1.0f / sum;
+}
+
+// p_j = e_j * (1 / S) (inference.rs:3535-3539), in place.
+__global__ __launch_bounds__(kTpT) void tp_norm_kernel(float* probs, int64_t ld_out, int V, const float* scratch) {
+    const int row = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+    const float inv = scratch[(size_t)row * (kTpCh + 1) + kTpCh];
+    float* e = probs + (size_t)row * ld_out;
+    const int lo = min(c * tp_chunk(V), V), hi = min(lo + tp_chunk(V), V);
+    for (int i = lo + t; i < hi; i += kTpT) e[i] = e[i] * inv;
 }
 
 // ---------------------------------------------------------------- fixed-point sampler
@@ -224,10 +259,17 @@ __global__ __launch_bounds__(kSpT) void sample_probs_kernel(const float* probs, 
     }
 }
 
+size_t temperature_scratch_floats(int rows) { return (size_t)rows * (kTpCh + 1); }
+
 int launch_temperature_probs(const float* logits, int64_t ld_in, float* probs, int64_t ld_out, int rows, int V,
-                             float temp, hipStream_t st) {
+                             float temp, float* scratch, hipStream_t st) {
     if (rows < 1 || V < 1 || !(temp > 0.0f)) return fail(NC_EINVAL, "temperature probs: rows, vocab and temp must be > 0");
-    hipLaunchKernelGGL(temperature_probs_kernel, dim3(rows), dim3(kSmT), 0, st, logits, ld_in, probs, ld_out, V, temp);
+    if (!scratch) return fail(NC_EINVAL, "temperature probs: no scratch");
+    const dim3 grid(kTpCh, rows);
+    hipLaunchKernelGGL(tp_max_kernel, grid, dim3(kTpT), 0, st, logits, ld_in, V, scratch);
+    hipLaunchKernelGGL(tp_exp_kernel, grid, dim3(kTpT), 0, st, logits, ld_in, probs, ld_out, V, temp, scratch);
+    hipLaunchKernelGGL(tp_sum_kernel, dim3(rows), dim3(kSmT), 0, st, probs, ld_out, V, scratch);
+    hipLaunchKernelGGL(tp_norm_kernel, grid, dim3(kTpT), 0, st, probs, ld_out, V, scratch);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
