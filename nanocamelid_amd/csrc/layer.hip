@@ -394,17 +394,17 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
     // are buffer loads whose quad offset is wave-uniform (scalar registers) and clamped, so
     // they are unconditional, need no per-lane address arithmetic, and keep the wait counts
     // exact; each batch's loads are pinned in order.  The batch's probabilities are read
-    // from LDS one batch ahead, so neither latency is exposed in the chain.  D = 2 measured
-    // as fast as deeper rings for a single unit and faster when many units share the chip
-    // (fewer registers, more resident workgroups).
+    // from LDS one batch ahead, so neither latency is exposed in the chain.  V rows come from
+    // HBM (a decode step streams the weights between two reads of a layer's cache), where
+    // three batches in flight (D = 4) run the chain at ~17 cycles per position against ~25
+    // for one; with the rows hot in L2 the two are equal.
     constexpr int HDv = HD;
     typedef float f4v __attribute__((ext_vector_type(4)));
     const char* vbase = (const char*)(a.vcache + (size_t)kvh * a.max_ctx * HD);
-    const char* vlane = vbase + t * 16;  // this lane's dim in quad 0 (tail loop)
     const __amdgpu_buffer_rsrc_t vres =
         __builtin_amdgcn_make_buffer_rsrc((void*)vbase, 0, a.max_ctx * HD * 4, 0x00020000);
     const int voff = t * 16;
-    constexpr int B = 8, D = 2;
+    constexpr int B = 8, D = 4;
     static_assert(D % 2 == 0, "probability slots follow the unrolled batch index");
     const int nq = L >> 2;    // whole position quads
     const int nbt = nq / B;   // whole batches
@@ -449,19 +449,27 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
 #undef NC_PV_PROBS
 #undef NC_PV_LOAD
     }
-    const f4v* vq = (const f4v*)vlane;  // [quad] stride HD f4v
-    for (int q = nbt * B; q < nq; q++) {
-        const f4v v = vq[(size_t)q * HDv];
-        acc = acc + probs[4 * q] * v.x;
-        acc = acc + probs[4 * q + 1] * v.y;
-        acc = acc + probs[4 * q + 2] * v.z;
-        acc = acc + probs[4 * q + 3] * v.w;
-    }
-    if (nq * 4 < L) {  // 1..3 positions of a last partial quad, each added only if it exists
-        const f4v v = vq[(size_t)nq * HDv];
-        acc = acc + probs[4 * nq] * v.x;
-        if (nq * 4 + 1 < L) acc = acc + probs[4 * nq + 1] * v.y;
-        if (nq * 4 + 2 < L) acc = acc + probs[4 * nq + 2] * v.z;
+    {
+        // the remaining whole quads (fewer than B) and the last partial quad: one batch of
+        // loads (quads clamped to the last one holding a position) and probabilities, then
+        // the chain; a position past the row leaves acc unchanged (a select, not a branch)
+        const int q0 = nbt * B;
+        const int qlast = (L - 1) >> 2;
+        f4v tv[B], tp[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const int q = min(q0 + j, qlast);
+            tv[j] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(vres, voff, q * (HD * 16), 0));
+            tp[j] = *(const f4v*)&probs[4 * q];
+        }
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const int p0 = (q0 + j) * 4;
+            acc = p0 < L ? acc + tp[j].x * tv[j].x : acc;
+            acc = p0 + 1 < L ? acc + tp[j].y * tv[j].y : acc;
+            acc = p0 + 2 < L ? acc + tp[j].z * tv[j].z : acc;
+            acc = p0 + 3 < L ? acc + tp[j].w * tv[j].w : acc;
+        }
     }
     const int aw = a.H * HDv;
     const int col = h * HDv + (t & ~31);

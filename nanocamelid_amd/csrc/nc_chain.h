@@ -22,7 +22,7 @@
 //     "sensitive" (typically the ~12 that contain a binade crossing of the growing sum).
 //  3. C_t = s0 + sum of the earlier D (block scan in double): the start of segment t if no
 //     earlier segment were sensitive.
-//  4. Walk.  One thread visits the sensitive segments in order: it advances the true chain
+//  4. Walk.  One wave visits the sensitive segments in order: it advances the true chain
 //     value over the insensitive segments in between (their increments add exactly),
 //     evaluates the sensitive segment term by term, and records the correction
 //     shift_k = (true end) - (C_k + D_k).  A segment's start is then C_t + shift of the last
@@ -204,7 +204,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
     int off, total_s;
     const double cstart = (double)s0 + block_excl_scan_f64_i32<T>(d, sens ? 1 : 0, sc.dtot, sc.itot, &off, &total_s);
 
-    // 4. sensitive list in ascending order, then the walk (one thread)
+    // 4. sensitive list in ascending order, then the walk (one wave)
     const bool listed = total_s <= kChainMaxSensitive;
     if (listed && sens) {
         ChainEntry& ce = sc.ent[off];
@@ -213,18 +213,35 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
         ce.seg = t;
     }
     __syncthreads();
-    if (listed && t == 0) {
-        float S = s0;         // true chain value at the end of the last walked segment
-        double cl = (double)s0;  // its uncorrected counterpart
-        for (int e = 0; e < total_s; e++) {
-            const double cs = sc.ent[e].cstart, ce = sc.ent[e].cend;
-            const float* ap = a_lds + sc.ent[e].seg * E;
-            // insensitive segments in between keep their shift: the advance is exact
-            S = S + (float)(cs - cl);
+    if (listed && t < 64) {
+        // wave 0: lane q holds entry e0 + q (its advance over the insensitive segments before
+        // it, which is exact, and its E terms); the chain then visits the entries in order
+        // with wave-uniform reads (v_readlane), so only the dependent adds are serial
+        float S = s0;  // true chain value at the end of the last walked segment
+        for (int e0 = 0; e0 < total_s; e0 += 64) {
+            const int me = e0 + t;
+            const int cnt = min(64, total_s - e0);
+            float adv = 0.0f, trm[E];
+            double ce = 0.0;
 #pragma unroll
-            for (int j = 0; j < E; j++) S = S + ap[j];
-            sc.ent[e].shift = (double)S - ce;
-            cl = ce;
+            for (int j = 0; j < E; j++) trm[j] = 0.0f;
+            if (me < total_s) {
+                const double cs = sc.ent[me].cstart;
+                ce = sc.ent[me].cend;
+                const double cl = me == 0 ? (double)s0 : sc.ent[me - 1].cend;
+                adv = (float)(cs - cl);
+                const float* ap = a_lds + sc.ent[me].seg * E;
+#pragma unroll
+                for (int j = 0; j < E; j++) trm[j] = ap[j];
+            }
+            float mine = 0.0f;
+            for (int q = 0; q < cnt; q++) {  // q is wave-uniform
+                S = S + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(adv), q));
+#pragma unroll
+                for (int j = 0; j < E; j++) S = S + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(trm[j]), q));
+                mine = t == q ? S : mine;
+            }
+            if (me < total_s) sc.ent[me].shift = (double)mine - ce;
         }
     }
     __syncthreads();
