@@ -440,7 +440,6 @@ __global__ __launch_bounds__(64 * S * TPG) void gemm_q4_0_r16_kernel(GemmParams 
     constexpr int BR = 4 * QR;               // blocks per round
     constexpr int NP = (NMAX + 1) / 2;       // token-pair activation dwords per block
     constexpr int NM = (NMAX + 7) / 8;       // meta dwords per block
-    constexpr int SW = U == 4 ? 2 : 1;       // scale dwords per wave round
     extern __shared__ float lds_all[];       // per tile group: [2][BR][NMAX][16]
     const int wave_all = wave_id_uniform();
     const int sub = wave_all / S;            // tile of the group (TPG = 4)
@@ -457,7 +456,7 @@ __global__ __launch_bounds__(64 * S * TPG) void gemm_q4_0_r16_kernel(GemmParams 
     const int nrounds = (nq + QR - 1) / QR;
 
     uint4 rw[D][U];
-    uint32_t rs[D][SW];
+    uint32_t rs[D][U];
     int rx[D][U][NP], rm[D][U][NM];
     // Unconditional loads (see the R64 kernel): exact wait counts across the ring.  Weights
     // and activations are buffer loads.  The weight chunk offset is wave-uniform (scalar) and
@@ -471,7 +470,7 @@ __global__ __launch_bounds__(64 * S * TPG) void gemm_q4_0_r16_kernel(GemmParams 
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, 0, N * p.K, 0x00020000);
     const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs, 0, N * nb * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t s8res = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs8, 0, N * nb * 4, 0x00020000);
-    const int wvo = lane * 16;
+    const int wvo = lane * 16, svo = lane * 2;  // a quad's nibbles, then its 64 scales
     int xvo[NP], mvo[NM], mt[NM];
 #pragma unroll
     for (int q = 0; q < NP; q++) xvo[q] = (2 * q + xtok) * p.K + 32 * j + 4 * (i16 & 7);
@@ -490,17 +489,10 @@ __global__ __launch_bounds__(64 * S * TPG) void gemm_q4_0_r16_kernel(GemmParams 
     do {                                                                                             \
         const int qd0_ = min(min((R), nrounds - 1) * QR + wave * U, qmax);                           \
         const int cb_ = (qd0_ >> 3) * kQ40ChunkBytes;                                                \
-        _Pragma("unroll") for (int u = 0; u < U; u++) rw[SLOT][u] = __builtin_bit_cast(               \
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wvo, cb_ + ((qd0_ + u) & 7) * 1024, 0)); \
-        const int so_ = cb_ + 8192 + (qd0_ & 7) * 2;                                                 \
-        if constexpr (SW == 2) {                                                                     \
-            const uint2 s2_ = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wres, wvo, so_, 0)); \
-            rs[SLOT][0] = s2_.x;                                                                     \
-            rs[SLOT][SW - 1] = s2_.y;                                                                \
-        } else if constexpr (U == 2) {                                                               \
-            rs[SLOT][0] = __builtin_amdgcn_raw_buffer_load_b32(wres, wvo, so_, 0);                   \
-        } else {                                                                                     \
-            rs[SLOT][0] = __builtin_amdgcn_raw_buffer_load_b16(wres, wvo, so_, 0);                   \
+        _Pragma("unroll") for (int u = 0; u < U; u++) {                                              \
+            const int qo_ = cb_ + ((qd0_ + u) & 7) * kQ40R16QuadBytes;                               \
+            rw[SLOT][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wvo, qo_, 0)); \
+            rs[SLOT][u] = __builtin_amdgcn_raw_buffer_load_b16(wres, svo, qo_ + 1024, 0);            \
         }                                                                                            \
         _Pragma("unroll") for (int u = 0; u < U; u++) {                                              \
             _Pragma("unroll") for (int q = 0; q < NP; q++) rx[SLOT][u][q] = (int)                     \
@@ -539,8 +531,7 @@ __global__ __launch_bounds__(64 * S * TPG) void gemm_q4_0_r16_kernel(GemmParams 
                                            (int)(v.z & 0x0F0F0F0Fu), (int)(v.w & 0x0F0F0F0Fu)};
                         const int hi[4] = {(int)((v.x >> 4) & 0x0F0F0F0Fu), (int)((v.y >> 4) & 0x0F0F0F0Fu),
                                            (int)((v.z >> 4) & 0x0F0F0F0Fu), (int)((v.w >> 4) & 0x0F0F0F0Fu)};
-                        const uint32_t sw = rs[k][(u >> 1) & (SW - 1)];
-                        const float ws = f16_to_f32((uint16_t)((u & 1) ? (sw >> 16) : (sw & 0xffff)));
+                        const float ws = f16_to_f32((uint16_t)rs[k][u]);
                         float* dst = buf + ((size_t)((wave * U + u) * 4 + j) * NMAX) * 16 + i16;
                         float t[NMAX];
                         terms_q40<NMAX>(t, rx[k][u], rm[k][u], lo, hi, ws);
@@ -860,7 +851,7 @@ __global__ void blockdots_q4_0_kernel(const uint8_t* w, int groups, int r16, int
         const uint8_t* nib;
         if (r16) {
             const int qd = b / 4, lane = 16 * (b & 3) + (r & 15);
-            nib = w + ((size_t)(r / 16) * groups + qd / 8) * kQ40ChunkBytes + (qd & 7) * 1024 + lane * 16;
+            nib = w + ((size_t)(r / 16) * groups + qd / 8) * kQ40ChunkBytes + (qd & 7) * kQ40R16QuadBytes + lane * 16;
         } else {
             nib = w + ((size_t)(r / 64) * groups + b / 8) * kQ40ChunkBytes + (b & 7) * 1024 + (r & 63) * 16;
         }

@@ -36,10 +36,12 @@ constexpr int kQ4KChunkBytes = 9 * 1024;
 
 // Q4_0 "R16" layout (matrices with fewer than 512 64-row tiles, so that a launch still
 // spans every CU): rows padded to 16-row tiles; blocks taken in quads (block b = 4*qd + j)
-// and groups of 8 quads.  Per (tile16, group) a 9216-byte chunk: 8 x [64 lanes x 16 B
-// nibbles] with lane = 16*j + r holding block 4*qd + j of row 16*tile + r, then [64 lanes x
-// 8 f16 scales] (one per quad of the group).  One wave load covers 4 blocks x 16 rows.
+// and groups of 8 quads.  Per (tile16, group) a 9216-byte chunk of 8 quads, each 1152 bytes:
+// [64 lanes x 16 B nibbles] with lane = 16*j + r holding block 4*qd + j of row 16*tile + r,
+// then [64 lanes x 1 f16 scale] of the same blocks.  One wave load covers 4 blocks x 16 rows
+// and its scales are one contiguous 128-byte line.
 constexpr int kTileRowsR16 = 16;
+constexpr int kQ40R16QuadBytes = 1024 + 128;  // 1152; 8 per chunk = kQ40ChunkBytes
 enum Layout : int { LAYOUT_R64 = 0, LAYOUT_R16 = 1, LAYOUT_R16K = 2 };  // R16K: Q4_K on 16-row tiles
 
 struct QMatDev {

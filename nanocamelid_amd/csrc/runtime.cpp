@@ -162,9 +162,9 @@ void repack_q4_0_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t
             for (int64_t b = 0; b < nb; b++) {
                 const uint8_t* blk = src + (r * nb + b) * 18;
                 const int64_t qd = b / 4, j = b % 4, lane = 16 * j + rr;
-                uint8_t* chunk = dst + (t * groups + qd / 8) * kQ40ChunkBytes;
-                std::memcpy(chunk + (qd % 8) * 1024 + lane * 16, blk + 2, 16);
-                std::memcpy(chunk + 8192 + lane * 16 + (qd % 8) * 2, blk, 2);
+                uint8_t* quad = dst + (t * groups + qd / 8) * kQ40ChunkBytes + (qd % 8) * kQ40R16QuadBytes;
+                std::memcpy(quad + lane * 16, blk + 2, 16);
+                std::memcpy(quad + 1024 + lane * 2, blk, 2);
             }
         }
     });
