@@ -279,7 +279,7 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
         const int u0_ = b0_ & 7;                                                                    \
         _Pragma("unroll") for (int u = 0; u < U; u++) rw[SLOT][u] =                                 \
             *(const uint4*)(chunk_ + (u0_ + u) * 1024 + lane * 16);                                 \
-        rs[SLOT] = *(const uint2*)(chunk_ + 8192 + lane * 16 + u0_ * 2);                            \
+        rs[SLOT] = *(const uint2*)(chunk_ + 8192 + (u0_ >> 2) * 512 + lane * 8);                    \
         _Pragma("unroll") for (int u = 0; u < U; u++) {                                             \
             const int b_ = min(b0_ + u, nb - 1);                                                    \
             _Pragma("unroll") for (int q = 0; q < NP; q++) {                                        \

@@ -25,8 +25,9 @@ int fail(int code, const std::string& msg);
 
 // ---------------------------------------------------------------- weight layouts
 // Q4_0 device layout ("tile-group"): rows padded to 64-row tiles; per (tile, group of 8
-// blocks) a 9216-byte chunk = 8 x [64 lanes x 16 B nibbles] followed by [64 lanes x 8 f16
-// scales].  Lane l of a wave loads row 64*tile + l; every load is 1 KB contiguous.
+// blocks) a 9216-byte chunk = 8 x [64 lanes x 16 B nibbles] followed by the f16 scales as
+// 2 x [64 lanes x 4 scales] (blocks 0-3, then 4-7).  Lane l of a wave loads row 64*tile + l;
+// a round of 4 blocks reads 4 KB of nibbles and 512 contiguous bytes of scales.
 constexpr int kTileRows = 64;
 constexpr int kQ40GroupBlocks = 8;
 constexpr int kQ40ChunkBytes = kQ40GroupBlocks * 1024 + 1024;  // 9216

@@ -141,7 +141,7 @@ void repack_q4_0(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* ds
                 const uint8_t* blk = src + (r * nb + b) * 18;
                 uint8_t* chunk = dst + (t * groups + b / 8) * kQ40ChunkBytes;
                 std::memcpy(chunk + (b % 8) * 1024 + l * 16, blk + 2, 16);
-                std::memcpy(chunk + 8192 + l * 16 + (b % 8) * 2, blk, 2);
+                std::memcpy(chunk + 8192 + (b % 8 / 4) * 512 + l * 8 + (b % 4) * 2, blk, 2);
             }
         }
     });
