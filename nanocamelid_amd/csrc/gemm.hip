@@ -941,13 +941,26 @@ int launch_r16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
             hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, TPG>), dim3(p.ntiles / TPG), dim3(64 * S * TPG),
                                lds, st, p);
     } else {
-        constexpr int S = 8;  // two waves per SIMD hide each other's dependency latency
-        const size_t lds = (size_t)2 * 4 * S * U * NMAX * 16 * sizeof(float);
-        if (ev0)
-            hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1>), dim3(p.ntiles), dim3(64 * S), lds, st,
-                                  ev0, ev1, 0, p);
-        else
-            hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+        // 8 waves (two per SIMD hide each other's dependency latency); 16 when K is long
+        // (at least 64 quads): half the rounds, each with its barrier and chain step
+        // (4096 x 14336 at N = 5: 11.81 -> 10.44 us; 6144 x 4096 is slower with 16), for
+        // widths whose round buffers stay within 48 KB of LDS
+        auto go = [&]<int S>() {
+            const size_t lds = (size_t)2 * 4 * S * U * NMAX * 16 * sizeof(float);
+            if (ev0)
+                hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1>), dim3(p.ntiles), dim3(64 * S), lds,
+                                      st, ev0, ev1, 0, p);
+            else
+                hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+        };
+        if constexpr (NMAX <= 6) {
+            if ((p.units + 3) / 4 >= 64)
+                go.template operator()<16>();
+            else
+                go.template operator()<8>();
+        } else {
+            go.template operator()<8>();
+        }
     }
     NC_HIP(hipGetLastError());
     return NC_OK;
