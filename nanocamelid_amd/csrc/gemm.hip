@@ -85,7 +85,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const float* 
                     p.q_out[(size_t)n * p.aw + rr] = v;
                 } else {
                     const int kvh = rr / p.hd, d = rr % p.hd;
-                    if (is_k) p.kcache[((size_t)kvh * p.max_ctx + pos) * p.hd + d] = v;
+                    if (is_k) p.kcache[(((size_t)kvh * (p.hd / 4) + d / 4) * p.max_ctx + pos) * 4 + (d & 3)] = v;
                     else p.vcache[(((size_t)kvh * (p.max_ctx / 4) + pos / 4) * p.hd + d) * 4 + (pos & 3)] = v;
                 }
                 break;
@@ -397,7 +397,7 @@ __device__ __forceinline__ void gemm_epilogue_r16(const GemmParams& p, float v, 
                 p.q_out[(size_t)n * p.aw + rr] = v;
             } else {
                 const int kvh = rr / p.hd, d = rr % p.hd;
-                if (is_k) p.kcache[((size_t)kvh * p.max_ctx + pos) * p.hd + d] = v;
+                if (is_k) p.kcache[(((size_t)kvh * (p.hd / 4) + d / 4) * p.max_ctx + pos) * 4 + (d & 3)] = v;
                 else p.vcache[(((size_t)kvh * (p.max_ctx / 4) + pos / 4) * p.hd + d) * 4 + (pos & 3)] = v;
             }
             break;

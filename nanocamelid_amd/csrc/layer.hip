@@ -280,10 +280,12 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(AttnParams a) {
         __syncthreads();  // previous tile's readers are done with kt
         if (tile * 64 > pos0 + min(a.N, ((int)blockIdx.z + 1) * RB) - 1) break;  // no row of this block reaches it
         const int rows = min(64, last + 1 - tile * 64);
-        const float4* src = (const float4*)(a.kcache + ((size_t)kvh * a.max_ctx + (size_t)tile * 64) * HD);
+        // keys are stored as dim quads [HD/4][max_ctx][4]: quad c of the tile's rows is
+        // 16 * rows contiguous bytes
+        const float4* src = (const float4*)a.kcache + (size_t)kvh * (HD / 4) * a.max_ctx + (size_t)tile * 64;
         for (int i = threadIdx.x; i < rows * (HD / 4); i += blockDim.x) {
-            const int r = i / (HD / 4), c = i % (HD / 4);
-            *(float4*)&kt[r * RS + c * 4] = src[(size_t)r * (HD / 4) + c];
+            const int c = i / rows, r = i % rows;
+            *(float4*)&kt[r * RS + c * 4] = src[(size_t)c * a.max_ctx + r];
         }
         __syncthreads();
         const int p = tile * 64 + lane;
@@ -371,23 +373,12 @@ __device__ __forceinline__ void softmax_row(const float* srow, int L, float (&pr
     for (int j = 0; j < E; j++) pr[j] = e[j] * inv;
 }
 
-template <int E, int T, int HD>
-__global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
-    __shared__ ChainScratch<T> sc;
-    __shared__ __align__(16) float probs[T * E];
-    __shared__ float red[T / 64];
-    const int unit = blockIdx.x;
-    const int n = unit / a.H, h = unit % a.H;
-    const int kvh = h / (a.H / a.Hkv);
-    const int L = a.d_pos[0] + n + 1;
+// The weighted V sum of unit (n, h) over positions 0..L-1 (probabilities in LDS) and the
+// Q8_0 quantisation of its output block; threads past the head dim return at once.
+template <int HD>
+__device__ __forceinline__ void weighted_v_q8(const AttnParams& a, int n, int h, int kvh, int L, const float* probs) {
     const int t = threadIdx.x;
-    const float* srow = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
-    float pr[E];
-    softmax_row<E, T>(srow, L, pr, sc, probs, red);
-#pragma unroll
-    for (int j = 0; j < E; j++) probs[t * E + j] = pr[j];
-    __syncthreads();
-    if (t >= HD) return;  // no barriers below
+    if (t >= HD) return;
     // Weighted V sum, lane = output dim t.  V is stored in position quads: one 16-byte load
     // brings positions 4q..4q+3 of this lane's dim (consecutive lanes read consecutive 16
     // bytes).  A ring of D batches of B quads keeps (D-1)*B*4 positions in flight.  The loads
@@ -477,11 +468,128 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
                    a.xs8 + (size_t)n * (aw / 32) + col / 32);
 }
 
+template <int E, int T, int HD>
+__global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
+    __shared__ ChainScratch<T> sc;
+    __shared__ __align__(16) float probs[T * E];
+    __shared__ float red[T / 64];
+    const int unit = blockIdx.x;
+    const int n = unit / a.H, h = unit % a.H;
+    const int kvh = h / (a.H / a.Hkv);
+    const int L = a.d_pos[0] + n + 1;
+    const int t = threadIdx.x;
+    const float* srow = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
+    float pr[E];
+    softmax_row<E, T>(srow, L, pr, sc, probs, red);
+#pragma unroll
+    for (int j = 0; j < E; j++) probs[t * E + j] = pr[j];
+    __syncthreads();
+    weighted_v_q8<HD>(a, n, h, kvh, L, probs);  // no barriers below
+}
+
+// Attention of one (row n, head h) unit in one kernel, for rows of at most T*E <= 1024
+// positions: the scores (as attn_scores_kernel: dot from -0.0 over the head dims in order,
+// then * scale) go to LDS, then the softmax and the weighted V sum as attn_softmax_pv_kernel.
+// Thread t scores positions t, t + T, ..., so a wave's key loads are consecutive positions:
+// keys are stored as dim quads [HD/4][max_ctx][4], one 16-byte load brings 4 dims of a
+// position and a wave load is 1 KB contiguous.  A ring of KD dim quads of loads is in
+// flight; a position past the row reads outside the buffer (0, no memory access) and its
+// score is not stored.
+template <int E, int T, int HD>
+__global__ __launch_bounds__(T) void attn_fused_kernel(AttnParams a) {
+    static_assert(T * E <= 1024, "rows up to 1024 positions");
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    __shared__ ChainScratch<T> sc;
+    __shared__ __align__(16) float probs[T * E];  // scores, then probabilities
+    __shared__ float red[T / 64];
+    __shared__ __align__(16) float qs[HD];
+    const int unit = blockIdx.x;
+    const int n = unit / a.H, h = unit % a.H;
+    const int kvh = h / (a.H / a.Hkv);
+    const int L = a.d_pos[0] + n + 1;
+    const int t = threadIdx.x;
+    if (t < HD) qs[t] = a.q[((size_t)n * a.H + h) * HD + t];
+    const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.kcache + (size_t)kvh * a.max_ctx * HD), 0, a.max_ctx * HD * 4, 0x00020000);
+    int koff[E];
+#pragma unroll
+    for (int m = 0; m < E; m++) koff[m] = t + T * m < L ? (t + T * m) * 16 : 0x40000000;
+    const int qstride = a.max_ctx * 16;  // bytes between dim quads
+    constexpr int KD = E <= 2 ? 8 : 4;   // dim quads in the ring (4 x E loads at E = 4: registers)
+    constexpr int NQ = HD / 4;
+    static_assert(NQ % KD == 0, "ring divides the dim quads");
+    f4v kr[KD][E];
+#define NC_K_LOAD(I, SLOT)                                                                              \
+    {                                                                                                   \
+        const int so_ = min((I), NQ - 1) * qstride;                                                     \
+        _Pragma("unroll") for (int m = 0; m < E; m++) kr[SLOT][m] =                                     \
+            __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(kres, koff[m], so_, 0));       \
+        __builtin_amdgcn_sched_barrier(0);                                                              \
+    }
+#pragma unroll
+    for (int k = 0; k < KD - 1; k++) NC_K_LOAD(k, k)
+    __syncthreads();  // q in LDS
+    float dot[E];
+#pragma unroll
+    for (int m = 0; m < E; m++) dot[m] = -0.0f;
+#pragma unroll 1
+    for (int i0 = 0; i0 < NQ; i0 += KD) {
+#pragma unroll
+        for (int k = 0; k < KD; k++) {
+            const int i = i0 + k;
+            NC_K_LOAD(i + KD - 1, (k + KD - 1) % KD)
+            const f4v qv = *(const f4v*)&qs[4 * i];
+#pragma unroll
+            for (int m = 0; m < E; m++) {
+                const f4v kv = kr[k][m];
+                dot[m] = dot[m] + qv.x * kv.x;
+                dot[m] = dot[m] + qv.y * kv.y;
+                dot[m] = dot[m] + qv.z * kv.z;
+                dot[m] = dot[m] + qv.w * kv.w;
+            }
+        }
+    }
+#undef NC_K_LOAD
+#pragma unroll
+    for (int m = 0; m < E; m++)
+        if (t + T * m < L) probs[t + T * m] = dot[m] * a.scale;
+    __syncthreads();
+    float pr[E];
+    softmax_row<E, T>(probs, L, pr, sc, probs, red);
+#pragma unroll
+    for (int j = 0; j < E; j++) probs[t * E + j] = pr[j];
+    __syncthreads();
+    weighted_v_q8<HD>(a, n, h, kvh, L, probs);  // no barriers below
+}
+
 int launch_attention(const AttnParams& a, hipStream_t st) {
     const int G = a.H / a.Hkv;
     if (G > 8 || a.H % a.Hkv) return fail(NC_EINVAL, "attention: at most 8 query heads per KV head supported");
     const int tiles = (a.max_pos + 64) / 64;
     if (a.hd != 64 && a.hd != 128) return fail(NC_EINVAL, "attention: head_dim must be 64 or 128");
+    // max_pos + 1 is the longest score row of the pass
+    const int len = a.max_pos + 1;
+    const dim3 grid(a.N * a.H);
+    if (len <= 1024) {
+        // one kernel per pass: each (row, head) unit scores its own keys (short rows: the
+        // units of a KV head re-read its keys from L2, which costs less than a second launch
+        // and the scores' round trip through memory)
+#define NC_FUSED(E)                                                                                  \
+    if (a.hd == 128) hipLaunchKernelGGL((attn_fused_kernel<E, 256, 128>), grid, dim3(256), 0, st, a); \
+    else hipLaunchKernelGGL((attn_fused_kernel<E, 256, 64>), grid, dim3(256), 0, st, a);
+        if (len <= 256) {
+            NC_FUSED(1)
+        } else if (len <= 512) {
+            NC_FUSED(2)
+        } else {
+            NC_FUSED(4)
+        }
+#undef NC_FUSED
+        NC_HIP(hipGetLastError());
+        return NC_OK;
+    }
+    // longer rows: scores by (KV head, 64-position tile) blocks that share each key tile
+    // between the query heads and rows of a group, then one kernel for softmax and V sum
     // rows per block: one or two interleaved dot chains per lane; row groups are spread over
     // blockIdx.z so that every SIMD gets a short chain instead of a few SIMDs getting long ones
     const int rb = a.N >= 2 ? 2 : 1;
@@ -502,19 +610,10 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
 #undef NC_SCORES_HD
 #undef NC_SCORES
     NC_HIP(hipGetLastError());
-    // max_pos + 1 is the longest score row of the pass
-    const int len = a.max_pos + 1;
-    const dim3 grid(a.N * a.H);
 #define NC_PV(E, T)                                                                              \
     if (a.hd == 128) hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 128>), grid, dim3(T), 0, st, a); \
     else hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 64>), grid, dim3(T), 0, st, a);
-    if (len <= 256) {
-        NC_PV(1, 256)
-    } else if (len <= 512) {
-        NC_PV(2, 256)
-    } else if (len <= 1024) {
-        NC_PV(4, 256)
-    } else if (len <= 2048) {
+    if (len <= 2048) {
         NC_PV(8, 256)
     } else if (len <= 4096) {
         NC_PV(16, 256)

@@ -97,7 +97,7 @@ struct GemmParams {
     float* q_out = nullptr;
     int aw = 0, kw = 0, hd = 0, rope_half = 0, max_ctx = 0, kv_heads = 0;
     const float* rope_tab = nullptr;  // [max_ctx][rope_half][2] = (sin, cos)
-    float* kcache = nullptr;          // layer base of [kv_heads][max_ctx][hd]
+    float* kcache = nullptr;          // layer base of [kv_heads][hd/4][max_ctx][4] (dim quads)
     float* vcache = nullptr;          // layer base of [kv_heads][max_ctx/4][hd][4] (position quads)
     const int32_t* d_pos = nullptr;   // start position of row 0
     // EPI_SWIGLU_Q8
@@ -129,7 +129,7 @@ int launch_set_pass_state(int32_t* d_pos, int32_t pos, uint32_t* d_toks, const u
 int launch_embed(const float* table, const uint32_t* toks, int N, int d, float* hidden, hipStream_t stream);
 struct AttnParams {
     const float* q = nullptr;  // [N][H*hd]
-    const float* kcache = nullptr;  // layer base [Hkv][max_ctx][hd]
+    const float* kcache = nullptr;  // layer base [Hkv][hd/4][max_ctx][4]: 4 dims of a position per 16 B
     const float* vcache = nullptr;  // layer base [Hkv][max_ctx/4][hd][4]: 4 positions of a dim per 16 B
     float* scores = nullptr;  // [N][H][max_ctx]
     int8_t* xq = nullptr;     // [N][H*hd] quantised attention output

@@ -54,7 +54,7 @@ struct nc_session {
     int64_t ctx_stride = 0;  // max_ctx rounded up to 4: KV rows, V position quads, score rows
     int max_batch = 0;
     int64_t maxw = 0;
-    float *kcache = nullptr, *vcache = nullptr;  // K [L][Hkv][ctx_stride][hd], V [L][Hkv][ctx_stride/4][hd][4]
+    float *kcache = nullptr, *vcache = nullptr;  // K [L][Hkv][hd/4][ctx_stride][4], V [L][Hkv][ctx_stride/4][hd][4]
     float* hidden = nullptr;                     // [B][d]
     int8_t* xq = nullptr;                        // [B][maxw]
     float* xs = nullptr;                         // [B][maxw/32]
