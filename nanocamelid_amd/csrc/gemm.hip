@@ -431,17 +431,104 @@ __device__ __forceinline__ void gemm_epilogue_r16(const GemmParams& p, float v, 
 // each, sharing the per-round barrier; used for the interleaved gate,up matrix, whose 64-row
 // groups hold 32 gate rows and the 32 matching up rows, so that SwiGLU and the Q8_0
 // quantisation of the 32-wide output block finish inside the workgroup.
-template <int NMAX, int S, int U, int D, int TPG>
-__global__ __launch_bounds__(64 * S * TPG) void gemm_q4_0_r16_kernel(GemmParams p) {
-    static_assert(16 * NMAX <= 64 * S, "chain threads must fit the workgroup");
+//
+// CW > 0: the chain threads are CW extra waves that only add terms, so the term-computing
+// waves carry no chain work.  A wave issues one VALU instruction per 8 cycles at most, so
+// chain work placed on a computing wave lengthens that wave's round by its BR dependent adds
+// and their LDS reads, and every round's barrier waits for it.  TPG = 1: chain thread c of
+// the extra waves is (token c / 16, row c % 16).  TPG = 4: one chain wave per token (CW =
+// NMAX), lane = 16 * tile + row, so the wave holds the token's 32 gate and 32 up outputs and
+// finishes SwiGLU and the Q8_0 block with shuffles.
+template <int NMAX, int S, int U, int D, int TPG, int CW = 0>
+__global__ __launch_bounds__(64 * (S * TPG + CW)) void gemm_q4_0_r16_kernel(GemmParams p) {
+    static_assert(CW > 0 ? 16 * NMAX <= 64 * CW : 16 * NMAX <= 64 * S, "chain threads must fit their waves");
     static_assert(U == 1 || U == 2 || U == 4, "quads per wave per round");
     static_assert(TPG == 1 || TPG == 4, "tiles per workgroup");
+    static_assert(CW == 0 || TPG == 1 || CW == NMAX, "four-tile groups: one chain wave per token");
     constexpr int QR = S * U;                // quads per round
     constexpr int BR = 4 * QR;               // blocks per round
     constexpr int NP = (NMAX + 1) / 2;       // token-pair activation dwords per block
     constexpr int NM = (NMAX + 7) / 8;       // meta dwords per block
     extern __shared__ float lds_all[];       // per tile group: [2][BR][NMAX][16]
     const int wave_all = wave_id_uniform();
+    if constexpr (CW > 0 && TPG == 4) {
+        if (wave_all >= S * TPG) {  // chain wave of token cn: one barrier per round, then its step
+            const int cn = wave_all - S * TPG;
+            const int lane = threadIdx.x & 63;
+            const int sub = lane >> 4, cr = lane & 15;
+            const int nb = p.units;
+            const int nrounds = ((nb + 3) / 4 + QR - 1) / QR;
+            const bool active = cn < p.N;  // wave-uniform
+            float acc = 0.0f;
+            for (int r = 0; r < nrounds; r++) {
+                __syncthreads();  // round r's terms are in buffer r & 1 of every tile
+                if (active) {
+                    const int nblk = min(BR, nb - r * BR);
+                    const float* src =
+                        lds_all + ((size_t)sub * 2 + (r & 1)) * BR * NMAX * 16 + cn * 16 + cr;
+                    int bl = 0;
+                    for (; bl + 16 <= nblk; bl += 16) {
+                        float v[16];
+#pragma unroll
+                        for (int i = 0; i < 16; i++) v[i] = src[(bl + i) * NMAX * 16];
+#pragma unroll
+                        for (int i = 0; i < 16; i++) acc = acc + v[i];
+                    }
+                    for (; bl < nblk; bl++) acc = acc + src[bl * NMAX * 16];
+                }
+            }
+            if (active) {
+                // EPI_SWIGLU_Q8 (fused_silu_mul inference.rs:3367-3390, then quantize_f32_to_q8_0 of
+                // the 32-wide block, inference.rs:4034-4041): lanes 0-31 gate, 32-63 up
+                const int l = lane & 31;
+                const float g = __shfl(acc, l, 64);
+                const float up = __shfl(acc, 32 + l, 64);
+                const float sig = 1.0f / (1.0f + expf_glibc(-g));
+                const float y = g * sig * up;
+                const float amax = halfwave_amax(y);
+                float scale;
+                const int q = quantize_lane_q8(y, amax, &scale);
+                const int qs = halfwave_isum(q);
+                if (lane < 32) {
+                    const int blk = blockIdx.x;
+                    p.xq_out[(size_t)cn * p.F + blk * 32 + lane] = (int8_t)q;
+                    if (lane == 0) {
+                        p.xs_out[(size_t)cn * (p.F / 32) + blk] = scale;
+                        p.xs8_out[(size_t)cn * (p.F / 32) + blk] = -8 * qs;
+                    }
+                }
+            }
+            return;
+        }
+    }
+    if constexpr (CW > 0 && TPG == 1) {
+        if (wave_all >= S) {  // dedicated chain wave: one barrier per round, then its chain step
+            const int c = threadIdx.x - 64 * S;
+            const int cn = c >> 4, cr = c & 15;
+            const int nb = p.units;
+            const int nrounds = ((nb + 3) / 4 + QR - 1) / QR;
+            const bool active = c < 16 * NMAX && cn < p.N;
+            float acc = 0.0f;
+            for (int r = 0; r < nrounds; r++) {
+                __syncthreads();  // round r's terms are in buffer r & 1
+                if (active) {
+                    const int nblk = min(BR, nb - r * BR);
+                    const float* src = lds_all + (size_t)(r & 1) * BR * NMAX * 16 + cn * 16 + cr;
+                    int bl = 0;
+                    for (; bl + 16 <= nblk; bl += 16) {
+                        float v[16];
+#pragma unroll
+                        for (int i = 0; i < 16; i++) v[i] = src[(bl + i) * NMAX * 16];
+#pragma unroll
+                        for (int i = 0; i < 16; i++) acc = acc + v[i];
+                    }
+                    for (; bl < nblk; bl++) acc = acc + src[bl * NMAX * 16];
+                }
+            }
+            if (active) gemm_epilogue_r16<NMAX>(p, acc, cn, blockIdx.x, cr);
+            return;
+        }
+    }
     const int sub = wave_all / S;            // tile of the group (TPG = 4)
     const int wave = wave_all % S;
     const int tile = blockIdx.x * TPG + sub;
@@ -540,7 +627,7 @@ __global__ __launch_bounds__(64 * S * TPG) void gemm_q4_0_r16_kernel(GemmParams 
                     }
                 }
                 __syncthreads();
-                if (tig < 16 * NMAX && cn < N) {
+                if (CW == 0 && tig < 16 * NMAX && cn < N) {
                     const int nblk = min(BR, nb - r * BR);
                     const float* src = buf + cn * 16 + cr;
                     // groups of 16 terms read ahead of their dependent adds
@@ -559,8 +646,8 @@ __global__ __launch_bounds__(64 * S * TPG) void gemm_q4_0_r16_kernel(GemmParams 
     }
 #undef NC_R16_LOAD
     if constexpr (TPG == 1) {
-        if (tig < 16 * NMAX && cn < N) gemm_epilogue_r16<NMAX>(p, acc, cn, tile, cr);
-    } else {
+        if (CW == 0 && tig < 16 * NMAX && cn < N) gemm_epilogue_r16<NMAX>(p, acc, cn, tile, cr);
+    } else if constexpr (CW == 0) {
         // EPI_SWIGLU_Q8 over the group's 64 rows: rows 0-31 gate, 32-63 up of output block
         // blockIdx.x (fused_silu_mul inference.rs:3367-3390, then quantize_f32_to_q8_0 of the
         // 32-wide block, inference.rs:4034-4041); the same expressions as the 64-row kernel.
@@ -931,31 +1018,35 @@ int launch_r16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
     if (p.epi == EPI_SWIGLU_Q8) {
         // four 16-row tiles per workgroup, 4 waves each (the fastest 16-row shape measured on
         // the 28672 x 4096 gate,up matrix)
-        constexpr int S = 4, TPG = 4;
+        // up to 8 rows: 2 waves per tile and one chain wave per token; wider: 4 waves per tile
+        // with the chains on the first two waves of each tile
+        constexpr int TPG = 4, CW = NMAX <= 8 ? NMAX : 0, S = CW ? 2 : 4;
         if (p.ntiles % TPG) return fail(NC_EINVAL, "gemm: SwiGLU rows must fill whole 64-row groups");
         const size_t lds = (size_t)TPG * 2 * 4 * S * U * NMAX * 16 * sizeof(float);
         if (ev0)
-            hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, TPG>), dim3(p.ntiles / TPG),
-                                  dim3(64 * S * TPG), lds, st, ev0, ev1, 0, p);
+            hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, TPG, CW>), dim3(p.ntiles / TPG),
+                                  dim3(64 * (S * TPG + CW)), lds, st, ev0, ev1, 0, p);
         else
-            hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, TPG>), dim3(p.ntiles / TPG), dim3(64 * S * TPG),
-                               lds, st, p);
+            hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, TPG, CW>), dim3(p.ntiles / TPG),
+                               dim3(64 * (S * TPG + CW)), lds, st, p);
     } else {
         // 8 waves (two per SIMD hide each other's dependency latency); 16 when K is long
         // (at least 64 quads): half the rounds, each with its barrier and chain step
         // (4096 x 14336 at N = 5: 11.81 -> 10.44 us; 6144 x 4096 is slower with 16), for
         // widths whose round buffers stay within 48 KB of LDS
+        constexpr int CW = (16 * NMAX + 63) / 64;  // dedicated chain waves
         auto go = [&]<int S>() {
             const size_t lds = (size_t)2 * 4 * S * U * NMAX * 16 * sizeof(float);
             if (ev0)
-                hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1>), dim3(p.ntiles), dim3(64 * S), lds,
-                                      st, ev0, ev1, 0, p);
+                hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1, CW>), dim3(p.ntiles),
+                                      dim3(64 * (S + CW)), lds, st, ev0, ev1, 0, p);
             else
-                hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+                hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1, CW>), dim3(p.ntiles), dim3(64 * (S + CW)),
+                                   lds, st, p);
         };
         if constexpr (NMAX <= 6) {
             if ((p.units + 3) / 4 >= 64)
-                go.template operator()<16>();
+                go.template operator()<12>();
             else
                 go.template operator()<8>();
         } else {
