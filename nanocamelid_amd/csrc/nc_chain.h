@@ -54,12 +54,22 @@ struct ChainEntry {
     int seg;        // segment (thread) index
 };
 
+// A sensitive entry as the walk reads it: the advance over the insensitive segments before
+// it, then its terms (padded to whole 16-byte rows).
+template <int E>
+struct WalkRow {
+    static constexpr int W = (E + 1 + 3) / 4 * 4;
+    float v[W];
+};
+
 template <int T>
 struct ChainScratch {
     double dtot[T / 64];
     int itot[T / 64];
     float last[T];
     ChainEntry ent[kChainMaxSensitive];
+    float walk_end[64];  // chain value after each entry of the current 64-entry window
+    int bad;             // set by any thread whose boundary check fails
     float result;
 };
 
@@ -212,36 +222,55 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
         ce.cend = cstart + d;
         ce.seg = t;
     }
+    if (t == 0) sc.bad = 0;  // read after the verification barrier, two barriers on
     __syncthreads();
     if (listed && t < 64) {
-        // wave 0: lane q holds entry e0 + q (its advance over the insensitive segments before
-        // it, which is exact, and its E terms); the chain then visits the entries in order
-        // with wave-uniform reads (v_readlane), so only the dependent adds are serial
-        float S = s0;  // true chain value at the end of the last walked segment
+        // wave 0: lane q stages entry e0 + q (its advance over the insensitive segments before
+        // it, which is exact, and its E terms) as one LDS row; lane 0 then walks the rows in
+        // order with 16-byte reads issued one entry ahead, so only the dependent adds are
+        // serial.
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        constexpr int W = WalkRow<E>::W;
+        __shared__ WalkRow<E> rows[64];
+        float S = s0;  // true chain value at the end of the last walked segment (lane 0)
         for (int e0 = 0; e0 < total_s; e0 += 64) {
             const int me = e0 + t;
             const int cnt = min(64, total_s - e0);
-            float adv = 0.0f, trm[E];
             double ce = 0.0;
-#pragma unroll
-            for (int j = 0; j < E; j++) trm[j] = 0.0f;
             if (me < total_s) {
                 const double cs = sc.ent[me].cstart;
                 ce = sc.ent[me].cend;
                 const double cl = me == 0 ? (double)s0 : sc.ent[me - 1].cend;
-                adv = (float)(cs - cl);
+                rows[t].v[0] = (float)(cs - cl);
                 const float* ap = a_lds + sc.ent[me].seg * E;
 #pragma unroll
-                for (int j = 0; j < E; j++) trm[j] = ap[j];
-            }
-            float mine = 0.0f;
-            for (int q = 0; q < cnt; q++) {  // q is wave-uniform
-                S = S + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(adv), q));
+                for (int j = 0; j < E; j++) rows[t].v[1 + j] = ap[j];
 #pragma unroll
-                for (int j = 0; j < E; j++) S = S + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(trm[j]), q));
-                mine = t == q ? S : mine;
+                for (int j = E + 1; j < W; j++) rows[t].v[j] = 0.0f;
             }
-            if (me < total_s) sc.ent[me].shift = (double)mine - ce;
+            if (t == 0) {
+                // rows of this wave's lanes: LDS operations of one wave complete in order
+                f4v cur[W / 4], nxt[W / 4];
+#pragma unroll
+                for (int c = 0; c < W / 4; c++) cur[c] = *(const f4v*)&rows[0].v[4 * c];
+                for (int q = 0; q < cnt; q++) {
+                    const int qn = min(q + 1, cnt - 1);
+#pragma unroll
+                    for (int c = 0; c < W / 4; c++) nxt[c] = *(const f4v*)&rows[qn].v[4 * c];
+#pragma unroll
+                    for (int c = 0; c < W / 4; c++) {
+                        // the padding after the E terms is never added
+                        if (4 * c + 0 <= E) S = S + cur[c].x;
+                        if (4 * c + 1 <= E) S = S + cur[c].y;
+                        if (4 * c + 2 <= E) S = S + cur[c].z;
+                        if (4 * c + 3 <= E) S = S + cur[c].w;
+                    }
+                    sc.walk_end[q] = S;
+#pragma unroll
+                    for (int c = 0; c < W / 4; c++) cur[c] = nxt[c];
+                }
+            }
+            if (me < total_s) sc.ent[me].shift = (double)sc.walk_end[t] - ce;
         }
     }
     __syncthreads();
@@ -262,7 +291,9 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
     }
     __syncthreads();
     if (listed && t > 0) bad |= (float)run != sc.last[t - 1];
-    const bool any_bad = __syncthreads_or(bad);
+    if (bad) sc.bad = 1;
+    __syncthreads();
+    const bool any_bad = sc.bad != 0;
     if (!any_bad) {
         if (t == T - 1) sc.result = y;
     } else if (t == 0) {
