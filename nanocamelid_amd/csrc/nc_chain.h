@@ -64,7 +64,8 @@ struct WalkRow {
 
 template <int T>
 struct ChainScratch {
-    double dtot[T / 64];
+    double dtot[T / 64];   // wave totals of the guess scan
+    double dtot2[T / 64];  // wave totals of the increment scan
     int itot[T / 64];
     float last[T];
     ChainEntry ent[kChainMaxSensitive];
@@ -124,7 +125,9 @@ __device__ __forceinline__ double chain_readlane(double v, int lane) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
-// Block-wide exclusive scan of a double (and optionally of an int in the same pass).
+// Block-wide exclusive scan of a double (and optionally of an int in the same pass).  The
+// wave totals array must not be written again before a later barrier (each scan of
+// exact_chain_sum has its own, and the routine ends with a barrier).
 template <int T>
 __device__ __forceinline__ double block_excl_scan_f64(double v, double* tot) {
     const int w = threadIdx.x >> 6;
@@ -136,7 +139,6 @@ __device__ __forceinline__ double block_excl_scan_f64(double v, double* tot) {
 #pragma unroll
     for (int i = 0; i < T / 64; i++)
         if (i < w) base += tot[i];
-    __syncthreads();
     return base + excl;
 }
 template <int T>
@@ -162,7 +164,6 @@ __device__ __forceinline__ double block_excl_scan_f64_i32(double v, int k, doubl
         }
         kall += ki;
     }
-    __syncthreads();
     *kexcl = kbase + kincl - k;
     *ktotal = kall;
     return base + excl;
@@ -212,7 +213,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
 
     // 3. uncorrected starts C_t, with the sensitive count scanned in the same pass
     int off, total_s;
-    const double cstart = (double)s0 + block_excl_scan_f64_i32<T>(d, sens ? 1 : 0, sc.dtot, sc.itot, &off, &total_s);
+    const double cstart = (double)s0 + block_excl_scan_f64_i32<T>(d, sens ? 1 : 0, sc.dtot2, sc.itot, &off, &total_s);
 
     // 4. sensitive list in ascending order, then the walk (one wave)
     const bool listed = total_s <= kChainMaxSensitive;
@@ -227,7 +228,7 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
     if (listed && t < 64) {
         // wave 0: lane q stages entry e0 + q (its advance over the insensitive segments before
         // it, which is exact, and its E terms) as one LDS row; lane 0 then walks the rows in
-        // order with 16-byte reads issued one entry ahead, so only the dependent adds are
+        // order with 16-byte reads issued two entries ahead, so only the dependent adds are
         // serial.
         typedef float f4v __attribute__((ext_vector_type(4)));
         constexpr int W = WalkRow<E>::W;
@@ -249,26 +250,39 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
                 for (int j = E + 1; j < W; j++) rows[t].v[j] = 0.0f;
             }
             if (t == 0) {
-                // rows of this wave's lanes: LDS operations of one wave complete in order
-                f4v cur[W / 4], nxt[W / 4];
-#pragma unroll
-                for (int c = 0; c < W / 4; c++) cur[c] = *(const f4v*)&rows[0].v[4 * c];
-                for (int q = 0; q < cnt; q++) {
-                    const int qn = min(q + 1, cnt - 1);
-#pragma unroll
-                    for (int c = 0; c < W / 4; c++) nxt[c] = *(const f4v*)&rows[qn].v[4 * c];
-#pragma unroll
-                    for (int c = 0; c < W / 4; c++) {
-                        // the padding after the E terms is never added
-                        if (4 * c + 0 <= E) S = S + cur[c].x;
-                        if (4 * c + 1 <= E) S = S + cur[c].y;
-                        if (4 * c + 2 <= E) S = S + cur[c].z;
-                        if (4 * c + 3 <= E) S = S + cur[c].w;
-                    }
-                    sc.walk_end[q] = S;
-#pragma unroll
-                    for (int c = 0; c < W / 4; c++) cur[c] = nxt[c];
+                // rows of this wave's lanes: LDS operations of one wave complete in order.  Three
+                // register sets rotate (unrolled by 3): entry q's row is read two entries ahead.
+                f4v r0[W / 4], r1[W / 4], r2[W / 4];
+#define NC_WALK_READ(R, Q)                                                                          \
+    {                                                                                               \
+        const int q_ = min((Q), cnt - 1);                                                           \
+        _Pragma("unroll") for (int c = 0; c < W / 4; c++) R[c] = *(const f4v*)&rows[q_].v[4 * c];  \
+    }
+#define NC_WALK_ADD(R, Q)                                                                           \
+    {                                                                                               \
+        _Pragma("unroll") for (int c = 0; c < W / 4; c++) {                                        \
+            if (4 * c + 0 <= E) S = S + R[c].x;                                                     \
+            if (4 * c + 1 <= E) S = S + R[c].y;                                                     \
+            if (4 * c + 2 <= E) S = S + R[c].z;                                                     \
+            if (4 * c + 3 <= E) S = S + R[c].w;                                                     \
+        }                                                                                           \
+        sc.walk_end[(Q)] = S;                                                                       \
+    }
+                // (the padding after the E terms is never added)
+                NC_WALK_READ(r0, 0)
+                NC_WALK_READ(r1, 1)
+                for (int q = 0; q < cnt; q += 3) {
+                    NC_WALK_READ(r2, q + 2)
+                    NC_WALK_ADD(r0, q)
+                    if (q + 1 >= cnt) break;
+                    NC_WALK_READ(r0, q + 3)
+                    NC_WALK_ADD(r1, q + 1)
+                    if (q + 2 >= cnt) break;
+                    NC_WALK_READ(r1, q + 4)
+                    NC_WALK_ADD(r2, q + 2)
                 }
+#undef NC_WALK_ADD
+#undef NC_WALK_READ
             }
             if (me < total_s) sc.ent[me].shift = (double)sc.walk_end[t] - ce;
         }
