@@ -169,33 +169,6 @@ __device__ __forceinline__ int dot32_bcast(int acc, int xp, int w0, int w1, int 
     return acc;
 }
 
-// Two tokens of a pair (2p, 2p+1) share the activation register xp: their 8-step chains
-// are interleaved (acc0 reads lanes 0..7 of each row, acc1 lanes 8..15) so that each
-// dot4c's dependency on its own accumulator is hidden behind the other chain.
-__device__ __forceinline__ void dot32_bcast_pair(int& acc0, int& acc1, int xp, int w0, int w1, int w2, int w3, int w4,
-                                                 int w5, int w6, int w7) {
-    asm("s_nop 1\n\t"
-        "v_dot4c_i32_i8_dpp %0, %2, %3 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %1, %2, %3 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %0, %2, %4 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %1, %2, %4 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %0, %2, %5 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %1, %2, %5 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %0, %2, %6 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %1, %2, %6 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %0, %2, %7 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %1, %2, %7 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %0, %2, %8 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %1, %2, %8 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %0, %2, %9 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %1, %2, %9 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %0, %2, %10 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot4c_i32_i8_dpp %1, %2, %10 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
-        "s_nop 2"
-        : "+v"(acc0), "+v"(acc1)
-        : "v"(xp), "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(w4), "v"(w5), "v"(w6), "v"(w7));
-}
-
 template <int J>
 __device__ __forceinline__ int bcast_i(int v) {
     return __builtin_amdgcn_mov_dpp(v, 0x150 + J, 0xf, 0xf, false);
@@ -205,14 +178,72 @@ __device__ __forceinline__ float bcast_f(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xf, 0xf, false));
 }
 
+// Two tokens of a pair (2p, 2p+1) share the activation register xp: their 8-step chains
+// are interleaved (acc0 reads lanes 0..7 of each row, acc1 lanes 8..15) so that each
+// dot4c's dependency on its own accumulator is hidden behind the other chain.
+// The scale products are folded into the same asm: besides the two dot chains, c0 = x_scale[n0] * ws and c1 = x_scale[n1] * ws, each one
+// v_mul_f32_dpp that reads the token's x_scale from lane X0 / X1 of the meta dword (the same
+// IEEE product as a broadcast followed by a multiply).  The leading s_nop covers a VALU write
+// of meta or xp just before the asm.
+template <int X0, int X1>
+__device__ __forceinline__ void dot32_bcast_pair_scaled(int& acc0, int& acc1, float& c0, float& c1, int xp, int meta,
+                                                        float ws, int w0, int w1, int w2, int w3, int w4, int w5,
+                                                        int w6, int w7) {
+    asm("s_nop 1\n\t"
+        "v_dot4c_i32_i8_dpp %0, %6, %7 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %6, %7 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %6, %8 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %6, %8 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %6, %9 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %6, %9 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %6, %10 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %6, %10 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %6, %11 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %6, %11 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %6, %12 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %6, %12 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %6, %13 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %6, %13 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %6, %14 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %1, %6, %14 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %2, %4, %5 row_newbcast:%15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %3, %4, %5 row_newbcast:%16 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 2"
+        : "+v"(acc0), "+v"(acc1), "=&v"(c0), "=&v"(c1)
+        : "v"(meta), "v"(ws), "v"(xp), "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(w4), "v"(w5), "v"(w6), "v"(w7),
+          "n"(X0), "n"(X1));
+}
+
+// One token's dot chain with its scale product folded in: c = x_scale (lane X of meta) * ws.
+template <int J0, int X>
+__device__ __forceinline__ int dot32_bcast_scaled(int acc, float& c, int xp, int meta, float ws, int w0, int w1, int w2,
+                                                  int w3, int w4, int w5, int w6, int w7) {
+    asm("s_nop 1\n\t"
+        "v_dot4c_i32_i8_dpp %0, %4, %5 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %4, %6 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %4, %7 row_newbcast:%15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %4, %8 row_newbcast:%16 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %4, %9 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %4, %10 row_newbcast:%18 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %4, %11 row_newbcast:%19 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot4c_i32_i8_dpp %0, %4, %12 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %1, %2, %3 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 2"
+        : "+v"(acc), "=&v"(c)
+        : "v"(meta), "v"(ws), "v"(xp), "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(w4), "v"(w5), "v"(w6), "v"(w7),
+          "n"(J0), "n"(J0 + 1), "n"(J0 + 2), "n"(J0 + 3), "n"(J0 + 4), "n"(J0 + 5), "n"(J0 + 6), "n"(J0 + 7), "n"(X));
+    return acc;
+}
+
 // Term of token n (compile-time) for one block: t = (ws * xs) * (float)sum (nib - 8) * x.
 template <int n>
 __device__ __forceinline__ float term_q40(const int* xp, const int* meta, const int (&lo)[4], const int (&hi)[4],
                                           float ws) {
     int d = bcast_i<8 + (n & 7)>(meta[n >> 3]);  // -8 * sum x: sum (nib-8)*x = sum nib*x - 8 sum x
-    d = dot32_bcast<8 * (n & 1)>(d, xp[n >> 1], lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]);
-    const float xs = bcast_f<n & 7>(__int_as_float(meta[n >> 3]));
-    return (xs * ws) * (float)d;  // IEEE multiplication is commutative: == (ws * xs) * d
+    float c;                                       // x_scale * ws (IEEE product, commutative)
+    d = dot32_bcast_scaled<8 * (n & 1), n & 7>(d, c, xp[n >> 1], meta[n >> 3], ws, lo[0], lo[1], lo[2], lo[3], hi[0],
+                                                hi[1], hi[2], hi[3]);
+    return c * (float)d;  // == (ws * xs) * d
 }
 
 // R64: a ring of D rounds of weights, scales and activations is kept in flight per wave.
@@ -228,9 +259,11 @@ __device__ __forceinline__ void terms_q40(float (&t)[NMAX], const int* xp, const
              if constexpr (n1 < NMAX) {
                  int d0 = bcast_i<8 + (n0 & 7)>(meta[n0 >> 3]);
                  int d1 = bcast_i<8 + (n1 & 7)>(meta[n1 >> 3]);
-                 dot32_bcast_pair(d0, d1, xp[P], lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]);
-                 t[n0] = (bcast_f<n0 & 7>(__int_as_float(meta[n0 >> 3])) * ws) * (float)d0;
-                 t[n1] = (bcast_f<n1 & 7>(__int_as_float(meta[n1 >> 3])) * ws) * (float)d1;
+                 float c0, c1;  // x_scale * ws (meta[n0 >> 3] == meta[n1 >> 3]: n0, n1 differ in bit 0)
+                 dot32_bcast_pair_scaled<n0 & 7, n1 & 7>(d0, d1, c0, c1, xp[P], meta[n0 >> 3], ws, lo[0], lo[1],
+                                                         lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]);
+                 t[n0] = c0 * (float)d0;
+                 t[n1] = c1 * (float)d1;
              } else {
                  t[n0] = term_q40<n0>(xp, meta, lo, hi, ws);
              }
