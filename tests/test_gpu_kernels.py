@@ -56,7 +56,7 @@ def test_q4_0_partial_group_and_tile(ctx):
     assert np.array_equal(out, O.matmul_q4_0(xq, xs, w, N, M, K))
 
 
-@pytest.mark.parametrize("N", [1, 2, 5, 8, 9, 16])
+@pytest.mark.parametrize("N", [1, 2, 3, 4, 5, 6, 7, 8, 9, 16])
 @pytest.mark.parametrize("shape", [(100, 416), (32800, 416)], ids=["r16-partial", "r64-partial"])
 def test_q4_0_layouts_partial(ctx, shape, N):
     """Both device layouts (16-row tiles below 512 64-row tiles, 64-row tiles above) with a

@@ -57,6 +57,24 @@ def test_verify_logits_bit_exact(ctx, hd):
         pos += n
 
 
+def test_verify_every_width(ctx):
+    """Every verify width 1..16 once (each width has its own GEMM, SwiGLU-epilogue and
+    attention instantiations): all rows' logits bit-identical to the oracle's."""
+    import nanocamelid_amd as nc
+    _, gm, om = _models(ctx, TINY, seed=31)
+    gs = nc.Session(gm, 256, 16)
+    os_ = O.Session(om, 256, 16)
+    pos = 0
+    for n in range(1, 17):
+        batch = nc.uniform_prompt(100 + n, n, 1000)
+        a, nxt, newpos, preds = gs.verify_greedy(batch, pos)
+        opreds, _, ologits = os_.verify_greedy(batch, pos, want_logits=True)
+        for i in range(n):
+            assert _same(gs.logits(i), ologits[i]), (n, i)
+        assert np.array_equal(preds, opreds), n
+        pos += n
+
+
 def test_hidden_and_forward_pass_match(ctx):
     import nanocamelid_amd as nc
     _, gm, om = _models(ctx, TINY, seed=4)
