@@ -269,14 +269,14 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(AttnParams a) {
     constexpr int RS = HD + 4;
     __shared__ float kt[64 * RS];
     __shared__ __align__(16) float qs[8][RB][HD];  // [head in group][row][dim]
-    const int kvh = blockIdx.y;
+    const int kvh = blockIdx.x;  // KV head fastest: one XCD per KV head (see attn_fused_kernel)
     const int G = a.H / a.Hkv;
     const int g = wave_id_uniform();
     const int h = kvh * G + g;
     const int lane = threadIdx.x & 63;
     const int pos0 = a.d_pos[0];
     const int last = pos0 + a.N - 1;
-    for (int tile = blockIdx.x; tile * 64 <= last; tile += gridDim.x) {
+    for (int tile = blockIdx.y; tile * 64 <= last; tile += gridDim.y) {
         __syncthreads();  // previous tile's readers are done with kt
         if (tile * 64 > pos0 + min(a.N, ((int)blockIdx.z + 1) * RB) - 1) break;  // no row of this block reaches it
         const int rows = min(64, last + 1 - tile * 64);
@@ -473,9 +473,12 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
     __shared__ ChainScratch<T> sc;
     __shared__ __align__(16) float probs[T * E];
     __shared__ float red[T / 64];
-    const int unit = blockIdx.x;
-    const int n = unit / a.H, h = unit % a.H;
-    const int kvh = h / (a.H / a.Hkv);
+    // unit order: KV head fastest, so that with round-robin dispatch over the 8 XCDs (and 8
+    // KV heads) every unit of a KV head lands on one XCD and its keys and values stay in that
+    // XCD's L2 instead of being re-read through the shared cache
+    const int G = a.H / a.Hkv;
+    const int kvh = blockIdx.x % a.Hkv, j = blockIdx.x / a.Hkv;
+    const int n = j / G, h = kvh * G + j % G;
     const int L = a.d_pos[0] + n + 1;
     const int t = threadIdx.x;
     const float* srow = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
@@ -503,9 +506,12 @@ __global__ __launch_bounds__(T) void attn_fused_kernel(AttnParams a) {
     __shared__ __align__(16) float probs[T * E];  // scores, then probabilities
     __shared__ float red[T / 64];
     __shared__ __align__(16) float qs[HD];
-    const int unit = blockIdx.x;
-    const int n = unit / a.H, h = unit % a.H;
-    const int kvh = h / (a.H / a.Hkv);
+    // unit order: KV head fastest, so that with round-robin dispatch over the 8 XCDs (and 8
+    // KV heads) every unit of a KV head lands on one XCD and its keys and values stay in that
+    // XCD's L2 instead of being re-read through the shared cache
+    const int G = a.H / a.Hkv;
+    const int kvh = blockIdx.x % a.Hkv, j = blockIdx.x / a.Hkv;
+    const int n = j / G, h = kvh * G + j % G;
     const int L = a.d_pos[0] + n + 1;
     const int t = threadIdx.x;
     if (t < HD) qs[t] = a.q[((size_t)n * a.H + h) * HD + t];
@@ -594,7 +600,7 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
     // blockIdx.z so that every SIMD gets a short chain instead of a few SIMDs getting long ones
     const int rb = a.N >= 2 ? 2 : 1;
 #define NC_SCORES(HD, RB)                                                                         \
-    hipLaunchKernelGGL((attn_scores_kernel<HD, RB>), dim3(tiles, a.Hkv, (a.N + (RB)-1) / (RB)), dim3(64 * G), 0, \
+    hipLaunchKernelGGL((attn_scores_kernel<HD, RB>), dim3(a.Hkv, tiles, (a.N + (RB)-1) / (RB)), dim3(64 * G), 0, \
                        st, a);                                                                    \
     break;
 #define NC_SCORES_HD(HD)            \
