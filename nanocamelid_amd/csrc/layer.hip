@@ -490,7 +490,7 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
     weighted_v_q8<HD>(a, n, h, kvh, L, probs);  // no barriers below
 }
 
-// Attention of one (row n, head h) unit in one kernel, for rows of at most T*E <= 1024
+// Attention of one (row n, head h) unit in one kernel, for rows of at most T*E <= 1536
 // positions: the scores (as attn_scores_kernel: dot from -0.0 over the head dims in order,
 // then * scale) go to LDS, then the softmax and the weighted V sum as attn_softmax_pv_kernel.
 // Thread t scores positions t, t + T, ..., so a wave's key loads are consecutive positions:
@@ -500,7 +500,7 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
 // score is not stored.
 template <int E, int T, int HD>
 __global__ __launch_bounds__(T) void attn_fused_kernel(AttnParams a) {
-    static_assert(T * E <= 1024, "rows up to 1024 positions");
+    static_assert(T * E <= 1536, "rows up to 1536 positions");
     typedef float f4v __attribute__((ext_vector_type(4)));
     __shared__ ChainScratch<T> sc;
     __shared__ __align__(16) float probs[T * E];  // scores, then probabilities
@@ -576,19 +576,25 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
     // max_pos + 1 is the longest score row of the pass
     const int len = a.max_pos + 1;
     const dim3 grid(a.N * a.H);
-    if (len <= 1024) {
-        // one kernel per pass: each (row, head) unit scores its own keys (short rows: the
-        // units of a KV head re-read its keys from L2, which costs less than a second launch
-        // and the scores' round trip through memory)
-#define NC_FUSED(E)                                                                                  \
-    if (a.hd == 128) hipLaunchKernelGGL((attn_fused_kernel<E, 256, 128>), grid, dim3(256), 0, st, a); \
-    else hipLaunchKernelGGL((attn_fused_kernel<E, 256, 64>), grid, dim3(256), 0, st, a);
-        if (len <= 256) {
-            NC_FUSED(1)
-        } else if (len <= 512) {
-            NC_FUSED(2)
+    if (len <= 1536) {
+        // one kernel per pass: each (row, head) unit scores its own keys (rows up to 1536
+        // positions: the units of a KV head, all on one XCD, re-read its keys from that XCD's
+        // L2, which costs less than a second launch and the scores' round trip through memory)
+        // positions per thread E matched to the row (fewer score slots past the row); rows of
+        // at most 512 positions on 512 threads (two waves per SIMD in the score phase)
+#define NC_FUSED(E, T)                                                                               \
+    if (a.hd == 128) hipLaunchKernelGGL((attn_fused_kernel<E, T, 128>), grid, dim3(T), 0, st, a);    \
+    else hipLaunchKernelGGL((attn_fused_kernel<E, T, 64>), grid, dim3(T), 0, st, a);
+        if (len <= 512) {
+            NC_FUSED(1, 512)
+        } else if (len <= 768) {
+            NC_FUSED(3, 256)
+        } else if (len <= 1024) {
+            NC_FUSED(4, 256)
+        } else if (len <= 1280) {
+            NC_FUSED(5, 256)
         } else {
-            NC_FUSED(4)
+            NC_FUSED(6, 256)
         }
 #undef NC_FUSED
         NC_HIP(hipGetLastError());

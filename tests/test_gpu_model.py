@@ -148,11 +148,14 @@ def test_q4_k_model_logits(ctx):
             assert _same(gs.logits(i), ologits[i])
 
 
-@pytest.mark.parametrize("hd,checks", [(128, (2045, 4093)), (64, (8190,))], ids=["hd128-4k", "hd64-8k"])
+@pytest.mark.parametrize("hd,checks", [(128, (2045, 4093)), (64, (8190,)), (128, (510, 765, 1021, 1277, 1533)),
+                                       (64, (766, 1534))],
+                         ids=["hd128-4k", "hd64-8k", "hd128-fused-tiers", "hd64-fused-tiers"])
 def test_long_context_logits(ctx, hd, checks):
     """Verify logits bit-exact at long contexts: 5-row passes that straddle the softmax
     instantiation boundaries at 2048, 4096 and 8192 positions (the 8192 one switches the
-    softmax to 512 threads)."""
+    softmax to 512 threads), and the single-kernel attention's row tiers (512, 768, 1024,
+    1280 and 1536 positions; past 1536 two kernels)."""
     import nanocamelid_amd as nc
     upto = checks[-1] + 5
     spec = dict(layers=1, embedding_length=2 * hd * 2, head_count=4, head_count_kv=2, feed_forward_length=512,
