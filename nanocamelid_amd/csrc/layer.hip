@@ -625,12 +625,15 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
 #define NC_PV(E, T)                                                                              \
     if (a.hd == 128) hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 128>), grid, dim3(T), 0, st, a); \
     else hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 64>), grid, dim3(T), 0, st, a);
+    // 512 threads: two waves per SIMD through the max, exp and sum phases (a wave issues one
+    // VALU instruction per 8 cycles at most); 2000 positions 27.2 -> 26.4 us, 8000 84.2 -> 78.4
+    // us for one row
     if (len <= 2048) {
-        NC_PV(8, 256)
+        NC_PV(4, 512)
     } else if (len <= 4096) {
-        NC_PV(16, 256)
+        NC_PV(8, 512)
     } else if (len <= 8192) {
-        NC_PV(32, 256)
+        NC_PV(16, 512)
     } else if (len <= 16384) {
         NC_PV(32, 512)
     } else {
