@@ -581,7 +581,8 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
         // positions: the units of a KV head, all on one XCD, re-read its keys from that XCD's
         // L2, which costs less than a second launch and the scores' round trip through memory)
         // positions per thread E matched to the row (fewer score slots past the row); rows of
-        // at most 512 positions on 512 threads (two waves per SIMD in the score phase)
+        // at most 512 and of 1281..1536 positions on 512 threads (two waves per SIMD in the
+        // score phase; measured faster there, slower for 513..1280)
 #define NC_FUSED(E, T)                                                                               \
     if (a.hd == 128) hipLaunchKernelGGL((attn_fused_kernel<E, T, 128>), grid, dim3(T), 0, st, a);    \
     else hipLaunchKernelGGL((attn_fused_kernel<E, T, 64>), grid, dim3(T), 0, st, a);
@@ -594,7 +595,7 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
         } else if (len <= 1280) {
             NC_FUSED(5, 256)
         } else {
-            NC_FUSED(6, 256)
+            NC_FUSED(3, 512)
         }
 #undef NC_FUSED
         NC_HIP(hipGetLastError());
