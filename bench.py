@@ -315,8 +315,8 @@ def main():
                     help="also run a 256 MiB device copy (known HBM bytes) to scale rocprofv3 --pmc byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on exactly one GPU; multi-GPU sharding is a design note "
-                                   "(DESIGN.md), run with --gpus 1"}))
+        print(json.dumps({"error": "this build runs on exactly one GPU (multi-GPU sharding is designed, not "
+                                   "built); run with --gpus 1"}))
         sys.exit(2)
 
     import numpy as np
