@@ -5,8 +5,9 @@
 //
 //     s_{-1} = s0 (0 unless a carry-in is given),   s_i = fl32(s_{i-1} + a_i),   i = 0 .. n-1.
 //
-// On gfx950 one dependent v_add_f32 costs ~10 cycles, so a 4096-term chain is ~17 us
-// when evaluated literally.  This routine returns the bit-identical s_{n-1} from a
+// On gfx950 a wave issues at most one VALU instruction per 8 cycles, so a dependent
+// v_add_f32 chain costs 8 cycles per term and a 4096-term chain ~14 us when evaluated
+// literally.  This routine returns the bit-identical s_{n-1} from a
 // workgroup of T threads; thread t owns the segment of terms a_{tE} .. a_{tE+E-1}:
 //
 //  1. Guess.  G_t = fl32(s0 + sum of all earlier terms), the prefix taken in double (a
