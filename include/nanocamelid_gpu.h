@@ -50,7 +50,10 @@ const char* nc_version(void);
 
 /* ---------------------------------------------------------------- context */
 /* Opens device `device` (HIP ordinal).  No reference counterpart: the reference
- * is CPU-only; this is the device handle the Rust `-sys` crate holds. */
+ * is CPU-only; this is the device handle the Rust `-sys` crate holds.  Also allocates the
+ * operator entry points' scratch (block sums for up to 16 rows of 65536 columns, temperature
+ * softmax partials for 16 rows): those calls allocate nothing at these sizes; a larger call
+ * grows the scratch once. */
 int nc_ctx_create(int device, nc_ctx** out);
 void nc_ctx_free(nc_ctx* ctx);
 /* Blocks until all work queued on the context's default stream finished. */
@@ -131,6 +134,13 @@ typedef struct nc_model_config {
     float rope_freq_base, rms_norm_epsilon;
     int64_t device_weight_bytes; /* repacked matrices incl. head */
     int64_t verify_weight_bytes; /* algorithmic weight bytes streamed by one verify pass */
+    /* Llama-3 RoPE frequency scaling, llama.rope.scaling.{factor, original_context_length,
+     * low_freq_factor, high_freq_factor} (rope_scaling_from_gguf src/main.rs:8522-8535).
+     * rope_scaling = 1 when all four keys are present, as cached_rope_angles
+     * (src/inference.rs:875-893) requires before it scales; the values are 0 otherwise. */
+    int32_t rope_scaling;
+    float rope_scaling_factor, rope_scaling_original_context_length;
+    float rope_scaling_low_freq_factor, rope_scaling_high_freq_factor;
 } nc_model_config;
 
 typedef struct nc_load_opts {
@@ -152,15 +162,21 @@ void nc_model_free(nc_model* m);
 /* ---------------------------------------------------------------- session */
 /* KV cache [layers][kv_heads][max_ctx][head_dim] f32 plus batch workspaces for up to
  * max_batch rows.  Replaces LlamaKvCache::new + LlamaWorkspace/LlamaBatchWorkspace
- * (src/inference.rs:505-695).  max_batch 1..16. */
+ * (src/inference.rs:505-695).  max_batch 1..16.  max_ctx 1..min(context_length,
+ * NC_MAX_CONTEXT): the attention kernels take score rows of at most NC_MAX_CONTEXT positions,
+ * so a longer session is refused here (NC_ERANGE) instead of failing inside a pass. */
+#define NC_MAX_CONTEXT 16384
 int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_session** out);
 void nc_session_free(nc_session* s);
 
 /* Batched forward of n tokens at positions start_pos.. (KV written for every row),
- * final hidden rows kept for nc_session_logits.  Replaces prefill_pass_batch
+ * final hidden rows kept for nc_session_hidden.  Replaces prefill_pass_batch
  * (src/inference.rs:3695-3744); n > max_batch is processed in max_batch chunks as
- * prefill_tokens does (src/main.rs:9415-9485).  Also computes every row's logits
- * and greedy prediction when want_logits != 0. */
+ * prefill_tokens does (src/main.rs:9415-9485).  want_logits != 0: the head runs on the
+ * last chunk's rows (their logits are then readable with nc_session_logits, rows
+ * 0 .. min(n, max_batch)-1 of that chunk); want_logits == 0: no head pass at all, as
+ * prefill_pass_batch computes no logits.  Token ids >= vocab_size: NC_ERANGE before any
+ * launch (the reference panics on the embedding index, src/inference.rs:3728-3733). */
 int nc_prefill(nc_session* s, const uint32_t* toks, int32_t n, int64_t start_pos, int32_t want_logits);
 /* Single-token forward (src/inference.rs:3649-3670 forward_pass).  logits_host may be
  * NULL; *pred_out (nullable) receives argmax (first max wins, inference.rs:4836-4846). */
@@ -263,6 +279,10 @@ typedef struct nc_synth_spec {
     int32_t norm_mode;   /* 0: norm weights 1.0; 1: N(1, 0.1) */
     float rope_freq_base, rms_norm_epsilon, weight_std;
     uint64_t seed;
+    /* rope_scaling_factor > 0: also write llama.rope.scaling.factor (f32),
+     * .original_context_length (u32), .low_freq_factor and .high_freq_factor (f32). */
+    float rope_scaling_factor, rope_scaling_low_freq_factor, rope_scaling_high_freq_factor;
+    uint32_t rope_scaling_original_context_length;
 } nc_synth_spec;
 
 /* Size in bytes of the GGUF v3 image nc_synth_write would produce. */

@@ -197,9 +197,11 @@ class Session:
         self.vocab = model.config["vocab_size"]
         self.d = model.config["embedding_length"]
 
-    def prefill_pass_batch(self, toks, start_pos: int):
+    def prefill_pass_batch(self, toks, start_pos: int, want_logits: bool = True):
+        """prefill_pass_batch (src/inference.rs:3695-3744) in max_batch chunks; want_logits: also
+        run the head on the last chunk's rows (readable with logits(row))."""
         a, p = _u32(toks)
-        check(lib().nc_prefill(self.h, p, a.size, start_pos, 1))
+        check(lib().nc_prefill(self.h, p, a.size, start_pos, 1 if want_logits else 0))
 
     def forward_pass(self, tok: int, pos: int, want_logits: bool = True):
         pred = C.c_uint32()
@@ -320,10 +322,15 @@ SYNTH_CONFIGS = {
 
 def synth_gguf(layers, embedding_length, head_count, head_count_kv, feed_forward_length, vocab_size,
                context_length=8192, weight_type=NC_TYPE_Q4_0, tied=1, norm_mode=0, rope_freq_base=500000.0,
-               rms_norm_epsilon=1e-5, weight_std=0.02, seed=0, nthreads=0) -> np.ndarray:
-    """Seeded random-init Llama GGUF v3 image (weights N(0, std) -> Q4_0 / Q4_K)."""
+               rms_norm_epsilon=1e-5, weight_std=0.02, seed=0, nthreads=0, rope_scaling=None) -> np.ndarray:
+    """Seeded random-init Llama GGUF v3 image (weights N(0, std) -> Q4_0 / Q4_K).
+
+    rope_scaling: optional (factor, original_context_length, low_freq_factor, high_freq_factor),
+    written as the llama.rope.scaling.* keys (Llama-3.1/3.2 files carry (32, 8192, 1, 4))."""
+    fac, orig, lo, hi = rope_scaling if rope_scaling else (0.0, 0, 0.0, 0.0)
     s = SynthSpec(layers, embedding_length, head_count, head_count_kv, feed_forward_length, vocab_size,
-                  context_length, weight_type, tied, norm_mode, rope_freq_base, rms_norm_epsilon, weight_std, seed)
+                  context_length, weight_type, tied, norm_mode, rope_freq_base, rms_norm_epsilon, weight_std, seed,
+                  fac, lo, hi, int(orig))
     size = C.c_uint64()
     check(lib().nc_synth_size(C.byref(s), C.byref(size)))
     buf = np.empty(size.value, np.uint8)

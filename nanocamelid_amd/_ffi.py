@@ -27,7 +27,10 @@ class ModelConfig(C.Structure):
         "head_count_kv", "head_dim", "rope_dimension_count", "vocab_size", "attention_output_width",
         "kv_width")] + [("weight_type", C.c_int32), ("tied_head", C.c_int32),
                         ("rope_freq_base", C.c_float), ("rms_norm_epsilon", C.c_float),
-                        ("device_weight_bytes", C.c_int64), ("verify_weight_bytes", C.c_int64)]
+                        ("device_weight_bytes", C.c_int64), ("verify_weight_bytes", C.c_int64),
+                        ("rope_scaling", C.c_int32), ("rope_scaling_factor", C.c_float),
+                        ("rope_scaling_original_context_length", C.c_float),
+                        ("rope_scaling_low_freq_factor", C.c_float), ("rope_scaling_high_freq_factor", C.c_float)]
 
 
 class LoadOpts(C.Structure):
@@ -48,7 +51,9 @@ class SynthSpec(C.Structure):
                 ("head_count_kv", C.c_int32), ("feed_forward_length", C.c_int32), ("vocab_size", C.c_int32),
                 ("context_length", C.c_int32), ("weight_type", C.c_int32), ("tied", C.c_int32),
                 ("norm_mode", C.c_int32), ("rope_freq_base", C.c_float), ("rms_norm_epsilon", C.c_float),
-                ("weight_std", C.c_float), ("seed", C.c_uint64)]
+                ("weight_std", C.c_float), ("seed", C.c_uint64), ("rope_scaling_factor", C.c_float),
+                ("rope_scaling_low_freq_factor", C.c_float), ("rope_scaling_high_freq_factor", C.c_float),
+                ("rope_scaling_original_context_length", C.c_uint32)]
 
 
 _vp, _i32, _i64, _u32p, _f32p = C.c_void_p, C.c_int32, C.c_int64, C.POINTER(C.c_uint32), C.POINTER(C.c_float)

@@ -304,7 +304,8 @@ std::vector<uint8_t> synth_header(const nc_synth_spec& s, std::vector<TSpec>& ts
     std::vector<uint8_t> h = {'G', 'G', 'U', 'F'};
     put_u32(h, 3);
     put_u64(h, ts.size());
-    put_u64(h, 13);
+    const bool scaled = s.rope_scaling_factor > 0.0f;
+    put_u64(h, scaled ? 17 : 13);
     kv_str(h, "general.architecture", "llama");
     kv_u32(h, "general.alignment", 32);
     kv_u32(h, "llama.context_length", (uint32_t)s.context_length);
@@ -318,6 +319,12 @@ std::vector<uint8_t> synth_header(const nc_synth_spec& s, std::vector<TSpec>& ts
     kv_u32(h, "llama.vocab_size", (uint32_t)s.vocab_size);
     kv_u32(h, "llama.rope.dimension_count", (uint32_t)(s.embedding_length / s.head_count));
     kv_str(h, "general.name", "nanocamelid-synthetic");
+    if (scaled) {  // Llama-3 RoPE frequency scaling keys (read by rope_scaling_from_gguf, main.rs:8522-8535)
+        kv_f32(h, "llama.rope.scaling.factor", s.rope_scaling_factor);
+        kv_u32(h, "llama.rope.scaling.original_context_length", s.rope_scaling_original_context_length);
+        kv_f32(h, "llama.rope.scaling.low_freq_factor", s.rope_scaling_low_freq_factor);
+        kv_f32(h, "llama.rope.scaling.high_freq_factor", s.rope_scaling_high_freq_factor);
+    }
     uint64_t off = 0;
     for (auto& t : ts) {
         put_str(h, t.name);

@@ -161,3 +161,20 @@ int launch_sample_probs(const float* probs, int V, uint64_t seed, int64_t pos, u
                         uint32_t* out1, hipStream_t st);
 
 }  // namespace nc
+
+// ---------------------------------------------------------------- C ABI handles (opaque in the header)
+struct nc_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    // Scratch of the operator-level entry points, allocated by nc_ctx_create for up to 16
+    // rows of 65536 columns (every Llama projection); a larger call grows it once.
+    int32_t* xsum = nullptr;  // -8 * per-block int8 sums of the activations
+    size_t xsum_cap = 0;
+    float* tp_scratch = nullptr;  // temperature softmax partials
+    size_t tp_cap = 0;
+};
+
+struct nc_qmat {
+    nc_ctx* ctx = nullptr;
+    nc::QMatDev m;
+};

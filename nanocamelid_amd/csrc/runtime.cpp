@@ -12,19 +12,10 @@
 #include "nc_internal.h"
 
 // ---------------------------------------------------------------- handles
-struct nc_ctx {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    int32_t* xsum = nullptr;  // grow-only scratch for the operator-level entry points
-    size_t xsum_cap = 0;
-    float* tp_scratch = nullptr;  // grow-only scratch of the temperature softmax
-    size_t tp_cap = 0;
-};
-
-struct nc_qmat {
-    nc_ctx* ctx = nullptr;
-    nc::QMatDev m;
-};
+// nc_ctx and nc_qmat are defined in nc_internal.h (shared with noalloc.hip).
+namespace {
+constexpr size_t kCtxScratchCols = 65536;
+}
 
 namespace {
 
@@ -443,6 +434,21 @@ static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_lo
         return fail(NC_EFORMAT, "inconsistent head geometry");
     float f;
     c.rope_freq_base = g.get_f32(P + "rope.freq_base", &f) ? f : 10000.0f;
+    {  // rope_scaling_from_gguf (main.rs:8522-8535): used only when all four keys are present
+        float fac = 0, lo = 0, hi = 0;
+        uint32_t orig = 0;
+        const bool a = g.get_f32(P + "rope.scaling.factor", &fac);
+        const bool b = g.get_u32(P + "rope.scaling.original_context_length", &orig);
+        const bool cc = g.get_f32(P + "rope.scaling.low_freq_factor", &lo);
+        const bool dd = g.get_f32(P + "rope.scaling.high_freq_factor", &hi);
+        c.rope_scaling = a && b && cc && dd ? 1 : 0;
+        if (c.rope_scaling) {
+            c.rope_scaling_factor = fac;
+            c.rope_scaling_original_context_length = (float)orig;
+            c.rope_scaling_low_freq_factor = lo;
+            c.rope_scaling_high_freq_factor = hi;
+        }
+    }
     c.rms_norm_epsilon = g.get_f32(P + "attention.layer_norm_rms_epsilon", &f) ? f : 1e-5f;
     const GgufTensor* te = g.find("token_embd.weight");
     if (!te || te->dims.size() != 2) return fail(NC_EFORMAT, "missing token_embd.weight");
@@ -459,6 +465,7 @@ static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_lo
     if (aw % 64 || kw % 64 || F % 32 || d % 256)
         return fail(NC_EINVAL, "model widths must be multiples of 64 (attention), 32 (ffn), 256 (embedding)");
     if (c.head_dim != 64 && c.head_dim != 128) return fail(NC_EINVAL, "head_dim must be 64 or 128");
+    if (c.head_count / c.head_count_kv > 8) return fail(NC_EINVAL, "at most 8 query heads per KV head");
     // weights (LlamaWeights::load, model.rs:461-545)
     std::vector<float> emb;
     int rc = tensor_to_f32(g, "token_embd.weight", emb);
@@ -569,7 +576,7 @@ static int flush_timing(nc_session* s) {
 // One forward over the n tokens already in d_toks at positions start_pos..: embedding,
 // all layers (run_layer_range_batch, inference.rs:3747-4111), final norm, head and
 // per-row argmax.  Writes d_preds and logits.
-static int run_pass(nc_session* s, int n, int64_t start_pos) {
+static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
     nc_model* m = s->m;
     const nc_model_config& c = m->cfg;
     const int d = (int)c.embedding_length, aw = (int)c.attention_output_width, kw = (int)c.kv_width;
@@ -658,6 +665,8 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
         pd.ld_out = d;
         if ((rc = timed_gemm(s, L.down, pd))) return rc;
     }
+    s->last_n = head ? n : 0;
+    if (!head) return NC_OK;  // a prompt chunk whose logits nobody reads (prefill_pass_batch)
     // compute_logits_from_hidden (inference.rs:4783-4832) for every row + argmax
     if ((rc = launch_rmsnorm_q8(s->hidden, m->out_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st))) return rc;
     GemmParams ph;
@@ -680,6 +689,13 @@ static int run_pass(nc_session* s, int n, int64_t start_pos) {
 // start position through kernel arguments.
 static int upload_toks(nc_session* s, const uint32_t* toks, int n) {
     if (n < 1 || n > 16) return fail(NC_ERANGE, "batch must be 1..16 tokens");
+    // The embedding gather indexes tok_emb[tok * d]: an id past the vocabulary is refused on
+    // the host before anything launches (the reference panics on the slice index,
+    // inference.rs:3728-3733).
+    for (int i = 0; i < n; i++)
+        if (toks[i] >= (uint32_t)s->m->cfg.vocab_size)
+            return fail(NC_ERANGE, "token id " + std::to_string(toks[i]) + " >= vocab_size " +
+                                       std::to_string(s->m->cfg.vocab_size));
     std::memcpy(s->staged, toks, n * sizeof(uint32_t));
     s->n_staged = n;
     s->pending_toks = true;
@@ -695,7 +711,8 @@ static int fetch_preds(nc_session* s, int n, uint32_t* out) {
 
 // prefill_tokens (main.rs:9415-9485): chunks of max_batch rows.  Returns the last row's
 // greedy prediction in *last_pred.
-static int prefill_chunks(nc_session* s, const uint32_t* toks, int n, int64_t start_pos, uint32_t* last_pred) {
+static int prefill_chunks(nc_session* s, const uint32_t* toks, int n, int64_t start_pos, uint32_t* last_pred,
+                          bool last_logits = false) {
     // per-kernel timing covers decode and verify passes only, never the prompt
     struct TimingOff {
         nc_session* s;
@@ -704,10 +721,15 @@ static int prefill_chunks(nc_session* s, const uint32_t* toks, int n, int64_t st
     } guard{s, s->timing};
     s->timing = false;
     int rc;
+    for (int i = 0; i < n; i++)  // every id is checked before the first chunk runs
+        if (toks[i] >= (uint32_t)s->m->cfg.vocab_size)
+            return fail(NC_ERANGE, "prompt token id " + std::to_string(toks[i]) + " >= vocab_size");
+    if (start_pos < 0 || start_pos + n > s->max_ctx) return fail(NC_ERANGE, "prompt exceeds the session context");
+    const bool head = last_pred || last_logits;
     for (int i = 0; i < n; i += s->max_batch) {
         const int len = std::min(s->max_batch, n - i);
         if ((rc = upload_toks(s, toks + i, len))) return rc;
-        if ((rc = run_pass(s, len, start_pos + i))) return rc;
+        if ((rc = run_pass(s, len, start_pos + i, head && i + len == n))) return rc;
     }
     if (last_pred) {
         uint32_t preds[16];
@@ -771,9 +793,17 @@ int nc_ctx_create(int device, nc_ctx** out) {
     auto* c = new nc_ctx();
     c->device = device;
     hipError_t e = hipStreamCreate(&c->stream);
+    if (e == hipSuccess) {
+        c->xsum_cap = 16 * kCtxScratchCols / 32;
+        e = hipMalloc((void**)&c->xsum, c->xsum_cap * sizeof(int32_t));
+    }
+    if (e == hipSuccess) {
+        c->tp_cap = temperature_scratch_floats(16);
+        e = hipMalloc((void**)&c->tp_scratch, c->tp_cap * sizeof(float));
+    }
     if (e != hipSuccess) {
-        delete c;
-        return fail(NC_EHIP, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+        nc_ctx_free(c);
+        return fail(NC_EHIP, std::string("nc_ctx_create: ") + hipGetErrorString(e));
     }
     *out = c;
     return NC_OK;
@@ -987,6 +1017,9 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
     if (max_batch < 1 || max_batch > 16) return fail(NC_EINVAL, "max_batch must be 1..16");
     if (max_ctx < 1 || max_ctx > m->cfg.context_length)
         return fail(NC_ERANGE, "max_ctx must be in 1..context_length");
+    if (max_ctx > NC_MAX_CONTEXT)
+        return fail(NC_ERANGE, "max_ctx exceeds the attention kernels' " + std::to_string(NC_MAX_CONTEXT) +
+                                   "-position score rows");
     NC_HIP(hipSetDevice(m->ctx->device));
     std::unique_ptr<nc_session, void (*)(nc_session*)> s(new nc_session(), nc_session_free);
     s->m = m;
@@ -1022,16 +1055,33 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
     NC_HIP(hipHostMalloc((void**)&s->h_preds, 64 * sizeof(uint32_t), hipHostMallocDefault));
     NC_HIP(hipHostMalloc((void**)&s->h_result, 16 * sizeof(int32_t), hipHostMallocDefault));
     NC_HIP(hipHostMalloc((void**)&s->h_pos, 16 * sizeof(int32_t), hipHostMallocDefault));
-    // RoPE (sin, cos) table, cached_rope_angles (inference.rs:880-901), from glibc on the
-    // host: theta = base.powf(-(2i)/rope_dim), (sin, cos) = (pos*theta).sin_cos().
+    // RoPE (sin, cos) table, cached_rope_angles (inference.rs:860-901), from glibc on the
+    // host: theta = base.powf(-(2i)/rope_dim), Llama-3 frequency scaling when the model
+    // carries it (inference.rs:875-893), (sin, cos) = (pos*theta).sin_cos().
     const int64_t half = c.rope_dimension_count / 2;
     std::vector<float> tab((size_t)max_ctx * half * 2);
     static float (*volatile p_sinf)(float) = sinf;
     static float (*volatile p_cosf)(float) = cosf;
     static float (*volatile p_powf)(float, float) = powf;
     std::vector<float> theta(half);
-    for (int64_t i = 0; i < half; i++)
-        theta[i] = p_powf(c.rope_freq_base, -((float)(i * 2)) / (float)c.rope_dimension_count);
+    for (int64_t i = 0; i < half; i++) {
+        float th = p_powf(c.rope_freq_base, -((float)(i * 2)) / (float)c.rope_dimension_count);
+        if (c.rope_scaling) {
+            const float factor = c.rope_scaling_factor, orig = c.rope_scaling_original_context_length;
+            const float low = c.rope_scaling_low_freq_factor, high = c.rope_scaling_high_freq_factor;
+            const float wavelength = (2.0f * 3.14159265358979323846f) / th;
+            const float low_wl = orig / low, high_wl = orig / high;
+            if (wavelength >= high_wl) {
+                if (wavelength > low_wl) {
+                    th = th / factor;
+                } else {
+                    const float smooth = (orig / wavelength - low) / (high - low);
+                    th = ((1.0f - smooth) * th / factor) + (smooth * th);
+                }
+            }
+        }
+        theta[i] = th;
+    }
     for (int64_t pos = 0; pos < max_ctx; pos++)
         for (int64_t i = 0; i < half; i++) {
             const float angle = (float)pos * theta[i];
@@ -1051,8 +1101,7 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
 int nc_prefill(nc_session* s, const uint32_t* toks, int32_t n, int64_t start_pos, int32_t want_logits) {
     if (!s || !toks || n < 1) return fail(NC_EINVAL, "nc_prefill: bad arguments");
     NC_HIP(hipSetDevice(s->ctx->device));
-    (void)want_logits;
-    int rc = prefill_chunks(s, toks, n, start_pos, nullptr);
+    int rc = prefill_chunks(s, toks, n, start_pos, nullptr, want_logits != 0);
     if (rc) return rc;
     NC_HIP(hipStreamSynchronize(s->stream));
     return flush_timing(s);
@@ -1147,6 +1196,9 @@ int nc_generate_speculative_oracle(nc_session* s, const uint32_t* prompt, int32_
     if (n_prompt + n_new > s->max_ctx) return fail(NC_ERANGE, "prompt + new tokens exceed the session context");
     NC_HIP(hipSetDevice(s->ctx->device));
     const uint32_t V = (uint32_t)s->m->cfg.vocab_size;
+    // the drafter copies greedy[] into verify batches: every id must be a vocabulary id
+    for (int32_t i = 0; i < n_greedy; i++)
+        if (greedy[i] >= V) return fail(NC_ERANGE, "greedy record holds an id >= vocab_size");
     const double t0 = now_s();
     uint32_t pending;
     int rc = prefill_chunks(s, prompt, n_prompt, 0, &pending);
@@ -1252,8 +1304,11 @@ int nc_generate_speculative_ngram(nc_session* s, const uint32_t* prompt, int32_t
 
 int nc_generate_speculative_draft(nc_session* tg, nc_session* dr, const uint32_t* prompt, int32_t n_prompt,
                                   int32_t n_new, int32_t draft_k, uint32_t* out, nc_decode_stats* stats) {
-    if (!tg || !dr || !prompt || !out || n_prompt < 1 || n_new < 1 || draft_k < 1)
+    if (!tg || !dr || tg == dr || !prompt || !out || n_prompt < 1 || n_new < 1 || draft_k < 1)
         return fail(NC_EINVAL, "nc_generate_speculative_draft: bad arguments");
+    // drafts produced by one model are fed to the other's embedding: the vocabularies must agree
+    if (tg->m->cfg.vocab_size != dr->m->cfg.vocab_size) return fail(NC_EINVAL, "target and draft vocabularies differ");
+    if (tg->ctx->device != dr->ctx->device) return fail(NC_EINVAL, "target and draft must share a device");
     NC_HIP(hipSetDevice(tg->ctx->device));
     const double t0 = now_s();
     uint32_t tlive, dlive;
@@ -1319,7 +1374,7 @@ int nc_generate_speculative_stochastic(nc_session* tg, nc_session* dr, const uin
     const int V = (int)tg->m->cfg.vocab_size;
     const double t0 = now_s();
     int rc = prefill_chunks(dr, prompt, n_prompt, 0, nullptr);
-    if (rc || (rc = prefill_chunks(tg, prompt, n_prompt, 0, nullptr))) return rc;
+    if (rc || (rc = prefill_chunks(tg, prompt, n_prompt, 0, nullptr, true))) return rc;
     NC_HIP(hipStreamSynchronize(dr->stream));
     // The draft's kernels run on the target's stream for the decode loop: the draft samples
     // feed the target's token buffer and probability rows without cross-stream waits.
@@ -1340,17 +1395,20 @@ int nc_generate_speculative_stochastic(nc_session* tg, nc_session* dr, const uin
     NC_HIP(hipStreamSynchronize(st));
     uint32_t pending = (uint32_t)tg->h_result[1];
     const double t1 = now_s();
-    int64_t pos = n_prompt, dvalid = n_prompt, produced = 0, steps = 0, drafted = 0, accepted = 0;
+    int64_t pos = n_prompt, produced = 0, steps = 0, drafted = 0, accepted = 0;
     uint32_t last_draft = 0, toks[16];
+    // catch_up: the last step drafted and accepted every draft, so the draft model has not
+    // run its last draft d_{k-1} (at pos - 1).  kk only shrinks with pos, so once a step
+    // drafts nothing (k = 0, or the context end) the draft model is never needed again.
+    bool catch_up = false;
     out[produced++] = pending;
     while (produced < n_new) {
         int64_t kk = std::min<int64_t>(k, tg->max_batch - 1);
         kk = std::min<int64_t>(kk, tg->max_ctx - pos - 1);
         kk = std::min<int64_t>(kk, dr->max_ctx - pos - 1);
         if (kk < 0) break;
-        if (dvalid < pos) {  // full acceptance last step: the draft has not seen d_{k-1}
-            if ((rc = upload_toks(dr, &last_draft, 1)) || (rc = run_pass(dr, 1, dvalid))) return rc;
-            dvalid++;
+        if (kk > 0 && catch_up) {
+            if ((rc = upload_toks(dr, &last_draft, 1)) || (rc = run_pass(dr, 1, pos - 1))) return rc;
         }
         // k draft forwards; draft i's sample becomes the next draft input and target row i+1
         for (int64_t i = 0; i < kk; i++) {
@@ -1362,7 +1420,6 @@ int nc_generate_speculative_stochastic(nc_session* tg, nc_session* dr, const uin
                                           dr->d_toks, st)))
                 return rc;
         }
-        if (kk > 0) dvalid = pos + kk;
         // target verify of [pending, d_0 .. d_{kk-1}]: only row 0 comes from the host
         nc_verify_result r;
         if ((rc = upload_toks(tg, &pending, 1)) || (rc = run_pass(tg, (int)kk + 1, pos)) ||
@@ -1374,6 +1431,7 @@ int nc_generate_speculative_stochastic(nc_session* tg, nc_session* dr, const uin
         for (int i = 1; i <= r.n_accepted && produced < n_new; i++) out[produced++] = toks[i];
         if (produced < n_new) out[produced++] = r.next_token;
         if (kk > 0) last_draft = toks[kk];
+        catch_up = kk > 0 && r.n_accepted == kk;
         pending = r.next_token;
         pos = r.new_pos;
         steps++;

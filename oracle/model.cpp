@@ -202,6 +202,8 @@ struct or_model {
     int64_t ctx = 0, d = 0, L = 0, F = 0, H = 0, Hkv = 0, hd = 0, rope_dim = 0, V = 0;
     int64_t attn_w = 0, kv_w = 0;
     float rope_base = 10000.0f, eps = 1e-5f;
+    bool has_rope_scaling = false;
+    float rope_scaling[4] = {0, 0, 0, 0};  // factor, original_context_length, low, high
     bool has_output = false;
     uint32_t wtype = 2;
     std::vector<float> tok_emb, out_norm;
@@ -292,6 +294,20 @@ bool build_model(or_model* m, const uint8_t* data, size_t size, std::string& err
     if (m->d % m->H || m->Hkv == 0 || m->H % m->Hkv) { err = "bad head geometry"; return false; }
     float f;
     m->rope_base = meta_f32(g, P + "rope.freq_base", &f) ? f : 10000.0f;
+    {  // rope_scaling_from_gguf (main.rs:8522-8535)
+        float fac, lo, hi;
+        uint32_t orig;
+        m->has_rope_scaling = meta_f32(g, P + "rope.scaling.factor", &fac) &&
+                              meta_u32(g, P + "rope.scaling.original_context_length", &orig) &&
+                              meta_f32(g, P + "rope.scaling.low_freq_factor", &lo) &&
+                              meta_f32(g, P + "rope.scaling.high_freq_factor", &hi);
+        if (m->has_rope_scaling) {
+            m->rope_scaling[0] = fac;
+            m->rope_scaling[1] = (float)orig;
+            m->rope_scaling[2] = lo;
+            m->rope_scaling[3] = hi;
+        }
+    }
     m->eps = meta_f32(g, P + "attention.layer_norm_rms_epsilon", &f) ? f : 1e-5f;
     const Tensor* te = g.find("token_embd.weight");
     if (!te) { err = "missing token_embd.weight"; return false; }
@@ -364,8 +380,9 @@ void run_layers(or_session* s, int64_t N, int64_t start_pos) {
         matmul(m, s->v.data(), s->xq.data(), s->xs.data(), ly.wv, N);
         for (int64_t t = 0; t < N; t++) {
             int64_t pos = start_pos + t;
-            or_rope(&s->q[t * aw], pos, m->H, m->hd, m->rope_dim, m->rope_base, 0);
-            or_rope(&s->k[t * kw], pos, m->Hkv, m->hd, m->rope_dim, m->rope_base, 0);
+            const float* rs = m->has_rope_scaling ? m->rope_scaling : nullptr;
+            or_rope_scaled(&s->q[t * aw], pos, m->H, m->hd, m->rope_dim, m->rope_base, 0, rs);
+            or_rope_scaled(&s->k[t * kw], pos, m->Hkv, m->hd, m->rope_dim, m->rope_base, 0, rs);
             size_t off = ((size_t)li * s->max_ctx + pos) * kw;  // inference.rs:539-548
             std::copy(&s->k[t * kw], &s->k[t * kw] + kw, &s->kc[off]);
             std::copy(&s->v[t * kw], &s->v[t * kw] + kw, &s->vc[off]);
@@ -885,8 +902,9 @@ int64_t or_generate_speculative_stochastic(or_session* tg, or_session* dr, const
     or_temperature_probs(tg->logits.data(), V, temp, p.data());
     uint32_t pending = 0;
     sample_fixed(p.data(), V, philox_u24(seed, (uint64_t)(n_prompt - 1), PURPOSE_BONUS), &pending);
-    int64_t pos = n_prompt, dvalid = n_prompt, produced = 0, steps = 0;
+    int64_t pos = n_prompt, produced = 0, steps = 0;
     uint32_t last_draft = 0;
+    bool catch_up = false;  // the last step accepted all of its drafts (and drafted some)
     stats[0] = stats[1] = 0;
     out[produced++] = pending;
     std::vector<uint32_t> batch;
@@ -895,10 +913,7 @@ int64_t or_generate_speculative_stochastic(or_session* tg, or_session* dr, const
         kk = std::min(kk, tg->max_ctx - pos - 1);
         kk = std::min(kk, dr->max_ctx - pos - 1);
         if (kk < 0) break;
-        if (dvalid < pos) {  // full acceptance last step: the draft has not seen d_{k-1}
-            or_forward_pass(dr, last_draft, dvalid);
-            dvalid++;
-        }
+        if (kk > 0 && catch_up) or_forward_pass(dr, last_draft, pos - 1);  // d_{k-1} at pos - 1
         batch.assign(1, pending);
         q.resize((size_t)kk * V);
         uint32_t x = pending;
@@ -908,7 +923,6 @@ int64_t or_generate_speculative_stochastic(or_session* tg, or_session* dr, const
             sample_fixed(&q[(size_t)i * V], V, philox_u24(seed, (uint64_t)(pos + i), PURPOSE_DRAFT), &x);
             batch.push_back(x);
         }
-        dvalid = pos + kk;
         or_prefill_pass_batch(tg, batch.data(), kk + 1, pos);
         lg.resize((size_t)(kk + 1) * V);
         for (int64_t i = 0; i <= kk; i++) or_batch_row_logits(tg, i, &lg[(size_t)i * V]);
@@ -920,6 +934,7 @@ int64_t or_generate_speculative_stochastic(or_session* tg, or_session* dr, const
         for (int64_t i = 1; i <= a && produced < n_new; i++) out[produced++] = batch[i];
         if (produced < n_new) out[produced++] = next;
         if (kk > 0) last_draft = batch[kk];
+        catch_up = kk > 0 && a == kk;
         pos += a + 1;
         pending = next;
         steps++;

@@ -74,6 +74,13 @@ void or_rope(float* data, int64_t pos, int64_t heads, int64_t head_dim, int64_t 
              float freq_base, int style);
 /* (sin, cos) table entry for pair i at pos (inference.rs:880-901). */
 void or_rope_sincos(int64_t pos, int64_t i, int64_t rope_dim, float freq_base, float* s, float* c);
+/* Llama-3 scaled RoPE (inference.rs:874-893; scaling = {factor, original_context_length,
+ * low_freq_factor, high_freq_factor} or NULL for none). */
+float or_rope_theta(int64_t i, int64_t rope_dim, float freq_base, const float* scaling);
+void or_rope_sincos_scaled(int64_t pos, int64_t i, int64_t rope_dim, float freq_base, const float* scaling,
+                           float* s, float* c);
+void or_rope_scaled(float* data, int64_t pos, int64_t heads, int64_t head_dim, int64_t rope_dim,
+                    float freq_base, int style, const float* scaling);
 void or_softmax(float* x, int64_t n);          /* :3522-3540 */
 float or_expf(float x);                        /* Rust f32::exp == glibc expf */
 void or_silu_mul(float* out, const float* gate, const float* up, int64_t n); /* :3367-3390 */

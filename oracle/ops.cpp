@@ -304,24 +304,51 @@ void or_rms_norm(float* out, const float* x, const float* w, int64_t n, float ep
 
 // inference.rs:880-901 cached_rope_angles (no rope scaling keys in these models):
 // theta = base.powf(-(2i) / rope_dim); (sin, cos) = (pos * theta).sin_cos().
-void or_rope_sincos(int64_t pos, int64_t i, int64_t rope_dim, float freq_base, float* s, float* c) {
+// inference.rs:874-893 (cached_rope_angles) / :763-786 (apply_rope): theta of pair i, with the
+// Llama-3 frequency scaling when scaling = {factor, original_context_length, low_freq_factor,
+// high_freq_factor} is given (all four present, as the reference requires).
+float or_rope_theta(int64_t i, int64_t rope_dim, float freq_base, const float* scaling) {
+    static float (*volatile p_powf)(float, float) = powf;
+    float theta = p_powf(freq_base, -((float)(i * 2)) / (float)rope_dim);
+    if (scaling) {
+        const float factor = scaling[0], orig_len = scaling[1], low = scaling[2], high = scaling[3];
+        const float wavelength = (2.0f * (float)M_PI) / theta;
+        const float low_freq_wavelength = orig_len / low;
+        const float high_freq_wavelength = orig_len / high;
+        if (wavelength >= high_freq_wavelength) {
+            if (wavelength > low_freq_wavelength) {
+                theta /= factor;
+            } else {
+                const float smooth = (orig_len / wavelength - low) / (high - low);
+                theta = ((1.0f - smooth) * theta / factor) + (smooth * theta);
+            }
+        }
+    }
+    return theta;
+}
+
+void or_rope_sincos_scaled(int64_t pos, int64_t i, int64_t rope_dim, float freq_base, const float* scaling, float* s,
+                           float* c) {
     // Separate sinf and cosf calls as Rust's f32::sin_cos makes; the volatile pointers keep
     // the compiler from merging them into one sincosf call.
     static float (*volatile p_sinf)(float) = sinf;
     static float (*volatile p_cosf)(float) = cosf;
-    static float (*volatile p_powf)(float, float) = powf;
-    float theta = p_powf(freq_base, -((float)(i * 2)) / (float)rope_dim);
+    float theta = or_rope_theta(i, rope_dim, freq_base, scaling);
     float angle = (float)pos * theta;
     *s = p_sinf(angle);
     *c = p_cosf(angle);
 }
 
+void or_rope_sincos(int64_t pos, int64_t i, int64_t rope_dim, float freq_base, float* s, float* c) {
+    or_rope_sincos_scaled(pos, i, rope_dim, freq_base, nullptr, s, c);
+}
+
 // inference.rs:914-933 apply_rope_cached.
-void or_rope(float* data, int64_t pos, int64_t heads, int64_t head_dim, int64_t rope_dim,
-             float freq_base, int style) {
+void or_rope_scaled(float* data, int64_t pos, int64_t heads, int64_t head_dim, int64_t rope_dim,
+                    float freq_base, int style, const float* scaling) {
     int64_t half = rope_dim / 2;
     std::vector<float> sn(half), cs(half);
-    for (int64_t i = 0; i < half; i++) or_rope_sincos(pos, i, rope_dim, freq_base, &sn[i], &cs[i]);
+    for (int64_t i = 0; i < half; i++) or_rope_sincos_scaled(pos, i, rope_dim, freq_base, scaling, &sn[i], &cs[i]);
     for (int64_t h = 0; h < heads; h++) {
         int64_t hs = h * head_dim;
         for (int64_t i = 0; i < half; i++) {
@@ -332,6 +359,11 @@ void or_rope(float* data, int64_t pos, int64_t heads, int64_t head_dim, int64_t 
             data[d1] = x0 * sn[i] + x1 * cs[i];
         }
     }
+}
+
+void or_rope(float* data, int64_t pos, int64_t heads, int64_t head_dim, int64_t rope_dim,
+             float freq_base, int style) {
+    or_rope_scaled(data, pos, heads, head_dim, rope_dim, freq_base, style, nullptr);
 }
 
 float or_expf(float x) { return expf(x); }

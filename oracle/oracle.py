@@ -54,6 +54,7 @@ def lib():
         "or_rms_norm": (None, [_f32p, _f32p, _f32p, _i64, C.c_float]),
         "or_rope": (None, [_f32p, _i64, _i64, _i64, _i64, C.c_float, C.c_int]),
         "or_rope_sincos": (None, [_i64, _i64, _i64, C.c_float, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+        "or_rope_theta": (C.c_float, [_i64, _i64, C.c_float, C.c_void_p]),
         "or_softmax": (None, [_f32p, _i64]),
         "or_expf": (C.c_float, [C.c_float]),
         "or_silu_mul": (None, [_f32p, _f32p, _f32p, _i64]),
@@ -181,6 +182,13 @@ def rope_sincos(pos, i, rope_dim, base):
     s, c = C.c_float(), C.c_float()
     lib().or_rope_sincos(pos, i, rope_dim, base, C.byref(s), C.byref(c))
     return s.value, c.value
+
+
+def rope_theta(i, rope_dim, base, scaling=None):
+    """theta of RoPE pair i (inference.rs:874-893), Llama-3 scaled when scaling =
+    (factor, original_context_length, low_freq_factor, high_freq_factor)."""
+    sc = np.asarray(scaling, np.float32) if scaling is not None else None
+    return lib().or_rope_theta(i, rope_dim, base, sc.ctypes.data if sc is not None else None)
 
 
 def softmax(x):

@@ -13,8 +13,12 @@ pytestmark = pytest.mark.gpu
 
 torch = pytest.importorskip("torch")
 
+# Untied: a tied N(0, 0.02) head keeps predicting the last input token, so its streams would
+# repeat one id and stream checks would be near-vacuous.  Every checked stream has a floor of
+# distinct ids.
 TINY = dict(layers=2, embedding_length=256, head_count=4, head_count_kv=2, feed_forward_length=512, vocab_size=1000,
-            context_length=512, tied=1, norm_mode=1)
+            context_length=512, tied=0, norm_mode=1)
+MIN_DISTINCT = 8
 
 
 @pytest.fixture(scope="module")
@@ -34,10 +38,10 @@ def _same(a, b):
     return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
 
-@pytest.mark.parametrize("hd", [64, 128])
-def test_verify_logits_bit_exact(ctx, hd):
+@pytest.mark.parametrize("hd,tied", [(64, 1), (128, 0)])
+def test_verify_logits_bit_exact(ctx, hd, tied):
     import nanocamelid_amd as nc
-    spec = dict(TINY, head_count=256 // hd * 2, head_count_kv=256 // hd, embedding_length=512)
+    spec = dict(TINY, head_count=256 // hd * 2, head_count_kv=256 // hd, embedding_length=512, tied=tied)
     _, gm, om = _models(ctx, spec, seed=hd)
     gs = nc.Session(gm, 256, 16)
     os_ = O.Session(om, 256, 16)
@@ -91,6 +95,7 @@ def test_greedy_and_speculative_streams(ctx):
     _, gm, om = _models(ctx, TINY, seed=31)
     prompt = nc.uniform_prompt(77, 24, 1000)
     ref = O.Session(om, 400, 16).generate_greedy(prompt, 96)
+    assert len(set(ref.tolist())) >= MIN_DISTINCT
     out, st = nc.Session(gm, 400, 16).generate_greedy(prompt, 96)
     assert np.array_equal(out, ref)
     for k, alpha in ((2, 0.5), (4, 0.8), (8, 0.8), (4, 1.0)):
@@ -109,6 +114,7 @@ def test_ngram_speculation_streams(ctx):
     base = nc.uniform_prompt(9, 6, 1000)
     prompt = np.concatenate([base, base, base, nc.uniform_prompt(10, 4, 1000), base[:4]]).astype(np.uint32)
     ref = O.Session(om, 256, 16).generate_greedy(prompt, 64)
+    assert len(set(ref.tolist())) >= MIN_DISTINCT
     for k, mn, mx in ((1, 3, 4), (4, 3, 4), (8, 2, 5), (15, 3, 4)):
         print(f"ngram k={k} n={mn}..{mx}", flush=True)
         g_out, st = nc.Session(gm, 256, 16).generate_speculative_ngram(prompt, 64, k, mn, mx)
@@ -125,12 +131,107 @@ def test_ngram_speculation_streams(ctx):
 
 def test_draft_model_speculation(ctx):
     import nanocamelid_amd as nc
-    _, gm, om = _models(ctx, TINY, seed=32)
+    _, gm, om = _models(ctx, TINY, seed=21)
     prompt = nc.uniform_prompt(78, 20, 1000)
     ref = O.Session(om, 300, 16).generate_greedy(prompt, 60)
+    assert len(set(ref.tolist())) >= MIN_DISTINCT
     out, st = nc.generate_speculative_draft(nc.Session(gm, 300, 16), nc.Session(gm, 300, 4), prompt, 60, 4)
     assert np.array_equal(out, ref)
     assert st.accepted == st.drafted and st.drafted > 0
+
+
+def test_draft_model_rejection_path(ctx):
+    """speculative_decoding_step (speculative.rs:384-447) with a draft that disagrees part of the
+    time (the target's weights with unit norm weights): corrective tokens, the corrective
+    forwards on both models and pos = at + 1 all run.  GPU stream == oracle stream == target
+    greedy stream, identical statistics, 0 < accepted < drafted."""
+    import nanocamelid_amd as nc
+    img, gm, om = _models(ctx, TINY, seed=21)
+    dimg = nc.synth_gguf(**dict(TINY, norm_mode=0), seed=21)
+    dm, odm = nc.Model(ctx, data=dimg), O.Model(data=dimg.tobytes())
+    prompt = nc.uniform_prompt(78, 20, 1000)
+    ref = O.Session(om, 300, 16).generate_greedy(prompt, 60)
+    for k in (1, 4, 8):
+        out, st = nc.generate_speculative_draft(nc.Session(gm, 300, 16), nc.Session(dm, 300, 8), prompt, 60, k)
+        o_out, drafted, accepted, steps = O.generate_speculative_draft(O.Session(om, 300, 16), O.Session(odm, 300, 8),
+                                                                       prompt, 60, k)
+        assert np.array_equal(out, ref) and np.array_equal(o_out, ref), k
+        assert (st.drafted, st.accepted, st.steps) == (drafted, accepted, steps), k
+        assert 0 < st.accepted < st.drafted, k
+
+
+def test_error_contract_keeps_session_usable(ctx):
+    """Bounds the reference enforces by panicking come back as NC_ERANGE / NC_EINVAL before any
+    launch, and the session still verifies bit-exactly afterwards."""
+    import nanocamelid_amd as nc
+    from nanocamelid_amd import NcError
+    _, gm, om = _models(ctx, TINY, seed=4)
+    gs, os_ = nc.Session(gm, 128, 16), O.Session(om, 128, 16)
+    toks = nc.uniform_prompt(3, 21, 1000)
+    gs.prefill_pass_batch(toks[:16], 0)
+    os_.prefill_pass_batch(toks[:16], 0)
+    bad = toks[16:].copy()
+    bad[2] = 1000  # == vocab_size (inference.rs:3728-3733 panics on the embedding index)
+    for call in (lambda: gs.verify_greedy(bad, 16), lambda: gs.forward_pass(5000, 16),
+                 lambda: gs.prefill_pass_batch(bad, 16),
+                 lambda: gs.generate_speculative_oracle(toks[:8], 8, 4, 0.8, 1, np.array([1, 2, 1000], np.uint32))):
+        with pytest.raises(NcError) as e:
+            call()
+        assert e.value.code == nc._ffi.NC_ERANGE
+    with pytest.raises(NcError) as e:  # a session longer than the attention kernels' rows
+        nc.Session(nc.Model(ctx, data=nc.synth_gguf(**dict(TINY, context_length=20000), seed=4)), 16385, 4)
+    assert e.value.code == nc._ffi.NC_ERANGE
+    other = nc.Model(ctx, data=nc.synth_gguf(**dict(TINY, vocab_size=999), seed=4))
+    with pytest.raises(NcError) as e:  # draft ids index the target's embedding
+        nc.generate_speculative_draft(gs, nc.Session(other, 128, 4), toks[:8], 8, 4)
+    assert e.value.code == nc._ffi.NC_EINVAL
+    _, _, _, preds = gs.verify_greedy(toks[16:], 16)
+    opreds, _, ologits = os_.verify_greedy(toks[16:], 16, want_logits=True)
+    assert np.array_equal(preds, opreds)
+    for i in range(5):
+        assert _same(gs.logits(i), ologits[i]), i
+
+
+def test_prefill_without_logits_then_verify(ctx):
+    """nc_prefill with want_logits = 0 runs no head pass: the KV written is the same and the
+    following verify is still bit-identical; with want_logits = 1 the last chunk's logits are
+    readable and equal the oracle's."""
+    import nanocamelid_amd as nc
+    _, gm, om = _models(ctx, TINY, seed=9)
+    toks = nc.uniform_prompt(12, 45, 1000)
+    gs, os_ = nc.Session(gm, 128, 16), O.Session(om, 128, 16)
+    gs.prefill_pass_batch(toks[:40], 0, want_logits=False)
+    for i in range(0, 40, 16):
+        os_.prefill_pass_batch(toks[i:min(i + 16, 40)], i)
+    _, _, _, preds = gs.verify_greedy(toks[40:], 40)
+    opreds, _, ologits = os_.verify_greedy(toks[40:], 40, want_logits=True)
+    assert np.array_equal(preds, opreds)
+    for i in range(5):
+        assert _same(gs.logits(i), ologits[i]), i
+    gs2, os2 = nc.Session(gm, 128, 16), O.Session(om, 128, 16)
+    gs2.prefill_pass_batch(toks[:20], 0)  # want_logits = 1: rows of the last chunk (16..19)
+    os2.prefill_pass_batch(toks[:16], 0)
+    os2.prefill_pass_batch(toks[16:20], 16)
+    for i in range(4):
+        assert _same(gs2.logits(i), os2.batch_row_logits(i)), i
+
+
+def test_rope_scaling_model_logits(ctx):
+    """A Llama-3.1/3.2-style file with llama.rope.scaling.* keys: the host RoPE table applies the
+    frequency scaling of cached_rope_angles (inference.rs:875-893) and the logits stay
+    bit-identical to the oracle's across several positions."""
+    import nanocamelid_amd as nc
+    spec = dict(TINY, rope_freq_base=10000.0, rope_scaling=(8.0, 64, 1.0, 4.0))
+    _, gm, om = _models(ctx, spec, seed=17)
+    assert gm.config["rope_scaling"] == 1 and gm.config["rope_scaling_factor"] == 8.0
+    gs, os_ = nc.Session(gm, 256, 16), O.Session(om, 256, 16)
+    toks = nc.uniform_prompt(8, 100, 1000)
+    for pos in range(0, 96, 16):
+        _, _, _, preds = gs.verify_greedy(toks[pos:pos + 16], pos)
+        opreds, _, ologits = os_.verify_greedy(toks[pos:pos + 16], pos, want_logits=True)
+        assert np.array_equal(preds, opreds)
+        for i in range(16):
+            assert _same(gs.logits(i), ologits[i]), (pos, i)
 
 
 def test_q4_k_model_logits(ctx):

@@ -11,8 +11,11 @@ import pytest
 import nanocamelid_amd as nc
 from oracle import oracle as O
 
+# Untied: with a tied N(0, 0.02) head the hidden state stays close to the input embedding and the
+# greedy stream repeats the last prompt token, which would make stream checks vacuous.
 TINY = dict(layers=2, embedding_length=256, head_count=4, head_count_kv=2, feed_forward_length=512, vocab_size=1000,
-            context_length=512, tied=1, norm_mode=1)
+            context_length=512, tied=0, norm_mode=1)
+MIN_DISTINCT = 8  # floor on distinct ids in a checked stream
 
 
 @pytest.fixture(scope="module")
@@ -46,8 +49,9 @@ def test_chunked_prefill_equals_one_batch(tiny):
 
 def test_speculative_streams_equal_greedy(tiny):
     _, m = tiny
-    prompt = nc.uniform_prompt(7, 16, 1000)
+    prompt = nc.uniform_prompt(6, 16, 1000)
     greedy = O.Session(m, 256, 16).generate_greedy(prompt, 40)
+    assert len(set(greedy.tolist())) >= MIN_DISTINCT
     # oracle drafter, k+1 form
     for alpha in (0.5, 0.8, 1.0):
         out, drafted, accepted, steps = O.Session(m, 256, 16).generate_speculative_oracle(
@@ -91,3 +95,21 @@ def test_stochastic_speculation(tiny):
     assert np.array_equal(a[0], b[0]) and a[1:] == b[1:]
     assert 0 < a[2] < a[1]
     assert np.all(a[0] < 1000)
+
+
+def test_draft_model_rejection_path(tiny):
+    """speculative_decoding_step (speculative.rs:384-447) with a draft that disagrees part of
+    the time: the draft has the target's weights but unit norm weights.  The rejections run
+    the corrective token and the corrective forwards on both models; the emitted stream must
+    still be the target's greedy stream, with 0 < accepted < drafted."""
+    img, m = tiny
+    dimg = nc.synth_gguf(**dict(TINY, norm_mode=0), seed=21)
+    dm = O.Model(data=dimg.tobytes())
+    prompt = nc.uniform_prompt(78, 20, 1000)
+    greedy = O.Session(m, 300, 16).generate_greedy(prompt, 60)
+    assert len(set(greedy.tolist())) >= MIN_DISTINCT
+    for k in (1, 4, 8):
+        out, drafted, accepted, steps = O.generate_speculative_draft(O.Session(m, 300, 16), O.Session(dm, 300, 8),
+                                                                     prompt, 60, k)
+        assert np.array_equal(out, greedy), k
+        assert 0 < accepted < drafted, (k, accepted, drafted)
