@@ -80,6 +80,13 @@ int64_t nc_qmat_device_bytes(const nc_qmat* w);
  * stream: a hipStream_t or NULL for the context's default stream. */
 int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, const float* x_scales,
                               float* out, int batch_size, int64_t rows, int64_t cols, void* stream);
+/* Allocation-free variant of nc_matmul_quantized_batch (no reference counterpart: it is for
+ * callers that cannot allocate device memory, such as code under HIP graph capture or serving
+ * loops that forbid hipMalloc).  Same arguments, semantics and results; its only scratch is a
+ * static per-device array sized for batch_size * cols <= 16 * 65536 (larger: NC_ERANGE).  It
+ * calls no hipMalloc/hipFree.  Calls that overlap on one device share that array and race. */
+int nc_matmul_quantized_batch_noalloc(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, const float* x_scales,
+                                      float* out, int batch_size, int64_t rows, int64_t cols, void* stream);
 /* Debug/parity variant: writes the int32 per-block dot products (Q4_0:
  * sum (nib-8)*x per 32-block, q8.rs:2699; Q4_K: W_j = sum nib*x per 32-sub-block,
  * q8.rs:1339-1376) as dots[t][r][cols/32] (device pointer). */

@@ -69,6 +69,7 @@ SIGNATURES = {
     "nc_qmat_free": (None, [_vp]),
     "nc_qmat_device_bytes": (_i64, [_vp]),
     "nc_matmul_quantized_batch": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _vp]),
+    "nc_matmul_quantized_batch_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _vp]),
     "nc_matmul_blockdots": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _vp]),
     "nc_quantize_q8_0_batch": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _vp]),
     "nc_rms_norm_q8_0_batch": (C.c_int, [_vp, _vp, _vp, C.c_float, _vp, _vp, C.c_int, _i64, _vp]),

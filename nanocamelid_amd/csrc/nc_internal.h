@@ -160,6 +160,12 @@ int launch_accept_stochastic(const float* p, const float* q, int64_t ld, const u
 int launch_sample_probs(const float* probs, int V, uint64_t seed, int64_t pos, uint32_t purpose, uint32_t* out0,
                         uint32_t* out1, hipStream_t st);
 
+// Address of the allocation-free entry point's scratch array on the current device
+// (hipGetSymbolAddress of a file-scope __device__ array; each device has its own copy).
+int static_scratch_address(int32_t** out);
+// Capacity of that array in int32 entries: per-block sums of up to 16 rows x 65536 columns.
+constexpr size_t kStaticScratchInts = 16 * 65536 / 32;
+
 }  // namespace nc
 
 // ---------------------------------------------------------------- C ABI handles (opaque in the header)
@@ -172,6 +178,8 @@ struct nc_ctx {
     size_t xsum_cap = 0;
     float* tp_scratch = nullptr;  // temperature softmax partials
     size_t tp_cap = 0;
+    // device address of the static scratch array on this context's device (never freed)
+    int32_t* static_scratch = nullptr;
 };
 
 struct nc_qmat {

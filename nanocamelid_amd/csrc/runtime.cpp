@@ -792,6 +792,12 @@ int nc_ctx_create(int device, nc_ctx** out) {
     NC_HIP(hipSetDevice(device));
     auto* c = new nc_ctx();
     c->device = device;
+    // device address of the allocation-free entry point's static scratch array (noalloc.hip)
+    int rc0 = static_scratch_address(&c->static_scratch);
+    if (rc0) {
+        delete c;
+        return rc0;
+    }
     hipError_t e = hipStreamCreate(&c->stream);
     if (e == hipSuccess) {
         c->xsum_cap = 16 * kCtxScratchCols / 32;
