@@ -8,11 +8,15 @@ rows through the whole model on the GPU, per-row head + argmax, acceptance on th
 
 value = tokens emitted by K timed steps / wall time of those K steps (prefill excluded,
 weights and KV resident in HBM).  Also reported:
+  config.full_decode : the whole 1024-token decode of the config (k in {2, 4, 8}, alpha in
+                 {0.5, 0.8}), each a separate call after the timed steps;
   roofline     : the quantized GEMM family (all verify matmuls), algorithmic bytes per
                  launch over its average launch time measured with HIP events on the
                  session stream (a separate pass over the same workload);
-  cpu_baseline : the CPU oracle (C++ restatement of the reference's portable x86 path)
-                 decoding the same model on the host's cores, on a bounded sample.
+  cpu_baseline : the CPU oracle (C++ restatement of the reference's portable x86 path) on the
+                 host's cores: verify steps of the same model at the workload's positions, on
+                 min(16, nproc) threads and on the reference's default 4, plus a GPU-vs-CPU
+                 greedy stream comparison on the same model.
 Prints one JSON line.
 """
 import argparse
@@ -25,7 +29,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
-HOST_THREADS = 16  # the GPU box's CPU share for one GPU
+# Host threads: the box's CPU share for one GPU is 16 cores, whatever nproc reports there.
+HOST_THREADS = min(16, len(os.sched_getaffinity(0)))
+REFERENCE_DEFAULT_THREADS = 4  # the reference's default worker count (src/main.rs:64, :549-551)
 # rocprofv3 FETCH_SIZE + WRITE_SIZE summary of the verify GEMMs on this workload (each counter
 # scaled by what it reads for a 256 MiB copy); the command that made it is in the file.
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_gemm_llama3-8b_q4_0_k4_pmc_traffic.md")
@@ -35,40 +41,72 @@ def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(img, cfg, args, threads):
-    """Oracle decode on a bounded sample: 16-token prompt, greedy record, then speculative
-    steps with the same drafter (k, alpha).  Returns verified tok/s on `threads` threads."""
+def cpu_model_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(img, cfg, args, tok_per_step, gpu_stream, stream_prompt):
+    """The oracle on the host, on the same model.  (1) Verify-step time at the workload's
+    positions: the session's KV rows 0..n_prompt are filled (a timing aid: a 512-token CPU
+    prefill alone would take minutes), then k+1-row verify passes run at positions n_prompt..;
+    tok/s = the GPU run's tokens per step (same seed, same drafter, same greedy stream) over the
+    CPU's seconds per step.  Timed on HOST_THREADS threads and on the reference's default 4.
+    (2) Greedy stream identity: the oracle's greedy continuation of a 16-token prompt against
+    the GPU's, with the oracle's top-2 logit margin at the first divergence."""
     import numpy as np
 
     from oracle import oracle as O
     t0 = time.time()
-    om = O.Model(data=img.tobytes(), nthreads=threads)
+    om = O.Model(data=img.tobytes(), nthreads=HOST_THREADS)
     log(f"oracle model loaded in {time.time() - t0:.1f}s")
-    n_prompt, n_rec, steps = 16, 24, args.cpu_steps
-    prompt = np.array(__import__("nanocamelid_amd").uniform_prompt(args.seed, n_prompt, cfg["vocab_size"]))
-    s = O.Session(om, 256, 16)
-    greedy = s.generate_greedy(prompt, n_rec)
+    # (2) stream identity
+    s = O.Session(om, 64, 16)
+    preds, margins, _ = s.verify_greedy(stream_prompt, 0)
+    cpu_stream, cpu_margins = [int(preds[-1])], [float(margins[-1])]
+    for i in range(len(gpu_stream) - 1):
+        p, m, _ = s.verify_greedy(np.array([cpu_stream[-1]], np.uint32), len(stream_prompt) + i)
+        cpu_stream.append(int(p[0]))
+        cpu_margins.append(float(m[0]))
     s.close()
-    s = O.Session(om, 256, 16)
-    # time only the decode steps: prefill is included in the call, so time prefill alone too
-    tp = time.time()
-    s.generate_speculative_oracle(prompt, 1, args.k, args.alpha, args.seed, greedy)
-    t_prefill = time.time() - tp
-    s.close()
-    s = O.Session(om, 256, 16)
-    td = time.time()
-    out, drafted, accepted, nsteps = s.generate_speculative_oracle(prompt, min(n_rec, steps * (args.k + 1)), args.k,
-                                                                   args.alpha, args.seed, greedy)
-    t_dec = time.time() - td - t_prefill
-    ok = bool((out == greedy[:len(out)]).all())
-    s.close()
+    diverge = next((i for i, (a, b) in enumerate(zip(cpu_stream, gpu_stream)) if a != int(b)), None)
+    identity = {"prompt_tokens": len(stream_prompt), "tokens": len(cpu_stream),
+                "identical": diverge is None, "first_divergence": diverge,
+                "cpu_top2_margin_at_divergence": None if diverge is None else cpu_margins[diverge],
+                "min_cpu_top2_margin": round(min(cpu_margins), 6)}
+    log(f"gpu vs cpu greedy stream: {identity}")
+    # (1) verify-step time at positions n_prompt..
+    batch = np.asarray(gpu_stream[:args.k + 1], np.uint32)
+    timed = {}
+    for th, steps in ((HOST_THREADS, args.cpu_steps), (REFERENCE_DEFAULT_THREADS, max(1, args.cpu_steps // 3))):
+        om.set_threads(th)
+        s = O.Session(om, args.n_prompt + args.k + 8, 16)
+        s.fill_kv(args.n_prompt, 7)
+        t1 = time.time()
+        for i in range(steps):
+            s.verify_greedy(batch, args.n_prompt + i)
+        dt = (time.time() - t1) / steps
+        s.close()
+        timed[th] = (dt, steps)
+        log(f"cpu verify step ({args.k + 1} rows at position {args.n_prompt}) on {th} threads: {dt:.2f} s")
     om.close()
-    # the first emitted token comes from the prefill; the steps emit the rest
-    tok = len(out) - 1
-    return {"value": round(tok / t_dec, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": (f"same 8B-shape model on the host: {n_prompt}-token prompt, {nsteps} speculative steps "
-                       f"(k={args.k}, alpha={args.alpha}, {tok} tokens, {accepted}/{drafted} drafts accepted) "
-                       f"in {t_dec:.1f}s; stream identical to its greedy stream: {ok}")}
+    dt, steps = timed[HOST_THREADS]
+    dt4, steps4 = timed[REFERENCE_DEFAULT_THREADS]
+    return {"value": round(tok_per_step / dt, 4), "unit": "tok/s", "cores": HOST_THREADS, "kind": "port",
+            "cpu_model": cpu_model_name(), "nproc": os.cpu_count(),
+            "value_reference_default_threads": round(tok_per_step / dt4, 4),
+            "reference_default_threads": REFERENCE_DEFAULT_THREADS,
+            "seconds_per_verify_step": round(dt, 3), "seconds_per_verify_step_4_threads": round(dt4, 3),
+            "sample": (f"same {args.config}-shape model on the host: {steps} verify passes of {args.k + 1} rows at "
+                       f"positions {args.n_prompt}.. on {HOST_THREADS} threads ({steps4} on "
+                       f"{REFERENCE_DEFAULT_THREADS}), KV rows 0..{args.n_prompt} filled; scaled by the GPU run's "
+                       f"{tok_per_step:.3f} tokens per step"),
+            "stream_vs_gpu": identity}
 
 
 def measured_traffic(args):
@@ -301,8 +339,9 @@ def main():
     ap.add_argument("--n-new", type=int, default=1024)
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--roofline-steps", type=int, default=40)
-    ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-full-decode", action="store_true", help="skip the 1024-token decodes at each (k, alpha)")
     ap.add_argument("--gemm-sweep", action="store_true", help="config 1: isolated GEMM bandwidth table")
     ap.add_argument("--config3", action="store_true",
                     help="config 3: 3B Q4_K target + 1B Q4_0 draft, stochastic acceptance (T=1, k=4)")
@@ -377,6 +416,24 @@ def main():
         achieved = gemm_bytes / (gemm_ms / 1e3) / 1e9
         log(f"gemm: {launches} launches, {gemm_ms / launches * 1e3:.2f} us avg, "
             f"{gemm_bytes / launches / 1e6:.2f} MB avg -> {achieved:.0f} GB/s")
+    # the config's whole 1024-token decode at every (k, alpha) point, each a separate call
+    full = {}
+    if not args.no_full_decode:
+        for k in (2, 4, 8):
+            for alpha in (0.5, 0.8):
+                o, fs = sess.generate_speculative_oracle(prompt, args.n_new + 1, k, alpha, args.seed, greedy)
+                ftok = fs.emitted - 1
+                full[f"k{k}_alpha{alpha}"] = {
+                    "tok_s": round(ftok / fs.decode_seconds, 2), "tokens": int(ftok), "steps": int(fs.steps),
+                    "drafted": int(fs.drafted), "accepted": int(fs.accepted),
+                    "positions": f"{args.n_prompt}..{args.n_prompt + ftok}",
+                    "stream_equals_greedy": bool(np.array_equal(o, greedy[:len(o)]))}
+                log(f"full decode k={k} alpha={alpha}: {full[f'k{k}_alpha{alpha}']}")
+    # GPU greedy continuation of a 16-token prompt, for the CPU stream comparison
+    stream_prompt = prompt[:16]
+    s16 = nc.Session(model, 64, 16)
+    gpu_stream, _ = s16.generate_greedy(stream_prompt, 9)
+    s16.close()
     if args.copy_calibration:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -386,10 +443,11 @@ def main():
         log("copy calibration: 3 x 256 MiB device-to-device copies")
 
     cpu = None
+    tok_per_step = emitted_by_steps / max(st.steps, 1)
     if not args.no_cpu_baseline:
         sess.close()
         model.close()
-        cpu = cpu_baseline(img, cfg, args, HOST_THREADS)
+        cpu = cpu_baseline(img, cfg, args, tok_per_step, gpu_stream, stream_prompt)
         log(f"cpu baseline: {cpu}")
 
     # whole-pass bytes: verify weights + the K and V rows each step reads once (positions grow
@@ -413,8 +471,11 @@ def main():
         "dtype": "int8 dot -> int32, f32 accumulate",
         "data": "synthetic (random-init weights N(0,0.02) -> Q4_0, seeded uniform prompt)",
         "config": {"workload": f"{args.config}-shape Q4_0 greedy speculative decode, oracle drafter k={args.k} "
-                               f"alpha={args.alpha}, {args.n_prompt}-token prompt, {args.steps} steps "
-                               f"(~{args.n_new} new tokens)",
+                               f"alpha={args.alpha}, {args.n_prompt}-token prompt; timed: {st.steps} steps emitting "
+                               f"{emitted_by_steps} tokens at positions {args.n_prompt}..{args.n_prompt + emitted_by_steps}"
+                               f" (the config's full {args.n_new}-token decode at every k, alpha: full_decode)",
+                   "timed_positions": [args.n_prompt, args.n_prompt + emitted_by_steps],
+                   "full_decode": full,
                    "k": args.k, "alpha": args.alpha, "prompt_tokens": args.n_prompt,
                    "tokens_emitted": int(emitted_by_steps), "drafted": int(st.drafted),
                    "accepted": int(st.accepted), "stream_equals_greedy": parity,

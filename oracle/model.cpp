@@ -295,8 +295,8 @@ bool build_model(or_model* m, const uint8_t* data, size_t size, std::string& err
     float f;
     m->rope_base = meta_f32(g, P + "rope.freq_base", &f) ? f : 10000.0f;
     {  // rope_scaling_from_gguf (main.rs:8522-8535)
-        float fac, lo, hi;
-        uint32_t orig;
+        float fac = 0, lo = 0, hi = 0;
+        uint32_t orig = 0;
         m->has_rope_scaling = meta_f32(g, P + "rope.scaling.factor", &fac) &&
                               meta_u32(g, P + "rope.scaling.original_context_length", &orig) &&
                               meta_f32(g, P + "rope.scaling.low_freq_factor", &lo) &&
@@ -545,6 +545,27 @@ or_session* or_session_create(or_model* m, int64_t max_ctx, int64_t max_batch) {
 }
 
 void or_session_free(or_session* s) { delete s; }
+
+void or_model_set_threads(or_model* m, int nthreads) { m->nthreads = nthreads > 0 ? nthreads : 1; }
+
+void or_session_fill_kv(or_session* s, int64_t n, uint64_t seed) {
+    // Timing aid only: deterministic values in [-1, 1) (xorshift64*) in KV rows [0, n) of every
+    // layer, so that a pass at start_pos = n does the attention work of a real n-token context.
+    const int64_t kw = s->m->kv_w;
+    uint64_t x = seed | 1;
+    for (int64_t l = 0; l < s->m->L; l++)
+        for (int64_t p = 0; p < n && p < s->max_ctx; p++) {
+            float* k = &s->kc[((size_t)l * s->max_ctx + p) * kw];
+            float* v = &s->vc[((size_t)l * s->max_ctx + p) * kw];
+            for (int64_t i = 0; i < 2 * kw; i++) {
+                x ^= x >> 12;
+                x ^= x << 25;
+                x ^= x >> 27;
+                const float u = (float)((x * 0x2545F4914F6CDD1Dull) >> 40) * (1.0f / 8388608.0f) - 1.0f;
+                (i < kw ? k[i] : v[i - kw]) = u;
+            }
+        }
+}
 
 void or_prefill_pass_batch(or_session* s, const uint32_t* toks, int64_t n, int64_t start_pos) {
     if (n <= 0) return;

@@ -112,7 +112,14 @@ void or_model_info_f(const or_model* m, float* out2);
  * requantised per q8.rs:2442); returns bytes written or -1. */
 int64_t or_model_head_q4_0(const or_model* m, uint8_t* out, int64_t cap);
 
+/* Host threads the model's matmuls and attention heads use (row-parallel as rayon). */
+void or_model_set_threads(or_model* m, int nthreads);
+
 or_session* or_session_create(or_model* m, int64_t max_ctx, int64_t max_batch);
+/* CPU-baseline timing aid (no reference counterpart): fills KV rows [0, n) of every layer with
+ * deterministic pseudo-random values so that a pass at start_pos = n costs what it costs after
+ * an n-token prefill.  The session's outputs are then timing data, not parity data. */
+void or_session_fill_kv(or_session* s, int64_t n, uint64_t seed);
 void or_session_free(or_session* s);
 /* prefill_pass_batch (inference.rs:3695-3744): writes KV for start_pos..+n and
  * keeps per-row final hidden states. */

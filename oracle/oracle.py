@@ -68,6 +68,8 @@ def lib():
         "or_model_info_f": (None, [C.c_void_p, _f32p]),
         "or_model_head_q4_0": (_i64, [C.c_void_p, _u8p, _i64]),
         "or_session_create": (C.c_void_p, [C.c_void_p, _i64, _i64]),
+        "or_model_set_threads": (None, [C.c_void_p, C.c_int]),
+        "or_session_fill_kv": (None, [C.c_void_p, _i64, C.c_uint64]),
         "or_session_free": (None, [C.c_void_p]),
         "or_prefill_pass_batch": (None, [C.c_void_p, _u32p, _i64, _i64]),
         "or_forward_pass": (None, [C.c_void_p, C.c_uint32, _i64]),
@@ -294,6 +296,9 @@ class Model:
         L.or_model_info_f(h, fl)
         self.rope_base, self.eps = float(fl[0]), float(fl[1])
 
+    def set_threads(self, n: int):
+        lib().or_model_set_threads(self.h, int(n))
+
     def head_q4_0(self):
         n = self.info["vocab"] * (self.info["d"] // 32) * 18
         out = np.zeros(n, np.uint8)
@@ -326,6 +331,10 @@ class Session:
     def forward_pass(self, tok, pos):
         lib().or_forward_pass(self.h, int(tok), pos)
         return np.ctypeslib.as_array(lib().or_session_logits(self.h), (self.V,)).copy()
+
+    def fill_kv(self, n, seed=1):
+        """Timing aid: pseudo-random KV rows [0, n) in every layer (no parity meaning)."""
+        lib().or_session_fill_kv(self.h, n, seed)
 
     def batch_row_logits(self, row):
         out = np.zeros(self.V, np.float32)
