@@ -59,6 +59,17 @@ void nc_ctx_free(nc_ctx* ctx);
 /* Blocks until all work queued on the context's default stream finished. */
 int nc_ctx_synchronize(nc_ctx* ctx);
 
+/* Dot-product path of the quantized matmuls on 16-row tiles, for every call made through this
+ * context and its models' sessions; the counterpart of the reference's Q8DotKernelSelector
+ * (src/q8.rs:42-46), which picks scalar / NEON / SDOT block dots.  AUTO (the default) takes
+ * v_dot4c, the faster path at every measured shape and width; MFMA computes the same int32
+ * block dots with v_mfma_i32_16x16x32_i8 (bit-identical results).  Set it between calls, not
+ * while work of the context is queued. */
+#define NC_GEMM_KERNEL_AUTO 0
+#define NC_GEMM_KERNEL_DOT4 1
+#define NC_GEMM_KERNEL_MFMA 2
+int nc_ctx_set_gemm_kernel(nc_ctx* ctx, int kernel);
+
 /* ---------------------------------------------------------------- operator boundary */
 /* Uploads a row-major GGUF quantized matrix (rows x cols, GGUF dims [cols, rows])
  * and repacks it into the device layout.  Replaces the load-time matrix

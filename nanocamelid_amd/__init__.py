@@ -50,6 +50,11 @@ class Context:
     def synchronize(self):
         check(lib().nc_ctx_synchronize(self.h))
 
+    def set_gemm_kernel(self, kernel: int):
+        """Dot-product path of the quantized matmuls (NC_GEMM_KERNEL_AUTO / _DOT4 / _MFMA), the
+        counterpart of the reference's Q8DotKernelSelector (src/q8.rs:42-46)."""
+        check(lib().nc_ctx_set_gemm_kernel(self.h, int(kernel)))
+
     def close(self):
         if getattr(self, "h", None):
             lib().nc_ctx_free(self.h)

@@ -460,6 +460,119 @@ __device__ __forceinline__ void gemm_epilogue_r16(const GemmParams& p, float v, 
     }
 }
 
+// ---------------------------------------------------------------- R16 chain threads
+// The block-ordered f32 chains of a 16-row tile: after each round's barrier, thread (token cn,
+// row cr) adds that round's BR terms [BR][NMAX][16] of LDS buffer r & 1 in block order
+// (inference.rs:1553-1573), so the sum is bit-identical to the reference's per-row loop.
+
+// One round's chain step: adds the round's nblk terms of (token cn, row cr) in block order.
+template <int NMAX, int BR>
+__device__ __forceinline__ float r16_chain_step(const float* buf, int nblk, int cn, int cr, float acc) {
+    const float* src = buf + cn * 16 + cr;
+    // groups of 16 terms read ahead of their dependent adds
+    int bl = 0;
+    for (; bl + 16 <= nblk; bl += 16) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = src[(bl + i) * NMAX * 16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc = acc + v[i];
+    }
+    for (; bl < nblk; bl++) acc = acc + src[bl * NMAX * 16];
+    return acc;
+}
+
+// Dedicated chain wave of a four-tile group, token cn: one barrier per round, then its step;
+// lane = 16 * tile + row, so the wave holds the token's 32 gate and 32 up outputs and finishes
+// SwiGLU and the Q8_0 block with shuffles.
+template <int NMAX, int BR>
+__device__ __forceinline__ void r16_chain_wave_tpg4(const GemmParams& p, const float* lds_all, int cn) {
+    const int lane = threadIdx.x & 63;
+    const int sub = lane >> 4, cr = lane & 15;
+    const int nb = p.units;
+    const int nrounds = ((nb + 3) / 4 + BR / 4 - 1) / (BR / 4);
+    const bool active = cn < p.N;  // wave-uniform
+    float acc = 0.0f;
+    for (int r = 0; r < nrounds; r++) {
+        __syncthreads();  // round r's terms are in buffer r & 1 of every tile
+        if (active)
+            acc = r16_chain_step<NMAX, BR>(lds_all + ((size_t)sub * 2 + (r & 1)) * BR * NMAX * 16,
+                                           min(BR, nb - r * BR), cn, cr, acc);
+    }
+    if (active) {
+        // EPI_SWIGLU_Q8 (fused_silu_mul inference.rs:3367-3390, then quantize_f32_to_q8_0 of
+        // the 32-wide block, inference.rs:4034-4041): lanes 0-31 gate, 32-63 up
+        const int l = lane & 31;
+        const float g = __shfl(acc, l, 64);
+        const float up = __shfl(acc, 32 + l, 64);
+        const float sig = 1.0f / (1.0f + expf_glibc(-g));
+        const float y = g * sig * up;
+        const float amax = halfwave_amax(y);
+        float scale;
+        const int q = quantize_lane_q8(y, amax, &scale);
+        const int qs = halfwave_isum(q);
+        if (lane < 32) {
+            const int blk = blockIdx.x;
+            p.xq_out[(size_t)cn * p.F + blk * 32 + lane] = (int8_t)q;
+            if (lane == 0) {
+                p.xs_out[(size_t)cn * (p.F / 32) + blk] = scale;
+                p.xs8_out[(size_t)cn * (p.F / 32) + blk] = -8 * qs;
+            }
+        }
+    }
+}
+
+// Dedicated chain wave(s) of a one-tile group with S term waves: chain thread c = (token
+// c / 16, row c % 16).
+template <int NMAX, int BR, int S>
+__device__ __forceinline__ void r16_chain_wave_tpg1(const GemmParams& p, const float* lds_all) {
+    const int c = threadIdx.x - 64 * S;
+    const int cn = c >> 4, cr = c & 15;
+    const int nb = p.units;
+    const int nrounds = ((nb + 3) / 4 + BR / 4 - 1) / (BR / 4);
+    const bool active = c < 16 * NMAX && cn < p.N;
+    float acc = 0.0f;
+    for (int r = 0; r < nrounds; r++) {
+        __syncthreads();  // round r's terms are in buffer r & 1
+        if (active) acc = r16_chain_step<NMAX, BR>(lds_all + (size_t)(r & 1) * BR * NMAX * 16, min(BR, nb - r * BR),
+                                                   cn, cr, acc);
+    }
+    if (active) gemm_epilogue_r16<NMAX>(p, acc, cn, blockIdx.x, cr);
+}
+
+// EPI_SWIGLU_Q8 of a four-tile group whose chains ran on the term waves: rows 0-31 gate,
+// 32-63 up of output block blockIdx.x (fused_silu_mul inference.rs:3367-3390, then
+// quantize_f32_to_q8_0 of the 32-wide block, inference.rs:4034-4041).
+template <int NMAX>
+__device__ __forceinline__ void r16_swiglu_epilogue(const GemmParams& p, float* lds_all, bool chain, int sub, int cn,
+                                                    int cr, float acc, int wave_all) {
+    float* outv = lds_all;  // [64 rows][NMAX]
+    __syncthreads();        // every chain has read its last round's terms
+    if (chain) outv[(sub * 16 + cr) * NMAX + cn] = acc;
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int n = wave_all;  // one wave per token, lanes 0-31 = the 32 outputs
+    if (n < p.N) {
+        const int l = lane & 31;
+        const float g = outv[l * NMAX + n];
+        const float up = outv[(32 + l) * NMAX + n];
+        const float sig = 1.0f / (1.0f + expf_glibc(-g));
+        const float y = g * sig * up;
+        const float amax = halfwave_amax(y);
+        float scale;
+        const int q = quantize_lane_q8(y, amax, &scale);
+        const int qs = halfwave_isum(q);
+        if (lane < 32) {
+            const int blk = blockIdx.x;
+            p.xq_out[(size_t)n * p.F + blk * 32 + lane] = (int8_t)q;
+            if (lane == 0) {
+                p.xs_out[(size_t)n * (p.F / 32) + blk] = scale;
+                p.xs8_out[(size_t)n * (p.F / 32) + blk] = -8 * qs;
+            }
+        }
+    }
+}
+
 // TPG = 4: one workgroup covers four consecutive tiles (64 rows) with a group of S waves
 // each, sharing the per-round barrier; used for the interleaved gate,up matrix, whose 64-row
 // groups hold 32 gate rows and the 32 matching up rows, so that SwiGLU and the Q8_0
@@ -485,80 +598,14 @@ __global__ __launch_bounds__(64 * (S * TPG + CW)) void gemm_q4_0_r16_kernel(Gemm
     extern __shared__ float lds_all[];       // per tile group: [2][BR][NMAX][16]
     const int wave_all = wave_id_uniform();
     if constexpr (CW > 0 && TPG == 4) {
-        if (wave_all >= S * TPG) {  // chain wave of token cn: one barrier per round, then its step
-            const int cn = wave_all - S * TPG;
-            const int lane = threadIdx.x & 63;
-            const int sub = lane >> 4, cr = lane & 15;
-            const int nb = p.units;
-            const int nrounds = ((nb + 3) / 4 + QR - 1) / QR;
-            const bool active = cn < p.N;  // wave-uniform
-            float acc = 0.0f;
-            for (int r = 0; r < nrounds; r++) {
-                __syncthreads();  // round r's terms are in buffer r & 1 of every tile
-                if (active) {
-                    const int nblk = min(BR, nb - r * BR);
-                    const float* src =
-                        lds_all + ((size_t)sub * 2 + (r & 1)) * BR * NMAX * 16 + cn * 16 + cr;
-                    int bl = 0;
-                    for (; bl + 16 <= nblk; bl += 16) {
-                        float v[16];
-#pragma unroll
-                        for (int i = 0; i < 16; i++) v[i] = src[(bl + i) * NMAX * 16];
-#pragma unroll
-                        for (int i = 0; i < 16; i++) acc = acc + v[i];
-                    }
-                    for (; bl < nblk; bl++) acc = acc + src[bl * NMAX * 16];
-                }
-            }
-            if (active) {
-                // EPI_SWIGLU_Q8 (fused_silu_mul inference.rs:3367-3390, then quantize_f32_to_q8_0 of
-                // the 32-wide block, inference.rs:4034-4041): lanes 0-31 gate, 32-63 up
-                const int l = lane & 31;
-                const float g = __shfl(acc, l, 64);
-                const float up = __shfl(acc, 32 + l, 64);
-                const float sig = 1.0f / (1.0f + expf_glibc(-g));
-                const float y = g * sig * up;
-                const float amax = halfwave_amax(y);
-                float scale;
-                const int q = quantize_lane_q8(y, amax, &scale);
-                const int qs = halfwave_isum(q);
-                if (lane < 32) {
-                    const int blk = blockIdx.x;
-                    p.xq_out[(size_t)cn * p.F + blk * 32 + lane] = (int8_t)q;
-                    if (lane == 0) {
-                        p.xs_out[(size_t)cn * (p.F / 32) + blk] = scale;
-                        p.xs8_out[(size_t)cn * (p.F / 32) + blk] = -8 * qs;
-                    }
-                }
-            }
+        if (wave_all >= S * TPG) {  // chain wave of token wave_all - S * TPG
+            r16_chain_wave_tpg4<NMAX, BR>(p, lds_all, wave_all - S * TPG);
             return;
         }
     }
     if constexpr (CW > 0 && TPG == 1) {
-        if (wave_all >= S) {  // dedicated chain wave: one barrier per round, then its chain step
-            const int c = threadIdx.x - 64 * S;
-            const int cn = c >> 4, cr = c & 15;
-            const int nb = p.units;
-            const int nrounds = ((nb + 3) / 4 + QR - 1) / QR;
-            const bool active = c < 16 * NMAX && cn < p.N;
-            float acc = 0.0f;
-            for (int r = 0; r < nrounds; r++) {
-                __syncthreads();  // round r's terms are in buffer r & 1
-                if (active) {
-                    const int nblk = min(BR, nb - r * BR);
-                    const float* src = lds_all + (size_t)(r & 1) * BR * NMAX * 16 + cn * 16 + cr;
-                    int bl = 0;
-                    for (; bl + 16 <= nblk; bl += 16) {
-                        float v[16];
-#pragma unroll
-                        for (int i = 0; i < 16; i++) v[i] = src[(bl + i) * NMAX * 16];
-#pragma unroll
-                        for (int i = 0; i < 16; i++) acc = acc + v[i];
-                    }
-                    for (; bl < nblk; bl++) acc = acc + src[bl * NMAX * 16];
-                }
-            }
-            if (active) gemm_epilogue_r16<NMAX>(p, acc, cn, blockIdx.x, cr);
+        if (wave_all >= S) {  // dedicated chain wave
+            r16_chain_wave_tpg1<NMAX, BR, S>(p, lds_all);
             return;
         }
     }
@@ -590,7 +637,8 @@ __global__ __launch_bounds__(64 * (S * TPG + CW)) void gemm_q4_0_r16_kernel(Gemm
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, 0, N * p.K, 0x00020000);
     const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs, 0, N * nb * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t s8res = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs8, 0, N * nb * 4, 0x00020000);
-    const int wvo = lane * 16, svo = lane * 2;  // a quad's nibbles, then its 64 scales
+    // a quad's nibbles, then its 64 scales ([row / 4][block][row % 4]: this lane's is (j, i16))
+    const int wvo = lane * 16, svo = 2 * (16 * (i16 >> 2) + 4 * j + (i16 & 3));
     int xvo[NP], mvo[NM], mt[NM];
 #pragma unroll
     for (int q = 0; q < NP; q++) xvo[q] = (2 * q + xtok) * p.K + 32 * j + 4 * (i16 & 7);
@@ -660,20 +708,7 @@ __global__ __launch_bounds__(64 * (S * TPG + CW)) void gemm_q4_0_r16_kernel(Gemm
                     }
                 }
                 __syncthreads();
-                if (CW == 0 && tig < 16 * NMAX && cn < N) {
-                    const int nblk = min(BR, nb - r * BR);
-                    const float* src = buf + cn * 16 + cr;
-                    // groups of 16 terms read ahead of their dependent adds
-                    int bl = 0;
-                    for (; bl + 16 <= nblk; bl += 16) {
-                        float v[16];
-#pragma unroll
-                        for (int i = 0; i < 16; i++) v[i] = src[(bl + i) * NMAX * 16];
-#pragma unroll
-                        for (int i = 0; i < 16; i++) acc = acc + v[i];
-                    }
-                    for (; bl < nblk; bl++) acc = acc + src[bl * NMAX * 16];
-                }
+                if (CW == 0 && tig < 16 * NMAX && cn < N) acc = r16_chain_step<NMAX, BR>(buf, min(BR, nb - r * BR), cn, cr, acc);
             }
         }
     }
@@ -681,34 +716,155 @@ __global__ __launch_bounds__(64 * (S * TPG + CW)) void gemm_q4_0_r16_kernel(Gemm
     if constexpr (TPG == 1) {
         if (CW == 0 && tig < 16 * NMAX && cn < N) gemm_epilogue_r16<NMAX>(p, acc, cn, tile, cr);
     } else if constexpr (CW == 0) {
-        // EPI_SWIGLU_Q8 over the group's 64 rows: rows 0-31 gate, 32-63 up of output block
-        // blockIdx.x (fused_silu_mul inference.rs:3367-3390, then quantize_f32_to_q8_0 of the
-        // 32-wide block, inference.rs:4034-4041); the same expressions as the 64-row kernel.
-        float* outv = lds_all;  // [64 rows][NMAX]
-        __syncthreads();        // every chain has read its last round's terms
-        if (tig < 16 * NMAX && cn < N) outv[(sub * 16 + cr) * NMAX + cn] = acc;
-        __syncthreads();
-        const int lane = threadIdx.x & 63;
-        const int n = wave_all;  // one wave per token, lanes 0-31 = the 32 outputs
-        if (n < N) {
-            const int l = lane & 31;
-            const float g = outv[l * NMAX + n];
-            const float up = outv[(32 + l) * NMAX + n];
-            const float sig = 1.0f / (1.0f + expf_glibc(-g));
-            const float y = g * sig * up;
-            const float amax = halfwave_amax(y);
-            float scale;
-            const int q = quantize_lane_q8(y, amax, &scale);
-            const int qs = halfwave_isum(q);
-            if (lane < 32) {
-                const int blk = blockIdx.x;
-                p.xq_out[(size_t)n * p.F + blk * 32 + lane] = (int8_t)q;
-                if (lane == 0) {
-                    p.xs_out[(size_t)n * (p.F / 32) + blk] = scale;
-                    p.xs8_out[(size_t)n * (p.F / 32) + blk] = -8 * qs;
+        r16_swiglu_epilogue<NMAX>(p, lds_all, tig < 16 * NMAX && cn < N, sub, cn, cr, acc, wave_all);
+    }
+}
+
+// ---------------------------------------------------------------- Q4_0, 16-row tiles, int8 MFMA
+// Same tiles, rounds, LDS term buffers, chain threads and epilogues as gemm_q4_0_r16_kernel; the
+// per-block int32 dots come from v_mfma_i32_16x16x32_i8 instead of v_dot4c:
+//   A (16 x 32, weights): lane (g, r) holds row r's K subset g = nibble bytes 4g..4g+3 of the
+//     block, i.e. weights 4g..4g+3 (low nibbles) and 16+4g..16+4g+3 (high nibbles);
+//   B (32 x 16, activations): lane (g, c) holds token c's x[4g..4g+3] and x[16+4g..16+4g+3];
+//   C = -8 * sum(x) of (token c, block), so D = sum (nib - 8) * x exactly (|D| <= 32512);
+//   D lane (g, c) = token c, rows 4g..4g+3 (byte k of an A lane meets byte k of the B lane in
+//     the same 16-lane group: measured, and covered by the bit-exact tests).
+// Operands arrive compactly, each datum loaded once per wave: the quad's nibbles as before
+// (lane (j, r) = block j of row r) and a 4x4 transpose of the 16-lane groups (two permlane32
+// and two permlane16 swaps) gives lane (g, r) dword g of every block; token c's 128 activation
+// bytes of the quad as two 16-byte pieces per lane plus the same transpose; one dword of the
+// quad's 128 scale bytes per lane, and x_scale / -8*sum of (token, block) per lane, spread
+// with ds_bpermute.  Each lane then forms 16 terms (4 rows x 4 blocks of its token), the
+// reference's (w_scale * x_scale) * (float)dot.  One MFMA covers 16 tokens, so every width
+// 1..16 costs the same.  Measured on the 8B shapes it is bit-exact but not faster than the
+// v_dot4c kernel at any width (the round structure and operand delivery bound both), so the
+// dispatch selects it only on request (nc_ctx_set_gemm_kernel).
+typedef int nc_v4i __attribute__((ext_vector_type(4)));
+
+// out register b of lane (g, x) = in register g of lane (b, x) (g, b: 16-lane groups)
+__device__ __forceinline__ void rows_transpose4(uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {
+    const auto p02 = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);
+    const auto p13 = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
+    const auto q01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+    const auto q23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+    r0 = q01[0];
+    r1 = q01[1];
+    r2 = q23[0];
+    r3 = q23[1];
+}
+
+template <int NMAX, int S, int D, int TPG, int CW>
+__global__ __launch_bounds__(64 * (S * TPG + CW)) void gemm_q4_0_mfma_kernel(GemmParams p) {
+    static_assert(CW > 0 ? 16 * NMAX <= 64 * CW : 16 * NMAX <= 64 * S, "chain threads must fit their waves");
+    static_assert(TPG == 1 || TPG == 4, "tiles per workgroup");
+    static_assert(CW == 0 || TPG == 1 || CW == NMAX, "four-tile groups: one chain wave per token");
+    constexpr int QR = S;       // quads per round (one per term wave)
+    constexpr int BR = 4 * QR;  // blocks per round
+    extern __shared__ float lds_all[];  // per tile: [2][BR][NMAX][16] terms
+    const int wave_all = wave_id_uniform();
+    if constexpr (CW > 0 && TPG == 4) {
+        if (wave_all >= S * TPG) {
+            r16_chain_wave_tpg4<NMAX, BR>(p, lds_all, wave_all - S * TPG);
+            return;
+        }
+    }
+    if constexpr (CW > 0 && TPG == 1) {
+        if (wave_all >= S) {
+            r16_chain_wave_tpg1<NMAX, BR, S>(p, lds_all);
+            return;
+        }
+    }
+    const int sub = wave_all / S;  // tile of the group (TPG = 4)
+    const int wave = wave_all % S;
+    const int tile = blockIdx.x * TPG + sub;
+    float* lds = lds_all + (size_t)sub * 2 * BR * NMAX * 16;
+    const int tig = threadIdx.x - sub * 64 * S;
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, c = lane & 15;
+    const int N = p.N, nb = p.units;
+    const int nq = (nb + 3) / 4;
+    const uint8_t* wt = p.w + (size_t)tile * p.groups * kQ40ChunkBytes;
+    const int nrounds = (nq + QR - 1) / QR;
+    const int qmax = 8 * p.groups - 1;
+    const __amdgpu_buffer_rsrc_t wres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)wt, 0, p.groups * kQ40ChunkBytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, 0, N * p.K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs, 0, N * nb * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t s8res = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs8, 0, N * nb * 4, 0x00020000);
+    const int wvo = lane * 16;
+    const int svo = 1024 + 4 * (lane & 31);  // one dword of the quad's 128 scale bytes per lane
+    const int xvo = c * p.K + 16 * g;        // token c's 16-byte piece g (and g + 4) of the quad
+    const int mvo = (c * nb + g) * 4;        // x_scale / -8*sum of (token c, block g of the quad)
+    // bpermute sources: scales dwords 8g..8g+7 (rows 4g..4g+3 of the 4 blocks), meta of (c, block b)
+    const int sperm = 32 * g;                // byte address of lane 8g
+    uint4 rw[D], rxa[D], rxb[D];
+    uint32_t rs[D], rms[D], rm8[D];
+#define NC_MF_LOAD(R, SLOT)                                                                          \
+    do {                                                                                             \
+        const int qd_ = min(min((R), nrounds - 1) * QR + wave, qmax);                                \
+        const int qo_ = (qd_ >> 3) * kQ40ChunkBytes + (qd_ & 7) * kQ40R16QuadBytes;                  \
+        rw[SLOT] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wvo, qo_, 0)); \
+        rs[SLOT] = __builtin_amdgcn_raw_buffer_load_b32(wres, svo, qo_, 0);                          \
+        rxa[SLOT] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, xvo + 128 * qd_, 0, 0)); \
+        rxb[SLOT] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, xvo + 128 * qd_ + 64, 0, 0)); \
+        rms[SLOT] = __builtin_amdgcn_raw_buffer_load_b32(sres, mvo + 16 * qd_, 0, 0);               \
+        rm8[SLOT] = __builtin_amdgcn_raw_buffer_load_b32(s8res, mvo + 16 * qd_, 0, 0);              \
+    } while (0)
+#pragma unroll
+    for (int k = 0; k < D - 1; k++) NC_MF_LOAD(k, k);
+    float acc = 0.0f;
+    const int cn = tig >> 4, cr = tig & 15;  // chain thread: token, row
+    for (int r0 = 0; r0 < nrounds; r0 += D) {
+#pragma unroll
+        for (int k = 0; k < D; k++) {
+            const int r = r0 + k;
+            NC_MF_LOAD(r + D - 1, (k + D - 1) % D);
+            if (r < nrounds) {  // uniform
+                float* buf = lds + (size_t)(r & 1) * BR * NMAX * 16;
+                if (r * QR + wave < nq) {  // uniform
+                    uint32_t w0 = rw[k].x, w1 = rw[k].y, w2 = rw[k].z, w3 = rw[k].w;
+                    rows_transpose4(w0, w1, w2, w3);  // wb = dword g of block b, row c
+                    const uint32_t wb[4] = {w0, w1, w2, w3};
+                    // activations: after the transposes, lane (g, c) holds dwords g and 4 + g of
+                    // token c's blocks 0, 1 (from pieces 0..3) and 2, 3 (pieces 4..7)
+                    uint32_t a0 = rxa[k].x, a1 = rxa[k].y, a2 = rxa[k].z, a3 = rxa[k].w;
+                    uint32_t b0 = rxb[k].x, b1 = rxb[k].y, b2 = rxb[k].z, b3 = rxb[k].w;
+                    rows_transpose4(a0, a1, a2, a3);
+                    rows_transpose4(b0, b1, b2, b3);
+                    const uint32_t xd[8] = {a0, a1, a2, a3, b0, b1, b2, b3};
+                    // weight scales of rows 4g..4g+3 x 4 blocks: dwords 8g..8g+7 of the 128 bytes
+                    uint32_t sw[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+                        sw[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(sperm + 4 * i, (int)rs[k]);
+#pragma unroll
+                    for (int b = 0; b < 4; b++) {
+                        const float xsb = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (16 * b + c), (int)rms[k]));
+                        const int x8b = __builtin_amdgcn_ds_bpermute(4 * (16 * b + c), (int)rm8[k]);
+                        const uint64_t a = (uint64_t)(wb[b] & 0x0F0F0F0Fu) |
+                                           ((uint64_t)((wb[b] >> 4) & 0x0F0F0F0Fu) << 32);
+                        const uint64_t bx = (uint64_t)xd[2 * b] | ((uint64_t)xd[2 * b + 1] << 32);
+                        const nc_v4i cinit = {x8b, x8b, x8b, x8b};
+                        const nc_v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)bx, cinit, 0, 0, 0);
+                        float4 t;
+                        t.x = (f16_to_f32((uint16_t)(sw[2 * b] & 0xffff)) * xsb) * (float)d[0];
+                        t.y = (f16_to_f32((uint16_t)(sw[2 * b] >> 16)) * xsb) * (float)d[1];
+                        t.z = (f16_to_f32((uint16_t)(sw[2 * b + 1] & 0xffff)) * xsb) * (float)d[2];
+                        t.w = (f16_to_f32((uint16_t)(sw[2 * b + 1] >> 16)) * xsb) * (float)d[3];
+                        if (c < NMAX) *(float4*)(buf + ((wave * 4 + b) * NMAX + c) * 16 + 4 * g) = t;
+                    }
                 }
+                __syncthreads();
+                if (CW == 0 && tig < 16 * NMAX && cn < N)
+                    acc = r16_chain_step<NMAX, BR>(buf, min(BR, nb - r * BR), cn, cr, acc);
             }
         }
+    }
+#undef NC_MF_LOAD
+    if constexpr (TPG == 1) {
+        if (CW == 0 && tig < 16 * NMAX && cn < N) gemm_epilogue_r16<NMAX>(p, acc, cn, tile, cr);
+    } else if constexpr (CW == 0) {
+        r16_swiglu_epilogue<NMAX>(p, lds_all, tig < 16 * NMAX && cn < N, sub, cn, cr, acc, wave_all);
     }
 }
 
@@ -1090,6 +1246,47 @@ int launch_r16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
     return NC_OK;
 }
 
+// R16 with MFMA dots: the same launch shapes as launch_r16 (term waves per tile, dedicated
+// chain waves where they fit).
+template <int NMAX>
+int launch_r16_mfma(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    constexpr int D = 2;
+    if (p.epi == EPI_SWIGLU_Q8) {
+        // four 16-row tiles per workgroup; up to 8 rows one chain wave per token, wider the
+        // chains run on the first waves of each tile
+        constexpr int TPG = 4, CW = NMAX <= 8 ? NMAX : 0, S = CW ? 2 : 4;
+        if (p.ntiles % TPG) return fail(NC_EINVAL, "gemm: SwiGLU rows must fill whole 64-row groups");
+        const size_t lds = (size_t)TPG * 2 * 4 * S * NMAX * 16 * sizeof(float);
+        if (ev0)
+            hipExtLaunchKernelGGL((gemm_q4_0_mfma_kernel<NMAX, S, D, TPG, CW>), dim3(p.ntiles / TPG),
+                                  dim3(64 * (S * TPG + CW)), lds, st, ev0, ev1, 0, p);
+        else
+            hipLaunchKernelGGL((gemm_q4_0_mfma_kernel<NMAX, S, D, TPG, CW>), dim3(p.ntiles / TPG),
+                               dim3(64 * (S * TPG + CW)), lds, st, p);
+    } else {
+        constexpr int CW = (16 * NMAX + 63) / 64;
+        auto go = [&]<int S>() {
+            const size_t lds = (size_t)2 * 4 * S * NMAX * 16 * sizeof(float);
+            if (ev0)
+                hipExtLaunchKernelGGL((gemm_q4_0_mfma_kernel<NMAX, S, D, 1, CW>), dim3(p.ntiles), dim3(64 * (S + CW)),
+                                      lds, st, ev0, ev1, 0, p);
+            else
+                hipLaunchKernelGGL((gemm_q4_0_mfma_kernel<NMAX, S, D, 1, CW>), dim3(p.ntiles), dim3(64 * (S + CW)),
+                                   lds, st, p);
+        };
+        if constexpr (NMAX <= 6) {
+            if ((p.units + 3) / 4 >= 64)
+                go.template operator()<12>();
+            else
+                go.template operator()<8>();
+        } else {
+            go.template operator()<8>();
+        }
+    }
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
 template <int NMAX>
 int launch_s(int S, const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     switch (S) {
@@ -1169,6 +1366,11 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent
     p.K = (int)w.cols;
     if (p.N < 1 || p.N > 16) return fail(NC_EINVAL, "gemm: batch must be 1..16");
     if (w.layout == LAYOUT_R16) {
+        // dot products by v_dot4c (AUTO: the faster path at every measured shape and width) or,
+        // on request, by int8 MFMA
+        if (p.kernel == NC_GEMM_KERNEL_MFMA) {
+            NC_GEMM_FOR_NMAX(launch_r16_mfma, p.N, w, p, st, ev0, ev1)
+        }
         NC_GEMM_FOR_NMAX(launch_r16, p.N, w, p, st, ev0, ev1)
     }
     if (w.layout == LAYOUT_R16K) {

@@ -39,8 +39,8 @@ constexpr int kQ4KChunkBytes = 9 * 1024;
 // spans every CU): rows padded to 16-row tiles; blocks taken in quads (block b = 4*qd + j)
 // and groups of 8 quads.  Per (tile16, group) a 9216-byte chunk of 8 quads, each 1152 bytes:
 // [64 lanes x 16 B nibbles] with lane = 16*j + r holding block 4*qd + j of row 16*tile + r,
-// then [64 lanes x 1 f16 scale] of the same blocks.  One wave load covers 4 blocks x 16 rows
-// and its scales are one contiguous 128-byte line.
+// then the 64 f16 scales of the same blocks in [r / 4][j][r % 4] order.  One wave load covers
+// 4 blocks x 16 rows and its scales are one contiguous 128-byte line.
 constexpr int kTileRowsR16 = 16;
 constexpr int kQ40R16QuadBytes = 1024 + 128;  // 1152; 8 per chunk = kQ40ChunkBytes
 enum Layout : int { LAYOUT_R64 = 0, LAYOUT_R16 = 1, LAYOUT_R16K = 2 };  // R16K: Q4_K on 16-row tiles
@@ -108,6 +108,7 @@ struct GemmParams {
     // EPI_HEAD
     float* part_val = nullptr;  // [N][ntiles]
     int32_t* part_idx = nullptr;
+    int kernel = NC_GEMM_KERNEL_AUTO;  // dot-product path for 16-row tiles (nc_ctx_set_gemm_kernel)
 };
 
 // ev0/ev1: optional events stamped at the kernel's own start and end (timing).
@@ -180,6 +181,7 @@ struct nc_ctx {
     size_t tp_cap = 0;
     // device address of the static scratch array on this context's device (never freed)
     int32_t* static_scratch = nullptr;
+    int gemm_kernel = NC_GEMM_KERNEL_AUTO;  // dot-product path of the quantized matmuls
 };
 
 struct nc_qmat {

@@ -44,6 +44,7 @@ extern "C" int nc_matmul_quantized_batch_noalloc(nc_ctx* ctx, const nc_qmat* w, 
     int rc = launch_block_sums(x_i8, batch_size, (int)cols, ctx->static_scratch, st);
     if (rc) return rc;
     GemmParams p;
+    p.kernel = ctx->gemm_kernel;
     p.x = x_i8;
     p.xs = x_scales;
     p.xs8 = ctx->static_scratch;

@@ -155,7 +155,9 @@ void repack_q4_0_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t
                 const int64_t qd = b / 4, j = b % 4, lane = 16 * j + rr;
                 uint8_t* quad = dst + (t * groups + qd / 8) * kQ40ChunkBytes + (qd % 8) * kQ40R16QuadBytes;
                 std::memcpy(quad + lane * 16, blk + 2, 16);
-                std::memcpy(quad + 1024 + lane * 2, blk, 2);
+                // scales in [row / 4][block j][row % 4] order: each 4-row group's 16 scales are
+                // 32 contiguous bytes (the MFMA kernel's lane group reads them in two 16-byte loads)
+                std::memcpy(quad + 1024 + 2 * (16 * (rr / 4) + 4 * j + (rr % 4)), blk, 2);
             }
         }
     });
@@ -596,6 +598,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         if ((rc = launch_rmsnorm_q8(s->hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
             return rc;
         GemmParams p;
+        p.kernel = s->ctx->gemm_kernel;
         p.x = s->xq;
         p.xs = s->xs;
         p.xs8 = s->xs8;
@@ -631,6 +634,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         a.scale = 1.0f / std::sqrt((float)hd);  // inference.rs:3927
         if ((rc = launch_attention(a, st))) return rc;
         GemmParams po;
+        po.kernel = s->ctx->gemm_kernel;
         po.x = s->xq;
         po.xs = s->xs;
         po.xs8 = s->xs8;
@@ -642,6 +646,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         if ((rc = launch_rmsnorm_q8(s->hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
             return rc;
         GemmParams pg;
+        pg.kernel = s->ctx->gemm_kernel;
         pg.x = s->xq;
         pg.xs = s->xs;
         pg.xs8 = s->xs8;
@@ -656,6 +661,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         pg.xs8_out = s->xs8 + (size_t)s->max_batch * (s->maxw / 32);
         if ((rc = timed_gemm(s, L.gateup, pg))) return rc;
         GemmParams pd;
+        pd.kernel = s->ctx->gemm_kernel;
         pd.x = pg.xq_out;
         pd.xs = pg.xs_out;
         pd.xs8 = pg.xs8_out;
@@ -670,6 +676,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
     // compute_logits_from_hidden (inference.rs:4783-4832) for every row + argmax
     if ((rc = launch_rmsnorm_q8(s->hidden, m->out_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st))) return rc;
     GemmParams ph;
+    ph.kernel = s->ctx->gemm_kernel;
     ph.x = s->xq;
     ph.xs = s->xs;
     ph.xs8 = s->xs8;
@@ -824,6 +831,13 @@ void nc_ctx_free(nc_ctx* c) {
     delete c;
 }
 
+int nc_ctx_set_gemm_kernel(nc_ctx* c, int kernel) {
+    if (!c || kernel < NC_GEMM_KERNEL_AUTO || kernel > NC_GEMM_KERNEL_MFMA)
+        return fail(NC_EINVAL, "nc_ctx_set_gemm_kernel: unknown kernel");
+    c->gemm_kernel = kernel;
+    return NC_OK;
+}
+
 int nc_ctx_synchronize(nc_ctx* c) {
     if (!c) return fail(NC_EINVAL, "ctx is null");
     NC_HIP(hipSetDevice(c->device));
@@ -876,6 +890,7 @@ int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8,
     if (rc) return rc;
     if ((rc = launch_block_sums(x_i8, batch_size, (int)cols, ctx->xsum, st))) return rc;
     GemmParams p;
+    p.kernel = ctx->gemm_kernel;
     p.x = x_i8;
     p.xs = x_scales;
     p.xs8 = ctx->xsum;
@@ -900,6 +915,7 @@ int nc_bench_matmul(nc_ctx* ctx, const nc_qmat* const* w, int32_t ncopies, const
     int rc = ensure_xsum(ctx, (size_t)batch_size * (cols / 32));
     if (rc || (rc = launch_block_sums(x_i8, batch_size, (int)cols, ctx->xsum, st))) return rc;
     GemmParams p;
+    p.kernel = ctx->gemm_kernel;
     p.x = x_i8;
     p.xs = x_scales;
     p.xs8 = ctx->xsum;

@@ -174,3 +174,19 @@ def test_quantize_q8_0_matches_oracle(ctx):
         rq, rs = O.quantize_q8_0(x[n])
         assert np.array_equal(q[n], rq)
         assert np.array_equal(s[n].view(np.uint32), rs.view(np.uint32))
+
+
+@pytest.mark.parametrize("N", [1, 3, 5, 8, 9, 12, 16])
+@pytest.mark.parametrize("shape", [(100, 416), (6144, 4096), (4096, 14336)], ids=["partial", "qkv", "down"])
+def test_q4_0_mfma_path_bit_exact(shape, N):
+    """The int8 MFMA dot path (nc_ctx_set_gemm_kernel(MFMA), the counterpart of the reference's
+    Q8DotKernelSelector) gives the same bits as the oracle: partial tile and partial quad,
+    K-split tiles, every MFMA token column count."""
+    import nanocamelid_amd as nc
+    mctx = nc.Context(0)
+    mctx.set_gemm_kernel(nc._ffi.NC_GEMM_KERNEL_MFMA)
+    M, K = shape
+    w = random_q4_0(M, K, seed=3 * M + N)
+    _, xq, xs = q8_activations(N, K, seed=5 * N + K)
+    out, _ = _run_gemm(mctx, nc.NC_TYPE_Q4_0, w, M, K, xq, xs)
+    assert np.array_equal(out.view(np.uint32), O.matmul_q4_0(xq, xs, w, N, M, K, nthreads=16).view(np.uint32))

@@ -79,6 +79,27 @@ def test_verify_every_width(ctx):
         pos += n
 
 
+def test_verify_every_width_mfma_path(ctx):
+    """The int8 MFMA dot path through every epilogue of a model pass (fused q,k,v with RoPE into
+    the KV cache, residual, the four-tile SwiGLU + Q8_0, the head): logits bit-identical to the
+    oracle's at every verify width."""
+    import nanocamelid_amd as nc
+    mctx = nc.Context(0)
+    mctx.set_gemm_kernel(nc._ffi.NC_GEMM_KERNEL_MFMA)
+    _, gm, om = _models(mctx, TINY, seed=33)
+    gs = nc.Session(gm, 256, 16)
+    os_ = O.Session(om, 256, 16)
+    pos = 0
+    for n in (1, 4, 5, 8, 9, 13, 16):
+        batch = nc.uniform_prompt(200 + n, n, 1000)
+        _, _, _, preds = gs.verify_greedy(batch, pos)
+        opreds, _, ologits = os_.verify_greedy(batch, pos, want_logits=True)
+        for i in range(n):
+            assert _same(gs.logits(i), ologits[i]), (n, i)
+        assert np.array_equal(preds, opreds), n
+        pos += n
+
+
 def test_hidden_and_forward_pass_match(ctx):
     import nanocamelid_amd as nc
     _, gm, om = _models(ctx, TINY, seed=4)
