@@ -376,7 +376,7 @@ __device__ __forceinline__ void softmax_row(const float* srow, int L, float (&pr
 
 // The weighted V sum of unit (n, h) over positions 0..L-1 (probabilities in LDS) and the
 // Q8_0 quantisation of its output block; threads past the head dim return at once.
-template <int HD>
+template <int HD, bool PIPE>
 __device__ __forceinline__ void weighted_v_q8(const AttnParams& a, int n, int h, int kvh, int L, const float* probs) {
     const int t = threadIdx.x;
     if (t >= HD) return;
@@ -390,6 +390,8 @@ __device__ __forceinline__ void weighted_v_q8(const AttnParams& a, int n, int h,
     // HBM (a decode step streams the weights between two reads of a layer's cache), where
     // three batches in flight (D = 4) run the chain at ~17 cycles per position against ~25
     // for one; with the rows hot in L2 the two are equal.
+    // PIPE selects a software-pipelined loop (below) for launches where several chains share
+    // a SIMD; with one chain per SIMD the plain loop is as fast or faster.
     constexpr int HDv = HD;
     typedef float f4v __attribute__((ext_vector_type(4)));
     const char* vbase = (const char*)(a.vcache + (size_t)kvh * a.max_ctx * HD);
@@ -416,6 +418,7 @@ __device__ __forceinline__ void weighted_v_q8(const AttnParams& a, int n, int h,
             const float* pp_ = &probs[min((BT), nbt - 1) * B * 4];                                  \
             _Pragma("unroll") for (int j = 0; j < B; j++) pq[SLOT][j] = *(const f4v*)(pp_ + 4 * j); \
         }
+        if constexpr (!PIPE) {
 #pragma unroll
         for (int k = 0; k < D - 1; k++) NC_PV_LOAD(k, k)
         NC_PV_PROBS(0, 0)
@@ -437,6 +440,47 @@ __device__ __forceinline__ void weighted_v_q8(const AttnParams& a, int n, int h,
                     }
                 }
             }
+        }
+        } else {
+        // Software pipeline: while batch b's products are added (a dependent chain, one add per
+        // add latency), batch b+1's products are formed in the issue slots between the adds.
+        // Each inline-asm group alternates "acc += prod" with "prod' = p * v" of the next batch,
+        // the same IEEE operations in the same order as the sequential loop.
+        f4v pr[B];  // products of the batch being added
+#pragma unroll
+        for (int k = 0; k < D - 1; k++) NC_PV_LOAD(k, k)
+        NC_PV_PROBS(0, 0)
+        NC_PV_PROBS(1, 1)
+#pragma unroll
+        for (int j = 0; j < B; j++) pr[j] = pq[0][j] * ring[0][j];
+        for (int b0 = 0; b0 < nbt; b0 += D) {
+#pragma unroll
+            for (int k = 0; k < D; k++) {
+                const int b = b0 + k;
+                NC_PV_LOAD(b + D - 1, (k + D - 1) % D)
+                if (b < nbt) {
+#pragma unroll
+                    for (int j = 0; j < B; j++) {
+                        const f4v p4 = pq[(k + 1) & 1][j];
+                        const f4v v = ring[(k + 1) % D][j];
+                        float c0 = pr[j].x, c1 = pr[j].y, c2 = pr[j].z, c3 = pr[j].w;
+                        asm volatile(
+                            "v_add_f32 %0, %0, %1\n\t"
+                            "v_mul_f32 %1, %5, %9\n\t"
+                            "v_add_f32 %0, %0, %2\n\t"
+                            "v_mul_f32 %2, %6, %10\n\t"
+                            "v_add_f32 %0, %0, %3\n\t"
+                            "v_mul_f32 %3, %7, %11\n\t"
+                            "v_add_f32 %0, %0, %4\n\t"
+                            "v_mul_f32 %4, %8, %12"
+                            : "+v"(acc), "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3)
+                            : "v"(p4.x), "v"(p4.y), "v"(p4.z), "v"(p4.w), "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+                        pr[j] = f4v{c0, c1, c2, c3};
+                    }
+                }
+                NC_PV_PROBS(b + 2, k & 1)
+            }
+        }
         }
 #undef NC_PV_PROBS
 #undef NC_PV_LOAD
@@ -469,7 +513,7 @@ __device__ __forceinline__ void weighted_v_q8(const AttnParams& a, int n, int h,
                    a.xs8 + (size_t)n * (aw / 32) + col / 32);
 }
 
-template <int E, int T, int HD>
+template <int E, int T, int HD, bool PIPE>
 __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
     __shared__ ChainScratch<T> sc;
     __shared__ __align__(16) float probs[T * E];
@@ -488,7 +532,7 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
 #pragma unroll
     for (int j = 0; j < E; j++) probs[t * E + j] = pr[j];
     __syncthreads();
-    weighted_v_q8<HD>(a, n, h, kvh, L, probs);  // no barriers below
+    weighted_v_q8<HD, PIPE>(a, n, h, kvh, L, probs);  // no barriers below
 }
 
 // Attention of one (row n, head h) unit in one kernel, for rows of at most T*E <= 1536
@@ -566,7 +610,7 @@ __global__ __launch_bounds__(T) void attn_fused_kernel(AttnParams a) {
 #pragma unroll
     for (int j = 0; j < E; j++) probs[t * E + j] = pr[j];
     __syncthreads();
-    weighted_v_q8<HD>(a, n, h, kvh, L, probs);  // no barriers below
+    weighted_v_q8<HD, false>(a, n, h, kvh, L, probs);  // no barriers below
 }
 
 int launch_attention(const AttnParams& a, hipStream_t st) {
@@ -624,22 +668,37 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
 #undef NC_SCORES_HD
 #undef NC_SCORES
     NC_HIP(hipGetLastError());
-#define NC_PV(E, T)                                                                              \
-    if (a.hd == 128) hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 128>), grid, dim3(T), 0, st, a); \
-    else hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 64>), grid, dim3(T), 0, st, a);
-    // 512 threads: two waves per SIMD through the max, exp and sum phases (a wave issues one
-    // VALU instruction per 8 cycles at most); 2000 positions 27.2 -> 26.4 us, 8000 84.2 -> 78.4
-    // us for one row
-    if (len <= 2048) {
-        NC_PV(4, 512)
-    } else if (len <= 4096) {
-        NC_PV(8, 512)
-    } else if (len <= 8192) {
-        NC_PV(16, 512)
-    } else if (len <= 16384) {
-        NC_PV(32, 512)
+#define NC_PV(E, T, PIPE)                                                                              \
+    if (a.hd == 128) hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 128, PIPE>), grid, dim3(T), 0, st, a); \
+    else hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 64, PIPE>), grid, dim3(T), 0, st, a);
+    if (len > 16384) return fail(NC_ERANGE, "attention: context longer than 16384 positions");
+    if (a.N * a.H <= 256 || len > 8192) {
+        // at most one unit per CU: 512 threads, two waves per SIMD through the max, exp and sum
+        // phases (a wave issues one VALU instruction per 8 cycles at most; 2000 positions 27.2
+        // -> 26.4 us, 8000 84.2 -> 78.4 us for one row), and the plain weighted-V loop
+        if (len <= 2048) {
+            NC_PV(4, 512, false)
+        } else if (len <= 4096) {
+            NC_PV(8, 512, false)
+        } else if (len <= 8192) {
+            NC_PV(16, 512, false)
+        } else {
+            NC_PV(32, 512, false)
+        }
     } else {
-        return fail(NC_ERANGE, "attention: context longer than 16384 positions");
+        // more units than CUs: 256 threads, so that three units fit on a CU at once (168 VGPRs
+        // allow three waves per SIMD; at 512 threads only one unit fits and 576 units ran in
+        // three rounds), and the software-pipelined weighted-V loop, which is faster when
+        // several chains share a SIMD.  70B shape, 9 rows x 64 heads at 8101 positions:
+        // softmax + weighted V 213 -> 126 us, 9 rows x 64 heads at 2001: 78 -> 51 us (both
+        // kernels)
+        if (len <= 2048) {
+            NC_PV(8, 256, true)
+        } else if (len <= 4096) {
+            NC_PV(16, 256, true)
+        } else {
+            NC_PV(32, 256, true)
+        }
     }
 #undef NC_PV
     NC_HIP(hipGetLastError());

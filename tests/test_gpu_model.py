@@ -300,6 +300,32 @@ def test_long_context_logits(ctx, hd, checks):
         pos = c
 
 
+def test_long_context_many_units(ctx):
+    """Long rows with more (row, head) units than CUs (9 rows x 32 heads = 288) take the
+    256-thread softmax tiers and the software-pipelined weighted-V loop: 9-row verify logits
+    bit-exact vs the oracle past 1536 and past 2048 positions (the 8192-position tier is
+    checked against single-row passes in the 70B-shape configuration test)."""
+    import nanocamelid_amd as nc
+    spec = dict(layers=1, embedding_length=32 * 64, head_count=32, head_count_kv=8, feed_forward_length=512,
+                vocab_size=1000, context_length=2048 + 128, tied=1, norm_mode=1)
+    _, gm, om = _models(ctx, spec, seed=288)
+    prompt = nc.uniform_prompt(288, 2100, 1000)
+    gs, os_ = nc.Session(gm, 2160, 16), O.Session(om, 2160, 16)
+    pos = 0
+    for c in (1600, 2100):
+        print(f"many units: prefill to {c}, verify 9 rows", flush=True)
+        gs.prefill_pass_batch(prompt[pos:c], pos)
+        for i in range(pos, c, 16):
+            os_.prefill_pass_batch(prompt[i:min(i + 16, c)], i)
+        batch = nc.uniform_prompt(c, 9, 1000)
+        _, _, _, preds = gs.verify_greedy(batch, c)
+        opreds, _, ologits = os_.verify_greedy(batch, c, want_logits=True)
+        assert np.array_equal(preds, opreds)
+        for i in range(9):
+            assert _same(gs.logits(i), ologits[i]), (c, i)
+        pos = c
+
+
 @pytest.mark.slow
 def test_config0_plumbing_run(ctx):
     """Config 0: Llama-3.2-1B shape, tied Q4_0 head, 32-token seeded prompt, greedy, k=4,
