@@ -141,6 +141,22 @@ struct AttnParams {
     float scale = 0.f;
 };
 int launch_attention(const AttnParams& a, hipStream_t stream);
+
+// ---------------------------------------------------------------- prompt (prefill) path
+// Q4_0 batch matmul for any number of tokens on int8 MFMA: out[n * ld_out + row] (R16 and R64
+// layouts; no scratch, no -8 * block sums needed).
+int launch_gemm_prompt(const QMatDev& w, const int8_t* x, const float* xs, float* out, int ld_out, int N,
+                       hipStream_t stream);
+// The verify GEMMs' epilogues as separate kernels over a prompt matmul's f32 output y.
+int launch_prompt_qkv_rope(const float* y, int N, int start, int aw, int kw, int hd, int rope_half,
+                           const float* rope_tab, float* q_out, float* kcache, float* vcache, int max_ctx,
+                           hipStream_t stream);
+int launch_prompt_residual(const float* y, float* hidden, int N, int d, hipStream_t stream);
+int launch_prompt_swiglu_q8(const float* y, int N, int F, int8_t* xq, float* xs, int32_t* xs8, hipStream_t stream);
+int launch_prompt_positions(int32_t* d, int start, int stride, int count, hipStream_t stream);
+constexpr int kPromptRows = 256;   // tokens per prompt pass
+constexpr int kPromptGroup = 64;   // rows per attention launch inside a prompt pass (score buffer rows)
+constexpr int kPromptMin = 32;     // shorter prompts run as verify-sized passes
 int launch_argmax_final(const float* part_val, const int32_t* part_idx, int N, int ntiles, uint32_t* preds,
                         hipStream_t stream);
 int launch_accept_greedy(const uint32_t* toks, const uint32_t* preds, int n, int32_t* d_pos, int32_t* result,

@@ -78,6 +78,17 @@ struct nc_session {
     size_t ev_used = 0;
     double gemm_ms = 0.0;
     int64_t gemm_launches = 0, gemm_bytes = 0, pending_bytes = 0;
+    // prompt passes of up to kPromptRows tokens (allocated by the first prompt that uses them)
+    bool prompt_ready = false;
+    float* p_hidden = nullptr;   // [R][d]
+    int8_t* p_xq = nullptr;      // [R][maxw]
+    float* p_xs = nullptr;       // [R][maxw/32]
+    int32_t* p_xs8 = nullptr;    // [R][maxw/32]
+    float* p_y = nullptr;        // [R][max(q|k|v rows, 2F, d)] matmul outputs
+    float* p_q = nullptr;        // [R][aw]
+    float* p_scores = nullptr;   // [kPromptGroup][H][ctx_stride]
+    uint32_t* p_toks = nullptr;  // [max_ctx] the prompt's ids
+    int32_t* p_pos = nullptr;    // [R / kPromptGroup] start positions of the attention row groups
     std::vector<void*> allocs;
 };
 
@@ -716,8 +727,98 @@ static int fetch_preds(nc_session* s, int n, uint32_t* out) {
     return NC_OK;
 }
 
+// ---------------------------------------------------------------- prompt passes
+// Prompt passes run every matrix of the layer through the MFMA prompt matmul, so they need
+// Q4_0 matrices throughout (R16 or R64 tiles).
+static bool prompt_path_ok(const nc_model* m) {
+    for (const LayerDev& L : m->layers)
+        for (const QMatDev* q : {&L.qkv, &L.wo, &L.gateup, &L.down})
+            if (q->type != NC_TYPE_Q4_0 || (q->layout != LAYOUT_R16 && q->layout != LAYOUT_R64)) return false;
+    return true;
+}
+
+static int ensure_prompt_bufs(nc_session* s) {
+    if (s->prompt_ready) return NC_OK;
+    const nc_model_config& c = s->m->cfg;
+    const size_t R = kPromptRows;
+    const size_t yw = std::max({c.attention_output_width + 2 * c.kv_width, 2 * c.feed_forward_length,
+                                c.embedding_length});
+    int rc;
+    if ((rc = dev_alloc(s->allocs, &s->p_hidden, R * c.embedding_length)) ||
+        (rc = dev_alloc(s->allocs, &s->p_xq, R * s->maxw)) || (rc = dev_alloc(s->allocs, &s->p_xs, R * (s->maxw / 32))) ||
+        (rc = dev_alloc(s->allocs, &s->p_xs8, R * (s->maxw / 32))) || (rc = dev_alloc(s->allocs, &s->p_y, R * yw)) ||
+        (rc = dev_alloc(s->allocs, &s->p_q, R * c.attention_output_width)) ||
+        (rc = dev_alloc(s->allocs, &s->p_scores, (size_t)kPromptGroup * c.head_count * s->ctx_stride)) ||
+        (rc = dev_alloc(s->allocs, &s->p_toks, (size_t)s->max_ctx)) ||
+        (rc = dev_alloc(s->allocs, &s->p_pos, R / kPromptGroup)))
+        return rc;
+    s->prompt_ready = true;
+    return NC_OK;
+}
+
+// One prompt pass over n <= kPromptRows ids p_toks[off..off+n) at positions start..: the
+// layers of run_pass (run_layer_range_batch, inference.rs:3747-4111) with the MFMA prompt
+// matmul and the epilogues as separate kernels; no head (prefill_pass_batch discards the
+// prompt's logits).  Attention runs in row groups of kPromptGroup (the score rows).
+static int run_prompt_pass(nc_session* s, int off, int n, int64_t start) {
+    nc_model* m = s->m;
+    const nc_model_config& c = m->cfg;
+    const int d = (int)c.embedding_length, aw = (int)c.attention_output_width, kw = (int)c.kv_width;
+    const int F = (int)c.feed_forward_length, hd = (int)c.head_dim, Hkv = (int)c.head_count_kv;
+    hipStream_t st = s->stream;
+    const int ngroups = (n + kPromptGroup - 1) / kPromptGroup;
+    int rc;
+    if ((rc = launch_embed(m->tok_emb, s->p_toks + off, n, d, s->p_hidden, st)) ||
+        (rc = launch_prompt_positions(s->p_pos, (int)start, kPromptGroup, ngroups, st)))
+        return rc;
+    const size_t layer_kv = (size_t)Hkv * s->ctx_stride * hd;
+    for (int64_t li = 0; li < c.block_count; li++) {
+        const LayerDev& L = m->layers[li];
+        float* kc = s->kcache + li * layer_kv;
+        float* vc = s->vcache + li * layer_kv;
+        if ((rc = launch_rmsnorm_q8(s->p_hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->p_xq, s->p_xs, s->p_xs8, st)) ||
+            (rc = launch_gemm_prompt(L.qkv, s->p_xq, s->p_xs, s->p_y, aw + 2 * kw, n, st)) ||
+            (rc = launch_prompt_qkv_rope(s->p_y, n, (int)start, aw, kw, hd, (int)c.rope_dimension_count / 2,
+                                         s->rope_tab, s->p_q, kc, vc, (int)s->ctx_stride, st)))
+            return rc;
+        for (int gi = 0; gi < ngroups; gi++) {
+            const int g0 = gi * kPromptGroup, ng = std::min(kPromptGroup, n - g0);
+            AttnParams a;
+            a.q = s->p_q + (size_t)g0 * aw;
+            a.kcache = kc;
+            a.vcache = vc;
+            a.scores = s->p_scores;
+            a.xq = s->p_xq + (size_t)g0 * aw;
+            a.xs = s->p_xs + (size_t)g0 * (aw / 32);
+            a.xs8 = s->p_xs8 + (size_t)g0 * (aw / 32);
+            a.d_pos = s->p_pos + gi;
+            a.N = ng;
+            a.H = (int)c.head_count;
+            a.Hkv = Hkv;
+            a.hd = hd;
+            a.max_ctx = (int)s->ctx_stride;
+            a.max_pos = (int)(start + g0 + ng - 1);
+            a.scale = 1.0f / std::sqrt((float)hd);  // inference.rs:3927
+            if ((rc = launch_attention(a, st))) return rc;
+        }
+        if ((rc = launch_gemm_prompt(L.wo, s->p_xq, s->p_xs, s->p_y, d, n, st)) ||
+            (rc = launch_prompt_residual(s->p_y, s->p_hidden, n, d, st)) ||
+            (rc = launch_rmsnorm_q8(s->p_hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->p_xq, s->p_xs, s->p_xs8, st)) ||
+            (rc = launch_gemm_prompt(L.gateup, s->p_xq, s->p_xs, s->p_y, 2 * F, n, st)) ||
+            // the gate/up matmul has read every activation before the SwiGLU kernel overwrites them
+            (rc = launch_prompt_swiglu_q8(s->p_y, n, F, s->p_xq, s->p_xs, s->p_xs8, st)) ||
+            (rc = launch_gemm_prompt(L.down, s->p_xq, s->p_xs, s->p_y, d, n, st)) ||
+            (rc = launch_prompt_residual(s->p_y, s->p_hidden, n, d, st)))
+            return rc;
+    }
+    s->last_n = 0;
+    return NC_OK;
+}
+
 // prefill_tokens (main.rs:9415-9485): chunks of max_batch rows.  Returns the last row's
-// greedy prediction in *last_pred.
+// greedy prediction in *last_pred.  Q4_0 models run all but the last max_batch tokens (all of
+// them when no logits are wanted) as prompt passes of up to kPromptRows tokens; every token's
+// arithmetic is the same in any chunking, so the KV cache and logits are the same bits.
 static int prefill_chunks(nc_session* s, const uint32_t* toks, int n, int64_t start_pos, uint32_t* last_pred,
                           bool last_logits = false) {
     // per-kernel timing covers decode and verify passes only, never the prompt
@@ -733,7 +834,20 @@ static int prefill_chunks(nc_session* s, const uint32_t* toks, int n, int64_t st
             return fail(NC_ERANGE, "prompt token id " + std::to_string(toks[i]) + " >= vocab_size");
     if (start_pos < 0 || start_pos + n > s->max_ctx) return fail(NC_ERANGE, "prompt exceeds the session context");
     const bool head = last_pred || last_logits;
-    for (int i = 0; i < n; i += s->max_batch) {
+    int i = 0;
+    const int tail = head ? std::min(n, s->max_batch) : 0;  // rows whose pass computes the head
+    if (n - tail >= kPromptMin && prompt_path_ok(s->m)) {
+        if ((rc = ensure_prompt_bufs(s))) return rc;
+        // synchronous: an earlier prompt pass on the session stream may still read p_toks
+        NC_HIP(hipStreamSynchronize(s->stream));
+        NC_HIP(hipMemcpy(s->p_toks, toks, (size_t)(n - tail) * sizeof(uint32_t), hipMemcpyHostToDevice));
+        for (; i < n - tail; i += kPromptRows) {
+            const int len = std::min(kPromptRows, n - tail - i);
+            if ((rc = run_prompt_pass(s, i, len, start_pos + i))) return rc;
+        }
+        i = n - tail;  // the verify-sized passes take the rest
+    }
+    for (; i < n; i += s->max_batch) {
         const int len = std::min(s->max_batch, n - i);
         if ((rc = upload_toks(s, toks + i, len))) return rc;
         if ((rc = run_pass(s, len, start_pos + i, head && i + len == n))) return rc;
@@ -883,37 +997,49 @@ int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8,
                               int batch_size, int64_t rows, int64_t cols, void* stream) {
     if (!ctx || !w || !x_i8 || !x_scales || !out) return fail(NC_EINVAL, "nc_matmul_quantized_batch: null argument");
     if (rows != w->m.rows || cols != w->m.cols) return fail(NC_EINVAL, "nc_matmul_quantized_batch: shape mismatch");
-    if (batch_size < 1 || batch_size > 16) return fail(NC_EINVAL, "nc_matmul_quantized_batch: batch must be 1..16");
+    if (batch_size < 1) return fail(NC_EINVAL, "nc_matmul_quantized_batch: batch must be >= 1");
     NC_HIP(hipSetDevice(ctx->device));
     hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
-    int rc = ensure_xsum(ctx, (size_t)batch_size * (cols / 32));
-    if (rc) return rc;
-    if ((rc = launch_block_sums(x_i8, batch_size, (int)cols, ctx->xsum, st))) return rc;
-    GemmParams p;
-    p.kernel = ctx->gemm_kernel;
-    p.x = x_i8;
-    p.xs = x_scales;
-    p.xs8 = ctx->xsum;
-    p.N = batch_size;
-    p.epi = EPI_STORE;
-    p.out = out;
-    p.ld_out = (int)rows;
-    return launch_gemm(w->m, p, st);
+    // more than 16 tokens: the MFMA prompt matmul (Q4_0), or 16-token slices (Q4_K)
+    if (batch_size > 16 && w->m.type == NC_TYPE_Q4_0)
+        return launch_gemm_prompt(w->m, x_i8, x_scales, out, (int)rows, batch_size, st);
+    for (int i = 0; i < batch_size; i += 16) {
+        const int nb = std::min(16, batch_size - i);
+        int rc = ensure_xsum(ctx, (size_t)nb * (cols / 32));
+        if (rc) return rc;
+        if ((rc = launch_block_sums(x_i8 + (size_t)i * cols, nb, (int)cols, ctx->xsum, st))) return rc;
+        GemmParams p;
+        p.kernel = ctx->gemm_kernel;
+        p.x = x_i8 + (size_t)i * cols;
+        p.xs = x_scales + (size_t)i * (cols / 32);
+        p.xs8 = ctx->xsum;
+        p.N = nb;
+        p.epi = EPI_STORE;
+        p.out = out + (size_t)i * rows;
+        p.ld_out = (int)rows;
+        if ((rc = launch_gemm(w->m, p, st))) return rc;
+    }
+    return NC_OK;
 }
 
 int nc_bench_matmul(nc_ctx* ctx, const nc_qmat* const* w, int32_t ncopies, const int8_t* x_i8, const float* x_scales,
                     float* out, int32_t batch_size, int32_t iters, float* us_out) {
     if (!ctx || !w || ncopies < 1 || !x_i8 || !x_scales || !out || !us_out || iters < 1)
         return fail(NC_EINVAL, "nc_bench_matmul: bad arguments");
-    if (batch_size < 1 || batch_size > 16) return fail(NC_EINVAL, "nc_bench_matmul: batch must be 1..16");
+    if (batch_size < 1) return fail(NC_EINVAL, "nc_bench_matmul: batch must be >= 1");
     for (int i = 0; i < ncopies; i++)
         if (!w[i] || w[i]->m.rows != w[0]->m.rows || w[i]->m.cols != w[0]->m.cols)
             return fail(NC_EINVAL, "nc_bench_matmul: weight copies differ in shape");
+    if (batch_size > 16 && w[0]->m.type != NC_TYPE_Q4_0)
+        return fail(NC_EINVAL, "nc_bench_matmul: more than 16 tokens only for Q4_0 matrices");
     NC_HIP(hipSetDevice(ctx->device));
     hipStream_t st = ctx->stream;
     const int64_t cols = w[0]->m.cols, rows = w[0]->m.rows;
-    int rc = ensure_xsum(ctx, (size_t)batch_size * (cols / 32));
-    if (rc || (rc = launch_block_sums(x_i8, batch_size, (int)cols, ctx->xsum, st))) return rc;
+    int rc = NC_OK;
+    if (batch_size <= 16) {
+        rc = ensure_xsum(ctx, (size_t)batch_size * (cols / 32));
+        if (rc || (rc = launch_block_sums(x_i8, batch_size, (int)cols, ctx->xsum, st))) return rc;
+    }
     GemmParams p;
     p.kernel = ctx->gemm_kernel;
     p.x = x_i8;
@@ -925,7 +1051,15 @@ int nc_bench_matmul(nc_ctx* ctx, const nc_qmat* const* w, int32_t ncopies, const
     p.ld_out = (int)rows;
     std::vector<hipEvent_t> ev(2 * (size_t)iters, nullptr);
     for (auto& e : ev) NC_HIP(hipEventCreate(&e));
-    for (int i = 0; i < iters && !rc; i++) rc = launch_gemm(w[i % ncopies]->m, p, st, ev[2 * i], ev[2 * i + 1]);
+    for (int i = 0; i < iters && !rc; i++) {
+        if (batch_size <= 16) {
+            rc = launch_gemm(w[i % ncopies]->m, p, st, ev[2 * i], ev[2 * i + 1]);
+        } else if (hipEventRecord(ev[2 * i], st) != hipSuccess ||
+                   (rc = launch_gemm_prompt(w[i % ncopies]->m, x_i8, x_scales, out, (int)rows, batch_size, st)) ||
+                   hipEventRecord(ev[2 * i + 1], st) != hipSuccess) {
+            if (!rc) rc = fail(NC_EHIP, "nc_bench_matmul: event record");
+        }
+    }
     if (!rc && hipStreamSynchronize(st) != hipSuccess) rc = fail(NC_EHIP, "nc_bench_matmul: stream failed");
     for (int i = 0; i < iters && !rc; i++) {
         float ms = 0.0f;

@@ -101,6 +101,39 @@ def test_q4_0_config1_shapes(ctx, shape):
             assert np.array_equal(dots, ref_dots)
 
 
+PROMPT_SHAPES = [(4096, 4096, (17, 64, 100, 256)), (1040, 96, (33, 300)), (32816, 64, (17, 129)),
+                 (14336, 4096, (48,)), (4096, 14336, (40,))]
+
+
+@pytest.mark.parametrize("M,K,Ns", PROMPT_SHAPES, ids=[f"{m}x{k}" for m, k, _ in PROMPT_SHAPES])
+def test_q4_0_prompt_matmul(ctx, M, K, Ns):
+    """More than 16 tokens take the MFMA prompt matmul (inference.rs:1385-1418 for any batch):
+    every output bit-identical to the oracle.  Covers 16-row tiles (R16) with 4096 and 3 blocks
+    per row (a partial quad) and rows not a multiple of 64, 64-row tiles (R64, >= 512 tiles) with
+    a partial last tile, token counts that leave partial 16- and 64-token tiles."""
+    import nanocamelid_amd as nc
+    w = random_q4_0(M, K, seed=M + 7 * K)
+    q = nc.QMat(ctx, nc.NC_TYPE_Q4_0, M, K, w)
+    for N in Ns:
+        x, xq, xs = q8_activations(N, K, seed=N * 17 + M)
+        xt, st = torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda()
+        out = nc.matmul_quantized_batch(ctx, q, xt, st).cpu().numpy()
+        ref = O.matmul_q4_0(xq, xs, w, N, M, K, nthreads=16)
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), N
+
+
+def test_q4_k_matmul_above_16_tokens(ctx):
+    """Q4_K matrices take 16-token slices of the verify kernel beyond 16 tokens."""
+    import nanocamelid_amd as nc
+    M, K, N = 512, 1024, 37
+    w = random_q4_k(M, K, seed=5)
+    q = nc.QMat(ctx, nc.NC_TYPE_Q4_K, M, K, w)
+    x, xq, xs = q8_activations(N, K, seed=6)
+    out = nc.matmul_quantized_batch(ctx, q, torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda()).cpu().numpy()
+    ref = O.matmul_q4_k(xq, xs, w, N, M, K, nthreads=16)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
 def _dequant(w):
     M, nb, _ = w.shape
     sc = (w[:, :, 0].astype(np.uint16) | (w[:, :, 1].astype(np.uint16) << 8)).view(np.float16).astype(np.float32)

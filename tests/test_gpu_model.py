@@ -300,6 +300,30 @@ def test_long_context_logits(ctx, hd, checks):
         pos = c
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_prompt_passes_match_oracle(ctx, hd):
+    """Prompts of 32 or more tokens on Q4_0 models run as MFMA prompt passes of up to 256 tokens
+    (epilogues as separate kernels, attention in 64-row groups): a 300-token prompt without
+    logits (passes of 256 + 44) and 400 more with logits (passes of 256 + 128, then the last 16
+    rows as a verify-sized pass), then a 9-row verify: every logit bit-identical to the oracle's
+    after 16-token chunks, i.e. the same KV cache bits."""
+    import nanocamelid_amd as nc
+    spec = dict(TINY, head_count=512 // hd, head_count_kv=256 // hd, embedding_length=512, context_length=1024)
+    _, gm, om = _models(ctx, spec, seed=40 + hd)
+    prompt = nc.uniform_prompt(41, 700, 1000)
+    gs, os_ = nc.Session(gm, 1024, 16), O.Session(om, 1024, 16)
+    gs.prefill_pass_batch(prompt[:300], 0, want_logits=False)
+    gs.prefill_pass_batch(prompt[300:700], 300)
+    for i in range(0, 700, 16):
+        os_.prefill_pass_batch(prompt[i:min(i + 16, 700)], i)
+    batch = nc.uniform_prompt(700, 9, 1000)
+    _, _, _, preds = gs.verify_greedy(batch, 700)
+    opreds, _, ologits = os_.verify_greedy(batch, 700, want_logits=True)
+    assert np.array_equal(preds, opreds)
+    for i in range(9):
+        assert _same(gs.logits(i), ologits[i]), i
+
+
 def test_long_context_many_units(ctx):
     """Long rows with more (row, head) units than CUs (9 rows x 32 heads = 288) take the
     256-thread softmax tiers and the software-pipelined weighted-V loop: 9-row verify logits
