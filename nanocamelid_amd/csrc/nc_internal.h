@@ -145,8 +145,11 @@ int launch_attention(const AttnParams& a, hipStream_t stream);
 // ---------------------------------------------------------------- prompt (prefill) path
 // Q4_0 batch matmul for any number of tokens on int8 MFMA: out[n * ld_out + row] (R16 and R64
 // layouts; no scratch, no -8 * block sums needed).
+// xm/xsm (optional): the activations repacked by launch_prompt_repack (xm: 16 * ceil(N/16) * K
+// bytes, xsm: 16 * ceil(N/16) * ceil(K/128) * 4 floats); coalesced operand loads.
 int launch_gemm_prompt(const QMatDev& w, const int8_t* x, const float* xs, float* out, int ld_out, int N,
-                       hipStream_t stream);
+                       hipStream_t stream, const void* xm = nullptr, const float* xsm = nullptr);
+int launch_prompt_repack(const int8_t* x, const float* xs, int N, int K, void* xm, float* xsm, hipStream_t stream);
 // The verify GEMMs' epilogues as separate kernels over a prompt matmul's f32 output y.
 int launch_prompt_qkv_rope(const float* y, int N, int start, int aw, int kw, int hd, int rope_half,
                            const float* rope_tab, float* q_out, float* kcache, float* vcache, int max_ctx,

@@ -33,12 +33,18 @@ struct PromptGemm {
     int M = 0, nb = 0, N = 0, ld_out = 0;
     const int8_t* x = nullptr;  // [N][32 * nb]
     const float* xs = nullptr;  // [N][nb]
+    // the same activations repacked in MFMA operand order (prompt_repack_kernel), or null:
+    // xm [N/16][nb][lane (g, c)] 8 bytes, xsm [N/16][nb/4][c] the 4 scales of a quad
+    const uint2* xm = nullptr;
+    const float4* xsm = nullptr;
     float* out = nullptr;       // out[n * ld_out + row]
 };
 
-template <int LAYOUT>
+template <int LAYOUT, int D, bool XM>
 __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    // wave index through readfirstlane: the tile bases below are then scalar (buffer-load
+    // soffsets) instead of per-lane values that the compiler would loop over
+    const int lane = threadIdx.x & 63, wv = wave_id_uniform();
     const int g = lane >> 4, r = lane & 15;  // A/B lane (g, r); D lane (g, c = r)
     const int row0 = blockIdx.x * 64 + (wv & 1) * 32;
     const int tok0 = blockIdx.y * 64 + (wv >> 1) * 32;
@@ -50,8 +56,14 @@ __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
 #pragma unroll
     for (int k = 0; k < 2; k++) tk[k] = min(tok0 + 16 * k + r, p.N - 1);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc((void*)p.w, 0, (int)p.w_bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, 0, p.N * K, 0x00020000);
-    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs, 0, p.N * p.nb * 4, 0x00020000);
+    const int n16 = (p.N + 15) / 16;  // 16-token tiles of the repacked activations
+    const __amdgpu_buffer_rsrc_t xres = XM ? __builtin_amdgcn_make_buffer_rsrc((void*)p.xm, 0, n16 * K * 16, 0x00020000)
+                                           : __builtin_amdgcn_make_buffer_rsrc((void*)p.x, 0, p.N * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sres = XM ? __builtin_amdgcn_make_buffer_rsrc((void*)p.xsm, 0, n16 * nq * 256, 0x00020000)
+                                           : __builtin_amdgcn_make_buffer_rsrc((void*)p.xs, 0, p.N * p.nb * 4, 0x00020000);
+    int tt[2];  // 16-token tiles (repacked layout), clamped into the buffer
+#pragma unroll
+    for (int k = 0; k < 2; k++) tt[k] = min(tok0 / 16 + k, n16 - 1);
     // per-lane parts of the addresses
     int nvo[2], svo[2];
 #pragma unroll
@@ -73,7 +85,6 @@ __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
         else
             return ((rt[i] >> 2) * p.groups + (qd >> 1)) * kQ40ChunkBytes;
     };
-    constexpr int D = 2;  // quads in flight
     uint32_t nib[D][2][4], sw[D][2][8], xa[D][2][4], xb[D][2][4];
     float4 xsv[D][2];
 #define NC_PQ_LOAD(QD, SLOT)                                                                                    \
@@ -92,11 +103,22 @@ __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
             sw[SLOT][i][4] = s1_.x; sw[SLOT][i][5] = s1_.y; sw[SLOT][i][6] = s1_.z; sw[SLOT][i][7] = s1_.w;     \
         }                                                                                                       \
         _Pragma("unroll") for (int k = 0; k < 2; k++) {                                                         \
-            _Pragma("unroll") for (int j = 0; j < 4; j++) {                                                     \
-                xa[SLOT][k][j] = __builtin_amdgcn_raw_buffer_load_b32(xres, xvo[k], 128 * qd_ + 32 * j, 0);     \
-                xb[SLOT][k][j] = __builtin_amdgcn_raw_buffer_load_b32(xres, xvo[k] + 16, 128 * qd_ + 32 * j, 0); \
+            if constexpr (XM) {                                                                                 \
+                _Pragma("unroll") for (int j = 0; j < 4; j++) {                                                 \
+                    const uint2 v_ = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(            \
+                        xres, lane * 8, (tt[k] * p.nb + 4 * qd_ + j) * 512, 0));                                \
+                    xa[SLOT][k][j] = v_.x;                                                                      \
+                    xb[SLOT][k][j] = v_.y;                                                                      \
+                }                                                                                               \
+                xsv[SLOT][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(               \
+                    sres, r * 16, (tt[k] * nq + qd_) * 256, 0));                                                \
+            } else {                                                                                            \
+                _Pragma("unroll") for (int j = 0; j < 4; j++) {                                                 \
+                    xa[SLOT][k][j] = __builtin_amdgcn_raw_buffer_load_b32(xres, xvo[k], 128 * qd_ + 32 * j, 0); \
+                    xb[SLOT][k][j] = __builtin_amdgcn_raw_buffer_load_b32(xres, xvo[k] + 16, 128 * qd_ + 32 * j, 0); \
+                }                                                                                               \
+                xsv[SLOT][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(sres, mvo[k], 16 * qd_, 0)); \
             }                                                                                                   \
-            xsv[SLOT][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(sres, mvo[k], 16 * qd_, 0)); \
         }                                                                                                       \
     } while (0)
     float acc[2][2][4];
@@ -172,7 +194,7 @@ __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
 }
 
 int launch_gemm_prompt(const QMatDev& w, const int8_t* x, const float* xs, float* out, int ld_out, int N,
-                       hipStream_t st) {
+                       hipStream_t st, const void* xm, const float* xsm) {
     if (w.type != NC_TYPE_Q4_0 || (w.layout != LAYOUT_R16 && w.layout != LAYOUT_R64))
         return fail(NC_EINVAL, "prompt matmul: Q4_0 matrices only");
     if (N < 1 || (int64_t)N * w.cols >= (int64_t)1 << 31 || w.dev_bytes >= (int64_t)1 << 31)
@@ -188,10 +210,63 @@ int launch_gemm_prompt(const QMatDev& w, const int8_t* x, const float* xs, float
     p.ld_out = ld_out;
     p.x = x;
     p.xs = xs;
+    p.xm = (const uint2*)xm;
+    p.xsm = (const float4*)xsm;
     p.out = out;
     const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 63) / 64));
-    if (w.layout == LAYOUT_R16) hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R16>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R64>), grid, dim3(256), 0, st, p);
+    if (xm && xsm) {
+        if (w.layout == LAYOUT_R16) hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R16, 2, true>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R64, 2, true>), grid, dim3(256), 0, st, p);
+    } else {
+        if (w.layout == LAYOUT_R16) hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R16, 2, false>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R64, 2, false>), grid, dim3(256), 0, st, p);
+    }
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
+// Activations in MFMA operand order for the prompt matmul: xm unit (tile t, block b, lane
+// (g, c)) = token 16t + c's bytes 32b + 4g..+3 and 32b + 16 + 4g..+3 (zero past N), so a wave
+// reads a block's B operand as 512 contiguous bytes; xsm (t, quad q, c) = token 16t + c's scales
+// of blocks 4q..4q+3 (zero past the row).  Units of x first, then of the scales.
+__global__ void prompt_repack_kernel(const int8_t* x, const float* xs, int N, int nb, uint2* xm, float4* xsm) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int n16 = (N + 15) / 16, nq = (nb + 3) / 4, K = 32 * nb;
+    const int64_t nx = (int64_t)n16 * nb * 64;
+    if (id < nx) {
+        const int lane = (int)(id & 63), g = lane >> 4, c = lane & 15;
+        const int64_t tb = id >> 6;
+        const int b = (int)(tb % nb), n = (int)(tb / nb) * 16 + c;
+        uint2 v = make_uint2(0u, 0u);
+        if (n < N) {
+            const int8_t* row = x + (size_t)n * K + 32 * b + 4 * g;
+            v.x = *(const uint32_t*)row;
+            v.y = *(const uint32_t*)(row + 16);
+        }
+        xm[id] = v;
+        return;
+    }
+    const int64_t id2 = id - nx;
+    if (id2 >= (int64_t)n16 * nq * 16) return;
+    const int c = (int)(id2 & 15);
+    const int64_t tq = id2 >> 4;
+    const int q = (int)(tq % nq), n = (int)(tq / nq) * 16 + c;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (n < N) {
+        const float* sr = xs + (size_t)n * nb + 4 * q;
+        v.x = sr[0];
+        if (4 * q + 1 < nb) v.y = sr[1];
+        if (4 * q + 2 < nb) v.z = sr[2];
+        if (4 * q + 3 < nb) v.w = sr[3];
+    }
+    xsm[id2] = v;
+}
+
+int launch_prompt_repack(const int8_t* x, const float* xs, int N, int K, void* xm, float* xsm, hipStream_t st) {
+    const int nb = K / 32, n16 = (N + 15) / 16, nq = (nb + 3) / 4;
+    const int64_t total = (int64_t)n16 * nb * 64 + (int64_t)n16 * nq * 16;
+    hipLaunchKernelGGL(prompt_repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x, xs, N, nb,
+                       (uint2*)xm, (float4*)xsm);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }

@@ -89,6 +89,8 @@ struct nc_session {
     float* p_scores = nullptr;   // [kPromptGroup][H][ctx_stride]
     uint32_t* p_toks = nullptr;  // [max_ctx] the prompt's ids
     int32_t* p_pos = nullptr;    // [R / kPromptGroup] start positions of the attention row groups
+    int8_t* p_xm = nullptr;      // matmul activations repacked in MFMA operand order
+    float* p_xsm = nullptr;
     std::vector<void*> allocs;
 };
 
@@ -750,10 +752,17 @@ static int ensure_prompt_bufs(nc_session* s) {
         (rc = dev_alloc(s->allocs, &s->p_q, R * c.attention_output_width)) ||
         (rc = dev_alloc(s->allocs, &s->p_scores, (size_t)kPromptGroup * c.head_count * s->ctx_stride)) ||
         (rc = dev_alloc(s->allocs, &s->p_toks, (size_t)s->max_ctx)) ||
-        (rc = dev_alloc(s->allocs, &s->p_pos, R / kPromptGroup)))
+        (rc = dev_alloc(s->allocs, &s->p_pos, R / kPromptGroup)) || (rc = dev_alloc(s->allocs, &s->p_xm, R * s->maxw)) ||
+        (rc = dev_alloc(s->allocs, &s->p_xsm, R * ((s->maxw + 127) / 128) * 4)))
         return rc;
     s->prompt_ready = true;
     return NC_OK;
+}
+
+// Prompt matmul of the pass's activations (repacked first into MFMA operand order).
+static int prompt_gemm(nc_session* s, const QMatDev& w, const int8_t* xq, const float* xs, float* out, int n) {
+    int rc = launch_prompt_repack(xq, xs, n, (int)w.cols, s->p_xm, s->p_xsm, s->stream);
+    return rc ? rc : launch_gemm_prompt(w, xq, xs, out, (int)w.rows, n, s->stream, s->p_xm, s->p_xsm);
 }
 
 // One prompt pass over n <= kPromptRows ids p_toks[off..off+n) at positions start..: the
@@ -777,7 +786,7 @@ static int run_prompt_pass(nc_session* s, int off, int n, int64_t start) {
         float* kc = s->kcache + li * layer_kv;
         float* vc = s->vcache + li * layer_kv;
         if ((rc = launch_rmsnorm_q8(s->p_hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->p_xq, s->p_xs, s->p_xs8, st)) ||
-            (rc = launch_gemm_prompt(L.qkv, s->p_xq, s->p_xs, s->p_y, aw + 2 * kw, n, st)) ||
+            (rc = prompt_gemm(s, L.qkv, s->p_xq, s->p_xs, s->p_y, n)) ||
             (rc = launch_prompt_qkv_rope(s->p_y, n, (int)start, aw, kw, hd, (int)c.rope_dimension_count / 2,
                                          s->rope_tab, s->p_q, kc, vc, (int)s->ctx_stride, st)))
             return rc;
@@ -801,13 +810,13 @@ static int run_prompt_pass(nc_session* s, int off, int n, int64_t start) {
             a.scale = 1.0f / std::sqrt((float)hd);  // inference.rs:3927
             if ((rc = launch_attention(a, st))) return rc;
         }
-        if ((rc = launch_gemm_prompt(L.wo, s->p_xq, s->p_xs, s->p_y, d, n, st)) ||
+        if ((rc = prompt_gemm(s, L.wo, s->p_xq, s->p_xs, s->p_y, n)) ||
             (rc = launch_prompt_residual(s->p_y, s->p_hidden, n, d, st)) ||
             (rc = launch_rmsnorm_q8(s->p_hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->p_xq, s->p_xs, s->p_xs8, st)) ||
-            (rc = launch_gemm_prompt(L.gateup, s->p_xq, s->p_xs, s->p_y, 2 * F, n, st)) ||
+            (rc = prompt_gemm(s, L.gateup, s->p_xq, s->p_xs, s->p_y, n)) ||
             // the gate/up matmul has read every activation before the SwiGLU kernel overwrites them
             (rc = launch_prompt_swiglu_q8(s->p_y, n, F, s->p_xq, s->p_xs, s->p_xs8, st)) ||
-            (rc = launch_gemm_prompt(L.down, s->p_xq, s->p_xs, s->p_y, d, n, st)) ||
+            (rc = prompt_gemm(s, L.down, s->p_xq, s->p_xs, s->p_y, n)) ||
             (rc = launch_prompt_residual(s->p_y, s->p_hidden, n, d, st)))
             return rc;
     }
