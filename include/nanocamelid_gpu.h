@@ -37,6 +37,7 @@ extern "C" {
 #define NC_TYPE_F32 0
 #define NC_TYPE_Q4_0 2
 #define NC_TYPE_Q4_K 12
+#define NC_TYPE_Q6_K 14
 
 typedef struct nc_ctx nc_ctx;         /* device context: device id, default stream */
 typedef struct nc_qmat nc_qmat;       /* device-resident repacked quantized matrix */
@@ -75,7 +76,9 @@ int nc_ctx_set_gemm_kernel(nc_ctx* ctx, int kernel);
  * and repacks it into the device layout.  Replaces the load-time matrix
  * construction load_q4_0_matrix / decode_q4_k_blocks (src/model.rs:1369-1401,
  * src/model.rs:1270) that feeds QuantizedMatrix (src/model.rs:294-310).
- * type: NC_TYPE_Q4_0 or NC_TYPE_Q4_K.  cols % 32 == 0 (Q4_K: % 256). */
+ * type: NC_TYPE_Q4_0, NC_TYPE_Q4_K or NC_TYPE_Q6_K (the Q6_K output projection of llama.cpp
+ * files, matmul_q6_k_batch src/inference.rs:1882-2000; batches of 1..16 tokens).
+ * cols % 32 == 0 (Q4_K, Q6_K: % 256; Q6_K: cols <= 16384). */
 int nc_qmat_upload(nc_ctx* ctx, int type, int64_t rows, int64_t cols, const void* gguf_blocks_host,
                    nc_qmat** out);
 void nc_qmat_free(nc_qmat* w);
@@ -87,7 +90,9 @@ int64_t nc_qmat_device_bytes(const nc_qmat* w);
  * Replaces matmul_quantized_batch (src/inference.rs:1246-1303) and, for batch_size 1,
  * matmul_quantized (src/inference.rs:1201-1244).  All pointers are device pointers:
  * x_i8 [batch][cols] int8, x_scales [batch][cols/32] f32, out [batch][rows] f32
- * (token-major, as write_batch_out src/inference.rs:1333-1341).  batch_size 1..16.
+ * (token-major, as write_batch_out src/inference.rs:1333-1341).  batch_size >= 1, no upper
+ * limit (matmul_quantized_batch takes any batch): up to 16 tokens run on the verify kernels;
+ * more run on the int8 MFMA prompt matmul (Q4_0) or as 16-token slices (Q4_K).
  * stream: a hipStream_t or NULL for the context's default stream. */
 int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, const float* x_scales,
                               float* out, int batch_size, int64_t rows, int64_t cols, void* stream);
@@ -168,13 +173,34 @@ typedef struct nc_load_opts {
 
 /* Parses a GGUF file / in-memory image, builds LlamaModelConfig and uploads the
  * weights.  Replaces gguf::read_file (src/gguf.rs:454-551),
- * LlamaModelConfig::from_gguf (src/model.rs:48-186) and LlamaWeights::load
- * (src/model.rs:461-545), including the tied-head Q4_0 requantisation
- * (src/q8.rs:2442-2488).  opts may be NULL. */
+ * LlamaModelConfig::from_gguf (src/model.rs:48-186), validate_model_tensors
+ * (src/model.rs:851-1036) and LlamaWeights::load (src/model.rs:461-545), including the
+ * tied-head Q4_0 requantisation (src/q8.rs:2442-2488).  The file is memory-mapped, never
+ * copied whole into host memory.  Token embeddings and norms may be F32, F16, BF16, Q8_0,
+ * Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K or Q6_K (decoded as load_f32_or_f16,
+ * src/model.rs:1081-1229); the layer matrices and an untied head must be Q4_0 or Q4_K.
+ * Fused q|k|v or gate|up tensors, attention biases and mixture-of-experts layers, which the
+ * reference also reads, are refused with NC_EFORMAT.  opts may be NULL. */
 int nc_model_load_gguf(nc_ctx* ctx, const char* path, const nc_load_opts* opts, nc_model** out);
 int nc_model_load_gguf_memory(nc_ctx* ctx, const void* data, size_t size, const nc_load_opts* opts,
                               nc_model** out);
 int nc_model_get_config(const nc_model* m, nc_model_config* out);
+/* Header-only checks of an in-memory GGUF image, no GPU: gguf::read_file (src/gguf.rs:454-551),
+ * LlamaModelConfig::from_gguf (src/model.rs:48-186) and validate_model_tensors
+ * (src/model.rs:851-1036), plus the shape limits of this build; fills *out on success.  The
+ * same checks nc_model_load_gguf makes before reading any weight. */
+int nc_gguf_read_config(const void* data, size_t size, nc_model_config* out);
+/* gguf::read_file's tensor descriptors (src/gguf.rs:498-550): the count (negative: error
+ * code), and for tensor `index` its name, dimension count, dims (unused ones 1), GGML type id,
+ * absolute data offset and byte size (tensor_nbytes, src/gguf.rs:737-763). */
+int64_t nc_gguf_tensor_count(const void* data, size_t size);
+int nc_gguf_tensor_info(const void* data, size_t size, int64_t index, char* name, int64_t name_cap, int32_t* n_dims,
+                        uint64_t* dims, int32_t* type, uint64_t* offset, uint64_t* nbytes);
+/* Host-side decode of n_values of one GGUF tensor's bytes to f32, exactly as the loader
+ * decodes token embeddings and norms: load_f32_or_f16 (src/model.rs:1081-1229) for GGML
+ * types 0 (F32), 1 (F16), 30 (BF16), 8 (Q8_0), 2 (Q4_0), 3 (Q4_1), 6 (Q5_0), 7 (Q5_1),
+ * 12 (Q4_K), 13 (Q5_K), 14 (Q6_K).  Host pointers; needs no GPU. */
+int nc_dequantize_f32(int32_t type, const void* blocks, int64_t n_values, float* out);
 void nc_model_free(nc_model* m);
 
 /* ---------------------------------------------------------------- session */

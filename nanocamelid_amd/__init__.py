@@ -20,7 +20,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._ffi import (NC_TYPE_Q4_0, NC_TYPE_Q4_K, DecodeStats, LoadOpts, ModelConfig, NcError, SynthSpec,
+from ._ffi import (NC_TYPE_Q4_0, NC_TYPE_Q4_K, NC_TYPE_Q6_K, DecodeStats, LoadOpts, ModelConfig, NcError, SynthSpec,
                    VerifyResult, check, lib)
 
 __all__ = ["Context", "QMat", "Model", "Session", "matmul_quantized_batch", "matmul_blockdots",
@@ -102,6 +102,44 @@ def matmul_quantized_batch(ctx: Context, w: QMat, x_i8, x_scales, out=None):
         out = torch.empty((n, w.rows), dtype=torch.float32, device=x_i8.device)
     check(lib().nc_matmul_quantized_batch(ctx.h, w.h, x_i8.data_ptr(), x_scales.data_ptr(), out.data_ptr(), n,
                                           w.rows, w.cols, _stream_of(x_i8)))
+    return out
+
+
+def dequantize_f32(ggml_type: int, data: np.ndarray, n: int) -> np.ndarray:
+    """Host decode of one GGUF tensor's bytes to f32 as the loader does for token embeddings and
+    norms (load_f32_or_f16, src/model.rs:1081-1229).  Needs no GPU."""
+    src = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.zeros(n, np.float32)
+    check(lib().nc_dequantize_f32(int(ggml_type), src.ctypes.data, n, out.ctypes.data))
+    return out
+
+
+def gguf_read_config(data) -> dict:
+    """Header-only GGUF checks (read_file + LlamaModelConfig::from_gguf + validate_model_tensors,
+    src/gguf.rs:454-551, src/model.rs:48-186, :851-1036) on an in-memory image; no GPU.  Raises
+    NcError with the reference-style message when the file is refused."""
+    buf = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray)) else data,
+                               dtype=np.uint8)
+    cfg = ModelConfig()
+    check(lib().nc_gguf_read_config(buf.ctypes.data, buf.size, C.byref(cfg)))
+    return {f: getattr(cfg, f) for f, _ in ModelConfig._fields_}
+
+
+def gguf_tensors(data) -> list:
+    """gguf::read_file tensor descriptors: (name, dims, type, absolute offset, n_bytes)."""
+    buf = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray)) else data,
+                               dtype=np.uint8)
+    n = lib().nc_gguf_tensor_count(buf.ctypes.data, buf.size)
+    check(int(n) if n < 0 else 0)
+    out = []
+    for i in range(n):
+        name = C.create_string_buffer(512)
+        nd, ty = C.c_int32(), C.c_int32()
+        dims = (C.c_uint64 * 4)()
+        off, nb = C.c_uint64(), C.c_uint64()
+        check(lib().nc_gguf_tensor_info(buf.ctypes.data, buf.size, i, name, 512, C.byref(nd), dims, C.byref(ty),
+                                        C.byref(off), C.byref(nb)))
+        out.append((name.value.decode(), [int(dims[k]) for k in range(nd.value)], ty.value, off.value, nb.value))
     return out
 
 

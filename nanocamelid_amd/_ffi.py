@@ -18,7 +18,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libnanocamelid_hip.so")
 
 NC_OK, NC_EINVAL, NC_ENOMEM, NC_EHIP, NC_EFORMAT, NC_ERANGE = 0, -1, -2, -3, -4, -5
-NC_TYPE_F32, NC_TYPE_Q4_0, NC_TYPE_Q4_K = 0, 2, 12
+NC_TYPE_F32, NC_TYPE_Q4_0, NC_TYPE_Q4_K, NC_TYPE_Q6_K = 0, 2, 12, 14
 NC_GEMM_KERNEL_AUTO, NC_GEMM_KERNEL_DOT4, NC_GEMM_KERNEL_MFMA = 0, 1, 2
 
 
@@ -81,6 +81,12 @@ SIGNATURES = {
     "nc_model_load_gguf": (C.c_int, [_vp, C.c_char_p, C.POINTER(LoadOpts), C.POINTER(_vp)]),
     "nc_model_load_gguf_memory": (C.c_int, [_vp, _vp, C.c_size_t, C.POINTER(LoadOpts), C.POINTER(_vp)]),
     "nc_model_get_config": (C.c_int, [_vp, C.POINTER(ModelConfig)]),
+    "nc_dequantize_f32": (C.c_int, [C.c_int32, _vp, _i64, _vp]),
+    "nc_gguf_read_config": (C.c_int, [_vp, C.c_size_t, C.POINTER(ModelConfig)]),
+    "nc_gguf_tensor_count": (_i64, [_vp, C.c_size_t]),
+    "nc_gguf_tensor_info": (C.c_int, [_vp, C.c_size_t, _i64, C.c_char_p, _i64, C.POINTER(C.c_int32),
+                                      C.POINTER(C.c_uint64), C.POINTER(C.c_int32), C.POINTER(C.c_uint64),
+                                      C.POINTER(C.c_uint64)]),
     "nc_model_free": (None, [_vp]),
     "nc_session_create": (C.c_int, [_vp, _i64, _i32, C.POINTER(_vp)]),
     "nc_session_free": (None, [_vp]),

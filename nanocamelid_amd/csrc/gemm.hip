@@ -1365,6 +1365,12 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent
     p.M = (int)w.rows;
     p.K = (int)w.cols;
     if (p.N < 1 || p.N > 16) return fail(NC_EINVAL, "gemm: batch must be 1..16");
+    if (w.layout == LAYOUT_Q6K) {
+        if (ev0) NC_HIP(hipEventRecord(ev0, st));
+        const int rc = launch_gemm_q6k(w, p, st);
+        if (!rc && ev1) NC_HIP(hipEventRecord(ev1, st));
+        return rc;
+    }
     if (w.layout == LAYOUT_R16) {
         // dot products by v_dot4c (AUTO: the faster path at every measured shape and width) or,
         // on request, by int8 MFMA
@@ -1393,6 +1399,7 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent
 }
 
 int launch_blockdots(const QMatDev& w, const int8_t* x, int32_t* dots, int N, hipStream_t st) {
+    if (w.type != NC_TYPE_Q4_0 && w.type != NC_TYPE_Q4_K) return fail(NC_EINVAL, "blockdots: Q4_0 and Q4_K only");
     const int64_t total = (int64_t)N * w.rows * (w.cols / 32);
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
     if (w.type == NC_TYPE_Q4_0)

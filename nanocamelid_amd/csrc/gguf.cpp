@@ -8,6 +8,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <set>
 #include <thread>
 
 namespace nc {
@@ -71,16 +72,59 @@ bool skip_or_read(Cur& c, uint32_t type, GgufValue& v, int depth) {
 
 }  // namespace
 
+// GgufTensorType::layout (gguf.rs:154-185): (values per block, bytes per block); false for
+// type ids that have no layout (removed or unknown types).
 bool gguf_type_layout(uint32_t t, uint64_t* block, uint64_t* bytes) {
-    switch (t) {
-        case 0: *block = 1; *bytes = 4; return true;
-        case 1: *block = 1; *bytes = 2; return true;
-        case 2: *block = 32; *bytes = 18; return true;
-        case 8: *block = 32; *bytes = 34; return true;
-        case 12: *block = 256; *bytes = 144; return true;
-        case 30: *block = 1; *bytes = 2; return true;
-        default: return false;
+    struct L {
+        uint32_t id;
+        uint16_t block, bytes;
+    };
+    static const L table[] = {
+        {0, 1, 4},      {1, 1, 2},      {2, 32, 18},    {3, 32, 20},    {6, 32, 22},    {7, 32, 24},
+        {8, 32, 34},    {9, 32, 36},    {10, 256, 84},  {11, 256, 110}, {12, 256, 144}, {13, 256, 176},
+        {14, 256, 210}, {15, 256, 292}, {16, 256, 66},  {17, 256, 74},  {18, 256, 98},  {19, 256, 50},
+        {20, 32, 18},   {21, 256, 110}, {22, 256, 82},  {23, 256, 136}, {24, 1, 1},     {25, 1, 2},
+        {26, 1, 4},     {27, 1, 8},     {28, 1, 8},     {29, 256, 56},  {30, 1, 2},
+    };
+    for (const L& e : table)
+        if (e.id == t) {
+            *block = e.block;
+            *bytes = e.bytes;
+            return true;
+        }
+    return false;
+}
+
+// tensor_nbytes (gguf.rs:737-763): the first dimension must be a whole number of blocks, and
+// neither the element count nor the byte size may overflow 64 bits.
+bool gguf_tensor_nbytes(const std::string& name, const std::vector<uint64_t>& dims, uint32_t type, uint64_t* out,
+                        std::string& err) {
+    uint64_t bs, ts;
+    if (!gguf_type_layout(type, &bs, &ts)) {
+        err = "tensor " + name + " has unknown or removed GGML type " + std::to_string(type);
+        return false;
     }
+    const uint64_t first = dims.empty() ? 1 : dims[0];
+    if (first % bs) {
+        err = "tensor " + name + " first dimension " + std::to_string(first) + " is not divisible by block size " +
+              std::to_string(bs);
+        return false;
+    }
+    uint64_t el = 1;
+    for (uint64_t d : dims) {
+        if (d != 0 && el > UINT64_MAX / d) {
+            err = "tensor " + name + " element count overflow";
+            return false;
+        }
+        el *= d;
+    }
+    const uint64_t blocks = el / bs;
+    if (blocks != 0 && ts > UINT64_MAX / blocks) {
+        err = "tensor " + name + " byte size overflow";
+        return false;
+    }
+    *out = blocks * ts;
+    return true;
 }
 
 bool gguf_parse(const uint8_t* data, size_t size, GgufFile& g, std::string& err) {
@@ -108,16 +152,21 @@ bool gguf_parse(const uint8_t* data, size_t size, GgufFile& g, std::string& err)
         }
         g.meta[k] = v;
     }
-    uint64_t align = 32;
+    if (!c.ok) {
+        err = "truncated GGUF metadata";
+        return false;
+    }
+    uint64_t align = 32;  // DEFAULT_ALIGNMENT (gguf.rs:10)
     auto a = g.meta.find("general.alignment");
     if (a != g.meta.end()) {
         if (a->second.type == 4 || a->second.type == 10) align = a->second.u;
         else if (a->second.type == 5) align = (uint64_t)a->second.i;
     }
     if (align == 0 || (align & (align - 1))) {
-        err = "invalid alignment";
+        err = "invalid GGUF alignment: " + std::to_string(align);
         return false;
     }
+    g.alignment = align;
     struct Raw {
         std::string name;
         std::vector<uint64_t> dims;
@@ -129,8 +178,9 @@ bool gguf_parse(const uint8_t* data, size_t size, GgufFile& g, std::string& err)
         Raw r;
         r.name = c.s();
         uint32_t nd = (uint32_t)c.u(4);
+        if (!c.ok) break;
         if (nd == 0 || nd > 4) {
-            err = "tensor " + r.name + " has invalid dimension count";
+            err = "tensor " + r.name + " has invalid dimension count " + std::to_string(nd);
             return false;
         }
         for (uint32_t k = 0; k < nd; k++) r.dims.push_back(c.u(8));
@@ -142,27 +192,37 @@ bool gguf_parse(const uint8_t* data, size_t size, GgufFile& g, std::string& err)
         err = "truncated GGUF header";
         return false;
     }
+    if (c.pos > UINT64_MAX - (align - 1) || ((c.pos + align - 1) & ~(align - 1)) > size) {
+        err = "aligned tensor data start overflows file";
+        return false;
+    }
     const uint64_t start = (c.pos + align - 1) & ~(align - 1);
+    g.data_start = start;
+    std::set<std::string> seen;
     for (auto& r : raws) {
-        uint64_t bs, ts;
-        if (!gguf_type_layout(r.type, &bs, &ts)) {
-            err = "tensor " + r.name + " has an unsupported type " + std::to_string(r.type);
+        if (!seen.insert(r.name).second) {
+            err = "duplicate tensor name " + r.name;
             return false;
         }
-        if (r.dims[0] % bs) {
-            err = "tensor " + r.name + " first dimension not divisible by block size";
+        uint64_t nbytes;
+        if (!gguf_tensor_nbytes(r.name, r.dims, r.type, &nbytes, err)) return false;
+        if (r.off > UINT64_MAX - start) {
+            err = "tensor " + r.name + " absolute offset overflow";
             return false;
         }
-        uint64_t el = 1;
-        for (auto d : r.dims) el *= d;
-        GgufTensor t{r.name, r.dims, r.type, start + r.off, el / bs * ts};
-        if (t.offset + t.nbytes > size) {
-            err = "tensor " + r.name + " exceeds the file";
-            return false;
-        }
-        g.tensors.push_back(std::move(t));
+        g.tensors.push_back(GgufTensor{r.name, r.dims, r.type, start + r.off, nbytes});
     }
     return true;
+}
+
+// tensor_bytes (model.rs:1054-1079): the tensor's byte range must lie inside the image.
+const uint8_t* GgufFile::bytes(const GgufTensor& t, std::string& err) const {
+    if (t.offset > size || t.nbytes > size - t.offset) {
+        err = "tensor " + t.name + " byte range " + std::to_string(t.offset) + ".." + std::to_string(t.offset + t.nbytes) +
+              " exceeds mapped GGUF size " + std::to_string(size);
+        return nullptr;
+    }
+    return data + t.offset;
 }
 
 const GgufTensor* GgufFile::find(const std::string& name) const {

@@ -31,16 +31,25 @@ struct GgufTensor {
 struct GgufFile {
     const uint8_t* data = nullptr;
     size_t size = 0;
+    uint64_t alignment = 32, data_start = 0;
     std::map<std::string, GgufValue> meta;
     std::vector<GgufTensor> tensors;
     const GgufTensor* find(const std::string& name) const;
+    // the tensor's bytes, or null (err set) when its range does not lie inside the image
+    const uint8_t* bytes(const GgufTensor& t, std::string& err) const;
     bool get_u32(const std::string& k, uint32_t* out) const;
     bool get_f32(const std::string& k, float* out) const;
     std::string get_str(const std::string& k) const;
 };
 
 bool gguf_type_layout(uint32_t type, uint64_t* block, uint64_t* bytes);
+bool gguf_tensor_nbytes(const std::string& name, const std::vector<uint64_t>& dims, uint32_t type, uint64_t* out,
+                        std::string& err);
 bool gguf_parse(const uint8_t* data, size_t size, GgufFile& out, std::string& err);
+
+// Tensor bytes -> f32 as the reference's load_f32_or_f16 (dequant.cpp); n values.
+bool dequant_supported(uint32_t type);
+int dequant_f32(uint32_t type, const uint8_t* src, uint64_t n, float* out, int nthreads);
 
 void philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 uint32_t philox_word(uint64_t seed, uint64_t ctr, uint32_t purpose);

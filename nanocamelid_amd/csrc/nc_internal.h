@@ -43,7 +43,7 @@ constexpr int kQ4KChunkBytes = 9 * 1024;
 // 4 blocks x 16 rows and its scales are one contiguous 128-byte line.
 constexpr int kTileRowsR16 = 16;
 constexpr int kQ40R16QuadBytes = 1024 + 128;  // 1152; 8 per chunk = kQ40ChunkBytes
-enum Layout : int { LAYOUT_R64 = 0, LAYOUT_R16 = 1, LAYOUT_R16K = 2 };  // R16K: Q4_K on 16-row tiles
+enum Layout : int { LAYOUT_R64 = 0, LAYOUT_R16 = 1, LAYOUT_R16K = 2, LAYOUT_Q6K = 3 };  // R16K: Q4_K on 16-row tiles
 
 struct QMatDev {
     int type = NC_TYPE_Q4_0;
@@ -115,6 +115,9 @@ struct GemmParams {
 int launch_gemm(const QMatDev& w, const GemmParams& p, hipStream_t stream, hipEvent_t ev0 = nullptr,
                 hipEvent_t ev1 = nullptr);
 int launch_blockdots(const QMatDev& w, const int8_t* x, int32_t* dots, int N, hipStream_t stream);
+// Q6_K matmul (plain outputs or the head's logits + argmax partials); rows per head tile
+int launch_gemm_q6k(const QMatDev& w, const GemmParams& p, hipStream_t stream);
+int q6k_rows_per_tile(int64_t cols);
 
 // ---------------------------------------------------------------- layer kernels
 int launch_rmsnorm_q8(const float* hidden, const float* weight, int N, int d, float eps, int8_t* xq, float* xs,

@@ -11,6 +11,12 @@
 #include "gguf.h"
 #include "nc_internal.h"
 
+#include <cerrno>
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 // ---------------------------------------------------------------- handles
 // nc_ctx and nc_qmat are defined in nc_internal.h (shared with noalloc.hip).
 namespace {
@@ -215,9 +221,40 @@ struct Part {
 
 // Builds one device matrix from one or more GGUF row blocks (fused q|k|v, interleaved
 // gate/up, or a single matrix).
+// Q6_K blocks (ql 128 | qh 64 | scales 16 | d 2 bytes) split into aligned planes
+static void repack_q6_k_planes(const uint8_t* src, int64_t nblk, uint8_t* dst) {
+    parallel_for(nblk, 0, [&](int64_t lo, int64_t hi) {
+        for (int64_t i = lo; i < hi; i++) {
+            const uint8_t* b = src + i * 210;
+            std::memcpy(dst + i * 128, b, 128);
+            std::memcpy(dst + nblk * 128 + i * 64, b + 128, 64);
+            std::memcpy(dst + nblk * 192 + i * 16, b + 192, 16);
+            std::memcpy(dst + nblk * 208 + i * 2, b + 208, 2);
+        }
+    });
+}
+
 static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector<Part>& parts, QMatDev& out) {
-    if (cols % 32 || (type == NC_TYPE_Q4_K && cols % 256))
-        return fail(NC_EINVAL, "matrix columns must be a multiple of 32 (Q4_K: 256)");
+    if (cols % 32 || ((type == NC_TYPE_Q4_K || type == NC_TYPE_Q6_K) && cols % 256))
+        return fail(NC_EINVAL, "matrix columns must be a multiple of 32 (Q4_K, Q6_K: 256)");
+    if (type == NC_TYPE_Q6_K) {
+        if (parts.size() != 1 || parts[0].half >= 0 || parts[0].rows != rows || cols > 16384)
+            return fail(NC_EINVAL, "Q6_K: single matrices of at most 16384 columns");
+        out.type = type;
+        out.layout = LAYOUT_Q6K;
+        out.rows = rows;
+        out.cols = cols;
+        out.units = cols / 256;
+        out.tiles = (rows + q6k_rows_per_tile(cols) - 1) / q6k_rows_per_tile(cols);
+        out.groups = 0;
+        out.algo_bytes = rows * (cols / 256) * 210;
+        out.dev_bytes = out.algo_bytes + 4;
+        std::vector<uint8_t> host(out.dev_bytes, 0);
+        repack_q6_k_planes(parts[0].src, rows * (cols / 256), host.data());
+        NC_HIP(hipMalloc((void**)&out.dev, out.dev_bytes));
+        NC_HIP(hipMemcpy(out.dev, host.data(), out.dev_bytes, hipMemcpyHostToDevice));
+        return NC_OK;
+    }
     out.type = type;
     out.rows = rows;
     out.cols = cols;
@@ -257,7 +294,6 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
 }
 
 // ---------------------------------------------------------------- f16 helpers (host)
-static inline float f16_to_f32_host(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
 // q8.rs:3644-3673 fast_f32_to_f16 (truncating), used by the tied-head requantisation.
 static uint16_t f32_to_f16_trunc(float value) {
@@ -318,63 +354,111 @@ static void requant_tied_head(const float* emb, int64_t rows, int64_t cols, uint
 }
 
 // load_f32_or_f16 (model.rs:1081-1230) for the types this path meets.
+// load_f32_or_f16 (model.rs:1081-1229): the tensor decoded to f32 (dequant.cpp).
 static int tensor_to_f32(const GgufFile& g, const std::string& name, std::vector<float>& out) {
     const GgufTensor* t = g.find(name);
-    if (!t) return fail(NC_EFORMAT, "missing tensor " + name);
+    if (!t) return fail(NC_EFORMAT, "tensor " + name + " not found in GGUF");
+    std::string err;
+    const uint8_t* p = g.bytes(*t, err);
+    if (!p) return fail(NC_EFORMAT, err);
     uint64_t el = 1;
     for (auto d : t->dims) el *= d;
     out.resize(el);
-    const uint8_t* p = g.data + t->offset;
-    if (t->type == NC_TYPE_F32) {
-        std::memcpy(out.data(), p, el * 4);
-    } else if (t->type == 1) {
-        for (uint64_t i = 0; i < el; i++) out[i] = f16_to_f32_host((uint16_t)(p[2 * i] | (p[2 * i + 1] << 8)));
-    } else if (t->type == NC_TYPE_Q4_0) {
-        parallel_for((int64_t)(el / 32), 0, [&](int64_t lo, int64_t hi) {
-            for (int64_t b = lo; b < hi; b++) {
-                const uint8_t* blk = p + b * 18;
-                const float sc = f16_to_f32_host((uint16_t)(blk[0] | (blk[1] << 8)));
-                for (int j = 0; j < 16; j++) {
-                    out[b * 32 + j] = (float)((int)(blk[2 + j] & 0x0f) - 8) * sc;
-                    out[b * 32 + 16 + j] = (float)((int)(blk[2 + j] >> 4) - 8) * sc;
-                }
-            }
-        });
-    } else if (t->type == NC_TYPE_Q4_K) {
-        // Q4KBlock::dequantize (q8.rs:1233-1264)
-        parallel_for((int64_t)(el / 256), 0, [&](int64_t lo, int64_t hi) {
-            for (int64_t b = lo; b < hi; b++) {
-                const uint8_t* blk = p + b * 144;
-                const float d = f16_to_f32_host((uint16_t)(blk[0] | (blk[1] << 8)));
-                const float dmin = f16_to_f32_host((uint16_t)(blk[2] | (blk[3] << 8)));
-                const uint8_t* sc = blk + 4;
-                const uint8_t* qs = blk + 16;
-                auto smin = [&](int j, uint8_t* s, uint8_t* m) {
-                    if (j < 4) {
-                        *s = sc[j] & 63;
-                        *m = sc[j + 4] & 63;
-                    } else {
-                        *s = (uint8_t)((sc[j + 4] & 0x0f) | ((sc[j - 4] >> 6) << 4));
-                        *m = (uint8_t)((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
-                    }
-                };
-                float* o = out.data() + b * 256;
-                for (int pr = 0; pr < 4; pr++) {
-                    uint8_t ls, lm, hs, hm;
-                    smin(2 * pr, &ls, &lm);
-                    smin(2 * pr + 1, &hs, &hm);
-                    const float lsc = d * (float)ls, hsc = d * (float)hs;
-                    const float lmn = dmin * (float)lm, hmn = dmin * (float)hm;
-                    for (int l = 0; l < 32; l++) {
-                        const uint8_t byte = qs[pr * 32 + l];
-                        o[pr * 64 + l] = lsc * (float)(byte & 0x0f) - lmn;
-                        o[pr * 64 + 32 + l] = hsc * (float)(byte >> 4) - hmn;
-                    }
-                }
-            }
-        });
-    } else {
-        return fail(NC_EFORMAT, "tensor " + name + ": unsupported type for an f32 load");
+    int rc = dequant_f32(t->type, p, el, out.data(), 0);
+    return rc ? fail(rc, name + ": " + t_err) : NC_OK;
+}
+
+// ---------------------------------------------------------------- tensor validation
+// validate_model_tensors (model.rs:851-1036) for the dense Llama layout this build runs:
+// every tensor the model needs is present with the descriptor shape the reference accepts
+// ([input, output] or its transpose for matrices, [width] for norms) and the token rows of
+// the embedding and the head fill their byte size exactly.  Layouts the reference also reads
+// but this build does not run (fused q|k|v or gate|up, attention biases, mixture-of-experts
+// layers) are refused here, before anything is uploaded.
+static std::string dims_str(const std::vector<uint64_t>& d) {
+    std::string s = "[";
+    for (size_t i = 0; i < d.size(); i++) s += (i ? ", " : "") + std::to_string(d[i]);
+    return s + "]";
+}
+
+static int require_shape(const GgufFile& g, const std::string& name, const std::vector<uint64_t>& want,
+                         const std::string& role, const GgufTensor** out = nullptr) {
+    const GgufTensor* t = g.find(name);
+    if (!t) return fail(NC_EFORMAT, "tensor " + name + " not found in GGUF");
+    if (t->dims != want)
+        return fail(NC_EFORMAT, role + " tensor " + name + " expected descriptor shape " + dims_str(want) + ", got " +
+                                    dims_str(t->dims));
+    if (out) *out = t;
+    return NC_OK;
+}
+
+static int require_matrix(const GgufFile& g, const std::string& name, uint64_t in, uint64_t outw,
+                          const std::string& role, const GgufTensor** out = nullptr) {
+    const GgufTensor* t = g.find(name);
+    if (!t) return fail(NC_EFORMAT, "tensor " + name + " not found in GGUF");
+    const std::vector<uint64_t> direct{in, outw}, transposed{outw, in};
+    if (t->dims != direct && t->dims != transposed)
+        return fail(NC_EFORMAT, role + " tensor " + name + " expected descriptor shape " + dims_str(direct) + " or " +
+                                    dims_str(transposed) + ", got " + dims_str(t->dims));
+    if (out) *out = t;
+    return NC_OK;
+}
+
+// validate_token_row_storage_layout (model.rs:1477-1530)
+static int require_token_rows(const GgufTensor& t, uint64_t hidden, uint64_t vocab, const std::string& role) {
+    uint64_t row_values;
+    if (t.dims.size() == 2 && t.dims[0] == hidden && t.dims[1] == vocab) row_values = hidden;
+    else if (t.dims.size() == 2 && t.dims[0] == vocab && t.dims[1] == hidden) row_values = hidden;
+    else return NC_OK;
+    uint64_t bs, ts;
+    if (!gguf_type_layout(t.type, &bs, &ts))
+        return fail(NC_EFORMAT, role + " tensor " + t.name + " has unsupported storage type for token-row validation");
+    if (row_values % bs)
+        return fail(NC_EFORMAT, role + " tensor " + t.name + " token-row width " + std::to_string(row_values) +
+                                    " is not divisible by block size " + std::to_string(bs));
+    const uint64_t expected = row_values / bs * ts * vocab;
+    if (t.nbytes != expected)
+        return fail(NC_EFORMAT, role + " tensor " + t.name + " byte size " + std::to_string(t.nbytes) +
+                                    " does not match " + std::to_string(vocab) + " token rows (" + std::to_string(expected) +
+                                    " bytes)");
+    return NC_OK;
+}
+
+static int validate_model_tensors(const GgufFile& g, const nc_model_config& c) {
+    const uint64_t d = c.embedding_length, V = c.vocab_size, F = c.feed_forward_length;
+    const uint64_t aw = c.attention_output_width, kw = c.kv_width;
+    const GgufTensor* t = nullptr;
+    int rc;
+    if ((rc = require_matrix(g, "token_embd.weight", d, V, "token embedding", &t)) ||
+        (rc = require_token_rows(*t, d, V, "token embedding")) ||
+        (rc = require_shape(g, "output_norm.weight", {d}, "output norm")))
+        return rc;
+    if (g.find("output.weight")) {
+        if ((rc = require_matrix(g, "output.weight", d, V, "output projection", &t)) ||
+            (rc = require_token_rows(*t, d, V, "output projection")))
+            return rc;
+    }
+    for (int64_t i = 0; i < c.block_count; i++) {
+        const std::string b = "blk." + std::to_string(i) + ".", L = "layer " + std::to_string(i) + " ";
+        if ((rc = require_shape(g, b + "attn_norm.weight", {d}, L + "attention norm"))) return rc;
+        if (g.find(b + "attn_qkv.weight"))
+            return fail(NC_EFORMAT, "tensor " + b + "attn_qkv.weight: fused q|k|v layers are not supported");
+        for (const char* bias : {"attn_q.bias", "attn_k.bias", "attn_v.bias"})
+            if (g.find(b + bias)) return fail(NC_EFORMAT, "tensor " + b + bias + ": attention biases are not supported");
+        if ((rc = require_matrix(g, b + "attn_q.weight", d, aw, L + "attention q")) ||
+            (rc = require_matrix(g, b + "attn_k.weight", d, kw, L + "attention k")) ||
+            (rc = require_matrix(g, b + "attn_v.weight", d, kw, L + "attention v")) ||
+            (rc = require_matrix(g, b + "attn_output.weight", aw, d, L + "attention output")) ||
+            (rc = require_shape(g, b + "ffn_norm.weight", {d}, L + "ffn norm")))
+            return rc;
+        if (g.find(b + "ffn_gate.0.weight") || g.find(b + "ffn_gate_inp.weight"))
+            return fail(NC_EFORMAT, "layer " + std::to_string(i) + ": mixture-of-experts layers are not supported");
+        if (!g.find(b + "ffn_gate.weight"))
+            return fail(NC_EFORMAT, "layer " + std::to_string(i) + ": fused ffn gate|up (no ffn_gate.weight) is not supported");
+        if ((rc = require_matrix(g, b + "ffn_gate.weight", d, F, L + "ffn gate")) ||
+            (rc = require_matrix(g, b + "ffn_up.weight", d, F, L + "ffn up")) ||
+            (rc = require_matrix(g, b + "ffn_down.weight", F, d, L + "ffn down")))
+            return rc;
     }
     return NC_OK;
 }
@@ -395,18 +479,27 @@ static int upload_f32(std::vector<void*>& list, const std::vector<float>& h, flo
     return NC_OK;
 }
 
-static const GgufTensor* matrix_desc(const GgufFile& g, const std::string& name, int64_t rows, int64_t cols, int* err) {
+static const GgufTensor* matrix_desc(const GgufFile& g, const std::string& name, int64_t rows, int64_t cols, int* err,
+                                     bool allow_q6k = false) {
     const GgufTensor* t = g.find(name);
     if (!t) {
         *err = fail(NC_EFORMAT, "missing tensor " + name);
         return nullptr;
     }
     if (t->dims.size() != 2 || (int64_t)t->dims[0] != cols || (int64_t)t->dims[1] != rows) {
-        *err = fail(NC_EFORMAT, "tensor " + name + " has an unexpected shape");
+        *err = fail(NC_EFORMAT, "tensor " + name + ": transposed (output-major) storage " + dims_str(t->dims) +
+                                    " is not supported");
         return nullptr;
     }
-    if (t->type != NC_TYPE_Q4_0 && t->type != NC_TYPE_Q4_K) {
-        *err = fail(NC_EFORMAT, "tensor " + name + ": only Q4_0 and Q4_K matrices are supported");
+    if (t->type != NC_TYPE_Q4_0 && t->type != NC_TYPE_Q4_K && !(allow_q6k && t->type == NC_TYPE_Q6_K)) {
+        *err = fail(NC_EFORMAT, "tensor " + name + ": only Q4_0 and Q4_K matrices are supported" +
+                                    (allow_q6k ? " (and Q6_K for the head)" : "") + ", got GGML type " +
+                                    std::to_string(t->type));
+        return nullptr;
+    }
+    std::string e;
+    if (!g.bytes(*t, e)) {
+        *err = fail(NC_EFORMAT, e);
         return nullptr;
     }
     return t;
@@ -422,15 +515,12 @@ static void free_model(nc_model* m) {
     delete m;
 }
 
-static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_load_opts* opts, nc_model** out) {
-    GgufFile g;
-    std::string err;
-    if (!gguf_parse(data, size, g, err)) return fail(NC_EFORMAT, err);
+// LlamaModelConfig::from_gguf (model.rs:48-186) plus this build's support checks and
+// validate_model_tensors: everything decided from the header, before any weight is read.
+static int read_config(const GgufFile& g, nc_model_config& c) {
+    c = nc_model_config{};
     if (g.get_str("general.architecture") != "llama")
         return fail(NC_EFORMAT, "unsupported architecture: " + g.get_str("general.architecture"));
-    std::unique_ptr<nc_model, void (*)(nc_model*)> m(new nc_model(), free_model);
-    m->ctx = ctx;
-    nc_model_config& c = m->cfg;
     // LlamaModelConfig::from_gguf (model.rs:48-186)
     uint32_t v;
     const std::string P = "llama.";
@@ -475,12 +565,26 @@ static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_lo
         return fail(NC_EFORMAT, "invalid rope.dimension_count");
     c.attention_output_width = c.head_count * c.head_dim;
     c.kv_width = c.head_count_kv * c.head_dim;
-    const int64_t d = c.embedding_length, F = c.feed_forward_length, V = c.vocab_size;
+    const int64_t d = c.embedding_length, F = c.feed_forward_length;
     const int64_t aw = c.attention_output_width, kw = c.kv_width;
     if (aw % 64 || kw % 64 || F % 32 || d % 256)
         return fail(NC_EINVAL, "model widths must be multiples of 64 (attention), 32 (ffn), 256 (embedding)");
     if (c.head_dim != 64 && c.head_dim != 128) return fail(NC_EINVAL, "head_dim must be 64 or 128");
     if (c.head_count / c.head_count_kv > 8) return fail(NC_EINVAL, "at most 8 query heads per KV head");
+    return validate_model_tensors(g, c);
+}
+
+static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_load_opts* opts, nc_model** out) {
+    GgufFile g;
+    std::string err;
+    if (!gguf_parse(data, size, g, err)) return fail(NC_EFORMAT, err);
+    std::unique_ptr<nc_model, void (*)(nc_model*)> m(new nc_model(), free_model);
+    m->ctx = ctx;
+    nc_model_config& c = m->cfg;
+    int rc0 = read_config(g, c);
+    if (rc0) return rc0;
+    const int64_t d = c.embedding_length, F = c.feed_forward_length, V = c.vocab_size;
+    const int64_t aw = c.attention_output_width, kw = c.kv_width;
     // weights (LlamaWeights::load, model.rs:461-545)
     std::vector<float> emb;
     int rc = tensor_to_f32(g, "token_embd.weight", emb);
@@ -493,7 +597,7 @@ static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_lo
     if ((rc = upload_f32(m->allocs, tmp, &m->out_norm))) return rc;
     if (const GgufTensor* ot = g.find("output.weight")) {
         int e = 0;
-        if (!matrix_desc(g, "output.weight", V, d, &e)) return e;
+        if (!matrix_desc(g, "output.weight", V, d, &e, true)) return e;
         if ((rc = upload_matrix((int)ot->type, V, d, {{g.data + ot->offset, V, 0, -1}}, m->head))) return rc;
         c.tied_head = 0;
     } else {
@@ -970,7 +1074,8 @@ int nc_ctx_synchronize(nc_ctx* c) {
 
 int nc_qmat_upload(nc_ctx* ctx, int type, int64_t rows, int64_t cols, const void* blocks, nc_qmat** out) {
     if (!ctx || !blocks || !out || rows <= 0 || cols <= 0) return fail(NC_EINVAL, "nc_qmat_upload: bad arguments");
-    if (type != NC_TYPE_Q4_0 && type != NC_TYPE_Q4_K) return fail(NC_EINVAL, "nc_qmat_upload: type must be Q4_0 or Q4_K");
+    if (type != NC_TYPE_Q4_0 && type != NC_TYPE_Q4_K && type != NC_TYPE_Q6_K)
+        return fail(NC_EINVAL, "nc_qmat_upload: type must be Q4_0, Q4_K or Q6_K");
     NC_HIP(hipSetDevice(ctx->device));
     auto* q = new nc_qmat();
     q->ctx = ctx;
@@ -1140,18 +1245,66 @@ int nc_model_load_gguf_memory(nc_ctx* ctx, const void* data, size_t size, const 
     return load_model(ctx, (const uint8_t*)data, size, opts, out);
 }
 
+// LlamaWeights::load maps the file (model.rs:461-467); so does this: the header is parsed from
+// the mapping and each matrix is repacked from it into a staging buffer of that matrix alone,
+// so no copy of the whole file is ever made in host memory.
 int nc_model_load_gguf(nc_ctx* ctx, const char* path, const nc_load_opts* opts, nc_model** out) {
     if (!ctx || !path || !out) return fail(NC_EINVAL, "nc_model_load_gguf: null argument");
-    FILE* fp = std::fopen(path, "rb");
-    if (!fp) return fail(NC_EINVAL, std::string("cannot open ") + path);
-    std::fseek(fp, 0, SEEK_END);
-    const long sz = std::ftell(fp);
-    std::fseek(fp, 0, SEEK_SET);
-    std::vector<uint8_t> buf((size_t)sz);
-    const size_t got = std::fread(buf.data(), 1, buf.size(), fp);
-    std::fclose(fp);
-    if (got != buf.size()) return fail(NC_EFORMAT, "short read");
-    return nc_model_load_gguf_memory(ctx, buf.data(), buf.size(), opts, out);
+    const int fd = ::open(path, O_RDONLY);
+    if (fd < 0) return fail(NC_EINVAL, std::string("cannot open ") + path + ": " + std::strerror(errno));
+    struct stat st;
+    if (::fstat(fd, &st) != 0 || st.st_size <= 0) {
+        ::close(fd);
+        return fail(NC_EFORMAT, std::string("cannot stat ") + path);
+    }
+    const size_t size = (size_t)st.st_size;
+    void* map = ::mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (map == MAP_FAILED) return fail(NC_EFORMAT, std::string("cannot map ") + path + ": " + std::strerror(errno));
+    (void)::madvise(map, size, MADV_WILLNEED);
+    const int rc = nc_model_load_gguf_memory(ctx, map, size, opts, out);
+    ::munmap(map, size);
+    return rc;
+}
+
+int nc_gguf_read_config(const void* data, size_t size, nc_model_config* out) {
+    if (!data || !out) return fail(NC_EINVAL, "nc_gguf_read_config: null argument");
+    GgufFile g;
+    std::string err;
+    if (!gguf_parse((const uint8_t*)data, size, g, err)) return fail(NC_EFORMAT, err);
+    nc_model_config c;
+    int rc = read_config(g, c);
+    if (rc) return rc;
+    *out = c;
+    return NC_OK;
+}
+
+int64_t nc_gguf_tensor_count(const void* data, size_t size) {
+    if (!data) return fail(NC_EINVAL, "nc_gguf_tensor_count: null argument");
+    GgufFile g;
+    std::string err;
+    if (!gguf_parse((const uint8_t*)data, size, g, err)) return fail(NC_EFORMAT, err);
+    return (int64_t)g.tensors.size();
+}
+
+int nc_gguf_tensor_info(const void* data, size_t size, int64_t index, char* name, int64_t name_cap, int32_t* n_dims,
+                        uint64_t* dims, int32_t* type, uint64_t* offset, uint64_t* nbytes) {
+    if (!data || !name || name_cap < 1 || !n_dims || !dims || !type || !offset || !nbytes)
+        return fail(NC_EINVAL, "nc_gguf_tensor_info: null argument");
+    GgufFile g;
+    std::string err;
+    if (!gguf_parse((const uint8_t*)data, size, g, err)) return fail(NC_EFORMAT, err);
+    if (index < 0 || index >= (int64_t)g.tensors.size()) return fail(NC_ERANGE, "nc_gguf_tensor_info: index out of range");
+    const GgufTensor& t = g.tensors[(size_t)index];
+    const size_t n = std::min((size_t)name_cap - 1, t.name.size());
+    std::memcpy(name, t.name.data(), n);
+    name[n] = 0;
+    *n_dims = (int32_t)t.dims.size();
+    for (size_t i = 0; i < 4; i++) dims[i] = i < t.dims.size() ? t.dims[i] : 1;
+    *type = (int32_t)t.type;
+    *offset = t.offset;
+    *nbytes = t.nbytes;
+    return NC_OK;
 }
 
 int nc_model_get_config(const nc_model* m, nc_model_config* out) {

@@ -71,16 +71,22 @@ struct Cursor {
 };
 
 // gguf.rs:154-185 GgufTensorType::layout (block size, type size) for the types used here.
+// gguf.rs:154-185 GgufTensorType::layout: (values per block, bytes per block)
 bool type_layout(uint32_t t, uint64_t* bs, uint64_t* ts) {
-    switch (t) {
-        case 0: *bs = 1; *ts = 4; return true;      // F32
-        case 1: *bs = 1; *ts = 2; return true;      // F16
-        case 2: *bs = 32; *ts = 18; return true;    // Q4_0
-        case 8: *bs = 32; *ts = 34; return true;    // Q8_0
-        case 12: *bs = 256; *ts = 144; return true; // Q4_K
-        case 30: *bs = 1; *ts = 2; return true;     // BF16
-        default: return false;
-    }
+    static const uint32_t tab[][3] = {
+        {0, 1, 4},     {1, 1, 2},     {2, 32, 18},   {3, 32, 20},   {6, 32, 22},   {7, 32, 24},
+        {8, 32, 34},   {9, 32, 36},   {10, 256, 84}, {11, 256, 110}, {12, 256, 144}, {13, 256, 176},
+        {14, 256, 210}, {15, 256, 292}, {16, 256, 66}, {17, 256, 74}, {18, 256, 98}, {19, 256, 50},
+        {20, 32, 18},  {21, 256, 110}, {22, 256, 82}, {23, 256, 136}, {24, 1, 1},   {25, 1, 2},
+        {26, 1, 4},    {27, 1, 8},    {28, 1, 8},    {29, 256, 56}, {30, 1, 2},
+    };
+    for (auto& e : tab)
+        if (e[0] == t) {
+            *bs = e[1];
+            *ts = e[2];
+            return true;
+        }
+    return false;
 }
 
 bool read_value(Cursor& c, uint32_t type, MetaVal& v, int depth = 0) {
@@ -229,43 +235,31 @@ struct or_session {
 namespace {
 
 bool load_f32_tensor(const Gguf& g, const std::string& name, std::vector<float>& out, std::string& err) {
-    // model.rs:1081-1230 load_f32_or_f16 (F32, F16, Q4_0, Q4_K used here)
+    // model.rs:1081-1230 load_f32_or_f16
     const Tensor* t = g.find(name);
     if (!t) { err = "missing tensor " + name; return false; }
-    const uint8_t* p = g.data + t->offset;
     uint64_t el = 1;
     for (auto dd : t->dims) el *= dd;
     out.resize(el);
-    if (t->type == 0) {
-        std::memcpy(out.data(), p, el * 4);
-    } else if (t->type == 1) {
-        for (uint64_t i = 0; i < el; i++) out[i] = or_f16_to_f32(load_u16(p + 2 * i));
-    } else if (t->type == 2) {
-        for (uint64_t b = 0; b < el / 32; b++) {
-            const uint8_t* blk = p + b * 18;
-            float sc = or_f16_to_f32(load_u16(blk));
-            for (int j = 0; j < 16; j++) {
-                out[b * 32 + j] = (float)((int)(blk[2 + j] & 0x0f) - 8) * sc;
-                out[b * 32 + 16 + j] = (float)((int)(blk[2 + j] >> 4) - 8) * sc;
-            }
-        }
-    } else if (t->type == 12) {
-        for (uint64_t b = 0; b < el / 256; b++) or_q4_k_dequantize(p + b * 144, out.data() + b * 256);
-    } else {
+    if (or_dequantize_f32((int)t->type, g.data + t->offset, (int64_t)el, out.data()) != 0) {
         err = "unsupported f32 source type for " + name;
         return false;
     }
     return true;
 }
 
-bool load_qmat(const Gguf& g, const std::string& name, int64_t rows, int64_t cols, QMat& q, std::string& err) {
+bool load_qmat(const Gguf& g, const std::string& name, int64_t rows, int64_t cols, QMat& q, std::string& err,
+               bool allow_q6k = false) {
     const Tensor* t = g.find(name);
     if (!t) { err = "missing tensor " + name; return false; }
     if (t->dims.size() != 2 || (int64_t)t->dims[0] != cols || (int64_t)t->dims[1] != rows) {
         err = "bad shape for " + name;
         return false;
     }
-    if (t->type != 2 && t->type != 12) { err = "unsupported matrix type for " + name; return false; }
+    if (t->type != 2 && t->type != 12 && !(allow_q6k && t->type == 14)) {
+        err = "unsupported matrix type for " + name;
+        return false;
+    }
     q.type = t->type;
     q.rows = rows;
     q.cols = cols;
@@ -321,7 +315,7 @@ bool build_model(or_model* m, const uint8_t* data, size_t size, std::string& err
     if (!load_f32_tensor(g, "output_norm.weight", m->out_norm, err)) return false;
     m->has_output = g.find("output.weight") != nullptr;
     if (m->has_output) {
-        if (!load_qmat(g, "output.weight", m->V, m->d, m->head, err)) return false;
+        if (!load_qmat(g, "output.weight", m->V, m->d, m->head, err, true)) return false;
     } else {
         // model.rs:471-532 tied head -> Q4_0 requantisation of the f32 embeddings.
         m->head.type = 2;
@@ -354,6 +348,7 @@ bool build_model(or_model* m, const uint8_t* data, size_t size, std::string& err
 void matmul(const or_model* m, float* out, const int8_t* x, const float* xs, const QMat& w, int64_t N) {
     // inference.rs:1246-1303 matmul_quantized_batch dispatch
     if (w.type == 2) or_matmul_q4_0(out, x, xs, w.blocks.data(), N, w.rows, w.cols, m->nthreads);
+    else if (w.type == 14) or_matmul_q6_k(out, x, xs, w.blocks.data(), N, w.rows, w.cols, m->nthreads);
     else or_matmul_q4_k(out, x, xs, w.blocks.data(), N, w.rows, w.cols, m->nthreads);
 }
 

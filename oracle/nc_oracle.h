@@ -49,6 +49,10 @@ void or_q4_k_subblock_ints(const uint8_t* block144, const int8_t* x256, int32_t*
 float or_q4_k_dot(const uint8_t* block144, const int8_t* x256, const float* xs8); /* q8.rs:1339 */
 /* Q4_K dequantisation (q8.rs:1240-1264). */
 void or_q4_k_dequantize(const uint8_t* block144, float* out256);
+int or_dequantize_f32(int type, const uint8_t* bytes, int64_t n, float* out);
+float or_q6_k_dot(const uint8_t* block210, const int8_t* x256, const float* xs8);
+void or_matmul_q6_k(float* out, const int8_t* x, const float* xs, const uint8_t* w, int64_t N, int64_t M, int64_t K,
+                    int nthreads);
 
 /* inference.rs:935-1029 (scalar x86 path): per 32-block f32 scale amax/127. */
 void or_quantize_q8_0(const float* x, int64_t n, int8_t* q, float* scales);

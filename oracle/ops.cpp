@@ -157,6 +157,128 @@ void or_q4_k_dequantize(const uint8_t* blk, float* out) {
     }
 }
 
+// load_f32_or_f16 (model.rs:1081-1229): one tensor's n values decoded to f32, written in the
+// reference's per-type loop order.  Types: 0 F32, 1 F16, 30 BF16, 8 Q8_0, 2 Q4_0, 3 Q4_1,
+// 6 Q5_0, 7 Q5_1, 12 Q4_K, 13 Q5_K, 14 Q6_K.  Returns 0, or -1 for any other type.
+int or_dequantize_f32(int type, const uint8_t* p, int64_t n, float* out) {
+    int64_t o = 0;
+    switch (type) {
+        case 0:
+            std::memcpy(out, p, (size_t)n * 4);
+            return 0;
+        case 1:
+            for (int64_t i = 0; i < n; i++) out[i] = or_f16_to_f32(load_u16(p + 2 * i));
+            return 0;
+        case 30:
+            for (int64_t i = 0; i < n; i++) out[i] = bits_f32((uint32_t)load_u16(p + 2 * i) << 16);
+            return 0;
+        case 8:  // q8.rs:478-511: value * scale
+            for (int64_t b = 0; b < n / 32; b++, p += 34) {
+                const float scale = or_f16_to_f32(load_u16(p));
+                for (int k = 0; k < 32; k++) out[o++] = (float)(int8_t)p[2 + k] * scale;
+            }
+            return 0;
+        case 2:  // q8.rs:514-547 unpack_values (low nibbles then high) - 8, * scale
+            for (int64_t b = 0; b < n / 32; b++, p += 18) {
+                const float scale = or_f16_to_f32(load_u16(p));
+                int8_t v[32];
+                for (int k = 0; k < 16; k++) {
+                    v[k] = (int8_t)((p[2 + k] & 0x0f) - 8);
+                    v[k + 16] = (int8_t)((p[2 + k] >> 4) - 8);
+                }
+                for (int k = 0; k < 32; k++) out[o++] = (float)v[k] * scale;
+            }
+            return 0;
+        case 3:  // q8.rs:549-599: value * scale + min
+            for (int64_t b = 0; b < n / 32; b++, p += 20) {
+                const float scale = or_f16_to_f32(load_u16(p)), mn = or_f16_to_f32(load_u16(p + 2));
+                uint8_t v[32];
+                for (int k = 0; k < 16; k++) {
+                    v[k] = p[4 + k] & 0x0f;
+                    v[k + 16] = p[4 + k] >> 4;
+                }
+                for (int k = 0; k < 32; k++) out[o++] = (float)v[k] * scale + mn;
+            }
+            return 0;
+        case 6:  // q8.rs:601-649: 5-bit values - 16, * scale
+        case 7:  // q8.rs:651-720: 5-bit values * scale + min
+            for (int64_t b = 0; b < n / 32; b++) {
+                const bool has_min = type == 7;
+                const float scale = or_f16_to_f32(load_u16(p));
+                const float mn = has_min ? or_f16_to_f32(load_u16(p + 2)) : 0.0f;
+                const uint8_t* hb = p + (has_min ? 4 : 2);
+                const uint32_t high = (uint32_t)hb[0] | ((uint32_t)hb[1] << 8) | ((uint32_t)hb[2] << 16) | ((uint32_t)hb[3] << 24);
+                const uint8_t* qs = hb + 4;
+                int v[32];
+                for (int k = 0; k < 16; k++) {
+                    v[k] = (qs[k] & 0x0f) | (int)(((high >> k) & 1u) << 4);
+                    v[k + 16] = (qs[k] >> 4) | (int)(((high >> (k + 16)) & 1u) << 4);
+                }
+                for (int k = 0; k < 32; k++) out[o++] = has_min ? (float)v[k] * scale + mn : (float)(v[k] - 16) * scale;
+                p += has_min ? 24 : 22;
+            }
+            return 0;
+        case 12:
+            for (int64_t b = 0; b < n / 256; b++) or_q4_k_dequantize(p + b * 144, out + b * 256);
+            return 0;
+        case 13:  // q8.rs:1467-1498 Q5KBlock::dequantize
+            for (int64_t b = 0; b < n / 256; b++, p += 176) {
+                const float d = or_f16_to_f32(load_u16(p)), dmin = or_f16_to_f32(load_u16(p + 2));
+                const uint8_t* scales = p + 4;
+                const uint8_t* high = p + 16;
+                const uint8_t* vals = p + 48;
+                float* ob = out + b * 256;
+                uint8_t u1 = 1, u2 = 2;
+                for (int pair = 0; pair < 4; pair++) {
+                    uint8_t ls, lm, hs, hm;
+                    q4k_scale_min(pair * 2, scales, &ls, &lm);
+                    q4k_scale_min(pair * 2 + 1, scales, &hs, &hm);
+                    const float lsc = d * (float)ls, hsc = d * (float)hs;
+                    const float lmn = dmin * (float)lm, hmn = dmin * (float)hm;
+                    for (int l = 0; l < 32; l++) {
+                        const uint8_t byte = vals[pair * 32 + l];
+                        const int low = (byte & 0x0f) + ((high[l] & u1) != 0 ? 16 : 0);
+                        const int hi = (byte >> 4) + ((high[l] & u2) != 0 ? 16 : 0);
+                        ob[pair * 64 + l] = lsc * (float)low - lmn;
+                        ob[pair * 64 + 32 + l] = hsc * (float)hi - hmn;
+                    }
+                    u1 = (uint8_t)(u1 << 2);
+                    u2 = (uint8_t)(u2 << 2);
+                }
+            }
+            return 0;
+        case 14:  // q8.rs:2063-2090 Q6KBlock::dequantize
+            for (int64_t b = 0; b < n / 256; b++, p += 210) {
+                const uint8_t* ql = p;
+                const uint8_t* qh = p + 128;
+                const int8_t* sc = (const int8_t*)(p + 192);
+                const float d = or_f16_to_f32(load_u16(p + 208));
+                float* ob = out + b * 256;
+                int qlo = 0, qho = 0, so = 0;
+                for (int nn = 0; nn < 256; nn += 128) {
+                    for (int l = 0; l < 32; l++) {
+                        const int is = l / 16;
+                        const uint8_t h = qh[qho + l];
+                        const int q1 = (int8_t)((ql[qlo + l] & 0x0f) | ((h & 0x03) << 4)) - 32;
+                        const int q2 = (int8_t)((ql[qlo + l + 32] & 0x0f) | (((h >> 2) & 0x03) << 4)) - 32;
+                        const int q3 = (int8_t)((ql[qlo + l] >> 4) | (((h >> 4) & 0x03) << 4)) - 32;
+                        const int q4 = (int8_t)((ql[qlo + l + 32] >> 4) | (((h >> 6) & 0x03) << 4)) - 32;
+                        ob[nn + l] = d * (float)sc[so + is] * (float)q1;
+                        ob[nn + l + 32] = d * (float)sc[so + is + 2] * (float)q2;
+                        ob[nn + l + 64] = d * (float)sc[so + is + 4] * (float)q3;
+                        ob[nn + l + 96] = d * (float)sc[so + is + 6] * (float)q4;
+                    }
+                    qlo += 64;
+                    qho += 32;
+                    so += 8;
+                }
+            }
+            return 0;
+        default:
+            return -1;
+    }
+}
+
 // Rust `(f32).clamp(-127.0, 127.0) as i8` after `.round()` (roundf: half away from zero).
 static inline int8_t round_clamp_i8(float v) {
     float q = std::round(v);
@@ -291,6 +413,60 @@ void or_matmul_q4_k(float* out, const int8_t* x, const float* xs, const uint8_t*
                 out[t * M + r] = sum;
             }
         }
+    });
+}
+
+// q8.rs:2093-2150 Q6KBlock::dot_q8_scaled: weight_scales[i] = d * scales[i]; per 128-value
+// half n, c*_low / c*_high = weight_scale * x_scale of the 32-value group; then for l in 0..16
+// (low scales) and l in 16..32 (high scales) the four terms of q1..q4 at x[n+l], x[n+l+32],
+// x[n+l+64], x[n+l+96], each (c * q) * x, added to one f32 sum that starts at 0.
+float or_q6_k_dot(const uint8_t* blk, const int8_t* x, const float* xs8) {
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    const int8_t* scales = (const int8_t*)(blk + 192);
+    const float d = or_f16_to_f32(load_u16(blk + 208));
+    float weight_scales[16];
+    for (int i = 0; i < 16; i++) weight_scales[i] = d * (float)scales[i];
+    float sum = 0.0f;
+    int ql_off = 0, qh_off = 0, sc_off = 0;
+    for (int n = 0; n < 256; n += 128) {
+        const int xo = n / 32;
+        const float c_low[4] = {weight_scales[sc_off] * xs8[xo], weight_scales[sc_off + 2] * xs8[xo + 1],
+                                weight_scales[sc_off + 4] * xs8[xo + 2], weight_scales[sc_off + 6] * xs8[xo + 3]};
+        const float c_high[4] = {weight_scales[sc_off + 1] * xs8[xo], weight_scales[sc_off + 3] * xs8[xo + 1],
+                                 weight_scales[sc_off + 5] * xs8[xo + 2], weight_scales[sc_off + 7] * xs8[xo + 3]};
+        for (int l = 0; l < 32; l++) {
+            const float* c = l < 16 ? c_low : c_high;
+            const uint8_t h = qh[qh_off + l];
+            const int q1 = (int8_t)((ql[ql_off + l] & 0x0f) | ((h & 0x03) << 4)) - 32;
+            const int q2 = (int8_t)((ql[ql_off + l + 32] & 0x0f) | (((h >> 2) & 0x03) << 4)) - 32;
+            const int q3 = (int8_t)((ql[ql_off + l] >> 4) | (((h >> 4) & 0x03) << 4)) - 32;
+            const int q4 = (int8_t)((ql[ql_off + l + 32] >> 4) | (((h >> 6) & 0x03) << 4)) - 32;
+            sum += c[0] * (float)q1 * (float)x[n + l];
+            sum += c[1] * (float)q2 * (float)x[n + l + 32];
+            sum += c[2] * (float)q3 * (float)x[n + l + 64];
+            sum += c[3] * (float)q4 * (float)x[n + l + 96];
+        }
+        ql_off += 64;
+        qh_off += 32;
+        sc_off += 8;
+    }
+    return sum;
+}
+
+// inference.rs:1882-2000 matmul_q6_k_batch (portable path): per row and token, the super-block
+// dots added in order to a sum that starts at 0.
+void or_matmul_q6_k(float* out, const int8_t* x, const float* xs, const uint8_t* w, int64_t N, int64_t M, int64_t K,
+                    int nthreads) {
+    const int64_t spr = K / 256;
+    parallel_rows(M, nthreads, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; r++)
+            for (int64_t t = 0; t < N; t++) {
+                float sum = 0.0f;
+                for (int64_t sb = 0; sb < spr; sb++)
+                    sum += or_q6_k_dot(w + (r * spr + sb) * 210, x + t * K + sb * 256, xs + t * (K / 32) + sb * 8);
+                out[t * M + r] = sum;
+            }
     });
 }
 

@@ -46,11 +46,14 @@ def lib():
         "or_q4_k_subblock_ints": (None, [_u8p, _i8p, _i32p, _i32p]),
         "or_q4_k_dot": (C.c_float, [_u8p, _i8p, _f32p]),
         "or_q4_k_dequantize": (None, [_u8p, _f32p]),
+        "or_dequantize_f32": (C.c_int, [C.c_int, _u8p, _i64, _f32p]),
         "or_quantize_q8_0": (None, [_f32p, _i64, _i8p, _f32p]),
         "or_quantize_q4_0_tied": (None, [_f32p, _i64, _i64, _u8p]),
         "or_matmul_q4_0": (None, [_f32p, _i8p, _f32p, _u8p, _i64, _i64, _i64, C.c_int]),
         "or_matmul_q4_0_blockdots": (None, [_i32p, _i8p, _u8p, _i64, _i64, _i64, C.c_int]),
         "or_matmul_q4_k": (None, [_f32p, _i8p, _f32p, _u8p, _i64, _i64, _i64, C.c_int]),
+        "or_matmul_q6_k": (None, [_f32p, _i8p, _f32p, _u8p, _i64, _i64, _i64, C.c_int]),
+        "or_q6_k_dot": (C.c_float, [_u8p, _i8p, _f32p]),
         "or_rms_norm": (None, [_f32p, _f32p, _f32p, _i64, C.c_float]),
         "or_rope": (None, [_f32p, _i64, _i64, _i64, _i64, C.c_float, C.c_int]),
         "or_rope_sincos": (None, [_i64, _i64, _i64, C.c_float, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
@@ -154,6 +157,18 @@ def matmul_q4_k(x_i8, x_scales, w_blocks, N, M, K, nthreads=8):
     return out.reshape(N, M)
 
 
+def matmul_q6_k(x_i8, x_scales, w_blocks, N, M, K, nthreads=8):
+    out = np.zeros(N * M, np.float32)
+    lib().or_matmul_q6_k(out, _c(x_i8, np.int8).ravel(), _c(x_scales, np.float32).ravel(),
+                         _c(w_blocks, np.uint8).ravel(), N, M, K, nthreads)
+    return out.reshape(N, M)
+
+
+def q6_k_dot(block210, x256, xs8) -> float:
+    return float(lib().or_q6_k_dot(_c(block210, np.uint8).ravel(), _c(x256, np.int8).ravel(),
+                                   _c(xs8, np.float32).ravel()))
+
+
 def q4_k_subblock_ints(block144, x256):
     W = np.zeros(8, np.int32)
     A = np.zeros(8, np.int32)
@@ -164,6 +179,14 @@ def q4_k_subblock_ints(block144, x256):
 def q4_k_dequantize(block144):
     out = np.zeros(256, np.float32)
     lib().or_q4_k_dequantize(_c(block144, np.uint8), out)
+    return out
+
+
+def dequantize_f32(ggml_type, data, n):
+    """load_f32_or_f16 (model.rs:1081-1229): n values of one tensor's bytes as f32."""
+    out = np.zeros(n, np.float32)
+    if lib().or_dequantize_f32(int(ggml_type), _c(data, np.uint8).ravel(), n, out) != 0:
+        raise ValueError(f"unsupported GGML type {ggml_type}")
     return out
 
 

@@ -122,6 +122,22 @@ def test_q4_0_prompt_matmul(ctx, M, K, Ns):
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), N
 
 
+@pytest.mark.parametrize("M,K", [(4096, 4096), (1000, 8192), (777, 3072)])
+def test_q6_k_matmul(ctx, M, K):
+    """Q6_K output projections (matmul_q6_k_batch, inference.rs:1882-2000, per-element f32 chain
+    in Q6KBlock::dot_q8_scaled order): every output bit-identical to the oracle at 1..16 tokens,
+    including a shape whose 12 super-blocks per row leave idle lanes."""
+    import nanocamelid_amd as nc
+    from tests.gguf_writer import random_blocks
+    w = random_blocks(nc.NC_TYPE_Q6_K, M * K // 256, seed=M + K)
+    q = nc.QMat(ctx, nc.NC_TYPE_Q6_K, M, K, w.reshape(M, K // 256, 210))
+    for N in (1, 3, 5, 9, 16, 21):
+        x, xq, xs = q8_activations(N, K, seed=N + K)
+        out = nc.matmul_quantized_batch(ctx, q, torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda()).cpu().numpy()
+        ref = O.matmul_q6_k(xq, xs, w, N, M, K, nthreads=16)
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), N
+
+
 def test_q4_k_matmul_above_16_tokens(ctx):
     """Q4_K matrices take 16-token slices of the verify kernel beyond 16 tokens."""
     import nanocamelid_amd as nc

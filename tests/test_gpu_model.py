@@ -324,6 +324,70 @@ def test_prompt_passes_match_oracle(ctx, hd):
         assert _same(gs.logits(i), ologits[i]), i
 
 
+@pytest.mark.parametrize("ty", [1, 30, 8, 3, 6, 13, 14])
+def test_embedding_types_model_logits(ctx, ty):
+    """Token embeddings stored as F16, BF16, Q8_0, Q4_1, Q5_0, Q5_K or Q6_K (load_f32_or_f16,
+    model.rs:1081-1229) load through the memory-mapped file path and give logits bit-identical
+    to the oracle's, which decodes them independently."""
+    import os
+    import tempfile
+    import nanocamelid_amd as nc
+    from tests import gguf_writer as GW
+    meta, ts = GW.read(nc.synth_gguf(**TINY, seed=50 + ty).tobytes())
+    d, V = TINY["embedding_length"], TINY["vocab_size"]
+    raw = GW.random_blocks(ty, d * V // GW.LAYOUT[ty][0], seed=ty).tobytes()
+    ts = [("token_embd.weight", [d, V], ty, raw) if t[0] == "token_embd.weight" else t for t in ts]
+    img = GW.write(meta, ts)
+    with tempfile.NamedTemporaryFile(suffix=".gguf", delete=False) as f:
+        f.write(img)
+    try:
+        gm = nc.Model(ctx, path=f.name)
+    finally:
+        os.unlink(f.name)
+    om = O.Model(data=img)
+    gs, os_ = nc.Session(gm, 64, 16), O.Session(om, 64, 16)
+    toks = nc.uniform_prompt(ty, 12, V)
+    _, _, _, preds = gs.verify_greedy(toks, 0)
+    opreds, _, ologits = os_.verify_greedy(toks, 0, want_logits=True)
+    assert np.array_equal(preds, opreds)
+    for i in range(12):
+        assert _same(gs.logits(i), ologits[i]), i
+
+
+def test_q6_k_head_model_logits(ctx):
+    """An untied Q6_K output.weight (llama.cpp keeps the head in Q6_K in its Q4_0 and Q4_K_M
+    files): verify logits and greedy predictions bit-identical to the oracle at several widths."""
+    import nanocamelid_amd as nc
+    from tests import gguf_writer as GW
+    meta, ts = GW.read(nc.synth_gguf(**TINY, seed=61).tobytes())
+    d, V = TINY["embedding_length"], TINY["vocab_size"]
+    raw = GW.random_blocks(nc.NC_TYPE_Q6_K, d * V // 256, seed=61).tobytes()
+    ts = [("output.weight", [d, V], nc.NC_TYPE_Q6_K, raw) if t[0] == "output.weight" else t for t in ts]
+    img = GW.write(meta, ts)
+    gm, om = nc.Model(ctx, data=np.frombuffer(img, np.uint8)), O.Model(data=img)
+    gs, os_ = nc.Session(gm, 128, 16), O.Session(om, 128, 16)
+    pos = 0
+    for n in (1, 5, 16, 9):
+        batch = nc.uniform_prompt(300 + n, n, V)
+        _, _, _, preds = gs.verify_greedy(batch, pos)
+        opreds, _, ologits = os_.verify_greedy(batch, pos, want_logits=True)
+        assert np.array_equal(preds, opreds), n
+        for i in range(n):
+            assert _same(gs.logits(i), ologits[i]), (n, i)
+        pos += n
+
+
+def test_loader_refuses_output_major_matrix(ctx):
+    import nanocamelid_amd as nc
+    from tests import gguf_writer as GW
+    meta, ts = GW.read(nc.synth_gguf(**TINY, seed=5).tobytes())
+    # attn_k is [d, kv_width] = [256, 128]: stored output-major it reads [128, 256]
+    ts = [(n, [dims[1], dims[0]], ty, raw) if n == "blk.0.attn_k.weight" else (n, dims, ty, raw)
+          for n, dims, ty, raw in ts]
+    with pytest.raises(nc.NcError, match="transposed"):
+        nc.Model(ctx, data=np.frombuffer(GW.write(meta, ts), np.uint8))
+
+
 def test_long_context_many_units(ctx):
     """Long rows with more (row, head) units than CUs (9 rows x 32 heads = 288) take the
     256-thread softmax tiers and the software-pipelined weighted-V loop: 9-row verify logits

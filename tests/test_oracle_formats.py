@@ -331,3 +331,69 @@ def test_quantize_q4_0_tied_closed_form():
     nib = [O.dot_q4_0_q8_0(blk, _unit(j)) + 8 for j in range(32)]
     assert nib[0] == 0  # x = -1 -> -1 * (1/0.125) + 8.5 = 0.5 -> 0
     assert max(nib) <= 15 and min(nib) >= 0
+
+
+def q6_k_block(scale_bits, seed):
+    """inference.rs:5589-5603 q6_k_block fixture."""
+    ql = [(seed + i * 5) % 256 for i in range(128)]
+    qh = [(seed + i * 7) % 256 for i in range(64)]
+    sc = [((seed + i * 3) % 15) - 7 for i in range(16)]
+    return np.array(ql + qh + [s & 0xFF for s in sc] + [scale_bits & 0xFF, scale_bits >> 8], np.uint8)
+
+
+def test_matmul_q6_k_matches_dequantized_reference():
+    # inference.rs:6605-6640 (rows 2, cols 512, tolerance 1e-4); the dequantised values come from
+    # the oracle's load_f32_or_f16 restatement, itself pinned by the reference's Q6_K known answers
+    rows, cols = 2, 512
+    x = np.array([((i * 5) % 61) - 30 for i in range(cols)], np.int8)
+    xs = np.array([0.125 + i * 0.03125 for i in range(cols // 32)], np.float32)
+    w = np.concatenate([q6_k_block(0x3800, 1), q6_k_block(0x3C00, 2), q6_k_block(0x4000, 3), q6_k_block(0x4200, 4)])
+    got = O.matmul_q6_k(x, xs, w, 1, rows, cols)[0]
+    for r in range(rows):
+        s = np.float32(0)
+        for b in range(2):
+            vals = O.dequantize_f32(14, w[(r * 2 + b) * 210:(r * 2 + b + 1) * 210], 256)
+            for i in range(256):
+                xi = b * 256 + i
+                s = np.float32(s + np.float32(np.float32(vals[i] * np.float32(x[xi])) * xs[xi // 32]))
+        assert abs(got[r] - s) < 1e-4
+
+
+def test_q6_k_dot_float64_and_term_order():
+    # the dot against a float64 evaluation of sum(d * sc * q * x * xs) over the block, and the
+    # reference's term order: one term moved to the front of the chain changes nothing only if
+    # the chain is the same multiset -- so check that the f32 result equals a float32 left-to-right
+    # sum in the order (half, l, k), and differs in general from the order (half, k, l)
+    rng = np.random.default_rng(14)
+    blk = q6_k_block(0x2E66, 9)
+    x = rng.integers(-127, 128, 256).astype(np.int8)
+    xs = rng.uniform(0.01, 0.05, 8).astype(np.float32)
+    got = O.q6_k_dot(blk, x, xs)
+    vals = O.dequantize_f32(14, blk, 256).astype(np.float64)
+    exact = float(np.sum(vals * x.astype(np.float64) * np.repeat(xs.astype(np.float64), 32)))
+    assert abs(got - exact) <= 1e-5 * max(1.0, abs(exact))
+    d = np.float32(O.f16_to_f32(0x2E66))
+    sc = blk[192:208].view(np.int8)
+    ql, qh = blk[:128].astype(int), blk[128:192].astype(int)
+
+    def chain(order):
+        s = np.float32(0)
+        for half, l, k in order:
+            lo, hi, hb = ql[64 * half + l], ql[64 * half + l + 32], qh[32 * half + l]
+            q = [(lo & 15) | ((hb & 3) << 4), (hi & 15) | (((hb >> 2) & 3) << 4),
+                 (lo >> 4) | (((hb >> 4) & 3) << 4), (hi >> 4) | (((hb >> 6) & 3) << 4)][k] - 32
+            g = 8 * half + 2 * k + (l >= 16)
+            c = np.float32(np.float32(d * np.float32(sc[g])) * xs[4 * half + k])
+            s = np.float32(s + np.float32(np.float32(c * np.float32(q)) * np.float32(x[128 * half + 32 * k + l])))
+        return s
+
+    ref_order = [(h, l, k) for h in range(2) for l in range(32) for k in range(4)]
+    assert np.float32(got) == chain(ref_order)
+    # the check is order-sensitive: the (half, k, l) order rounds differently for some inputs
+    other = [(h, l, k) for h in range(2) for k in range(4) for l in range(32)]
+    differs = False
+    for seed in range(20):
+        x = np.random.default_rng(seed).integers(-127, 128, 256).astype(np.int8)
+        assert np.float32(O.q6_k_dot(blk, x, xs)) == chain(ref_order)
+        differs |= bool(chain(other) != chain(ref_order))
+    assert differs
