@@ -342,9 +342,12 @@ __global__ __launch_bounds__(512) void attn_scores_kernel(AttnParams a) {
 // the sum of e left to right (exact_chain_sum), p = e * (1 / sum).  Thread t returns the
 // probabilities of positions t*E .. t*E + E - 1 (0 past L).  Every thread of the block calls
 // it; lds_terms: T*E floats used by the chain.
-template <int E, int T>
+// X = 1: the row continues for up to T more positions, thread t holding position T*E + t; its
+// e joins the chain after the first T*E terms (exact_chain_sum from the carried sum, with
+// lds_terms + T*E as its T floats of scratch) and its probability is returned in *px.
+template <int E, int T, int X = 0>
 __device__ __forceinline__ void softmax_row(const float* srow, int L, float (&pr)[E], ChainScratch<T>& sc,
-                                            float* lds_terms, float* red) {
+                                            float* lds_terms, float* red, float* px = nullptr) {
     const int t = threadIdx.x;
     float sv[E];
 #pragma unroll
@@ -352,9 +355,12 @@ __device__ __forceinline__ void softmax_row(const float* srow, int L, float (&pr
         const int p = t * E + j;
         sv[j] = p < L ? srow[p] : -__builtin_inff();
     }
+    const int px_pos = T * E + t;
+    const float svx = X && px_pos < L ? srow[px_pos] : -__builtin_inff();
     float mx = sv[0];
 #pragma unroll
     for (int j = 1; j < E; j++) mx = sv[j] > mx ? sv[j] : mx;
+    if (X) mx = svx > mx ? svx : mx;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         const float o = __shfl_xor(mx, off, 64);
@@ -368,10 +374,16 @@ __device__ __forceinline__ void softmax_row(const float* srow, int L, float (&pr
     float e[E];
 #pragma unroll
     for (int j = 0; j < E; j++) e[j] = t * E + j < L ? expf_glibc(sv[j] - mx) : 0.0f;
-    const float sum = exact_chain_sum<E, T>(e, sc, lds_terms);
+    float sum = exact_chain_sum<E, T>(e, sc, lds_terms);
+    float ex[1] = {0.0f};
+    if constexpr (X) {
+        ex[0] = px_pos < L ? expf_glibc(svx - mx) : 0.0f;
+        sum = exact_chain_sum<1, T>(ex, sc, lds_terms + T * E, sum);
+    }
     const float inv = 1.0f / sum;
 #pragma unroll
     for (int j = 0; j < E; j++) pr[j] = e[j] * inv;
+    if constexpr (X) *px = ex[0] * inv;
 }
 
 // The weighted V sum of unit (n, h) over positions 0..L-1 (probabilities in LDS) and the
@@ -513,10 +525,10 @@ __device__ __forceinline__ void weighted_v_q8(const AttnParams& a, int n, int h,
                    a.xs8 + (size_t)n * (aw / 32) + col / 32);
 }
 
-template <int E, int T, int HD, bool PIPE>
+template <int E, int T, int HD, bool PIPE, int X = 0>
 __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
     __shared__ ChainScratch<T> sc;
-    __shared__ __align__(16) float probs[T * E];
+    __shared__ __align__(16) float probs[T * E + X * T];
     __shared__ float red[T / 64];
     // unit order: KV head fastest, so that with round-robin dispatch over the 8 XCDs (and 8
     // KV heads) every unit of a KV head lands on one XCD and its keys and values stay in that
@@ -527,10 +539,11 @@ __global__ __launch_bounds__(T) void attn_softmax_pv_kernel(AttnParams a) {
     const int L = a.d_pos[0] + n + 1;
     const int t = threadIdx.x;
     const float* srow = a.scores + ((size_t)n * a.H + h) * a.max_ctx;
-    float pr[E];
-    softmax_row<E, T>(srow, L, pr, sc, probs, red);
+    float pr[E], px = 0.0f;
+    softmax_row<E, T, X>(srow, L, pr, sc, probs, red, &px);
 #pragma unroll
     for (int j = 0; j < E; j++) probs[t * E + j] = pr[j];
+    if (X) probs[T * E + t] = px;
     __syncthreads();
     weighted_v_q8<HD, PIPE>(a, n, h, kvh, L, probs);  // no barriers below
 }
@@ -672,7 +685,13 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
     if (a.hd == 128) hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 128, PIPE>), grid, dim3(T), 0, st, a); \
     else hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 64, PIPE>), grid, dim3(T), 0, st, a);
     if (len > 16384) return fail(NC_ERANGE, "attention: context longer than 16384 positions");
-    if (a.N * a.H <= 256 || len > 8192) {
+    if (a.N * a.H > 256 && len > 8192 && len <= 8192 + 256) {
+        // more units than CUs on rows just past 8192 positions (a verify over an 8192-position
+        // cache): the 256-thread tier with one extra position per thread (70B shape, 9 rows x
+        // 64 heads at 8201 positions)
+        if (a.hd == 128) hipLaunchKernelGGL((attn_softmax_pv_kernel<32, 256, 128, true, 1>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((attn_softmax_pv_kernel<32, 256, 64, true, 1>), grid, dim3(256), 0, st, a);
+    } else if (a.N * a.H <= 256 || len > 8192) {
         // at most one unit per CU: 512 threads, two waves per SIMD through the max, exp and sum
         // phases (a wave issues one VALU instruction per 8 cycles at most; 2000 positions 27.2
         // -> 26.4 us, 8000 84.2 -> 78.4 us for one row), and the plain weighted-V loop

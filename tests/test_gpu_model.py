@@ -414,6 +414,29 @@ def test_long_context_many_units(ctx):
         pos = c
 
 
+def test_long_context_many_units_past_8192(ctx):
+    """9 rows x 32 heads (288 units) at 8193..8201 positions take the 256-thread tier with one
+    extra position per thread (its e joins the exact chain after the first 8192): every verify
+    row's logits equal single-row passes at the same positions, which take the 512-thread tier
+    that the oracle pins at 8190 positions (test_long_context_logits)."""
+    import nanocamelid_amd as nc
+    spec = dict(layers=1, embedding_length=32 * 64, head_count=32, head_count_kv=8, feed_forward_length=512,
+                vocab_size=1000, context_length=8192 + 64, tied=1, norm_mode=1)
+    img = nc.synth_gguf(**spec, seed=8201)
+    gm = nc.Model(ctx, data=img)
+    prompt = nc.uniform_prompt(8201, 8192, 1000)
+    sess = nc.Session(gm, 8192 + 32, 16)
+    sess.prefill_pass_batch(prompt, 0, want_logits=False)
+    batch = nc.uniform_prompt(9, 9, 1000)
+    single = []
+    for i in range(9):
+        _, lg = sess.forward_pass(int(batch[i]), 8192 + i)
+        single.append(lg)
+    sess.verify_greedy(batch, 8192)
+    for i in range(9):
+        assert _same(sess.logits(i), single[i]), i
+
+
 @pytest.mark.slow
 def test_config0_plumbing_run(ctx):
     """Config 0: Llama-3.2-1B shape, tied Q4_0 head, 32-token seeded prompt, greedy, k=4,
