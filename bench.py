@@ -29,6 +29,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA
 # Host threads: the box's CPU share for one GPU is 16 cores, whatever nproc reports there.
 HOST_THREADS = min(16, len(os.sched_getaffinity(0)))
 REFERENCE_DEFAULT_THREADS = 4  # the reference's default worker count (src/main.rs:64, :549-551)
@@ -170,6 +171,71 @@ def run_gemm_sweep(args):
         print(json.dumps(res), flush=True)
         for m in mats:
             m.close()
+
+
+def run_prefill(args):
+    """Prompt prefill (the reference's prefill_tokens, main.rs:9415-9485): (1) the prompt matmul
+    alone on the 8B and 70B shapes at 64 and 256 tokens, median of dispatch-stamped events,
+    against the int8 MFMA peak; (2) wall time of an 8B-shape prefill of 512, 2048 and 8192
+    tokens in prompt passes, beside the same prompt in 16-token verify-sized passes, whose
+    last-row logits must be the same bits."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    import nanocamelid_amd as nc
+    ctx = nc.Context(0)
+    shapes = [(6144, 4096, "8b q,k,v"), (4096, 4096, "8b wo"), (28672, 4096, "8b gate,up"),
+              (4096, 14336, "8b down"), (57344, 8192, "70b gate,up"), (8192, 28672, "70b down")]
+    for M, K, name in (shapes if not args.prefill_tokens else []):
+        q = nc.QMat(ctx, nc.NC_TYPE_Q4_0, M, K, _q4_0_random_blocks(M, K, M + K))
+        handles = (C.c_void_p * 1)(q.h)
+        res = {"shape": f"{M}x{K}", "role": name}
+        for N in (64, 256):
+            rng = np.random.default_rng(N)
+            xq = torch.from_numpy(rng.integers(-127, 128, (N, K), dtype=np.int8)).cuda()
+            xs = torch.from_numpy(rng.uniform(0.005, 0.02, (N, K // 32)).astype(np.float32)).cuda()
+            out = torch.empty((N, M), dtype=torch.float32, device="cuda")
+            us = np.zeros(23, np.float32)
+            nc.check(nc.lib().nc_bench_matmul(ctx.h, handles, 1, xq.data_ptr(), xs.data_ptr(), out.data_ptr(), N,
+                                              len(us), us.ctypes.data))
+            med = float(np.median(us[3:]))
+            tops = 2.0 * M * K * N / med / 1e6
+            res[f"N{N}"] = {"us_median": round(med, 1), "int8_TOPs": round(tops, 1),
+                            "frac_int8_mfma_peak": round(tops / PEAK_INT8_TOPS, 4)}
+        q.close()
+        print(json.dumps(res), flush=True)
+    t0 = time.time()
+    img = nc.synth_gguf(**nc.SYNTH_CONFIGS["llama-3-8b"], context_length=8192 + 64, seed=args.seed,
+                        nthreads=HOST_THREADS)
+    model = nc.Model(ctx, data=img, nthreads=HOST_THREADS)
+    del img
+    log(f"llama-3-8b-shape model on device in {time.time() - t0:.1f}s")
+    prompt = nc.uniform_prompt(args.seed, 8192, model.config["vocab_size"])
+    for n in ((args.prefill_tokens,) if args.prefill_tokens else (512, 2048, 8192)):
+        s = nc.Session(model, 8192 + 64, 16)
+        s.prefill_pass_batch(prompt[:64], 0, want_logits=False)  # the prompt buffers, allocated once
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        s.prefill_pass_batch(prompt[:n], 0)
+        torch.cuda.synchronize()
+        tp = time.perf_counter() - t
+        res = {"prefill_tokens": n, "prompt_passes_ms": round(tp * 1e3, 1), "prompt_passes_tok_s": round(n / tp)}
+        if n <= 2048 and not args.prefill_tokens:
+            s2 = nc.Session(model, 8192 + 64, 16)
+            t = time.perf_counter()
+            for i in range(0, n, 16):
+                s2.prefill_pass_batch(prompt[i:i + 16], i, want_logits=(i + 16 >= n))
+            torch.cuda.synchronize()
+            t16 = time.perf_counter() - t
+            res["16_token_passes_ms"] = round(t16 * 1e3, 1)
+            res["16_token_passes_tok_s"] = round(n / t16)
+            res["last_logits_bit_equal"] = bool(np.array_equal(s.logits(15).view(np.uint32),
+                                                               s2.logits(15).view(np.uint32)))
+            s2.close()
+        s.close()
+        print(json.dumps(res), flush=True)
 
 
 def run_config3(args):
@@ -349,6 +415,10 @@ def main():
                     help="config 3: 3B Q4_K target + 1B Q4_0 draft, stochastic acceptance (T=1, k=4)")
     ap.add_argument("--config4", action="store_true",
                     help="config 4: 70B Q4_0, one 9-row verify pass over an 8192-position KV cache")
+    ap.add_argument("--prefill", action="store_true",
+                    help="prompt prefill: prompt matmul at 64/256 tokens and 8B-shape prefill wall times")
+    ap.add_argument("--prefill-tokens", type=int, default=0,
+                    help="with --prefill: only one prefill of this many tokens (for a kernel profile)")
     ap.add_argument("--c4-passes", type=int, default=10)
     ap.add_argument("--c3-prompt", type=int, default=3072)
     ap.add_argument("--c3-new", type=int, default=768)
@@ -374,6 +444,9 @@ def main():
         return
     if args.config4:
         run_config4(args)
+        return
+    if args.prefill:
+        run_prefill(args)
         return
     spec = dict(nc.SYNTH_CONFIGS[args.config])
     t0 = time.time()

@@ -92,14 +92,17 @@ int64_t nc_qmat_device_bytes(const nc_qmat* w);
  * x_i8 [batch][cols] int8, x_scales [batch][cols/32] f32, out [batch][rows] f32
  * (token-major, as write_batch_out src/inference.rs:1333-1341).  batch_size >= 1, no upper
  * limit (matmul_quantized_batch takes any batch): up to 16 tokens run on the verify kernels;
- * more run on the int8 MFMA prompt matmul (Q4_0) or as 16-token slices (Q4_K).
+ * more run on the int8 MFMA prompt matmul (Q4_0; slices of up to 256 tokens through buffers
+ * that nc_ctx_create allocates, 18 MiB) or as 16-token slices (Q4_K, Q6_K).  Calls that share
+ * a context and overlap on different streams race on those buffers.
  * stream: a hipStream_t or NULL for the context's default stream. */
 int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, const float* x_scales,
                               float* out, int batch_size, int64_t rows, int64_t cols, void* stream);
 /* Allocation-free variant of nc_matmul_quantized_batch (no reference counterpart: it is for
  * callers that cannot allocate device memory, such as code under HIP graph capture or serving
  * loops that forbid hipMalloc).  Same arguments, semantics and results; its only scratch is a
- * static per-device array sized for batch_size * cols <= 16 * 65536 (larger: NC_ERANGE).  It
+ * static per-device array sized for batch_size * cols <= 16 * 65536 (larger: NC_ERANGE;
+ * batch_size above 16: NC_EINVAL).  It
  * calls no hipMalloc/hipFree.  Calls that overlap on one device share that array and race. */
 int nc_matmul_quantized_batch_noalloc(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, const float* x_scales,
                                       float* out, int batch_size, int64_t rows, int64_t cols, void* stream);

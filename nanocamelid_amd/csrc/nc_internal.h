@@ -201,6 +201,10 @@ struct nc_ctx {
     size_t xsum_cap = 0;
     float* tp_scratch = nullptr;  // temperature softmax partials
     size_t tp_cap = 0;
+    // activations of the prompt matmul (more than 16 tokens) repacked in MFMA operand order,
+    // for kPromptRows tokens of 65536 columns per slice; allocated by nc_ctx_create
+    int8_t* pxm = nullptr;
+    float* pxsm = nullptr;
     // device address of the static scratch array on this context's device (never freed)
     int32_t* static_scratch = nullptr;
     int gemm_kernel = NC_GEMM_KERNEL_AUTO;  // dot-product path of the quantized matmuls

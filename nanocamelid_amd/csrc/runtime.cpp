@@ -1041,6 +1041,8 @@ int nc_ctx_create(int device, nc_ctx** out) {
         c->tp_cap = temperature_scratch_floats(16);
         e = hipMalloc((void**)&c->tp_scratch, c->tp_cap * sizeof(float));
     }
+    if (e == hipSuccess) e = hipMalloc((void**)&c->pxm, kPromptRows * kCtxScratchCols);
+    if (e == hipSuccess) e = hipMalloc((void**)&c->pxsm, kPromptRows * (kCtxScratchCols / 128 + 1) * 4 * sizeof(float));
     if (e != hipSuccess) {
         nc_ctx_free(c);
         return fail(NC_EHIP, std::string("nc_ctx_create: ") + hipGetErrorString(e));
@@ -1054,6 +1056,8 @@ void nc_ctx_free(nc_ctx* c) {
     (void)hipSetDevice(c->device);
     if (c->xsum) (void)hipFree(c->xsum);
     if (c->tp_scratch) (void)hipFree(c->tp_scratch);
+    if (c->pxm) (void)hipFree(c->pxm);
+    if (c->pxsm) (void)hipFree(c->pxsm);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -1107,6 +1111,28 @@ static int ensure_xsum(nc_ctx* ctx, size_t count) {
     return NC_OK;
 }
 
+// Tokens per slice of the operator-level prompt matmul: the context's repack buffers hold
+// kPromptRows tokens of kCtxScratchCols columns (0: columns too wide for a 16-token slice).
+static int prompt_slice_tokens(int64_t cols) {
+    return (int)std::min<int64_t>(kPromptRows, (int64_t)kPromptRows * (int64_t)kCtxScratchCols / cols / 16 * 16);
+}
+
+// The Q4_0 prompt matmul of batch_size > 16 tokens through the context's repack buffers, in
+// slices of prompt_slice_tokens (every token's outputs are the same bits in any slicing).
+static int ctx_prompt_matmul(nc_ctx* ctx, const QMatDev& w, const int8_t* x, const float* xs, float* out, int n,
+                             hipStream_t st) {
+    const int cols = (int)w.cols, T = prompt_slice_tokens(cols);
+    for (int i = 0; i < n; i += T) {
+        const int len = std::min(T, n - i);
+        const int8_t* xi = x + (size_t)i * cols;
+        const float* xsi = xs + (size_t)i * (cols / 32);
+        int rc = launch_prompt_repack(xi, xsi, len, cols, ctx->pxm, ctx->pxsm, st);
+        if (rc || (rc = launch_gemm_prompt(w, xi, xsi, out + (size_t)i * w.rows, (int)w.rows, len, st, ctx->pxm, ctx->pxsm)))
+            return rc;
+    }
+    return NC_OK;
+}
+
 int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, const float* x_scales, float* out,
                               int batch_size, int64_t rows, int64_t cols, void* stream) {
     if (!ctx || !w || !x_i8 || !x_scales || !out) return fail(NC_EINVAL, "nc_matmul_quantized_batch: null argument");
@@ -1115,8 +1141,8 @@ int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8,
     NC_HIP(hipSetDevice(ctx->device));
     hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
     // more than 16 tokens: the MFMA prompt matmul (Q4_0), or 16-token slices (Q4_K)
-    if (batch_size > 16 && w->m.type == NC_TYPE_Q4_0)
-        return launch_gemm_prompt(w->m, x_i8, x_scales, out, (int)rows, batch_size, st);
+    if (batch_size > 16 && w->m.type == NC_TYPE_Q4_0 && prompt_slice_tokens(cols) >= 16)
+        return ctx_prompt_matmul(ctx, w->m, x_i8, x_scales, out, batch_size, st);
     for (int i = 0; i < batch_size; i += 16) {
         const int nb = std::min(16, batch_size - i);
         int rc = ensure_xsum(ctx, (size_t)nb * (cols / 32));
@@ -1144,8 +1170,8 @@ int nc_bench_matmul(nc_ctx* ctx, const nc_qmat* const* w, int32_t ncopies, const
     for (int i = 0; i < ncopies; i++)
         if (!w[i] || w[i]->m.rows != w[0]->m.rows || w[i]->m.cols != w[0]->m.cols)
             return fail(NC_EINVAL, "nc_bench_matmul: weight copies differ in shape");
-    if (batch_size > 16 && w[0]->m.type != NC_TYPE_Q4_0)
-        return fail(NC_EINVAL, "nc_bench_matmul: more than 16 tokens only for Q4_0 matrices");
+    if (batch_size > 16 && (w[0]->m.type != NC_TYPE_Q4_0 || prompt_slice_tokens(w[0]->m.cols) < 16))
+        return fail(NC_EINVAL, "nc_bench_matmul: more than 16 tokens only for Q4_0 matrices of <= 1M columns");
     NC_HIP(hipSetDevice(ctx->device));
     hipStream_t st = ctx->stream;
     const int64_t cols = w[0]->m.cols, rows = w[0]->m.rows;
@@ -1169,7 +1195,7 @@ int nc_bench_matmul(nc_ctx* ctx, const nc_qmat* const* w, int32_t ncopies, const
         if (batch_size <= 16) {
             rc = launch_gemm(w[i % ncopies]->m, p, st, ev[2 * i], ev[2 * i + 1]);
         } else if (hipEventRecord(ev[2 * i], st) != hipSuccess ||
-                   (rc = launch_gemm_prompt(w[i % ncopies]->m, x_i8, x_scales, out, (int)rows, batch_size, st)) ||
+                   (rc = ctx_prompt_matmul(ctx, w[i % ncopies]->m, x_i8, x_scales, out, batch_size, st)) ||
                    hipEventRecord(ev[2 * i + 1], st) != hipSuccess) {
             if (!rc) rc = fail(NC_EHIP, "nc_bench_matmul: event record");
         }

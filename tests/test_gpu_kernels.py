@@ -110,7 +110,8 @@ def test_q4_0_prompt_matmul(ctx, M, K, Ns):
     """More than 16 tokens take the MFMA prompt matmul (inference.rs:1385-1418 for any batch):
     every output bit-identical to the oracle.  Covers 16-row tiles (R16) with 4096 and 3 blocks
     per row (a partial quad) and rows not a multiple of 64, 64-row tiles (R64, >= 512 tiles) with
-    a partial last tile, token counts that leave partial 16- and 64-token tiles."""
+    a partial last tile, token counts that leave partial 16- and 64-token tiles, and 300 tokens
+    (two slices through the context's 256-token repack buffers)."""
     import nanocamelid_amd as nc
     w = random_q4_0(M, K, seed=M + 7 * K)
     q = nc.QMat(ctx, nc.NC_TYPE_Q4_0, M, K, w)
