@@ -111,6 +111,11 @@ int nc_matmul_quantized_batch_noalloc(nc_ctx* ctx, const nc_qmat* w, const int8_
  * q8.rs:1339-1376) as dots[t][r][cols/32] (device pointer). */
 int nc_matmul_blockdots(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, int32_t* dots, int batch_size,
                         int64_t rows, int64_t cols, void* stream);
+/* Debug/parity hook: out[i] = the device's exp of the float with bits first_bits + i, for
+ * 0 <= i < count (device pointer; count <= 2^32).  The device restates glibc's expf, which is
+ * what the reference's f32::exp calls in softmax (src/inference.rs:3522-3540) and SiLU
+ * (src/inference.rs:3367-3390); this entry point lets a test compare the two on every input. */
+int nc_debug_expf(nc_ctx* ctx, uint32_t first_bits, int64_t count, float* out, void* stream);
 /* Per-32-block Q8_0 activation quantiser: scale = amax/127 (f32), q = round-half-away
  * (x * (1/scale)) clamped to +-127.  Replaces quantize_f32_to_q8_0_batch
  * (src/inference.rs:967-989, scalar path :991-1029).  Device pointers. */

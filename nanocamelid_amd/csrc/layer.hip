@@ -202,6 +202,22 @@ __global__ void quantize_q8_kernel(const float* x, int dim, int nblocks_total, i
     store_q8_block(y, lane32, xq + (size_t)gb * 32, xs + gb, xsum + gb);
 }
 
+// expf_glibc over consecutive input bit patterns first, first + 1, ... (a parity check of the
+// device restatement against the host's glibc expf, which Rust's f32::exp calls)
+__global__ void expf_range_kernel(uint32_t first, int64_t count, float* out) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = expf_glibc(__uint_as_float(first + (uint32_t)i));
+}
+
+int launch_expf_range(uint32_t first, int64_t count, float* out, hipStream_t st) {
+    if (count < 0 || count > ((int64_t)1 << 32)) return fail(NC_ERANGE, "expf range: 0..2^32 values");
+    if (count == 0) return NC_OK;
+    const int64_t blocks = std::min<int64_t>((count + 255) / 256, 65536);
+    hipLaunchKernelGGL(expf_range_kernel, dim3((unsigned)blocks), dim3(256), 0, st, first, count, out);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
 int launch_quantize_q8(const float* x, int N, int dim, int8_t* xq, float* xs, int32_t* xsum, hipStream_t st) {
     if (dim % 32) return fail(NC_EINVAL, "quantize: width must be a multiple of 32");
     const int total = N * (dim / 32);

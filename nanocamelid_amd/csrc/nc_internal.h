@@ -124,6 +124,7 @@ int launch_rmsnorm_q8(const float* hidden, const float* weight, int N, int d, fl
                       int32_t* xs8, hipStream_t stream);
 // Activation side buffers: xs = per-block f32 scale, xs8 = -8 * per-block int8 sum.
 int launch_quantize_q8(const float* x, int N, int dim, int8_t* xq, float* xs, int32_t* xs8, hipStream_t stream);
+int launch_expf_range(uint32_t first, int64_t count, float* out, hipStream_t stream);
 int launch_block_sums(const int8_t* x, int N, int dim, int32_t* xs8, hipStream_t stream);
 struct TokenArgs {
     uint32_t t[16];

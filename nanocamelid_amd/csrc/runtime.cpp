@@ -1218,6 +1218,12 @@ int nc_matmul_blockdots(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, int32
     return launch_blockdots(w->m, x_i8, dots, batch_size, stream ? (hipStream_t)stream : ctx->stream);
 }
 
+int nc_debug_expf(nc_ctx* ctx, uint32_t first_bits, int64_t count, float* out, void* stream) {
+    if (!ctx || (!out && count > 0)) return fail(NC_EINVAL, "nc_debug_expf: null argument");
+    NC_HIP(hipSetDevice(ctx->device));
+    return launch_expf_range(first_bits, count, out, stream ? (hipStream_t)stream : ctx->stream);
+}
+
 int nc_quantize_q8_0_batch(nc_ctx* ctx, const float* x, int8_t* x_i8, float* x_scales, int batch_size, int64_t dim,
                            void* stream) {
     if (!ctx || !x || !x_i8 || !x_scales || dim % 32) return fail(NC_EINVAL, "nc_quantize_q8_0_batch: bad arguments");

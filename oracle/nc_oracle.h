@@ -87,6 +87,7 @@ void or_rope_scaled(float* data, int64_t pos, int64_t heads, int64_t head_dim, i
                     float freq_base, int style, const float* scaling);
 void or_softmax(float* x, int64_t n);          /* :3522-3540 */
 float or_expf(float x);                        /* Rust f32::exp == glibc expf */
+int64_t or_expf_mismatches(uint32_t first, int64_t count, const float* vals, int nthreads, uint32_t* first_bad);
 void or_silu_mul(float* out, const float* gate, const float* up, int64_t n); /* :3367-3390 */
 int64_t or_argmax(const float* logits, int64_t n); /* :4834-4845 first max wins */
 /* One attention head over an f32 KV slice, inference.rs:4242-4292 (x86 path).

@@ -544,6 +544,38 @@ void or_rope(float* data, int64_t pos, int64_t heads, int64_t head_dim, int64_t 
 
 float or_expf(float x) { return expf(x); }
 
+// Checker for the device restatement of expf: vals[i] against glibc expf of the float with
+// bits first + i, bit for bit (NaN inputs: any NaN).  Returns the mismatch count and the first
+// mismatching input's bits in *first_bad.
+int64_t or_expf_mismatches(uint32_t first, int64_t count, const float* vals, int nthreads, uint32_t* first_bad) {
+    std::vector<int64_t> bad(std::max(1, nthreads), 0);
+    std::vector<int64_t> firsts(bad.size(), -1);
+    parallel_rows(count, nthreads, [&](int64_t lo, int64_t hi) {
+        const size_t slot = (size_t)(lo * (int64_t)bad.size() / std::max<int64_t>(count, 1));
+        for (int64_t i = lo; i < hi; i++) {
+            const uint32_t ub = first + (uint32_t)i;
+            float x;
+            std::memcpy(&x, &ub, 4);
+            const float want = expf(x);
+            uint32_t wb, gb;
+            std::memcpy(&wb, &want, 4);
+            std::memcpy(&gb, &vals[i], 4);
+            const bool ok = std::isnan(x) ? std::isnan(vals[i]) : wb == gb;
+            if (!ok) {
+                if (firsts[slot] < 0) firsts[slot] = i;
+                bad[slot]++;
+            }
+        }
+    });
+    int64_t total = 0, fb = -1;
+    for (size_t k = 0; k < bad.size(); k++) {
+        total += bad[k];
+        if (firsts[k] >= 0 && (fb < 0 || firsts[k] < fb)) fb = firsts[k];
+    }
+    if (first_bad) *first_bad = fb < 0 ? 0 : first + (uint32_t)fb;
+    return total;
+}
+
 // inference.rs:3522-3540 softmax.
 void or_softmax(float* x, int64_t n) {
     float mx = -INFINITY;

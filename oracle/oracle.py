@@ -60,6 +60,7 @@ def lib():
         "or_rope_theta": (C.c_float, [_i64, _i64, C.c_float, C.c_void_p]),
         "or_softmax": (None, [_f32p, _i64]),
         "or_expf": (C.c_float, [C.c_float]),
+        "or_expf_mismatches": (C.c_int64, [C.c_uint32, C.c_int64, C.c_void_p, C.c_int, C.c_void_p]),
         "or_silu_mul": (None, [_f32p, _f32p, _f32p, _i64]),
         "or_argmax": (_i64, [_f32p, _i64]),
         "or_attention_head": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, C.c_float]),
@@ -224,6 +225,15 @@ def softmax(x):
 
 def expf(x: float) -> float:
     return lib().or_expf(x)
+
+
+def expf_mismatches(first: int, vals: np.ndarray, nthreads: int = 16):
+    """(mismatch count, first mismatching input bits) of vals[i] against glibc expf of the float
+    with bits first + i."""
+    vals = np.ascontiguousarray(vals, np.float32)
+    fb = C.c_uint32(0)
+    n = lib().or_expf_mismatches(first, vals.size, vals.ctypes.data, nthreads, C.byref(fb))
+    return int(n), int(fb.value)
 
 
 def silu_mul(g, u):
