@@ -133,6 +133,18 @@ def _q4_0_random_blocks(M, K, seed):
     return blk
 
 
+def _q4_k_random_blocks(M, K, seed):
+    """Random valid Q4_K super-blocks (d, dmin small positive f16; random 6-bit scales and nibbles)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    blk = rng.integers(0, 256, (M, K // 256, 144), dtype=np.uint8)
+    for off, scale in ((0, 0.002), (2, 0.001)):
+        v = (np.abs(rng.normal(0, scale, (M, K // 256))) + 1e-4).astype(np.float16).view(np.uint16)
+        blk[:, :, off] = v & 0xFF
+        blk[:, :, off + 1] = v >> 8
+    return blk
+
+
 def run_gemm_sweep(args):
     """Config 1: per-shape median kernel time (dispatch-stamped events around each of >= 60
     back-to-back launches) rotating >= 1 GB of distinct weight copies."""
@@ -175,7 +187,7 @@ def run_gemm_sweep(args):
 
 def run_prefill(args):
     """Prompt prefill (the reference's prefill_tokens, main.rs:9415-9485): (1) the prompt matmul
-    alone on the 8B and 70B shapes at 64 and 256 tokens, median of dispatch-stamped events,
+    alone on the 8B and 70B Q4_0 and 3B Q4_K shapes at 64 and 256 tokens, median of events,
     against the int8 MFMA peak; (2) wall time of an 8B-shape prefill of 512, 2048 and 8192
     tokens in prompt passes, beside the same prompt in 16-token verify-sized passes, whose
     last-row logits must be the same bits."""
@@ -186,10 +198,12 @@ def run_prefill(args):
 
     import nanocamelid_amd as nc
     ctx = nc.Context(0)
-    shapes = [(6144, 4096, "8b q,k,v"), (4096, 4096, "8b wo"), (28672, 4096, "8b gate,up"),
-              (4096, 14336, "8b down"), (57344, 8192, "70b gate,up"), (8192, 28672, "70b down")]
-    for M, K, name in (shapes if not args.prefill_tokens else []):
-        q = nc.QMat(ctx, nc.NC_TYPE_Q4_0, M, K, _q4_0_random_blocks(M, K, M + K))
+    shapes = [(6144, 4096, "8b q,k,v", 2), (4096, 4096, "8b wo", 2), (28672, 4096, "8b gate,up", 2),
+              (4096, 14336, "8b down", 2), (57344, 8192, "70b gate,up", 2), (8192, 28672, "70b down", 2),
+              (8192, 3072, "3b Q4_K gate", 12), (3072, 8192, "3b Q4_K down", 12)]
+    for M, K, name, ty in (shapes if not args.prefill_tokens else []):
+        blocks = _q4_0_random_blocks(M, K, M + K) if ty == 2 else _q4_k_random_blocks(M, K, M + K)
+        q = nc.QMat(ctx, ty, M, K, blocks)
         handles = (C.c_void_p * 1)(q.h)
         res = {"shape": f"{M}x{K}", "role": name}
         for N in (64, 256):

@@ -148,12 +148,17 @@ int launch_attention(const AttnParams& a, hipStream_t stream);
 
 // ---------------------------------------------------------------- prompt (prefill) path
 // Q4_0 batch matmul for any number of tokens on int8 MFMA: out[n * ld_out + row] (R16 and R64
-// layouts; no scratch, no -8 * block sums needed).
-// xm/xsm (optional): the activations repacked by launch_prompt_repack (xm: 16 * ceil(N/16) * K
-// bytes, xsm: 16 * ceil(N/16) * ceil(K/128) * 4 floats); coalesced operand loads.
+// layouts) over xm / xsm, the activations x / xs repacked by launch_prompt_repack (xm:
+// 16 * ceil(N/16) * K bytes, xsm: 16 * ceil(N/16) * ceil(K/128) * 4 floats).
 int launch_gemm_prompt(const QMatDev& w, const int8_t* x, const float* xs, float* out, int ld_out, int N,
-                       hipStream_t stream, const void* xm = nullptr, const float* xsm = nullptr);
-int launch_prompt_repack(const int8_t* x, const float* xs, int N, int K, void* xm, float* xsm, hipStream_t stream);
+                       hipStream_t stream, const void* xm, const float* xsm);
+// xam (optional, as xsm): the float sums of each 32-value block's int8 values (Q4_K's A_j)
+int launch_prompt_repack(const int8_t* x, const float* xs, int N, int K, void* xm, float* xsm, hipStream_t stream,
+                         float* xam = nullptr);
+// Q4_K batch matmul for any number of tokens on int8 MFMA (R16K and R64 layouts) over
+// activations repacked with their block sums
+int launch_gemm_prompt_q4k(const QMatDev& w, float* out, int ld_out, int N, hipStream_t stream, const void* xm,
+                           const float* xsm, const float* xam);
 // The verify GEMMs' epilogues as separate kernels over a prompt matmul's f32 output y.
 int launch_prompt_qkv_rope(const float* y, int N, int start, int aw, int kw, int hd, int rope_half,
                            const float* rope_tab, float* q_out, float* kcache, float* vcache, int max_ctx,
@@ -202,10 +207,12 @@ struct nc_ctx {
     size_t xsum_cap = 0;
     float* tp_scratch = nullptr;  // temperature softmax partials
     size_t tp_cap = 0;
-    // activations of the prompt matmul (more than 16 tokens) repacked in MFMA operand order,
-    // for kPromptRows tokens of 65536 columns per slice; allocated by nc_ctx_create
+    // activations of the prompt matmul (more than 16 tokens) repacked in MFMA operand order
+    // with their scales and block sums, for kPromptRows tokens of 65536 columns per slice;
+    // allocated by nc_ctx_create
     int8_t* pxm = nullptr;
     float* pxsm = nullptr;
+    float* pxam = nullptr;
     // device address of the static scratch array on this context's device (never freed)
     int32_t* static_scratch = nullptr;
     int gemm_kernel = NC_GEMM_KERNEL_AUTO;  // dot-product path of the quantized matmuls

@@ -97,6 +97,7 @@ struct nc_session {
     int32_t* p_pos = nullptr;    // [R / kPromptGroup] start positions of the attention row groups
     int8_t* p_xm = nullptr;      // matmul activations repacked in MFMA operand order
     float* p_xsm = nullptr;
+    float* p_xam = nullptr;      // their block sums (Q4_K)
     std::vector<void*> allocs;
 };
 
@@ -836,11 +837,27 @@ static int fetch_preds(nc_session* s, int n, uint32_t* out) {
 // ---------------------------------------------------------------- prompt passes
 // Prompt passes run every matrix of the layer through the MFMA prompt matmul, so they need
 // Q4_0 matrices throughout (R16 or R64 tiles).
+static bool prompt_matrix_ok(const QMatDev& q) {
+    if (q.type == NC_TYPE_Q4_0) return q.layout == LAYOUT_R16 || q.layout == LAYOUT_R64;
+    if (q.type == NC_TYPE_Q4_K) return q.layout == LAYOUT_R16K || q.layout == LAYOUT_R64;
+    return false;
+}
+
 static bool prompt_path_ok(const nc_model* m) {
     for (const LayerDev& L : m->layers)
         for (const QMatDev* q : {&L.qkv, &L.wo, &L.gateup, &L.down})
-            if (q->type != NC_TYPE_Q4_0 || (q->layout != LAYOUT_R16 && q->layout != LAYOUT_R64)) return false;
+            if (!prompt_matrix_ok(*q)) return false;
     return true;
+}
+
+// Prompt matmul of n tokens (Q4_0 or Q4_K) over activations repacked into xm / xsm (/ xam).
+static int prompt_matmul(const QMatDev& w, const int8_t* xq, const float* xs, float* out, int ld_out, int n,
+                         hipStream_t st, int8_t* xm, float* xsm, float* xam) {
+    const bool k = w.type == NC_TYPE_Q4_K;
+    int rc = launch_prompt_repack(xq, xs, n, (int)w.cols, xm, xsm, st, k ? xam : nullptr);
+    if (rc) return rc;
+    return k ? launch_gemm_prompt_q4k(w, out, ld_out, n, st, xm, xsm, xam)
+             : launch_gemm_prompt(w, xq, xs, out, ld_out, n, st, xm, xsm);
 }
 
 static int ensure_prompt_bufs(nc_session* s) {
@@ -857,7 +874,8 @@ static int ensure_prompt_bufs(nc_session* s) {
         (rc = dev_alloc(s->allocs, &s->p_scores, (size_t)kPromptGroup * c.head_count * s->ctx_stride)) ||
         (rc = dev_alloc(s->allocs, &s->p_toks, (size_t)s->max_ctx)) ||
         (rc = dev_alloc(s->allocs, &s->p_pos, R / kPromptGroup)) || (rc = dev_alloc(s->allocs, &s->p_xm, R * s->maxw)) ||
-        (rc = dev_alloc(s->allocs, &s->p_xsm, R * ((s->maxw + 127) / 128) * 4)))
+        (rc = dev_alloc(s->allocs, &s->p_xsm, R * ((s->maxw + 127) / 128) * 4)) ||
+        (rc = dev_alloc(s->allocs, &s->p_xam, R * ((s->maxw + 127) / 128) * 4)))
         return rc;
     s->prompt_ready = true;
     return NC_OK;
@@ -865,8 +883,7 @@ static int ensure_prompt_bufs(nc_session* s) {
 
 // Prompt matmul of the pass's activations (repacked first into MFMA operand order).
 static int prompt_gemm(nc_session* s, const QMatDev& w, const int8_t* xq, const float* xs, float* out, int n) {
-    int rc = launch_prompt_repack(xq, xs, n, (int)w.cols, s->p_xm, s->p_xsm, s->stream);
-    return rc ? rc : launch_gemm_prompt(w, xq, xs, out, (int)w.rows, n, s->stream, s->p_xm, s->p_xsm);
+    return prompt_matmul(w, xq, xs, out, (int)w.rows, n, s->stream, s->p_xm, s->p_xsm, s->p_xam);
 }
 
 // One prompt pass over n <= kPromptRows ids p_toks[off..off+n) at positions start..: the
@@ -1043,6 +1060,7 @@ int nc_ctx_create(int device, nc_ctx** out) {
     }
     if (e == hipSuccess) e = hipMalloc((void**)&c->pxm, kPromptRows * kCtxScratchCols);
     if (e == hipSuccess) e = hipMalloc((void**)&c->pxsm, kPromptRows * (kCtxScratchCols / 128 + 1) * 4 * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void**)&c->pxam, kPromptRows * (kCtxScratchCols / 128 + 1) * 4 * sizeof(float));
     if (e != hipSuccess) {
         nc_ctx_free(c);
         return fail(NC_EHIP, std::string("nc_ctx_create: ") + hipGetErrorString(e));
@@ -1058,6 +1076,7 @@ void nc_ctx_free(nc_ctx* c) {
     if (c->tp_scratch) (void)hipFree(c->tp_scratch);
     if (c->pxm) (void)hipFree(c->pxm);
     if (c->pxsm) (void)hipFree(c->pxsm);
+    if (c->pxam) (void)hipFree(c->pxam);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -1117,18 +1136,17 @@ static int prompt_slice_tokens(int64_t cols) {
     return (int)std::min<int64_t>(kPromptRows, (int64_t)kPromptRows * (int64_t)kCtxScratchCols / cols / 16 * 16);
 }
 
-// The Q4_0 prompt matmul of batch_size > 16 tokens through the context's repack buffers, in
-// slices of prompt_slice_tokens (every token's outputs are the same bits in any slicing).
+// The prompt matmul (Q4_0 or Q4_K) of batch_size > 16 tokens through the context's repack
+// buffers, in slices of prompt_slice_tokens (every token's outputs are the same bits in any
+// slicing).
 static int ctx_prompt_matmul(nc_ctx* ctx, const QMatDev& w, const int8_t* x, const float* xs, float* out, int n,
                              hipStream_t st) {
     const int cols = (int)w.cols, T = prompt_slice_tokens(cols);
     for (int i = 0; i < n; i += T) {
         const int len = std::min(T, n - i);
-        const int8_t* xi = x + (size_t)i * cols;
-        const float* xsi = xs + (size_t)i * (cols / 32);
-        int rc = launch_prompt_repack(xi, xsi, len, cols, ctx->pxm, ctx->pxsm, st);
-        if (rc || (rc = launch_gemm_prompt(w, xi, xsi, out + (size_t)i * w.rows, (int)w.rows, len, st, ctx->pxm, ctx->pxsm)))
-            return rc;
+        int rc = prompt_matmul(w, x + (size_t)i * cols, xs + (size_t)i * (cols / 32), out + (size_t)i * w.rows,
+                               (int)w.rows, len, st, ctx->pxm, ctx->pxsm, ctx->pxam);
+        if (rc) return rc;
     }
     return NC_OK;
 }
@@ -1141,7 +1159,7 @@ int nc_matmul_quantized_batch(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8,
     NC_HIP(hipSetDevice(ctx->device));
     hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
     // more than 16 tokens: the MFMA prompt matmul (Q4_0), or 16-token slices (Q4_K)
-    if (batch_size > 16 && w->m.type == NC_TYPE_Q4_0 && prompt_slice_tokens(cols) >= 16)
+    if (batch_size > 16 && prompt_matrix_ok(w->m) && prompt_slice_tokens(cols) >= 16)
         return ctx_prompt_matmul(ctx, w->m, x_i8, x_scales, out, batch_size, st);
     for (int i = 0; i < batch_size; i += 16) {
         const int nb = std::min(16, batch_size - i);
@@ -1170,8 +1188,8 @@ int nc_bench_matmul(nc_ctx* ctx, const nc_qmat* const* w, int32_t ncopies, const
     for (int i = 0; i < ncopies; i++)
         if (!w[i] || w[i]->m.rows != w[0]->m.rows || w[i]->m.cols != w[0]->m.cols)
             return fail(NC_EINVAL, "nc_bench_matmul: weight copies differ in shape");
-    if (batch_size > 16 && (w[0]->m.type != NC_TYPE_Q4_0 || prompt_slice_tokens(w[0]->m.cols) < 16))
-        return fail(NC_EINVAL, "nc_bench_matmul: more than 16 tokens only for Q4_0 matrices of <= 1M columns");
+    if (batch_size > 16 && (!prompt_matrix_ok(w[0]->m) || prompt_slice_tokens(w[0]->m.cols) < 16))
+        return fail(NC_EINVAL, "nc_bench_matmul: more than 16 tokens only for Q4_0 / Q4_K matrices of <= 1M columns");
     NC_HIP(hipSetDevice(ctx->device));
     hipStream_t st = ctx->stream;
     const int64_t cols = w[0]->m.cols, rows = w[0]->m.rows;

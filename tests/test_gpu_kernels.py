@@ -139,16 +139,24 @@ def test_q6_k_matmul(ctx, M, K):
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), N
 
 
-def test_q4_k_matmul_above_16_tokens(ctx):
-    """Q4_K matrices take 16-token slices of the verify kernel beyond 16 tokens."""
+Q4K_PROMPT_SHAPES = [(512, 1024, (17, 37, 64, 100, 300)), (1000, 768, (33, 129)), (16400, 256, (17, 70))]
+
+
+@pytest.mark.parametrize("M,K,Ns", Q4K_PROMPT_SHAPES, ids=[f"{m}x{k}" for m, k, _ in Q4K_PROMPT_SHAPES])
+def test_q4_k_prompt_matmul(ctx, M, K, Ns):
+    """More than 16 tokens on Q4_K matrices take the MFMA prompt matmul (matmul_q4_k_batch,
+    inference.rs:2006-2132, any batch): every output bit-identical to the oracle.  16-row tiles
+    (R16K) with 4 and 3 super-blocks per row and a partial last tile, 64-row tiles (R64, >= 256
+    tiles) with a partial last tile; token counts that leave partial 16- and 64-token tiles, and
+    300 tokens (two repack slices)."""
     import nanocamelid_amd as nc
-    M, K, N = 512, 1024, 37
-    w = random_q4_k(M, K, seed=5)
+    w = random_q4_k(M, K, seed=M + K)
     q = nc.QMat(ctx, nc.NC_TYPE_Q4_K, M, K, w)
-    x, xq, xs = q8_activations(N, K, seed=6)
-    out = nc.matmul_quantized_batch(ctx, q, torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda()).cpu().numpy()
-    ref = O.matmul_q4_k(xq, xs, w, N, M, K, nthreads=16)
-    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    for N in Ns:
+        x, xq, xs = q8_activations(N, K, seed=N + 3 * M)
+        out = nc.matmul_quantized_batch(ctx, q, torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda()).cpu().numpy()
+        ref = O.matmul_q4_k(xq, xs, w, N, M, K, nthreads=16)
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), N
 
 
 def _dequant(w):

@@ -300,15 +300,16 @@ def test_long_context_logits(ctx, hd, checks):
         pos = c
 
 
-@pytest.mark.parametrize("hd", [64, 128])
-def test_prompt_passes_match_oracle(ctx, hd):
-    """Prompts of 32 or more tokens on Q4_0 models run as MFMA prompt passes of up to 256 tokens
-    (epilogues as separate kernels, attention in 64-row groups): a 300-token prompt without
-    logits (passes of 256 + 44) and 400 more with logits (passes of 256 + 128, then the last 16
-    rows as a verify-sized pass), then a 9-row verify: every logit bit-identical to the oracle's
-    after 16-token chunks, i.e. the same KV cache bits."""
+@pytest.mark.parametrize("hd,wt", [(64, 2), (128, 2), (128, 12)], ids=["hd64-q4_0", "hd128-q4_0", "hd128-q4_k"])
+def test_prompt_passes_match_oracle(ctx, hd, wt):
+    """Prompts of 32 or more tokens on Q4_0 and Q4_K models run as MFMA prompt passes of up to
+    256 tokens (epilogues as separate kernels, attention in 64-row groups): a 300-token prompt
+    without logits (passes of 256 + 44) and 400 more with logits (passes of 256 + 128, then the
+    last 16 rows as a verify-sized pass), then a 9-row verify: every logit bit-identical to the
+    oracle's after 16-token chunks, i.e. the same KV cache bits."""
     import nanocamelid_amd as nc
-    spec = dict(TINY, head_count=512 // hd, head_count_kv=256 // hd, embedding_length=512, context_length=1024)
+    spec = dict(TINY, head_count=512 // hd, head_count_kv=256 // hd, embedding_length=512, context_length=1024,
+                weight_type=wt)
     _, gm, om = _models(ctx, spec, seed=40 + hd)
     prompt = nc.uniform_prompt(41, 700, 1000)
     gs, os_ = nc.Session(gm, 1024, 16), O.Session(om, 1024, 16)
