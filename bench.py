@@ -224,7 +224,6 @@ def run_prefill(args):
     img = nc.synth_gguf(**nc.SYNTH_CONFIGS["llama-3-8b"], context_length=8192 + 64, seed=args.seed,
                         nthreads=HOST_THREADS)
     model = nc.Model(ctx, data=img, nthreads=HOST_THREADS)
-    del img
     log(f"llama-3-8b-shape model on device in {time.time() - t0:.1f}s")
     prompt = nc.uniform_prompt(args.seed, 8192, model.config["vocab_size"])
     for n in ((args.prefill_tokens,) if args.prefill_tokens else (512, 2048, 8192)):
@@ -250,6 +249,57 @@ def run_prefill(args):
             s2.close()
         s.close()
         print(json.dumps(res), flush=True)
+    if not args.no_cpu_baseline and not args.prefill_tokens:
+        # the oracle (C++ restatement of the reference's portable path) prefilling the same
+        # model: a bounded sample of 64 tokens in the reference's 16-row passes
+        from oracle import oracle as O
+        om = O.Model(data=img.tobytes(), nthreads=HOST_THREADS)
+        n = 64
+        s = O.Session(om, n + 16, 16)
+        t = time.perf_counter()
+        for i in range(0, n, 16):
+            s.prefill_pass_batch(prompt[i:i + 16], i)
+        dt = time.perf_counter() - t
+        s.close()
+        om.close()
+        print(json.dumps({"cpu_baseline": {"value": round(n / dt, 2), "unit": "prefill tok/s", "cores": HOST_THREADS,
+                                           "kind": "port", "cpu_model": cpu_model_name(),
+                                           "sample": f"{n}-token prefill of the same llama-3-8b-shape model in "
+                                                     f"16-row passes on {HOST_THREADS} threads"}}), flush=True)
+    del img
+
+
+def run_loader(args):
+    """GGUF load (gguf.rs:454-551 read_file, model.rs:461-545 LlamaWeights::load, with
+    validate_model_tensors model.rs:851-1036): the 8B-shape synthetic file from disk to a model
+    ready to run, on the GPU path (mmap, validation, f32 decode of the embedding, repack, upload)
+    and in the CPU oracle (its own reader and decode of the same file)."""
+    import tempfile
+
+    import nanocamelid_amd as nc
+    from oracle import oracle as O
+    img = nc.synth_gguf(**nc.SYNTH_CONFIGS["llama-3-8b"], context_length=8192, seed=args.seed, nthreads=HOST_THREADS)
+    size = img.nbytes
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        path = os.path.join(d, "llama-3-8b-q4_0.gguf")
+        img.tofile(path)
+        del img
+        ctx = nc.Context(0)
+        t = time.perf_counter()
+        m = nc.Model(ctx, path=path, nthreads=HOST_THREADS)
+        ctx.synchronize()
+        gpu_s = time.perf_counter() - t
+        dev_bytes = int(m.config["device_weight_bytes"])
+        m.close()
+        t = time.perf_counter()
+        om = O.Model(path=path, nthreads=HOST_THREADS)
+        cpu_s = time.perf_counter() - t
+        om.close()
+    print(json.dumps({"metric": "GGUF model load, file to ready model (llama-3-8b shape, Q4_0)", "value": round(gpu_s, 3),
+                      "unit": "s", "higher_is_better": False, "file_bytes": int(size), "device_bytes": dev_bytes,
+                      "file_GB_per_s": round(size / gpu_s / 1e9, 2),
+                      "cpu_baseline": {"value": round(cpu_s, 3), "unit": "s", "cores": HOST_THREADS, "kind": "port",
+                                       "sample": "the oracle's load of the same file"}}), flush=True)
 
 
 def run_config3(args):
@@ -431,6 +481,7 @@ def main():
                     help="config 4: 70B Q4_0, one 9-row verify pass over an 8192-position KV cache")
     ap.add_argument("--prefill", action="store_true",
                     help="prompt prefill: prompt matmul at 64/256 tokens and 8B-shape prefill wall times")
+    ap.add_argument("--loader", action="store_true", help="GGUF load time from disk (GPU path and CPU oracle)")
     ap.add_argument("--prefill-tokens", type=int, default=0,
                     help="with --prefill: only one prefill of this many tokens (for a kernel profile)")
     ap.add_argument("--c4-passes", type=int, default=10)
@@ -461,6 +512,9 @@ def main():
         return
     if args.prefill:
         run_prefill(args)
+        return
+    if args.loader:
+        run_loader(args)
         return
     spec = dict(nc.SYNTH_CONFIGS[args.config])
     t0 = time.time()

@@ -40,19 +40,21 @@ struct PromptGemm {
     float* out = nullptr;       // out[n * ld_out + row]
 };
 
-template <int LAYOUT, int D>
+template <int LAYOUT, int D, int RT>
 __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
     // wave index through readfirstlane: the tile bases below are then scalar (buffer-load
     // soffsets) instead of per-lane values that the compiler would loop over
     const int lane = threadIdx.x & 63, wv = wave_id_uniform();
     const int g = lane >> 4, r = lane & 15;  // A/B lane (g, r); D lane (g, c = r)
-    const int row0 = blockIdx.x * 64 + (wv & 1) * 32;
-    const int tok0 = blockIdx.y * 64 + (wv >> 1) * 32;
+    // RT = 2: a wave covers 32 rows x 32 tokens, a workgroup 64 x 64; RT = 1 (matrices whose
+    // 32 x 32 tiles would leave a SIMD one wave): 16 rows x 32 tokens, a workgroup 64 x 32
+    const int row0 = RT == 2 ? blockIdx.x * 64 + (wv & 1) * 32 : blockIdx.x * 64 + wv * 16;
+    const int tok0 = RT == 2 ? blockIdx.y * 64 + (wv >> 1) * 32 : blockIdx.y * 32;
     if (row0 >= p.M || tok0 >= p.N) return;  // wave-uniform; the kernel has no barriers
     const int K = 32 * p.nb, nq = (p.nb + 3) / 4;
-    int rt[2];
+    int rt[RT];
 #pragma unroll
-    for (int i = 0; i < 2; i++) rt[i] = min(row0 / 16 + i, p.tiles16 - 1);  // storage is padded to 16 rows
+    for (int i = 0; i < RT; i++) rt[i] = min(row0 / 16 + i, p.tiles16 - 1);  // storage is padded to 16 rows
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc((void*)p.w, 0, (int)p.w_bytes, 0x00020000);
     const int n16 = (p.N + 15) / 16;  // 16-token tiles of the repacked activations
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc((void*)p.xm, 0, n16 * K * 16, 0x00020000);
@@ -61,9 +63,9 @@ __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
 #pragma unroll
     for (int k = 0; k < 2; k++) tt[k] = min(tok0 / 16 + k, n16 - 1);
     // per-lane parts of the addresses
-    int nvo[2], svo[2];
+    int nvo[RT], svo[RT];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < RT; i++) {
         if constexpr (LAYOUT == LAYOUT_R16) {
             nvo[i] = r * 16 + 4 * g;  // + 256 j within the quad
             svo[i] = 1024 + 32 * g;   // scales [row / 4][j][row % 4]
@@ -79,12 +81,12 @@ __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
         else
             return ((rt[i] >> 2) * p.groups + (qd >> 1)) * kQ40ChunkBytes;
     };
-    uint32_t nib[D][2][4], sw[D][2][8], xa[D][2][4], xb[D][2][4];
+    uint32_t nib[D][RT][4], sw[D][RT][8], xa[D][2][4], xb[D][2][4];
     float4 xsv[D][2];
 #define NC_PQ_LOAD(QD, SLOT)                                                                                    \
     do {                                                                                                        \
         const int qd_ = min((QD), nq - 1);                                                                      \
-        _Pragma("unroll") for (int i = 0; i < 2; i++) {                                                         \
+        _Pragma("unroll") for (int i = 0; i < RT; i++) {                                                         \
             const int tb_ = tile_base(i, qd_);                                                                  \
             _Pragma("unroll") for (int j = 0; j < 4; j++) {                                                     \
                 const int jo_ = LAYOUT == LAYOUT_R16 ? 256 * j : 1024 * ((qd_ & 1) * 4 + j);                   \
@@ -107,9 +109,9 @@ __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
                 sres, r * 16, (tt[k] * nq + qd_) * 256, 0));                                                    \
         }                                                                                                       \
     } while (0)
-    float acc[2][2][4];
+    float acc[RT][2][4];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < RT; i++)
 #pragma unroll
         for (int k = 0; k < 2; k++)
 #pragma unroll
@@ -137,7 +139,7 @@ __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
                         xsj[k] = j == 0 ? xsv[s][k].x : j == 1 ? xsv[s][k].y : j == 2 ? xsv[s][k].z : xsv[s][k].w;
                     }
 #pragma unroll
-                    for (int i = 0; i < 2; i++) {
+                    for (int i = 0; i < RT; i++) {
                         const uint32_t wn = nib[s][i][j];
                         const long a = (long)((uint64_t)(wn & 0x0F0F0F0Fu) | ((uint64_t)((wn >> 4) & 0x0F0F0F0Fu) << 32));
                         float ws[4];
@@ -165,7 +167,7 @@ __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
         const int n = tok0 + 16 * k + r;
         if (n >= p.N) continue;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < RT; i++) {
             const int row = row0 + 16 * i + 4 * g;
             float* o = p.out + (size_t)n * p.ld_out + row;
             if (row + 3 < p.M && (p.ld_out & 3) == 0) {
@@ -177,6 +179,12 @@ __global__ __launch_bounds__(256) void gemm_q4_0_prompt_kernel(PromptGemm p) {
             }
         }
     }
+}
+
+// Row tiles per wave: 2 (32 x 32 wave tiles) when that gives every SIMD at least two waves
+// (2048 waves on 256 CUs), else 1 (16 x 32: twice the waves for the same work).
+static int prompt_row_tiles(int64_t rows, int N) {
+    return ((rows + 31) / 32) * ((N + 31) / 32) >= 2048 ? 2 : 1;
 }
 
 int launch_gemm_prompt(const QMatDev& w, const int8_t* x, const float* xs, float* out, int ld_out, int N,
@@ -200,9 +208,15 @@ int launch_gemm_prompt(const QMatDev& w, const int8_t* x, const float* xs, float
     p.xm = (const uint2*)xm;
     p.xsm = (const float4*)xsm;
     p.out = out;
-    const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 63) / 64));
-    if (w.layout == LAYOUT_R16) hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R16, 2>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R64, 2>), grid, dim3(256), 0, st, p);
+    if (prompt_row_tiles(w.rows, N) == 2) {
+        const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 63) / 64));
+        if (w.layout == LAYOUT_R16) hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R16, 2, 2>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R64, 2, 2>), grid, dim3(256), 0, st, p);
+    } else {
+        const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 31) / 32));
+        if (w.layout == LAYOUT_R16) hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R16, 2, 1>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R64, 2, 1>), grid, dim3(256), 0, st, p);
+    }
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
@@ -247,13 +261,15 @@ __device__ __forceinline__ void q4k_scale_min_dev(int j, uint32_t s0, uint32_t s
     }
 }
 
-template <int LAYOUT>
+template <int LAYOUT, int RT>
 __global__ __launch_bounds__(256) void gemm_q4_k_prompt_kernel(PromptGemmK p) {
     __shared__ __align__(16) float tab[4][2][8][2][16];  // per wave: [tile][sub-block][sc, mn][row]
     const int lane = threadIdx.x & 63, wv = wave_id_uniform();
     const int g = lane >> 4, r = lane & 15;
-    const int row0 = blockIdx.x * 64 + (wv & 1) * 32;
-    const int tok0 = blockIdx.y * 64 + (wv >> 1) * 32;
+    // RT = 2: a wave covers 32 rows x 32 tokens, a workgroup 64 x 64; RT = 1 (matrices whose
+    // 32 x 32 tiles would leave a SIMD one wave): 16 rows x 32 tokens, a workgroup 64 x 32
+    const int row0 = RT == 2 ? blockIdx.x * 64 + (wv & 1) * 32 : blockIdx.x * 64 + wv * 16;
+    const int tok0 = RT == 2 ? blockIdx.y * 64 + (wv >> 1) * 32 : blockIdx.y * 32;
     if (row0 >= p.M || tok0 >= p.N) return;  // wave-uniform; the kernel has no barriers
     const int n16 = (p.N + 15) / 16, nq = 2 * p.nsb;  // 16-token tiles, quads of sub-blocks
     int tt[2];
@@ -274,12 +290,12 @@ __global__ __launch_bounds__(256) void gemm_q4_k_prompt_kernel(PromptGemmK p) {
     };
     // one stage = half a super-block (sub-blocks 4h..4h+3): per tile the nibble dwords of two
     // pairs and the header; per token tile four B operands, the x_scales and the sums
-    uint32_t hd[2][2][4], nb0[2][2][2], nb1[2][2][2], xa[2][2][4], xb[2][2][4];
+    uint32_t hd[2][RT][4], nb0[2][RT][2], nb1[2][RT][2], xa[2][2][4], xb[2][2][4];
     float4 xsv[2][2], xav[2][2];
 #define NC_PK_LOAD(ST, SLOT)                                                                                    \
     do {                                                                                                        \
         const int st_ = min((ST), nq - 1), sb_ = st_ >> 1, h_ = st_ & 1;                                        \
-        _Pragma("unroll") for (int i = 0; i < 2; i++) {                                                         \
+        _Pragma("unroll") for (int i = 0; i < RT; i++) {                                                         \
             const int c_ = chunk(i, sb_);                                                                       \
             const uint4 hv_ = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, r * 16, c_, 0)); \
             hd[SLOT][i][0] = hv_.x; hd[SLOT][i][1] = hv_.y; hd[SLOT][i][2] = hv_.z; hd[SLOT][i][3] = hv_.w;     \
@@ -300,9 +316,9 @@ __global__ __launch_bounds__(256) void gemm_q4_k_prompt_kernel(PromptGemmK p) {
             xav[SLOT][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ares, r * 16, (tt[k] * nq + st_) * 256, 0)); \
         }                                                                                                       \
     } while (0)
-    float acc[2][2][4], part[2][2][4];
+    float acc[RT][2][4], part[RT][2][4];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < RT; i++)
 #pragma unroll
         for (int k = 0; k < 2; k++)
 #pragma unroll
@@ -318,7 +334,7 @@ __global__ __launch_bounds__(256) void gemm_q4_k_prompt_kernel(PromptGemmK p) {
             if (s == 0) {
                 // this lane's row r, sub-blocks 2g and 2g + 1: scales and mins into the table
 #pragma unroll
-                for (int i = 0; i < 2; i++) {
+                for (int i = 0; i < RT; i++) {
                     const float d = f16_to_f32((uint16_t)(hd[0][i][0] & 0xffff));
                     const float dmin = f16_to_f32((uint16_t)(hd[0][i][0] >> 16));
 #pragma unroll
@@ -333,7 +349,7 @@ __global__ __launch_bounds__(256) void gemm_q4_k_prompt_kernel(PromptGemmK p) {
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+                for (int i = 0; i < RT; i++)
 #pragma unroll
                     for (int k = 0; k < 2; k++)
 #pragma unroll
@@ -352,7 +368,7 @@ __global__ __launch_bounds__(256) void gemm_q4_k_prompt_kernel(PromptGemmK p) {
                     xaj[k] = jj == 0 ? xa4.x : jj == 1 ? xa4.y : jj == 2 ? xa4.z : xa4.w;
                 }
 #pragma unroll
-                for (int i = 0; i < 2; i++) {
+                for (int i = 0; i < RT; i++) {
                     const uint32_t w0 = hi ? (nb0[s][i][pp] >> 4) : nb0[s][i][pp];
                     const uint32_t w1 = hi ? (nb1[s][i][pp] >> 4) : nb1[s][i][pp];
                     const long a = (long)((uint64_t)(w0 & 0x0F0F0F0Fu) | ((uint64_t)(w1 & 0x0F0F0F0Fu) << 32));
@@ -373,7 +389,7 @@ __global__ __launch_bounds__(256) void gemm_q4_k_prompt_kernel(PromptGemmK p) {
             }
             if (s == 1) {
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+                for (int i = 0; i < RT; i++)
 #pragma unroll
                     for (int k = 0; k < 2; k++)
 #pragma unroll
@@ -391,7 +407,7 @@ __global__ __launch_bounds__(256) void gemm_q4_k_prompt_kernel(PromptGemmK p) {
         const int n = tok0 + 16 * k + r;
         if (n >= p.N) continue;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < RT; i++) {
             const int row = row0 + 16 * i + 4 * g;
             float* o = p.out + (size_t)n * p.ld_out + row;
             if (row + 3 < p.M && (p.ld_out & 3) == 0) {
@@ -425,9 +441,15 @@ int launch_gemm_prompt_q4k(const QMatDev& w, float* out, int ld_out, int N, hipS
     p.xsm = (const float4*)xsm;
     p.xam = (const float4*)xam;
     p.out = out;
-    const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 63) / 64));
-    if (w.layout == LAYOUT_R16K) hipLaunchKernelGGL((gemm_q4_k_prompt_kernel<LAYOUT_R16K>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((gemm_q4_k_prompt_kernel<LAYOUT_R64>), grid, dim3(256), 0, st, p);
+    if (prompt_row_tiles(w.rows, N) == 2) {
+        const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 63) / 64));
+        if (w.layout == LAYOUT_R16K) hipLaunchKernelGGL((gemm_q4_k_prompt_kernel<LAYOUT_R16K, 2>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((gemm_q4_k_prompt_kernel<LAYOUT_R64, 2>), grid, dim3(256), 0, st, p);
+    } else {
+        const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 31) / 32));
+        if (w.layout == LAYOUT_R16K) hipLaunchKernelGGL((gemm_q4_k_prompt_kernel<LAYOUT_R16K, 1>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((gemm_q4_k_prompt_kernel<LAYOUT_R64, 1>), grid, dim3(256), 0, st, p);
+    }
     NC_HIP(hipGetLastError());
     return NC_OK;
 }

@@ -111,7 +111,8 @@ def test_q4_0_prompt_matmul(ctx, M, K, Ns):
     every output bit-identical to the oracle.  Covers 16-row tiles (R16) with 4096 and 3 blocks
     per row (a partial quad) and rows not a multiple of 64, 64-row tiles (R64, >= 512 tiles) with
     a partial last tile, token counts that leave partial 16- and 64-token tiles, and 300 tokens
-    (two slices through the context's 256-token repack buffers)."""
+    (two slices through the context's 256-token repack buffers); wave tiles of 16 rows (small
+    matrices) and 32 rows (32816 x 64)."""
     import nanocamelid_amd as nc
     w = random_q4_0(M, K, seed=M + 7 * K)
     q = nc.QMat(ctx, nc.NC_TYPE_Q4_0, M, K, w)
@@ -139,7 +140,7 @@ def test_q6_k_matmul(ctx, M, K):
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), N
 
 
-Q4K_PROMPT_SHAPES = [(512, 1024, (17, 37, 64, 100, 300)), (1000, 768, (33, 129)), (16400, 256, (17, 70))]
+Q4K_PROMPT_SHAPES = [(512, 1024, (17, 37, 64, 100, 300)), (1000, 768, (33, 129)), (16400, 256, (17, 70, 300))]
 
 
 @pytest.mark.parametrize("M,K,Ns", Q4K_PROMPT_SHAPES, ids=[f"{m}x{k}" for m, k, _ in Q4K_PROMPT_SHAPES])
@@ -148,7 +149,7 @@ def test_q4_k_prompt_matmul(ctx, M, K, Ns):
     inference.rs:2006-2132, any batch): every output bit-identical to the oracle.  16-row tiles
     (R16K) with 4 and 3 super-blocks per row and a partial last tile, 64-row tiles (R64, >= 256
     tiles) with a partial last tile; token counts that leave partial 16- and 64-token tiles, and
-    300 tokens (two repack slices)."""
+    300 tokens (two repack slices); wave tiles of 16 rows and, for 16400 rows at 300 tokens, 32."""
     import nanocamelid_amd as nc
     w = random_q4_k(M, K, seed=M + K)
     q = nc.QMat(ctx, nc.NC_TYPE_Q4_K, M, K, w)
