@@ -145,6 +145,13 @@ int nc_rms_norm_q8_0_batch(nc_ctx* ctx, const float* x, const float* w, float ep
  *            floor(k24 * sum W / 2^24), k24 = u * 2^24.  At the first rejection the next
  *            token is drawn from w = max(0, p_i - q_i) (from p_i if that has no mass) with
  *            the resample uniform; after k acceptances from p_k with the bonus uniform. */
+/* sample_logits (src/inference.rs:4834-4873) of rows 1..16 rows of logits (device, row stride
+ * vocab): temp <= 0 the first maximum; temp > 0 e_j = expf((l_j - max)/temp), S = sum e_j left
+ * to right, r = u * S with u = rand_simple() (one draw of *rng_state per row, in row order), then
+ * r -= e_j until r <= 0 (the last id if never), every f32 operation as the reference's.  work:
+ * rows x vocab device floats (temp > 0).  tokens: host ids[rows]. */
+int nc_sample_logits_batch(nc_ctx* ctx, const float* logits, int32_t rows, int64_t vocab, float temp,
+                           uint64_t* rng_state, float* work, uint32_t* tokens, void* stream);
 /* probs[r][j] for rows x vocab (device pointers, row stride vocab); temp > 0. */
 int nc_temperature_probs_batch(nc_ctx* ctx, const float* logits, float* probs, int32_t rows, int64_t vocab, float temp,
                                void* stream);
@@ -308,6 +315,17 @@ int nc_generate_speculative_ngram(nc_session* s, const uint32_t* prompt, int32_t
 int nc_generate_speculative_draft(nc_session* target, nc_session* draft, const uint32_t* prompt,
                                   int32_t n_prompt, int32_t n_new, int32_t draft_k, uint32_t* out,
                                   nc_decode_stats* stats);
+
+/* The same step at temperature temp (src/speculative.rs:299-494 with temp > 0): drafts are
+ * drawn with sample_logits (src/inference.rs:4834-4873) from the draft's logits, the target
+ * draws its own token at each verified position with sample_logits, a draft is accepted iff
+ * the two ids match, and the first mismatch (or, after k matches, the trailing draw) is
+ * emitted and run on both models.  *rng_state is the reference's LCG state (rand_simple,
+ * src/inference.rs:4876-4883; the reference starts it at 0x123456789abcdef0), advanced by one
+ * draw per sample the reference makes, in its order.  temp <= 0: the greedy loop above. */
+int nc_generate_speculative_draft_temp(nc_session* target, nc_session* draft, const uint32_t* prompt,
+                                       int32_t n_prompt, int32_t n_new, int32_t draft_k, float temp,
+                                       uint64_t* rng_state, uint32_t* out, nc_decode_stats* stats);
 
 /* Draft-model speculative sampling at temperature temp > 0, k+1 form (no reference
  * counterpart; the draft-model loop shape follows src/speculative.rs:299-494).  Both models

@@ -187,6 +187,26 @@ def temperature_probs_batch(ctx: Context, logits, temp: float, out=None):
     return out
 
 
+# The reference's initial rand_simple state (src/inference.rs:4875).
+REFERENCE_RNG_STATE = 0x123456789ABCDEF0
+
+
+def sample_logits_batch(ctx: Context, logits, temp: float, rng_state: int = REFERENCE_RNG_STATE):
+    """sample_logits (src/inference.rs:4834-4873) of each row on the GPU: temp <= 0 the first
+    maximum; temp > 0 the reference's draw (r = rand_simple() * sum e, r -= e_j until r <= 0),
+    one LCG draw per row in row order.  logits: [rows][vocab] f32 device tensor (rows <= 16).
+    Returns (ids, rng_state after the draws)."""
+    import torch
+    rows, vocab = logits.shape
+    work = torch.empty_like(logits) if temp > 0 else None
+    st = C.c_uint64(rng_state)
+    ids = np.zeros(rows, np.uint32)
+    check(lib().nc_sample_logits_batch(ctx.h, logits.data_ptr(), rows, vocab, float(temp), C.byref(st),
+                                       work.data_ptr() if work is not None else None,
+                                       ids.ctypes.data_as(C.POINTER(C.c_uint32)), _stream_of(logits)))
+    return ids, int(st.value)
+
+
 def stochastic_accept(ctx: Context, p_probs, q_probs, drafts, seed: int, start_pos: int):
     """k+1 stochastic acceptance on the GPU (no reference counterpart; the library's Philox /
     min(1, p/q) / fixed-point resampling specification).  p_probs [k+1][V], q_probs [k][V]
@@ -337,6 +357,21 @@ def generate_speculative_draft(target: Session, draft: Session, prompt, n_new: i
     check(lib().nc_generate_speculative_draft(target.h, draft.h, p, a.size, n_new, draft_k,
                                               out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
     return out[:st.emitted], st
+
+
+def generate_speculative_draft_temp(target: Session, draft: Session, prompt, n_new: int, draft_k: int, temp: float,
+                                    rng_state: int = REFERENCE_RNG_STATE):
+    """speculative_decoding_step at temperature temp (src/speculative.rs:299-494): drafts and
+    target tokens drawn with sample_logits and the reference's LCG, acceptance by id match.
+    Returns (tokens, stats, rng_state after the run)."""
+    a, p = _u32(prompt)
+    out = np.zeros(n_new, np.uint32)
+    st = DecodeStats()
+    rs = C.c_uint64(rng_state)
+    check(lib().nc_generate_speculative_draft_temp(target.h, draft.h, p, a.size, n_new, draft_k, float(temp),
+                                                   C.byref(rs), out.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                                   C.byref(st)))
+    return out[:st.emitted], st, int(rs.value)
 
 
 def generate_speculative_stochastic(target: Session, draft: Session, prompt, n_new: int, k: int, temp: float,

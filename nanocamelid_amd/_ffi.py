@@ -78,6 +78,7 @@ SIGNATURES = {
     "nc_rms_norm_q8_0_batch": (C.c_int, [_vp, _vp, _vp, C.c_float, _vp, _vp, C.c_int, _i64, _vp]),
     "nc_bench_matmul": (C.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _vp]),
     "nc_temperature_probs_batch": (C.c_int, [_vp, _vp, _vp, _i32, _i64, C.c_float, _vp]),
+    "nc_sample_logits_batch": (C.c_int, [_vp, _vp, _i32, _i64, C.c_float, C.POINTER(C.c_uint64), _vp, _u32p, _vp]),
     "nc_stochastic_accept": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _i64, C.c_uint64, _i64, _vp, _vp]),
     "nc_model_load_gguf": (C.c_int, [_vp, C.c_char_p, C.POINTER(LoadOpts), C.POINTER(_vp)]),
     "nc_model_load_gguf_memory": (C.c_int, [_vp, _vp, C.c_size_t, C.POINTER(LoadOpts), C.POINTER(_vp)]),
@@ -101,6 +102,8 @@ SIGNATURES = {
     "nc_generate_speculative_oracle": (C.c_int, [_vp, _u32p, _i32, _i32, _i32, _i32, C.c_float, C.c_uint64, _u32p,
                                                  _i32, _u32p, C.POINTER(DecodeStats)]),
     "nc_generate_speculative_draft": (C.c_int, [_vp, _vp, _u32p, _i32, _i32, _i32, _u32p, C.POINTER(DecodeStats)]),
+    "nc_generate_speculative_draft_temp": (C.c_int, [_vp, _vp, _u32p, _i32, _i32, _i32, C.c_float,
+                                                     C.POINTER(C.c_uint64), _u32p, C.POINTER(DecodeStats)]),
     "nc_generate_speculative_stochastic": (C.c_int, [_vp, _vp, _u32p, _i32, _i32, _i32, C.c_float, C.c_uint64, _u32p,
                                                      C.POINTER(DecodeStats)]),
     "nc_synth_size": (C.c_int, [C.POINTER(SynthSpec), C.POINTER(C.c_uint64)]),

@@ -35,7 +35,9 @@
 //     kChainMaxSensitive segments are sensitive), thread 0 recomputes the chain sequentially.
 //
 // The result is therefore always bit-identical to the sequential loop; the guesses only
-// decide how fast it is found.  Terms must be >= 0 (sums of squares, exponentials).
+// decide how fast it is found.  Terms must be >= 0 (sums of squares, exponentials); the start
+// may be negative (a subtraction chain r_i = r_{i-1} - a_i is the negation of this chain from
+// -r, since round-to-nearest is symmetric).
 //
 // Wave-level scans use gfx9 DPP (row_shr, row_bcast, wave_shr): no LDS round trips.
 #pragma once
@@ -72,6 +74,7 @@ struct ChainScratch {
     ChainEntry ent[kChainMaxSensitive];
     float walk_end[64];  // chain value after each entry of the current 64-entry window
     int bad;             // set by any thread whose boundary check fails
+    int first;           // FIND: first term index whose chain value is >= 0 (INT_MAX: none)
     float result;
 };
 
@@ -173,11 +176,13 @@ __device__ __forceinline__ double block_excl_scan_f64_i32(double v, int k, doubl
 constexpr int kChainMargin = 256;  // ulps between a guess and the true state that are tolerated
 
 // Thread t holds terms a[0..E) = a_{tE} .. a_{tE+E-1} (n = T*E terms; pad with zeros, which
-// leave the chain unchanged).  The chain starts from s_{-1} = s0 >= 0, so a long sum can be
-// evaluated as consecutive segments, each starting from the previous segment's result.
-// a_lds: n floats of LDS used by the walk and the fallback.  Every thread of the block must
-// call it; returns s_{n-1} to all threads.
-template <int E, int T>
+// leave the chain unchanged).  The chain starts from s_{-1} = s0, so a long sum can be
+// evaluated as consecutive segments, each starting from the previous segment's result.  A
+// negative s0 is allowed (terms stay >= 0): the state then rises through zero, whose
+// neighbourhood only makes segments sensitive.  a_lds: n floats of LDS used by the walk and
+// the fallback.  Every thread of the block must call it; returns s_{n-1} to all threads.
+// FIND: sc.first also receives the first index i (0 .. n-1) with s_i >= 0, or INT_MAX.
+template <int E, int T, bool FIND = false>
 __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float* a_lds, float s0 = 0.0f) {
     static_assert(E >= 1 && E <= 32, "terms per thread");
     const int t = threadIdx.x;
@@ -193,9 +198,10 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
 
     // 2. the segment evaluated from the guess, with the tie and binade tests
     const uint32_t bg = __float_as_uint(g);
-    const int eg = (int)(bg >> 23);
-    // half an ulp of g's binade, 2^(eg - 151); only used when eg >= 25 (else sensitive anyway)
-    const float half = __uint_as_float((uint32_t)(eg > 25 ? eg - 24 : 1) << 23);
+    const int eg = (int)(bg >> 23);  // sign and exponent: the binade test below includes the sign
+    const int ea = eg & 0xff;
+    // half an ulp of g's binade, 2^(ea - 151); only used when ea >= 25 (else sensitive anyway)
+    const float half = __uint_as_float((uint32_t)(ea > 25 ? ea - 24 : 1) << 23);
     float x = g;
     bool tie = false;
 #pragma unroll
@@ -207,9 +213,10 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
     }
     const uint32_t bx = __float_as_uint(x);
     const int mg = (int)(bg & 0x7fffff), mx = (int)(bx & 0x7fffff);
-    // g == 0: every earlier term and s0 are 0, so the start is exact and the run is the truth
-    const bool sens = (bg != 0) & ((eg < 25) | ((int)(bx >> 23) != eg) | (mg < kChainMargin) |
-                                   (mx + kChainMargin >= (1 << 23)) | tie);
+    // g == 0 with s0 >= 0: every earlier term and s0 are 0, so the start is exact and the run
+    // is the truth (with a negative s0 a zero guess is a cancellation, not an exact start)
+    const bool sens = ((bg != 0) | (s0 < 0.0f)) & ((ea < 25) | ((int)(bx >> 23) != eg) | (mg < kChainMargin) |
+                                                   (mx + kChainMargin >= (1 << 23)) | tie);
     const double d = (double)x - (double)g;
 
     // 3. uncorrected starts C_t, with the sensitive count scanned in the same pass
@@ -224,7 +231,10 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
         ce.cend = cstart + d;
         ce.seg = t;
     }
-    if (t == 0) sc.bad = 0;  // read after the verification barrier, two barriers on
+    if (t == 0) {
+        sc.bad = 0;  // read after the verification barrier, two barriers on
+        if (FIND) sc.first = 0x7fffffff;
+    }
     __syncthreads();
     if (listed && t < 64) {
         // wave 0: lane q stages entry e0 + q (its advance over the insensitive segments before
@@ -297,8 +307,13 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
         const double sh = off == 0 ? 0.0 : sc.ent[off - 1].shift;
         const float start = (float)(cstart + sh);
         y = start;
+        int fi = -1;
 #pragma unroll
-        for (int j = 0; j < E; j++) y = y + a[j];
+        for (int j = 0; j < E; j++) {
+            y = y + a[j];
+            if (FIND && fi < 0 && y >= 0.0f) fi = j;
+        }
+        if (FIND && fi >= 0) atomicMin(&sc.first, t * E + fi);  // meaningful only if every check passes
         sc.last[t] = y;
         bad = t == 0 ? start != s0 : false;
         // the start is compared with the previous segment's end after the barrier
@@ -313,8 +328,13 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
         if (t == T - 1) sc.result = y;
     } else if (t == 0) {
         float v = s0;
-        for (int i = 0; i < T * E; i++) v = v + a_lds[i];
+        int fi = 0x7fffffff;
+        for (int i = 0; i < T * E; i++) {
+            v = v + a_lds[i];
+            if (FIND && fi == 0x7fffffff && v >= 0.0f) fi = i;
+        }
         sc.result = v;
+        if (FIND) sc.first = fi;
     }
     __syncthreads();
     return sc.result;

@@ -179,6 +179,15 @@ int launch_accept_greedy(const uint32_t* toks, const uint32_t* preds, int n, int
 // Temperature probabilities of `rows` rows; scratch: temperature_scratch_floats(rows) floats of
 // device memory owned by the caller (stream-ordered reuse).
 size_t temperature_scratch_floats(int rows);
+// sample_logits (inference.rs:4834-4873) of `rows` rows (<= kSampleMaxRows): temp > 0 draws row r
+// with the uniform u[r] (the reference's inverse-CDF walk, bit-exact); temp <= 0 takes the first
+// maximum.  probs: rows x ld_p floats of work (the rows' e_j), scratch as above; out: device ids.
+constexpr int kSampleMaxRows = 17;
+struct SampleUniforms {
+    float u[kSampleMaxRows];
+};
+int launch_sample_logits(const float* logits, int64_t ld_in, int rows, int V, float temp, const float* u, float* probs,
+                         int64_t ld_p, float* scratch, uint32_t* out, hipStream_t stream);
 int launch_temperature_probs(const float* logits, int64_t ld_in, float* probs, int64_t ld_out, int rows, int V,
                              float temp, float* scratch, hipStream_t st);
 // p [k+1][ld] target probs, q [k][ld] draft probs, drafts[k] (device); result = {n_accepted,

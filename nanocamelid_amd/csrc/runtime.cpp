@@ -68,6 +68,7 @@ struct nc_session {
     uint32_t* d_preds = nullptr;
     int32_t* d_pos = nullptr;
     int32_t* d_result = nullptr;
+    uint32_t* d_samp = nullptr;  // [kSampleMaxRows] ids drawn by sample_logits
     float* rope_tab = nullptr;
     // pinned host mirrors
     uint32_t* h_toks = nullptr;
@@ -834,6 +835,28 @@ static int fetch_preds(nc_session* s, int n, uint32_t* out) {
     return NC_OK;
 }
 
+// rand_simple (inference.rs:4876-4883): the reference's LCG, state advanced before each draw;
+// u32::MAX as f32 is 4294967296.0f.
+static float lcg_next(uint64_t* state) {
+    *state = *state * 6364136223846793005ull + 1ull;
+    const uint32_t x = (uint32_t)(*state >> 32);
+    return (float)x / (float)UINT32_MAX;
+}
+
+// sample_logits (inference.rs:4834-4873) of rows row0 .. row0 + rows - 1 of the session's last
+// pass, row r with the uniform u[r] (temp > 0; temp <= 0: first maximum, no uniform).
+static int sample_session_rows(nc_session* s, int row0, int rows, float temp, const float* u, uint32_t* out) {
+    const int V = (int)s->m->cfg.vocab_size;
+    if (rows < 1 || row0 < 0 || row0 + rows > s->max_batch) return fail(NC_EINVAL, "sample_logits: rows outside the pass");
+    int rc = launch_sample_logits(s->logits + (size_t)row0 * V, V, rows, V, temp, u, s->probs, V, s->tp_scratch, s->d_samp,
+                                  s->stream);
+    if (rc) return rc;
+    NC_HIP(hipMemcpyAsync(s->h_preds, s->d_samp, rows * sizeof(uint32_t), hipMemcpyDeviceToHost, s->stream));
+    NC_HIP(hipStreamSynchronize(s->stream));
+    std::memcpy(out, s->h_preds, rows * sizeof(uint32_t));
+    return NC_OK;
+}
+
 // ---------------------------------------------------------------- prompt passes
 // Prompt passes run every matrix of the layer through the MFMA prompt matmul, so they need
 // Q4_0 matrices throughout (R16 or R64 tiles).
@@ -1415,7 +1438,8 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
         (rc = dev_alloc(s->allocs, &s->part_val, B * m->head.tiles)) ||
         (rc = dev_alloc(s->allocs, &s->part_idx, B * m->head.tiles)) ||
         (rc = dev_alloc(s->allocs, &s->d_toks, B)) || (rc = dev_alloc(s->allocs, &s->d_preds, B)) ||
-        (rc = dev_alloc(s->allocs, &s->d_pos, 4)) || (rc = dev_alloc(s->allocs, &s->d_result, 4)))
+        (rc = dev_alloc(s->allocs, &s->d_pos, 4)) || (rc = dev_alloc(s->allocs, &s->d_result, 4)) ||
+        (rc = dev_alloc(s->allocs, &s->d_samp, (size_t)kSampleMaxRows)))
         return rc;
     NC_HIP(hipMemset(s->kcache, 0, kv * 4));
     NC_HIP(hipMemset(s->vcache, 0, kv * 4));
@@ -1728,6 +1752,95 @@ int nc_generate_speculative_draft(nc_session* tg, nc_session* dr, const uint32_t
     const double t2 = now_s();
     if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};
     return flush_timing(tg);
+}
+
+int nc_generate_speculative_draft_temp(nc_session* tg, nc_session* dr, const uint32_t* prompt, int32_t n_prompt,
+                                       int32_t n_new, int32_t draft_k, float temp, uint64_t* rng_state, uint32_t* out,
+                                       nc_decode_stats* stats) {
+    // sample_logits at temp <= 0 is the argmax and draws nothing: the greedy loop
+    if (!(temp > 0.0f)) return nc_generate_speculative_draft(tg, dr, prompt, n_prompt, n_new, draft_k, out, stats);
+    if (!tg || !dr || tg == dr || !prompt || !out || !rng_state || n_prompt < 1 || n_new < 1 || draft_k < 1)
+        return fail(NC_EINVAL, "nc_generate_speculative_draft_temp: bad arguments");
+    if (tg->m->cfg.vocab_size != dr->m->cfg.vocab_size) return fail(NC_EINVAL, "target and draft vocabularies differ");
+    if (tg->ctx->device != dr->ctx->device) return fail(NC_EINVAL, "target and draft must share a device");
+    NC_HIP(hipSetDevice(tg->ctx->device));
+    const double t0 = now_s();
+    // main.rs:9643-9706: prefill both models; their last rows' logits are the live ones
+    int rc = prefill_chunks(dr, prompt, n_prompt, 0, nullptr, true);
+    if (rc || (rc = prefill_chunks(tg, prompt, n_prompt, 0, nullptr, true))) return rc;
+    int dlive = dr->last_n - 1, tlive = tg->last_n - 1;  // rows of the live logits in the last pass
+    const double t1 = now_s();
+    int64_t pos = n_prompt, produced = 0, steps = 0, drafted = 0, accepted = 0;
+    uint32_t drafts[16], tt[17];
+    float uv[17];
+    while (produced < n_new && pos < tg->max_ctx) {
+        // speculative.rs:318-321 clamp
+        int64_t k = std::min<int64_t>(draft_k, n_new - produced);
+        k = std::min<int64_t>(k, tg->max_batch);
+        k = std::min<int64_t>(k, tg->max_ctx - (pos + 1));
+        k = std::min<int64_t>(k, dr->max_ctx - (pos + 1));
+        if (k <= 0) break;
+        // 1. drafting (speculative.rs:327-350): one draw per draft from the draft's live logits
+        for (int64_t i = 0; i < k; i++) {
+            const float u = lcg_next(rng_state);
+            if ((rc = sample_session_rows(dr, dlive, 1, temp, &u, &drafts[i])) ||
+                (rc = nc_forward1(dr, drafts[i], pos + i, nullptr, nullptr)))
+                return rc;
+            dlive = 0;
+        }
+        // 2. the first verification draw, from the target's live logits, before the batch pass
+        // replaces them (speculative.rs:384-403)
+        const uint64_t st0 = *rng_state;
+        uint64_t st = st0;
+        uv[0] = lcg_next(&st);
+        if ((rc = sample_session_rows(tg, tlive, 1, temp, uv, &tt[0]))) return rc;
+        // 3. batched target pass over the drafts (speculative.rs:365-373); row r predicts
+        // position pos + r + 1, so draw r + 1 samples it, provisionally: only the draws the
+        // verification reaches are kept
+        if ((rc = upload_toks(tg, drafts, (int)k)) || (rc = run_pass(tg, (int)k, pos))) return rc;
+        for (int64_t r = 0; r < k; r++) uv[1 + r] = lcg_next(&st);
+        if ((rc = sample_session_rows(tg, 0, (int)k, temp, uv + 1, &tt[1]))) return rc;
+        // 4. verification (speculative.rs:384-447) and the trailing token (:450-489)
+        drafted += k;
+        int64_t i = 0;
+        for (; i < k && drafts[i] == tt[i]; i++) {
+            accepted++;
+            if (produced < n_new) out[produced++] = drafts[i];
+        }
+        const uint32_t fix = tt[i];             // corrective (i < k) or trailing (i == k) token
+        const int64_t at = pos + i;
+        st = st0;
+        for (int64_t r = 0; r <= i; r++) (void)lcg_next(&st);  // draws 0 .. i were made
+        *rng_state = st;
+        if (produced < n_new) out[produced++] = fix;
+        if ((rc = nc_forward1(tg, fix, at, nullptr, nullptr)) || (rc = nc_forward1(dr, fix, at, nullptr, nullptr)))
+            return rc;
+        tlive = dlive = 0;
+        pos = at + 1;
+        steps++;
+    }
+    const double t2 = now_s();
+    if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};
+    return flush_timing(tg);
+}
+
+int nc_sample_logits_batch(nc_ctx* ctx, const float* logits, int32_t rows, int64_t vocab, float temp,
+                           uint64_t* rng_state, float* work, uint32_t* tokens, void* stream) {
+    if (!ctx || !logits || !tokens || rows < 1 || rows > 16 || vocab < 1 || vocab > INT32_MAX)
+        return fail(NC_EINVAL, "nc_sample_logits_batch: bad arguments");
+    const bool t = temp > 0.0f;
+    if (t && (!rng_state || !work)) return fail(NC_EINVAL, "nc_sample_logits_batch: temperature needs rng_state and work");
+    NC_HIP(hipSetDevice(ctx->device));
+    hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+    float u[16] = {};
+    if (t)
+        for (int r = 0; r < rows; r++) u[r] = lcg_next(rng_state);  // rows in order, one draw each
+    uint32_t* d_out = (uint32_t*)ctx->xsum;  // >= 16 ids of the context's operator scratch
+    int rc = launch_sample_logits(logits, vocab, rows, (int)vocab, temp, u, work, vocab, ctx->tp_scratch, d_out, st);
+    if (rc) return rc;
+    NC_HIP(hipMemcpyAsync(tokens, d_out, rows * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    NC_HIP(hipStreamSynchronize(st));
+    return NC_OK;
 }
 
 int nc_generate_speculative_stochastic(nc_session* tg, nc_session* dr, const uint32_t* prompt, int32_t n_prompt,

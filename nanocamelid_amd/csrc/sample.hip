@@ -69,6 +69,7 @@ __device__ inline float wave_max(float v) {
 // between the passes.  scratch: per row kTpCh chunk maxima, then 1/S.
 constexpr int kTpCh = 64;
 constexpr int kTpT = 256;
+constexpr int kTpStride = kTpCh + 2;  // per row: chunk maxima, 1/S, S
 
 __device__ inline int tp_chunk(int V) { return (V + kTpCh - 1) / kTpCh; }
 
@@ -85,7 +86,7 @@ __global__ __launch_bounds__(kTpT) void tp_max_kernel(const float* logits, int64
     if (t == 0) {
 #pragma unroll
         for (int w = 1; w < kTpT / 64; w++) mx = fmaxf(mx, wm[w]);
-        scratch[(size_t)row * (kTpCh + 1) + c] = mx;
+        scratch[(size_t)row * kTpStride + c] = mx;
     }
 }
 
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(kTpT) void tp_max_kernel(const float* logits, int64
 __global__ __launch_bounds__(kTpT) void tp_exp_kernel(const float* logits, int64_t ld_in, float* probs, int64_t ld_out,
                                                       int V, float temp, const float* scratch) {
     const int row = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
-    const float* pm = scratch + (size_t)row * (kTpCh + 1);
+    const float* pm = scratch + (size_t)row * kTpStride;
     static_assert(kTpCh == 64, "one chunk maximum per lane");
     float mx = pm[t & 63];
     mx = wave_max(mx);  // every wave reduces all kTpCh chunk maxima
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(kTpT) void tp_exp_kernel(const float* logits, int64
     for (int i = lo + t; i < hi; i += kTpT) e[i] = expf_glibc((l[i] - mx) / temp);
 }
 
-// S = sum e_j left to right, one exact segment of kSmSeg terms at a time; scratch gets 1/S.
+// S = sum e_j left to right, one exact segment of kSmSeg terms at a time; scratch gets 1/S and S.
 __global__ __launch_bounds__(kSmT) void tp_sum_kernel(const float* probs, int64_t ld_out, int V, float* scratch) {
     __shared__ ChainScratch<kSmT> sc;
     __shared__ __align__(16) float a_lds[kSmSeg];
@@ -120,16 +121,90 @@ __global__ __launch_bounds__(kSmT) void tp_sum_kernel(const float* probs, int64_
         }
         sum = exact_chain_sum<kSmE, kSmT>(a, sc, a_lds, sum);
     }
-    if (t == 0) scratch[(size_t)blockIdx.x * (kTpCh + 1) + kTpCh] = 1.0f / sum;
+    if (t == 0) {
+        scratch[(size_t)blockIdx.x * kTpStride + kTpCh] = 1.0f / sum;
+        scratch[(size_t)blockIdx.x * kTpStride + kTpCh + 1] = sum;
+    }
 }
 
 // p_j = e_j * (1 / S) (inference.rs:3535-3539), in place.
 __global__ __launch_bounds__(kTpT) void tp_norm_kernel(float* probs, int64_t ld_out, int V, const float* scratch) {
     const int row = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
-    const float inv = scratch[(size_t)row * (kTpCh + 1) + kTpCh];
+    const float inv = scratch[(size_t)row * kTpStride + kTpCh];
     float* e = probs + (size_t)row * ld_out;
     const int lo = min(c * tp_chunk(V), V), hi = min(lo + tp_chunk(V), V);
     for (int i = lo + t; i < hi; i += kTpT) e[i] = e[i] * inv;
+}
+
+// ---------------------------------------------------------------- the reference's sampler
+// sample_logits for temperature > 0 (inference.rs:4846-4873): with e_j = expf((l_j - max) / T)
+// and S = sum e_j left to right (the passes above), r = u * S with u from the caller's LCG
+// (rand_simple, inference.rs:4876-4883), then r -= e_j for j = 0, 1, ... and the first j with
+// r <= 0 is the sample (V - 1 if none).  r_j = fl(r_{j-1} - e_j) is the negation of the chain
+// q_j = fl(q_{j-1} + e_j) from q = -r (round to nearest is symmetric), so exact_chain_sum
+// evaluates it bit for bit from a negative start and finds its first j with q_j >= 0.
+__global__ __launch_bounds__(kSmT) void lcg_walk_kernel(const float* probs, int64_t ld, int V, const float* scratch,
+                                                        SampleUniforms uu, uint32_t* out) {
+    __shared__ ChainScratch<kSmT> sc;
+    __shared__ __align__(16) float a_lds[kSmSeg];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const float* e = probs + (size_t)row * ld;
+    const float S = scratch[(size_t)row * kTpStride + kTpCh + 1];
+    float q = -(uu.u[row] * S);
+    int found = -1;
+    for (int base = 0; base < V; base += kSmSeg) {
+        float a[kSmE];
+#pragma unroll
+        for (int j = 0; j < kSmE; j++) {
+            const int i = base + t * kSmE + j;
+            a[j] = i < V ? e[i] : 0.0f;  // zeros past the row leave the chain and its sign unchanged
+        }
+        q = exact_chain_sum<kSmE, kSmT, true>(a, sc, a_lds, q);
+        if (sc.first != 0x7fffffff) {  // uniform: read after the routine's last barrier
+            found = base + sc.first;
+            break;
+        }
+    }
+    if (t == 0) out[row] = (uint32_t)(found >= 0 && found < V ? found : V - 1);
+}
+
+// Greedy sample_logits (inference.rs:4835-4845): the first maximum of each row.
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* logits, int64_t ld, int V, uint32_t* out) {
+    __shared__ float bvs[16];
+    __shared__ int bis[16];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const float* l = logits + (size_t)row * ld;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = t; i < V; i += 1024) {
+        const float v = l[i];
+        if (v > bv) {  // ascending i per thread: the first of equal values stays
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((t & 63) == 0) {
+        bvs[t >> 6] = bv;
+        bis[t >> 6] = bi;
+    }
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < 16; w++)
+            if (bvs[w] > bv || (bvs[w] == bv && bis[w] < bi)) {
+                bv = bvs[w];
+                bi = bis[w];
+            }
+        out[row] = (uint32_t)(bi == 0x7fffffff ? 0 : bi);
+    }
 }
 
 // ---------------------------------------------------------------- fixed-point sampler
@@ -259,7 +334,27 @@ __global__ __launch_bounds__(kSpT) void sample_probs_kernel(const float* probs, 
     }
 }
 
-size_t temperature_scratch_floats(int rows) { return (size_t)rows * (kTpCh + 1); }
+size_t temperature_scratch_floats(int rows) { return (size_t)rows * kTpStride; }
+
+int launch_sample_logits(const float* logits, int64_t ld_in, int rows, int V, float temp, const float* u, float* probs,
+                         int64_t ld_p, float* scratch, uint32_t* out, hipStream_t st) {
+    if (rows < 1 || rows > kSampleMaxRows || V < 1) return fail(NC_EINVAL, "sample_logits: 1..17 rows of vocab >= 1");
+    if (!(temp > 0.0f)) {
+        hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(1024), 0, st, logits, ld_in, V, out);
+        NC_HIP(hipGetLastError());
+        return NC_OK;
+    }
+    if (!u || !probs || !scratch) return fail(NC_EINVAL, "sample_logits: uniforms and work buffers required");
+    SampleUniforms uu;
+    for (int r = 0; r < kSampleMaxRows; r++) uu.u[r] = r < rows ? u[r] : 0.0f;
+    const dim3 grid(kTpCh, rows);
+    hipLaunchKernelGGL(tp_max_kernel, grid, dim3(kTpT), 0, st, logits, ld_in, V, scratch);
+    hipLaunchKernelGGL(tp_exp_kernel, grid, dim3(kTpT), 0, st, logits, ld_in, probs, ld_p, V, temp, scratch);
+    hipLaunchKernelGGL(tp_sum_kernel, dim3(rows), dim3(kSmT), 0, st, probs, ld_p, V, scratch);
+    hipLaunchKernelGGL(lcg_walk_kernel, dim3(rows), dim3(kSmT), 0, st, probs, ld_p, V, scratch, uu, out);
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
 
 int launch_temperature_probs(const float* logits, int64_t ld_in, float* probs, int64_t ld_out, int rows, int V,
                              float temp, float* scratch, hipStream_t st) {

@@ -627,9 +627,20 @@ int64_t or_generate_speculative_draft(or_session* tg, or_session* dr, const uint
                                       int64_t n_prompt, int64_t n_new, int64_t draft_k,
                                       int64_t prefill_batch, uint32_t* out, int64_t* stats,
                                       int64_t* steps_out) {
+    return or_generate_speculative_draft_temp(tg, dr, prompt, n_prompt, n_new, draft_k, 0.0f, nullptr,
+                                              prefill_batch, out, stats, steps_out);
+}
+
+int64_t or_generate_speculative_draft_temp(or_session* tg, or_session* dr, const uint32_t* prompt,
+                                           int64_t n_prompt, int64_t n_new, int64_t draft_k, float temp,
+                                           uint64_t* rng_state, int64_t prefill_batch, uint32_t* out,
+                                           int64_t* stats, int64_t* steps_out) {
     // main.rs:9643-9706 prefill of both models, then speculative.rs:299-494 per step
-    // (greedy, temp 0, no stop tokens).
+    // (no stop tokens); every sample is sample_logits (argmax at temp <= 0).
     const int64_t V = tg->m->V;
+    uint64_t st_unused = 0;
+    uint64_t* rs = rng_state ? rng_state : &st_unused;
+    auto sample = [&](const float* l) { return (uint32_t)or_sample_logits(l, V, temp, rs); };
     prefill(dr, prompt, n_prompt - 1, 0, std::min(prefill_batch, dr->max_batch));
     or_forward_pass(dr, prompt[n_prompt - 1], n_prompt - 1);
     prefill(tg, prompt, n_prompt - 1, 0, prefill_batch);
@@ -646,7 +657,7 @@ int64_t or_generate_speculative_draft(or_session* tg, or_session* dr, const uint
         std::vector<uint32_t> drafts;
         int64_t cdp = pos;
         while ((int64_t)drafts.size() < k) {
-            uint32_t t = (uint32_t)or_argmax(dr->logits.data(), V);
+            uint32_t t = sample(dr->logits.data());
             drafts.push_back(t);
             or_forward_pass(dr, t, cdp);
             cdp++;
@@ -663,7 +674,7 @@ int64_t or_generate_speculative_draft(or_session* tg, or_session* dr, const uint
             } else {
                 l = tg->logits.data();
             }
-            uint32_t tt = (uint32_t)or_argmax(l, V);
+            uint32_t tt = sample(l);
             if (drafts[i] == tt) {
                 acc.push_back(tt);
                 stats[1]++;
@@ -678,7 +689,7 @@ int64_t or_generate_speculative_draft(or_session* tg, or_session* dr, const uint
         }
         if (!rejected) {
             or_batch_row_logits(tg, k - 1, lg.data());
-            uint32_t tt = (uint32_t)or_argmax(lg.data(), V);
+            uint32_t tt = sample(lg.data());
             acc.push_back(tt);
             or_forward_pass(tg, tt, pos + k);
             or_forward_pass(dr, tt, pos + k);

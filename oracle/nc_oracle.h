@@ -90,6 +90,9 @@ float or_expf(float x);                        /* Rust f32::exp == glibc expf */
 int64_t or_expf_mismatches(uint32_t first, int64_t count, const float* vals, int nthreads, uint32_t* first_bad);
 void or_silu_mul(float* out, const float* gate, const float* up, int64_t n); /* :3367-3390 */
 int64_t or_argmax(const float* logits, int64_t n); /* :4834-4845 first max wins */
+float or_rand_simple(uint64_t* state);             /* inference.rs:4876-4883 LCG draw */
+/* inference.rs:4834-4873 sample_logits (temp <= 0: argmax, no draw) */
+int64_t or_sample_logits(const float* logits, int64_t V, float temp, uint64_t* state);
 /* One attention head over an f32 KV slice, inference.rs:4242-4292 (x86 path).
  * k_cache/v_cache: [>=pos+1][kv_width]; scores scratch >= pos+1. */
 void or_attention_head(float* out_head, float* scores, const float* q_head,
@@ -155,6 +158,13 @@ int64_t or_generate_speculative_draft(or_session* target, or_session* draft,
                                       const uint32_t* prompt, int64_t n_prompt, int64_t n_new,
                                       int64_t draft_k, int64_t prefill_batch,
                                       uint32_t* out, int64_t* stats, int64_t* steps_out);
+/* The same at temperature temp > 0: every draw through or_sample_logits with the LCG state
+ * *rng_state, in the reference's order (drafts, then one per verified position, then the
+ * trailing token), acceptance by id match. */
+int64_t or_generate_speculative_draft_temp(or_session* target, or_session* draft, const uint32_t* prompt,
+                                           int64_t n_prompt, int64_t n_new, int64_t draft_k, float temp,
+                                           uint64_t* rng_state, int64_t prefill_batch, uint32_t* out,
+                                           int64_t* stats, int64_t* steps_out);
 
 /* k+1 speculative decoding with the seeded oracle drafter (no reference
  * counterpart): draft i of a step at position p copies greedy[p - n_prompt]

@@ -544,6 +544,36 @@ void or_rope(float* data, int64_t pos, int64_t heads, int64_t head_dim, int64_t 
 
 float or_expf(float x) { return expf(x); }
 
+// inference.rs:4876-4883 rand_simple: state = state * 6364136223846793005 + 1 (wrapping),
+// ((state >> 32) as u32) as f32 / (u32::MAX as f32).
+float or_rand_simple(uint64_t* state) {
+    *state = *state * 6364136223846793005ull + 1ull;
+    const float x = (float)(uint32_t)(*state >> 32);
+    return x / (float)UINT32_MAX;
+}
+
+// inference.rs:4834-4873 sample_logits: temp <= 0 the first maximum; else max, e_i =
+// ((l_i - max) / temp).exp() summed left to right, r = rand_simple() * sum, then r -= e_i
+// until r <= 0 (the last index if never).
+int64_t or_sample_logits(const float* logits, int64_t V, float temp, uint64_t* state) {
+    if (temp <= 0.0f) return or_argmax(logits, V);
+    float mx = logits[0];
+    for (int64_t i = 0; i < V; i++)
+        if (logits[i] > mx) mx = logits[i];
+    std::vector<float> e(V);
+    float sum = 0.0f;
+    for (int64_t i = 0; i < V; i++) {
+        e[i] = expf((logits[i] - mx) / temp);
+        sum += e[i];
+    }
+    float r = or_rand_simple(state) * sum;
+    for (int64_t i = 0; i < V; i++) {
+        r -= e[i];
+        if (r <= 0.0f) return i;
+    }
+    return V - 1;
+}
+
 // Checker for the device restatement of expf: vals[i] against glibc expf of the float with
 // bits first + i, bit for bit (NaN inputs: any NaN).  Returns the mismatch count and the first
 // mismatching input's bits in *first_bad.

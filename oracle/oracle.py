@@ -63,6 +63,10 @@ def lib():
         "or_expf_mismatches": (C.c_int64, [C.c_uint32, C.c_int64, C.c_void_p, C.c_int, C.c_void_p]),
         "or_silu_mul": (None, [_f32p, _f32p, _f32p, _i64]),
         "or_argmax": (_i64, [_f32p, _i64]),
+        "or_rand_simple": (C.c_float, [C.POINTER(C.c_uint64)]),
+        "or_sample_logits": (_i64, [_f32p, _i64, C.c_float, C.POINTER(C.c_uint64)]),
+        "or_generate_speculative_draft_temp": (_i64, [C.c_void_p, C.c_void_p, _u32p, _i64, _i64, _i64, C.c_float,
+                                                      C.POINTER(C.c_uint64), _i64, _u32p, _i64p, _i64p]),
         "or_attention_head": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, C.c_float]),
         "or_philox4x32_10": (None, [_u32p, _u32p, _u32p]),
         "or_model_load": (C.c_void_p, [C.c_char_p, C.c_int, C.c_char_p, C.c_int]),
@@ -246,6 +250,23 @@ def silu_mul(g, u):
 def argmax(logits) -> int:
     logits = _c(logits, np.float32)
     return lib().or_argmax(logits, logits.size)
+
+
+REFERENCE_RNG_STATE = 0x123456789ABCDEF0  # inference.rs:4875
+
+
+def rand_simple(state: int):
+    """inference.rs:4876-4883: (u, new state)."""
+    st = C.c_uint64(state)
+    u = lib().or_rand_simple(C.byref(st))
+    return u, int(st.value)
+
+
+def sample_logits(logits, temp: float, state: int = REFERENCE_RNG_STATE):
+    """inference.rs:4834-4873: (index, new state)."""
+    st = C.c_uint64(state)
+    i = lib().or_sample_logits(_c(logits, np.float32), np.asarray(logits).size, float(temp), C.byref(st))
+    return int(i), int(st.value)
 
 
 def attention_head(q_head, k_cache, v_cache, pos, kv_width, kv_h, head_dim, scale):
@@ -432,6 +453,20 @@ def generate_speculative_draft(target: Session, draft: Session, prompt, n_new, d
     n = lib().or_generate_speculative_draft(target.h, draft.h, p, p.size, n_new, draft_k, prefill_batch,
                                             out, stats, steps)
     return out[:n], int(stats[0]), int(stats[1]), int(steps[0])
+
+
+def generate_speculative_draft_temp(target: Session, draft: Session, prompt, n_new, draft_k, temp,
+                                    rng_state=REFERENCE_RNG_STATE, prefill_batch=16):
+    """speculative.rs:299-494 at temperature temp with the reference's sampler and LCG; returns
+    (tokens, drafted, accepted, steps, rng_state)."""
+    p = _c(prompt, np.uint32)
+    out = np.zeros(n_new, np.uint32)
+    stats = np.zeros(2, np.int64)
+    steps = np.zeros(1, np.int64)
+    st = C.c_uint64(rng_state)
+    n = lib().or_generate_speculative_draft_temp(target.h, draft.h, p, p.size, n_new, draft_k, float(temp),
+                                                 C.byref(st), prefill_batch, out, stats, steps)
+    return out[:n], int(stats[0]), int(stats[1]), int(steps[0]), int(st.value)
 
 
 def generate_speculative_stochastic(target: Session, draft: Session, prompt, n_new, k, temp, seed, prefill_batch=16):

@@ -167,3 +167,53 @@ def test_generate_speculative_stochastic(ctx):
                                                                         prompt, 60, 4, 1.0, 3)
     assert np.array_equal(g_out, o_out)
     assert st.accepted == st.drafted > 0
+
+
+# ---------------------------------------------------------------- the reference's sampler
+# sample_logits (inference.rs:4834-4873) with the reference's LCG (rand_simple, :4876-4883):
+# every id and the LCG state after the draws identical to the oracle's, on rows whose
+# subtraction walk crosses many binades (flat: e = 1 everywhere), stays on one term (peaked),
+# skips long runs of zero terms (wide) or ends past several 16384-term segments.
+@pytest.mark.parametrize("V", [7, 1000, 16385, 128256])
+@pytest.mark.parametrize("temp", [0.0, 0.5, 1.0, 1.7])
+def test_sample_logits_batch_matches_oracle(ctx, V, temp):
+    import nanocamelid_amd as nc
+    rng = np.random.default_rng(V + 3)
+    base = list(_rows(V, rng).values())
+    x = np.stack(base + [rng.normal(0, 1 + r, V).astype(np.float32) for r in range(16 - len(base))])
+    xt = torch.from_numpy(x).cuda()
+    st = O.REFERENCE_RNG_STATE
+    for call in range(3):
+        print(f"sample_logits V={V} T={temp} call={call}", flush=True)
+        ids, st_gpu = nc.sample_logits_batch(ctx, xt, temp, st)
+        want = []
+        for r in range(x.shape[0]):
+            i, st = O.sample_logits(x[r], temp, st)
+            want.append(i)
+        assert ids.tolist() == want, (V, temp, call)
+        assert st_gpu == st
+
+
+TINY_UNTIED = dict(TINY, tied=0)
+
+
+@pytest.mark.parametrize("draft_seed,k,temp", [(72, 2, 0.3), (71, 4, 0.05)])
+def test_speculative_draft_temp_matches_oracle(ctx, draft_seed, k, temp):
+    """speculative_decoding_step at temp > 0 (speculative.rs:299-494): the GPU loop's tokens,
+    drafted/accepted counts and final LCG state equal the oracle's, with a draft that is another
+    model (every draft rejected) and one with the target's weights at a low temperature (drafts
+    accepted and rejected)."""
+    import nanocamelid_amd as nc
+    imgs = {s: nc.synth_gguf(**TINY_UNTIED, seed=s) for s in {71, draft_seed}}
+    gt, gd = nc.Model(ctx, data=imgs[71]), nc.Model(ctx, data=imgs[draft_seed])
+    ot, od = O.Model(data=imgs[71].tobytes(), nthreads=16), O.Model(data=imgs[draft_seed].tobytes(), nthreads=16)
+    prompt = nc.uniform_prompt(73, 20, 1000)
+    print(f"draft temp loop draft={draft_seed} k={k} T={temp}", flush=True)
+    toks, stats, st = nc.generate_speculative_draft_temp(nc.Session(gt, 512, 16), nc.Session(gd, 512, 16), prompt,
+                                                         40, k, temp)
+    otoks, odrafted, oacc, osteps, ost = O.generate_speculative_draft_temp(O.Session(ot, 512, 16),
+                                                                           O.Session(od, 512, 16), prompt, 40, k, temp)
+    assert np.array_equal(toks, otoks)
+    assert (stats.drafted, stats.accepted, stats.steps, st) == (odrafted, oacc, osteps, ost)
+    if temp < 0.1:
+        assert 0 < stats.accepted < stats.drafted

@@ -1,0 +1,146 @@
+"""The reference's own temperature sampling (CPU): rand_simple, sample_logits and the
+temperature draft-model step, each pinned by an independent restatement.
+
+  rand_simple (inference.rs:4876-4883): Python integers for the 64-bit LCG, numpy float32 for
+    the u32 -> f32 conversion and the division by u32::MAX as f32 (IEEE, correctly rounded);
+  sample_logits (inference.rs:4834-4873): the reference loop emulated in numpy float32 (each
+    subtraction, division, sum and multiply rounded as IEEE f32), with glibc expf (the oracle's
+    or_expf, which Rust's f32::exp calls) for the exponentials;
+  speculative_decoding_step at temp > 0 (speculative.rs:299-494): the step rewritten in Python
+    over the oracle session's forward_pass / prefill_pass_batch / batch_row_logits and the
+    sampler above, against the oracle's C loop: same tokens, counts and final LCG state.
+"""
+import numpy as np
+import pytest
+
+import nanocamelid_amd as nc
+from oracle import oracle as O
+
+F = np.float32
+
+
+def _lcg_py(state, n):
+    out = []
+    for _ in range(n):
+        state = (state * 6364136223846793005 + 1) % (1 << 64)
+        out.append(F(np.uint32(state >> 32)) / F(4294967295))  # u32::MAX as f32 == 2^32
+    return out, state
+
+
+def test_rand_simple_matches_integer_lcg():
+    want, st_end = _lcg_py(O.REFERENCE_RNG_STATE, 2000)
+    st = O.REFERENCE_RNG_STATE
+    for i, w in enumerate(want):
+        u, st = O.rand_simple(st)
+        assert F(u).view(np.uint32) == F(w).view(np.uint32), i
+    assert st == st_end
+    assert all(0.0 <= w <= 1.0 for w in want)
+
+
+def _sample_emulated(logits, temp, state):
+    """inference.rs:4846-4873 step by step in float32."""
+    l = np.asarray(logits, F)
+    mx = l[0]
+    for v in l:
+        if v > mx:
+            mx = v
+    e = np.array([O.expf(F(F(v - mx) / F(temp))) for v in l], F)
+    s = F(0.0)
+    for v in e:
+        s = F(s + v)
+    (u,), state = _lcg_py(state, 1)
+    r = F(u * s)
+    for i, v in enumerate(e):
+        r = F(r - v)
+        if r <= 0:
+            return i, state
+    return len(l) - 1, state
+
+
+@pytest.mark.parametrize("V", [7, 100, 1000])
+@pytest.mark.parametrize("temp", [0.5, 1.0, 1.7])
+def test_sample_logits_matches_float32_emulation(V, temp):
+    rng = np.random.default_rng(V + int(temp * 10))
+    st_o = st_e = O.REFERENCE_RNG_STATE
+    rows = [rng.normal(0, 2, V), np.zeros(V), np.round(rng.normal(0, 1, V) * 4) / 4, np.linspace(-20, 5, V)]
+    for trial in range(40):
+        l = np.asarray(rows[trial % len(rows)], F)
+        io, st_o = O.sample_logits(l, temp, st_o)
+        ie, st_e = _sample_emulated(l, temp, st_e)
+        assert (io, st_o) == (ie, st_e), trial
+
+
+def test_sample_logits_edges():
+    st = O.REFERENCE_RNG_STATE
+    l = np.array([0.5, 3.0, -1.0, 3.0], F)
+    assert O.sample_logits(l, 0.0, st) == (1, st)  # greedy: first maximum, no draw
+    hot = np.full(50, -200.0, F)
+    hot[17] = 0.0
+    for _ in range(20):  # one term carries all the mass (the others underflow to 0)
+        i, st = O.sample_logits(hot, 1.0, st)
+        assert i == 17
+
+
+def _models(spec, seed):
+    img = nc.synth_gguf(**spec, seed=seed)
+    return O.Model(data=img.tobytes(), nthreads=8)
+
+
+TINY = dict(layers=2, embedding_length=256, head_count=4, head_count_kv=2, feed_forward_length=512, vocab_size=1000,
+            context_length=512, tied=0, norm_mode=1)
+
+
+def _step_loop_python(tg, dr, prompt, n_new, k, temp, state, max_batch=16):
+    """speculative.rs:299-494 (no stop tokens) driven as main.rs:9643-9706, in Python."""
+    n = len(prompt)
+    for s in (tg, dr):
+        for i in range(0, n - 1, 16):
+            s.prefill_pass_batch(prompt[i:min(i + 16, n - 1)], i)
+    tl = tg.forward_pass(prompt[-1], n - 1)
+    dl = dr.forward_pass(prompt[-1], n - 1)
+    pos, out, drafted, accepted, steps = n, [], 0, 0, 0
+    while len(out) < n_new:
+        kk = min(k, n_new - len(out), max_batch, 512 - (pos + 1))
+        drafts = []
+        for i in range(kk):
+            t, state = O.sample_logits(dl, temp, state)
+            drafts.append(t)
+            dl = dr.forward_pass(t, pos + i)
+        tg.prefill_pass_batch(np.array(drafts, np.uint32), pos)
+        drafted += kk
+        emitted = []
+        for i in range(kk):
+            lg = tl if i == 0 else tg.batch_row_logits(i - 1)
+            tt, state = O.sample_logits(lg, temp, state)
+            if tt == drafts[i]:
+                accepted += 1
+                emitted.append(tt)
+                continue
+            emitted.append(tt)
+            tl, dl = tg.forward_pass(tt, pos + i), dr.forward_pass(tt, pos + i)
+            pos += i + 1
+            break
+        else:
+            tt, state = O.sample_logits(tg.batch_row_logits(kk - 1), temp, state)
+            emitted.append(tt)
+            tl, dl = tg.forward_pass(tt, pos + kk), dr.forward_pass(tt, pos + kk)
+            pos += kk + 1
+        out += emitted[:n_new - len(out)]
+        steps += 1
+    return np.array(out, np.uint32), drafted, accepted, steps, state
+
+
+@pytest.mark.parametrize("draft_seed,k,temp", [(72, 2, 0.3), (71, 4, 1.0), (71, 4, 0.05)])
+def test_speculative_draft_temp_loop_matches_python_restatement(draft_seed, k, temp):
+    """Another model as draft (every draft rejected), and the target's own weights as draft, where
+    a low temperature makes the two draws agree often: acceptances and rejections both occur."""
+    tm, dm = _models(TINY, 71), _models(TINY, draft_seed)
+    prompt = nc.uniform_prompt(73, 20, 1000)
+    res_py = _step_loop_python(O.Session(tm, 512, 16), O.Session(dm, 512, 16), prompt, 40, k, temp,
+                               O.REFERENCE_RNG_STATE)
+    res_c = O.generate_speculative_draft_temp(O.Session(tm, 512, 16), O.Session(dm, 512, 16), prompt, 40, k, temp)
+    assert np.array_equal(res_py[0], res_c[0])
+    assert res_py[1:] == res_c[1:]
+    assert len(set(res_c[0].tolist())) >= 8
+    if temp < 0.1:
+        assert 0 < res_c[2] < res_c[1]  # drafted, accepted
