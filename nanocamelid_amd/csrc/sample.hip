@@ -1,9 +1,11 @@
-// Stochastic speculative acceptance on the device.
+// Sampling on the device: the reference's sample_logits, and stochastic speculative acceptance.
 //
-// Temperature softmax over the vocabulary, the min(1, p/q) acceptance test and
-// fixed-point inverse-CDF sampling driven by Philox4x32-10 uniforms.  The reference has
-// no speculative sampler (its temperature path matches tokens, speculative.rs:403, and
-// samples with an LCG, inference.rs:4834-4883); this specification is the library's own:
+// sample_logits (inference.rs:4834-4873) is restated exactly (lcg_walk_kernel, below): the
+// uniform comes from the caller's copy of the reference's LCG, and the reference's f32 walk
+// over the vocabulary is evaluated bit for bit.  Its speculative temperature path matches
+// sampled tokens (speculative.rs:403).  The speculative sampler here is the library's own
+// specification: temperature softmax over the vocabulary, the min(1, p/q) acceptance test and
+// fixed-point inverse-CDF sampling driven by Philox4x32-10 uniforms:
 //
 //   probs     p_j = e_j * (1 / S),  e_j = expf((l_j - max) / T),  S = sum_j e_j taken left
 //             to right in f32 (the reference's softmax formula, inference.rs:3522-3540,
