@@ -771,9 +771,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         pg.xs8 = s->xs8;
         pg.N = n;
         pg.epi = EPI_SWIGLU_Q8;
-        pg.xq_out = s->xq;  // gate/up read xq[.][0..d) and write xq[.][0..F): different kernels
-        pg.xs_out = s->xs;
-                pg.F = F;
+        pg.F = F;
         // In-place would race (readers of row n's block b vs writers); use the upper half.
         pg.xq_out = s->xq + (size_t)s->max_batch * s->maxw;
         pg.xs_out = s->xs + (size_t)s->max_batch * (s->maxw / 32);
