@@ -164,7 +164,8 @@ int launch_prompt_qkv_rope(const float* y, int N, int start, int aw, int kw, int
                            const float* rope_tab, float* q_out, float* kcache, float* vcache, int max_ctx,
                            hipStream_t stream);
 int launch_prompt_residual(const float* y, float* hidden, int N, int d, hipStream_t stream);
-int launch_prompt_swiglu_q8(const float* y, int N, int F, int8_t* xq, float* xs, int32_t* xs8, hipStream_t stream);
+int launch_prompt_swiglu_q8(const float* y, int N, int F, int8_t* xq, float* xs, int32_t* xs8, hipStream_t stream,
+                            bool split = false);
 int launch_prompt_positions(int32_t* d, int start, int stride, int count, hipStream_t stream);
 constexpr int kPromptRows = 256;   // tokens per prompt pass
 constexpr int kPromptGroup = 64;   // rows per attention launch inside a prompt pass (score buffer rows)

@@ -576,17 +576,18 @@ int launch_prompt_residual(const float* y, float* hidden, int N, int d, hipStrea
 }
 
 // fused_silu_mul (inference.rs:3367-3390) on the interleaved gate|up output (64-row group t:
-// gate rows 32t..32t+31 in rows 64t..64t+31, the matching up rows in 64t+32..64t+63), then
-// quantize_f32_to_q8_0 of each 32-wide block (inference.rs:4034-4041), as the EPI_SWIGLU_Q8
-// epilogue.  One half-wave per (token, block).
+// gate rows 32t..32t+31 in rows 64t..64t+31, the matching up rows in 64t+32..64t+63) or, with
+// split, on gate rows 0..F-1 followed by up rows F..2F-1; then quantize_f32_to_q8_0 of each
+// 32-wide block (inference.rs:4034-4041), as the EPI_SWIGLU_Q8 epilogue.  One half-wave per
+// (token, block).
 __global__ void prompt_swiglu_q8_kernel(const float* y, int F, int total_blocks, int8_t* xq, float* xs,
-                                        int32_t* xs8) {
+                                        int32_t* xs8, int split) {
     const int hb = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;  // (token, block) index
     if (hb >= total_blocks) return;                                 // whole half-waves exit together
     const int l = threadIdx.x & 31;
     const int nbf = F / 32, n = hb / nbf, t = hb % nbf;
-    const float* yr = y + (size_t)n * 2 * F + 64 * t;
-    const float g = yr[l], up = yr[32 + l];
+    const float* yr = y + (size_t)n * 2 * F + (split ? 32 * t : 64 * t);
+    const float g = yr[l], up = yr[(split ? F : 32) + l];
     const float sig = 1.0f / (1.0f + expf_glibc(-g));
     const float v = g * sig * up;
     const float amax = halfwave_amax(v);
@@ -600,11 +601,12 @@ __global__ void prompt_swiglu_q8_kernel(const float* y, int F, int total_blocks,
     }
 }
 
-int launch_prompt_swiglu_q8(const float* y, int N, int F, int8_t* xq, float* xs, int32_t* xs8, hipStream_t st) {
+int launch_prompt_swiglu_q8(const float* y, int N, int F, int8_t* xq, float* xs, int32_t* xs8, hipStream_t st,
+                            bool split) {
     if (F % 32) return fail(NC_EINVAL, "prompt SwiGLU: width must be a multiple of 32");
     const int total = N * (F / 32);
     hipLaunchKernelGGL(prompt_swiglu_q8_kernel, dim3((total * 32 + 255) / 256), dim3(256), 0, st, y, F, total, xq, xs,
-                       xs8);
+                       xs8, split ? 1 : 0);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }

@@ -2,6 +2,7 @@
 // the Llama model loader, sessions (KV cache + workspaces + stream), the verify pass,
 // the decode loops and the C ABI declared in include/nanocamelid_gpu.h.
 #include <algorithm>
+#include <array>
 #include <chrono>
 #include <cmath>
 #include <cstring>
@@ -29,6 +30,14 @@ struct LayerDev {
     float* attn_norm = nullptr;
     float* ffn_norm = nullptr;
     nc::QMatDev qkv, wo, gateup, down;
+    // q, k, v (gate, up) as separate matrices when their types differ or are not Q4_0 / Q4_K
+    // (llama.cpp's Q4_K_M files keep attn_v and ffn_down in Q6_K on some layers): each matmul
+    // then stores plain rows and the epilogue runs as its own kernel
+    bool split_qkv = false, split_gateup = false;
+    nc::QMatDev q, k, v, gate, up;
+    // every matrix of the layer, for loops over them (unused ones have dev == nullptr)
+    std::array<nc::QMatDev*, 9> all() { return {&qkv, &wo, &gateup, &down, &q, &k, &v, &gate, &up}; }
+    std::array<const nc::QMatDev*, 9> all() const { return {&qkv, &wo, &gateup, &down, &q, &k, &v, &gate, &up}; }
 };
 
 }  // namespace
@@ -69,6 +78,7 @@ struct nc_session {
     int32_t* d_pos = nullptr;
     int32_t* d_result = nullptr;
     uint32_t* d_samp = nullptr;  // [kSampleMaxRows] ids drawn by sample_logits
+    float* ybuf = nullptr;       // [B][max(q|k|v rows, 2F, d)] plain matmul rows of split layers
     float* rope_tab = nullptr;
     // pinned host mirrors
     uint32_t* h_toks = nullptr;
@@ -494,9 +504,8 @@ static const GgufTensor* matrix_desc(const GgufFile& g, const std::string& name,
         return nullptr;
     }
     if (t->type != NC_TYPE_Q4_0 && t->type != NC_TYPE_Q4_K && !(allow_q6k && t->type == NC_TYPE_Q6_K)) {
-        *err = fail(NC_EFORMAT, "tensor " + name + ": only Q4_0 and Q4_K matrices are supported" +
-                                    (allow_q6k ? " (and Q6_K for the head)" : "") + ", got GGML type " +
-                                    std::to_string(t->type));
+        *err = fail(NC_EFORMAT, "tensor " + name + ": only Q4_0, Q4_K" + (allow_q6k ? " and Q6_K" : "") +
+                                    " matrices are supported, got GGML type " + std::to_string(t->type));
         return nullptr;
     }
     std::string e;
@@ -512,7 +521,7 @@ static void free_model(nc_model* m) {
     for (void* p : m->allocs) (void)hipFree(p);
     if (m->head.dev) (void)hipFree(m->head.dev);
     for (auto& l : m->layers)
-        for (auto* q : {&l.qkv, &l.wo, &l.gateup, &l.down})
+        for (auto* q : l.all())
             if (q->dev) (void)hipFree(q->dev);
     delete m;
 }
@@ -620,34 +629,48 @@ static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_lo
         if ((rc = upload_f32(m->allocs, tmp, &L.attn_norm))) return rc;
         if ((rc = tensor_to_f32(g, b + "ffn_norm.weight", tmp))) return rc;
         if ((rc = upload_f32(m->allocs, tmp, &L.ffn_norm))) return rc;
+        // each matrix keeps its own type, as matmul_quantized_batch dispatches per matrix
+        // (inference.rs:1246-1303)
         int e = 0;
-        const GgufTensor* tq = matrix_desc(g, b + "attn_q.weight", aw, d, &e);
-        const GgufTensor* tk = tq ? matrix_desc(g, b + "attn_k.weight", kw, d, &e) : nullptr;
-        const GgufTensor* tv = tk ? matrix_desc(g, b + "attn_v.weight", kw, d, &e) : nullptr;
-        const GgufTensor* to = tv ? matrix_desc(g, b + "attn_output.weight", d, aw, &e) : nullptr;
-        const GgufTensor* tg = to ? matrix_desc(g, b + "ffn_gate.weight", F, d, &e) : nullptr;
-        const GgufTensor* tu = tg ? matrix_desc(g, b + "ffn_up.weight", F, d, &e) : nullptr;
-        const GgufTensor* tdn = tu ? matrix_desc(g, b + "ffn_down.weight", d, F, &e) : nullptr;
+        const GgufTensor* tq = matrix_desc(g, b + "attn_q.weight", aw, d, &e, true);
+        const GgufTensor* tk = tq ? matrix_desc(g, b + "attn_k.weight", kw, d, &e, true) : nullptr;
+        const GgufTensor* tv = tk ? matrix_desc(g, b + "attn_v.weight", kw, d, &e, true) : nullptr;
+        const GgufTensor* to = tv ? matrix_desc(g, b + "attn_output.weight", d, aw, &e, true) : nullptr;
+        const GgufTensor* tg = to ? matrix_desc(g, b + "ffn_gate.weight", F, d, &e, true) : nullptr;
+        const GgufTensor* tu = tg ? matrix_desc(g, b + "ffn_up.weight", F, d, &e, true) : nullptr;
+        const GgufTensor* tdn = tu ? matrix_desc(g, b + "ffn_down.weight", d, F, &e, true) : nullptr;
         if (!tdn) return e;
         const int ty = (int)tq->type;
-        if (tk->type != (uint32_t)ty || tv->type != (uint32_t)ty || tg->type != tu->type)
-            return fail(NC_EFORMAT, "q/k/v (and gate/up) must share one quantisation type");
-        if ((rc = upload_matrix(ty, aw + 2 * kw, d,
-                                {{g.data + tq->offset, aw, 0, -1}, {g.data + tk->offset, kw, aw, -1},
-                                 {g.data + tv->offset, kw, aw + kw, -1}},
-                                L.qkv)))
-            return rc;
-        if ((rc = upload_matrix((int)to->type, d, aw, {{g.data + to->offset, d, 0, -1}}, L.wo))) return rc;
-        if ((rc = upload_matrix((int)tg->type, 2 * F, d, {{g.data + tg->offset, F, 0, 0}, {g.data + tu->offset, F, 0, 1}},
-                                L.gateup)))
-            return rc;
-        if ((rc = upload_matrix((int)tdn->type, d, F, {{g.data + tdn->offset, d, 0, -1}}, L.down))) return rc;
+        const auto fusable = [](uint32_t t) { return t == NC_TYPE_Q4_0 || t == NC_TYPE_Q4_K; };
+        const auto one = [&](const GgufTensor* t, int64_t rows, int64_t cols, QMatDev& out) {
+            return upload_matrix((int)t->type, rows, cols, {{g.data + t->offset, rows, 0, -1}}, out);
+        };
+        if (fusable(tq->type) && tk->type == tq->type && tv->type == tq->type) {
+            if ((rc = upload_matrix(ty, aw + 2 * kw, d,
+                                    {{g.data + tq->offset, aw, 0, -1}, {g.data + tk->offset, kw, aw, -1},
+                                     {g.data + tv->offset, kw, aw + kw, -1}},
+                                    L.qkv)))
+                return rc;
+        } else {
+            L.split_qkv = true;
+            if ((rc = one(tq, aw, d, L.q)) || (rc = one(tk, kw, d, L.k)) || (rc = one(tv, kw, d, L.v))) return rc;
+        }
+        if ((rc = one(to, d, aw, L.wo))) return rc;
+        if (fusable(tg->type) && tu->type == tg->type) {
+            if ((rc = upload_matrix((int)tg->type, 2 * F, d,
+                                    {{g.data + tg->offset, F, 0, 0}, {g.data + tu->offset, F, 0, 1}}, L.gateup)))
+                return rc;
+        } else {
+            L.split_gateup = true;
+            if ((rc = one(tg, F, d, L.gate)) || (rc = one(tu, F, d, L.up))) return rc;
+        }
+        if ((rc = one(tdn, d, F, L.down))) return rc;
         wtype = ty;
     }
     c.weight_type = wtype;
     int64_t devb = m->head.dev_bytes, algo = m->head.algo_bytes;
     for (auto& L : m->layers)
-        for (auto* q : {&L.qkv, &L.wo, &L.gateup, &L.down}) {
+        for (auto* q : L.all()) {
             devb += q->dev_bytes;
             algo += q->algo_bytes;
         }
@@ -694,6 +717,33 @@ static int flush_timing(nc_session* s) {
     return NC_OK;
 }
 
+// A matmul of the session's quantised rows (xq / xs / xs8) stored as plain f32 rows.
+static GemmParams plain_rows(const nc_session* s, int n, float* out, int ld_out) {
+    GemmParams p;
+    p.kernel = s->ctx->gemm_kernel;
+    p.x = s->xq;
+    p.xs = s->xs;
+    p.xs8 = s->xs8;
+    p.N = n;
+    p.epi = EPI_STORE;
+    p.out = out;
+    p.ld_out = ld_out;
+    return p;
+}
+
+// hidden += matmul (the residual adds, inference.rs:3985, 4073): in the epilogue, or for
+// Q6_K matrices (plain and head outputs only) as plain rows and a separate add.
+static int residual_gemm(nc_session* s, const QMatDev& w, GemmParams& p, int n) {
+    if (w.type != NC_TYPE_Q6_K) return timed_gemm(s, w, p);
+    GemmParams pp = p;
+    pp.epi = EPI_STORE;
+    pp.out = s->ybuf;
+    pp.ld_out = (int)w.rows;
+    int rc = timed_gemm(s, w, pp);
+    if (!rc) rc = launch_prompt_residual(s->ybuf, p.out, n, (int)w.rows, s->stream);
+    return rc;
+}
+
 // One forward over the n tokens already in d_toks at positions start_pos..: embedding,
 // all layers (run_layer_range_batch, inference.rs:3747-4111), final norm, head and
 // per-row argmax.  Writes d_preds and logits.
@@ -734,7 +784,18 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         p.kcache = s->kcache + li * layer_kv;
         p.vcache = s->vcache + li * layer_kv;
         p.d_pos = s->d_pos;
-        if ((rc = timed_gemm(s, L.qkv, p))) return rc;
+        if (!L.split_qkv) {
+            if ((rc = timed_gemm(s, L.qkv, p))) return rc;
+        } else {
+            // q, k, v rows side by side in ybuf, then RoPE and the cache stores as one kernel
+            const int ldy = aw + 2 * kw;
+            const std::pair<const QMatDev*, int> parts[3] = {{&L.q, 0}, {&L.k, aw}, {&L.v, aw + kw}};
+            for (const auto& [w, off] : parts)
+                if ((rc = timed_gemm(s, *w, plain_rows(s, n, s->ybuf + off, ldy)))) return rc;
+            if ((rc = launch_prompt_qkv_rope(s->ybuf, n, (int)start_pos, aw, kw, hd, p.rope_half, s->rope_tab, s->q,
+                                             p.kcache, p.vcache, (int)s->ctx_stride, st)))
+                return rc;
+        }
         AttnParams a;
         a.q = s->q;
         a.kcache = p.kcache;
@@ -761,7 +822,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         po.epi = EPI_RESIDUAL;
         po.out = s->hidden;
         po.ld_out = d;
-        if ((rc = timed_gemm(s, L.wo, po))) return rc;
+        if ((rc = residual_gemm(s, L.wo, po, n))) return rc;
         if ((rc = launch_rmsnorm_q8(s->hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
             return rc;
         GemmParams pg;
@@ -776,7 +837,15 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         pg.xq_out = s->xq + (size_t)s->max_batch * s->maxw;
         pg.xs_out = s->xs + (size_t)s->max_batch * (s->maxw / 32);
         pg.xs8_out = s->xs8 + (size_t)s->max_batch * (s->maxw / 32);
-        if ((rc = timed_gemm(s, L.gateup, pg))) return rc;
+        if (!L.split_gateup) {
+            if ((rc = timed_gemm(s, L.gateup, pg))) return rc;
+        } else {
+            // gate rows then up rows in ybuf, then SwiGLU and the Q8_0 blocks as one kernel
+            if ((rc = timed_gemm(s, L.gate, plain_rows(s, n, s->ybuf, 2 * F))) ||
+                (rc = timed_gemm(s, L.up, plain_rows(s, n, s->ybuf + F, 2 * F))) ||
+                (rc = launch_prompt_swiglu_q8(s->ybuf, n, F, pg.xq_out, pg.xs_out, pg.xs8_out, st, true)))
+                return rc;
+        }
         GemmParams pd;
         pd.kernel = s->ctx->gemm_kernel;
         pd.x = pg.xq_out;
@@ -786,7 +855,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         pd.epi = EPI_RESIDUAL;
         pd.out = s->hidden;
         pd.ld_out = d;
-        if ((rc = timed_gemm(s, L.down, pd))) return rc;
+        if ((rc = residual_gemm(s, L.down, pd, n))) return rc;
     }
     s->last_n = head ? n : 0;
     if (!head) return NC_OK;  // a prompt chunk whose logits nobody reads (prefill_pass_batch)
@@ -864,10 +933,14 @@ static bool prompt_matrix_ok(const QMatDev& q) {
     return false;
 }
 
+// Prompt passes need every layer matrix on a prompt kernel and the fused q,k,v and gate,up
+// layouts; other models prefill through 16-row passes.
 static bool prompt_path_ok(const nc_model* m) {
-    for (const LayerDev& L : m->layers)
+    for (const LayerDev& L : m->layers) {
+        if (L.split_qkv || L.split_gateup) return false;
         for (const QMatDev* q : {&L.qkv, &L.wo, &L.gateup, &L.down})
             if (!prompt_matrix_ok(*q)) return false;
+    }
     return true;
 }
 
@@ -1437,7 +1510,10 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
         (rc = dev_alloc(s->allocs, &s->part_idx, B * m->head.tiles)) ||
         (rc = dev_alloc(s->allocs, &s->d_toks, B)) || (rc = dev_alloc(s->allocs, &s->d_preds, B)) ||
         (rc = dev_alloc(s->allocs, &s->d_pos, 4)) || (rc = dev_alloc(s->allocs, &s->d_result, 4)) ||
-        (rc = dev_alloc(s->allocs, &s->d_samp, (size_t)kSampleMaxRows)))
+        (rc = dev_alloc(s->allocs, &s->d_samp, (size_t)kSampleMaxRows)) ||
+        (rc = dev_alloc(s->allocs, &s->ybuf,
+                        B * std::max({c.attention_output_width + 2 * c.kv_width, 2 * c.feed_forward_length,
+                                      c.embedding_length}))))
         return rc;
     NC_HIP(hipMemset(s->kcache, 0, kv * 4));
     NC_HIP(hipMemset(s->vcache, 0, kv * 4));

@@ -333,13 +333,14 @@ bool build_model(or_model* m, const uint8_t* data, size_t size, std::string& err
         std::string b = "blk." + std::to_string(i) + ".";
         if (!load_f32_tensor(g, b + "attn_norm.weight", ly.attn_norm, err)) return false;
         if (!load_f32_tensor(g, b + "ffn_norm.weight", ly.ffn_norm, err)) return false;
-        if (!load_qmat(g, b + "attn_q.weight", m->attn_w, m->d, ly.wq, err)) return false;
-        if (!load_qmat(g, b + "attn_k.weight", m->kv_w, m->d, ly.wk, err)) return false;
-        if (!load_qmat(g, b + "attn_v.weight", m->kv_w, m->d, ly.wv, err)) return false;
-        if (!load_qmat(g, b + "attn_output.weight", m->d, m->attn_w, ly.wo, err)) return false;
-        if (!load_qmat(g, b + "ffn_gate.weight", m->F, m->d, ly.w1, err)) return false;
-        if (!load_qmat(g, b + "ffn_up.weight", m->F, m->d, ly.w3, err)) return false;
-        if (!load_qmat(g, b + "ffn_down.weight", m->d, m->F, ly.w2, err)) return false;
+        // each matrix in its own type (Q4_0, Q4_K or Q6_K), as matmul_quantized_batch dispatches
+        if (!load_qmat(g, b + "attn_q.weight", m->attn_w, m->d, ly.wq, err, true)) return false;
+        if (!load_qmat(g, b + "attn_k.weight", m->kv_w, m->d, ly.wk, err, true)) return false;
+        if (!load_qmat(g, b + "attn_v.weight", m->kv_w, m->d, ly.wv, err, true)) return false;
+        if (!load_qmat(g, b + "attn_output.weight", m->d, m->attn_w, ly.wo, err, true)) return false;
+        if (!load_qmat(g, b + "ffn_gate.weight", m->F, m->d, ly.w1, err, true)) return false;
+        if (!load_qmat(g, b + "ffn_up.weight", m->F, m->d, ly.w3, err, true)) return false;
+        if (!load_qmat(g, b + "ffn_down.weight", m->d, m->F, ly.w2, err, true)) return false;
         m->wtype = ly.wq.type;
     }
     return true;

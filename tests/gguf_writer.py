@@ -134,6 +134,33 @@ def random_blocks(ty, nblk, seed):
 
 
 
+def q6_k_weights(nblk, seed, std=0.02):
+    """Random Q6_K blocks whose elements d * scale * (q - 32) have a standard deviation near
+    std (random 6-bit values, scales in [-24, 24], d set from std), like a quantised N(0, std)
+    weight matrix rather than random_blocks' full-range scales."""
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, (nblk, 210), dtype=np.uint8)
+    b[:, 192:208] = rng.integers(-24, 25, (nblk, 16)).astype(np.int8).view(np.uint8)
+    d = rng.uniform(0.6, 1.4, nblk) * std / (18.5 * 14.1)  # std of (q - 32) and of the scales
+    b[:, 208:210] = d.astype(np.float16).view(np.uint8).reshape(nblk, 2)
+    return b.ravel()
+
+
+def with_types(image, types, seed=0):
+    """The GGUF image with the named matrices replaced by random blocks of another type
+    (Q6_K: q6_k_weights; Q4_0: random_blocks), the way llama.cpp's Q4_K_M recipe keeps some
+    attn_v / ffn_down matrices in Q6_K."""
+    meta, ts = read(bytes(image))
+    out = []
+    for i, (n, dims, ty, raw) in enumerate(ts):
+        if n in types:
+            ty = types[n]
+            nblk = int(np.prod(dims)) // LAYOUT[ty][0]
+            raw = (q6_k_weights(nblk, seed + i) if ty == 14 else random_blocks(ty, nblk, seed + i)).tobytes()
+        out.append((n, dims, ty, raw))
+    return write(meta, out)
+
+
 def nbytes(dims, ty) -> int:
     bs, ts = LAYOUT[ty]
     return int(np.prod(dims)) // bs * ts

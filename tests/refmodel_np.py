@@ -28,7 +28,7 @@ import numpy as np
 _FIXED = {0: ("<B", 1), 1: ("<b", 1), 2: ("<H", 2), 3: ("<h", 2), 4: ("<I", 4), 5: ("<i", 4), 6: ("<f", 4),
           7: ("<?", 1), 10: ("<Q", 8), 11: ("<q", 8), 12: ("<d", 8)}
 # tensor types used here: (block elements, block bytes)
-_LAYOUT = {0: (1, 4), 1: (1, 2), 2: (32, 18), 12: (256, 144)}
+_LAYOUT = {0: (1, 4), 1: (1, 2), 2: (32, 18), 12: (256, 144), 14: (256, 210)}
 
 
 class Gguf:
@@ -97,6 +97,8 @@ class Gguf:
             v = _dequant_q4_0(b)
         elif t == 12:
             v = _dequant_q4_k(b)
+        elif t == 14:
+            v = _dequant_q6_k(b)
         else:
             raise ValueError(f"type {t}")
         return v.reshape(list(reversed(dims))) if len(dims) > 1 else v
@@ -128,6 +130,27 @@ def _dequant_q4_k(b):
         nib = (byte >> 4) if hi else (byte & 0x0F)
         out[:, j * 32:(j + 1) * 32] = (d * s)[:, None] * nib - (dmin * m)[:, None]
     return out.reshape(-1)
+
+
+def _dequant_q6_k(b):
+    """Q6_K super-blocks of 256 (ql 128 | qh 64 | int8 scales 16 | f16 d), in llama.cpp's
+    published layout: per 128-element half h and l < 32, element 128h + l + 32k takes the low
+    (k = 0, 1) or high (k = 2, 3) nibble of ql[64h + l + 32(k % 2)], two bits 2k.. of
+    qh[32h + l] on top, minus 32, times d * scale[8h + l // 16 + 2k]."""
+    blk = b.reshape(-1, 210)
+    ql = blk[:, :128].astype(np.int64)
+    qh = blk[:, 128:192].astype(np.int64)
+    sc = blk[:, 192:208].view(np.int8).astype(np.float64)
+    d = blk[:, 208:210].copy().view(np.float16).astype(np.float64)[:, 0]
+    y = np.empty((blk.shape[0], 256))
+    for h in range(2):
+        for l in range(32):
+            lo, hi, bits = ql[:, 64 * h + l], ql[:, 64 * h + l + 32], qh[:, 32 * h + l]
+            qs = ((lo & 15) | ((bits & 3) << 4), (hi & 15) | (((bits >> 2) & 3) << 4),
+                  (lo >> 4) | (((bits >> 4) & 3) << 4), (hi >> 4) | (((bits >> 6) & 3) << 4))
+            for k in range(4):
+                y[:, 128 * h + l + 32 * k] = d * sc[:, 8 * h + l // 16 + 2 * k] * (qs[k] - 32)
+    return y.ravel()
 
 
 def q8_0(x: np.ndarray) -> np.ndarray:

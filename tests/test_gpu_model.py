@@ -378,6 +378,42 @@ def test_q6_k_head_model_logits(ctx):
         pos += n
 
 
+@pytest.mark.parametrize("base", ["q4_k", "q4_0"])
+def test_mixed_type_layers_model_logits(ctx, base):
+    """Layers whose matrices differ in type, as in llama.cpp's Q4_K_M files (attn_v and ffn_down
+    in Q6_K on some layers): q,k,v and gate,up that no longer share one type run as separate
+    matmuls storing plain rows, followed by the RoPE / cache and SwiGLU kernels, and Q6_K
+    attn_output / ffn_down add their rows to the residual in a separate kernel.  A 40-token
+    prefill (16-row passes: the prompt passes decline these models), then verify logits and
+    greedy predictions bit-identical to the oracle at widths 1, 5, 16 and 9."""
+    import nanocamelid_amd as nc
+    from tests import gguf_writer as GW
+    from tests.test_reference_forward import mixed_model_image, MIXED_SPEC
+    if base == "q4_k":
+        img, V = mixed_model_image(), MIXED_SPEC["vocab_size"]
+    else:
+        types = {"blk.0.attn_v.weight": 14, "blk.0.ffn_up.weight": 14, "blk.1.ffn_down.weight": 14,
+                 "blk.1.attn_output.weight": 14}
+        img = np.frombuffer(GW.with_types(nc.synth_gguf(**TINY, seed=29), types, seed=29), np.uint8)
+        V = TINY["vocab_size"]
+    gm, om = nc.Model(ctx, data=img), O.Model(data=img.tobytes())
+    gs, os_ = nc.Session(gm, 128, 16), O.Session(om, 128, 16)
+    prompt = nc.uniform_prompt(31, 40, V)
+    gs.prefill_pass_batch(prompt, 0, want_logits=False)
+    for i in range(0, 40, 16):
+        os_.prefill_pass_batch(prompt[i:i + 16], i)
+    pos = 40
+    for n in (1, 5, 16, 9):
+        batch = nc.uniform_prompt(400 + n, n, V)
+        _, _, _, preds = gs.verify_greedy(batch, pos)
+        opreds, _, ologits = os_.verify_greedy(batch, pos, want_logits=True)
+        assert np.array_equal(preds, opreds), n
+        for i in range(n):
+            assert _same(gs.logits(i), ologits[i]), (n, i)
+        pos += n
+    assert len(set(preds.tolist())) >= 3
+
+
 def test_loader_refuses_output_major_matrix(ctx):
     import nanocamelid_amd as nc
     from tests import gguf_writer as GW

@@ -153,3 +153,36 @@ def test_rope_scaling_regimes():
     m = R.Model.__new__(R.Model)
     m.base, m.rope_dim, m.rope_scaling = base, rope_dim, sc
     assert np.allclose(th1, m.theta(), rtol=1e-6, atol=0)
+
+
+def test_q6_k_float64_decode_matches_oracle():
+    """The float64 Q6_K decode against the oracle's (itself pinned by the reference's Q6_K known
+    answers), on realistic and full-range random blocks."""
+    from tests import gguf_writer as GW
+    for raw in (GW.q6_k_weights(40, seed=1), GW.random_blocks(14, 40, seed=2)):
+        got = O.dequantize_f32(14, raw, 40 * 256).astype(np.float64)
+        ref = R._dequant_q6_k(np.asarray(raw, np.uint8))
+        assert np.allclose(got, ref, rtol=1e-6, atol=0)
+        assert np.abs(ref).max() > 0
+
+
+# A Q4_K model with some matrices in other types, as llama.cpp's Q4_K_M recipe stores attn_v
+# and ffn_down in Q6_K on some layers: q,k,v and gate,up then no longer share one type.
+MIXED_SPEC = dict(layers=2, embedding_length=512, head_count=4, head_count_kv=2, feed_forward_length=1024,
+                  vocab_size=500, tied=0, norm_mode=1, weight_type=nc.NC_TYPE_Q4_K, context_length=256)
+MIXED_TYPES = {"blk.0.attn_v.weight": 14, "blk.0.attn_output.weight": 14, "blk.1.ffn_down.weight": 14,
+               "blk.1.ffn_gate.weight": 14, "blk.1.attn_k.weight": 2}
+
+
+def mixed_model_image(seed=23):
+    from tests import gguf_writer as GW
+    return np.frombuffer(GW.with_types(nc.synth_gguf(**MIXED_SPEC, seed=seed), MIXED_TYPES, seed=seed), np.uint8)
+
+
+def test_mixed_type_layers_match_float64_forward():
+    img = mixed_model_image()
+    toks = nc.uniform_prompt(6, 14, MIXED_SPEC["vocab_size"])
+    ref = R.Model(img).logits(toks)
+    rel, argmax_ok, n_clear = _compare(ref, _oracle_logits(img, toks))
+    assert rel < TOL, rel
+    assert argmax_ok and n_clear >= len(toks) // 2
