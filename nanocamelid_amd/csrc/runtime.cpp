@@ -933,14 +933,11 @@ static bool prompt_matrix_ok(const QMatDev& q) {
     return false;
 }
 
-// Prompt passes need every layer matrix on a prompt kernel and the fused q,k,v and gate,up
-// layouts; other models prefill through 16-row passes.
+// Prompt passes take every layer matrix on a prompt kernel, or Q6_K ones in 16-row slices.
 static bool prompt_path_ok(const nc_model* m) {
-    for (const LayerDev& L : m->layers) {
-        if (L.split_qkv || L.split_gateup) return false;
-        for (const QMatDev* q : {&L.qkv, &L.wo, &L.gateup, &L.down})
-            if (!prompt_matrix_ok(*q)) return false;
-    }
+    for (const LayerDev& L : m->layers)
+        for (const QMatDev* q : L.all())
+            if (q->dev && !prompt_matrix_ok(*q) && q->type != NC_TYPE_Q6_K) return false;
     return true;
 }
 
@@ -976,8 +973,46 @@ static int ensure_prompt_bufs(nc_session* s) {
 }
 
 // Prompt matmul of the pass's activations (repacked first into MFMA operand order).
-static int prompt_gemm(nc_session* s, const QMatDev& w, const int8_t* xq, const float* xs, float* out, int n) {
-    return prompt_matmul(w, xq, xs, out, (int)w.rows, n, s->stream, s->p_xm, s->p_xsm, s->p_xam);
+// A prompt pass's matmul into rows of stride ld (default: the matrix's rows): the MFMA prompt
+// kernels, or for Q6_K matrices (no prompt kernel) the verify kernel on 16-row slices.
+static int prompt_gemm(nc_session* s, const QMatDev& w, const int8_t* xq, const float* xs, float* out, int n,
+                       int ld = 0) {
+    if (ld == 0) ld = (int)w.rows;
+    if (prompt_matrix_ok(w)) return prompt_matmul(w, xq, xs, out, ld, n, s->stream, s->p_xm, s->p_xsm, s->p_xam);
+    for (int i = 0; i < n; i += 16) {
+        GemmParams p;
+        p.x = xq + (size_t)i * w.cols;
+        p.xs = xs + (size_t)i * (w.cols / 32);
+        p.xs8 = s->p_xs8 + (size_t)i * (w.cols / 32);
+        p.N = std::min(16, n - i);
+        p.epi = EPI_STORE;
+        p.out = out + (size_t)i * ld;
+        p.ld_out = ld;
+        if (const int rc = launch_gemm(w, p, s->stream)) return rc;
+    }
+    return NC_OK;
+}
+
+// q, k, v rows of a prompt pass side by side in p_y ([n][aw + 2 kw]), fused or split.
+static int prompt_qkv(nc_session* s, const LayerDev& L, int n, int aw, int kw) {
+    if (!L.split_qkv) return prompt_gemm(s, L.qkv, s->p_xq, s->p_xs, s->p_y, n);
+    const int ld = aw + 2 * kw;
+    int rc;
+    if ((rc = prompt_gemm(s, L.q, s->p_xq, s->p_xs, s->p_y, n, ld)) ||
+        (rc = prompt_gemm(s, L.k, s->p_xq, s->p_xs, s->p_y + aw, n, ld)) ||
+        (rc = prompt_gemm(s, L.v, s->p_xq, s->p_xs, s->p_y + aw + kw, n, ld)))
+        return rc;
+    return NC_OK;
+}
+
+// gate and up rows of a prompt pass in p_y: interleaved when fused, gate then up when split.
+static int prompt_gateup(nc_session* s, const LayerDev& L, int n, int F) {
+    if (!L.split_gateup) return prompt_gemm(s, L.gateup, s->p_xq, s->p_xs, s->p_y, n);
+    int rc;
+    if ((rc = prompt_gemm(s, L.gate, s->p_xq, s->p_xs, s->p_y, n, 2 * F)) ||
+        (rc = prompt_gemm(s, L.up, s->p_xq, s->p_xs, s->p_y + F, n, 2 * F)))
+        return rc;
+    return NC_OK;
 }
 
 // One prompt pass over n <= kPromptRows ids p_toks[off..off+n) at positions start..: the
@@ -1001,7 +1036,7 @@ static int run_prompt_pass(nc_session* s, int off, int n, int64_t start) {
         float* kc = s->kcache + li * layer_kv;
         float* vc = s->vcache + li * layer_kv;
         if ((rc = launch_rmsnorm_q8(s->p_hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->p_xq, s->p_xs, s->p_xs8, st)) ||
-            (rc = prompt_gemm(s, L.qkv, s->p_xq, s->p_xs, s->p_y, n)) ||
+            (rc = prompt_qkv(s, L, n, aw, kw)) ||
             (rc = launch_prompt_qkv_rope(s->p_y, n, (int)start, aw, kw, hd, (int)c.rope_dimension_count / 2,
                                          s->rope_tab, s->p_q, kc, vc, (int)s->ctx_stride, st)))
             return rc;
@@ -1028,9 +1063,9 @@ static int run_prompt_pass(nc_session* s, int off, int n, int64_t start) {
         if ((rc = prompt_gemm(s, L.wo, s->p_xq, s->p_xs, s->p_y, n)) ||
             (rc = launch_prompt_residual(s->p_y, s->p_hidden, n, d, st)) ||
             (rc = launch_rmsnorm_q8(s->p_hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->p_xq, s->p_xs, s->p_xs8, st)) ||
-            (rc = prompt_gemm(s, L.gateup, s->p_xq, s->p_xs, s->p_y, n)) ||
+            (rc = prompt_gateup(s, L, n, F)) ||
             // the gate/up matmul has read every activation before the SwiGLU kernel overwrites them
-            (rc = launch_prompt_swiglu_q8(s->p_y, n, F, s->p_xq, s->p_xs, s->p_xs8, st)) ||
+            (rc = launch_prompt_swiglu_q8(s->p_y, n, F, s->p_xq, s->p_xs, s->p_xs8, st, L.split_gateup)) ||
             (rc = prompt_gemm(s, L.down, s->p_xq, s->p_xs, s->p_y, n)) ||
             (rc = launch_prompt_residual(s->p_y, s->p_hidden, n, d, st)))
             return rc;

@@ -384,8 +384,9 @@ def test_mixed_type_layers_model_logits(ctx, base):
     in Q6_K on some layers): q,k,v and gate,up that no longer share one type run as separate
     matmuls storing plain rows, followed by the RoPE / cache and SwiGLU kernels, and Q6_K
     attn_output / ffn_down add their rows to the residual in a separate kernel.  A 40-token
-    prefill (16-row passes: the prompt passes decline these models), then verify logits and
-    greedy predictions bit-identical to the oracle at widths 1, 5, 16 and 9."""
+    prefill (one prompt pass: split matmuls on the MFMA prompt kernels, Q6_K ones in 16-row
+    slices), then verify logits and greedy predictions bit-identical to the oracle at widths
+    1, 5, 16 and 9."""
     import nanocamelid_amd as nc
     from tests import gguf_writer as GW
     from tests.test_reference_forward import mixed_model_image, MIXED_SPEC
