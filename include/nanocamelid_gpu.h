@@ -322,10 +322,15 @@ int nc_generate_speculative_draft(nc_session* target, nc_session* draft, const u
  * the two ids match, and the first mismatch (or, after k matches, the trailing draw) is
  * emitted and run on both models.  *rng_state is the reference's LCG state (rand_simple,
  * src/inference.rs:4876-4883; the reference starts it at 0x123456789abcdef0), advanced by one
- * draw per sample the reference makes, in its order.  temp <= 0: the greedy loop above. */
+ * draw per sample the reference makes, in its order.  temp <= 0: the greedy loop above.
+ * stop[n_stop] (n_stop = 0: none) are the step's is_stop_token ids (speculative.rs:305-447):
+ * a drafted stop token ends drafting without a draft forward, an accepted one ends the
+ * verification with no trailing draw; as the generate loop (src/main.rs:9852-9866), the
+ * first stop token among a step's tokens ends decoding and is not written to out. */
 int nc_generate_speculative_draft_temp(nc_session* target, nc_session* draft, const uint32_t* prompt,
                                        int32_t n_prompt, int32_t n_new, int32_t draft_k, float temp,
-                                       uint64_t* rng_state, uint32_t* out, nc_decode_stats* stats);
+                                       uint64_t* rng_state, const uint32_t* stop, int32_t n_stop, uint32_t* out,
+                                       nc_decode_stats* stats);
 
 /* Draft-model speculative sampling at temperature temp > 0, k+1 form (no reference
  * counterpart; the draft-model loop shape follows src/speculative.rs:299-494).  Both models

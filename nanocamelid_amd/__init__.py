@@ -360,17 +360,19 @@ def generate_speculative_draft(target: Session, draft: Session, prompt, n_new: i
 
 
 def generate_speculative_draft_temp(target: Session, draft: Session, prompt, n_new: int, draft_k: int, temp: float,
-                                    rng_state: int = REFERENCE_RNG_STATE):
-    """speculative_decoding_step at temperature temp (src/speculative.rs:299-494): drafts and
-    target tokens drawn with sample_logits and the reference's LCG, acceptance by id match.
+                                    rng_state: int = REFERENCE_RNG_STATE, stop=()):
+    """speculative_decoding_step at temperature temp (src/speculative.rs:299-494; greedy at
+    temp <= 0): drafts and target tokens drawn with sample_logits and the reference's LCG,
+    acceptance by id match, stop tokens as the step and the generate loop treat them.
     Returns (tokens, stats, rng_state after the run)."""
     a, p = _u32(prompt)
+    sa, sp = _u32(np.array(list(stop) or [0], np.uint32))
     out = np.zeros(n_new, np.uint32)
     st = DecodeStats()
     rs = C.c_uint64(rng_state)
     check(lib().nc_generate_speculative_draft_temp(target.h, draft.h, p, a.size, n_new, draft_k, float(temp),
-                                                   C.byref(rs), out.ctypes.data_as(C.POINTER(C.c_uint32)),
-                                                   C.byref(st)))
+                                                   C.byref(rs), sp, len(stop),
+                                                   out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
     return out[:st.emitted], st, int(rs.value)
 
 

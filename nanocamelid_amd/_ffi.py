@@ -103,7 +103,8 @@ SIGNATURES = {
                                                  _i32, _u32p, C.POINTER(DecodeStats)]),
     "nc_generate_speculative_draft": (C.c_int, [_vp, _vp, _u32p, _i32, _i32, _i32, _u32p, C.POINTER(DecodeStats)]),
     "nc_generate_speculative_draft_temp": (C.c_int, [_vp, _vp, _u32p, _i32, _i32, _i32, C.c_float,
-                                                     C.POINTER(C.c_uint64), _u32p, C.POINTER(DecodeStats)]),
+                                                     C.POINTER(C.c_uint64), _u32p, _i32, _u32p,
+                                                     C.POINTER(DecodeStats)]),
     "nc_generate_speculative_stochastic": (C.c_int, [_vp, _vp, _u32p, _i32, _i32, _i32, C.c_float, C.c_uint64, _u32p,
                                                      C.POINTER(DecodeStats)]),
     "nc_synth_size": (C.c_int, [C.POINTER(SynthSpec), C.POINTER(C.c_uint64)]),

@@ -1803,10 +1803,18 @@ int nc_generate_speculative_ngram(nc_session* s, const uint32_t* prompt, int32_t
     return flush_timing(s);
 }
 
-int nc_generate_speculative_draft(nc_session* tg, nc_session* dr, const uint32_t* prompt, int32_t n_prompt,
-                                  int32_t n_new, int32_t draft_k, uint32_t* out, nc_decode_stats* stats) {
-    if (!tg || !dr || tg == dr || !prompt || !out || n_prompt < 1 || n_new < 1 || draft_k < 1)
+}  // extern "C"
+
+namespace nc {
+// The greedy draft-model loop with stop tokens (is_stop_token of speculative.rs:305-447 and
+// the generate loop's turn end, main.rs:9852-9866; n_stop = 0: none).
+static int draft_loop_greedy(nc_session* tg, nc_session* dr, const uint32_t* prompt, int32_t n_prompt, int32_t n_new,
+                             int32_t draft_k, const uint32_t* stop, int32_t n_stop, uint32_t* out,
+                             nc_decode_stats* stats) {
+    if (!tg || !dr || tg == dr || !prompt || !out || n_prompt < 1 || n_new < 1 || draft_k < 1 || n_stop < 0 ||
+        (n_stop > 0 && !stop))
         return fail(NC_EINVAL, "nc_generate_speculative_draft: bad arguments");
+    const auto is_stop = [&](uint32_t t) { return std::find(stop, stop + n_stop, t) != stop + n_stop; };
     // drafts produced by one model are fed to the other's embedding: the vocabularies must agree
     if (tg->m->cfg.vocab_size != dr->m->cfg.vocab_size) return fail(NC_EINVAL, "target and draft vocabularies differ");
     if (tg->ctx->device != dr->ctx->device) return fail(NC_EINVAL, "target and draft must share a device");
@@ -1819,57 +1827,83 @@ int nc_generate_speculative_draft(nc_session* tg, nc_session* dr, const uint32_t
     const double t1 = now_s();
     int64_t pos = n_prompt, produced = 0, steps = 0, drafted = 0, accepted = 0;
     uint32_t drafts[16], preds[16];
-    while (produced < n_new && pos < tg->max_ctx) {
+    bool saw_stop = false;  // the turn has ended (main.rs:9852-9866)
+    while (!saw_stop && produced < n_new && pos < tg->max_ctx) {
         // speculative.rs:318-321 clamp
         int64_t k = std::min<int64_t>(draft_k, n_new - produced);
         k = std::min<int64_t>(k, tg->max_batch);
         k = std::min<int64_t>(k, tg->max_ctx - (pos + 1));
         k = std::min<int64_t>(k, dr->max_ctx - (pos + 1));
         if (k <= 0) break;
-        // 1. drafting: sample from the draft's live prediction, then a draft forward
-        for (int64_t i = 0; i < k; i++) {
-            drafts[i] = dlive;
-            if ((rc = nc_forward1(dr, drafts[i], pos + i, nullptr, &dlive))) return rc;
+        // 1. drafting: sample from the draft's live prediction, then a draft forward; a
+        // stop token is drafted but not run on the draft and ends drafting (speculative.rs:327-350)
+        int64_t nd = 0;
+        while (nd < k) {
+            drafts[nd] = dlive;
+            if (is_stop(drafts[nd++])) break;
+            if ((rc = nc_forward1(dr, drafts[nd - 1], pos + nd - 1, nullptr, &dlive))) return rc;
         }
         // 2. batched target pass over the drafts
-        if ((rc = upload_toks(tg, drafts, (int)k)) || (rc = run_pass(tg, (int)k, pos)) ||
-            (rc = fetch_preds(tg, (int)k, preds)))
+        if ((rc = upload_toks(tg, drafts, (int)nd)) || (rc = run_pass(tg, (int)nd, pos)) ||
+            (rc = fetch_preds(tg, (int)nd, preds)))
             return rc;
-        // 3. verification (speculative.rs:384-447)
-        drafted += k;
+        // 3. verification (speculative.rs:384-447); an accepted stop token ends it with no
+        // trailing token and ends the turn
+        drafted += nd;
         int64_t i = 0;
-        for (; i < k; i++) {
+        bool stop_accepted = false;
+        for (; i < nd; i++) {
             const uint32_t tt = i == 0 ? tlive : preds[i - 1];
             if (drafts[i] != tt) break;
             accepted++;
+            if (is_stop(tt)) {
+                stop_accepted = true;
+                break;
+            }
             if (produced < n_new) out[produced++] = drafts[i];
+        }
+        steps++;
+        if (stop_accepted) {
+            pos += i + 1;
+            saw_stop = true;
+            break;
         }
         uint32_t fix;
         int64_t at;
-        if (i < k) {
+        if (i < nd) {
             fix = i == 0 ? tlive : preds[i - 1];  // corrective token
             at = pos + i;
         } else {
-            fix = preds[k - 1];  // 4. trailing verified token
-            at = pos + k;
+            fix = preds[nd - 1];  // 4. trailing verified token
+            at = pos + nd;
         }
-        if (produced < n_new) out[produced++] = fix;
         if ((rc = nc_forward1(tg, fix, at, nullptr, &tlive)) || (rc = nc_forward1(dr, fix, at, nullptr, &dlive))) return rc;
+        if (is_stop(fix)) saw_stop = true;  // not part of the stream
+        else if (produced < n_new) out[produced++] = fix;
         pos = at + 1;
-        steps++;
     }
     const double t2 = now_s();
     if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};
     return flush_timing(tg);
 }
+}  // namespace nc
+
+extern "C" {
+
+int nc_generate_speculative_draft(nc_session* tg, nc_session* dr, const uint32_t* prompt, int32_t n_prompt,
+                                  int32_t n_new, int32_t draft_k, uint32_t* out, nc_decode_stats* stats) {
+    return draft_loop_greedy(tg, dr, prompt, n_prompt, n_new, draft_k, nullptr, 0, out, stats);
+}
 
 int nc_generate_speculative_draft_temp(nc_session* tg, nc_session* dr, const uint32_t* prompt, int32_t n_prompt,
-                                       int32_t n_new, int32_t draft_k, float temp, uint64_t* rng_state, uint32_t* out,
-                                       nc_decode_stats* stats) {
+                                       int32_t n_new, int32_t draft_k, float temp, uint64_t* rng_state,
+                                       const uint32_t* stop, int32_t n_stop, uint32_t* out, nc_decode_stats* stats) {
     // sample_logits at temp <= 0 is the argmax and draws nothing: the greedy loop
-    if (!(temp > 0.0f)) return nc_generate_speculative_draft(tg, dr, prompt, n_prompt, n_new, draft_k, out, stats);
-    if (!tg || !dr || tg == dr || !prompt || !out || !rng_state || n_prompt < 1 || n_new < 1 || draft_k < 1)
+    if (!(temp > 0.0f)) return draft_loop_greedy(tg, dr, prompt, n_prompt, n_new, draft_k, stop, n_stop, out, stats);
+    if (!tg || !dr || tg == dr || !prompt || !out || !rng_state || n_prompt < 1 || n_new < 1 || draft_k < 1 ||
+        n_stop < 0 || (n_stop > 0 && !stop))
         return fail(NC_EINVAL, "nc_generate_speculative_draft_temp: bad arguments");
+    const auto is_stop = [&](uint32_t t) { return std::find(stop, stop + n_stop, t) != stop + n_stop; };
     if (tg->m->cfg.vocab_size != dr->m->cfg.vocab_size) return fail(NC_EINVAL, "target and draft vocabularies differ");
     if (tg->ctx->device != dr->ctx->device) return fail(NC_EINVAL, "target and draft must share a device");
     NC_HIP(hipSetDevice(tg->ctx->device));
@@ -1882,21 +1916,25 @@ int nc_generate_speculative_draft_temp(nc_session* tg, nc_session* dr, const uin
     int64_t pos = n_prompt, produced = 0, steps = 0, drafted = 0, accepted = 0;
     uint32_t drafts[16], tt[17];
     float uv[17];
-    while (produced < n_new && pos < tg->max_ctx) {
+    bool saw_stop = false;  // the turn has ended (main.rs:9852-9866)
+    while (!saw_stop && produced < n_new && pos < tg->max_ctx) {
         // speculative.rs:318-321 clamp
         int64_t k = std::min<int64_t>(draft_k, n_new - produced);
         k = std::min<int64_t>(k, tg->max_batch);
         k = std::min<int64_t>(k, tg->max_ctx - (pos + 1));
         k = std::min<int64_t>(k, dr->max_ctx - (pos + 1));
         if (k <= 0) break;
-        // 1. drafting (speculative.rs:327-350): one draw per draft from the draft's live logits
-        for (int64_t i = 0; i < k; i++) {
+        // 1. drafting (speculative.rs:327-350): one draw per draft from the draft's live logits;
+        // a stop token is drafted but not run on the draft and ends drafting
+        int64_t nd = 0;
+        while (nd < k) {
             const float u = lcg_next(rng_state);
-            if ((rc = sample_session_rows(dr, dlive, 1, temp, &u, &drafts[i])) ||
-                (rc = nc_forward1(dr, drafts[i], pos + i, nullptr, nullptr)))
-                return rc;
+            if ((rc = sample_session_rows(dr, dlive, 1, temp, &u, &drafts[nd]))) return rc;
+            if (is_stop(drafts[nd++])) break;
+            if ((rc = nc_forward1(dr, drafts[nd - 1], pos + nd - 1, nullptr, nullptr))) return rc;
             dlive = 0;
         }
+        k = nd;
         // 2. the first verification draw, from the target's live logits, before the batch pass
         // replaces them (speculative.rs:384-403)
         const uint64_t st0 = *rng_state;
@@ -1909,24 +1947,36 @@ int nc_generate_speculative_draft_temp(nc_session* tg, nc_session* dr, const uin
         if ((rc = upload_toks(tg, drafts, (int)k)) || (rc = run_pass(tg, (int)k, pos))) return rc;
         for (int64_t r = 0; r < k; r++) uv[1 + r] = lcg_next(&st);
         if ((rc = sample_session_rows(tg, 0, (int)k, temp, uv + 1, &tt[1]))) return rc;
-        // 4. verification (speculative.rs:384-447) and the trailing token (:450-489)
+        // 4. verification (speculative.rs:384-447) and the trailing token (:450-489); an accepted
+        // stop token ends verification with no trailing draw and ends the turn
         drafted += k;
         int64_t i = 0;
+        bool stop_accepted = false;
         for (; i < k && drafts[i] == tt[i]; i++) {
             accepted++;
+            if (is_stop(drafts[i])) {
+                stop_accepted = true;
+                break;
+            }
             if (produced < n_new) out[produced++] = drafts[i];
         }
-        const uint32_t fix = tt[i];             // corrective (i < k) or trailing (i == k) token
-        const int64_t at = pos + i;
         st = st0;
         for (int64_t r = 0; r <= i; r++) (void)lcg_next(&st);  // draws 0 .. i were made
         *rng_state = st;
-        if (produced < n_new) out[produced++] = fix;
+        steps++;
+        if (stop_accepted) {
+            pos += i + 1;
+            saw_stop = true;
+            break;
+        }
+        const uint32_t fix = tt[i];  // corrective (i < k) or trailing (i == k) token
+        const int64_t at = pos + i;
         if ((rc = nc_forward1(tg, fix, at, nullptr, nullptr)) || (rc = nc_forward1(dr, fix, at, nullptr, nullptr)))
             return rc;
+        if (is_stop(fix)) saw_stop = true;  // not part of the stream
+        else if (produced < n_new) out[produced++] = fix;
         tlive = dlive = 0;
         pos = at + 1;
-        steps++;
     }
     const double t2 = now_s();
     if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};

@@ -628,20 +628,23 @@ int64_t or_generate_speculative_draft(or_session* tg, or_session* dr, const uint
                                       int64_t n_prompt, int64_t n_new, int64_t draft_k,
                                       int64_t prefill_batch, uint32_t* out, int64_t* stats,
                                       int64_t* steps_out) {
-    return or_generate_speculative_draft_temp(tg, dr, prompt, n_prompt, n_new, draft_k, 0.0f, nullptr,
+    return or_generate_speculative_draft_temp(tg, dr, prompt, n_prompt, n_new, draft_k, 0.0f, nullptr, nullptr, 0,
                                               prefill_batch, out, stats, steps_out);
 }
 
 int64_t or_generate_speculative_draft_temp(or_session* tg, or_session* dr, const uint32_t* prompt,
                                            int64_t n_prompt, int64_t n_new, int64_t draft_k, float temp,
-                                           uint64_t* rng_state, int64_t prefill_batch, uint32_t* out,
-                                           int64_t* stats, int64_t* steps_out) {
-    // main.rs:9643-9706 prefill of both models, then speculative.rs:299-494 per step
-    // (no stop tokens); every sample is sample_logits (argmax at temp <= 0).
+                                           uint64_t* rng_state, const uint32_t* stop, int64_t n_stop,
+                                           int64_t prefill_batch, uint32_t* out, int64_t* stats,
+                                           int64_t* steps_out) {
+    // main.rs:9643-9706 prefill of both models, then speculative.rs:299-494 per step with the
+    // generate loop's turn end (main.rs:9852-9866); every sample is sample_logits (argmax at
+    // temp <= 0).
     const int64_t V = tg->m->V;
     uint64_t st_unused = 0;
     uint64_t* rs = rng_state ? rng_state : &st_unused;
     auto sample = [&](const float* l) { return (uint32_t)or_sample_logits(l, V, temp, rs); };
+    auto is_stop = [&](uint32_t t) { return std::find(stop, stop + n_stop, t) != stop + n_stop; };
     prefill(dr, prompt, n_prompt - 1, 0, std::min(prefill_batch, dr->max_batch));
     or_forward_pass(dr, prompt[n_prompt - 1], n_prompt - 1);
     prefill(tg, prompt, n_prompt - 1, 0, prefill_batch);
@@ -649,7 +652,8 @@ int64_t or_generate_speculative_draft_temp(or_session* tg, or_session* dr, const
     int64_t pos = n_prompt, dpos = n_prompt, produced = 0, steps = 0;
     stats[0] = stats[1] = 0;
     std::vector<float> lg(V);
-    while (produced < n_new && pos < tg->max_ctx) {
+    bool saw_stop = false;
+    while (!saw_stop && produced < n_new && pos < tg->max_ctx) {
         int64_t k = std::min(draft_k, n_new - produced);
         k = std::min(k, tg->max_batch);
         k = std::min(k, tg->max_ctx - (pos + 1));
@@ -660,9 +664,11 @@ int64_t or_generate_speculative_draft_temp(or_session* tg, or_session* dr, const
         while ((int64_t)drafts.size() < k) {
             uint32_t t = sample(dr->logits.data());
             drafts.push_back(t);
+            if (is_stop(t)) break;  // speculative.rs:336-338: drafted, never run on the draft
             or_forward_pass(dr, t, cdp);
             cdp++;
         }
+        k = (int64_t)drafts.size();
         or_prefill_pass_batch(tg, drafts.data(), k, pos);
         std::vector<uint32_t> acc;
         bool rejected = false;
@@ -679,6 +685,11 @@ int64_t or_generate_speculative_draft_temp(or_session* tg, or_session* dr, const
             if (drafts[i] == tt) {
                 acc.push_back(tt);
                 stats[1]++;
+                if (is_stop(tt)) {  // speculative.rs:404-412: verification ends, no trailing token
+                    pos = dpos = pos + i + 1;
+                    rejected = true;
+                    break;
+                }
             } else {
                 rejected = true;
                 acc.push_back(tt);
@@ -696,8 +707,13 @@ int64_t or_generate_speculative_draft_temp(or_session* tg, or_session* dr, const
             or_forward_pass(dr, tt, pos + k);
             pos = dpos = pos + k + 1;
         }
-        for (auto t : acc)
+        for (auto t : acc) {
+            if (is_stop(t)) {  // the turn ends; the stop token is not part of the stream
+                saw_stop = true;
+                break;
+            }
             if (produced < n_new) out[produced++] = t;
+        }
         steps++;
     }
     (void)dpos;

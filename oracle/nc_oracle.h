@@ -160,11 +160,15 @@ int64_t or_generate_speculative_draft(or_session* target, or_session* draft,
                                       uint32_t* out, int64_t* stats, int64_t* steps_out);
 /* The same at temperature temp > 0: every draw through or_sample_logits with the LCG state
  * *rng_state, in the reference's order (drafts, then one per verified position, then the
- * trailing token), acceptance by id match. */
+ * trailing token), acceptance by id match.  stop[n_stop]: is_stop_token (a drafted stop token
+ * ends drafting, an accepted one ends verification with no trailing draw) and the generate
+ * loop's turn end (tokens after the first stop token of a step are dropped, the stop token
+ * itself too, and decoding ends). */
 int64_t or_generate_speculative_draft_temp(or_session* target, or_session* draft, const uint32_t* prompt,
                                            int64_t n_prompt, int64_t n_new, int64_t draft_k, float temp,
-                                           uint64_t* rng_state, int64_t prefill_batch, uint32_t* out,
-                                           int64_t* stats, int64_t* steps_out);
+                                           uint64_t* rng_state, const uint32_t* stop, int64_t n_stop,
+                                           int64_t prefill_batch, uint32_t* out, int64_t* stats,
+                                           int64_t* steps_out);
 
 /* k+1 speculative decoding with the seeded oracle drafter (no reference
  * counterpart): draft i of a step at position p copies greedy[p - n_prompt]

@@ -66,7 +66,8 @@ def lib():
         "or_rand_simple": (C.c_float, [C.POINTER(C.c_uint64)]),
         "or_sample_logits": (_i64, [_f32p, _i64, C.c_float, C.POINTER(C.c_uint64)]),
         "or_generate_speculative_draft_temp": (_i64, [C.c_void_p, C.c_void_p, _u32p, _i64, _i64, _i64, C.c_float,
-                                                      C.POINTER(C.c_uint64), _i64, _u32p, _i64p, _i64p]),
+                                                      C.POINTER(C.c_uint64), _u32p, _i64, _i64, _u32p, _i64p,
+                                                      _i64p]),
         "or_attention_head": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, C.c_float]),
         "or_philox4x32_10": (None, [_u32p, _u32p, _u32p]),
         "or_model_load": (C.c_void_p, [C.c_char_p, C.c_int, C.c_char_p, C.c_int]),
@@ -456,16 +457,17 @@ def generate_speculative_draft(target: Session, draft: Session, prompt, n_new, d
 
 
 def generate_speculative_draft_temp(target: Session, draft: Session, prompt, n_new, draft_k, temp,
-                                    rng_state=REFERENCE_RNG_STATE, prefill_batch=16):
-    """speculative.rs:299-494 at temperature temp with the reference's sampler and LCG; returns
-    (tokens, drafted, accepted, steps, rng_state)."""
+                                    rng_state=REFERENCE_RNG_STATE, prefill_batch=16, stop=()):
+    """speculative.rs:299-494 at temperature temp (greedy at temp <= 0) with the reference's
+    sampler and LCG and its stop tokens; returns (tokens, drafted, accepted, steps, rng_state)."""
     p = _c(prompt, np.uint32)
+    sp = _c(np.array(list(stop) or [0], np.uint32), np.uint32)
     out = np.zeros(n_new, np.uint32)
     stats = np.zeros(2, np.int64)
     steps = np.zeros(1, np.int64)
     st = C.c_uint64(rng_state)
     n = lib().or_generate_speculative_draft_temp(target.h, draft.h, p, p.size, n_new, draft_k, float(temp),
-                                                 C.byref(st), prefill_batch, out, stats, steps)
+                                                 C.byref(st), sp, len(stop), prefill_batch, out, stats, steps)
     return out[:n], int(stats[0]), int(stats[1]), int(steps[0]), int(st.value)
 
 

@@ -217,3 +217,28 @@ def test_speculative_draft_temp_matches_oracle(ctx, draft_seed, k, temp):
     assert (stats.drafted, stats.accepted, stats.steps, st) == (odrafted, oacc, osteps, ost)
     if temp < 0.1:
         assert 0 < stats.accepted < stats.drafted
+
+
+@pytest.mark.parametrize("draft_seed,temp", [(71, 0.05), (71, 0.0), (72, 0.3)])
+def test_speculative_draft_stop_tokens_match_oracle(ctx, draft_seed, temp):
+    """Stop tokens in the draft-model loop (is_stop_token, speculative.rs:305-447, and the
+    generate loop's turn end, main.rs:9852-9866), at temperature and greedy: for stop ids taken
+    from the unstopped stream (so that drafted, accepted, corrective and trailing stops occur),
+    the GPU loop's tokens, counts, steps and LCG state equal the oracle's, and no stop token is
+    emitted."""
+    import nanocamelid_amd as nc
+    imgs = {s: nc.synth_gguf(**TINY_UNTIED, seed=s) for s in {71, draft_seed}}
+    gt, gd = nc.Model(ctx, data=imgs[71]), nc.Model(ctx, data=imgs[draft_seed])
+    ot, od = O.Model(data=imgs[71].tobytes(), nthreads=16), O.Model(data=imgs[draft_seed].tobytes(), nthreads=16)
+    prompt = nc.uniform_prompt(73, 20, 1000)
+    free = O.generate_speculative_draft_temp(O.Session(ot, 512, 16), O.Session(od, 512, 16), prompt, 40, 4, temp)[0]
+    for cut in (3, 12, 21, 33):
+        stop = (int(free[cut]), 999)
+        print(f"draft stop loop draft={draft_seed} T={temp} stop={stop}", flush=True)
+        toks, stats, st = nc.generate_speculative_draft_temp(nc.Session(gt, 512, 16), nc.Session(gd, 512, 16),
+                                                             prompt, 40, 4, temp, stop=stop)
+        otoks, odrafted, oacc, osteps, ost = O.generate_speculative_draft_temp(
+            O.Session(ot, 512, 16), O.Session(od, 512, 16), prompt, 40, 4, temp, stop=stop)
+        assert np.array_equal(toks, otoks), cut
+        assert (stats.drafted, stats.accepted, stats.steps, st) == (odrafted, oacc, osteps, ost), cut
+        assert stop[0] not in toks.tolist()

@@ -90,44 +90,60 @@ TINY = dict(layers=2, embedding_length=256, head_count=4, head_count_kv=2, feed_
             context_length=512, tied=0, norm_mode=1)
 
 
-def _step_loop_python(tg, dr, prompt, n_new, k, temp, state, max_batch=16):
-    """speculative.rs:299-494 (no stop tokens) driven as main.rs:9643-9706, in Python."""
+def _step_loop_python(tg, dr, prompt, n_new, k, temp, state, max_batch=16, stop=(), kinds=None):
+    """speculative.rs:299-494 with its is_stop_token, driven as main.rs:9643-9706 / 9799-9870,
+    in Python.  Also returns how the run ended: "n_new", "accepted-stop" (a drafted stop
+    token the target accepted), "corrective-stop" or "trailing-stop"; kinds (a list) receives
+    "draft", "corrective" or "trailing" for each emitted token."""
     n = len(prompt)
     for s in (tg, dr):
         for i in range(0, n - 1, 16):
             s.prefill_pass_batch(prompt[i:min(i + 16, n - 1)], i)
     tl = tg.forward_pass(prompt[-1], n - 1)
     dl = dr.forward_pass(prompt[-1], n - 1)
-    pos, out, drafted, accepted, steps = n, [], 0, 0, 0
-    while len(out) < n_new:
+    pos, out, drafted, accepted, steps, end = n, [], 0, 0, 0, "n_new"
+    while end == "n_new" and len(out) < n_new:
         kk = min(k, n_new - len(out), max_batch, 512 - (pos + 1))
         drafts = []
-        for i in range(kk):
+        for i in range(kk):  # drafting: a stop token is kept but not run on the draft
             t, state = O.sample_logits(dl, temp, state)
             drafts.append(t)
+            if t in stop:
+                break
             dl = dr.forward_pass(t, pos + i)
         tg.prefill_pass_batch(np.array(drafts, np.uint32), pos)
-        drafted += kk
-        emitted = []
-        for i in range(kk):
+        drafted += len(drafts)
+        emitted, rejected, how, kind = [], False, "trailing-stop", []
+        for i in range(len(drafts)):
             lg = tl if i == 0 else tg.batch_row_logits(i - 1)
             tt, state = O.sample_logits(lg, temp, state)
+            emitted.append(tt)
+            kind.append("draft" if tt == drafts[i] else "corrective")
             if tt == drafts[i]:
                 accepted += 1
-                emitted.append(tt)
+                if tt in stop:  # verification ends, no trailing token
+                    pos, rejected, how = pos + i + 1, True, "accepted-stop"
+                    break
                 continue
-            emitted.append(tt)
             tl, dl = tg.forward_pass(tt, pos + i), dr.forward_pass(tt, pos + i)
-            pos += i + 1
+            pos, rejected, how = pos + i + 1, True, "corrective-stop"
             break
-        else:
-            tt, state = O.sample_logits(tg.batch_row_logits(kk - 1), temp, state)
+        if not rejected:
+            tt, state = O.sample_logits(tg.batch_row_logits(len(drafts) - 1), temp, state)
             emitted.append(tt)
-            tl, dl = tg.forward_pass(tt, pos + kk), dr.forward_pass(tt, pos + kk)
-            pos += kk + 1
-        out += emitted[:n_new - len(out)]
+            kind.append("trailing")
+            tl, dl = tg.forward_pass(tt, pos + len(drafts)), dr.forward_pass(tt, pos + len(drafts))
+            pos += len(drafts) + 1
+        for t, kd in zip(emitted, kind):  # main.rs:9852-9866: the stop token ends the turn, unemitted
+            if t in stop:
+                end = how
+                break
+            if len(out) < n_new:
+                out.append(t)
+                if kinds is not None:
+                    kinds.append(kd)
         steps += 1
-    return np.array(out, np.uint32), drafted, accepted, steps, state
+    return np.array(out, np.uint32), drafted, accepted, steps, state, end
 
 
 @pytest.mark.parametrize("draft_seed,k,temp", [(72, 2, 0.3), (71, 4, 1.0), (71, 4, 0.05)])
@@ -140,7 +156,42 @@ def test_speculative_draft_temp_loop_matches_python_restatement(draft_seed, k, t
                                O.REFERENCE_RNG_STATE)
     res_c = O.generate_speculative_draft_temp(O.Session(tm, 512, 16), O.Session(dm, 512, 16), prompt, 40, k, temp)
     assert np.array_equal(res_py[0], res_c[0])
-    assert res_py[1:] == res_c[1:]
+    assert res_py[1:5] == res_c[1:] and res_py[5] == "n_new"
     assert len(set(res_c[0].tolist())) >= 8
     if temp < 0.1:
         assert 0 < res_c[2] < res_c[1]  # drafted, accepted
+
+
+def test_speculative_draft_stop_tokens_match_python_restatement():
+    """Stop tokens (is_stop_token, speculative.rs:305-447; the generate loop's turn end,
+    main.rs:9852-9866) at temperature and greedy, with the target's own weights as draft (many
+    acceptances) and another model: the oracle's C loop equals the Python restatement in
+    tokens, counts and LCG state; no stop token is emitted; greedy runs end just before the
+    first stop token of the unstopped stream; every way a stop can end a run occurs (an
+    accepted stop draft, a corrective and a trailing stop)."""
+    tm = _models(TINY, 71)
+    prompt = nc.uniform_prompt(73, 20, 1000)
+    ends = set()
+    for draft_seed, temp in ((71, 0.05), (71, 0.0), (72, 0.3), (71, 1.0)):
+        dm = _models(TINY, draft_seed)
+        kinds = []
+        free = _step_loop_python(O.Session(tm, 512, 16), O.Session(dm, 512, 16), prompt, 40, 4, temp,
+                                 O.REFERENCE_RNG_STATE, kinds=kinds)[0]
+        # first occurrences of a value as a corrective or trailing token end the run there
+        firsts = [i for i in range(40) if free[i] not in free[:i].tolist()]
+        extra = [next((i for i in firsts if kinds[i] == kd), 3) for kd in ("corrective", "trailing")]
+        for cut in (3, 9, 17, 26, 34, *extra):
+            stop = (int(free[cut]), 999)
+            res_py = _step_loop_python(O.Session(tm, 512, 16), O.Session(dm, 512, 16), prompt, 40, 4, temp,
+                                       O.REFERENCE_RNG_STATE, stop=stop)
+            res_c = O.generate_speculative_draft_temp(O.Session(tm, 512, 16), O.Session(dm, 512, 16), prompt, 40,
+                                                      4, temp, stop=stop)
+            assert np.array_equal(res_py[0], res_c[0]), (draft_seed, temp, cut)
+            assert res_py[1:5] == res_c[1:], (draft_seed, temp, cut)
+            assert stop[0] not in res_c[0].tolist()
+            if temp == 0.0:  # greedy: the stream is the unstopped one cut before the stop token
+                first = free.tolist().index(stop[0])
+                assert np.array_equal(res_c[0], free[:first]) and res_py[5] != "n_new"
+            # (at temperature a stop token changes the draws that follow, so the run may not meet it)
+            ends.add(res_py[5])
+    assert ends >= {"accepted-stop", "corrective-stop", "trailing-stop"}, ends
