@@ -279,6 +279,16 @@ typedef struct nc_decode_stats {
 int nc_generate_greedy(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new,
                        uint32_t* out, nc_decode_stats* stats);
 
+/* The plain decode loop with sampling and stop tokens (src/main.rs:9894-9928): each token is
+ * drawn with sample_logits (src/inference.rs:4834-4873) from the live logits, one
+ * rand_simple draw (*rng_state) per token at temp > 0; decoding ends before a stop token
+ * (stop[n_stop]; n_stop = 0: none, and the ids are not emitted), at the session context or
+ * after n_new tokens.  stats->emitted is the number of tokens written to out.  temp <= 0
+ * with no stop tokens is nc_generate_greedy (rng_state may then be NULL). */
+int nc_generate_plain(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new, float temp,
+                      uint64_t* rng_state, const uint32_t* stop, int32_t n_stop, uint32_t* out,
+                      nc_decode_stats* stats);
+
 /* k+1 speculative decode with the seeded oracle drafter (no reference counterpart;
  * the drafter exists only for the benchmark configs): the draft for absolute
  * position p copies greedy[p - n_prompt] (greedy = the target's recorded greedy

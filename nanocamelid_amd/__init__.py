@@ -307,6 +307,18 @@ class Session:
                                        C.byref(st)))
         return out, st
 
+    def generate_plain(self, prompt, n_new: int, temp: float, rng_state: int = REFERENCE_RNG_STATE, stop=()):
+        """The plain decode loop (src/main.rs:9894-9928) with sample_logits, the reference's LCG and
+        stop tokens; returns (tokens, stats, rng_state after the run)."""
+        a, p = _u32(prompt)
+        sa, sp = _u32(np.array(list(stop) or [0], np.uint32))
+        out = np.zeros(n_new, np.uint32)
+        st = DecodeStats()
+        rs = C.c_uint64(rng_state)
+        check(lib().nc_generate_plain(self.h, p, a.size, n_new, float(temp), C.byref(rs), sp, len(stop),
+                                      out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
+        return out[:st.emitted], st, int(rs.value)
+
     def generate_speculative_oracle(self, prompt, n_new: int, k: int, alpha: float, seed: int, greedy,
                                     max_steps: int = 0):
         a, p = _u32(prompt)

@@ -99,6 +99,8 @@ SIGNATURES = {
     "nc_session_logits": (C.c_int, [_vp, _i32, _f32p]),
     "nc_session_hidden": (C.c_int, [_vp, _i32, _f32p]),
     "nc_generate_greedy": (C.c_int, [_vp, _u32p, _i32, _i32, _u32p, C.POINTER(DecodeStats)]),
+    "nc_generate_plain": (C.c_int, [_vp, _u32p, _i32, _i32, C.c_float, C.POINTER(C.c_uint64), _u32p, _i32, _u32p,
+                                    C.POINTER(DecodeStats)]),
     "nc_generate_speculative_oracle": (C.c_int, [_vp, _u32p, _i32, _i32, _i32, _i32, C.c_float, C.c_uint64, _u32p,
                                                  _i32, _u32p, C.POINTER(DecodeStats)]),
     "nc_generate_speculative_draft": (C.c_int, [_vp, _vp, _u32p, _i32, _i32, _i32, _u32p, C.POINTER(DecodeStats)]),

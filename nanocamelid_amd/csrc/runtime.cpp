@@ -925,8 +925,7 @@ static int sample_session_rows(nc_session* s, int row0, int rows, float temp, co
 }
 
 // ---------------------------------------------------------------- prompt passes
-// Prompt passes run every matrix of the layer through the MFMA prompt matmul, so they need
-// Q4_0 matrices throughout (R16 or R64 tiles).
+// Matrices with an MFMA prompt matmul: Q4_0 (R16 or R64 tiles) and Q4_K (R16K or R64).
 static bool prompt_matrix_ok(const QMatDev& q) {
     if (q.type == NC_TYPE_Q4_0) return q.layout == LAYOUT_R16 || q.layout == LAYOUT_R64;
     if (q.type == NC_TYPE_Q4_K) return q.layout == LAYOUT_R16K || q.layout == LAYOUT_R64;
@@ -1686,6 +1685,45 @@ int nc_generate_greedy(nc_session* s, const uint32_t* prompt, int32_t n_prompt, 
     if (stats) {
         *stats = nc_decode_stats{steps, 0, 0, n_new, t2 - t1, t1 - t0};
     }
+    return flush_timing(s);
+}
+
+int nc_generate_plain(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new, float temp,
+                      uint64_t* rng_state, const uint32_t* stop, int32_t n_stop, uint32_t* out, nc_decode_stats* stats) {
+    const bool t = temp > 0.0f;
+    if (!s || !prompt || !out || n_prompt < 1 || n_new < 1 || n_stop < 0 || (n_stop > 0 && !stop) ||
+        (t && !rng_state))
+        return fail(NC_EINVAL, "nc_generate_plain: bad arguments");
+    if (!t && n_stop == 0) return nc_generate_greedy(s, prompt, n_prompt, n_new, out, stats);
+    if (n_prompt >= s->max_ctx) return fail(NC_ERANGE, "prompt fills the session context");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    const auto is_stop = [&](uint32_t id) { return std::find(stop, stop + n_stop, id) != stop + n_stop; };
+    const double t0 = now_s();
+    // main.rs:9676-9706 prefill; the last row's logits (and argmax) are the live ones
+    uint32_t pending;
+    int rc = prefill_chunks(s, prompt, n_prompt, 0, &pending, t);
+    if (rc) return rc;
+    int live = s->last_n - 1;
+    const double t1 = now_s();
+    int64_t pos = n_prompt, produced = 0, steps = 0;
+    // the plain loop (main.rs:9894-9928): sample, end at a stop token, the context end or
+    // n_new, emit, end at n_new, forward
+    for (;;) {
+        uint32_t id = pending;
+        if (t) {
+            const float u = lcg_next(rng_state);
+            if ((rc = sample_session_rows(s, live, 1, temp, &u, &id))) return rc;
+        }
+        if (is_stop(id) || pos >= s->max_ctx || produced >= n_new) break;
+        out[produced++] = id;
+        if (produced >= n_new) break;
+        if ((rc = nc_forward1(s, id, pos, nullptr, &pending))) return rc;
+        live = 0;
+        pos++;
+        steps++;
+    }
+    const double t2 = now_s();
+    if (stats) *stats = nc_decode_stats{steps, 0, 0, produced, t2 - t1, t1 - t0};
     return flush_timing(s);
 }
 

@@ -624,6 +624,29 @@ int or_generate_greedy(or_session* s, const uint32_t* prompt, int64_t n_prompt, 
     return 0;
 }
 
+int64_t or_generate_plain(or_session* s, const uint32_t* prompt, int64_t n_prompt, int64_t n_new, float temp,
+                          uint64_t* rng_state, const uint32_t* stop, int64_t n_stop, int64_t prefill_batch,
+                          uint32_t* out) {
+    // main.rs:9676-9706 prefill, then the plain loop (main.rs:9894-9928): sample, end at a stop
+    // token, the context end or n_new, emit, end at n_new, forward
+    uint64_t st_unused = 0;
+    uint64_t* rs = rng_state ? rng_state : &st_unused;
+    prefill(s, prompt, n_prompt - 1, 0, prefill_batch);
+    int64_t pos = n_prompt - 1;
+    or_forward_pass(s, prompt[n_prompt - 1], pos);
+    pos++;
+    int64_t produced = 0;
+    for (;;) {
+        const uint32_t t = (uint32_t)or_sample_logits(s->logits.data(), s->m->V, temp, rs);
+        if (std::find(stop, stop + n_stop, t) != stop + n_stop || pos >= s->max_ctx || produced >= n_new) break;
+        out[produced++] = t;
+        if (produced >= n_new) break;
+        or_forward_pass(s, t, pos);
+        pos++;
+    }
+    return produced;
+}
+
 int64_t or_generate_speculative_draft(or_session* tg, or_session* dr, const uint32_t* prompt,
                                       int64_t n_prompt, int64_t n_new, int64_t draft_k,
                                       int64_t prefill_batch, uint32_t* out, int64_t* stats,

@@ -151,6 +151,14 @@ void or_verify_greedy(or_session* s, const uint32_t* toks, int64_t n, int64_t st
 int or_generate_greedy(or_session* s, const uint32_t* prompt, int64_t n_prompt, int64_t n_new,
                        int64_t prefill_batch, uint32_t* out);
 
+/* The plain decode loop at temperature temp (main.rs:9894-9928, greedy at temp <= 0): each
+ * token drawn with or_sample_logits (*rng_state, may be NULL at temp <= 0) from the live
+ * logits; decoding ends before a stop token (stop[n_stop]), at the session context or after
+ * n_new tokens.  Returns the number of tokens written to out. */
+int64_t or_generate_plain(or_session* s, const uint32_t* prompt, int64_t n_prompt, int64_t n_new, float temp,
+                          uint64_t* rng_state, const uint32_t* stop, int64_t n_stop, int64_t prefill_batch,
+                          uint32_t* out);
+
 /* Draft-model speculative decoding (speculative.rs:299-494) for n_new tokens.
  * target/draft sessions; temp <= 0 greedy.  out[n_new]; stats[2] = drafted,
  * accepted; steps_out = number of steps.  Returns number of tokens written. */

@@ -87,6 +87,8 @@ def lib():
         "or_session_batch_hidden": (C.POINTER(C.c_float), [C.c_void_p]),
         "or_verify_greedy": (None, [C.c_void_p, _u32p, _i64, _i64, _u32p, C.c_void_p, C.c_void_p]),
         "or_generate_greedy": (C.c_int, [C.c_void_p, _u32p, _i64, _i64, _i64, _u32p]),
+        "or_generate_plain": (_i64, [C.c_void_p, _u32p, _i64, _i64, C.c_float, C.POINTER(C.c_uint64), _u32p,
+                                     _i64, _i64, _u32p]),
         "or_generate_speculative_draft": (_i64, [C.c_void_p, C.c_void_p, _u32p, _i64, _i64, _i64, _i64, _u32p, _i64p, _i64p]),
         "or_generate_speculative_stochastic": (_i64, [C.c_void_p, C.c_void_p, _u32p, _i64, _i64, _i64, C.c_float, C.c_uint64, _i64, _u32p, _i64p, _i64p]),
         "or_generate_speculative_oracle": (_i64, [C.c_void_p, _u32p, _i64, _i64, _i64, C.c_float, C.c_uint64, _u32p, _i64, _u32p, _i64p, _i64p]),
@@ -444,6 +446,17 @@ class Session:
             self.close()
         except Exception:
             pass
+
+
+def generate_plain(s: Session, prompt, n_new, temp, rng_state=REFERENCE_RNG_STATE, stop=(), prefill_batch=16):
+    """The plain decode loop (main.rs:9894-9928) at temperature temp with stop tokens; returns
+    (tokens, rng_state)."""
+    p = _c(prompt, np.uint32)
+    sp = _c(np.array(list(stop) or [0], np.uint32), np.uint32)
+    out = np.zeros(n_new, np.uint32)
+    st = C.c_uint64(rng_state)
+    n = lib().or_generate_plain(s.h, p, p.size, n_new, float(temp), C.byref(st), sp, len(stop), prefill_batch, out)
+    return out[:n], int(st.value)
 
 
 def generate_speculative_draft(target: Session, draft: Session, prompt, n_new, draft_k, prefill_batch=16):

@@ -242,3 +242,24 @@ def test_speculative_draft_stop_tokens_match_oracle(ctx, draft_seed, temp):
         assert np.array_equal(toks, otoks), cut
         assert (stats.drafted, stats.accepted, stats.steps, st) == (odrafted, oacc, osteps, ost), cut
         assert stop[0] not in toks.tolist()
+
+
+@pytest.mark.parametrize("temp", [0.0, 0.7, 1.3])
+def test_plain_loop_matches_oracle(ctx, temp):
+    """The plain decode loop (main.rs:9894-9928) with sample_logits, the reference's LCG and stop
+    tokens: the GPU loop's tokens and LCG state equal the oracle's, with and without stops, and
+    a run stops before the first stop token of the unstopped stream."""
+    import nanocamelid_amd as nc
+    img = nc.synth_gguf(**TINY_UNTIED, seed=71)
+    gm, om = nc.Model(ctx, data=img), O.Model(data=img.tobytes(), nthreads=16)
+    prompt = nc.uniform_prompt(75, 20, 1000)
+    print(f"plain loop T={temp}", flush=True)
+    free, stats, st = nc.Session(gm, 512, 16).generate_plain(prompt, 30, temp)
+    ofree, ost = O.generate_plain(O.Session(om, 512, 16), prompt, 30, temp)
+    assert np.array_equal(free, ofree) and st == ost and stats.emitted == 30
+    for cut in (0, 7, 22):
+        stop = (int(free[cut]), 5)
+        toks, stats, st = nc.Session(gm, 512, 16).generate_plain(prompt, 30, temp, stop=stop)
+        otoks, ost = O.generate_plain(O.Session(om, 512, 16), prompt, 30, temp, stop=stop)
+        assert np.array_equal(toks, otoks) and st == ost, cut
+        assert np.array_equal(toks, free[:free.tolist().index(stop[0])]) or 5 in free[:len(toks) + 1].tolist()

@@ -195,3 +195,45 @@ def test_speculative_draft_stop_tokens_match_python_restatement():
             # (at temperature a stop token changes the draws that follow, so the run may not meet it)
             ends.add(res_py[5])
     assert ends >= {"accepted-stop", "corrective-stop", "trailing-stop"}, ends
+
+
+def _plain_loop_python(s, prompt, n_new, temp, state, stop=(), max_ctx=512):
+    """main.rs:9676-9706 prefill and the plain loop of main.rs:9894-9928, in Python."""
+    n = len(prompt)
+    for i in range(0, n - 1, 16):
+        s.prefill_pass_batch(prompt[i:min(i + 16, n - 1)], i)
+    lg, pos, out = s.forward_pass(prompt[-1], n - 1), n, []
+    while True:
+        t, state = O.sample_logits(lg, temp, state)
+        if t in stop or pos >= max_ctx or len(out) >= n_new:
+            break
+        out.append(t)
+        if len(out) >= n_new:
+            break
+        lg = s.forward_pass(t, pos)
+        pos += 1
+    return np.array(out, np.uint32), state
+
+
+@pytest.mark.parametrize("temp", [0.0, 0.7, 1.3])
+def test_plain_loop_matches_python_restatement(temp):
+    """The oracle's plain decode loop with sampling and stop tokens against the restatement:
+    same tokens and LCG state; greedy runs are the unstopped stream cut before the stop token;
+    a context end stops the run too."""
+    tm = _models(TINY, 71)
+    prompt = nc.uniform_prompt(75, 20, 1000)
+    free, st_free = O.generate_plain(O.Session(tm, 512, 16), prompt, 30, temp)
+    assert len(free) == 30
+    py, st_py = _plain_loop_python(O.Session(tm, 512, 16), prompt, 30, temp, O.REFERENCE_RNG_STATE)
+    assert np.array_equal(free, py) and st_free == st_py
+    if temp == 0.0:
+        assert st_free == O.REFERENCE_RNG_STATE  # the argmax draws nothing
+    for cut in (0, 7, 22):
+        stop = (int(free[cut]),)
+        got, st = O.generate_plain(O.Session(tm, 512, 16), prompt, 30, temp, stop=stop)
+        py, st_py = _plain_loop_python(O.Session(tm, 512, 16), prompt, 30, temp, O.REFERENCE_RNG_STATE, stop)
+        assert np.array_equal(got, py) and st == st_py
+        first = free.tolist().index(stop[0])
+        assert np.array_equal(got, free[:first])  # the draws before the stop are unchanged
+    short, _ = O.generate_plain(O.Session(tm, 26, 16), prompt, 30, temp)
+    assert np.array_equal(short, free[:6])  # positions 20..25: six tokens fit the context
