@@ -309,14 +309,27 @@ int32_t nc_ngram_draft(const uint32_t* history, int64_t len, int32_t min_ngram, 
                        uint32_t* out);
 
 /* n-gram speculative decode, greedy: ngram_speculative_step (src/speculative.rs:122-286)
- * in the k+1 verify form (src/bin/cluster_tcp_smoke.rs:905-979).  Each step verifies the
- * pending token plus up to k drafts that nc_ngram_draft proposes from prompt + emitted
+ * driven by the generate loop (src/main.rs:9729-9776: k clamped to the token budget minus
+ * one), in the k+1 verify form (src/bin/cluster_tcp_smoke.rs:905-979).  Each step verifies
+ * the pending token plus up to k drafts that nc_ngram_draft proposes from prompt + emitted
  * tokens; no proposal means a one-row pass.  The emitted stream is the target's greedy
  * stream, cut before the first of the n_stop stop tokens (a stop token is neither emitted
  * nor consumed).  stats->emitted (<= n_new) is the number of tokens written to out. */
 int nc_generate_speculative_ngram(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new, int32_t k,
                                   int32_t min_ngram, int32_t max_ngram, const uint32_t* stop, int32_t n_stop,
                                   uint32_t* out, nc_decode_stats* stats);
+
+/* The same at temperature temp > 0 (temp <= 0: the greedy loop above): each step draws t0
+ * from the live logits with sample_logits (src/inference.rs:4834-4873), verifies t0 plus the
+ * drafts in one pass, draws one token per verified row in order (a matching draw accepts the
+ * draft, a different one is emitted and run as a corrective forward, a stop token ends the
+ * turn), and when every draft matches the last row's logits predict the next step's t0.
+ * *rng_state is the reference's LCG state (rand_simple), one draw per sample in the step's
+ * order. */
+int nc_generate_speculative_ngram_temp(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new,
+                                       int32_t k, int32_t min_ngram, int32_t max_ngram, float temp,
+                                       uint64_t* rng_state, const uint32_t* stop, int32_t n_stop, uint32_t* out,
+                                       nc_decode_stats* stats);
 
 /* Draft-model speculative decode, greedy, as speculative_decoding_step
  * (src/speculative.rs:299-494) driven by the generate loop (src/main.rs:9799-9870):

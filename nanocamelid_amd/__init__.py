@@ -341,6 +341,21 @@ class Session:
                                                   out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
         return out[:st.emitted], st
 
+    def generate_speculative_ngram_temp(self, prompt, n_new: int, k: int, temp: float,
+                                        rng_state: int = REFERENCE_RNG_STATE, min_ngram: int = 3, max_ngram: int = 4,
+                                        stop=()):
+        """ngram_speculative_step at temperature (speculative.rs:122-286, main.rs:9729-9776) with
+        sample_logits and the reference's LCG; returns (tokens, stats, rng_state)."""
+        a, p = _u32(prompt)
+        so, sp = _u32(np.asarray(stop, np.uint32).reshape(-1) if len(stop) else np.zeros(1, np.uint32))
+        out = np.zeros(n_new, np.uint32)
+        st = DecodeStats()
+        rs = C.c_uint64(rng_state)
+        check(lib().nc_generate_speculative_ngram_temp(self.h, p, a.size, n_new, k, min_ngram, max_ngram, float(temp),
+                                                       C.byref(rs), sp, len(stop),
+                                                       out.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(st)))
+        return out[:st.emitted], st, int(rs.value)
+
     def timing(self, enable: bool):
         check(lib().nc_session_timing_enable(self.h, 1 if enable else 0))
 

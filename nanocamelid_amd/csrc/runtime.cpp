@@ -1800,9 +1800,10 @@ int nc_generate_speculative_ngram(nc_session* s, const uint32_t* prompt, int32_t
     int rc = prefill_chunks(s, prompt, n_prompt, 0, &pending);
     if (rc) return rc;
     const double t1 = now_s();
-    // ngram_speculative_step (speculative.rs:122-286) in the k+1 verify form
-    // (cluster_tcp_smoke.rs:905-979): [pending] + drafts from the history ending in pending;
-    // accepted = matching prefix; next pending = pred[accepted].  The emitted stream is the
+    // ngram_speculative_step (speculative.rs:122-286) driven by main.rs:9729-9776, greedy, in
+    // the k+1 verify form (cluster_tcp_smoke.rs:905-979): [pending] + drafts from the history
+    // ending in pending; accepted = matching prefix; next pending = pred[accepted], which is
+    // the step's corrective token and the next step's t0 at once.  The emitted stream is the
     // target's greedy stream cut before the first stop token (never emitted nor consumed).
     std::vector<uint32_t> history(prompt, prompt + n_prompt);
     history.reserve((size_t)n_prompt + n_new);
@@ -1812,7 +1813,9 @@ int nc_generate_speculative_ngram(nc_session* s, const uint32_t* prompt, int32_t
         out[produced++] = pending;
         history.push_back(pending);
         if (produced >= n_new || pos + 1 >= s->max_ctx) break;
-        int64_t kk = std::min<int64_t>(k, s->max_batch - 1);
+        // main.rs:9736-9737: a step emits at most the token budget (t0 is already counted)
+        int64_t kk = std::min<int64_t>(k, n_new - produced);
+        kk = std::min<int64_t>(kk, s->max_batch - 1);
         kk = std::min<int64_t>(kk, s->max_ctx - pos - 1);
         batch[0] = pending;
         const int nd = kk > 0 ? nc_ngram_draft(history.data(), (int64_t)history.size(), min_ngram, max_ngram, (int)kk,
@@ -1821,20 +1824,108 @@ int nc_generate_speculative_ngram(nc_session* s, const uint32_t* prompt, int32_t
         nc_verify_result r;
         if ((rc = upload_toks(s, batch, nd + 1)) || (rc = verify_step(s, nd + 1, pos, &r))) return rc;
         drafted += nd;
-        accepted += r.n_accepted;
         bool stopped = false;
+        int counted = r.n_accepted;  // the step stops counting at a stop prediction
         for (int i = 1; i <= r.n_accepted && produced < n_new; i++) {
             if (is_stop(batch[i])) {
                 stopped = true;
+                counted = i;
                 break;
             }
             out[produced++] = batch[i];
             history.push_back(batch[i]);
         }
+        accepted += counted;
         pending = r.next_token;
         pos = r.new_pos;
         steps++;
         if (stopped) break;
+    }
+    const double t2 = now_s();
+    if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};
+    return flush_timing(s);
+}
+
+int nc_generate_speculative_ngram_temp(nc_session* s, const uint32_t* prompt, int32_t n_prompt, int32_t n_new,
+                                       int32_t k, int32_t min_ngram, int32_t max_ngram, float temp,
+                                       uint64_t* rng_state, const uint32_t* stop, int32_t n_stop, uint32_t* out,
+                                       nc_decode_stats* stats) {
+    if (!(temp > 0.0f))
+        return nc_generate_speculative_ngram(s, prompt, n_prompt, n_new, k, min_ngram, max_ngram, stop, n_stop, out,
+                                             stats);
+    if (!s || !prompt || !out || !rng_state || n_prompt < 1 || n_new < 1 || k < 0 || min_ngram < 1 ||
+        max_ngram < min_ngram || n_stop < 0 || (n_stop > 0 && !stop))
+        return fail(NC_EINVAL, "nc_generate_speculative_ngram_temp: bad arguments");
+    if (n_prompt >= s->max_ctx) return fail(NC_ERANGE, "prompt fills the session context");
+    NC_HIP(hipSetDevice(s->ctx->device));
+    auto is_stop = [&](uint32_t t) { return std::find(stop, stop + n_stop, t) != stop + n_stop; };
+    const double t0 = now_s();
+    int rc = prefill_chunks(s, prompt, n_prompt, 0, nullptr, true);
+    if (rc) return rc;
+    int live = s->last_n - 1;  // row of the live logits in the last pass
+    const double t1 = now_s();
+    // main.rs:9729-9776 over ngram_speculative_step (speculative.rs:122-286): t0 drawn from the
+    // live logits (a stop token ends the turn unemitted); drafts from the history ending in t0;
+    // one pass over t0 + drafts; one draw per verified row in order (drawn provisionally for
+    // every row, kept as far as the verification reaches): a stop prediction ends the turn, a
+    // mismatch emits the prediction and runs it as a corrective forward, and when every draft
+    // matches the last row's logits are the next step's live logits.
+    std::vector<uint32_t> history(prompt, prompt + n_prompt);
+    history.reserve((size_t)n_prompt + n_new + 1);
+    int64_t pos = n_prompt, produced = 0, steps = 0, drafted = 0, accepted = 0;
+    uint32_t batch[16], tt[16];
+    float uv[16];
+    for (;;) {
+        if (pos >= s->max_ctx || produced >= n_new) break;
+        const int64_t ck = std::min<int64_t>(k, n_new - produced - 1);
+        const float u0 = lcg_next(rng_state);
+        if ((rc = sample_session_rows(s, live, 1, temp, &u0, &batch[0]))) return rc;
+        if (is_stop(batch[0])) break;
+        history.push_back(batch[0]);
+        int64_t nd = ck > 0 ? nc_ngram_draft(history.data(), (int64_t)history.size(), min_ngram, max_ngram, (int)ck,
+                                             batch + 1)
+                            : 0;
+        nd = std::min<int64_t>(nd, std::min<int64_t>(s->max_batch - 1, s->max_ctx - (pos + 1)));
+        steps++;
+        if (nd <= 0) {
+            if ((rc = nc_forward1(s, batch[0], pos, nullptr, nullptr))) return rc;
+            live = 0;
+            out[produced++] = batch[0];
+            pos++;
+            continue;
+        }
+        drafted += nd;
+        if ((rc = upload_toks(s, batch, (int)nd + 1)) || (rc = run_pass(s, (int)nd + 1, pos))) return rc;
+        uint64_t st = *rng_state;
+        for (int64_t r = 0; r < nd; r++) uv[r] = lcg_next(&st);
+        if ((rc = sample_session_rows(s, 0, (int)nd, temp, uv, tt))) return rc;
+        out[produced++] = batch[0];
+        int64_t i = 0;
+        bool hit_stop = false, done = false;
+        for (; i < nd; i++) {
+            if (batch[1 + i] == tt[i]) accepted++;
+            if (is_stop(tt[i])) {  // neither emitted nor consumed
+                hit_stop = done = true;
+                pos += i + 1;
+                break;
+            }
+            out[produced++] = tt[i];
+            history.push_back(tt[i]);
+            if (batch[1 + i] != tt[i]) {  // corrective forward
+                if ((rc = nc_forward1(s, tt[i], pos + i + 1, nullptr, nullptr))) return rc;
+                live = 0;
+                pos += i + 2;
+                done = true;
+                break;
+            }
+        }
+        const int64_t used = done ? i + 1 : nd;  // draws the verification made
+        for (int64_t r = 0; r < used; r++) (void)lcg_next(rng_state);
+        if (!done) {
+            live = (int)nd;
+            pos += nd + 1;
+        }
+        if (hit_stop) break;
     }
     const double t2 = now_s();
     if (stats) *stats = nc_decode_stats{steps, drafted, accepted, produced, t2 - t1, t1 - t0};

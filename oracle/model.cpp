@@ -820,9 +820,10 @@ int64_t or_generate_speculative_ngram(or_session* s, const uint32_t* prompt, int
                                       int64_t k, int64_t min_ngram, int64_t max_ngram, const uint32_t* stop,
                                       int64_t n_stop, int64_t prefill_batch, uint32_t* out, int64_t* stats,
                                       int64_t* steps_out) {
-    // ngram_speculative_step (speculative.rs:122-286) in the k+1 verify form
-    // (cluster_tcp_smoke.rs:905-979): each step verifies [pending] + drafts drawn from the
-    // history that ends with pending; the emitted stream is the target's greedy stream,
+    // ngram_speculative_step (speculative.rs:122-286) driven by main.rs:9729-9776, greedy, in
+    // the k+1 verify form (cluster_tcp_smoke.rs:905-979): each step verifies [pending] + drafts
+    // drawn from the history that ends with pending, and the corrective token is the next
+    // step's pending (no separate forward); the emitted stream is the target's greedy stream,
     // cut before the first stop token (stop tokens are neither emitted nor consumed).
     const int64_t V = s->m->V;
     auto is_stop = [&](uint32_t t) { return std::find(stop, stop + n_stop, t) != stop + n_stop; };
@@ -838,7 +839,9 @@ int64_t or_generate_speculative_ngram(or_session* s, const uint32_t* prompt, int
         out[produced++] = pending;
         history.push_back(pending);
         if (produced >= n_new) break;
-        int64_t kk = std::min(k, s->max_batch - 1);
+        // main.rs:9736-9737: a step emits at most the token budget (pending is counted)
+        int64_t kk = std::min(k, n_new - produced);
+        kk = std::min(kk, s->max_batch - 1);
         kk = std::min(kk, s->max_ctx - pos - 1);
         if (kk < 0) break;
         const int64_t nd = kk > 0 ? or_ngram_draft(history.data(), (int64_t)history.size(), min_ngram, max_ngram,
@@ -851,18 +854,104 @@ int64_t or_generate_speculative_ngram(or_session* s, const uint32_t* prompt, int
         int64_t a = 0;
         while (a < nd && batch[a + 1] == preds[a]) a++;
         stats[0] += nd;
-        stats[1] += a;
+        int64_t counted = a;  // the step stops counting at a stop prediction
         for (int64_t i = 1; i <= a && produced < n_new; i++) {
             if (is_stop(batch[i])) {
                 stopped = true;
+                counted = i;
                 break;
             }
             out[produced++] = batch[i];
             history.push_back(batch[i]);
         }
+        stats[1] += counted;
         pending = preds[a];
         pos += a + 1;
         steps++;
+    }
+    if (steps_out) *steps_out = steps;
+    return produced;
+}
+
+int64_t or_generate_speculative_ngram_temp(or_session* s, const uint32_t* prompt, int64_t n_prompt, int64_t n_new,
+                                           int64_t k, int64_t min_ngram, int64_t max_ngram, float temp,
+                                           uint64_t* rng_state, const uint32_t* stop, int64_t n_stop,
+                                           int64_t prefill_batch, uint32_t* out, int64_t* stats,
+                                           int64_t* steps_out) {
+    if (!(temp > 0.0f))
+        return or_generate_speculative_ngram(s, prompt, n_prompt, n_new, k, min_ngram, max_ngram, stop, n_stop,
+                                             prefill_batch, out, stats, steps_out);
+    // The generate loop of main.rs:9729-9776 over ngram_speculative_step (speculative.rs:122-286):
+    // t0 drawn from the live logits (a stop token ends the turn unemitted), drafts from the
+    // history that ends in t0 (k clamped to the token budget minus one, then to the batch and
+    // the context), one batched pass over t0 + drafts, one draw per verified row in order:
+    // a stop prediction ends the turn, a mismatch emits the prediction and runs it as a
+    // corrective forward, and when every draft matches the last row's logits are the next
+    // step's live logits.
+    const int64_t V = s->m->V;
+    uint64_t st_unused = 0;
+    uint64_t* rs = rng_state ? rng_state : &st_unused;
+    auto sample = [&](const float* l) { return (uint32_t)or_sample_logits(l, V, temp, rs); };
+    auto is_stop = [&](uint32_t t) { return std::find(stop, stop + n_stop, t) != stop + n_stop; };
+    prefill(s, prompt, n_prompt - 1, 0, prefill_batch);
+    or_forward_pass(s, prompt[n_prompt - 1], n_prompt - 1);
+    std::vector<uint32_t> history(prompt, prompt + n_prompt), drafts(std::max<int64_t>(k, 1)), emitted;
+    std::vector<float> lg(V);
+    int64_t live_row = -1;  // -1: s->logits; else that row of the last batched pass
+    int64_t pos = n_prompt, produced = 0, steps = 0;
+    stats[0] = stats[1] = 0;
+    for (;;) {
+        if (pos >= s->max_ctx || produced >= n_new) break;
+        const int64_t ck = std::min(k, n_new - produced - 1);
+        if (live_row >= 0) or_batch_row_logits(s, live_row, lg.data());
+        const uint32_t t0 = sample(live_row >= 0 ? lg.data() : s->logits.data());
+        if (is_stop(t0)) break;
+        history.push_back(t0);
+        int64_t nd = ck > 0 ? or_ngram_draft(history.data(), (int64_t)history.size(), min_ngram, max_ngram, ck,
+                                             drafts.data())
+                            : 0;
+        nd = std::min(nd, std::min(s->max_batch - 1, s->max_ctx - (pos + 1)));
+        steps++;
+        if (nd <= 0) {
+            or_forward_pass(s, t0, pos);
+            live_row = -1;
+            out[produced++] = t0;
+            pos++;
+            continue;
+        }
+        stats[0] += nd;
+        std::vector<uint32_t> batch(1, t0);
+        batch.insert(batch.end(), drafts.begin(), drafts.begin() + nd);
+        or_prefill_pass_batch(s, batch.data(), nd + 1, pos);
+        emitted.assign(1, t0);
+        bool hit_stop = false, done = false;
+        for (int64_t i = 0; i < nd; i++) {
+            or_batch_row_logits(s, i, lg.data());
+            const uint32_t tt = sample(lg.data());
+            if (drafts[i] == tt) stats[1]++;
+            if (is_stop(tt)) {  // neither emitted nor consumed
+                hit_stop = done = true;
+                pos += i + 1;
+                break;
+            }
+            if (drafts[i] == tt) {
+                emitted.push_back(tt);
+            } else {
+                emitted.push_back(tt);
+                or_forward_pass(s, tt, pos + i + 1);
+                live_row = -1;
+                pos += i + 2;
+                done = true;
+                break;
+            }
+        }
+        if (!done) {
+            live_row = nd;
+            pos += nd + 1;
+        }
+        for (size_t j = 1; j < emitted.size(); j++) history.push_back(emitted[j]);
+        for (uint32_t t : emitted) out[produced++] = t;  // at most ck + 1 <= the budget
+        if (hit_stop) break;
     }
     if (steps_out) *steps_out = steps;
     return produced;

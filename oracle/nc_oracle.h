@@ -191,13 +191,22 @@ int64_t or_generate_speculative_oracle(or_session* target, const uint32_t* promp
  * returns how many. */
 int64_t or_ngram_draft(const uint32_t* history, int64_t len, int64_t min_ngram, int64_t max_ngram,
                        int64_t max_tokens, uint32_t* out);
-/* n-gram prompt-lookup speculation (speculative.rs:122-286) in the k+1 verify form; the
+/* n-gram prompt-lookup speculation, greedy: ngram_speculative_step (speculative.rs:122-286)
+ * driven by main.rs:9729-9776 in the k+1 verify form (cluster_tcp_smoke.rs:905-979); the
  * stream stops before the first of the n_stop stop tokens.  stats[2] = drafted, accepted.
  * Returns tokens written (<= n_new). */
 int64_t or_generate_speculative_ngram(or_session* target, const uint32_t* prompt, int64_t n_prompt,
                                       int64_t n_new, int64_t k, int64_t min_ngram, int64_t max_ngram,
                                       const uint32_t* stop, int64_t n_stop, int64_t prefill_batch,
                                       uint32_t* out, int64_t* stats, int64_t* steps_out);
+/* At temperature temp > 0 (temp <= 0: the greedy loop above): the step itself, t0 and every
+ * verified row drawn with or_sample_logits (*rng_state) in its order, a mismatch run as a
+ * corrective forward. */
+int64_t or_generate_speculative_ngram_temp(or_session* target, const uint32_t* prompt, int64_t n_prompt,
+                                           int64_t n_new, int64_t k, int64_t min_ngram, int64_t max_ngram,
+                                           float temp, uint64_t* rng_state, const uint32_t* stop, int64_t n_stop,
+                                           int64_t prefill_batch, uint32_t* out, int64_t* stats,
+                                           int64_t* steps_out);
 
 /* Oracle-drafter proposal for absolute position p (shared spec with the product). */
 uint32_t or_oracle_draft(uint64_t seed, int64_t p, float alpha, const uint32_t* greedy,

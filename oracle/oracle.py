@@ -96,6 +96,9 @@ def lib():
         "or_ngram_draft": (_i64, [_u32p, _i64, _i64, _i64, _i64, _u32p]),
         "or_generate_speculative_ngram": (_i64, [C.c_void_p, _u32p, _i64, _i64, _i64, _i64, _i64, _u32p, _i64, _i64,
                                                  _u32p, _i64p, _i64p]),
+        "or_generate_speculative_ngram_temp": (_i64, [C.c_void_p, _u32p, _i64, _i64, _i64, _i64, _i64, C.c_float,
+                                                      C.POINTER(C.c_uint64), _u32p, _i64, _i64, _u32p, _i64p,
+                                                      _i64p]),
         "or_uniform_prompt": (None, [C.c_uint64, _i64, C.c_uint32, _u32p]),
         "or_stochastic_accept": (None, [_f32p, _f32p, _u32p, _i64, _i64, C.c_float, C.c_uint64, _i64, C.POINTER(_i64), C.POINTER(C.c_uint32)]),
         "or_temperature_probs": (None, [_f32p, _i64, C.c_float, _f32p]),
@@ -435,6 +438,20 @@ class Session:
         n = lib().or_generate_speculative_ngram(self.h, p, p.size, n_new, k, min_ngram, max_ngram, st, len(stop),
                                                 prefill_batch, out, stats, steps)
         return out[:n], int(stats[0]), int(stats[1]), int(steps[0])
+
+    def generate_speculative_ngram_temp(self, prompt, n_new, k, temp, rng_state=REFERENCE_RNG_STATE, min_ngram=3,
+                                        max_ngram=4, stop=(), prefill_batch=16):
+        """ngram_speculative_step at temperature (speculative.rs:122-286, main.rs:9729-9776);
+        returns (tokens, drafted, accepted, steps, rng_state)."""
+        p = _c(prompt, np.uint32)
+        st = _c(np.asarray(stop, np.uint32).reshape(-1) if len(stop) else np.zeros(1, np.uint32), np.uint32)
+        out = np.zeros(n_new, np.uint32)
+        stats = np.zeros(2, np.int64)
+        steps = np.zeros(1, np.int64)
+        rs = C.c_uint64(rng_state)
+        n = lib().or_generate_speculative_ngram_temp(self.h, p, p.size, n_new, k, min_ngram, max_ngram, float(temp),
+                                                     C.byref(rs), st, len(stop), prefill_batch, out, stats, steps)
+        return out[:n], int(stats[0]), int(stats[1]), int(steps[0]), int(rs.value)
 
     def close(self):
         if self.h:

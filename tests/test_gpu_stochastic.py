@@ -263,3 +263,31 @@ def test_plain_loop_matches_oracle(ctx, temp):
         otoks, ost = O.generate_plain(O.Session(om, 512, 16), prompt, 30, temp, stop=stop)
         assert np.array_equal(toks, otoks) and st == ost, cut
         assert np.array_equal(toks, free[:free.tolist().index(stop[0])]) or 5 in free[:len(toks) + 1].tolist()
+
+
+@pytest.mark.parametrize("temp,prompt_seed", [(0.0, 77), (0.08, 78), (0.12, 79)])
+def test_ngram_loop_temp_matches_oracle(ctx, temp, prompt_seed):
+    """ngram_speculative_step at temperature (speculative.rs:122-286, main.rs:9729-9776): the GPU
+    loop's tokens, drafted/accepted counts, steps and LCG state equal the oracle's on repetitive
+    prompts (drafts accepted and rejected), with and without stop tokens; greedy (temp 0) runs
+    the k+1 fast path, whose counts must agree with the oracle's step form too."""
+    import nanocamelid_amd as nc
+    img = nc.synth_gguf(**TINY_UNTIED, seed=71)
+    gm, om = nc.Model(ctx, data=img), O.Model(data=img.tobytes(), nthreads=16)
+    prompt = np.tile(nc.uniform_prompt(prompt_seed, 6, 1000), 8 if temp == 0.12 else 5)
+    base, stops_done = None, []
+    for stop in [()] + [None] * 3:
+        if stop is None:
+            stop = (int(base[3 + 9 * len(stops_done)]),)
+        print(f"ngram loop T={temp} stop={stop}", flush=True)
+        toks, stats, st = nc.Session(gm, 512, 16).generate_speculative_ngram_temp(prompt, 40, 4, temp, stop=stop)
+        otoks, odr, oacc, osteps, ost = O.Session(om, 512, 16).generate_speculative_ngram_temp(prompt, 40, 4, temp,
+                                                                                            stop=stop)
+        assert np.array_equal(toks, otoks), stop
+        assert (stats.drafted, stats.accepted, stats.steps, st) == (odr, oacc, osteps, ost), stop
+        if base is None:
+            base = toks
+            assert stats.drafted > 0
+        else:
+            stops_done.append(stop)
+            assert stop[0] not in toks.tolist()

@@ -237,3 +237,119 @@ def test_plain_loop_matches_python_restatement(temp):
         assert np.array_equal(got, free[:first])  # the draws before the stop are unchanged
     short, _ = O.generate_plain(O.Session(tm, 26, 16), prompt, 30, temp)
     assert np.array_equal(short, free[:6])  # positions 20..25: six tokens fit the context
+
+
+def _ngram_loop_python(s, prompt, n_new, k, temp, state, stop=(), max_ctx=512, max_batch=16):
+    """ngram_speculative_step (speculative.rs:122-286) driven by main.rs:9729-9776, in Python."""
+    n = len(prompt)
+    for i in range(0, n - 1, 16):
+        s.prefill_pass_batch(prompt[i:min(i + 16, n - 1)], i)
+    live = s.forward_pass(prompt[-1], n - 1)
+    hist, pos, out, drafted, accepted, steps = list(prompt), n, [], 0, 0, 0
+    while pos < max_ctx and len(out) < n_new:
+        ck = min(k, n_new - len(out) - 1)  # a step emits at most the token budget
+        t0, state = O.sample_logits(live, temp, state)
+        if t0 in stop:
+            break
+        hist.append(t0)
+        drafts = [int(t) for t in O.ngram_draft(hist, ck)] if ck > 0 else []
+        drafts = drafts[:min(max_batch - 1, max_ctx - (pos + 1))]
+        steps += 1
+        if not drafts:
+            live = s.forward_pass(t0, pos)
+            out.append(t0)
+            pos += 1
+            continue
+        drafted += len(drafts)
+        s.prefill_pass_batch(np.array([t0] + drafts, np.uint32), pos)
+        emitted, hit, done = [t0], False, False
+        for i, d in enumerate(drafts):
+            tt, state = O.sample_logits(s.batch_row_logits(i), temp, state)
+            accepted += d == tt
+            if tt in stop:  # neither emitted nor consumed
+                hit, done, pos = True, True, pos + i + 1
+                break
+            emitted.append(tt)
+            if d != tt:  # corrective forward
+                live, pos, done = s.forward_pass(tt, pos + i + 1), pos + i + 2, True
+                break
+        if not done:
+            live, pos = s.batch_row_logits(len(drafts)), pos + len(drafts) + 1
+        hist += emitted[1:]
+        out += emitted
+        if hit:
+            break
+    return np.array(out, np.uint32), drafted, accepted, steps, state
+
+
+def _ngram_kplus1_python(s, prompt, n_new, k, stop=(), max_ctx=512, max_batch=16):
+    """The greedy n-gram loop in the k+1 verify form (cluster_tcp_smoke.rs:905-979: [pending] +
+    drafts in one pass, next pending = pred[accepted]) with main.rs:9729-9776's budget clamp and
+    ngram_speculative_step's stop handling (counting ends at a stop prediction), in Python."""
+    n = len(prompt)
+    for i in range(0, n - 1, 16):
+        s.prefill_pass_batch(prompt[i:min(i + 16, n - 1)], i)
+    pending = int(np.argmax(s.forward_pass(prompt[-1], n - 1)))
+    hist, pos, out, drafted, accepted, steps = list(prompt), n, [], 0, 0, 0
+    while len(out) < n_new and pending not in stop:
+        out.append(pending)
+        hist.append(pending)
+        if len(out) >= n_new or pos + 1 >= max_ctx:
+            break
+        kk = min(k, n_new - len(out), max_batch - 1, max_ctx - pos - 1)
+        drafts = [int(t) for t in O.ngram_draft(hist, kk)] if kk > 0 else []
+        batch = [pending] + drafts
+        s.prefill_pass_batch(np.array(batch, np.uint32), pos)
+        pred = [int(np.argmax(s.batch_row_logits(i))) for i in range(len(batch))]
+        a = 0
+        while a < len(drafts) and drafts[a] == pred[a]:
+            a += 1
+        drafted, steps, counted, stopped = drafted + len(drafts), steps + 1, a, False
+        for i in range(1, a + 1):
+            if batch[i] in stop:
+                counted, stopped = i, True
+                break
+            if len(out) < n_new:
+                out.append(batch[i])
+                hist.append(batch[i])
+        accepted += counted
+        pending, pos = pred[a], pos + a + 1
+        if stopped:
+            break
+    return np.array(out, np.uint32), drafted, accepted, steps
+
+
+@pytest.mark.parametrize("temp,prompt_seed", [(0.0, 77), (0.08, 78), (0.12, 79)])
+def test_ngram_loop_matches_python_restatement(temp, prompt_seed):
+    """The oracle's n-gram loops against Python restatements, with the budget clamp and stop
+    tokens, on repetitive prompts where drafts are both accepted and rejected.  At temperature
+    (the step form: t0 draw, one draw per verified row, corrective forward): same tokens,
+    counts, steps and LCG state.  Greedy (the k+1 verify form): same tokens, counts and steps;
+    the stream is the step form's and the plain greedy loop's, cut before a stop token."""
+    tm = _models(TINY, 71)
+    prompt = np.tile(nc.uniform_prompt(prompt_seed, 6, 1000), 8 if temp == 0.12 else 5)
+    cases, base = [()], None
+    while cases:
+        stop = cases.pop(0)
+        got = O.Session(tm, 512, 16).generate_speculative_ngram_temp(prompt, 40, 4, temp, stop=stop)
+        step = _ngram_loop_python(O.Session(tm, 512, 16), prompt, 40, 4, temp, O.REFERENCE_RNG_STATE, stop)
+        if temp > 0:
+            assert np.array_equal(got[0], step[0]) and got[1:] == step[1:], stop
+        else:
+            k1 = _ngram_kplus1_python(O.Session(tm, 512, 16), prompt, 40, 4, stop)
+            assert np.array_equal(got[0], k1[0]) and got[1:4] == k1[1:], stop
+            assert np.array_equal(got[0], step[0]) and got[4] == O.REFERENCE_RNG_STATE, stop
+        if base is None:
+            base = got
+            cases = [(int(base[0][c]),) for c in (2, 11, 30)]
+        else:
+            assert stop[0] not in got[0].tolist()
+    toks, drafted, acc = base[:3]
+    assert 0 < acc < drafted
+    if temp == 0.0:
+        plain, _ = O.generate_plain(O.Session(tm, 512, 16), prompt, 40, 0.0)
+        assert np.array_equal(toks, plain)
+        for c in (2, 11, 30):
+            st = int(toks[c])
+            cut = O.Session(tm, 512, 16).generate_speculative_ngram(prompt, 40, 4, stop=(st,))[0]
+            assert np.array_equal(cut, toks[:toks.tolist().index(st)])
