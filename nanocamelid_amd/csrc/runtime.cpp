@@ -1882,10 +1882,12 @@ int nc_generate_speculative_ngram_temp(nc_session* s, const uint32_t* prompt, in
         if ((rc = sample_session_rows(s, live, 1, temp, &u0, &batch[0]))) return rc;
         if (is_stop(batch[0])) break;
         history.push_back(batch[0]);
-        int64_t nd = ck > 0 ? nc_ngram_draft(history.data(), (int64_t)history.size(), min_ngram, max_ngram, (int)ck,
-                                             batch + 1)
-                            : 0;
-        nd = std::min<int64_t>(nd, std::min<int64_t>(s->max_batch - 1, s->max_ctx - (pos + 1)));
+        // drafts are truncated to the batch and the context (speculative.rs:154-159); asking the
+        // drafter for no more than that gives the same prefix and keeps batch in bounds
+        const int64_t cap = std::min<int64_t>(ck, std::min<int64_t>(s->max_batch - 1, s->max_ctx - (pos + 1)));
+        const int64_t nd = cap > 0 ? nc_ngram_draft(history.data(), (int64_t)history.size(), min_ngram, max_ngram,
+                                                    (int)cap, batch + 1)
+                                   : 0;
         steps++;
         if (nd <= 0) {
             if ((rc = nc_forward1(s, batch[0], pos, nullptr, nullptr))) return rc;

@@ -291,3 +291,16 @@ def test_ngram_loop_temp_matches_oracle(ctx, temp, prompt_seed):
         else:
             stops_done.append(stop)
             assert stop[0] not in toks.tolist()
+
+
+def test_ngram_loop_temp_k_beyond_batch(ctx):
+    """k larger than a verify batch holds (20 > max_batch - 1): drafts are capped by the batch as
+    ngram_speculative_step truncates them (speculative.rs:154-159), same as the oracle."""
+    import nanocamelid_amd as nc
+    img = nc.synth_gguf(**TINY_UNTIED, seed=71)
+    gm, om = nc.Model(ctx, data=img), O.Model(data=img.tobytes(), nthreads=16)
+    prompt = np.tile(nc.uniform_prompt(78, 6, 1000), 5)
+    toks, stats, st = nc.Session(gm, 512, 16).generate_speculative_ngram_temp(prompt, 40, 20, 0.08)
+    otoks, odr, oacc, osteps, ost = O.Session(om, 512, 16).generate_speculative_ngram_temp(prompt, 40, 20, 0.08)
+    assert np.array_equal(toks, otoks)
+    assert (stats.drafted, stats.accepted, stats.steps, st) == (odr, oacc, osteps, ost)
