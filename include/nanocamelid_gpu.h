@@ -205,6 +205,17 @@ int nc_model_get_config(const nc_model* m, nc_model_config* out);
  * (src/model.rs:851-1036), plus the shape limits of this build; fills *out on success.  The
  * same checks nc_model_load_gguf makes before reading any weight. */
 int nc_gguf_read_config(const void* data, size_t size, nc_model_config* out);
+
+/* The ids that end a turn for the file's tokenizer: is_generation_stop_token
+ * (src/main.rs:8518-8520) is membership in SpecialTokens::eog, built by Tokenizer::from_gguf
+ * (src/tokenizer.rs:287-323) from eos, eot, eom and Phi-3's "<|end|>": metadata
+ * tokenizer.ggml.{eos,eot,eom}_token_id, else eos = 2 ("llama" SentencePiece vocabularies) or
+ * the id of "<|end_of_text|>" ("gpt2" BPE), eot = the id of "<|eot_id|>".  Sorted, distinct,
+ * written to out[0..*n) (these are the stop ids the decode loops take).  NC_EFORMAT when the
+ * file has no usable tokenizer model or token list, or a special id (bos, eos, unk, eot, eom,
+ * sep, pad, mask) lies outside the vocabulary, as the reference's tokenizer load refuses it;
+ * NC_ERANGE (with *n set) when max is too small.  Host only; needs no device. */
+int nc_gguf_stop_tokens(const void* data, size_t size, uint32_t* out, int32_t max, int32_t* n);
 /* gguf::read_file's tensor descriptors (src/gguf.rs:498-550): the count (negative: error
  * code), and for tensor `index` its name, dimension count, dims (unused ones 1), GGML type id,
  * absolute data offset and byte size (tensor_nbytes, src/gguf.rs:737-763). */

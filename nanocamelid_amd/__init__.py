@@ -125,6 +125,21 @@ def gguf_read_config(data) -> dict:
     return {f: getattr(cfg, f) for f, _ in ModelConfig._fields_}
 
 
+def gguf_stop_tokens(data) -> np.ndarray:
+    """The ids that end a turn (SpecialTokens::eog of the file's tokenizer, src/tokenizer.rs:287-323,
+    tested by is_generation_stop_token, src/main.rs:8518-8520), from an image or a path (mapped,
+    not read); no GPU."""
+    if isinstance(data, str):
+        data = np.memmap(data, dtype=np.uint8, mode="r")
+    buf = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray)) else data,
+                               dtype=np.uint8)
+    out = np.zeros(16, np.uint32)
+    n = C.c_int32()
+    check(lib().nc_gguf_stop_tokens(buf.ctypes.data, buf.size, out.ctypes.data_as(C.POINTER(C.c_uint32)), 16,
+                                    C.byref(n)))
+    return out[:n.value]
+
+
 def gguf_tensors(data) -> list:
     """gguf::read_file tensor descriptors: (name, dims, type, absolute offset, n_bytes)."""
     buf = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, (bytes, bytearray)) else data,

@@ -85,6 +85,7 @@ SIGNATURES = {
     "nc_model_get_config": (C.c_int, [_vp, C.POINTER(ModelConfig)]),
     "nc_dequantize_f32": (C.c_int, [C.c_int32, _vp, _i64, _vp]),
     "nc_gguf_read_config": (C.c_int, [_vp, C.c_size_t, C.POINTER(ModelConfig)]),
+    "nc_gguf_stop_tokens": (C.c_int, [_vp, C.c_size_t, _u32p, _i32, C.POINTER(C.c_int32)]),
     "nc_gguf_tensor_count": (_i64, [_vp, C.c_size_t]),
     "nc_gguf_tensor_info": (C.c_int, [_vp, C.c_size_t, _i64, C.c_char_p, _i64, C.POINTER(C.c_int32),
                                       C.POINTER(C.c_uint64), C.POINTER(C.c_int32), C.POINTER(C.c_uint64),

@@ -57,9 +57,12 @@ bool skip_or_read(Cur& c, uint32_t type, GgufValue& v, int depth) {
             if (depth) return false;
             uint32_t it = (uint32_t)c.u(4);
             uint64_t len = c.u(8);
+            v.item_type = (int)it;
+            v.count = len;
             for (uint64_t k = 0; k < len && c.ok; k++) {
                 GgufValue t;
                 if (!skip_or_read(c, it, t, 1)) return false;
+                if (it == 8) v.strs.push_back(std::move(t.s));  // string arrays are kept (tokens)
             }
             return c.ok;
         }
@@ -254,6 +257,75 @@ bool GgufFile::get_f32(const std::string& k, float* out) const {  // gguf.rs:239
 std::string GgufFile::get_str(const std::string& k) const {
     auto it = meta.find(k);
     return (it == meta.end() || it->second.type != 8) ? std::string() : it->second.s;
+}
+
+// ---------------------------------------------------------------- tokenizer end-of-generation ids
+// Tokenizer::from_gguf (src/tokenizer.rs:203-360), the parts that decide SpecialTokens::eog:
+// the tokenizer model ("llama": SentencePiece ids, "gpt2": BPE), the token texts, and the
+// special ids from metadata or their defaults (eos: 2 / "<|end_of_text|>", eot: "<|eot_id|>",
+// Phi-3's "<|end|>"); every special id must lie inside the vocabulary (validate_token_id,
+// :1180-1189).  A text lookup takes the last token with that text, as the reference's
+// text -> id map is filled in id order.  The rest of the tokenizer (pre-tokenizer, scores,
+// merges) is not read: text <-> id conversion stays with the caller.
+bool gguf_stop_tokens(const GgufFile& g, std::vector<uint32_t>& out, std::string& err) {
+    out.clear();
+    auto mit = g.meta.find("tokenizer.ggml.model");
+    if (mit == g.meta.end() || mit->second.type != 8) {
+        err = "tokenizer.ggml.model missing";
+        return false;
+    }
+    const std::string& model = mit->second.s;
+    if (model != "llama" && model != "gpt2") {
+        err = "unsupported tokenizer model: " + model;
+        return false;
+    }
+    const bool spm = model == "llama";
+    auto tit = g.meta.find("tokenizer.ggml.tokens");
+    if (tit == g.meta.end() || tit->second.type != 9 || (tit->second.count > 0 && tit->second.item_type != 8)) {
+        err = "tokenizer.ggml.tokens missing or invalid";
+        return false;
+    }
+    const std::vector<std::string>& texts = tit->second.strs;
+    if (texts.empty()) {
+        err = "tokenizer.ggml.tokens must not be empty";
+        return false;
+    }
+    const auto find_text = [&](const char* t, int64_t* id) {
+        for (int64_t i = (int64_t)texts.size() - 1; i >= 0; i--)
+            if (texts[i] == t) {
+                *id = i;
+                return true;
+            }
+        return false;
+    };
+    // (id or -1) from a metadata key, else a default
+    const auto meta_id = [&](const char* key, int64_t dflt) {
+        uint32_t v;
+        return g.get_u32(key, &v) ? (int64_t)v : dflt;
+    };
+    int64_t tmp;
+    const int64_t bos = meta_id("tokenizer.ggml.bos_token_id", spm ? 1 : (find_text("<|begin_of_text|>", &tmp) ? tmp : -1));
+    const int64_t eos = meta_id("tokenizer.ggml.eos_token_id", spm ? 2 : (find_text("<|end_of_text|>", &tmp) ? tmp : -1));
+    const int64_t unk = meta_id("tokenizer.ggml.unknown_token_id", spm ? 0 : -1);
+    const int64_t eot = meta_id("tokenizer.ggml.eot_token_id", find_text("<|eot_id|>", &tmp) ? tmp : -1);
+    const int64_t eom = meta_id("tokenizer.ggml.eom_token_id", -1);
+    const int64_t phi_end = find_text("<|end|>", &tmp) ? tmp : -1;
+    const int64_t sep = meta_id("tokenizer.ggml.separator_token_id", meta_id("tokenizer.ggml.seperator_token_id", -1));
+    const int64_t pad = meta_id("tokenizer.ggml.padding_token_id", -1);
+    const int64_t mask = meta_id("tokenizer.ggml.mask_token_id", -1);
+    const std::pair<const char*, int64_t> special[] = {{"bos", bos}, {"eos", eos}, {"unk", unk},  {"eot", eot},
+                                                       {"eom", eom}, {"sep", sep}, {"pad", pad}, {"mask", mask}};
+    for (const auto& [name, id] : special)
+        if (id >= (int64_t)texts.size()) {
+            err = std::string(name) + " token id " + std::to_string(id) + " out of range for vocab size " +
+                  std::to_string(texts.size());
+            return false;
+        }
+    for (int64_t id : {eos, eot, eom, phi_end})
+        if (id >= 0) out.push_back((uint32_t)id);
+    std::sort(out.begin(), out.end());
+    out.erase(std::unique(out.begin(), out.end()), out.end());
+    return true;
 }
 
 // ---------------------------------------------------------------- Philox4x32-10

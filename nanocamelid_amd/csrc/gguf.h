@@ -18,6 +18,10 @@ struct GgufValue {
     int64_t i = 0;
     double f = 0;
     std::string s;
+    // arrays (type 9): the item type and count; the items themselves only for strings
+    int item_type = -1;
+    uint64_t count = 0;
+    std::vector<std::string> strs;
 };
 
 struct GgufTensor {
@@ -46,6 +50,9 @@ bool gguf_type_layout(uint32_t type, uint64_t* block, uint64_t* bytes);
 bool gguf_tensor_nbytes(const std::string& name, const std::vector<uint64_t>& dims, uint32_t type, uint64_t* out,
                         std::string& err);
 bool gguf_parse(const uint8_t* data, size_t size, GgufFile& out, std::string& err);
+
+// SpecialTokens::eog of the file's tokenizer (src/tokenizer.rs:203-323): sorted, distinct ids.
+bool gguf_stop_tokens(const GgufFile& g, std::vector<uint32_t>& out, std::string& err);
 
 // Tensor bytes -> f32 as the reference's load_f32_or_f16 (dequant.cpp); n values.
 bool dequant_supported(uint32_t type);

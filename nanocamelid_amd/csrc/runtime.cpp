@@ -1457,6 +1457,19 @@ int nc_gguf_read_config(const void* data, size_t size, nc_model_config* out) {
     return NC_OK;
 }
 
+int nc_gguf_stop_tokens(const void* data, size_t size, uint32_t* out, int32_t max, int32_t* n) {
+    if (!data || !n || max < 0 || (max > 0 && !out)) return fail(NC_EINVAL, "nc_gguf_stop_tokens: bad arguments");
+    GgufFile g;
+    std::string err;
+    if (!gguf_parse((const uint8_t*)data, size, g, err)) return fail(NC_EFORMAT, err);
+    std::vector<uint32_t> ids;
+    if (!gguf_stop_tokens(g, ids, err)) return fail(NC_EFORMAT, err);
+    *n = (int32_t)ids.size();
+    if ((int64_t)ids.size() > max) return fail(NC_ERANGE, "nc_gguf_stop_tokens: more ids than max");
+    std::copy(ids.begin(), ids.end(), out);
+    return NC_OK;
+}
+
 int64_t nc_gguf_tensor_count(const void* data, size_t size) {
     if (!data) return fail(NC_EINVAL, "nc_gguf_tensor_count: null argument");
     GgufFile g;

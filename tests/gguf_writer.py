@@ -7,7 +7,7 @@ import struct
 
 import numpy as np
 
-T_U32, T_I32, T_F32, T_STR, T_U64 = 4, 5, 6, 8, 10
+T_U32, T_I32, T_F32, T_STR, T_ARR, T_U64 = 4, 5, 6, 8, 9, 10
 
 
 def _str(s: str) -> bytes:
@@ -26,6 +26,9 @@ def _val(t: int, v) -> bytes:
         return struct.pack("<Q", v)
     if t == T_STR:
         return _str(v)
+    if t == T_ARR:  # v = (item type, items)
+        it, items = v
+        return struct.pack("<I", it) + struct.pack("<Q", len(items)) + b"".join(_val(it, x) for x in items)
     raise ValueError(t)
 
 
