@@ -270,13 +270,21 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
     out.type = type;
     out.rows = rows;
     out.cols = cols;
-    // R16 for Q4_0 matrices too small to fill the chip with 64-row tiles.  An interleaved
-    // gate/up pair keeps its 64-row groups (gate rows 32t.. in rows 0-31 of group t, up rows in
-    // 32-63): with R16 those are four consecutive 16-row tiles, which one workgroup covers.
+    // R16 for Q4_0 matrices below 1024 64-row tiles: every layer matrix up to the 70B shape
+    // (57344 x 8192 as a plain matmul, us at N = 1 / 5 / 9 / 16: R64 47.7 / 78.1 / 110.2 / 288.3,
+    // R16 43.6 / 70.1 / 92.1 / 129.0; the 70B verify pass 34.6 -> 30.5 ms), while the 128256 x 4096
+    // head stays on R64 (R16 78.7 against 69.5 us at N = 5).  An interleaved gate/up pair keeps
+    // its 64-row groups (gate rows 32t.. in rows 0-31 of group t, up rows in 32-63): with R16
+    // those are four consecutive 16-row tiles, which one workgroup covers.
     // Q4_K likewise on 16-row tiles below 256 64-row tiles, except an interleaved gate/up pair
     // (its SwiGLU epilogue needs the 64-row groups; those matrices are large anyway).
     const bool single = std::all_of(parts.begin(), parts.end(), [](const Part& q) { return q.half < 0; });
-    out.layout = type == NC_TYPE_Q4_0 && (rows + 63) / 64 < 512 ? LAYOUT_R16 : LAYOUT_R64;
+    // NC_R16_MAX_TILES=<n>: tuning override of the 64-row tile count below which Q4_0 takes R16
+    static const int64_t r16_max = [] {
+        const char* e = getenv("NC_R16_MAX_TILES");
+        return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)1024;
+    }();
+    out.layout = type == NC_TYPE_Q4_0 && (rows + 63) / 64 < r16_max ? LAYOUT_R16 : LAYOUT_R64;
     if (type == NC_TYPE_Q4_K && single && (rows + 63) / 64 < 256) out.layout = LAYOUT_R16K;
     out.units = type == NC_TYPE_Q4_0 ? cols / 32 : cols / 256;
     if (out.layout == LAYOUT_R16) {
