@@ -42,6 +42,21 @@ def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
+GEMM_KERNELS = {"auto": 0, "dot4": 1, "mfma": 2}  # NC_GEMM_KERNEL_*
+GEMM_KERNEL = "auto"
+ATTENTION_ORDERS = {"sequential": 0, "split": 1}  # NC_ATTN_*
+ATTENTION = "sequential"
+
+
+def make_ctx(nc):
+    """Device context on GPU 0 with the --gemm-kernel dot-product path and the --attention
+    summation order selected."""
+    ctx = nc.Context(0)
+    ctx.set_gemm_kernel(GEMM_KERNELS[GEMM_KERNEL])
+    ctx.set_attention(ATTENTION_ORDERS[ATTENTION])
+    return ctx
+
+
 def cpu_model_name():
     try:
         for line in open("/proc/cpuinfo"):
@@ -154,7 +169,7 @@ def run_gemm_sweep(args):
     import torch
 
     import nanocamelid_amd as nc
-    ctx = nc.Context(0)
+    ctx = make_ctx(nc)
     shapes = [(4096, 4096, "q/o"), (1024, 4096, "k/v"), (14336, 4096, "gate/up"), (4096, 14336, "down"),
               (128256, 4096, "lm_head")]
     stream = torch.cuda.current_stream()
@@ -197,7 +212,7 @@ def run_prefill(args):
     import torch
 
     import nanocamelid_amd as nc
-    ctx = nc.Context(0)
+    ctx = make_ctx(nc)
     shapes = [(6144, 4096, "8b q,k,v", 2), (4096, 4096, "8b wo", 2), (28672, 4096, "8b gate,up", 2),
               (4096, 14336, "8b down", 2), (57344, 8192, "70b gate,up", 2), (8192, 28672, "70b down", 2),
               (8192, 3072, "3b Q4_K gate", 12), (3072, 8192, "3b Q4_K down", 12)]
@@ -284,7 +299,7 @@ def run_loader(args):
         path = os.path.join(d, "llama-3-8b-q4_0.gguf")
         img.tofile(path)
         del img
-        ctx = nc.Context(0)
+        ctx = make_ctx(nc)
         t = time.perf_counter()
         m = nc.Model(ctx, path=path, nthreads=HOST_THREADS)
         ctx.synchronize()
@@ -316,7 +331,7 @@ def run_config3(args):
     dimg = nc.synth_gguf(**nc.SYNTH_CONFIGS["llama-3.2-1b"], context_length=8192, seed=args.seed + 1,
                          nthreads=HOST_THREADS)
     log(f"synthetic target {timg.nbytes / 1e9:.2f} GB + draft {dimg.nbytes / 1e9:.2f} GB in {time.time() - t0:.1f}s")
-    ctx = nc.Context(0)
+    ctx = make_ctx(nc)
     tm = nc.Model(ctx, data=timg, nthreads=HOST_THREADS)
     dm = nc.Model(ctx, data=dimg, nthreads=HOST_THREADS)
     V = tm.config["vocab_size"]
@@ -399,7 +414,7 @@ def run_config4(args):
     img = nc.synth_gguf(**nc.SYNTH_CONFIGS["llama-3-70b"], context_length=8192 + 64, seed=args.seed,
                         nthreads=HOST_THREADS)
     log(f"synthetic llama-3-70b GGUF: {img.nbytes / 1e9:.2f} GB in {time.time() - t0:.1f}s")
-    ctx = nc.Context(0)
+    ctx = make_ctx(nc)
     t0 = time.time()
     model = nc.Model(ctx, data=img, nthreads=HOST_THREADS)
     del img
@@ -487,9 +502,16 @@ def main():
     ap.add_argument("--c4-passes", type=int, default=10)
     ap.add_argument("--c3-prompt", type=int, default=3072)
     ap.add_argument("--c3-new", type=int, default=768)
+    ap.add_argument("--gemm-kernel", choices=sorted(GEMM_KERNELS), default="auto",
+                    help="dot-product path of the Q4_0 16-row matmuls (nc_ctx_set_gemm_kernel)")
+    ap.add_argument("--attention", choices=sorted(ATTENTION_ORDERS), default="sequential",
+                    help="summation order of the verify passes' attention (nc_ctx_set_attention)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy (known HBM bytes) to scale rocprofv3 --pmc byte counters")
     args = ap.parse_args()
+    global GEMM_KERNEL, ATTENTION
+    GEMM_KERNEL = args.gemm_kernel
+    ATTENTION = args.attention
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU (multi-GPU sharding is designed, not "
                                    "built); run with --gpus 1"}))
@@ -520,7 +542,7 @@ def main():
     t0 = time.time()
     img = nc.synth_gguf(**spec, context_length=8192, seed=args.seed, nthreads=HOST_THREADS)
     log(f"synthetic {args.config} GGUF: {img.nbytes / 1e9:.2f} GB in {time.time() - t0:.1f}s")
-    ctx = nc.Context(0)
+    ctx = make_ctx(nc)
     t0 = time.time()
     model = nc.Model(ctx, data=img, nthreads=HOST_THREADS)
     cfg = model.config

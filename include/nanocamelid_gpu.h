@@ -71,6 +71,20 @@ int nc_ctx_synchronize(nc_ctx* ctx);
 #define NC_GEMM_KERNEL_MFMA 2
 int nc_ctx_set_gemm_kernel(nc_ctx* ctx, int kernel);
 
+/* Summation order of the attention in the verify and decode passes (nc_verify_greedy,
+ * nc_forward1 and the decode loops) of this context's sessions; replaces the softmax and
+ * weighted-V loops of the reference's attention (src/inference.rs:3522-3540, :3603-3623).
+ * SEQUENTIAL (the default): the reference's left-to-right sums, bit-identical.  SPLIT: each
+ * row's positions in 64-position chunks, per chunk a max, a sum of exp and an exp-weighted V
+ * sum, the chunks combined in a fixed order; f32 outputs equal the sequential ones up to
+ * rounding (the verify path's 1e-3 relative bound for f32 outputs), and a row's result does
+ * not depend on the batch it is in, so speculative and plain decoding emit one stream.  Keys
+ * and values are read once per KV head and chunk for all heads and rows of a pass.  Prompt
+ * passes (nc_prefill) keep the sequential order.  Set it between calls. */
+#define NC_ATTN_SEQUENTIAL 0
+#define NC_ATTN_SPLIT 1
+int nc_ctx_set_attention(nc_ctx* ctx, int order);
+
 /* ---------------------------------------------------------------- operator boundary */
 /* Uploads a row-major GGUF quantized matrix (rows x cols, GGUF dims [cols, rows])
  * and repacks it into the device layout.  Replaces the load-time matrix

@@ -55,6 +55,12 @@ class Context:
         counterpart of the reference's Q8DotKernelSelector (src/q8.rs:42-46)."""
         check(lib().nc_ctx_set_gemm_kernel(self.h, int(kernel)))
 
+    def set_attention(self, order: int):
+        """Summation order of the verify and decode passes' attention: NC_ATTN_SEQUENTIAL (the
+        reference's left-to-right sums, bit-identical) or NC_ATTN_SPLIT (64-position chunks
+        combined in a fixed order; equal up to f32 rounding, batch-independent)."""
+        check(lib().nc_ctx_set_attention(self.h, int(order)))
+
     def close(self):
         if getattr(self, "h", None):
             lib().nc_ctx_free(self.h)

@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(_HERE, "lib", "libnanocamelid_hip.so")
 NC_OK, NC_EINVAL, NC_ENOMEM, NC_EHIP, NC_EFORMAT, NC_ERANGE = 0, -1, -2, -3, -4, -5
 NC_TYPE_F32, NC_TYPE_Q4_0, NC_TYPE_Q4_K, NC_TYPE_Q6_K = 0, 2, 12, 14
 NC_GEMM_KERNEL_AUTO, NC_GEMM_KERNEL_DOT4, NC_GEMM_KERNEL_MFMA = 0, 1, 2
+NC_ATTN_SEQUENTIAL, NC_ATTN_SPLIT = 0, 1
 
 
 class ModelConfig(C.Structure):
@@ -67,6 +68,7 @@ SIGNATURES = {
     "nc_ctx_free": (None, [_vp]),
     "nc_ctx_synchronize": (C.c_int, [_vp]),
     "nc_ctx_set_gemm_kernel": (C.c_int, [_vp, C.c_int]),
+    "nc_ctx_set_attention": (C.c_int, [_vp, C.c_int]),
     "nc_qmat_upload": (C.c_int, [_vp, C.c_int, _i64, _i64, _vp, C.POINTER(_vp)]),
     "nc_qmat_free": (None, [_vp]),
     "nc_qmat_device_bytes": (_i64, [_vp]),

@@ -8,7 +8,8 @@
 // parallel evaluation that is verified step by step against the sequential recurrence);
 // each attention dot product and the weighted V sum are evaluated in order.  The parallel
 // parts are the order-free ones (max, elementwise maps, integer sums, independent
-// rows/heads/positions).
+// rows/heads/positions).  The one exception is opt-in: the split-position attention
+// (NC_ATTN_SPLIT) sums in a fixed chunked order of its own.
 #include "nc_device.h"
 #include "nc_chain.h"
 #include "nc_internal.h"
@@ -642,11 +643,259 @@ __global__ __launch_bounds__(T) void attn_fused_kernel(AttnParams a) {
     weighted_v_q8<HD, false>(a, n, h, kvh, L, probs);  // no barriers below
 }
 
+// ---------------------------------------------------------------- split-position attention
+// NC_ATTN_SPLIT.  The reference's attention (inference.rs:3522-3540 softmax, 3603-3623 weighted
+// V sum) with its sums taken in a fixed split order instead of left to right: the positions of
+// a row are cut into chunks of kSplitChunk, and per (query, chunk)
+//   m_c = max s_p,  l_c = sum_p exp(s_p - m_c),  o_c[d] = sum_p exp(s_p - m_c) * v_p[d];
+// the combine step takes M = max m_c, w_c = exp(m_c - M), out = (sum_c w_c o_c) / (sum_c w_c l_c).
+// Equal to the sequential softmax and weighted sum up to f32 rounding.  Chunks sit at absolute
+// positions and each query's arithmetic is the same whichever workgroup computes it, so a row's
+// output does not depend on the batch it is in.  One workgroup = (KV head, query group, chunk):
+// the chunk's keys and values are read from HBM once for all query heads and rows of the group
+// (the sequential kernels read them once per (row, head) unit), and a long row is spread over
+// as many workgroups as it has chunks.
+constexpr int kSplitChunk = 64;
+
+// Workgroup of 4 waves over CPW consecutive chunks of one KV head and WGQ = QG * 4 / CPW
+// queries: wave w takes chunk CPW * blockIdx.z + w % CPW and queries (w / CPW) * QG .. + QG - 1
+// of the group.  CPW = 4: every key and value of a chunk is read once per workgroup (long rows);
+// CPW = 1: four waves share one chunk (short rows, where chunks are few).  Query j of group z is
+// qi = z * WGQ + j = g * N + n (head kvh * G + g, row n).  Score phase: lane = position of the
+// chunk.  Value phase: lane = output dims lane (and lane + 64 at HD = 128).
+template <int HD, int QG, int CPW>
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnParams a) {
+    constexpr int C = kSplitChunk, NQ = HD / 4, DL = HD / 64, WGQ = QG * 4 / CPW;
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) float qs[WGQ][HD];
+    __shared__ __align__(16) float es[4][QG][C];
+    const int G = a.H / a.Hkv, GN = G * a.N;
+    const int kvh = blockIdx.x, z = blockIdx.y;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int c = CPW * blockIdx.z + w % CPW;  // this wave's chunk (past the last: all masked)
+    const int q0 = z * WGQ + (w / CPW) * QG;   // this wave's first query
+    const int pos0 = a.d_pos[0];
+    const int plast = pos0 + a.N - 1;
+    const bool chunk_live = c * C <= plast;  // uniform
+    const int p0 = c * C;
+    for (int e = t; e < WGQ * HD; e += 256) {
+        const int i = e / HD, d = e % HD, qi = z * WGQ + i;
+        float v = 0.0f;
+        if (qi < GN) v = a.q[((size_t)(qi % a.N) * a.H + kvh * G + qi / a.N) * HD + d];
+        qs[i][d] = v;
+    }
+    __syncthreads();
+    // scores s_p = (q . k_p) * scale of this lane's position; keys are dim quads
+    // [HD/4][max_ctx][4], so a wave's 16-byte loads of one dim quad are 1 KB contiguous.  A lane
+    // past the pass's last row takes an offset outside the buffer (reads 0, no access).
+    const int p = p0 + lane;
+    const int kvo = p <= plast ? p * 16 : 0x40000000;
+    const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.kcache + (size_t)kvh * a.max_ctx * HD), 0, a.max_ctx * HD * 4, 0x00020000);
+    const int qstride = a.max_ctx * 16;
+    float dot[QG];
+#pragma unroll
+    for (int k = 0; k < QG; k++) dot[k] = 0.0f;
+    constexpr int KB = 4;  // dim quads per batch of loads
+#pragma unroll 1
+    for (int h0 = 0; h0 < NQ; h0 += KB) {
+        f4v kv[KB];
+#pragma unroll
+        for (int i = 0; i < KB; i++)
+            kv[i] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(kres, kvo, (h0 + i) * qstride, 0));
+#pragma unroll
+        for (int i = 0; i < KB; i++) {
+#pragma unroll
+            for (int k = 0; k < QG; k++) {
+                const f4v qv = *(const f4v*)&qs[(w / CPW) * QG + k][4 * (h0 + i)];
+                dot[k] = __builtin_fmaf(qv.x, kv[i].x, dot[k]);
+                dot[k] = __builtin_fmaf(qv.y, kv[i].y, dot[k]);
+                dot[k] = __builtin_fmaf(qv.z, kv[i].z, dot[k]);
+                dot[k] = __builtin_fmaf(qv.w, kv[i].w, dot[k]);
+            }
+        }
+    }
+    // chunk softmax partials: a position past the query's row is masked
+#pragma unroll
+    for (int k = 0; k < QG; k++) {
+        const int qi = q0 + k;
+        const bool live = qi < GN && p <= pos0 + qi % a.N;
+        const float s = live ? dot[k] * a.scale : -__builtin_inff();
+        float m = s;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float o = __shfl_xor(m, off, 64);
+            m = o > m ? o : m;
+        }
+        const float e = live ? expf_glibc(s - m) : 0.0f;
+        float l = e;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) l = l + __shfl_xor(l, off, 64);
+        es[w][k][lane] = e;
+        if (lane == 0 && qi < GN && chunk_live) {
+            const size_t u = ((size_t)(qi % a.N) * a.H + kvh * G + qi / a.N) * a.nchunks + c;
+            a.part_ml[2 * u] = m;  // -inf (and l = 0) when the whole chunk is past the row
+            a.part_ml[2 * u + 1] = l;
+        }
+    }
+    __syncthreads();
+    // o_c[d] = sum_p e_p * v_p[d]; values are position quads [max_ctx/4][HD][4].  Quads past the
+    // one holding the pass's last row are not read (the quad index is clamped to it) and
+    // positions past that row are zeroed (never-written cache rows may hold any bits; e = 0 there)
+    const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.vcache + (size_t)kvh * a.max_ctx * HD), 0, a.max_ctx * HD * 4, 0x00020000);
+    const int qlast = plast >> 2;
+    float o[QG][DL];
+#pragma unroll
+    for (int k = 0; k < QG; k++)
+#pragma unroll
+        for (int dl = 0; dl < DL; dl++) o[k][dl] = 0.0f;
+    constexpr int PB = 2;  // position quads per batch of loads
+#pragma unroll 1
+    for (int b0 = 0; b0 < C / 4; b0 += PB) {
+        f4v vv[PB][DL];
+#pragma unroll
+        for (int j = 0; j < PB; j++)
+#pragma unroll
+            for (int dl = 0; dl < DL; dl++)
+                vv[j][dl] = __builtin_bit_cast(
+                    f4v, __builtin_amdgcn_raw_buffer_load_b128(vres, (lane + 64 * dl) * 16,
+                                                               min(p0 / 4 + b0 + j, qlast) * (HD * 16), 0));
+#pragma unroll
+        for (int j = 0; j < PB; j++) {
+            const int pq = p0 + 4 * (b0 + j);
+            if (pq + 3 > plast) {  // uniform: the quad holding the pass's last row, or past it
+#pragma unroll
+                for (int dl = 0; dl < DL; dl++) {
+                    vv[j][dl].x = pq <= plast ? vv[j][dl].x : 0.0f;
+                    vv[j][dl].y = pq + 1 <= plast ? vv[j][dl].y : 0.0f;
+                    vv[j][dl].z = pq + 2 <= plast ? vv[j][dl].z : 0.0f;
+                    vv[j][dl].w = 0.0f;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < QG; k++) {
+                const f4v e4 = *(const f4v*)&es[w][k][4 * (b0 + j)];
+#pragma unroll
+                for (int dl = 0; dl < DL; dl++) {
+                    o[k][dl] = __builtin_fmaf(e4.x, vv[j][dl].x, o[k][dl]);
+                    o[k][dl] = __builtin_fmaf(e4.y, vv[j][dl].y, o[k][dl]);
+                    o[k][dl] = __builtin_fmaf(e4.z, vv[j][dl].z, o[k][dl]);
+                    o[k][dl] = __builtin_fmaf(e4.w, vv[j][dl].w, o[k][dl]);
+                }
+            }
+        }
+    }
+    if (!chunk_live) return;
+#pragma unroll
+    for (int k = 0; k < QG; k++) {
+        const int qi = q0 + k;
+        if (qi < GN) {  // uniform
+            const size_t u = ((size_t)(qi % a.N) * a.H + kvh * G + qi / a.N) * a.nchunks + c;
+#pragma unroll
+            for (int dl = 0; dl < DL; dl++) a.part_o[u * HD + lane + 64 * dl] = o[k][dl];
+        }
+    }
+}
+
+// Combine of a (row n, head h) unit's chunk partials, then the Q8_0 quantisation of its output
+// block for the wo matmul; thread = output dim.  The chunk max M and the weights
+// w_c = expf(m_c - M) are formed in parallel into LDS; the sums l = fma(w_c, l_c, l) and
+// o = fma(w_c, o_c, o) run in chunk order, the partial outputs loaded a batch ahead.
+constexpr int kSplitMaxChunks = NC_MAX_CONTEXT / kSplitChunk;
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams a) {
+    __shared__ float wl[2][kSplitMaxChunks];  // w_c, l_c
+    __shared__ float red[HD / 64];
+    const int n = blockIdx.x / a.H, h = blockIdx.x % a.H;
+    const int t = threadIdx.x;
+    const int nc = (a.d_pos[0] + n) / kSplitChunk + 1;  // chunks holding positions 0..pos
+    const size_t u0 = ((size_t)n * a.H + h) * a.nchunks;
+    const float* ml = a.part_ml + 2 * u0;
+    float M = -__builtin_inff();
+    for (int c = t; c < nc; c += HD) M = ml[2 * c] > M ? ml[2 * c] : M;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(M, off, 64);
+        M = o > M ? o : M;
+    }
+    if ((t & 63) == 0) red[t >> 6] = M;
+    __syncthreads();
+    M = red[0];
+#pragma unroll
+    for (int i = 1; i < HD / 64; i++) M = red[i] > M ? red[i] : M;
+    for (int c = t; c < nc; c += HD) {
+        wl[0][c] = expf_glibc(ml[2 * c] - M);  // chunk 0 always holds position 0: M finite
+        wl[1][c] = ml[2 * c + 1];
+    }
+    __syncthreads();
+    const float* po = a.part_o + u0 * HD + t;
+    float l = 0.0f, o = 0.0f;
+    constexpr int B = 8;
+    for (int c0 = 0; c0 < nc; c0 += B) {
+        float v[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) v[j] = po[(size_t)min(c0 + j, nc - 1) * HD];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            if (c0 + j < nc) {  // uniform
+                l = __builtin_fmaf(wl[0][c0 + j], wl[1][c0 + j], l);
+                o = __builtin_fmaf(wl[0][c0 + j], v[j], o);
+            }
+        }
+    }
+    const float y = o / l;
+    const int aw = a.H * HD;
+    const int col = h * HD + (t & ~31);
+    store_q8_block(y, t & 31, a.xq + (size_t)n * aw + col, a.xs + (size_t)n * (aw / 32) + col / 32,
+                   a.xs8 + (size_t)n * (aw / 32) + col / 32);
+}
+
+static int launch_attention_split(const AttnParams& a, hipStream_t st) {
+    const int G = a.H / a.Hkv, GN = G * a.N;
+    const int nch = a.max_pos / kSplitChunk + 1;
+    if (nch > a.nchunks) return fail(NC_ERANGE, "attention: row longer than the split partials hold");
+    // Queries per wave (4..16, a multiple of 4): as many as still give ~1024 chunk waves (one
+    // per SIMD), since every query group re-reads the chunk's keys and values; at most 16
+    // (registers).  Rows with too few chunks for that put four waves on one chunk (CPW = 1).
+    const int want = (1024 + a.Hkv * nch - 1) / (a.Hkv * nch);
+    const int ngroups = std::max((GN + 15) / 16, std::min((GN + 3) / 4, want));
+    const int qg = ((GN + ngroups - 1) / ngroups + 3) / 4 * 4;
+    const bool wide = a.Hkv * nch * ((GN + qg - 1) / qg) >= 1024;
+    const int cpw = wide ? 4 : 1, wgq = qg * 4 / cpw;
+    const dim3 grid(a.Hkv, (GN + wgq - 1) / wgq, (nch + cpw - 1) / cpw);
+#define NC_SPLIT_QG(HD, CPW)                                                                               \
+    switch (qg) {                                                                                          \
+        case 4: hipLaunchKernelGGL((attn_split_kernel<HD, 4, CPW>), grid, dim3(256), 0, st, a); break;    \
+        case 8: hipLaunchKernelGGL((attn_split_kernel<HD, 8, CPW>), grid, dim3(256), 0, st, a); break;    \
+        case 12: hipLaunchKernelGGL((attn_split_kernel<HD, 12, CPW>), grid, dim3(256), 0, st, a); break;  \
+        default: hipLaunchKernelGGL((attn_split_kernel<HD, 16, CPW>), grid, dim3(256), 0, st, a); break;  \
+    }
+#define NC_SPLIT(HD)                                                                            \
+    if (wide) {                                                                                 \
+        NC_SPLIT_QG(HD, 4)                                                                      \
+    } else {                                                                                    \
+        NC_SPLIT_QG(HD, 1)                                                                      \
+    }                                                                                           \
+    NC_HIP(hipGetLastError());                                                                  \
+    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.N * a.H), dim3(HD), 0, st, a);
+    if (a.hd == 128) {
+        NC_SPLIT(128)
+    } else {
+        NC_SPLIT(64)
+    }
+#undef NC_SPLIT
+#undef NC_SPLIT_QG
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
 int launch_attention(const AttnParams& a, hipStream_t st) {
     const int G = a.H / a.Hkv;
     if (G > 8 || a.H % a.Hkv) return fail(NC_EINVAL, "attention: at most 8 query heads per KV head supported");
     const int tiles = (a.max_pos + 64) / 64;
     if (a.hd != 64 && a.hd != 128) return fail(NC_EINVAL, "attention: head_dim must be 64 or 128");
+    if (a.split) return launch_attention_split(a, st);
     // max_pos + 1 is the longest score row of the pass
     const int len = a.max_pos + 1;
     const dim3 grid(a.N * a.H);

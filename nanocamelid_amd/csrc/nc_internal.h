@@ -143,6 +143,11 @@ struct AttnParams {
     const int32_t* d_pos = nullptr;
     int N = 0, H = 0, Hkv = 0, hd = 0, max_ctx = 0, max_pos = 0;
     float scale = 0.f;
+    // split-position order (NC_ATTN_SPLIT): per (row, head, 64-position chunk) partials
+    bool split = false;
+    float* part_o = nullptr;   // [N][H][nchunks][hd]
+    float* part_ml = nullptr;  // [N][H][nchunks][2] chunk max, chunk sum of exp
+    int nchunks = 0;
 };
 int launch_attention(const AttnParams& a, hipStream_t stream);
 
@@ -226,6 +231,7 @@ struct nc_ctx {
     // device address of the static scratch array on this context's device (never freed)
     int32_t* static_scratch = nullptr;
     int gemm_kernel = NC_GEMM_KERNEL_AUTO;  // dot-product path of the quantized matmuls
+    int attn_order = NC_ATTN_SEQUENTIAL;     // summation order of the verify passes' attention
 };
 
 struct nc_qmat {

@@ -67,6 +67,9 @@ struct nc_session {
     int32_t* xs8 = nullptr;  // -8 * per-block int8 sums
     float* q = nullptr;       // [B][aw]
     float* scores = nullptr;  // [B][H][ctx_stride]
+    float* attn_part_o = nullptr;   // [B][H][attn_chunks][hd] split-order attention partials
+    float* attn_part_ml = nullptr;  // [B][H][attn_chunks][2]
+    int attn_chunks = 0;
     float* logits = nullptr;  // [B][V]
     float* probs = nullptr;   // [B][V] temperature probabilities of the last pass's rows
     float* qbuf = nullptr;    // [B][V] draft probabilities of the current speculative step
@@ -820,6 +823,10 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         a.max_ctx = (int)s->ctx_stride;
         a.max_pos = (int)(start_pos + n - 1);
         a.scale = 1.0f / std::sqrt((float)hd);  // inference.rs:3927
+        a.split = s->ctx->attn_order == NC_ATTN_SPLIT;
+        a.part_o = s->attn_part_o;
+        a.part_ml = s->attn_part_ml;
+        a.nchunks = s->attn_chunks;
         if ((rc = launch_attention(a, st))) return rc;
         GemmParams po;
         po.kernel = s->ctx->gemm_kernel;
@@ -1217,6 +1224,13 @@ void nc_ctx_free(nc_ctx* c) {
     delete c;
 }
 
+int nc_ctx_set_attention(nc_ctx* c, int order) {
+    if (!c || (order != NC_ATTN_SEQUENTIAL && order != NC_ATTN_SPLIT))
+        return fail(NC_EINVAL, "nc_ctx_set_attention: unknown summation order");
+    c->attn_order = order;
+    return NC_OK;
+}
+
 int nc_ctx_set_gemm_kernel(nc_ctx* c, int kernel) {
     if (!c || kernel < NC_GEMM_KERNEL_AUTO || kernel > NC_GEMM_KERNEL_MFMA)
         return fail(NC_EINVAL, "nc_ctx_set_gemm_kernel: unknown kernel");
@@ -1543,6 +1557,7 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
     s->ctx = m->ctx;
     s->max_ctx = max_ctx;
     s->ctx_stride = (max_ctx + 3) / 4 * 4;
+    s->attn_chunks = (int)((max_ctx + 63) / 64);  // 64-position chunks of the split-order attention
     s->max_batch = max_batch;
     NC_HIP(hipStreamCreate(&s->stream));
     const nc_model_config& c = m->cfg;
@@ -1557,6 +1572,8 @@ int nc_session_create(nc_model* m, int64_t max_ctx, int32_t max_batch, nc_sessio
         (rc = dev_alloc(s->allocs, &s->xs8, 2 * B * (s->maxw / 32))) ||
         (rc = dev_alloc(s->allocs, &s->q, B * c.attention_output_width)) ||
         (rc = dev_alloc(s->allocs, &s->scores, (size_t)B * c.head_count * s->ctx_stride)) ||
+        (rc = dev_alloc(s->allocs, &s->attn_part_o, (size_t)B * c.head_count * s->attn_chunks * c.head_dim)) ||
+        (rc = dev_alloc(s->allocs, &s->attn_part_ml, (size_t)B * c.head_count * s->attn_chunks * 2)) ||
         (rc = dev_alloc(s->allocs, &s->logits, (size_t)B * c.vocab_size)) ||
         (rc = dev_alloc(s->allocs, &s->probs, (size_t)B * c.vocab_size)) ||
         (rc = dev_alloc(s->allocs, &s->qbuf, (size_t)B * c.vocab_size)) ||

@@ -230,6 +230,7 @@ struct or_session {
     std::vector<float> xs;
     std::vector<float> logits;  // single-token workspace logits [V]
     std::vector<float> row_hidden;
+    int attn_order = 0;  // 0: or_attention_head, 1: or_attention_head_split
 };
 
 namespace {
@@ -390,9 +391,14 @@ void run_layers(or_session* s, int64_t N, int64_t start_pos) {
             int64_t pos = start_pos + t;
             parallel_rows(m->H, m->H >= 8 ? std::min<int>(m->nthreads, 8) : 1, [&](int64_t lo, int64_t hi) {
                 std::vector<float> sc(pos + 1);
-                for (int64_t h = lo; h < hi; h++)
-                    or_attention_head(&s->attn[t * aw + h * m->hd], sc.data(), &s->q[t * aw + h * m->hd],
-                                      kc, vc, pos, kw, h / kv_mul, m->hd, scale);
+                for (int64_t h = lo; h < hi; h++) {
+                    if (s->attn_order == 1)
+                        or_attention_head_split(&s->attn[t * aw + h * m->hd], &s->q[t * aw + h * m->hd], kc, vc, pos,
+                                                start_pos + N - 1, kw, h / kv_mul, m->hd, scale);
+                    else
+                        or_attention_head(&s->attn[t * aw + h * m->hd], sc.data(), &s->q[t * aw + h * m->hd], kc, vc,
+                                          pos, kw, h / kv_mul, m->hd, scale);
+                }
             });
         }
         quantize_rows(s->attn.data(), N, aw, s->xq.data(), s->xs.data());
@@ -541,6 +547,7 @@ or_session* or_session_create(or_model* m, int64_t max_ctx, int64_t max_batch) {
 }
 
 void or_session_free(or_session* s) { delete s; }
+void or_session_set_attention(or_session* s, int order) { s->attn_order = order == 1 ? 1 : 0; }
 
 void or_model_set_threads(or_model* m, int nthreads) { m->nthreads = nthreads > 0 ? nthreads : 1; }
 

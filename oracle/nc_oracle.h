@@ -99,6 +99,13 @@ void or_attention_head(float* out_head, float* scores, const float* q_head,
                        const float* k_cache, const float* v_cache, int64_t pos,
                        int64_t kv_width, int64_t kv_h, int64_t head_dim, float scale);
 
+/* Split-order attention head (the device's NC_ATTN_SPLIT; no reference counterpart): 64-position
+ * chunks with per-chunk max / sum of exp / exp-weighted V, combined in chunk order; v past plast
+ * (the pass's last position) read as 0.  out_head is overwritten. */
+void or_attention_head_split(float* out_head, const float* q_head, const float* k_cache, const float* v_cache,
+                             int64_t pos, int64_t plast, int64_t kv_width, int64_t kv_h, int64_t head_dim,
+                             float scale);
+
 /* ---------------- Philox4x32-10 (Salmon et al., SC'11) ---------------- */
 void or_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 
@@ -124,6 +131,9 @@ int64_t or_model_head_q4_0(const or_model* m, uint8_t* out, int64_t cap);
 void or_model_set_threads(or_model* m, int nthreads);
 
 or_session* or_session_create(or_model* m, int64_t max_ctx, int64_t max_batch);
+/* Attention order of the session's passes: 0 the reference's (default), 1 the split order of
+ * or_attention_head_split (the checker of the device's NC_ATTN_SPLIT). */
+void or_session_set_attention(or_session* s, int order);
 /* CPU-baseline timing aid (no reference counterpart): fills KV rows [0, n) of every layer with
  * deterministic pseudo-random values so that a pass at start_pos = n costs what it costs after
  * an n-token prefill.  The session's outputs are then timing data, not parity data. */

@@ -662,6 +662,67 @@ void or_attention_head(float* out_head, float* scores, const float* q_head,
     }
 }
 
+// Split-order attention head: the device's NC_ATTN_SPLIT order (no reference counterpart; the
+// reference's order is or_attention_head above, which this equals up to f32 rounding).
+// Positions 0..pos in chunks of 64; per chunk c, lanes j = p - 64c:
+//   s_p = fmaf-chain dot(q, k_p) in dim order from 0, times scale;  m_c = max of the live s_p;
+//   e_p = expf(s_p - m_c) (0 past pos);  l_c = the xor-butterfly sum of the 64 lanes' e
+//   (offsets 32, 16, ..., 1);  o_c[i] = fmaf chain over the chunk's 64 positions in order of
+//   e_p * v_p[i], v taken as 0 past plast (the pass's last position);
+// then, in chunk order: M = max m_c, w_c = expf(m_c - M), l = fmaf(w_c, l_c, l),
+// o[i] = fmaf(w_c, o_c[i], o[i]), out[i] = o[i] / l.  out_head is overwritten.
+void or_attention_head_split(float* out_head, const float* q_head, const float* k_cache, const float* v_cache,
+                             int64_t pos, int64_t plast, int64_t kv_width, int64_t kv_h, int64_t head_dim,
+                             float scale) {
+    const int64_t C = 64, nch = pos / C + 1;
+    std::vector<float> mc(nch), lc(nch), oc((size_t)nch * head_dim);
+    for (int64_t c = 0; c < nch; c++) {
+        float sv[64], e[64];
+        float m = -INFINITY;
+        for (int64_t j = 0; j < C; j++) {
+            const int64_t p = c * C + j;
+            sv[j] = -INFINITY;
+            if (p > pos) continue;
+            const float* k = k_cache + p * kv_width + kv_h * head_dim;
+            float dot = 0.0f;
+            for (int64_t i = 0; i < head_dim; i++) dot = fmaf(q_head[i], k[i], dot);
+            sv[j] = dot * scale;
+            m = sv[j] > m ? sv[j] : m;
+        }
+        for (int64_t j = 0; j < C; j++) e[j] = c * C + j <= pos ? expf(sv[j] - m) : 0.0f;
+        float b[64], nb[64];
+        std::memcpy(b, e, sizeof b);
+        for (int off = 32; off >= 1; off >>= 1) {
+            for (int i = 0; i < 64; i++) nb[i] = b[i] + b[i ^ off];
+            std::memcpy(b, nb, sizeof b);
+        }
+        mc[c] = m;
+        lc[c] = b[0];
+        for (int64_t i = 0; i < head_dim; i++) {
+            float o = 0.0f;
+            for (int64_t j = 0; j < C; j++) {
+                const int64_t p = c * C + j;
+                const float v = p <= plast ? v_cache[p * kv_width + kv_h * head_dim + i] : 0.0f;
+                o = fmaf(e[j], v, o);
+            }
+            oc[(size_t)c * head_dim + i] = o;
+        }
+    }
+    float M = mc[0];
+    for (int64_t c = 1; c < nch; c++) M = mc[c] > M ? mc[c] : M;
+    std::vector<float> w(nch);
+    float l = 0.0f;
+    for (int64_t c = 0; c < nch; c++) {
+        w[c] = expf(mc[c] - M);
+        l = fmaf(w[c], lc[c], l);
+    }
+    for (int64_t i = 0; i < head_dim; i++) {
+        float o = 0.0f;
+        for (int64_t c = 0; c < nch; c++) o = fmaf(w[c], oc[(size_t)c * head_dim + i], o);
+        out_head[i] = o / l;
+    }
+}
+
 // Philox4x32-10, Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as
 // 1, 2, 3", SC'11: round multipliers 0xD2511F53 / 0xCD9E8D57, Weyl key increments
 // 0x9E3779B9 / 0xBB67AE85, ten rounds.

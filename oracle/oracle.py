@@ -69,6 +69,7 @@ def lib():
                                                       C.POINTER(C.c_uint64), _u32p, _i64, _i64, _u32p, _i64p,
                                                       _i64p]),
         "or_attention_head": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, C.c_float]),
+        "or_attention_head_split": (None, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64, C.c_float]),
         "or_philox4x32_10": (None, [_u32p, _u32p, _u32p]),
         "or_model_load": (C.c_void_p, [C.c_char_p, C.c_int, C.c_char_p, C.c_int]),
         "or_model_load_memory": (C.c_void_p, [C.c_void_p, C.c_size_t, C.c_int, C.c_char_p, C.c_int]),
@@ -80,6 +81,7 @@ def lib():
         "or_model_set_threads": (None, [C.c_void_p, C.c_int]),
         "or_session_fill_kv": (None, [C.c_void_p, _i64, C.c_uint64]),
         "or_session_free": (None, [C.c_void_p]),
+        "or_session_set_attention": (None, [C.c_void_p, C.c_int]),
         "or_prefill_pass_batch": (None, [C.c_void_p, _u32p, _i64, _i64]),
         "or_forward_pass": (None, [C.c_void_p, C.c_uint32, _i64]),
         "or_batch_row_logits": (None, [C.c_void_p, _i64, _f32p]),
@@ -283,6 +285,14 @@ def attention_head(q_head, k_cache, v_cache, pos, kv_width, kv_h, head_dim, scal
     return out
 
 
+def attention_head_split(q_head, k_cache, v_cache, pos, plast, kv_width, kv_h, head_dim, scale):
+    """The device's split-order attention head (64-position chunks combined in order)."""
+    out = np.zeros(head_dim, np.float32)
+    lib().or_attention_head_split(out, _c(q_head, np.float32), _c(k_cache, np.float32).ravel(),
+                                  _c(v_cache, np.float32).ravel(), pos, plast, kv_width, kv_h, head_dim, scale)
+    return out
+
+
 def philox4x32_10(ctr, key):
     out = np.zeros(4, np.uint32)
     lib().or_philox4x32_10(_c(ctr, np.uint32), _c(key, np.uint32), out)
@@ -391,6 +401,10 @@ class Session:
     def forward_pass(self, tok, pos):
         lib().or_forward_pass(self.h, int(tok), pos)
         return np.ctypeslib.as_array(lib().or_session_logits(self.h), (self.V,)).copy()
+
+    def set_attention(self, order):
+        """0: the reference's attention order (default); 1: the device's split order."""
+        lib().or_session_set_attention(self.h, int(order))
 
     def fill_kv(self, n, seed=1):
         """Timing aid: pseudo-random KV rows [0, n) in every layer (no parity meaning)."""
