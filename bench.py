@@ -385,6 +385,7 @@ def run_config3(args):
         "data": "synthetic (random-init weights N(0,0.02) -> Q4_K / Q4_0, seeded uniform prompt)",
         "config": {"workload": f"llama-3.2-3b-q4k target + llama-3.2-1b draft, stochastic speculative sampling k={args.k} "
                                f"T=1.0, {n_prompt}-token prompt, {int(tok)} new tokens, 4096-position KV",
+                   "gemm_kernel": GEMM_KERNEL, "attention": ATTENTION,
                    "k": args.k, "temperature": temp, "prompt_tokens": n_prompt, "tokens_emitted": int(tok),
                    "drafted": int(st.drafted), "accepted": int(st.accepted),
                    "target_verify_weight_bytes": int(tm.config["verify_weight_bytes"]),
@@ -461,6 +462,7 @@ def run_config4(args):
         "dtype": "int8 dot -> int32, f32 accumulate",
         "data": "synthetic (random-init weights N(0,0.02) -> Q4_0, seeded uniform 8192-token prompt)",
         "config": {"workload": "llama-3-70b-shape Q4_0 single k+1 verify (k=8) over an 8192-position KV cache",
+                   "gemm_kernel": GEMM_KERNEL, "attention": ATTENTION,
                    "rows": n, "kv_positions": n_prompt, "verify_weight_bytes": int(cfg["verify_weight_bytes"]),
                    "kv_bytes_read": int(kv_bytes), "greedy_drafts_all_accepted": consistent,
                    "prefill_8192_tokens_s": round(prefill_s, 2)},
@@ -641,6 +643,7 @@ def main():
                                f" (the config's full {args.n_new}-token decode at every k, alpha: full_decode)",
                    "timed_positions": [args.n_prompt, args.n_prompt + emitted_by_steps],
                    "full_decode": full,
+                   "gemm_kernel": GEMM_KERNEL, "attention": ATTENTION,
                    "k": args.k, "alpha": args.alpha, "prompt_tokens": args.n_prompt,
                    "tokens_emitted": int(emitted_by_steps), "drafted": int(st.drafted),
                    "accepted": int(st.accepted), "stream_equals_greedy": parity,

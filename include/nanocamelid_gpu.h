@@ -76,11 +76,13 @@ int nc_ctx_set_gemm_kernel(nc_ctx* ctx, int kernel);
  * weighted-V loops of the reference's attention (src/inference.rs:3522-3540, :3603-3623).
  * SEQUENTIAL (the default): the reference's left-to-right sums, bit-identical.  SPLIT: each
  * row's positions in 64-position chunks, per chunk a max, a sum of exp and an exp-weighted V
- * sum, the chunks combined in a fixed order; f32 outputs equal the sequential ones up to
- * rounding (the verify path's 1e-3 relative bound for f32 outputs), and a row's result does
- * not depend on the batch it is in, so speculative and plain decoding emit one stream.  Keys
- * and values are read once per KV head and chunk for all heads and rows of a pass.  Prompt
- * passes (nc_prefill) keep the sequential order.  Set it between calls. */
+ * sum, the chunks combined in a fixed order.  Attention outputs equal the sequential ones up
+ * to f32 rounding; the Q8_0 quantisation that follows can turn such a difference into one
+ * quantisation step, so logits are not bit-identical to the reference's and a greedy stream
+ * can leave the reference's where its top-2 margin is that small.  A row's result does not
+ * depend on the batch it is in, so speculative and plain decoding emit one stream.  Keys and
+ * values are read once per KV head and chunk for all heads and rows of a pass.  Prompt passes
+ * (nc_prefill) keep the sequential order.  Set it between calls. */
 #define NC_ATTN_SEQUENTIAL 0
 #define NC_ATTN_SPLIT 1
 int nc_ctx_set_attention(nc_ctx* ctx, int order);
