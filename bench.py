@@ -558,6 +558,16 @@ def main():
     greedy, gst = sess.generate_greedy(prompt, n_rec)
     log(f"greedy record: {n_rec} tokens in {gst.decode_seconds:.2f}s ({n_rec / gst.decode_seconds:.1f} tok/s plain "
         f"greedy), prefill {gst.prefill_seconds:.2f}s")
+    ref_order = None
+    if ATTENTION != "sequential":
+        # the same greedy continuation in the reference's attention order: where does the
+        # split order's stream first leave it
+        ctx.set_attention(ATTENTION_ORDERS["sequential"])
+        rgreedy, _ = nc.Session(model, max_ctx, 16).generate_greedy(prompt, n_rec)
+        ctx.set_attention(ATTENTION_ORDERS[ATTENTION])
+        div = next((i for i in range(n_rec) if int(rgreedy[i]) != int(greedy[i])), None)
+        ref_order = {"tokens": n_rec, "identical": div is None, "first_divergence": div}
+        log(f"greedy stream against the reference attention order: {ref_order}")
 
     # warmup steps (untimed), then exactly K timed steps
     sess.generate_speculative_oracle(prompt, n_rec, args.k, args.alpha, args.seed, greedy, max_steps=args.warmup)
@@ -647,6 +657,7 @@ def main():
                    "k": args.k, "alpha": args.alpha, "prompt_tokens": args.n_prompt,
                    "tokens_emitted": int(emitted_by_steps), "drafted": int(st.drafted),
                    "accepted": int(st.accepted), "stream_equals_greedy": parity,
+                   "greedy_vs_reference_attention_order": ref_order,
                    "verify_weight_bytes": int(cfg["verify_weight_bytes"]),
                    "kv_bytes_read_per_step": int(kv_step),
                    "whole_pass_GBps": round(whole_gbs, 1)},

@@ -660,7 +660,7 @@ constexpr int kSplitChunk = 64;
 // Workgroup of 4 waves over CPW consecutive chunks of one KV head and WGQ = QG * 4 / CPW
 // queries: wave w takes chunk CPW * blockIdx.z + w % CPW and queries (w / CPW) * QG .. + QG - 1
 // of the group.  CPW = 4: every key and value of a chunk is read once per workgroup (long rows);
-// CPW = 1: four waves share one chunk (short rows, where chunks are few).  Query j of group z is
+// CPW = 1 or 2: four or two waves share a chunk, when the queries fill more than one group.  Query j of group z is
 // qi = z * WGQ + j = g * N + n (head kvh * G + g, row n).  Score phase: lane = position of the
 // chunk.  Value phase: lane = output dims lane (and lane + 64 at HD = 128).
 template <int HD, int QG, int CPW>
@@ -696,7 +696,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams a) {
     float dot[QG];
 #pragma unroll
     for (int k = 0; k < QG; k++) dot[k] = 0.0f;
-    constexpr int KB = 4;  // dim quads per batch of loads
+    constexpr int KB = QG <= 8 ? 8 : 4;  // dim quads per batch of loads (registers allowing)
 #pragma unroll 1
     for (int h0 = 0; h0 < NQ; h0 += KB) {
         f4v kv[KB];
@@ -750,7 +750,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnParams a) {
     for (int k = 0; k < QG; k++)
 #pragma unroll
         for (int dl = 0; dl < DL; dl++) o[k][dl] = 0.0f;
-    constexpr int PB = 2;  // position quads per batch of loads
+    constexpr int PB = QG <= 4 ? 8 : (QG <= 8 ? 4 : 2);  // position quads per batch of loads
 #pragma unroll 1
     for (int b0 = 0; b0 < C / 4; b0 += PB) {
         f4v vv[PB][DL];
@@ -831,7 +831,7 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams a) {
     __syncthreads();
     const float* po = a.part_o + u0 * HD + t;
     float l = 0.0f, o = 0.0f;
-    constexpr int B = 8;
+    constexpr int B = 32;  // partial outputs in flight
     for (int c0 = 0; c0 < nc; c0 += B) {
         float v[B];
 #pragma unroll
@@ -855,14 +855,21 @@ static int launch_attention_split(const AttnParams& a, hipStream_t st) {
     const int G = a.H / a.Hkv, GN = G * a.N;
     const int nch = a.max_pos / kSplitChunk + 1;
     if (nch > a.nchunks) return fail(NC_ERANGE, "attention: row longer than the split partials hold");
-    // Queries per wave (4..16, a multiple of 4): as many as still give ~1024 chunk waves (one
-    // per SIMD), since every query group re-reads the chunk's keys and values; at most 16
-    // (registers).  Rows with too few chunks for that put four waves on one chunk (CPW = 1).
-    const int want = (1024 + a.Hkv * nch - 1) / (a.Hkv * nch);
-    const int ngroups = std::max((GN + 15) / 16, std::min((GN + 3) / 4, want));
-    const int qg = ((GN + ngroups - 1) / ngroups + 3) / 4 * 4;
-    const bool wide = a.Hkv * nch * ((GN + qg - 1) / qg) >= 1024;
-    const int cpw = wide ? 4 : 1, wgq = qg * 4 / cpw;
+    // Queries per wave QG (4, 8, 12 or 16): the largest that still gives ~1024 chunk waves (one
+    // per SIMD), since every query group re-reads the chunk's keys and values; 16 at most
+    // (registers).  Chunks per workgroup CPW: with chunk waves to spare (long rows, config 4:
+    // 24.2 against 28.9 ms per pass) each wave takes its own chunk; otherwise query groups that
+    // share a chunk share a workgroup, its waves reading the chunk through one CU's cache
+    // (config 2: 1466 tok/s, config 3: 291 tok/s).
+    auto waves = [&](int q) { return a.Hkv * nch * ((GN + q - 1) / q); };
+    int qg = 4;
+    for (int q : {16, 12, 8})
+        if (waves(q) >= 1024) {
+            qg = q;
+            break;
+        }
+    const int subsets = (GN + qg - 1) / qg;
+    const int cpw = subsets == 1 || waves(qg) >= 2048 ? 4 : (subsets >= 4 ? 1 : 2), wgq = qg * 4 / cpw;
     const dim3 grid(a.Hkv, (GN + wgq - 1) / wgq, (nch + cpw - 1) / cpw);
 #define NC_SPLIT_QG(HD, CPW)                                                                               \
     switch (qg) {                                                                                          \
@@ -872,8 +879,10 @@ static int launch_attention_split(const AttnParams& a, hipStream_t st) {
         default: hipLaunchKernelGGL((attn_split_kernel<HD, 16, CPW>), grid, dim3(256), 0, st, a); break;  \
     }
 #define NC_SPLIT(HD)                                                                            \
-    if (wide) {                                                                                 \
+    if (cpw == 4) {                                                                             \
         NC_SPLIT_QG(HD, 4)                                                                      \
+    } else if (cpw == 2) {                                                                      \
+        NC_SPLIT_QG(HD, 2)                                                                      \
     } else {                                                                                    \
         NC_SPLIT_QG(HD, 1)                                                                      \
     }                                                                                           \
