@@ -864,7 +864,7 @@ static int launch_attention_split(const AttnParams& a, hipStream_t st) {
     auto waves = [&](int q) { return a.Hkv * nch * ((GN + q - 1) / q); };
     int qg = 4;
     for (int q : {16, 12, 8})
-        if (waves(q) >= 1024) {
+        if (q <= (GN + 3) / 4 * 4 && waves(q) >= 1024) {  // no more slots than queries
             qg = q;
             break;
         }

@@ -140,3 +140,26 @@ def test_split_streams_equal_oracle(sctx):
     d_out, st = nc.generate_speculative_draft(nc.Session(gm, 400, 16), nc.Session(dm, 400, 8), prompt, 96, 4)
     assert np.array_equal(d_out, ref)
     assert 0 < st.accepted < st.drafted
+
+
+@pytest.mark.parametrize("ctx_len", [2000, 8192])
+def test_split_many_queries_long_rows_batch_independent(sctx, ctx_len):
+    """Many query vectors per KV head (4 heads x 9 rows) over long rows: the launch takes 16
+    queries per wave (and one chunk per wave at 8192 positions), the shapes of the 70B
+    verify; every 9-row verify row equals a single-token pass at its position, bit for bit
+    (those take 4 queries per wave)."""
+    import nanocamelid_amd as nc
+    spec = dict(layers=1, embedding_length=32 * 64, head_count=32, head_count_kv=8, feed_forward_length=512,
+                vocab_size=1000, context_length=ctx_len + 64, tied=1, norm_mode=1)
+    gm = nc.Model(sctx, data=nc.synth_gguf(**spec, seed=ctx_len))
+    prompt = nc.uniform_prompt(ctx_len, ctx_len, 1000)
+    batch = nc.uniform_prompt(ctx_len + 1, 9, 1000)
+    a, b = nc.Session(gm, ctx_len + 16, 16), nc.Session(gm, ctx_len + 16, 16)
+    print(f"split many queries: prefill {ctx_len}, verify 9 rows", flush=True)
+    a.prefill_pass_batch(prompt, 0)
+    b.prefill_pass_batch(prompt, 0)
+    a.verify_greedy(batch, ctx_len)
+    rows = [np.array(a.logits(i), np.float32) for i in range(9)]
+    for i in range(9):
+        _, lg = b.forward_pass(int(batch[i]), ctx_len + i)
+        assert _same(lg, rows[i]), (ctx_len, i)
