@@ -812,6 +812,11 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams a) {
     const int nc = (a.d_pos[0] + n) / kSplitChunk + 1;  // chunks holding positions 0..pos
     const size_t u0 = ((size_t)n * a.H + h) * a.nchunks;
     const float* ml = a.part_ml + 2 * u0;
+    const float* po = a.part_o + u0 * HD + t;
+    constexpr int B = 32;  // partial outputs in flight
+    float v[B];            // the first batch is loaded before the max and the weights
+#pragma unroll
+    for (int j = 0; j < B; j++) v[j] = po[(size_t)min(j, nc - 1) * HD];
     float M = -__builtin_inff();
     for (int c = t; c < nc; c += HD) M = ml[2 * c] > M ? ml[2 * c] : M;
 #pragma unroll
@@ -829,13 +834,12 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams a) {
         wl[1][c] = ml[2 * c + 1];
     }
     __syncthreads();
-    const float* po = a.part_o + u0 * HD + t;
     float l = 0.0f, o = 0.0f;
-    constexpr int B = 32;  // partial outputs in flight
     for (int c0 = 0; c0 < nc; c0 += B) {
-        float v[B];
+        if (c0 > 0) {
 #pragma unroll
-        for (int j = 0; j < B; j++) v[j] = po[(size_t)min(c0 + j, nc - 1) * HD];
+            for (int j = 0; j < B; j++) v[j] = po[(size_t)min(c0 + j, nc - 1) * HD];
+        }
 #pragma unroll
         for (int j = 0; j < B; j++) {
             if (c0 + j < nc) {  // uniform
