@@ -13,6 +13,9 @@ weights and KV resident in HBM).  Also reported:
   roofline     : the quantized GEMM family (all verify matmuls), algorithmic bytes per
                  launch over its average launch time measured with HIP events on the
                  session stream (a separate pass over the same workload);
+  config.opt_in_split_attention : the same timed steps with the opt-in split-position attention
+                 (nc_ctx_set_attention; not the reference's arithmetic, so not the headline) and
+                 where its greedy stream first leaves the reference order's;
   cpu_baseline : the CPU oracle (C++ restatement of the reference's portable x86 path) on the
                  host's cores: verify steps of the same model at the workload's positions, on
                  min(16, nproc) threads and on the reference's default 4, plus a GPU-vs-CPU
@@ -508,6 +511,8 @@ def main():
                     help="dot-product path of the Q4_0 16-row matmuls (nc_ctx_set_gemm_kernel)")
     ap.add_argument("--attention", choices=sorted(ATTENTION_ORDERS), default="sequential",
                     help="summation order of the verify passes' attention (nc_ctx_set_attention)")
+    ap.add_argument("--no-split-report", action="store_true",
+                    help="skip the extra run of the opt-in split-position attention")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy (known HBM bytes) to scale rocprofv3 --pmc byte counters")
     args = ap.parse_args()
@@ -606,6 +611,25 @@ def main():
                     "positions": f"{args.n_prompt}..{args.n_prompt + ftok}",
                     "stream_equals_greedy": bool(np.array_equal(o, greedy[:len(o)]))}
                 log(f"full decode k={k} alpha={alpha}: {full[f'k{k}_alpha{alpha}']}")
+    # the opt-in split-position attention on the same model and drafter (not the headline: its
+    # arithmetic is not the reference's); where its greedy stream leaves the reference order's
+    split = None
+    if ATTENTION == "sequential" and not args.no_split_report:
+        ctx.set_attention(ATTENTION_ORDERS["split"])
+        ss = nc.Session(model, max_ctx, 16)
+        sgreedy, _ = ss.generate_greedy(prompt, n_rec)
+        ss.generate_speculative_oracle(prompt, n_rec, args.k, args.alpha, args.seed, sgreedy, max_steps=args.warmup)
+        torch.cuda.synchronize()
+        so, sst = ss.generate_speculative_oracle(prompt, n_rec, args.k, args.alpha, args.seed, sgreedy,
+                                                 max_steps=args.steps)
+        ss.close()
+        ctx.set_attention(ATTENTION_ORDERS["sequential"])
+        stok = sst.emitted - 1  # as the headline: the first token comes from the prefill pass
+        div = next((i for i in range(n_rec) if int(sgreedy[i]) != int(greedy[i])), None)
+        split = {"tok_s": round(stok / sst.decode_seconds, 2), "steps": int(sst.steps), "tokens": int(stok),
+                 "stream_equals_its_greedy": bool(np.array_equal(so, sgreedy[:len(so)])),
+                 "greedy_first_divergence_from_reference_order": div}
+        log(f"split attention (opt-in): {split}")
     # GPU greedy continuation of a 16-token prompt, for the CPU stream comparison
     stream_prompt = prompt[:16]
     s16 = nc.Session(model, 64, 16)
@@ -658,6 +682,7 @@ def main():
                    "tokens_emitted": int(emitted_by_steps), "drafted": int(st.drafted),
                    "accepted": int(st.accepted), "stream_equals_greedy": parity,
                    "greedy_vs_reference_attention_order": ref_order,
+                   "opt_in_split_attention": split,
                    "verify_weight_bytes": int(cfg["verify_weight_bytes"]),
                    "kv_bytes_read_per_step": int(kv_step),
                    "whole_pass_GBps": round(whole_gbs, 1)},
