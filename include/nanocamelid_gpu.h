@@ -183,7 +183,9 @@ typedef struct nc_model_config {
     int64_t context_length, embedding_length, block_count, feed_forward_length;
     int64_t head_count, head_count_kv, head_dim, rope_dimension_count, vocab_size;
     int64_t attention_output_width, kv_width;
-    int32_t weight_type;  /* NC_TYPE_Q4_0 or NC_TYPE_Q4_K */
+    int32_t weight_type;  /* GGUF type of blk.0.attn_q.weight: NC_TYPE_Q4_0, NC_TYPE_Q4_K or NC_TYPE_Q6_K.
+                           Files that mix types (llama.cpp Q4_K_M) keep each matrix's own type; this
+                           field names the first layer's attention-query type only. */
     int32_t tied_head;    /* 1 when the head was requantised from token_embd */
     float rope_freq_base, rms_norm_epsilon;
     int64_t device_weight_bytes; /* repacked matrices incl. head */

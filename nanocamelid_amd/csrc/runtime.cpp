@@ -593,7 +593,12 @@ static int read_config(const GgufFile& g, nc_model_config& c) {
         return fail(NC_EINVAL, "model widths must be multiples of 64 (attention), 32 (ffn), 256 (embedding)");
     if (c.head_dim != 64 && c.head_dim != 128) return fail(NC_EINVAL, "head_dim must be 64 or 128");
     if (c.head_count / c.head_count_kv > 8) return fail(NC_EINVAL, "at most 8 query heads per KV head");
-    return validate_model_tensors(g, c);
+    if (const int rc = validate_model_tensors(g, c)) return rc;
+    // the first layer's attention-query type; each matrix keeps its own type when a file
+    // mixes them (llama.cpp Q4_K_M), so this does not describe the other matrices
+    const GgufTensor* tq = g.find("blk.0.attn_q.weight");
+    c.weight_type = tq ? (int32_t)tq->type : -1;
+    return NC_OK;
 }
 
 static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_load_opts* opts, nc_model** out) {
@@ -632,7 +637,6 @@ static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_lo
     emb.clear();
     emb.shrink_to_fit();
     m->layers.resize(c.block_count);
-    int wtype = -1;
     for (int64_t i = 0; i < c.block_count; i++) {
         LayerDev& L = m->layers[i];
         const std::string b = "blk." + std::to_string(i) + ".";
@@ -676,9 +680,7 @@ static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_lo
             if ((rc = one(tg, F, d, L.gate)) || (rc = one(tu, F, d, L.up))) return rc;
         }
         if ((rc = one(tdn, d, F, L.down))) return rc;
-        wtype = ty;
     }
-    c.weight_type = wtype;
     int64_t devb = m->head.dev_bytes, algo = m->head.algo_bytes;
     for (auto& L : m->layers)
         for (auto* q : L.all()) {

@@ -219,3 +219,15 @@ def test_embedding_types_pass_validation(base, ty):
     raw = random_blocks(ty, 256 * 300 // REF_LAYOUT[ty][0], seed=ty).tobytes()
     img = _edit(base, replace={"token_embd.weight": ("token_embd.weight", [256, 300], ty, raw)})
     assert nc.gguf_read_config(img)["vocab_size"] == 300
+
+
+def test_weight_type_names_the_first_attention_query_matrix():
+    # weight_type reports blk.0.attn_q.weight's type; a file that mixes types per matrix (the
+    # Q4_K_M recipe's Q6_K attn_v / ffn_down) keeps it, whatever the other matrices are
+    img = nc.synth_gguf(**SPEC, seed=3)
+    assert nc.gguf_read_config(bytes(img))["weight_type"] == nc.NC_TYPE_Q4_0
+    mixed = GW.with_types(img, {"blk.0.attn_v.weight": nc.NC_TYPE_Q6_K, "blk.1.ffn_down.weight": nc.NC_TYPE_Q6_K,
+                             "blk.1.attn_q.weight": nc.NC_TYPE_Q6_K})
+    assert nc.gguf_read_config(mixed)["weight_type"] == nc.NC_TYPE_Q4_0
+    first_q6 = GW.with_types(img, {"blk.0.attn_q.weight": nc.NC_TYPE_Q6_K})
+    assert nc.gguf_read_config(first_q6)["weight_type"] == nc.NC_TYPE_Q6_K
