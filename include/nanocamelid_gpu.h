@@ -434,6 +434,16 @@ int nc_uniform_prompt(uint64_t seed, int64_t n, uint32_t vocab, uint32_t* ids);
 uint32_t nc_oracle_draft(uint64_t seed, int64_t p, float alpha, const uint32_t* greedy, int64_t n_prompt,
                          int64_t n_greedy, uint32_t vocab);
 
+/* Benchmark and test helpers for BASELINE config 4's "KV cache filled with N(0, 1) keys and
+ * values" (no reference counterpart).  nc_synth_kv_values (host only): N(0, 1) values, Philox4x32-10
+ * with counter (pair index, stream 2 * layer + kind, purpose 10) and key seed, Box-Muller in
+ * double, rounded to f32; elements [start, start + count) of the stream (start, count even) into
+ * out.  kind 0 = keys, 1 = values.  nc_session_fill_kv: rows [0, n) of every layer's key and
+ * value cache from those streams, element i of row p being element p * kv_width + i; a pass at
+ * start_pos = n then attends over n positions of N(0, 1) keys and values.  Synchronous. */
+int nc_synth_kv_values(uint64_t seed, int32_t layer, int32_t kind, int64_t start, int64_t count, float* out);
+int nc_session_fill_kv(nc_session* s, int64_t n, uint64_t seed);
+
 /* ---------------------------------------------------------------- timing hooks */
 /* Average device time (ms) per launch of the named kernel family recorded with HIP
  * events on the session stream since the last reset; used by the benchmark's

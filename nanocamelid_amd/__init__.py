@@ -310,6 +310,11 @@ class Session:
                                          float(temp), seed, C.byref(r)))
         return r.n_accepted, r.next_token, r.new_pos
 
+    def fill_kv(self, n: int, seed: int):
+        """Benchmark/test helper: N(0, 1) keys and values in KV rows [0, n) of every layer
+        (synth_kv_values streams), so a pass at start_pos = n attends over n such positions."""
+        check(lib().nc_session_fill_kv(self.h, n, seed))
+
     def logits(self, row: int) -> np.ndarray:
         out = np.empty(self.vocab, np.float32)
         check(lib().nc_session_logits(self.h, row, out.ctypes.data_as(C.POINTER(C.c_float))))
@@ -464,6 +469,14 @@ def synth_gguf(layers, embedding_length, head_count, head_count_kv, feed_forward
     buf = np.empty(size.value, np.uint8)
     check(lib().nc_synth_write(C.byref(s), buf.ctypes.data, size.value, nthreads))
     return buf
+
+
+def synth_kv_values(seed: int, layer: int, kind: int, start: int, count: int) -> np.ndarray:
+    """Host-only: elements [start, start + count) of the N(0, 1) stream of layer `layer`'s keys
+    (kind 0) or values (kind 1) that Session.fill_kv writes (element p * kv_width + i = row p, i)."""
+    out = np.empty(count, np.float32)
+    check(lib().nc_synth_kv_values(seed, layer, kind, start, count, out.ctypes.data_as(C.POINTER(C.c_float))))
+    return out
 
 
 def uniform_prompt(seed: int, n: int, vocab: int) -> np.ndarray:

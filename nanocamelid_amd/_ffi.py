@@ -120,6 +120,8 @@ SIGNATURES = {
     "nc_generate_speculative_ngram": (C.c_int, [_vp, _u32p, _i32, _i32, _i32, _i32, _i32, _u32p, _i32, _u32p, _vp]),
     "nc_generate_speculative_ngram_temp": (C.c_int, [_vp, _u32p, _i32, _i32, _i32, _i32, _i32, C.c_float,
                                                      C.POINTER(C.c_uint64), _u32p, _i32, _u32p, _vp]),
+    "nc_synth_kv_values": (C.c_int, [C.c_uint64, _i32, _i32, _i64, _i64, _f32p]),
+    "nc_session_fill_kv": (C.c_int, [_vp, _i64, C.c_uint64]),
     "nc_session_kernel_timing": (_i64, [_vp, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
     "nc_session_timing_enable": (C.c_int, [_vp, _i32]),
 }

@@ -580,6 +580,16 @@ void quant_q4_k_block(const float* x, uint8_t* out) {
 
 }  // namespace
 
+void synth_normal_values(uint64_t seed, uint32_t tid, uint64_t start, uint64_t count, uint32_t purpose, float* out) {
+    // elements [start, start + count) of stream tid (start and count even): (float) z
+    for (uint64_t e = 0; e < count; e += 2) {
+        double z0, z1;
+        normal_pair(seed, tid, (start + e) / 2, purpose, &z0, &z1);
+        out[e] = (float)z0;
+        out[e + 1] = (float)z1;
+    }
+}
+
 int synth_size(const nc_synth_spec& s, uint64_t* size) {
     auto ts = synth_tensors(s);
     uint64_t start;

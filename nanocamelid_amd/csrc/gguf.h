@@ -66,6 +66,11 @@ float philox_uniform(uint64_t seed, uint64_t ctr, uint32_t purpose);
 constexpr uint32_t kPurposeDraft = 1, kPurposeAccept = 2, kPurposeResample = 3, kPurposePrompt = 4;
 constexpr uint32_t kPurposeOracleU = 5, kPurposeOracleId = 6, kPurposeBonus = 7;
 
+// N(0, 1) values (Philox4x32-10 counter (pair index, stream tid, purpose), Box-Muller in double,
+// rounded to f32) of elements [start, start + count) of stream tid; start and count even.
+constexpr uint32_t kPurposeKvFill = 10;
+void synth_normal_values(uint64_t seed, uint32_t tid, uint64_t start, uint64_t count, uint32_t purpose, float* out);
+
 int synth_size(const nc_synth_spec& s, uint64_t* size);
 int synth_write(const nc_synth_spec& s, uint8_t* dst, uint64_t size, int nthreads);
 

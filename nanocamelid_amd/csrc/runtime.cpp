@@ -2278,6 +2278,65 @@ uint32_t nc_oracle_draft(uint64_t seed, int64_t p, float alpha, const uint32_t* 
     return philox_word(seed, (uint64_t)p, kPurposeOracleId) % vocab;
 }
 
+int nc_synth_kv_values(uint64_t seed, int32_t layer, int32_t kind, int64_t start, int64_t count, float* out) {
+    if (!out || layer < 0 || (kind != 0 && kind != 1) || start < 0 || count < 0 || (start | count) & 1)
+        return fail(NC_EINVAL, "nc_synth_kv_values: bad arguments");
+    synth_normal_values(seed, (uint32_t)(2 * layer + kind), (uint64_t)start, (uint64_t)count, kPurposeKvFill, out);
+    return NC_OK;
+}
+
+// Keys and values of rows [0, n) of every layer from nc_synth_kv_values: element i of row p of
+// layer l's keys (kind 0) or values (kind 1) is stream 2l + kind, element p * kv_width + i.
+// Layers are drawn on host threads and copied into the device layouts (keys in dim quads
+// [Hkv][hd/4][ctx][4], values in position quads [Hkv][ctx/4][hd][4]); the rest of the cache keeps
+// its contents, except the positions n.. of a value quad that n cuts, which are zeroed.
+int nc_session_fill_kv(nc_session* s, int64_t n, uint64_t seed) {
+    if (!s || n < 0 || n > s->max_ctx) return fail(NC_EINVAL, "nc_session_fill_kv: n outside [0, max_ctx]");
+    if (n == 0) return NC_OK;
+    const nc_model_config& c = s->m->cfg;
+    const int64_t L = c.block_count, Hkv = c.head_count_kv, hd = c.head_dim, kw = c.kv_width;
+    const int64_t stride = s->ctx_stride, layer_kv = Hkv * hd * stride, nq = (n + 3) / 4;
+    NC_HIP(hipStreamSynchronize(s->stream));
+    const int nth = (int)std::max<unsigned>(1, std::min<unsigned>(16, std::thread::hardware_concurrency()));
+    std::vector<std::vector<float>> kst(nth), vst(nth);
+    for (int64_t l0 = 0; l0 < L; l0 += nth) {
+        const int cnt = (int)std::min<int64_t>(nth, L - l0);
+        std::vector<std::thread> th;
+        for (int t = 0; t < cnt; t++)
+            th.emplace_back([&, t] {
+                const int64_t l = l0 + t;
+                std::vector<float> row(kw);
+                std::vector<float>& K = kst[t];
+                std::vector<float>& V = vst[t];
+                K.assign((size_t)Hkv * (hd / 4) * n * 4, 0.0f);
+                V.assign((size_t)Hkv * nq * hd * 4, 0.0f);
+                for (int64_t p = 0; p < n; p++) {
+                    synth_normal_values(seed, (uint32_t)(2 * l), (uint64_t)(p * kw), (uint64_t)kw, kPurposeKvFill,
+                                        row.data());
+                    for (int64_t i = 0; i < kw; i++) {
+                        const int64_t h = i / hd, d = i % hd;
+                        K[((size_t)(h * (hd / 4) + d / 4) * n + p) * 4 + (d & 3)] = row[i];
+                    }
+                    synth_normal_values(seed, (uint32_t)(2 * l + 1), (uint64_t)(p * kw), (uint64_t)kw, kPurposeKvFill,
+                                        row.data());
+                    for (int64_t i = 0; i < kw; i++) {
+                        const int64_t h = i / hd, d = i % hd;
+                        V[((size_t)(h * nq + p / 4) * hd + d) * 4 + (p & 3)] = row[i];
+                    }
+                }
+            });
+        for (auto& x : th) x.join();
+        for (int t = 0; t < cnt; t++) {
+            const int64_t l = l0 + t;
+            NC_HIP(hipMemcpy2D(s->kcache + l * layer_kv, (size_t)stride * 16, kst[t].data(), (size_t)n * 16,
+                               (size_t)n * 16, (size_t)Hkv * (hd / 4), hipMemcpyHostToDevice));
+            NC_HIP(hipMemcpy2D(s->vcache + l * layer_kv, (size_t)(stride / 4) * hd * 16, vst[t].data(),
+                               (size_t)nq * hd * 16, (size_t)nq * hd * 16, (size_t)Hkv, hipMemcpyHostToDevice));
+        }
+    }
+    return NC_OK;
+}
+
 int nc_session_timing_enable(nc_session* s, int32_t enable) {
     if (!s) return fail(NC_EINVAL, "null session");
     int rc = flush_timing(s);

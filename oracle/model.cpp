@@ -11,6 +11,7 @@
 #include <map>
 #include <memory>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "oracle_internal.h"
@@ -551,23 +552,44 @@ void or_session_set_attention(or_session* s, int order) { s->attn_order = order 
 
 void or_model_set_threads(or_model* m, int nthreads) { m->nthreads = nthreads > 0 ? nthreads : 1; }
 
+void or_synth_kv_values(uint64_t seed, int32_t layer, int32_t kind, int64_t start, int64_t count, float* out) {
+    // No reference counterpart: BASELINE config 4's KV cache "filled with N(0, 1) keys and
+    // values".  Pair j = element / 2 of stream 2 * layer + kind: Philox4x32-10 with counter
+    // (j low, j high, stream, purpose 10) and key (seed low, seed high); two 53-bit uniforms
+    // u1 in (0, 1] and u2 in [0, 1); Box-Muller in double, z0 = r cos(2 pi u2), z1 = r sin(2 pi u2)
+    // with r = sqrt(-2 ln u1); each rounded to f32.
+    const uint32_t stream = (uint32_t)(2 * layer + kind);
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    for (int64_t e = 0; e < count; e += 2) {
+        const uint64_t j = (uint64_t)(start + e) / 2;
+        const uint32_t ctr[4] = {(uint32_t)j, (uint32_t)(j >> 32), stream, 10u};
+        uint32_t w[4];
+        or_philox4x32_10(ctr, key, w);
+        const double u1 = ((double)(((uint64_t)(w[0] >> 5) << 26) | (w[1] >> 6)) + 1.0) / 9007199254740992.0;
+        const double u2 = (double)(((uint64_t)(w[2] >> 5) << 26) | (w[3] >> 6)) / 9007199254740992.0;
+        const double r = std::sqrt(-2.0 * std::log(u1));
+        const double a = 6.283185307179586 * u2;
+        out[e] = (float)(r * std::cos(a));
+        out[e + 1] = (float)(r * std::sin(a));
+    }
+}
+
 void or_session_fill_kv(or_session* s, int64_t n, uint64_t seed) {
-    // Timing aid only: deterministic values in [-1, 1) (xorshift64*) in KV rows [0, n) of every
-    // layer, so that a pass at start_pos = n does the attention work of a real n-token context.
-    const int64_t kw = s->m->kv_w;
-    uint64_t x = seed | 1;
-    for (int64_t l = 0; l < s->m->L; l++)
-        for (int64_t p = 0; p < n && p < s->max_ctx; p++) {
-            float* k = &s->kc[((size_t)l * s->max_ctx + p) * kw];
-            float* v = &s->vc[((size_t)l * s->max_ctx + p) * kw];
-            for (int64_t i = 0; i < 2 * kw; i++) {
-                x ^= x >> 12;
-                x ^= x << 25;
-                x ^= x >> 27;
-                const float u = (float)((x * 0x2545F4914F6CDD1Dull) >> 40) * (1.0f / 8388608.0f) - 1.0f;
-                (i < kw ? k[i] : v[i - kw]) = u;
-            }
-        }
+    // rows [0, n) of every layer: key row p = elements [p * kv_width, (p + 1) * kv_width) of
+    // stream (layer, 0), value row p the same of stream (layer, 1)
+    const int64_t kw = s->m->kv_w, L = s->m->L;
+    n = std::min(n, s->max_ctx);
+    const int nth = std::max(1, s->m->nthreads);
+    std::vector<std::thread> th;
+    for (int t = 0; t < nth; t++)
+        th.emplace_back([=] {
+            for (int64_t l = t; l < L; l += nth)
+                for (int64_t p = 0; p < n; p++) {
+                    or_synth_kv_values(seed, (int32_t)l, 0, p * kw, kw, &s->kc[((size_t)l * s->max_ctx + p) * kw]);
+                    or_synth_kv_values(seed, (int32_t)l, 1, p * kw, kw, &s->vc[((size_t)l * s->max_ctx + p) * kw]);
+                }
+        });
+    for (auto& x : th) x.join();
 }
 
 void or_prefill_pass_batch(or_session* s, const uint32_t* toks, int64_t n, int64_t start_pos) {

@@ -134,9 +134,13 @@ or_session* or_session_create(or_model* m, int64_t max_ctx, int64_t max_batch);
 /* Attention order of the session's passes: 0 the reference's (default), 1 the split order of
  * or_attention_head_split (the checker of the device's NC_ATTN_SPLIT). */
 void or_session_set_attention(or_session* s, int order);
-/* CPU-baseline timing aid (no reference counterpart): fills KV rows [0, n) of every layer with
- * deterministic pseudo-random values so that a pass at start_pos = n costs what it costs after
- * an n-token prefill.  The session's outputs are then timing data, not parity data. */
+/* N(0, 1) KV fill (no reference counterpart): or_synth_kv_values writes
+ * elements [start, start + count) (even) of the stream of layer `layer`'s keys (kind 0) or values
+ * (kind 1): Philox4x32-10, counter (pair index, 2 * layer + kind, purpose 10), key seed, Box-Muller
+ * in double, rounded to f32.  or_session_fill_kv puts row p = elements [p * kv_width, (p + 1) *
+ * kv_width) into KV rows [0, n) of every layer, so a pass at start_pos = n attends over n
+ * positions of N(0, 1) keys and values, the same ones the device's nc_session_fill_kv writes. */
+void or_synth_kv_values(uint64_t seed, int32_t layer, int32_t kind, int64_t start, int64_t count, float* out);
 void or_session_fill_kv(or_session* s, int64_t n, uint64_t seed);
 void or_session_free(or_session* s);
 /* prefill_pass_batch (inference.rs:3695-3744): writes KV for start_pos..+n and

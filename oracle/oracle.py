@@ -80,6 +80,7 @@ def lib():
         "or_session_create": (C.c_void_p, [C.c_void_p, _i64, _i64]),
         "or_model_set_threads": (None, [C.c_void_p, C.c_int]),
         "or_session_fill_kv": (None, [C.c_void_p, _i64, C.c_uint64]),
+        "or_synth_kv_values": (None, [C.c_uint64, C.c_int32, C.c_int32, _i64, _i64, _f32p]),
         "or_session_free": (None, [C.c_void_p]),
         "or_session_set_attention": (None, [C.c_void_p, C.c_int]),
         "or_prefill_pass_batch": (None, [C.c_void_p, _u32p, _i64, _i64]),
@@ -299,6 +300,12 @@ def philox4x32_10(ctr, key):
     return out
 
 
+def synth_kv_values(seed, layer, kind, start, count):
+    out = np.zeros(count, np.float32)
+    lib().or_synth_kv_values(seed, layer, kind, start, count, out)
+    return out
+
+
 def uniform_prompt(seed, n, vocab):
     ids = np.zeros(n, np.uint32)
     lib().or_uniform_prompt(seed, n, vocab, ids)
@@ -407,7 +414,7 @@ class Session:
         lib().or_session_set_attention(self.h, int(order))
 
     def fill_kv(self, n, seed=1):
-        """Timing aid: pseudo-random KV rows [0, n) in every layer (no parity meaning)."""
+        """N(0, 1) keys and values in KV rows [0, n) of every layer (or_synth_kv_values streams)."""
         lib().or_session_fill_kv(self.h, n, seed)
 
     def batch_row_logits(self, row):

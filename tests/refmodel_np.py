@@ -244,18 +244,23 @@ class Model:
         out[:, :, 1:self.rope_dim:2] = x0 * s + x1 * c
         return out.reshape(x.shape)
 
-    def logits(self, tokens) -> np.ndarray:
-        """Logits [T][V] of every position of `tokens` (positions 0..T-1, causal)."""
+    def logits(self, tokens, start=0, past=None) -> np.ndarray:
+        """Logits [T][V] of every position of `tokens` at positions start..start+T-1, causal.
+        past[layer] = (keys, values), each [start][Hkv*hd]: the cache rows before `start` as
+        stored (keys after RoPE)."""
         T = len(tokens)
-        pos = np.arange(T, dtype=np.float64)
+        pos = np.arange(start, start + T, dtype=np.float64)
         h = self.emb[np.asarray(tokens, np.int64)].copy()
         G = self.H // self.Hkv
-        causal = np.tril(np.ones((T, T), bool))
-        for ly in self.layers:
+        causal = np.arange(start + T)[None, :] <= (start + np.arange(T))[:, None]
+        for li, ly in enumerate(self.layers):
             x = q8_0(self._norm(h, ly["an"]))
             q = self._rope(x @ ly["q"].T, pos, self.H).reshape(T, self.H, self.hd)
             k = self._rope(x @ ly["k"].T, pos, self.Hkv).reshape(T, self.Hkv, self.hd)
             v = (x @ ly["v"].T).reshape(T, self.Hkv, self.hd)
+            if start:
+                k = np.concatenate([np.asarray(past[li][0], np.float64).reshape(start, self.Hkv, self.hd), k])
+                v = np.concatenate([np.asarray(past[li][1], np.float64).reshape(start, self.Hkv, self.hd), v])
             att = np.zeros((T, self.H, self.hd))
             for hh in range(self.H):
                 kv = hh // G

@@ -1,17 +1,23 @@
 """GPU tests at the benchmark configurations' full shapes (3 and 4).
 
-Where the CPU oracle can run the model in seconds, the GPU logits and streams are checked bit
-for bit against it; at the full workload sizes, size-independent properties stand in:
+The GPU logits are checked bit for bit against the CPU oracle at each configuration's own
+positions, with the KV cache filled by the seeded N(0, 1) streams both sides draw identically
+(nc_session_fill_kv / or_session_fill_kv); where the oracle cannot run the whole workload,
+size-independent properties stand in:
   config 2 (Llama-3-8B shape, Q4_0): one 5-row verify bit-exact vs the oracle after a short
-    prompt; at a 512-token prompt the speculative stream equals the GPU greedy record for
-    k in {2, 4, 8} x alpha in {0.5, 0.8}, with consistent statistics.
+    prompt and one at position 1024 over 1024 N(0, 1) positions; at a 512-token prompt the
+    speculative stream equals the GPU greedy record for k in {2, 4, 8} x alpha in {0.5, 0.8},
+    with consistent statistics.
   config 3 (Llama-3.2-3B shape Q4_K target, 1B-shape Q4_0 draft, T = 1): the stochastic stream
-    and statistics equal the oracle's at a short prompt; at a 4096-position context a draft
-    identical to the target is always accepted and the stream does not depend on how the
+    and statistics equal the oracle's at a short prompt; a 5-row verify of the target at position
+    4000 over 4000 N(0, 1) positions is bit-exact vs the oracle; at a 4096-position context a
+    draft identical to the target is always accepted and the stream does not depend on how the
     draft's prompt was chunked.
-  config 4 (Llama-3-70B shape, Q4_0): after an 8192-token prefill, the 9-row verify of the
-    greedy continuation accepts all 8 drafts and its 9 rows' logits equal nine single-token
-    forwards bit for bit.
+  config 4 (Llama-3-70B shape, Q4_0, 9-row verify over an 8192-token KV cache of N(0, 1) keys and
+    values): a two-layer model at the 70B width (d 8192, 64 heads, 8 KV heads, hd 128, FFN 28672,
+    vocab 128256: the same matmul shapes and attention tiers) is bit-exact vs the oracle at
+    position 8192; the full 80-layer model's 9-row verify of its greedy continuation accepts all
+    8 drafts and its rows' logits equal nine single-token forwards bit for bit.
 """
 import os
 
@@ -58,6 +64,19 @@ def test_config2_llama3_8b(ctx):
     for i in range(5):
         assert _same(gs.logits(i), ologits[i]), i
     os_.close()
+    # (a') the config's own positions: 1024 N(0, 1) positions, then a 5-row verify at 1024
+    print("config 2: N(0, 1) fill of 1024 positions, 5-row verify at 1024 vs the oracle", flush=True)
+    n = 1024
+    gs, os_ = nc.Session(gm, n + 16, 16), O.Session(om, n + 16, 16)
+    gs.fill_kv(n, 2)
+    os_.fill_kv(n, 2)
+    toks = nc.uniform_prompt(1024, 5, V)
+    a, nxt, newpos, preds = gs.verify_greedy(toks, n)
+    opreds, _, ologits = os_.verify_greedy(toks, n, want_logits=True)
+    assert np.array_equal(preds, opreds)
+    for i in range(5):
+        assert _same(gs.logits(i), ologits[i]), i
+    os_.close()
     om.close()
     del om
     # (b) 512-token prompt: speculative streams equal the greedy record at every (k, alpha)
@@ -93,6 +112,20 @@ def test_config3_q4k_target_stochastic(ctx):
                                                                         123)
     assert np.array_equal(out, o_out)
     assert (st.drafted, st.accepted, st.steps) == (drafted, accepted, steps)
+    # (a') the target at the config's context: a 5-row verify at position 4000 over 4000 N(0, 1)
+    # positions, every row bit-exact
+    print("config 3: N(0, 1) fill of 4000 positions, target 5-row verify at 4000 vs the oracle", flush=True)
+    n = 4000
+    gs, os_ = nc.Session(tm, n + 16, 16), O.Session(tmo, n + 16, 16)
+    gs.fill_kv(n, 3)
+    os_.fill_kv(n, 3)
+    toks = nc.uniform_prompt(4000, 5, V)
+    _, _, _, preds = gs.verify_greedy(toks, n)
+    opreds, _, ologits = os_.verify_greedy(toks, n, want_logits=True)
+    assert np.array_equal(preds, opreds)
+    for i in range(5):
+        assert _same(gs.logits(i), ologits[i]), i
+    os_.close()
     tmo.close()
     dmo.close()
     # (b) 4096-position context: draft == target => every draft accepted; the stream does not
@@ -109,6 +142,31 @@ def test_config3_q4k_target_stochastic(ctx):
     assert len(set(runs[0][0].tolist())) >= 8
 
 
+def test_config4_70b_width_two_layers_vs_oracle(ctx):
+    import nanocamelid_amd as nc
+    spec = dict(nc.SYNTH_CONFIGS["llama-3-70b"], layers=2, context_length=8192 + 64)
+    print("config 4: two-layer model at the 70B width", flush=True)
+    img = nc.synth_gguf(**spec, seed=71, nthreads=THREADS)
+    gm = nc.Model(ctx, data=img, nthreads=THREADS)
+    om = O.Model(data=img.tobytes(), nthreads=THREADS)
+    del img
+    V = gm.config["vocab_size"]
+    n, rows = 8192, 9
+    gs, os_ = nc.Session(gm, n + 16, 16), O.Session(om, n + 16, 16)
+    print("config 4: N(0, 1) fill of 8192 positions on both sides", flush=True)
+    gs.fill_kv(n, 70)
+    os_.fill_kv(n, 70)
+    toks = nc.uniform_prompt(8192, rows, V)
+    print("config 4: 9-row verify at 8192 (rows of 8193..8201 positions)", flush=True)
+    _, _, _, preds = gs.verify_greedy(toks, n)
+    opreds, _, ologits = os_.verify_greedy(toks, n, want_logits=True)
+    assert np.array_equal(preds, opreds)
+    for i in range(rows):
+        assert _same(gs.logits(i), ologits[i]), i
+    os_.close()
+    om.close()
+
+
 def test_config4_llama3_70b_verify(ctx):
     import nanocamelid_amd as nc
     print("config 4: synthesising the 70B-shape model (~40 GB)", flush=True)
@@ -116,22 +174,18 @@ def test_config4_llama3_70b_verify(ctx):
     gm = nc.Model(ctx, data=img, nthreads=THREADS)
     del img
     V = gm.config["vocab_size"]
-    n_prompt, n = 8192, 9
-    prompt = nc.uniform_prompt(70, n_prompt, V)
-    sess = nc.Session(gm, n_prompt + 64, 16)
-    print("config 4: 8192-token prefill", flush=True)
-    sess.prefill_pass_batch(prompt, 0, want_logits=False)
-    # greedy continuation by single-token passes, keeping every row's logits
-    pending, lg = sess.forward_pass(int(prompt[-1]), n_prompt - 1)
-    greedy, single = [pending], []
-    for i in range(n - 1):
-        nxt, lg = sess.forward_pass(greedy[-1], n_prompt + i)
+    n_ctx, n = 8192, 9
+    sess = nc.Session(gm, n_ctx + 64, 16)
+    print("config 4: N(0, 1) fill of the 8192-position KV cache", flush=True)
+    sess.fill_kv(n_ctx, 70)
+    # greedy continuation by single-token passes from position 8192, keeping every row's logits
+    greedy, single = [int(nc.uniform_prompt(70, 1, V)[0])], []
+    for i in range(n):
+        nxt, lg = sess.forward_pass(greedy[-1], n_ctx + i)
         single.append(lg)
         greedy.append(nxt)
-    _, lg = sess.forward_pass(greedy[-1], n_prompt + n - 1)
-    single.append(lg)
     print("config 4: 9-row verify of the greedy continuation", flush=True)
-    a, nxt, newpos, preds = sess.verify_greedy(np.array(greedy, np.uint32), n_prompt)
-    assert a == n - 1 and np.array_equal(preds[:n - 1], greedy[1:]) and newpos == n_prompt + n
+    a, nxt, newpos, preds = sess.verify_greedy(np.array(greedy[:n], np.uint32), n_ctx)
+    assert a == n - 1 and np.array_equal(preds, greedy[1:]) and newpos == n_ctx + n
     for i in range(n):
         assert _same(sess.logits(i), single[i]), i
