@@ -353,3 +353,74 @@ def test_ngram_loop_matches_python_restatement(temp, prompt_seed):
             st = int(toks[c])
             cut = O.Session(tm, 512, 16).generate_speculative_ngram(prompt, 40, 4, stop=(st,))[0]
             assert np.array_equal(cut, toks[:toks.tolist().index(st)])
+
+
+# ---------------------------------------------------------------- pins fixed by the mathematics
+_LCG_A = 6364136223846793005
+_LCG_A_INV = pow(_LCG_A, -1, 1 << 64)
+
+
+def _state_drawing(x: int) -> int:
+    """The LCG state whose next draw has upper word x (rand_simple then returns f32(x) / 2^32)."""
+    return ((((x << 32) - 1) * _LCG_A_INV) % (1 << 64))
+
+
+def test_lcg_state_construction():
+    for x in (0, 1, 2**31, 2**32 - 1):
+        u, _ = O.rand_simple(_state_drawing(x))
+        assert F(u) == F(np.uint32(x)) / F(4294967295)
+
+
+# Hand-worked walks: logits whose exponentials are exact (equal logits give e = 1, a logit 1000
+# below the maximum gives expf(-1000) = 0), so S and every r are exact and the boundary u·S = a
+# prefix sum can be hit on the nose.  The walk r -= e_i, stop at the first r <= 0.
+@pytest.mark.parametrize("logits,temp,x,want", [
+    # V = 2, e = [1, 1], S = 2: r = 2u; u = 1/2 gives r - 1 = 0 <= 0 -> id 0 (on the boundary)
+    ([0.0, 0.0], 1.0, 2**31, 0),
+    ([0.0, 0.0], 1.0, 2**31 - 128, 0),      # u just below 1/2: r - 1 < 0 -> id 0
+    ([0.0, 0.0], 1.0, 2**31 + 256, 1),      # u just above 1/2 (next f32): r - 1 > 0 -> id 1
+    ([0.0, 0.0], 0.25, 2**31 + 256, 1),     # temperature does not move equal logits
+    ([0.0, 0.0], 1.0, 0, 0),                # u = 0: r = 0 <= 0 at the first step
+    ([0.0, 0.0], 1.0, 2**32 - 1, 1),        # u = 1 (x rounds to 2^32): r = 2 - 1 - 1 = 0 -> last id
+    # V = 3, e = [1, 0, 1], S = 2: the zero-mass id 1 is never returned; above the first
+    # boundary the walk passes it (r stays > 0) and stops at id 2
+    ([0.0, -1000.0, 0.0], 1.0, 2**31, 0),
+    ([0.0, -1000.0, 0.0], 1.0, 2**31 + 256, 2),
+    # V = 3, e = [1, 1, 1], S = 3: r = fl(3u); u = f32(1/3) = 11184811 * 2^-25 gives
+    # 3u = 1 + 2^-25 -> r = 1.0 -> id 0; the next f32 above gives r = 1 + 2^-23 -> id 1;
+    # u = f32(2/3) = 11184811 * 2^-24: 3u = 2 + 2^-24 -> r = 2.0 -> id 1; next above -> id 2
+    ([0.0, 0.0, 0.0], 1.0, 1431655808, 0),
+    ([0.0, 0.0, 0.0], 1.0, 1431655808 + 128, 1),
+    ([0.0, 0.0, 0.0], 1.0, 2863311616, 1),
+    ([0.0, 0.0, 0.0], 1.0, 2863311616 + 256, 2),
+])
+def test_sample_logits_hand_worked_boundaries(logits, temp, x, want):
+    st0 = _state_drawing(x)
+    i, st = O.sample_logits(np.array(logits, F), temp, st0)
+    assert i == want
+    assert st == (st0 * _LCG_A + 1) % (1 << 64)  # exactly one draw
+
+
+def _chi2_pvalue(counts, p):
+    from scipy import stats
+    exp = p * counts.sum()
+    return stats.chi2.sf(float(((counts - exp) ** 2 / exp).sum()), len(p) - 1)
+
+
+@pytest.mark.parametrize("temp", [0.7, 1.3])
+def test_sample_logits_frequencies_follow_softmax(temp):
+    # the distribution sample_logits draws from is softmax(l / T): chi-square over 60000 draws
+    # of the reference's LCG, against float64 softmax; a planted mistake (the temperature
+    # dropped) is rejected by the same statistic
+    l = np.array([1.0, 0.5, 0.0, -0.5, 2.0, -1.0], F)
+    st, counts = O.REFERENCE_RNG_STATE, np.zeros(len(l))
+    for _ in range(60000):
+        i, st = O.sample_logits(l, temp, st)
+        counts[i] += 1
+    z = l.astype(np.float64) / temp
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    assert _chi2_pvalue(counts, p) > 1e-4
+    q = np.exp(l.astype(np.float64) - l.max())
+    q /= q.sum()
+    assert _chi2_pvalue(counts, q) < 1e-12
