@@ -163,6 +163,23 @@ def _q4_k_random_blocks(M, K, seed):
     return blk
 
 
+def _cpu_matmul_leg(blocks, xq, xs, N, M, K, algo):
+    """The oracle's matmul (the reference's portable x86 path: per-row block-ordered f32 sums, rows
+    split over threads as inference.rs:1318-1330 does) on the same weights and activations, on
+    HOST_THREADS and on the reference's default 4 threads; GB/s of the same algorithmic bytes."""
+    from oracle import oracle as O
+    out = {}
+    for nt in sorted({HOST_THREADS, 4}):
+        t = time.perf_counter()
+        reps = 0
+        while reps < 1 or time.perf_counter() - t < 0.2:
+            O.matmul_q4_0(xq, xs, blocks, N, M, K, nthreads=nt)
+            reps += 1
+        dt = (time.perf_counter() - t) / reps
+        out[f"{nt}_threads_GBps"] = round(algo / dt / 1e9, 2)
+    return out
+
+
 def run_gemm_sweep(args):
     """Config 1: per-shape median kernel time (dispatch-stamped events around each of >= 60
     back-to-back launches) rotating >= 1 GB of distinct weight copies."""
@@ -198,6 +215,8 @@ def run_gemm_sweep(args):
             algo = wbytes + N * K + 4 * N * (K // 32) + 4 * N * M
             res[f"N{N}"] = {"us_median": round(med, 2), "GBps": round(algo / med / 1e3, 1),
                             "us_mean": round(float(np.mean(us[copies:])), 2)}
+            if not args.no_cpu_baseline:
+                res[f"N{N}"]["cpu"] = _cpu_matmul_leg(blocks, xq.cpu().numpy(), xs.cpu().numpy(), N, M, K, algo)
         print(json.dumps(res), flush=True)
         for m in mats:
             m.close()
@@ -621,6 +640,24 @@ def main():
         achieved = gemm_bytes / (gemm_ms / 1e3) / 1e9
         log(f"gemm: {launches} launches, {gemm_ms / launches * 1e3:.2f} us avg, "
             f"{gemm_bytes / launches / 1e6:.2f} MB avg -> {achieved:.0f} GB/s")
+    # stage pass: HIP events between the stages of every verify pass, named as the reference's
+    # NANOCAMELID_TRACE stages (inference.rs:179-229); a separate run, outside the timed region
+    stages = None
+    if args.roofline_steps > 0:
+        sess.stage_timing(True)
+        _, sst2 = sess.generate_speculative_oracle(prompt, n_rec, args.k, args.alpha, args.seed, greedy,
+                                                   max_steps=args.roofline_steps)
+        raw = sess.stages()
+        sess.stage_timing(False)
+        npass = max(sst2.steps, 1)
+        per = {k: round(v[0] / npass * 1e3, 2) for k, v in raw.items()}
+        total = sum(per.values())
+        stages = {"us_per_verify_pass": per, "sum_us": round(total, 1),
+                  "share": {k: round(v / total, 4) for k, v in per.items()} if total else {},
+                  "passes": int(npass), "calls": {k: int(v[1]) for k, v in raw.items()},
+                  "note": "events between stages on the session stream; stage names are the reference's trace "
+                          "stages, '+' joins stages the device runs as one kernel"}
+        log(f"stages (us per verify pass): {per}")
     # the config's whole 1024-token decode at every (k, alpha) point, each a separate call
     full = {}
     if not args.no_full_decode:
@@ -708,7 +745,8 @@ def main():
                    "opt_in_split_attention": split,
                    "verify_weight_bytes": int(cfg["verify_weight_bytes"]),
                    "kv_bytes_read_per_step": int(kv_step),
-                   "whole_pass_GBps": round(whole_gbs, 1)},
+                   "whole_pass_GBps": round(whole_gbs, 1),
+                   "stages": stages},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": measured_traffic(args),
                      "kernel": "gemm_q4_0_r16_kernel + gemm_q4_0_kernel (all verify matmuls)",

@@ -450,7 +450,15 @@ int nc_session_fill_kv(nc_session* s, int64_t n, uint64_t seed);
  * roofline.  family: "gemm_q4_0" (all verify matmuls).  Prompt prefill passes are
  * never timed: only decode and verify passes count.  Returns launches counted. */
 int64_t nc_session_kernel_timing(nc_session* s, const char* family, double* total_ms, int64_t* bytes);
+/* enable: bit 0 = the matmul timing above; bit 1 = per-stage timing (HIP events between the
+ * stages of every verify and decode pass, the reference's NANOCAMELID_TRACE stage breakdown,
+ * inference.rs:179-229).  Either resets its totals. */
 int nc_session_timing_enable(nc_session* s, int32_t enable);
+/* Per-stage totals since the last enable: returns the number of stages; for 0 <= index < that
+ * number writes the stage's name (the reference's trace stage names, joined with '+' where the
+ * device runs them as one kernel), its total ms and the number of times it ran. */
+int32_t nc_session_stage_timing(nc_session* s, int32_t index, char* name, int32_t name_cap, double* total_ms,
+                                int64_t* calls);
 
 #ifdef __cplusplus
 }

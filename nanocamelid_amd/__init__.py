@@ -385,6 +385,23 @@ class Session:
     def timing(self, enable: bool):
         check(lib().nc_session_timing_enable(self.h, 1 if enable else 0))
 
+    def stage_timing(self, enable: bool):
+        """Per-stage timing of verify and decode passes (the reference's trace stages)."""
+        check(lib().nc_session_timing_enable(self.h, 2 if enable else 0))
+
+    def stages(self) -> dict:
+        """{stage name: (total ms, passes)} since stage_timing(True)."""
+        n = lib().nc_session_stage_timing(self.h, -1, None, 0, None, None)
+        if n < 0:
+            check(n)
+        out = {}
+        for i in range(n):
+            name = C.create_string_buffer(96)
+            ms, calls = C.c_double(), C.c_int64()
+            check(min(0, lib().nc_session_stage_timing(self.h, i, name, 96, C.byref(ms), C.byref(calls))))
+            out[name.value.decode()] = (ms.value, int(calls.value))
+        return out
+
     def gemm_timing(self):
         ms = C.c_double()
         by = C.c_int64()

@@ -124,6 +124,8 @@ SIGNATURES = {
     "nc_session_fill_kv": (C.c_int, [_vp, _i64, C.c_uint64]),
     "nc_session_kernel_timing": (_i64, [_vp, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
     "nc_session_timing_enable": (C.c_int, [_vp, _i32]),
+    "nc_session_stage_timing": (C.c_int32, [_vp, _i32, C.c_char_p, _i32, C.POINTER(C.c_double),
+                                            C.POINTER(C.c_int64)]),
 }
 
 _lib = None

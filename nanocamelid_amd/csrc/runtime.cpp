@@ -92,6 +92,13 @@ struct nc_session {
     uint32_t staged[16] = {};
     int n_staged = 0;  // staged tokens land in d_toks[0..n_staged); the rest stay as they are
     bool pending_toks = false;
+    // per-stage timing (events between the pass's stages, named as the reference's trace stages)
+    bool stage_timing = false;
+    std::vector<hipEvent_t> stage_ev;
+    std::vector<int> stage_of;  // stage id of each recorded mark, -1 for a pass's end mark
+    size_t stage_used = 0;
+    std::vector<double> stage_ms;
+    std::vector<int64_t> stage_calls;
     // per-kernel timing (HIP events on the session stream)
     bool timing = false;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
@@ -757,6 +764,56 @@ static int residual_gemm(nc_session* s, const QMatDev& w, GemmParams& p, int n) 
     return rc;
 }
 
+// Stages of a verify / decode pass, named as the reference's NANOCAMELID_TRACE stages
+// (inference.rs:179-229, recorded at :3732-4109 and :4460-4832); stages the device fuses into one
+// kernel carry the names of all of them.
+static const char* const kStageNames[] = {
+    "batch.embed_lookup",
+    "batch.attn_norm+batch.attn_quant",
+    "batch.wq+batch.wk+batch.wv+batch.rope_store_kv",
+    "batch.attention+batch.wo_quant",
+    "batch.wo",
+    "batch.ffn_norm+batch.ffn_quant",
+    "batch.w1+batch.w3+batch.silu_mul+batch.down_quant",
+    "batch.w2",
+    "decode.head_norm+decode.head_quant",
+    "decode.head",
+};
+constexpr int kStages = (int)(sizeof(kStageNames) / sizeof(kStageNames[0]));
+enum Stage { ST_EMBED, ST_ATTN_NORM, ST_QKV, ST_ATTENTION, ST_WO, ST_FFN_NORM, ST_GATEUP, ST_DOWN, ST_HEAD_NORM, ST_HEAD };
+
+// Resolves the recorded marks: each mark's stage lasts until the next mark of its pass.
+static int flush_stages(nc_session* s) {
+    if (s->stage_used == 0) return NC_OK;
+    NC_HIP(hipStreamSynchronize(s->stream));
+    for (size_t i = 0; i + 1 < s->stage_used; i++) {
+        if (s->stage_of[i] < 0) continue;
+        float ms = 0;
+        NC_HIP(hipEventElapsedTime(&ms, s->stage_ev[i], s->stage_ev[i + 1]));
+        s->stage_ms[s->stage_of[i]] += ms;
+        s->stage_calls[s->stage_of[i]]++;
+    }
+    s->stage_used = 0;
+    return NC_OK;
+}
+
+// Records the start of `stage` (or, with stage = -1, the end of the pass) on the session stream.
+static int stage_mark(nc_session* s, int stage) {
+    if (!s->stage_timing) return NC_OK;
+    NC_HIP(hipEventRecord(s->stage_ev[s->stage_used], s->stream));
+    s->stage_of[s->stage_used++] = stage;
+    return NC_OK;
+}
+
+// Before a pass: room for its marks (the embedding, 7 per layer, 2 for the head and the end),
+// else resolve the recorded ones.
+static int stage_reserve(nc_session* s) {
+    if (!s->stage_timing) return NC_OK;
+    const size_t need = 4 + 7 * (size_t)s->m->cfg.block_count;
+    if (s->stage_used + need > s->stage_ev.size()) return flush_stages(s);
+    return NC_OK;
+}
+
 // One forward over the n tokens already in d_toks at positions start_pos..: embedding,
 // all layers (run_layer_range_batch, inference.rs:3747-4111), final norm, head and
 // per-row argmax.  Writes d_preds and logits.
@@ -768,8 +825,10 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
     if (n < 1 || n > s->max_batch) return fail(NC_ERANGE, "batch exceeds the session's max_batch");
     if (start_pos < 0 || start_pos + n > s->max_ctx) return fail(NC_ERANGE, "batch end exceeds the session context");
     hipStream_t st = s->stream;
-    int rc = launch_set_pass_state(s->d_pos, (int32_t)start_pos, s->d_toks, s->pending_toks ? s->staged : nullptr,
-                                   s->pending_toks ? s->n_staged : 0, st);
+    int rc = stage_reserve(s);
+    if (rc || (rc = stage_mark(s, ST_EMBED))) return rc;
+    rc = launch_set_pass_state(s->d_pos, (int32_t)start_pos, s->d_toks, s->pending_toks ? s->staged : nullptr,
+                               s->pending_toks ? s->n_staged : 0, st);
     if (rc) return rc;
     s->pending_toks = false;
     rc = launch_embed(m->tok_emb, s->d_toks, n, d, s->hidden, st);
@@ -777,7 +836,9 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
     const size_t layer_kv = (size_t)Hkv * s->ctx_stride * hd;
     for (int64_t li = 0; li < c.block_count; li++) {
         const LayerDev& L = m->layers[li];
-        if ((rc = launch_rmsnorm_q8(s->hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
+        if ((rc = stage_mark(s, ST_ATTN_NORM)) ||
+            (rc = launch_rmsnorm_q8(s->hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)) ||
+            (rc = stage_mark(s, ST_QKV)))
             return rc;
         GemmParams p;
         p.kernel = s->ctx->gemm_kernel;
@@ -829,7 +890,8 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         a.part_o = s->attn_part_o;
         a.part_ml = s->attn_part_ml;
         a.nchunks = s->attn_chunks;
-        if ((rc = launch_attention(a, st))) return rc;
+        if ((rc = stage_mark(s, ST_ATTENTION)) || (rc = launch_attention(a, st)) || (rc = stage_mark(s, ST_WO)))
+            return rc;
         GemmParams po;
         po.kernel = s->ctx->gemm_kernel;
         po.x = s->xq;
@@ -839,8 +901,9 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         po.epi = EPI_RESIDUAL;
         po.out = s->hidden;
         po.ld_out = d;
-        if ((rc = residual_gemm(s, L.wo, po, n))) return rc;
-        if ((rc = launch_rmsnorm_q8(s->hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
+        if ((rc = residual_gemm(s, L.wo, po, n)) || (rc = stage_mark(s, ST_FFN_NORM)) ||
+            (rc = launch_rmsnorm_q8(s->hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)) ||
+            (rc = stage_mark(s, ST_GATEUP)))
             return rc;
         GemmParams pg;
         pg.kernel = s->ctx->gemm_kernel;
@@ -872,12 +935,15 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         pd.epi = EPI_RESIDUAL;
         pd.out = s->hidden;
         pd.ld_out = d;
-        if ((rc = residual_gemm(s, L.down, pd, n))) return rc;
+        if ((rc = stage_mark(s, ST_DOWN)) || (rc = residual_gemm(s, L.down, pd, n))) return rc;
     }
     s->last_n = head ? n : 0;
-    if (!head) return NC_OK;  // a prompt chunk whose logits nobody reads (prefill_pass_batch)
+    if (!head) return stage_mark(s, -1);  // a prompt chunk whose logits nobody reads (prefill_pass_batch)
     // compute_logits_from_hidden (inference.rs:4783-4832) for every row + argmax
-    if ((rc = launch_rmsnorm_q8(s->hidden, m->out_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st))) return rc;
+    if ((rc = stage_mark(s, ST_HEAD_NORM)) ||
+        (rc = launch_rmsnorm_q8(s->hidden, m->out_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)) ||
+        (rc = stage_mark(s, ST_HEAD)))
+        return rc;
     GemmParams ph;
     ph.kernel = s->ctx->gemm_kernel;
     ph.x = s->xq;
@@ -892,7 +958,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
     if ((rc = timed_gemm(s, m->head, ph))) return rc;
     if ((rc = launch_argmax_final(s->part_val, s->part_idx, n, (int)m->head.tiles, s->d_preds, st))) return rc;
     s->last_n = n;
-    return NC_OK;
+    return stage_mark(s, -1);
 }
 
 // Stages the next pass's tokens; run_pass writes them to the device together with the
@@ -1099,10 +1165,14 @@ static int prefill_chunks(nc_session* s, const uint32_t* toks, int n, int64_t st
     // per-kernel timing covers decode and verify passes only, never the prompt
     struct TimingOff {
         nc_session* s;
-        bool was;
-        ~TimingOff() { s->timing = was; }
-    } guard{s, s->timing};
+        bool was, was_stage;
+        ~TimingOff() {
+            s->timing = was;
+            s->stage_timing = was_stage;
+        }
+    } guard{s, s->timing, s->stage_timing};
     s->timing = false;
+    s->stage_timing = false;
     int rc;
     for (int i = 0; i < n; i++)  // every id is checked before the first chunk runs
         if (toks[i] >= (uint32_t)s->m->cfg.vocab_size)
@@ -1538,6 +1608,7 @@ void nc_session_free(nc_session* s) {
         (void)hipEventDestroy(e.first);
         (void)hipEventDestroy(e.second);
     }
+    for (auto e : s->stage_ev) (void)hipEventDestroy(e);
     for (void* p : s->allocs) (void)hipFree(p);
     for (void* p : {(void*)s->h_toks, (void*)s->h_preds, (void*)s->h_result, (void*)s->h_pos})
         if (p) (void)hipHostFree(p);
@@ -2340,13 +2411,36 @@ int nc_session_fill_kv(nc_session* s, int64_t n, uint64_t seed) {
 int nc_session_timing_enable(nc_session* s, int32_t enable) {
     if (!s) return fail(NC_EINVAL, "null session");
     int rc = flush_timing(s);
-    if (rc) return rc;
-    s->timing = enable != 0;
+    if (rc || (rc = flush_stages(s))) return rc;
+    if ((enable & 2) && s->stage_ev.empty()) {
+        s->stage_ev.resize(4096);
+        s->stage_of.resize(4096);
+        for (auto& e : s->stage_ev) NC_HIP(hipEventCreate(&e));
+    }
+    s->stage_timing = (enable & 2) != 0;
+    s->stage_ms.assign(kStages, 0.0);
+    s->stage_calls.assign(kStages, 0);
+    s->timing = (enable & 1) != 0;
     s->gemm_ms = 0.0;
     s->gemm_launches = 0;
     s->gemm_bytes = 0;
     s->pending_bytes = 0;
     return NC_OK;
+}
+
+int32_t nc_session_stage_timing(nc_session* s, int32_t index, char* name, int32_t name_cap, double* total_ms,
+                                int64_t* calls) {
+    if (!s) return fail(NC_EINVAL, "null session");
+    if (int rc = flush_stages(s)) return rc;
+    if (index >= 0 && index < kStages) {
+        if (name && name_cap > 0) {
+            std::strncpy(name, kStageNames[index], (size_t)name_cap - 1);
+            name[name_cap - 1] = 0;
+        }
+        if (total_ms) *total_ms = s->stage_ms.empty() ? 0.0 : s->stage_ms[index];
+        if (calls) *calls = s->stage_calls.empty() ? 0 : s->stage_calls[index];
+    }
+    return kStages;
 }
 
 int64_t nc_session_kernel_timing(nc_session* s, const char* family, double* total_ms, int64_t* bytes) {
