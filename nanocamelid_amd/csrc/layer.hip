@@ -171,7 +171,7 @@ int launch_rmsnorm_q8(const float* hidden, const float* weight, int N, int d, fl
     // 4.9 us against 6.0 us for 1024 threads, at d = 8192 6.4 against 6.8 us; 256 threads were
     // slower still), small ones 256.
 #define NC_RMS(E, T)                                                                                     \
-    hipLaunchKernelGGL((rmsnorm_q8_kernel<E, T>), dim3(N), dim3(T), 0, st, hidden, weight, eps, xq, xs, xsum); \
+    NC_LAUNCH((rmsnorm_q8_kernel<E, T>), dim3(N), dim3(T), 0, st, hidden, weight, eps, xq, xs, xsum); \
     break;
     switch (d) {
         case 256: NC_RMS(1, 256)
@@ -214,7 +214,7 @@ int launch_expf_range(uint32_t first, int64_t count, float* out, hipStream_t st)
     if (count < 0 || count > ((int64_t)1 << 32)) return fail(NC_ERANGE, "expf range: 0..2^32 values");
     if (count == 0) return NC_OK;
     const int64_t blocks = std::min<int64_t>((count + 255) / 256, 65536);
-    hipLaunchKernelGGL(expf_range_kernel, dim3((unsigned)blocks), dim3(256), 0, st, first, count, out);
+    NC_LAUNCH(expf_range_kernel, dim3((unsigned)blocks), dim3(256), 0, st, first, count, out);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
@@ -222,7 +222,7 @@ int launch_expf_range(uint32_t first, int64_t count, float* out, hipStream_t st)
 int launch_quantize_q8(const float* x, int N, int dim, int8_t* xq, float* xs, int32_t* xsum, hipStream_t st) {
     if (dim % 32) return fail(NC_EINVAL, "quantize: width must be a multiple of 32");
     const int total = N * (dim / 32);
-    hipLaunchKernelGGL(quantize_q8_kernel, dim3((total * 32 + 255) / 256), dim3(256), 0, st, x, dim, total, xq, xs, xsum);
+    NC_LAUNCH(quantize_q8_kernel, dim3((total * 32 + 255) / 256), dim3(256), 0, st, x, dim, total, xq, xs, xsum);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
@@ -238,7 +238,7 @@ __global__ void block_sums_kernel(const int8_t* x, int total_blocks, int32_t* xs
 
 int launch_block_sums(const int8_t* x, int N, int dim, int32_t* xsum, hipStream_t st) {
     const int total = N * (dim / 32);
-    hipLaunchKernelGGL(block_sums_kernel, dim3((total + 255) / 256), dim3(256), 0, st, x, total, xsum);
+    NC_LAUNCH(block_sums_kernel, dim3((total + 255) / 256), dim3(256), 0, st, x, total, xsum);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
@@ -255,7 +255,7 @@ __global__ void set_pass_state_kernel(int32_t* d_pos, int32_t pos, uint32_t* d_t
 int launch_set_pass_state(int32_t* d_pos, int32_t pos, uint32_t* d_toks, const uint32_t* toks, int n, hipStream_t st) {
     TokenArgs a{};
     for (int i = 0; i < n && i < 16; i++) a.t[i] = toks ? toks[i] : 0u;
-    hipLaunchKernelGGL(set_pass_state_kernel, dim3(1), dim3(64), 0, st, d_pos, pos, d_toks, a, toks ? n : 0);
+    NC_LAUNCH(set_pass_state_kernel, dim3(1), dim3(64), 0, st, d_pos, pos, d_toks, a, toks ? n : 0);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
@@ -269,7 +269,7 @@ __global__ void embed_kernel(const float* table, const uint32_t* toks, int d, fl
 }
 
 int launch_embed(const float* table, const uint32_t* toks, int N, int d, float* hidden, hipStream_t st) {
-    hipLaunchKernelGGL(embed_kernel, dim3((d + 255) / 256, N), dim3(256), 0, st, table, toks, d, hidden);
+    NC_LAUNCH(embed_kernel, dim3((d + 255) / 256, N), dim3(256), 0, st, table, toks, d, hidden);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
@@ -877,10 +877,10 @@ static int launch_attention_split(const AttnParams& a, hipStream_t st) {
     const dim3 grid(a.Hkv, (GN + wgq - 1) / wgq, (nch + cpw - 1) / cpw);
 #define NC_SPLIT_QG(HD, CPW)                                                                               \
     switch (qg) {                                                                                          \
-        case 4: hipLaunchKernelGGL((attn_split_kernel<HD, 4, CPW>), grid, dim3(256), 0, st, a); break;    \
-        case 8: hipLaunchKernelGGL((attn_split_kernel<HD, 8, CPW>), grid, dim3(256), 0, st, a); break;    \
-        case 12: hipLaunchKernelGGL((attn_split_kernel<HD, 12, CPW>), grid, dim3(256), 0, st, a); break;  \
-        default: hipLaunchKernelGGL((attn_split_kernel<HD, 16, CPW>), grid, dim3(256), 0, st, a); break;  \
+        case 4: NC_LAUNCH((attn_split_kernel<HD, 4, CPW>), grid, dim3(256), 0, st, a); break;    \
+        case 8: NC_LAUNCH((attn_split_kernel<HD, 8, CPW>), grid, dim3(256), 0, st, a); break;    \
+        case 12: NC_LAUNCH((attn_split_kernel<HD, 12, CPW>), grid, dim3(256), 0, st, a); break;  \
+        default: NC_LAUNCH((attn_split_kernel<HD, 16, CPW>), grid, dim3(256), 0, st, a); break;  \
     }
 #define NC_SPLIT(HD)                                                                            \
     if (cpw == 4) {                                                                             \
@@ -891,7 +891,7 @@ static int launch_attention_split(const AttnParams& a, hipStream_t st) {
         NC_SPLIT_QG(HD, 1)                                                                      \
     }                                                                                           \
     NC_HIP(hipGetLastError());                                                                  \
-    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(a.N * a.H), dim3(HD), 0, st, a);
+    NC_LAUNCH((attn_combine_kernel<HD>), dim3(a.N * a.H), dim3(HD), 0, st, a);
     if (a.hd == 128) {
         NC_SPLIT(128)
     } else {
@@ -920,8 +920,8 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
         // at most 512 and of 1281..1536 positions on 512 threads (two waves per SIMD in the
         // score phase; measured faster there, slower for 513..1280)
 #define NC_FUSED(E, T)                                                                               \
-    if (a.hd == 128) hipLaunchKernelGGL((attn_fused_kernel<E, T, 128>), grid, dim3(T), 0, st, a);    \
-    else hipLaunchKernelGGL((attn_fused_kernel<E, T, 64>), grid, dim3(T), 0, st, a);
+    if (a.hd == 128) NC_LAUNCH((attn_fused_kernel<E, T, 128>), grid, dim3(T), 0, st, a);    \
+    else NC_LAUNCH((attn_fused_kernel<E, T, 64>), grid, dim3(T), 0, st, a);
         if (len <= 512) {
             NC_FUSED(1, 512)
         } else if (len <= 768) {
@@ -943,7 +943,7 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
     // blockIdx.z so that every SIMD gets a short chain instead of a few SIMDs getting long ones
     const int rb = a.N >= 2 ? 2 : 1;
 #define NC_SCORES(HD, RB)                                                                         \
-    hipLaunchKernelGGL((attn_scores_kernel<HD, RB>), dim3(a.Hkv, tiles, (a.N + (RB)-1) / (RB)), dim3(64 * G), 0, \
+    NC_LAUNCH((attn_scores_kernel<HD, RB>), dim3(a.Hkv, tiles, (a.N + (RB)-1) / (RB)), dim3(64 * G), 0, \
                        st, a);                                                                    \
     break;
 #define NC_SCORES_HD(HD)            \
@@ -960,15 +960,15 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
 #undef NC_SCORES
     NC_HIP(hipGetLastError());
 #define NC_PV(E, T, PIPE)                                                                              \
-    if (a.hd == 128) hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 128, PIPE>), grid, dim3(T), 0, st, a); \
-    else hipLaunchKernelGGL((attn_softmax_pv_kernel<E, T, 64, PIPE>), grid, dim3(T), 0, st, a);
+    if (a.hd == 128) NC_LAUNCH((attn_softmax_pv_kernel<E, T, 128, PIPE>), grid, dim3(T), 0, st, a); \
+    else NC_LAUNCH((attn_softmax_pv_kernel<E, T, 64, PIPE>), grid, dim3(T), 0, st, a);
     if (len > 16384) return fail(NC_ERANGE, "attention: context longer than 16384 positions");
     if (a.N * a.H > 256 && len > 8192 && len <= 8192 + 256) {
         // more units than CUs on rows just past 8192 positions (a verify over an 8192-position
         // cache): the 256-thread tier with one extra position per thread (70B shape, 9 rows x
         // 64 heads at 8201 positions)
-        if (a.hd == 128) hipLaunchKernelGGL((attn_softmax_pv_kernel<32, 256, 128, true, 1>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((attn_softmax_pv_kernel<32, 256, 64, true, 1>), grid, dim3(256), 0, st, a);
+        if (a.hd == 128) NC_LAUNCH((attn_softmax_pv_kernel<32, 256, 128, true, 1>), grid, dim3(256), 0, st, a);
+        else NC_LAUNCH((attn_softmax_pv_kernel<32, 256, 64, true, 1>), grid, dim3(256), 0, st, a);
     } else if (a.N * a.H <= 256 || len > 8192) {
         // at most one unit per CU: 512 threads, two waves per SIMD through the max, exp and sum
         // phases (a wave issues one VALU instruction per 8 cycles at most; 2000 positions 27.2
@@ -1037,7 +1037,7 @@ __global__ void argmax_final_kernel(const float* pv, const int32_t* pi, int ntil
 
 int launch_argmax_final(const float* part_val, const int32_t* part_idx, int N, int ntiles, uint32_t* preds,
                         hipStream_t st) {
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(N), dim3(256), 0, st, part_val, part_idx, ntiles, preds);
+    NC_LAUNCH(argmax_final_kernel, dim3(N), dim3(256), 0, st, part_val, part_idx, ntiles, preds);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
@@ -1060,7 +1060,7 @@ __global__ void accept_greedy_kernel(const uint32_t* toks, const uint32_t* preds
 
 int launch_accept_greedy(const uint32_t* toks, const uint32_t* preds, int n, int32_t* d_pos, int32_t* result,
                          uint32_t* next_tok_slot, hipStream_t st) {
-    hipLaunchKernelGGL(accept_greedy_kernel, dim3(1), dim3(64), 0, st, toks, preds, n, d_pos, result, next_tok_slot);
+    NC_LAUNCH(accept_greedy_kernel, dim3(1), dim3(64), 0, st, toks, preds, n, d_pos, result, next_tok_slot);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }

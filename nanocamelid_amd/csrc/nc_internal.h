@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <cstdint>
 #include <cstdio>
@@ -21,6 +22,22 @@ int fail(int code, const std::string& msg);
         hipError_t _e = (call);                                                        \
         if (_e != hipSuccess)                                                          \
             return ::nc::fail(NC_EHIP, std::string(#call) + ": " + hipGetErrorString(_e)); \
+    } while (0)
+
+// ---------------------------------------------------------------- stage timing
+// While t_stage_ev1 is set (a session's stage timing), kernels launched through NC_LAUNCH are
+// dispatched with events stamped by the dispatch itself: t_stage_ev0 records the first such
+// kernel's start (and is then cleared), t_stage_ev1 every kernel's end, so the pair spans the
+// kernels of one stage and nothing between launches.
+extern thread_local hipEvent_t t_stage_ev0, t_stage_ev1;
+#define NC_LAUNCH(K, G, B, L, S, ...)                                                          \
+    do {                                                                                       \
+        if (::nc::t_stage_ev1) {                                                               \
+            hipExtLaunchKernelGGL(K, G, B, L, S, ::nc::t_stage_ev0, ::nc::t_stage_ev1, 0, __VA_ARGS__); \
+            ::nc::t_stage_ev0 = nullptr;                                                       \
+        } else {                                                                               \
+            hipLaunchKernelGGL(K, G, B, L, S, __VA_ARGS__);                                    \
+        }                                                                                      \
     } while (0)
 
 // ---------------------------------------------------------------- weight layouts

@@ -210,12 +210,12 @@ int launch_gemm_prompt(const QMatDev& w, const int8_t* x, const float* xs, float
     p.out = out;
     if (prompt_row_tiles(w.rows, N) == 2) {
         const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 63) / 64));
-        if (w.layout == LAYOUT_R16) hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R16, 2, 2>), grid, dim3(256), 0, st, p);
-        else hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R64, 2, 2>), grid, dim3(256), 0, st, p);
+        if (w.layout == LAYOUT_R16) NC_LAUNCH((gemm_q4_0_prompt_kernel<LAYOUT_R16, 2, 2>), grid, dim3(256), 0, st, p);
+        else NC_LAUNCH((gemm_q4_0_prompt_kernel<LAYOUT_R64, 2, 2>), grid, dim3(256), 0, st, p);
     } else {
         const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 31) / 32));
-        if (w.layout == LAYOUT_R16) hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R16, 2, 1>), grid, dim3(256), 0, st, p);
-        else hipLaunchKernelGGL((gemm_q4_0_prompt_kernel<LAYOUT_R64, 2, 1>), grid, dim3(256), 0, st, p);
+        if (w.layout == LAYOUT_R16) NC_LAUNCH((gemm_q4_0_prompt_kernel<LAYOUT_R16, 2, 1>), grid, dim3(256), 0, st, p);
+        else NC_LAUNCH((gemm_q4_0_prompt_kernel<LAYOUT_R64, 2, 1>), grid, dim3(256), 0, st, p);
     }
     NC_HIP(hipGetLastError());
     return NC_OK;
@@ -443,12 +443,12 @@ int launch_gemm_prompt_q4k(const QMatDev& w, float* out, int ld_out, int N, hipS
     p.out = out;
     if (prompt_row_tiles(w.rows, N) == 2) {
         const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 63) / 64));
-        if (w.layout == LAYOUT_R16K) hipLaunchKernelGGL((gemm_q4_k_prompt_kernel<LAYOUT_R16K, 2>), grid, dim3(256), 0, st, p);
-        else hipLaunchKernelGGL((gemm_q4_k_prompt_kernel<LAYOUT_R64, 2>), grid, dim3(256), 0, st, p);
+        if (w.layout == LAYOUT_R16K) NC_LAUNCH((gemm_q4_k_prompt_kernel<LAYOUT_R16K, 2>), grid, dim3(256), 0, st, p);
+        else NC_LAUNCH((gemm_q4_k_prompt_kernel<LAYOUT_R64, 2>), grid, dim3(256), 0, st, p);
     } else {
         const dim3 grid((unsigned)((w.rows + 63) / 64), (unsigned)((N + 31) / 32));
-        if (w.layout == LAYOUT_R16K) hipLaunchKernelGGL((gemm_q4_k_prompt_kernel<LAYOUT_R16K, 1>), grid, dim3(256), 0, st, p);
-        else hipLaunchKernelGGL((gemm_q4_k_prompt_kernel<LAYOUT_R64, 1>), grid, dim3(256), 0, st, p);
+        if (w.layout == LAYOUT_R16K) NC_LAUNCH((gemm_q4_k_prompt_kernel<LAYOUT_R16K, 1>), grid, dim3(256), 0, st, p);
+        else NC_LAUNCH((gemm_q4_k_prompt_kernel<LAYOUT_R64, 1>), grid, dim3(256), 0, st, p);
     }
     NC_HIP(hipGetLastError());
     return NC_OK;
@@ -511,7 +511,7 @@ int launch_prompt_repack(const int8_t* x, const float* xs, int N, int K, void* x
                          float* xam) {
     const int nb = K / 32, n16 = (N + 15) / 16, nq = (nb + 3) / 4;
     const int64_t total = (int64_t)n16 * nb * 64 + (int64_t)n16 * nq * 16;
-    hipLaunchKernelGGL(prompt_repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x, xs, N, nb,
+    NC_LAUNCH(prompt_repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x, xs, N, nb,
                        (uint2*)xm, (float4*)xsm, (float4*)xam);
     NC_HIP(hipGetLastError());
     return NC_OK;
@@ -555,7 +555,7 @@ int launch_prompt_qkv_rope(const float* y, int N, int start, int aw, int kw, int
                            hipStream_t st) {
     if ((aw | kw) & 1) return fail(NC_EINVAL, "prompt RoPE: widths must be even");
     const int rows = aw + 2 * kw;
-    hipLaunchKernelGGL(prompt_qkv_rope_kernel, dim3((rows + 255) / 256, N), dim3(256), 0, st, y, rows, start, aw, kw,
+    NC_LAUNCH(prompt_qkv_rope_kernel, dim3((rows + 255) / 256, N), dim3(256), 0, st, y, rows, start, aw, kw,
                        hd, rope_half, rope_tab, q_out, kcache, vcache, max_ctx);
     NC_HIP(hipGetLastError());
     return NC_OK;
@@ -570,7 +570,7 @@ __global__ void prompt_residual_kernel(const float* y, float* hidden, int64_t to
 
 int launch_prompt_residual(const float* y, float* hidden, int N, int d, hipStream_t st) {
     const int64_t total = (int64_t)N * d;
-    hipLaunchKernelGGL(prompt_residual_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, y, hidden, total);
+    NC_LAUNCH(prompt_residual_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, y, hidden, total);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }
@@ -605,7 +605,7 @@ int launch_prompt_swiglu_q8(const float* y, int N, int F, int8_t* xq, float* xs,
                             bool split) {
     if (F % 32) return fail(NC_EINVAL, "prompt SwiGLU: width must be a multiple of 32");
     const int total = N * (F / 32);
-    hipLaunchKernelGGL(prompt_swiglu_q8_kernel, dim3((total * 32 + 255) / 256), dim3(256), 0, st, y, F, total, xq, xs,
+    NC_LAUNCH(prompt_swiglu_q8_kernel, dim3((total * 32 + 255) / 256), dim3(256), 0, st, y, F, total, xq, xs,
                        xs8, split ? 1 : 0);
     NC_HIP(hipGetLastError());
     return NC_OK;
@@ -619,7 +619,7 @@ __global__ void prompt_positions_kernel(int32_t* d, int start, int stride, int c
 
 int launch_prompt_positions(int32_t* d, int start, int stride, int count, hipStream_t st) {
     if (count < 1 || count > 256) return fail(NC_EINVAL, "prompt positions: 1..256 groups");
-    hipLaunchKernelGGL(prompt_positions_kernel, dim3(1), dim3(256), 0, st, d, start, stride, count);
+    NC_LAUNCH(prompt_positions_kernel, dim3(1), dim3(256), 0, st, d, start, stride, count);
     NC_HIP(hipGetLastError());
     return NC_OK;
 }

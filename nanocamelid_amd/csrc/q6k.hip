@@ -172,7 +172,7 @@ int launch_gemm_q6k(const QMatDev& w, const GemmParams& p0, hipStream_t st) {
     p.K = (int)w.cols;
     p.ntiles = (int)w.tiles;
     const dim3 grid((unsigned)w.tiles);
-#define NC_Q6K(NM) hipLaunchKernelGGL((gemm_q6_k_kernel<NM>), grid, dim3(256), 0, st, p, nb, rpw)
+#define NC_Q6K(NM) NC_LAUNCH((gemm_q6_k_kernel<NM>), grid, dim3(256), 0, st, p, nb, rpw)
     if (p.N <= 1) NC_Q6K(1);
     else if (p.N <= 4) NC_Q6K(4);
     else if (p.N <= 8) NC_Q6K(8);

@@ -94,8 +94,8 @@ struct nc_session {
     bool pending_toks = false;
     // per-stage timing (events between the pass's stages, named as the reference's trace stages)
     bool stage_timing = false;
-    std::vector<hipEvent_t> stage_ev;
-    std::vector<int> stage_of;  // stage id of each recorded mark, -1 for a pass's end mark
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> stage_ev;  // first kernel's start, last kernel's end
+    std::vector<int> stage_of;                                // stage id of each recorded pair
     size_t stage_used = 0;
     std::vector<double> stage_ms;
     std::vector<int64_t> stage_calls;
@@ -782,14 +782,15 @@ static const char* const kStageNames[] = {
 constexpr int kStages = (int)(sizeof(kStageNames) / sizeof(kStageNames[0]));
 enum Stage { ST_EMBED, ST_ATTN_NORM, ST_QKV, ST_ATTENTION, ST_WO, ST_FFN_NORM, ST_GATEUP, ST_DOWN, ST_HEAD_NORM, ST_HEAD };
 
-// Resolves the recorded marks: each mark's stage lasts until the next mark of its pass.
+thread_local hipEvent_t t_stage_ev0 = nullptr, t_stage_ev1 = nullptr;
+
+// Resolves the recorded stages: each pair spans the kernels of one stage (dispatch-stamped).
 static int flush_stages(nc_session* s) {
     if (s->stage_used == 0) return NC_OK;
     NC_HIP(hipStreamSynchronize(s->stream));
-    for (size_t i = 0; i + 1 < s->stage_used; i++) {
-        if (s->stage_of[i] < 0) continue;
+    for (size_t i = 0; i < s->stage_used; i++) {
         float ms = 0;
-        NC_HIP(hipEventElapsedTime(&ms, s->stage_ev[i], s->stage_ev[i + 1]));
+        NC_HIP(hipEventElapsedTime(&ms, s->stage_ev[i].first, s->stage_ev[i].second));
         s->stage_ms[s->stage_of[i]] += ms;
         s->stage_calls[s->stage_of[i]]++;
     }
@@ -797,19 +798,22 @@ static int flush_stages(nc_session* s) {
     return NC_OK;
 }
 
-// Records the start of `stage` (or, with stage = -1, the end of the pass) on the session stream.
-static int stage_mark(nc_session* s, int stage) {
-    if (!s->stage_timing) return NC_OK;
-    NC_HIP(hipEventRecord(s->stage_ev[s->stage_used], s->stream));
-    s->stage_of[s->stage_used++] = stage;
-    return NC_OK;
+// Ends the current stage and, for stage >= 0, starts the next: the kernels launched until the
+// next mark stamp its event pair (NC_LAUNCH).
+static void stage_mark(nc_session* s, int stage) {
+    t_stage_ev0 = t_stage_ev1 = nullptr;
+    if (!s->stage_timing || stage < 0) return;
+    const size_t i = s->stage_used++;
+    t_stage_ev0 = s->stage_ev[i].first;
+    t_stage_ev1 = s->stage_ev[i].second;
+    s->stage_of[i] = stage;
 }
 
-// Before a pass: room for its marks (the embedding, 7 per layer, 2 for the head and the end),
-// else resolve the recorded ones.
+// Before a pass: room for its stages (the embedding, 7 per layer, 2 for the head), else resolve
+// the recorded ones.
 static int stage_reserve(nc_session* s) {
     if (!s->stage_timing) return NC_OK;
-    const size_t need = 4 + 7 * (size_t)s->m->cfg.block_count;
+    const size_t need = 3 + 7 * (size_t)s->m->cfg.block_count;
     if (s->stage_used + need > s->stage_ev.size()) return flush_stages(s);
     return NC_OK;
 }
@@ -826,7 +830,11 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
     if (start_pos < 0 || start_pos + n > s->max_ctx) return fail(NC_ERANGE, "batch end exceeds the session context");
     hipStream_t st = s->stream;
     int rc = stage_reserve(s);
-    if (rc || (rc = stage_mark(s, ST_EMBED))) return rc;
+    if (rc) return rc;
+    struct StageEnd {  // no stage stays open past the pass, whatever path returns
+        ~StageEnd() { t_stage_ev0 = t_stage_ev1 = nullptr; }
+    } stage_end;
+    stage_mark(s, ST_EMBED);
     rc = launch_set_pass_state(s->d_pos, (int32_t)start_pos, s->d_toks, s->pending_toks ? s->staged : nullptr,
                                s->pending_toks ? s->n_staged : 0, st);
     if (rc) return rc;
@@ -836,10 +844,10 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
     const size_t layer_kv = (size_t)Hkv * s->ctx_stride * hd;
     for (int64_t li = 0; li < c.block_count; li++) {
         const LayerDev& L = m->layers[li];
-        if ((rc = stage_mark(s, ST_ATTN_NORM)) ||
-            (rc = launch_rmsnorm_q8(s->hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)) ||
-            (rc = stage_mark(s, ST_QKV)))
+        stage_mark(s, ST_ATTN_NORM);
+        if ((rc = launch_rmsnorm_q8(s->hidden, L.attn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
             return rc;
+        stage_mark(s, ST_QKV);
         GemmParams p;
         p.kernel = s->ctx->gemm_kernel;
         p.x = s->xq;
@@ -890,8 +898,9 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         a.part_o = s->attn_part_o;
         a.part_ml = s->attn_part_ml;
         a.nchunks = s->attn_chunks;
-        if ((rc = stage_mark(s, ST_ATTENTION)) || (rc = launch_attention(a, st)) || (rc = stage_mark(s, ST_WO)))
-            return rc;
+        stage_mark(s, ST_ATTENTION);
+        if ((rc = launch_attention(a, st))) return rc;
+        stage_mark(s, ST_WO);
         GemmParams po;
         po.kernel = s->ctx->gemm_kernel;
         po.x = s->xq;
@@ -901,10 +910,11 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         po.epi = EPI_RESIDUAL;
         po.out = s->hidden;
         po.ld_out = d;
-        if ((rc = residual_gemm(s, L.wo, po, n)) || (rc = stage_mark(s, ST_FFN_NORM)) ||
-            (rc = launch_rmsnorm_q8(s->hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)) ||
-            (rc = stage_mark(s, ST_GATEUP)))
+        if ((rc = residual_gemm(s, L.wo, po, n))) return rc;
+        stage_mark(s, ST_FFN_NORM);
+        if ((rc = launch_rmsnorm_q8(s->hidden, L.ffn_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
             return rc;
+        stage_mark(s, ST_GATEUP);
         GemmParams pg;
         pg.kernel = s->ctx->gemm_kernel;
         pg.x = s->xq;
@@ -935,15 +945,16 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         pd.epi = EPI_RESIDUAL;
         pd.out = s->hidden;
         pd.ld_out = d;
-        if ((rc = stage_mark(s, ST_DOWN)) || (rc = residual_gemm(s, L.down, pd, n))) return rc;
+        stage_mark(s, ST_DOWN);
+        if ((rc = residual_gemm(s, L.down, pd, n))) return rc;
     }
     s->last_n = head ? n : 0;
-    if (!head) return stage_mark(s, -1);  // a prompt chunk whose logits nobody reads (prefill_pass_batch)
+    if (!head) return NC_OK;  // a prompt chunk whose logits nobody reads (prefill_pass_batch)
     // compute_logits_from_hidden (inference.rs:4783-4832) for every row + argmax
-    if ((rc = stage_mark(s, ST_HEAD_NORM)) ||
-        (rc = launch_rmsnorm_q8(s->hidden, m->out_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)) ||
-        (rc = stage_mark(s, ST_HEAD)))
+    stage_mark(s, ST_HEAD_NORM);
+    if ((rc = launch_rmsnorm_q8(s->hidden, m->out_norm, n, d, c.rms_norm_epsilon, s->xq, s->xs, s->xs8, st)))
         return rc;
+    stage_mark(s, ST_HEAD);
     GemmParams ph;
     ph.kernel = s->ctx->gemm_kernel;
     ph.x = s->xq;
@@ -958,7 +969,7 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
     if ((rc = timed_gemm(s, m->head, ph))) return rc;
     if ((rc = launch_argmax_final(s->part_val, s->part_idx, n, (int)m->head.tiles, s->d_preds, st))) return rc;
     s->last_n = n;
-    return stage_mark(s, -1);
+    return NC_OK;
 }
 
 // Stages the next pass's tokens; run_pass writes them to the device together with the
@@ -1608,7 +1619,10 @@ void nc_session_free(nc_session* s) {
         (void)hipEventDestroy(e.first);
         (void)hipEventDestroy(e.second);
     }
-    for (auto e : s->stage_ev) (void)hipEventDestroy(e);
+    for (auto& e : s->stage_ev) {
+        (void)hipEventDestroy(e.first);
+        (void)hipEventDestroy(e.second);
+    }
     for (void* p : s->allocs) (void)hipFree(p);
     for (void* p : {(void*)s->h_toks, (void*)s->h_preds, (void*)s->h_result, (void*)s->h_pos})
         if (p) (void)hipHostFree(p);
@@ -2412,10 +2426,14 @@ int nc_session_timing_enable(nc_session* s, int32_t enable) {
     if (!s) return fail(NC_EINVAL, "null session");
     int rc = flush_timing(s);
     if (rc || (rc = flush_stages(s))) return rc;
+    if ((enable & 3) == 3) return fail(NC_EINVAL, "nc_session_timing_enable: matmul and stage timing are exclusive");
     if ((enable & 2) && s->stage_ev.empty()) {
         s->stage_ev.resize(4096);
         s->stage_of.resize(4096);
-        for (auto& e : s->stage_ev) NC_HIP(hipEventCreate(&e));
+        for (auto& e : s->stage_ev) {
+            NC_HIP(hipEventCreate(&e.first));
+            NC_HIP(hipEventCreate(&e.second));
+        }
     }
     s->stage_timing = (enable & 2) != 0;
     s->stage_ms.assign(kStages, 0.0);
