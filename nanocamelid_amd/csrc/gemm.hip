@@ -465,6 +465,14 @@ __device__ __forceinline__ void gemm_epilogue_r16(const GemmParams& p, float v, 
 // row cr) adds that round's BR terms [BR][NMAX][16] of LDS buffer r & 1 in block order
 // (inference.rs:1553-1573), so the sum is bit-identical to the reference's per-row loop.
 
+// LDS floats per tile of a tile group: the double-buffered terms [2][BR][NMAX][16], padded by 16
+// floats in four-tile groups so that a chain wave's four 16-lane rows (one per tile) read
+// disjoint LDS banks (unpadded, the tiles' buffers sit a multiple of 64 banks apart).
+template <int BR, int NMAX, int TPG>
+constexpr int r16_tile_lds() {
+    return 2 * BR * NMAX * 16 + (TPG > 1 ? 16 : 0);
+}
+
 // One round's chain step: adds the round's nblk terms of (token cn, row cr) in block order.
 template <int NMAX, int BR>
 __device__ __forceinline__ float r16_chain_step(const float* buf, int nblk, int cn, int cr, float acc) {
@@ -496,7 +504,7 @@ __device__ __forceinline__ void r16_chain_wave_tpg4(const GemmParams& p, const f
     for (int r = 0; r < nrounds; r++) {
         __syncthreads();  // round r's terms are in buffer r & 1 of every tile
         if (active)
-            acc = r16_chain_step<NMAX, BR>(lds_all + ((size_t)sub * 2 + (r & 1)) * BR * NMAX * 16,
+            acc = r16_chain_step<NMAX, BR>(lds_all + (size_t)sub * r16_tile_lds<BR, NMAX, 4>() + (r & 1) * BR * NMAX * 16,
                                            min(BR, nb - r * BR), cn, cr, acc);
     }
     if (active) {
@@ -612,7 +620,7 @@ __global__ __launch_bounds__(64 * (S * TPG + CW)) void gemm_q4_0_r16_kernel(Gemm
     const int sub = wave_all / S;            // tile of the group (TPG = 4)
     const int wave = wave_all % S;
     const int tile = blockIdx.x * TPG + sub;
-    float* lds = lds_all + (size_t)sub * 2 * BR * NMAX * 16;
+    float* lds = lds_all + (size_t)sub * r16_tile_lds<BR, NMAX, TPG>();
     const int tig = threadIdx.x - sub * 64 * S;  // thread index within the tile's group
     const int lane = threadIdx.x & 63;
     const int j = lane >> 4, i16 = lane & 15;
@@ -777,7 +785,7 @@ __global__ __launch_bounds__(64 * (S * TPG + CW)) void gemm_q4_0_mfma_kernel(Gem
     const int sub = wave_all / S;  // tile of the group (TPG = 4)
     const int wave = wave_all % S;
     const int tile = blockIdx.x * TPG + sub;
-    float* lds = lds_all + (size_t)sub * 2 * BR * NMAX * 16;
+    float* lds = lds_all + (size_t)sub * r16_tile_lds<BR, NMAX, TPG>();
     const int tig = threadIdx.x - sub * 64 * S;
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, c = lane & 15;
@@ -1183,7 +1191,7 @@ int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
                 hipExtLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0,
                                       ev1, 0, p);
             else
-                hipLaunchKernelGGL((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+                NC_LAUNCH((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
         }
     } else {
         constexpr int D = 2;  // one super-block ahead
@@ -1192,7 +1200,7 @@ int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
             hipExtLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0,
                                   p);
         else
-            hipLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+            NC_LAUNCH((gemm_q4_k_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
     }
     NC_HIP(hipGetLastError());
     return NC_OK;
@@ -1211,12 +1219,12 @@ int launch_r16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
         // with the chains on the first two waves of each tile
         constexpr int TPG = 4, CW = NMAX <= 8 ? NMAX : 0, S = CW ? 2 : 4;
         if (p.ntiles % TPG) return fail(NC_EINVAL, "gemm: SwiGLU rows must fill whole 64-row groups");
-        const size_t lds = (size_t)TPG * 2 * 4 * S * U * NMAX * 16 * sizeof(float);
+        const size_t lds = (size_t)TPG * r16_tile_lds<4 * S * U, NMAX, TPG>() * sizeof(float);
         if (ev0)
             hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, TPG, CW>), dim3(p.ntiles / TPG),
                                   dim3(64 * (S * TPG + CW)), lds, st, ev0, ev1, 0, p);
         else
-            hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, TPG, CW>), dim3(p.ntiles / TPG),
+            NC_LAUNCH((gemm_q4_0_r16_kernel<NMAX, S, U, D, TPG, CW>), dim3(p.ntiles / TPG),
                                dim3(64 * (S * TPG + CW)), lds, st, p);
     } else {
         // 8 waves (two per SIMD hide each other's dependency latency); 16 when K is long
@@ -1230,7 +1238,7 @@ int launch_r16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
                 hipExtLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1, CW>), dim3(p.ntiles),
                                       dim3(64 * (S + CW)), lds, st, ev0, ev1, 0, p);
             else
-                hipLaunchKernelGGL((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1, CW>), dim3(p.ntiles), dim3(64 * (S + CW)),
+                NC_LAUNCH((gemm_q4_0_r16_kernel<NMAX, S, U, D, 1, CW>), dim3(p.ntiles), dim3(64 * (S + CW)),
                                    lds, st, p);
         };
         if constexpr (NMAX <= 6) {
@@ -1256,12 +1264,12 @@ int launch_r16_mfma(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEv
         // chains run on the first waves of each tile
         constexpr int TPG = 4, CW = NMAX <= 8 ? NMAX : 0, S = CW ? 2 : 4;
         if (p.ntiles % TPG) return fail(NC_EINVAL, "gemm: SwiGLU rows must fill whole 64-row groups");
-        const size_t lds = (size_t)TPG * 2 * 4 * S * NMAX * 16 * sizeof(float);
+        const size_t lds = (size_t)TPG * r16_tile_lds<4 * S, NMAX, TPG>() * sizeof(float);
         if (ev0)
             hipExtLaunchKernelGGL((gemm_q4_0_mfma_kernel<NMAX, S, D, TPG, CW>), dim3(p.ntiles / TPG),
                                   dim3(64 * (S * TPG + CW)), lds, st, ev0, ev1, 0, p);
         else
-            hipLaunchKernelGGL((gemm_q4_0_mfma_kernel<NMAX, S, D, TPG, CW>), dim3(p.ntiles / TPG),
+            NC_LAUNCH((gemm_q4_0_mfma_kernel<NMAX, S, D, TPG, CW>), dim3(p.ntiles / TPG),
                                dim3(64 * (S * TPG + CW)), lds, st, p);
     } else {
         constexpr int CW = (16 * NMAX + 63) / 64;
@@ -1271,7 +1279,7 @@ int launch_r16_mfma(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEv
                 hipExtLaunchKernelGGL((gemm_q4_0_mfma_kernel<NMAX, S, D, 1, CW>), dim3(p.ntiles), dim3(64 * (S + CW)),
                                       lds, st, ev0, ev1, 0, p);
             else
-                hipLaunchKernelGGL((gemm_q4_0_mfma_kernel<NMAX, S, D, 1, CW>), dim3(p.ntiles), dim3(64 * (S + CW)),
+                NC_LAUNCH((gemm_q4_0_mfma_kernel<NMAX, S, D, 1, CW>), dim3(p.ntiles), dim3(64 * (S + CW)),
                                    lds, st, p);
         };
         if constexpr (NMAX <= 6) {
@@ -1322,7 +1330,7 @@ int launch_k16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
             hipExtLaunchKernelGGL((gemm_q4_k_r16_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0, ev1, 0,
                                   p);
         else
-            hipLaunchKernelGGL((gemm_q4_k_r16_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
+            NC_LAUNCH((gemm_q4_k_r16_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
     };
     if (p.epi == EPI_SWIGLU_Q8) return fail(NC_EINVAL, "gemm: the 16-row Q4_K layout has no SwiGLU epilogue");
     if (w.groups >= 8) go.template operator()<8>();
