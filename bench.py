@@ -39,6 +39,7 @@ REFERENCE_DEFAULT_THREADS = 4  # the reference's default worker count (src/main.
 # rocprofv3 FETCH_SIZE + WRITE_SIZE summary of the verify GEMMs on this workload (each counter
 # scaled by what it reads for a 256 MiB copy); the command that made it is in the file.
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_gemm_llama3-8b_q4_0_k4_pmc_traffic.md")
+TRAFFIC_PROFILE_C4 = os.path.join(ROOT, "profiles", "config4_verify_gemm_llama3-70b_q4_0_pmc_traffic.md")
 
 
 def log(msg):
@@ -128,15 +129,21 @@ def cpu_baseline(img, cfg, args, tok_per_step, gpu_stream, stream_prompt):
             "stream_vs_gpu": identity}
 
 
-def measured_traffic(args):
-    """HBM bytes per verify-GEMM launch from the committed counter summary, or None when
-    the summary is absent or was taken on another workload."""
-    if args.config != "llama-3-8b" or args.k != 4 or not os.path.exists(TRAFFIC_PROFILE):
+def _traffic_from(path):
+    if not os.path.exists(path):
         return None
-    for line in open(TRAFFIC_PROFILE):
+    for line in open(path):
         if line.startswith("traffic_bytes_per_launch:"):
             return int(line.split(":")[1])
     return None
+
+
+def measured_traffic(args):
+    """HBM bytes per verify-GEMM launch from the committed counter summary, or None when
+    the summary is absent or was taken on another workload."""
+    if args.config != "llama-3-8b" or args.k != 4:
+        return None
+    return _traffic_from(TRAFFIC_PROFILE)
 
 
 def _q4_0_random_blocks(M, K, seed):
@@ -477,6 +484,13 @@ def run_config4(args):
     log(f"verify pass: {dt * 1e3:.2f} ms ({(cfg['verify_weight_bytes'] + kv_bytes) / dt / 1e9:.0f} GB/s incl. KV); "
         f"matmuls {gemm_ms / reps:.2f} ms -> {achieved:.0f} GB/s")
     gpu_logits = [sess.logits(i) for i in range(n)]
+    if args.copy_calibration:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 256 MiB device-to-device copies")
     cpu, parity = None, None
     if not args.no_cpu_baseline:
         from oracle import oracle as O
@@ -512,7 +526,7 @@ def run_config4(args):
                    "kv_bytes_read": int(kv_bytes), "greedy_drafts_all_accepted": consistent,
                    "kv_fill_s": round(fill_s, 2), "oracle_parity": parity},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": _traffic_from(TRAFFIC_PROFILE_C4),
                      "kernel": "gemm_q4_0_kernel / gemm_q4_0_r16_kernel (all verify matmuls)",
                      "launches": int(launches), "avg_us": round(gemm_ms / max(launches, 1) * 1e3, 3),
                      "avg_algorithmic_bytes": int(gemm_bytes // max(launches, 1))},
