@@ -132,6 +132,11 @@ int nc_matmul_blockdots(nc_ctx* ctx, const nc_qmat* w, const int8_t* x_i8, int32
  * what the reference's f32::exp calls in softmax (src/inference.rs:3522-3540) and SiLU
  * (src/inference.rs:3367-3390); this entry point lets a test compare the two on every input. */
 int nc_debug_expf(nc_ctx* ctx, uint32_t first_bits, int64_t count, float* out, void* stream);
+/* Debug hook: after nc_temperature_probs_batch or nc_sample_logits_batch on this context (and on
+ * this stream), fast[r] (host) = 1 if row r's exact left-to-right sum came from the evaluation
+ * that runs the vocabulary's segments in parallel, 0 if from the segment-after-segment one (a
+ * row whose checks failed, or a vocabulary above 262144).  Synchronises the stream. */
+int nc_debug_temperature_paths(nc_ctx* ctx, int32_t rows, int32_t* fast, void* stream);
 /* Per-32-block Q8_0 activation quantiser: scale = amax/127 (f32), q = round-half-away
  * (x * (1/scale)) clamped to +-127.  Replaces quantize_f32_to_q8_0_batch
  * (src/inference.rs:967-989, scalar path :991-1029).  Device pointers. */
@@ -174,7 +179,9 @@ int nc_temperature_probs_batch(nc_ctx* ctx, const float* logits, float* probs, i
 /* k+1 acceptance over device buffers: p_probs [k+1][vocab] target probabilities of the rows
  * at start_pos .. start_pos+k, q_probs [k][vocab] draft probabilities, drafts [k] ids.
  * result (device, 3 x int32) = {n_accepted, next_token, start_pos + n_accepted + 1}.
- * k 0..15; a draft id >= vocab counts as rejected. */
+ * k 0..15; a draft id >= vocab counts as rejected.  nc_sample_logits_batch,
+ * nc_temperature_probs_batch and nc_stochastic_accept use the context's device scratch: calls
+ * on one context are ordered on their stream, and calls on different streams must not overlap. */
 int nc_stochastic_accept(nc_ctx* ctx, const float* p_probs, const float* q_probs, const uint32_t* drafts, int32_t k,
                          int64_t vocab, uint64_t seed, int64_t start_pos, int32_t* result, void* stream);
 

@@ -208,6 +208,15 @@ def temperature_probs_batch(ctx: Context, logits, temp: float, out=None):
     return out
 
 
+def temperature_paths(ctx: Context, rows: int, stream=None):
+    """Debug: for each of the last temperature pass's rows on this context, 1 if its exact sum
+    came from the parallel-segment evaluation, 0 if from the segment-after-segment one."""
+    import numpy as np
+    out = np.zeros(rows, np.int32)
+    check(lib().nc_debug_temperature_paths(ctx.h, rows, out.ctypes.data, stream))
+    return out
+
+
 # The reference's initial rand_simple state (src/inference.rs:4875).
 REFERENCE_RNG_STATE = 0x123456789ABCDEF0
 

@@ -76,6 +76,7 @@ SIGNATURES = {
     "nc_matmul_quantized_batch_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _vp]),
     "nc_matmul_blockdots": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _vp]),
     "nc_debug_expf": (C.c_int, [_vp, C.c_uint32, _i64, _vp, _vp]),
+    "nc_debug_temperature_paths": (C.c_int, [_vp, C.c_int32, _vp, _vp]),
     "nc_quantize_q8_0_batch": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _vp]),
     "nc_rms_norm_q8_0_batch": (C.c_int, [_vp, _vp, _vp, C.c_float, _vp, _vp, C.c_int, _i64, _vp]),
     "nc_bench_matmul": (C.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _vp]),

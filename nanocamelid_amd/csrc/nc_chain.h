@@ -175,6 +175,86 @@ __device__ __forceinline__ double block_excl_scan_f64_i32(double v, int k, doubl
 
 constexpr int kChainMargin = 256;  // ulps between a guess and the true state that are tolerated
 
+// Step 2 for one thread: its E terms added in order from the guess g; x receives the end
+// value.  Returns whether moving the run to the true start might not translate it exactly:
+// the guess or the end lies within kChainMargin ulps of a binade edge, the run leaves the
+// guess's binade, a step rounds an exact tie, or the binade is too small for the test.
+// s0_neg: the chain started below zero, so a zero guess is a cancellation, not an exact start.
+template <int E>
+__device__ __forceinline__ bool chain_run_sensitive(const float (&a)[E], float g, bool s0_neg, float& x_out) {
+    const uint32_t bg = __float_as_uint(g);
+    const int eg = (int)(bg >> 23);  // sign and exponent: the binade test below includes the sign
+    const int ea = eg & 0xff;
+    // half an ulp of g's binade, 2^(ea - 151); only used when ea >= 25 (else sensitive anyway)
+    const float half = __uint_as_float((uint32_t)(ea > 25 ? ea - 24 : 1) << 23);
+    float x = g;
+    bool tie = false;
+#pragma unroll
+    for (int j = 0; j < E; j++) {
+        const float r = x + a[j];
+        // Fast2Sum error of the step (exact while x >= a[j], i.e. whenever the binade holds)
+        tie |= __builtin_fabsf(a[j] - (r - x)) == half;
+        x = r;
+    }
+    x_out = x;
+    const uint32_t bx = __float_as_uint(x);
+    const int mg = (int)(bg & 0x7fffff), mx = (int)(bx & 0x7fffff);
+    // Absorbed runs translate exactly from any start: all-zero terms, or (binade >= 2^-100)
+    // every term below a quarter ulp of g's binade, which is below half an ulp of any start
+    // within the margin (that start's binade is g's or a neighbour, whose ulp is at least
+    // half of g's), so every step rounds back to its start.
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < E; j++) amax = fmaxf(amax, a[j]);
+    const bool absorbed = (amax == 0.0f) | ((ea >= 27) & (amax < 0.5f * half));
+    // g == 0 with s0 >= 0: every earlier term and s0 are 0, so the start is exact and the run
+    // is the truth
+    return !absorbed & ((bg != 0) | s0_neg) &
+           ((ea < 25) | ((int)(bx >> 23) != eg) | (mg < kChainMargin) | (mx + kChainMargin >= (1 << 23)) | tie);
+}
+
+// The walk's serial part, run by one lane: adds rows[0 .. cnt) in order to S (a row holds the
+// advance over the insensitive runs before its entry, then the entry's E terms) and records
+// the value after each row in walk_end[q].  Three register sets rotate, so entry q's row is
+// read from LDS two entries ahead and only the dependent adds are serial.
+template <int E>
+__device__ __forceinline__ float chain_walk_rows(const WalkRow<E>* rows, int cnt, float S, float* walk_end) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    constexpr int W = WalkRow<E>::W;
+    f4v r0[W / 4], r1[W / 4], r2[W / 4];
+#define NC_WALK_READ(R, Q)                                                                          \
+    {                                                                                               \
+        const int q_ = min((Q), cnt - 1);                                                           \
+        _Pragma("unroll") for (int c = 0; c < W / 4; c++) R[c] = *(const f4v*)&rows[q_].v[4 * c];  \
+    }
+#define NC_WALK_ADD(R, Q)                                                                           \
+    {                                                                                               \
+        _Pragma("unroll") for (int c = 0; c < W / 4; c++) {                                        \
+            if (4 * c + 0 <= E) S = S + R[c].x;                                                     \
+            if (4 * c + 1 <= E) S = S + R[c].y;                                                     \
+            if (4 * c + 2 <= E) S = S + R[c].z;                                                     \
+            if (4 * c + 3 <= E) S = S + R[c].w;                                                     \
+        }                                                                                           \
+        walk_end[(Q)] = S;                                                                          \
+    }
+    // (the padding after the E terms is never added)
+    NC_WALK_READ(r0, 0)
+    NC_WALK_READ(r1, 1)
+    for (int q = 0; q < cnt; q += 3) {
+        NC_WALK_READ(r2, q + 2)
+        NC_WALK_ADD(r0, q)
+        if (q + 1 >= cnt) break;
+        NC_WALK_READ(r0, q + 3)
+        NC_WALK_ADD(r1, q + 1)
+        if (q + 2 >= cnt) break;
+        NC_WALK_READ(r1, q + 4)
+        NC_WALK_ADD(r2, q + 2)
+    }
+#undef NC_WALK_ADD
+#undef NC_WALK_READ
+    return S;
+}
+
 // Thread t holds terms a[0..E) = a_{tE} .. a_{tE+E-1} (n = T*E terms; pad with zeros, which
 // leave the chain unchanged).  The chain starts from s_{-1} = s0, so a long sum can be
 // evaluated as consecutive segments, each starting from the previous segment's result.  A
@@ -197,26 +277,8 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
     const float g = (float)exclp;  // segment 0: exactly s0
 
     // 2. the segment evaluated from the guess, with the tie and binade tests
-    const uint32_t bg = __float_as_uint(g);
-    const int eg = (int)(bg >> 23);  // sign and exponent: the binade test below includes the sign
-    const int ea = eg & 0xff;
-    // half an ulp of g's binade, 2^(ea - 151); only used when ea >= 25 (else sensitive anyway)
-    const float half = __uint_as_float((uint32_t)(ea > 25 ? ea - 24 : 1) << 23);
-    float x = g;
-    bool tie = false;
-#pragma unroll
-    for (int j = 0; j < E; j++) {
-        const float r = x + a[j];
-        // Fast2Sum error of the step (exact while x >= a[j], i.e. whenever the binade holds)
-        tie |= __builtin_fabsf(a[j] - (r - x)) == half;
-        x = r;
-    }
-    const uint32_t bx = __float_as_uint(x);
-    const int mg = (int)(bg & 0x7fffff), mx = (int)(bx & 0x7fffff);
-    // g == 0 with s0 >= 0: every earlier term and s0 are 0, so the start is exact and the run
-    // is the truth (with a negative s0 a zero guess is a cancellation, not an exact start)
-    const bool sens = ((bg != 0) | (s0 < 0.0f)) & ((ea < 25) | ((int)(bx >> 23) != eg) | (mg < kChainMargin) |
-                                                   (mx + kChainMargin >= (1 << 23)) | tie);
+    float x;
+    const bool sens = chain_run_sensitive<E>(a, g, s0 < 0.0f, x);
     const double d = (double)x - (double)g;
 
     // 3. uncorrected starts C_t, with the sensitive count scanned in the same pass
@@ -241,7 +303,6 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
         // it, which is exact, and its E terms) as one LDS row; lane 0 then walks the rows in
         // order with 16-byte reads issued two entries ahead, so only the dependent adds are
         // serial.
-        typedef float f4v __attribute__((ext_vector_type(4)));
         constexpr int W = WalkRow<E>::W;
         __shared__ WalkRow<E> rows[64];
         float S = s0;  // true chain value at the end of the last walked segment (lane 0)
@@ -260,41 +321,8 @@ __device__ float exact_chain_sum(const float (&a)[E], ChainScratch<T>& sc, float
 #pragma unroll
                 for (int j = E + 1; j < W; j++) rows[t].v[j] = 0.0f;
             }
-            if (t == 0) {
-                // rows of this wave's lanes: LDS operations of one wave complete in order.  Three
-                // register sets rotate (unrolled by 3): entry q's row is read two entries ahead.
-                f4v r0[W / 4], r1[W / 4], r2[W / 4];
-#define NC_WALK_READ(R, Q)                                                                          \
-    {                                                                                               \
-        const int q_ = min((Q), cnt - 1);                                                           \
-        _Pragma("unroll") for (int c = 0; c < W / 4; c++) R[c] = *(const f4v*)&rows[q_].v[4 * c];  \
-    }
-#define NC_WALK_ADD(R, Q)                                                                           \
-    {                                                                                               \
-        _Pragma("unroll") for (int c = 0; c < W / 4; c++) {                                        \
-            if (4 * c + 0 <= E) S = S + R[c].x;                                                     \
-            if (4 * c + 1 <= E) S = S + R[c].y;                                                     \
-            if (4 * c + 2 <= E) S = S + R[c].z;                                                     \
-            if (4 * c + 3 <= E) S = S + R[c].w;                                                     \
-        }                                                                                           \
-        sc.walk_end[(Q)] = S;                                                                       \
-    }
-                // (the padding after the E terms is never added)
-                NC_WALK_READ(r0, 0)
-                NC_WALK_READ(r1, 1)
-                for (int q = 0; q < cnt; q += 3) {
-                    NC_WALK_READ(r2, q + 2)
-                    NC_WALK_ADD(r0, q)
-                    if (q + 1 >= cnt) break;
-                    NC_WALK_READ(r0, q + 3)
-                    NC_WALK_ADD(r1, q + 1)
-                    if (q + 2 >= cnt) break;
-                    NC_WALK_READ(r1, q + 4)
-                    NC_WALK_ADD(r2, q + 2)
-                }
-#undef NC_WALK_ADD
-#undef NC_WALK_READ
-            }
+            // rows of this wave's lanes: LDS operations of one wave complete in order
+            if (t == 0) S = chain_walk_rows<E>(rows, cnt, S, sc.walk_end);
             if (me < total_s) sc.ent[me].shift = (double)sc.walk_end[t] - ce;
         }
     }

@@ -200,7 +200,8 @@ int launch_accept_greedy(const uint32_t* toks, const uint32_t* preds, int n, int
 // ---------------------------------------------------------------- stochastic acceptance
 // probs[r][j] = expf((l_j - max)/temp) * (1 / sum), the sum exact left to right (rows x V).
 // Temperature probabilities of `rows` rows; scratch: temperature_scratch_floats(rows) floats of
-// device memory owned by the caller (stream-ordered reuse).
+// device memory owned by the caller (stream-ordered reuse), 256-byte aligned; the samplers below
+// use its first part, so a sample may follow the probabilities it reads on the same stream.
 size_t temperature_scratch_floats(int rows);
 // sample_logits (inference.rs:4834-4873) of `rows` rows (<= kSampleMaxRows): temp > 0 draws row r
 // with the uniform u[r] (the reference's inverse-CDF walk, bit-exact); temp <= 0 takes the first
@@ -213,13 +214,16 @@ int launch_sample_logits(const float* logits, int64_t ld_in, int rows, int V, fl
                          int64_t ld_p, float* scratch, uint32_t* out, hipStream_t stream);
 int launch_temperature_probs(const float* logits, int64_t ld_in, float* probs, int64_t ld_out, int rows, int V,
                              float temp, float* scratch, hipStream_t st);
+// fast[r] (host) = which evaluation gave row r's sum in the last temperature pass on scratch.
+int temperature_row_paths(const float* scratch, int rows, int32_t* fast, hipStream_t st);
 // p [k+1][ld] target probs, q [k][ld] draft probs, drafts[k] (device); result = {n_accepted,
 // next_token, start_pos + n_accepted + 1}; d_pos (nullable) receives the new position.
 int launch_accept_stochastic(const float* p, const float* q, int64_t ld, const uint32_t* drafts, int k, int V,
-                             uint64_t seed, int64_t start_pos, int32_t* result, int32_t* d_pos, hipStream_t st);
+                             uint64_t seed, int64_t start_pos, int32_t* result, int32_t* d_pos, float* scratch,
+                             hipStream_t st);
 // One fixed-point inverse-CDF sample of probs[V] with the Philox uniform (seed, pos, purpose).
 int launch_sample_probs(const float* probs, int V, uint64_t seed, int64_t pos, uint32_t purpose, uint32_t* out0,
-                        uint32_t* out1, hipStream_t st);
+                        uint32_t* out1, float* scratch, hipStream_t st);
 
 // Address of the allocation-free entry point's scratch array on the current device
 // (hipGetSymbolAddress of a file-scope __device__ array; each device has its own copy).

@@ -1235,7 +1235,7 @@ static int accept_stochastic_step(nc_session* s, int n, int64_t start_pos, const
     int rc = launch_temperature_probs(s->logits, V, s->probs, V, n, V, temp, s->tp_scratch, s->stream);
     if (rc) return rc;
     return launch_accept_stochastic(s->probs, q, V, s->d_toks + 1, n - 1, V, seed, start_pos, s->d_result, s->d_pos,
-                                    s->stream);
+                                    s->tp_scratch, s->stream);
 }
 
 static int fetch_result(nc_session* s, int n_toks, nc_verify_result* r, uint32_t* toks_out) {
@@ -1475,6 +1475,13 @@ int nc_debug_expf(nc_ctx* ctx, uint32_t first_bits, int64_t count, float* out, v
     return launch_expf_range(first_bits, count, out, stream ? (hipStream_t)stream : ctx->stream);
 }
 
+int nc_debug_temperature_paths(nc_ctx* ctx, int32_t rows, int32_t* fast, void* stream) {
+    if (!ctx || !fast || rows < 1 || temperature_scratch_floats(rows) > ctx->tp_cap)
+        return fail(NC_EINVAL, "nc_debug_temperature_paths: bad arguments");
+    NC_HIP(hipSetDevice(ctx->device));
+    return temperature_row_paths(ctx->tp_scratch, rows, fast, stream ? (hipStream_t)stream : ctx->stream);
+}
+
 int nc_quantize_q8_0_batch(nc_ctx* ctx, const float* x, int8_t* x_i8, float* x_scales, int batch_size, int64_t dim,
                            void* stream) {
     if (!ctx || !x || !x_i8 || !x_scales || dim % 32) return fail(NC_EINVAL, "nc_quantize_q8_0_batch: bad arguments");
@@ -1519,7 +1526,7 @@ int nc_stochastic_accept(nc_ctx* ctx, const float* p_probs, const float* q_probs
         return fail(NC_EINVAL, "nc_stochastic_accept: bad arguments");
     NC_HIP(hipSetDevice(ctx->device));
     return launch_accept_stochastic(p_probs, q_probs, vocab, drafts, k, (int)vocab, seed, start_pos, result, nullptr,
-                                    stream ? (hipStream_t)stream : ctx->stream);
+                                    ctx->tp_scratch, stream ? (hipStream_t)stream : ctx->stream);
 }
 
 int nc_model_load_gguf_memory(nc_ctx* ctx, const void* data, size_t size, const nc_load_opts* opts, nc_model** out) {
@@ -2285,7 +2292,7 @@ int nc_generate_speculative_stochastic(nc_session* tg, nc_session* dr, const uin
     if ((rc = launch_temperature_probs(tg->logits + (size_t)(tg->last_n - 1) * V, V, tg->probs, V, 1, V, temp,
                                        tg->tp_scratch, st)) ||
         (rc = launch_sample_probs(tg->probs, V, seed, n_prompt - 1, kPurposeBonus, (uint32_t*)(tg->d_result + 1),
-                                         nullptr, st)))
+                                  nullptr, tg->tp_scratch, st)))
         return rc;
     NC_HIP(hipMemcpyAsync(tg->h_result, tg->d_result, 4 * sizeof(int32_t), hipMemcpyDeviceToHost, st));
     NC_HIP(hipStreamSynchronize(st));
@@ -2313,7 +2320,7 @@ int nc_generate_speculative_stochastic(nc_session* tg, nc_session* dr, const uin
                 (rc = launch_temperature_probs(dr->logits, V, tg->qbuf + (size_t)i * V, V, 1, V, temp,
                                                tg->tp_scratch, st)) ||
                 (rc = launch_sample_probs(tg->qbuf + (size_t)i * V, V, seed, pos + i, kPurposeDraft, tg->d_toks + 1 + i,
-                                          dr->d_toks, st)))
+                                          dr->d_toks, tg->tp_scratch, st)))
                 return rc;
         }
         // target verify of [pending, d_0 .. d_{kk-1}]: only row 0 comes from the host

@@ -35,10 +35,15 @@ def _rows(V, rng):
         "ties": np.round(rng.normal(0, 1, V) * 4) / 4,     # many equal logits
         "ramp": np.linspace(-20, 5, V),
     }
+    if V >= 16384:
+        # ~e^-80 terms first: the partial sums stay below 2^-102 for thousands of terms, where
+        # every run is sensitive; a parallel segment lists at most 256 of them, so the row takes
+        # the segment-after-segment evaluation
+        rows["tiny_prefix"] = np.concatenate([rng.normal(-80, 0.5, 12000), rng.normal(0, 1, V - 12000)])
     return {k: v.astype(np.float32) for k, v in rows.items()}
 
 
-@pytest.mark.parametrize("V", [7, 1000, 16384, 128256])
+@pytest.mark.parametrize("V", [7, 1000, 16384, 128256, 300000])
 @pytest.mark.parametrize("temp", [1.0, 0.7, 2.5])
 def test_temperature_probs_bit_exact(ctx, V, temp):
     import nanocamelid_amd as nc
@@ -46,10 +51,18 @@ def test_temperature_probs_bit_exact(ctx, V, temp):
     names = list(rows)
     x = np.stack([rows[k] for k in names])
     print(f"temperature probs V={V} T={temp}", flush=True)
-    got = nc.temperature_probs_batch(ctx, torch.from_numpy(x).cuda(), temp).cpu().numpy()
+    got = nc.temperature_probs_batch(ctx, torch.from_numpy(x).cuda(), temp)
+    paths = dict(zip(names, nc.temperature_paths(ctx, len(names), torch.cuda.current_stream().cuda_stream)))
+    got = got.cpu().numpy()
     for r, name in enumerate(names):
         ref = O.temperature_probs(x[r], temp)
         assert np.array_equal(got[r].view(np.uint32), ref.view(np.uint32)), f"{name} V={V} T={temp}"
+    # which evaluation gave each sum: segments in parallel up to 262144 terms; the tiny prefix
+    # (at T = 1, where its terms stay near e^-80) forces the sequential one
+    for name in ("normal", "flat", "peaked", "ramp"):
+        assert paths[name] == (1 if V <= 262144 else 0), (name, V, temp)
+    if "tiny_prefix" in paths and temp == 1.0:
+        assert paths["tiny_prefix"] == 0
 
 
 def _accept_case(ctx, p_logits, q, drafts, temp, seed, start):
