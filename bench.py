@@ -421,7 +421,7 @@ def run_config3(args):
                    "draft_weight_bytes": int(dm.config["verify_weight_bytes"])},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "target verify matmuls (gemm_q4_k_kernel layers + gemm_q4_0_kernel head)",
+                     "kernel": "target verify matmuls (gemm_q4_k_r16_kernel q,k,v, wo, down + gemm_q4_k_ps_kernel gate,up + gemm_q4_0_kernel head)",
                      "launches": int(launches), "avg_us": round(gemm_ms / max(launches, 1) * 1e3, 3),
                      "avg_algorithmic_bytes": int(gemm_bytes // max(launches, 1))},
         "cpu_baseline": cpu,

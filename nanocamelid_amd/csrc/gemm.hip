@@ -1123,6 +1123,178 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_k_r16_kernel(GemmParams p) {
     if (threadIdx.x < 16 * NMAX && cn < N) gemm_epilogue_r16<NMAX>(p, acc, cn, tile, cr);
 }
 
+// ---------------------------------------------------------------- Q4_K, 16-row tiles, pair-split
+// The R16K layout with the work of a super-block quad split over four waves, one per pair of
+// sub-blocks, so that four 16-row tiles (the interleaved gate,up's 64-row group, whose SwiGLU
+// epilogue needs all four) fit one workgroup of 16 waves.  Workgroup = TPG 16-row tiles x QL
+// quad lanes x 4 pair waves; in round
+// r, wave (tile tt, quad lane ql, pair pr) takes quad r*QL + ql of tile tt: slot 0 (d, dmin and
+// the packed scales) and the pair's two nibble slots, one activation dword per token (the pair's
+// 64 int8 values of the lane's super-block, broadcast by DPP rows) and the meta dword.  It
+// computes the two sub-block values xs_j * (sc_j*W_j - mn_j*A_j) (q8.rs:1372-1375) of every
+// token and stores them in LDS as [tile][super-block][sub-block][token][row].  After a barrier
+// the super-block sums 0 + v_0 + ... + v_7 are taken in sub-block order (one thread per tile,
+// super-block, token and row), and after a second barrier the chain threads add them in
+// super-block order: the same f32 operations in the same order as the one-wave-per-quad kernel.
+// TPG = 4: the interleaved gate,up matrix (32 gate rows and their 32 up rows per four tiles);
+// the SwiGLU + Q8_0 epilogue finishes the group's 32 outputs.  Two barriers per round make one
+// buffer enough: round r+1 writes values only after every thread passed round r's second
+// barrier, which follows the last read of round r's values.
+template <int NMAX, int QL, int TPG>
+constexpr int kps_sbl() { return 4 * QL; }  // super-blocks per tile per round
+template <int NMAX, int QL, int TPG>
+constexpr int kps_lds_floats() {
+    return TPG * kps_sbl<NMAX, QL, TPG>() * 8 * NMAX * 16 + TPG * kps_sbl<NMAX, QL, TPG>() * NMAX * 16;
+}
+
+template <int NMAX, int QL, int TPG, int PR>
+__device__ __forceinline__ void gemm_q4_k_ps_body(const GemmParams& p, float* lds) {
+    constexpr int SBL = kps_sbl<NMAX, QL, TPG>();
+    constexpr int NT = 256 * QL * TPG;  // threads per workgroup
+    constexpr int jl = 2 * PR, jh = 2 * PR + 1;
+    float* vals = lds;                                // [TPG][SBL][8][NMAX][16]
+    float* parts = lds + TPG * SBL * 8 * NMAX * 16;   // [TPG][SBL][NMAX][16]
+    const int w = wave_id_uniform();
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 4, j = lane & 15;
+    const int ql = (w >> 2) % QL, tt = w / (4 * QL);
+    const int tile = blockIdx.x * TPG + tt;
+    const int N = p.N, nsb = p.units, nb = nsb * 8;
+    const int nquads = p.groups;
+    const int nrounds = (nquads + QL - 1) / QL;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.w + (size_t)tile * p.groups * kQ4KChunkBytes), 0, p.groups * kQ4KChunkBytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, 0, N * p.K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs, 0, N * nb * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t s8res = __builtin_amdgcn_make_buffer_rsrc((void*)p.xs8, 0, N * nb * 4, 0x00020000);
+    const int wvo = lane * 16;
+    const int xvo = q * 256 + j * 4 + PR * 64;  // + n*K + quad*1024
+    const int mvo = q * 32 + (j & 7) * 4;       // + n*nb*4 + quad*128
+    const bool meta_s = j < 8;
+    constexpr int D = 2;  // ring of rounds in flight
+    uint4 rs[D], r0[D], r1[D];
+    int ax[D][NMAX], am[D][NMAX];
+#define NC_KPS_LOAD(R, SLOT)                                                                               \
+    do {                                                                                                   \
+        const int g_ = min((R) * QL + ql, p.groups - 1);                                                   \
+        rs[SLOT] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wvo, g_ * kQ4KChunkBytes, 0)); \
+        r0[SLOT] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(                        \
+                                                 wres, wvo, g_ * kQ4KChunkBytes + (1 + 2 * PR) * 1024, 0));  \
+        r1[SLOT] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(                        \
+                                                 wres, wvo, g_ * kQ4KChunkBytes + (2 + 2 * PR) * 1024, 0));  \
+        _Pragma("unroll") for (int n = 0; n < NMAX; n++) {                                                 \
+            ax[SLOT][n] = (int)__builtin_amdgcn_raw_buffer_load_b32(xres, xvo + n * p.K + g_ * 1024, 0, 0); \
+            const int mo_ = mvo + n * nb * 4 + g_ * 128;                                                   \
+            const int ms_ = (int)__builtin_amdgcn_raw_buffer_load_b32(sres, mo_, 0, 0);                    \
+            const int m8_ = (int)__builtin_amdgcn_raw_buffer_load_b32(s8res, mo_, 0, 0);                   \
+            am[SLOT][n] = meta_s ? ms_ : m8_;                                                              \
+        }                                                                                                  \
+    } while (0)
+    NC_KPS_LOAD(0, 0);
+    // chain thread c: TPG = 1 token c / 16, row c % 16; TPG = 4 token c / 64 (one wave per
+    // token, as the SwiGLU epilogue wants), tile (c % 64) / 16, row c % 16
+    const int c = threadIdx.x;
+    const int cn = TPG == 1 ? c >> 4 : c >> 6;
+    const int ct = TPG == 1 ? 0 : (c & 63) >> 4;
+    const int cr = c & 15;
+    const bool chain = c < TPG * NMAX * 16 && cn < N;
+    float acc = 0.0f;
+    for (int r0i = 0; r0i < nrounds; r0i += D) {
+#pragma unroll
+        for (int k = 0; k < D; k++) {
+            const int r = r0i + k;
+            if (r >= nrounds) break;  // uniform
+            NC_KPS_LOAD(min(r + 1, nrounds - 1), (k + 1) % D);
+            const int g = r * QL + ql;
+            if (g < nquads) {  // uniform per wave
+                const uint4 v = rs[k];
+                const float d = f16_to_f32((uint16_t)(v.x & 0xffff));
+                const float dmin = f16_to_f32((uint16_t)(v.x >> 16));
+                // q8.rs:2008-2018 q4_k_scale_min for sub-blocks jl and jh
+                uint32_t sl, ml, sh, mh;
+                if constexpr (jl < 4) {
+                    sl = kbyte(v.y, v.z, v.w, jl) & 63;
+                    ml = kbyte(v.y, v.z, v.w, jl + 4) & 63;
+                    sh = kbyte(v.y, v.z, v.w, jh) & 63;
+                    mh = kbyte(v.y, v.z, v.w, jh + 4) & 63;
+                } else {
+                    sl = (kbyte(v.y, v.z, v.w, jl + 4) & 0x0f) | ((kbyte(v.y, v.z, v.w, jl - 4) >> 6) << 4);
+                    ml = (kbyte(v.y, v.z, v.w, jl + 4) >> 4) | ((kbyte(v.y, v.z, v.w, jl) >> 6) << 4);
+                    sh = (kbyte(v.y, v.z, v.w, jh + 4) & 0x0f) | ((kbyte(v.y, v.z, v.w, jh - 4) >> 6) << 4);
+                    mh = (kbyte(v.y, v.z, v.w, jh + 4) >> 4) | ((kbyte(v.y, v.z, v.w, jh) >> 6) << 4);
+                }
+                const float scl = d * (float)sl, mnl = dmin * (float)ml;
+                const float sch = d * (float)sh, mnh = dmin * (float)mh;
+                const uint32_t qw[8] = {r0[k].x, r0[k].y, r0[k].z, r0[k].w, r1[k].x, r1[k].y, r1[k].z, r1[k].w};
+                int lo[8], hi[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    lo[i] = (int)(qw[i] & 0x0F0F0F0Fu);
+                    hi[i] = (int)((qw[i] >> 4) & 0x0F0F0F0Fu);
+                }
+                float* vb = vals + ((size_t)(tt * SBL + ql * 4 + q) * 8) * NMAX * 16 + j;
+                [&]<int... Ns>(std::integer_sequence<int, Ns...>) {
+                    (([&] {
+                         constexpr int n = Ns;
+                         const int wl = dot32_bcast<0>(0, ax[k][n], lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6],
+                                                       lo[7]);
+                         const int wh = dot32_bcast<8>(0, ax[k][n], hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6],
+                                                       hi[7]);
+                         const float xl = bcast_f<jl>(__int_as_float(am[k][n]));
+                         const float xh = bcast_f<jh>(__int_as_float(am[k][n]));
+                         const int al = bcast_i<8 + jl>(am[k][n]) / -8;  // A_j = sum of x
+                         const int ah = bcast_i<8 + jh>(am[k][n]) / -8;
+                         vb[(jl * NMAX + n) * 16] = xl * (scl * (float)wl - mnl * (float)al);
+                         vb[(jh * NMAX + n) * 16] = xh * (sch * (float)wh - mnh * (float)ah);
+                     }()),
+                     ...);
+                }(std::make_integer_sequence<int, NMAX>{});
+            }
+            __syncthreads();
+            // super-block sums in sub-block order, starting from 0 as the reference's per-
+            // super-block loop does
+            const int sb0 = r * QL * 4;  // first super-block of the round
+            for (int i = c; i < TPG * SBL * NMAX * 16; i += NT) {
+                const int sbl = (i / (NMAX * 16)) % SBL;
+                if (sb0 + sbl < nsb) {
+                    const int tsb = i / (NMAX * 16);  // tile * SBL + sbl
+                    const int nr = i % (NMAX * 16);   // token * 16 + row
+                    const float* vv = vals + (size_t)tsb * 8 * NMAX * 16 + nr;
+                    float part = 0.0f;
+#pragma unroll
+                    for (int s = 0; s < 8; s++) part = part + vv[s * NMAX * 16];
+                    parts[i] = part;
+                }
+            }
+            __syncthreads();
+            if (chain) {
+                const int nblk = min(SBL, nsb - sb0);
+                const float* pp = parts + (size_t)ct * SBL * NMAX * 16 + cn * 16 + cr;
+                for (int bl = 0; bl < nblk; bl++) acc = acc + pp[bl * NMAX * 16];
+            }
+        }
+    }
+#undef NC_KPS_LOAD
+    if constexpr (TPG == 1) {
+        if (chain) gemm_epilogue_r16<NMAX>(p, acc, cn, tile, cr);
+    } else {
+        r16_swiglu_epilogue<NMAX>(p, lds, chain, ct, cn, cr, acc, w);
+    }
+}
+
+template <int NMAX, int QL, int TPG>
+__global__ __launch_bounds__(256 * QL * TPG) void gemm_q4_k_ps_kernel(GemmParams p) {
+    static_assert(TPG == 1 || (TPG == 4 && QL == 1), "tile groups: one tile with 1..4 quad lanes, or four tiles");
+    static_assert(NMAX <= 9, "LDS holds the sub-block values of at most 9 tokens");
+    __shared__ float lds[kps_lds_floats<NMAX, QL, TPG>()];
+    switch (wave_id_uniform() & 3) {  // the wave's sub-block pair (uniform)
+        case 0: gemm_q4_k_ps_body<NMAX, QL, TPG, 0>(p, lds); break;
+        case 1: gemm_q4_k_ps_body<NMAX, QL, TPG, 1>(p, lds); break;
+        case 2: gemm_q4_k_ps_body<NMAX, QL, TPG, 2>(p, lds); break;
+        default: gemm_q4_k_ps_body<NMAX, QL, TPG, 3>(p, lds); break;
+    }
+}
+
 // ---------------------------------------------------------------- per-block dots (parity debug)
 __global__ void blockdots_q4_0_kernel(const uint8_t* w, int groups, int r16, int M, int K, const int8_t* x, int N,
                                       int32_t* dots) {
@@ -1332,9 +1504,32 @@ int launch_k16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
         else
             NC_LAUNCH((gemm_q4_k_r16_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
     };
-    if (p.epi == EPI_SWIGLU_Q8) return fail(NC_EINVAL, "gemm: the 16-row Q4_K layout has no SwiGLU epilogue");
-    if (w.groups >= 8) go.template operator()<8>();
-    else go.template operator()<4>();
+    if constexpr (NMAX <= 9) {
+        // The interleaved gate,up as four-tile groups with the SwiGLU epilogue on the pair-split
+        // kernel (3B, N = 5: 14.9 us against 15.4 for the 64-row kernel in the verify step).
+        // Plain matrices stay one wave per quad: the pair-split kernel with 1-4 quad lanes
+        // measured no faster inside the step (3B q,k,v 10.2 / wo 7.1 us against 9.7 / 6.8).
+        auto ps = [&]<int QL, int TPG>() {
+            const dim3 grid(p.ntiles / TPG), block(256 * QL * TPG);
+            if (ev0)
+                hipExtLaunchKernelGGL((gemm_q4_k_ps_kernel<NMAX, QL, TPG>), grid, block, 0, st, ev0, ev1, 0, p);
+            else
+                NC_LAUNCH((gemm_q4_k_ps_kernel<NMAX, QL, TPG>), grid, block, 0, st, p);
+        };
+        if (p.epi == EPI_SWIGLU_Q8) {
+            if (p.ntiles % 4) return fail(NC_EINVAL, "gemm: interleaved gate,up needs whole 64-row groups");
+            ps.template operator()<1, 4>();
+        } else if (w.groups >= 8) {
+            go.template operator()<8>();
+        } else {
+            go.template operator()<4>();
+        }
+    } else {
+        if (p.epi == EPI_SWIGLU_Q8)
+            return fail(NC_EINVAL, "gemm: the 16-row Q4_K SwiGLU epilogue takes at most 9 tokens");
+        if (w.groups >= 8) go.template operator()<8>();
+        else go.template operator()<4>();
+    }
     NC_HIP(hipGetLastError());
     return NC_OK;
 }

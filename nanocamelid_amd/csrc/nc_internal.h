@@ -88,9 +88,10 @@ int64_t q40_layout_bytes(int64_t rows, int64_t cols);
 int64_t q4k_layout_bytes(int64_t rows, int64_t cols);
 int64_t q4k_r16_layout_bytes(int64_t rows, int64_t cols);
 // Q4_K on 16-row tiles: per (tile, quad of 4 super-blocks) 9 x [64 lanes x 16 B], lane
-// 16*q + r = super-block 4*quad + q of row r.
+// 16*q + r = super-block 4*quad + q of row r.  half >= 0: rows of an interleaved gate (0) or up
+// (1) matrix, placed in 64-row groups as the Q4_0 repacks do.
 void repack_q4_k_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups,
-                     int64_t row_off);
+                     int64_t row_off, int half = -1);
 
 // ---------------------------------------------------------------- GEMM launch
 enum Epi : int {

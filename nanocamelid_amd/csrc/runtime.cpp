@@ -220,11 +220,11 @@ void repack_q4_k(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* ds
 }
 
 void repack_q4_k_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups,
-                     int64_t row_off) {
+                     int64_t row_off, int half) {
     const int64_t nsb = cols / 256;
     parallel_for(rows_src, 0, [&](int64_t lo, int64_t hi) {
         for (int64_t r = lo; r < hi; r++) {
-            const int64_t R = r + row_off, t = R / 16, rr = R % 16;
+            const int64_t R = dst_row(r, row_off, half), t = R / 16, rr = R % 16;
             for (int64_t s = 0; s < nsb; s++) {
                 const uint8_t* blk = src + (r * nsb + s) * 144;
                 uint8_t* chunk = dst + (t * groups + s / 4) * kQ4KChunkBytes + (16 * (s % 4) + rr) * 16;
@@ -286,8 +286,8 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
     // head stays on R64 (R16 78.7 against 69.5 us at N = 5).  An interleaved gate/up pair keeps
     // its 64-row groups (gate rows 32t.. in rows 0-31 of group t, up rows in 32-63): with R16
     // those are four consecutive 16-row tiles, which one workgroup covers.
-    // Q4_K likewise on 16-row tiles below 256 64-row tiles, except an interleaved gate/up pair
-    // (its SwiGLU epilogue needs the 64-row groups; those matrices are large anyway).
+    // Q4_K likewise on 16-row tiles below 256 64-row tiles; an interleaved gate/up pair below
+    // 1024 64-row groups (its SwiGLU epilogue takes four consecutive 16-row tiles).
     const bool single = std::all_of(parts.begin(), parts.end(), [](const Part& q) { return q.half < 0; });
     // NC_R16_MAX_TILES=<n>: tuning override of the 64-row tile count below which Q4_0 takes R16
     static const int64_t r16_max = [] {
@@ -295,7 +295,7 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
         return e ? std::max<int64_t>(1, atoll(e)) : (int64_t)1024;
     }();
     out.layout = type == NC_TYPE_Q4_0 && (rows + 63) / 64 < r16_max ? LAYOUT_R16 : LAYOUT_R64;
-    if (type == NC_TYPE_Q4_K && single && (rows + 63) / 64 < 256) out.layout = LAYOUT_R16K;
+    if (type == NC_TYPE_Q4_K && (rows + 63) / 64 < (single ? 256 : 1024)) out.layout = LAYOUT_R16K;
     out.units = type == NC_TYPE_Q4_0 ? cols / 32 : cols / 256;
     if (out.layout == LAYOUT_R16) {
         out.tiles = (rows + 15) / 16;
@@ -314,7 +314,7 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
     std::vector<uint8_t> host(out.dev_bytes, 0);
     for (const auto& p : parts) {
         if (out.layout == LAYOUT_R16) repack_q4_0_r16(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
-        else if (out.layout == LAYOUT_R16K) repack_q4_k_r16(p.src, p.rows, cols, host.data(), out.groups, p.row_off);
+        else if (out.layout == LAYOUT_R16K) repack_q4_k_r16(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
         else if (type == NC_TYPE_Q4_0) repack_q4_0(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
         else repack_q4_k(p.src, p.rows, cols, host.data(), p.row_off, p.half);
     }
@@ -927,8 +927,13 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
         pg.xq_out = s->xq + (size_t)s->max_batch * s->maxw;
         pg.xs_out = s->xs + (size_t)s->max_batch * (s->maxw / 32);
         pg.xs8_out = s->xs8 + (size_t)s->max_batch * (s->maxw / 32);
-        if (!L.split_gateup) {
+        if (!L.split_gateup && (L.gateup.layout != LAYOUT_R16K || n <= 9)) {
             if ((rc = timed_gemm(s, L.gateup, pg))) return rc;
+        } else if (!L.split_gateup) {
+            // Q4_K four-tile groups take at most 9 tokens: interleaved rows, then SwiGLU + Q8_0
+            if ((rc = timed_gemm(s, L.gateup, plain_rows(s, n, s->ybuf, 2 * F))) ||
+                (rc = launch_prompt_swiglu_q8(s->ybuf, n, F, pg.xq_out, pg.xs_out, pg.xs8_out, st, false)))
+                return rc;
         } else {
             // gate rows then up rows in ybuf, then SwiGLU and the Q8_0 blocks as one kernel
             if ((rc = timed_gemm(s, L.gate, plain_rows(s, n, s->ybuf, 2 * F))) ||

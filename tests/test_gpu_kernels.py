@@ -185,11 +185,12 @@ def test_q4_k_bit_exact(ctx, N):
                 assert np.array_equal(dots[n, r, sb * 8:(sb + 1) * 8], W)
 
 
-@pytest.mark.parametrize("shape", [(130, 2048), (192, 3072), (64, 8192)], ids=["S8", "S12", "S8x4"])
+@pytest.mark.parametrize("shape", [(130, 2048), (192, 3072), (64, 8192), (4200, 3072)],
+                         ids=["S8", "S12", "S8x4", "S12-ps2"])
 @pytest.mark.parametrize("N", [1, 5, 9, 16])
 def test_q4_k_wave_splits(ctx, shape, N):
-    """Q4_K K-split widths: 8 super-blocks (8 waves, one round), 12 (12 waves), 32 (8 waves,
-    four rounds), with a partial 64-row tile."""
+    """Q4_K on 16-row tiles, one wave per super-block quad: 2 and 3 quads (4 waves, one round,
+    a partial last tile), 8 quads (8 waves), and more tiles than CUs (4200 rows)."""
     import nanocamelid_amd as nc
     M, K = shape
     w = random_q4_k(M, K, seed=M + K + N)
