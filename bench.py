@@ -229,6 +229,41 @@ def run_gemm_sweep(args):
             m.close()
 
 
+def run_q4k_sweep(args):
+    """The 3B Q4_K layer matrices in isolation: per-shape median kernel time at N = 1, 5, 9
+    (dispatch-stamped events, >= 60 launches over >= 1 GB of weight copies).  The kernel variant
+    follows the environment (NC_Q4K_PS=<1..4>: pair-split with that many quad lanes)."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    import nanocamelid_amd as nc
+    ctx = make_ctx(nc)
+    res = {"variant": os.environ.get("NC_Q4K_PS", "one wave per quad")}
+    for M, K, name in [(5120, 3072, "q,k,v"), (3072, 3072, "wo"), (3072, 8192, "down")]:
+        blocks = _q4_k_random_blocks(M, K, M + K)
+        wbytes = M * K // 256 * 144
+        copies = max(2, int(np.ceil(1.0e9 / wbytes)))
+        mats = [nc.QMat(ctx, nc.NC_TYPE_Q4_K, M, K, blocks) for _ in range(copies)]
+        handles = (C.c_void_p * copies)(*[m.h for m in mats])
+        for N in (1, 5, 9):
+            rng = np.random.default_rng(N)
+            xq = torch.from_numpy(rng.integers(-127, 128, (N, K), dtype=np.int8)).cuda()
+            xs = torch.from_numpy(rng.uniform(0.005, 0.02, (N, K // 32)).astype(np.float32)).cuda()
+            out = torch.empty((N, M), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            iters = max(60, 2 * copies)
+            us = np.zeros(copies + iters, np.float32)
+            nc.check(nc.lib().nc_bench_matmul(ctx.h, handles, copies, xq.data_ptr(), xs.data_ptr(), out.data_ptr(), N,
+                                              copies + iters, us.ctypes.data))
+            med = float(np.median(us[copies:]))
+            res[f"{name} {M}x{K} N{N}"] = {"us_median": round(med, 2), "GBps": round(wbytes / med / 1e3, 1)}
+        for m in mats:
+            m.close()
+    print(json.dumps(res), flush=True)
+
+
 def run_prefill(args):
     """Prompt prefill (the reference's prefill_tokens, main.rs:9415-9485): (1) the prompt matmul
     alone on the 8B and 70B Q4_0 and 3B Q4_K shapes at 64 and 256 tokens, median of events,
@@ -551,6 +586,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-full-decode", action="store_true", help="skip the 1024-token decodes at each (k, alpha)")
     ap.add_argument("--gemm-sweep", action="store_true", help="config 1: isolated GEMM bandwidth table")
+    ap.add_argument("--q4k-sweep", action="store_true", help="config 3's Q4_K layer matrices in isolation")
     ap.add_argument("--config3", action="store_true",
                     help="config 3: 3B Q4_K target + 1B Q4_0 draft, stochastic acceptance (T=1, k=4)")
     ap.add_argument("--config4", action="store_true",
@@ -586,6 +622,9 @@ def main():
     import nanocamelid_amd as nc
 
     assert torch.cuda.is_available(), "bench needs the MI355X"
+    if args.q4k_sweep:
+        run_q4k_sweep(args)
+        return
     if args.gemm_sweep:
         run_gemm_sweep(args)
         return

@@ -1516,9 +1516,23 @@ int launch_k16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
             else
                 NC_LAUNCH((gemm_q4_k_ps_kernel<NMAX, QL, TPG>), grid, block, 0, st, p);
         };
+        // NC_Q4K_PS=<1..4>: tuning override, plain matrices on the pair-split kernel with that many
+        // quad lanes (each width ran the Q4_K matmul tests bit-exact)
+        static const int forced = [] {
+            const char* e = getenv("NC_Q4K_PS");
+            return e ? atoi(e) : 0;
+        }();
         if (p.epi == EPI_SWIGLU_Q8) {
             if (p.ntiles % 4) return fail(NC_EINVAL, "gemm: interleaved gate,up needs whole 64-row groups");
             ps.template operator()<1, 4>();
+        } else if (forced == 1) {
+            ps.template operator()<1, 1>();
+        } else if (forced == 2) {
+            ps.template operator()<2, 1>();
+        } else if (forced == 3) {
+            ps.template operator()<3, 1>();
+        } else if (forced == 4) {
+            ps.template operator()<4, 1>();
         } else if (w.groups >= 8) {
             go.template operator()<8>();
         } else {
