@@ -387,6 +387,93 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_0_kernel(GemmParams p) {
     gemm_epilogue<NMAX, S>(p, acc, tile, wave, lane);
 }
 
+// ---------------------------------------------------------------- Q8_0 (64-row tiles)
+// matmul_q8_0_batch (inference.rs:1343-1383): per row and token, sum += ws * xs * dot over the
+// 32-blocks in order, dot = the signed int8 block dot (dot_i8_scalar, q8.rs:3376-3382), ws the
+// block's f16 scale.  Lane l owns row 64*tile + l; in round r wave w takes block r*S + w (its
+// 32 weight bytes as two 16-byte loads, its scale); the token's 32 activation bytes and x_scale
+// are wave-uniform, read as scalar loads.  Terms of the S blocks of a round go through a
+// double-buffered LDS array and are added in block order by the chain threads (thread
+// (w, l): tokens w, w + S, ...), one barrier per round; the epilogues are the 64-row ones.
+template <int NMAX, int S>
+__global__ __launch_bounds__(64 * S) void gemm_q8_0_kernel(GemmParams p) {
+    constexpr int TPW = (NMAX + S - 1) / S;  // chain tokens per thread
+    constexpr int D = 2;                      // ring of rounds in flight
+    extern __shared__ float lds[];            // [2][S][NMAX][64] terms when S > 1
+    const int tile = blockIdx.x;
+    const int wave = wave_id_uniform();
+    const int lane = threadIdx.x & 63;
+    const int N = p.N, nb = p.units;
+    const uint8_t* wt = p.w + (size_t)tile * p.groups * kQ80ChunkBytes;
+    const int nrounds = (nb + S - 1) / S;
+    float acc[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; j++) acc[j] = 0.0f;
+    uint4 rw[D][2];
+    uint32_t rs[D];
+    // loads are unconditional, with the block index clamped into the row (a clamped block's
+    // term is never added)
+#define NC_Q80_LOAD(R, SLOT)                                                                       \
+    do {                                                                                           \
+        const int b_ = min(min((R), nrounds - 1) * S + wave, nb - 1);                              \
+        const uint8_t* c_ = wt + (size_t)(b_ / kQ80GroupBlocks) * kQ80ChunkBytes;                  \
+        const int u_ = b_ % kQ80GroupBlocks;                                                       \
+        rw[SLOT][0] = *(const uint4*)(c_ + (2 * u_) * 1024 + lane * 16);                           \
+        rw[SLOT][1] = *(const uint4*)(c_ + (2 * u_ + 1) * 1024 + lane * 16);                       \
+        rs[SLOT] = *(const uint16_t*)(c_ + kQ80GroupBlocks * 2048 + u_ * 128 + lane * 2);          \
+    } while (0)
+    NC_Q80_LOAD(0, 0);
+    for (int r0 = 0; r0 < nrounds; r0 += D) {
+#pragma unroll
+        for (int k = 0; k < D; k++) {
+            const int r = r0 + k;
+            if (r >= nrounds) break;  // uniform
+            NC_Q80_LOAD(r + 1, (k + 1) % D);
+            const int b = r * S + wave;
+            float* buf = lds + (size_t)(r & 1) * S * NMAX * 64;
+            if (b < nb) {  // uniform
+                const float ws = f16_to_f32((uint16_t)rs[k]);
+                const int wv[8] = {(int)rw[k][0].x, (int)rw[k][0].y, (int)rw[k][0].z, (int)rw[k][0].w,
+                                   (int)rw[k][1].x, (int)rw[k][1].y, (int)rw[k][1].z, (int)rw[k][1].w};
+                float t[NMAX];
+#pragma unroll
+                for (int n = 0; n < NMAX; n++) {
+                    // tokens >= N read the last token's activations and are never stored
+                    const int nn = min(n, N - 1);
+                    sptr_i32 xw = as_scalar_i32(p.x + (size_t)nn * p.K + (size_t)b * 32);
+                    sptr_f32 xsp = as_scalar_f32(p.xs + (size_t)nn * nb + b);
+                    int dot = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) dot = __builtin_amdgcn_sdot4(wv[i], xw[i], dot, false);
+                    t[n] = ws * xsp[0] * (float)dot;
+                }
+#pragma unroll
+                for (int n = 0; n < NMAX; n++) {
+                    if constexpr (S == 1) acc[n] = acc[n] + t[n];
+                    else buf[(wave * NMAX + n) * 64 + lane] = t[n];
+                }
+            }
+            if constexpr (S > 1) {
+                // buffer r & 1 is rewritten in round r + 2, after every thread passed round r + 1's
+                // barrier
+                __syncthreads();
+                const int nblk = min(S, nb - r * S);
+#pragma unroll
+                for (int j = 0; j < TPW; j++) {
+                    const int n = wave + j * S;
+                    if (n < N) {
+                        float a = acc[j];
+                        for (int bl = 0; bl < nblk; bl++) a = a + buf[(bl * NMAX + n) * 64 + lane];
+                        acc[j] = a;
+                    }
+                }
+            }
+        }
+    }
+#undef NC_Q80_LOAD
+    gemm_epilogue<NMAX, S>(p, acc, tile, wave, lane);
+}
+
 // ---------------------------------------------------------------- Q4_0, 16-row tiles (R16)
 // Workgroup = one 16-row tile, S waves.  A wave instruction covers one quad of blocks:
 // lane = 16*j + r holds block 4*qd + j of row r, so each DPP row of 16 lanes is one block
@@ -1550,6 +1637,28 @@ int launch_k16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
 
 }  // namespace
 
+template <int NMAX>
+int launch_q80(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+    // K-split waves: enough that ~1000+ waves stream the matrix, at most one per block
+    int S = 1;
+    while (S < 8 && w.tiles * S < 1024 && 2 * S <= w.units) S *= 2;
+    auto go = [&]<int SS>() {
+        const size_t lds = SS > 1 ? (size_t)2 * SS * NMAX * 64 * sizeof(float) : 0;
+        if (ev0)
+            hipExtLaunchKernelGGL((gemm_q8_0_kernel<NMAX, SS>), dim3(p.ntiles), dim3(64 * SS), lds, st, ev0, ev1, 0, p);
+        else
+            NC_LAUNCH((gemm_q8_0_kernel<NMAX, SS>), dim3(p.ntiles), dim3(64 * SS), lds, st, p);
+    };
+    switch (S) {
+        case 1: go.template operator()<1>(); break;
+        case 2: go.template operator()<2>(); break;
+        case 4: go.template operator()<4>(); break;
+        default: go.template operator()<8>(); break;
+    }
+    NC_HIP(hipGetLastError());
+    return NC_OK;
+}
+
 // R64 waves per workgroup: enough K-split waves that ~1000+ waves stream the matrix
 // (1, 2 or 4; LDS terms double-buffered: 2 * S * 4 * NMAX * 64 floats).
 static int pick_waves(int64_t tiles) {
@@ -1598,6 +1707,9 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent
     }
     if (w.layout == LAYOUT_R16K) {
         NC_GEMM_FOR_NMAX(launch_k16, p.N, w, p, st, ev0, ev1)
+    }
+    if (w.layout == LAYOUT_Q80) {
+        NC_GEMM_FOR_NMAX(launch_q80, p.N, w, p, st, ev0, ev1)
     }
     if (w.type == NC_TYPE_Q4_K) {
         const int nsb = (int)w.units;

@@ -523,6 +523,19 @@ void quant_q4_0_block(const float* x, uint8_t* out) {
     }
 }
 
+// llama.cpp quantize_row_q8_0_ref: d = max|x| / 127, q = round(x / d) (half away from zero),
+// f16 scale rounded to nearest even.
+void quant_q8_0_block(const float* x, uint8_t* out) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) amax = std::fmax(amax, std::fabs(x[j]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t h = f32_to_f16_rne(d);
+    out[0] = (uint8_t)(h & 0xff);
+    out[1] = (uint8_t)(h >> 8);
+    for (int j = 0; j < 32; j++) out[2 + j] = (uint8_t)(int8_t)std::round(x[j] * id);
+}
+
 // A valid Q4_K encoding: per 32-sub-block affine [min, max] range, 6-bit scales/mins
 // relative to f16 super-block factors d, dmin; packing as llama.cpp's get_scale_min_k4
 // inverse.
@@ -646,6 +659,11 @@ int synth_write(const nc_synth_spec& s, uint8_t* dst, uint64_t size, int nthread
                 for (uint64_t b = it.b0; b < it.b1; b++) {
                     gen_values(s.seed, it.tid, b * 32, 32, s.weight_std, 0.0f, kPurposeWeight, buf.data());
                     quant_q4_0_block(buf.data(), tp + b * 18);
+                }
+            } else if (t.type == NC_TYPE_Q8_0) {
+                for (uint64_t b = it.b0; b < it.b1; b++) {
+                    gen_values(s.seed, it.tid, b * 32, 32, s.weight_std, 0.0f, kPurposeWeight, buf.data());
+                    quant_q8_0_block(buf.data(), tp + b * 34);
                 }
             } else {
                 for (uint64_t b = it.b0; b < it.b1; b++) {

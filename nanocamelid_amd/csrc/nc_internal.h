@@ -60,15 +60,20 @@ constexpr int kQ4KChunkBytes = 9 * 1024;
 // 4 blocks x 16 rows and its scales are one contiguous 128-byte line.
 constexpr int kTileRowsR16 = 16;
 constexpr int kQ40R16QuadBytes = 1024 + 128;  // 1152; 8 per chunk = kQ40ChunkBytes
-enum Layout : int { LAYOUT_R64 = 0, LAYOUT_R16 = 1, LAYOUT_R16K = 2, LAYOUT_Q6K = 3 };  // R16K: Q4_K on 16-row tiles
+// Q8_0 layout: rows padded to 64-row tiles; per (tile, group of 4 blocks) an 8704-byte chunk =
+// [4 blocks][2 halves][64 lanes x 16 B] of int8 weights (lane l = row 64*tile + l), then the
+// f16 scales as [4 blocks][64 lanes].  Every load of a wave is 1 KB (or 128 B) contiguous.
+constexpr int kQ80GroupBlocks = 4;
+constexpr int kQ80ChunkBytes = kQ80GroupBlocks * 2048 + kQ80GroupBlocks * 128;  // 8704
+enum Layout : int { LAYOUT_R64 = 0, LAYOUT_R16 = 1, LAYOUT_R16K = 2, LAYOUT_Q6K = 3, LAYOUT_Q80 = 4 };  // R16K: Q4_K on 16-row tiles
 
 struct QMatDev {
     int type = NC_TYPE_Q4_0;
     int layout = LAYOUT_R64;
     int64_t rows = 0, cols = 0;
     int64_t tiles = 0;       // padded rows / 64 (R16: / 16)
-    int64_t units = 0;       // Q4_0: blocks per row; Q4_K: super-blocks per row
-    int64_t groups = 0;      // Q4_0: ceil(blocks / 8) (R16: ceil(blocks / 32))
+    int64_t units = 0;       // Q4_0, Q8_0: blocks per row; Q4_K: super-blocks per row
+    int64_t groups = 0;      // Q4_0: ceil(blocks / 8) (R16: ceil(blocks / 32)); Q8_0: ceil(blocks / 4)
     uint8_t* dev = nullptr;  // repacked bytes
     int64_t dev_bytes = 0;
     int64_t algo_bytes = 0;  // rows * cols * 18/32 (Q4_0) or 144/256 (Q4_K)
@@ -90,6 +95,9 @@ int64_t q4k_r16_layout_bytes(int64_t rows, int64_t cols);
 // Q4_K on 16-row tiles: per (tile, quad of 4 super-blocks) 9 x [64 lanes x 16 B], lane
 // 16*q + r = super-block 4*quad + q of row r.  half >= 0: rows of an interleaved gate (0) or up
 // (1) matrix, placed in 64-row groups as the Q4_0 repacks do.
+int64_t q80_layout_bytes(int64_t rows, int64_t cols);
+void repack_q8_0(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups, int64_t row_off,
+                 int half);
 void repack_q4_k_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups,
                      int64_t row_off, int half = -1);
 

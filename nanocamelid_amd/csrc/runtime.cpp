@@ -179,6 +179,30 @@ void repack_q4_0(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* ds
     });
 }
 
+int64_t q80_layout_bytes(int64_t rows, int64_t cols) {
+    return (rows + 63) / 64 * ((cols / 32 + kQ80GroupBlocks - 1) / kQ80GroupBlocks) * kQ80ChunkBytes;
+}
+
+// Q8_0 block = f16 scale + 32 int8 (34 bytes, Q8_0Block::from_bytes q8.rs:479-487).
+void repack_q8_0(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups, int64_t row_off,
+                 int half) {
+    const int64_t nb = cols / 32;
+    parallel_for(rows_src, 0, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; r++) {
+            const int64_t R = dst_row(r, row_off, half);
+            const int64_t t = R / 64, l = R % 64;
+            for (int64_t b = 0; b < nb; b++) {
+                const uint8_t* blk = src + (r * nb + b) * 34;
+                uint8_t* chunk = dst + (t * groups + b / kQ80GroupBlocks) * kQ80ChunkBytes;
+                const int64_t u = b % kQ80GroupBlocks;
+                std::memcpy(chunk + (2 * u) * 1024 + l * 16, blk + 2, 16);
+                std::memcpy(chunk + (2 * u + 1) * 1024 + l * 16, blk + 18, 16);
+                std::memcpy(chunk + kQ80GroupBlocks * 2048 + u * 128 + l * 2, blk, 2);
+            }
+        }
+    });
+}
+
 int64_t q40_r16_layout_bytes(int64_t rows, int64_t cols) {
     const int64_t tiles = (rows + 15) / 16, groups = (cols / 32 + 31) / 32;
     return tiles * groups * kQ40ChunkBytes;
@@ -280,6 +304,19 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
     out.type = type;
     out.rows = rows;
     out.cols = cols;
+    if (type == NC_TYPE_Q8_0) {
+        out.layout = LAYOUT_Q80;
+        out.units = cols / 32;
+        out.tiles = (rows + 63) / 64;
+        out.groups = (out.units + kQ80GroupBlocks - 1) / kQ80GroupBlocks;
+        out.dev_bytes = q80_layout_bytes(rows, cols);
+        out.algo_bytes = rows * cols / 32 * 34;
+        std::vector<uint8_t> host(out.dev_bytes, 0);
+        for (const auto& p : parts) repack_q8_0(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
+        NC_HIP(hipMalloc((void**)&out.dev, out.dev_bytes));
+        NC_HIP(hipMemcpy(out.dev, host.data(), out.dev_bytes, hipMemcpyHostToDevice));
+        return NC_OK;
+    }
     // R16 for Q4_0 matrices below 1024 64-row tiles: every layer matrix up to the 70B shape
     // (57344 x 8192 as a plain matmul, us at N = 1 / 5 / 9 / 16: R64 47.7 / 78.1 / 110.2 / 288.3,
     // R16 43.6 / 70.1 / 92.1 / 129.0; the 70B verify pass 34.6 -> 30.5 ms), while the 128256 x 4096
@@ -521,8 +558,9 @@ static const GgufTensor* matrix_desc(const GgufFile& g, const std::string& name,
                                     " is not supported");
         return nullptr;
     }
-    if (t->type != NC_TYPE_Q4_0 && t->type != NC_TYPE_Q4_K && !(allow_q6k && t->type == NC_TYPE_Q6_K)) {
-        *err = fail(NC_EFORMAT, "tensor " + name + ": only Q4_0, Q4_K" + (allow_q6k ? " and Q6_K" : "") +
+    if (t->type != NC_TYPE_Q4_0 && t->type != NC_TYPE_Q4_K && t->type != NC_TYPE_Q8_0 &&
+        !(allow_q6k && t->type == NC_TYPE_Q6_K)) {
+        *err = fail(NC_EFORMAT, "tensor " + name + ": only Q4_0, Q4_K, Q8_0" + (allow_q6k ? " and Q6_K" : "") +
                                     " matrices are supported, got GGML type " + std::to_string(t->type));
         return nullptr;
     }
@@ -663,7 +701,7 @@ static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_lo
         const GgufTensor* tdn = tu ? matrix_desc(g, b + "ffn_down.weight", d, F, &e, true) : nullptr;
         if (!tdn) return e;
         const int ty = (int)tq->type;
-        const auto fusable = [](uint32_t t) { return t == NC_TYPE_Q4_0 || t == NC_TYPE_Q4_K; };
+        const auto fusable = [](uint32_t t) { return t == NC_TYPE_Q4_0 || t == NC_TYPE_Q4_K || t == NC_TYPE_Q8_0; };
         const auto one = [&](const GgufTensor* t, int64_t rows, int64_t cols, QMatDev& out) {
             return upload_matrix((int)t->type, rows, cols, {{g.data + t->offset, rows, 0, -1}}, out);
         };
@@ -1031,11 +1069,11 @@ static bool prompt_matrix_ok(const QMatDev& q) {
     return false;
 }
 
-// Prompt passes take every layer matrix on a prompt kernel, or Q6_K ones in 16-row slices.
+// Prompt passes take every layer matrix on a prompt kernel, or Q6_K and Q8_0 ones in 16-row slices.
 static bool prompt_path_ok(const nc_model* m) {
     for (const LayerDev& L : m->layers)
         for (const QMatDev* q : L.all())
-            if (q->dev && !prompt_matrix_ok(*q) && q->type != NC_TYPE_Q6_K) return false;
+            if (q->dev && !prompt_matrix_ok(*q) && q->type != NC_TYPE_Q6_K && q->type != NC_TYPE_Q8_0) return false;
     return true;
 }
 
@@ -1072,7 +1110,7 @@ static int ensure_prompt_bufs(nc_session* s) {
 
 // Prompt matmul of the pass's activations (repacked first into MFMA operand order).
 // A prompt pass's matmul into rows of stride ld (default: the matrix's rows): the MFMA prompt
-// kernels, or for Q6_K matrices (no prompt kernel) the verify kernel on 16-row slices.
+// kernels, or for Q6_K and Q8_0 matrices (no prompt kernel) the verify kernel on 16-row slices.
 static int prompt_gemm(nc_session* s, const QMatDev& w, const int8_t* xq, const float* xs, float* out, int n,
                        int ld = 0) {
     if (ld == 0) ld = (int)w.rows;
@@ -1335,8 +1373,8 @@ int nc_ctx_synchronize(nc_ctx* c) {
 
 int nc_qmat_upload(nc_ctx* ctx, int type, int64_t rows, int64_t cols, const void* blocks, nc_qmat** out) {
     if (!ctx || !blocks || !out || rows <= 0 || cols <= 0) return fail(NC_EINVAL, "nc_qmat_upload: bad arguments");
-    if (type != NC_TYPE_Q4_0 && type != NC_TYPE_Q4_K && type != NC_TYPE_Q6_K)
-        return fail(NC_EINVAL, "nc_qmat_upload: type must be Q4_0, Q4_K or Q6_K");
+    if (type != NC_TYPE_Q4_0 && type != NC_TYPE_Q4_K && type != NC_TYPE_Q8_0 && type != NC_TYPE_Q6_K)
+        return fail(NC_EINVAL, "nc_qmat_upload: type must be Q4_0, Q4_K, Q8_0 or Q6_K");
     NC_HIP(hipSetDevice(ctx->device));
     auto* q = new nc_qmat();
     q->ctx = ctx;
@@ -2358,6 +2396,8 @@ int nc_synth_write(const nc_synth_spec* spec, void* dst, uint64_t size, int32_t 
     if (!spec || !dst) return fail(NC_EINVAL, "null argument");
     if (spec->embedding_length % spec->head_count || spec->embedding_length % 256 || spec->feed_forward_length % 256)
         return fail(NC_EINVAL, "synth: widths must be multiples of 256");
+    if (spec->weight_type != NC_TYPE_Q4_0 && spec->weight_type != NC_TYPE_Q4_K && spec->weight_type != NC_TYPE_Q8_0)
+        return fail(NC_EINVAL, "synth: weight_type must be Q4_0, Q4_K or Q8_0");
     return synth_write(*spec, (uint8_t*)dst, size, nthreads);
 }
 

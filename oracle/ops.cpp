@@ -385,6 +385,33 @@ void or_matmul_q4_0(float* out, const int8_t* x, const float* xs, const uint8_t*
     });
 }
 
+// inference.rs:1343-1383 matmul_q8_0_batch: per row and token, sum += ws * xs * dot over the
+// 32-blocks in order, dot = dot_i8_scalar of the block's int8 weights and activations
+// (q8.rs:3376-3382), ws = fast_f16_to_f32 of the block's scale (q8.rs:500-502); block =
+// f16 scale then 32 int8 (Q8_0Block::from_bytes, q8.rs:479-487).
+void or_matmul_q8_0(float* out, const int8_t* x, const float* xs, const uint8_t* w,
+                    int64_t N, int64_t M, int64_t K, int nthreads) {
+    int64_t bpr = K / 32;
+    parallel_rows(M, nthreads, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; r++) {
+            const uint8_t* wrow = w + r * bpr * 34;
+            for (int64_t t = 0; t < N; t++) {
+                const int8_t* xt = x + t * K;
+                const float* st = xs + t * bpr;
+                float sum = 0.0f;
+                for (int64_t b = 0; b < bpr; b++) {
+                    const uint8_t* blk = wrow + b * 34;
+                    int32_t dot = 0;
+                    for (int i = 0; i < 32; i++) dot += (int32_t)(int8_t)blk[2 + i] * (int32_t)xt[b * 32 + i];
+                    const float ws = or_f16_to_f32(load_u16(blk));
+                    sum += ws * st[b] * (float)dot;
+                }
+                out[t * M + r] = sum;
+            }
+        }
+    });
+}
+
 void or_matmul_q4_0_blockdots(int32_t* dots, const int8_t* x, const uint8_t* w,
                               int64_t N, int64_t M, int64_t K, int nthreads) {
     int64_t bpr = K / 32;

@@ -38,6 +38,16 @@ def random_q4_k(M, K, seed):
     return out
 
 
+def random_q8_0(M, K, seed):
+    """Random Q8_0 blocks [M, K/32, 34]: int8 values over the full range, small f16 scales."""
+    rng = np.random.default_rng(seed)
+    out = rng.integers(-128, 128, (M, K // 32, 34), dtype=np.int16).astype(np.int8).view(np.uint8)
+    d = rng.uniform(5e-4, 4e-3, (M, K // 32)).astype(np.float16).view(np.uint16)
+    out[:, :, 0] = d & 0xFF
+    out[:, :, 1] = d >> 8
+    return out
+
+
 def q8_activations(N, K, seed):
     from oracle import oracle as O
     rng = np.random.default_rng(seed)

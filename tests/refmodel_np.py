@@ -28,7 +28,7 @@ import numpy as np
 _FIXED = {0: ("<B", 1), 1: ("<b", 1), 2: ("<H", 2), 3: ("<h", 2), 4: ("<I", 4), 5: ("<i", 4), 6: ("<f", 4),
           7: ("<?", 1), 10: ("<Q", 8), 11: ("<q", 8), 12: ("<d", 8)}
 # tensor types used here: (block elements, block bytes)
-_LAYOUT = {0: (1, 4), 1: (1, 2), 2: (32, 18), 12: (256, 144), 14: (256, 210)}
+_LAYOUT = {0: (1, 4), 1: (1, 2), 2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
 
 
 class Gguf:
@@ -95,6 +95,8 @@ class Gguf:
             v = b.view(np.float16).astype(np.float64)
         elif t == 2:
             v = _dequant_q4_0(b)
+        elif t == 8:
+            v = _dequant_q8_0(b)
         elif t == 12:
             v = _dequant_q4_k(b)
         elif t == 14:
@@ -110,6 +112,13 @@ def _dequant_q4_0(b):
     q = blk[:, 2:]
     nib = np.concatenate([q & 0x0F, q >> 4], axis=1).astype(np.float64) - 8.0  # element j<16 low, j>=16 high
     return (nib * d).reshape(-1)
+
+
+def _dequant_q8_0(b):
+    # GGML Q8_0 block: f16 scale d, then 32 int8 values q; value = d * q
+    blk = b.reshape(-1, 34)
+    d = blk[:, :2].copy().view(np.float16).astype(np.float64)
+    return (blk[:, 2:].copy().view(np.int8).astype(np.float64) * d).reshape(-1)
 
 
 def _dequant_q4_k(b):

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.gpu_util import q8_activations, random_q4_0, random_q4_k
+from tests.gpu_util import q8_activations, random_q4_0, random_q4_k, random_q8_0
 
 pytestmark = pytest.mark.gpu
 
@@ -218,6 +218,24 @@ def test_q4_k_layouts(ctx, shape, N):
             for sb in range(K // 256):
                 W, _ = O.q4_k_subblock_ints(w[r, sb], xq[n, sb * 256:(sb + 1) * 256])
                 assert np.array_equal(dots[n, r, sb * 8:(sb + 1) * 8], W)
+
+
+@pytest.mark.parametrize("shape", [(130, 1024), (192, 4096), (4200, 96), (64, 32)],
+                         ids=["partial-tile", "S8", "partial-group", "one-block"])
+@pytest.mark.parametrize("N", [1, 5, 9, 16, 21])
+def test_q8_0_bit_exact(ctx, shape, N):
+    """Q8_0 matrices (matmul_q8_0_batch, inference.rs:1343-1383) on 64-row tiles with 1-8
+    K-split waves, a partial last tile and a partial last group of 4 blocks; 21 tokens run as
+    16-token slices.  Every output bit-identical to the oracle."""
+    import nanocamelid_amd as nc
+    M, K = shape
+    w = random_q8_0(M, K, seed=M + K + N)
+    _, xq, xs = q8_activations(N, K, seed=500 + N)
+    q = nc.QMat(ctx, nc.NC_TYPE_Q8_0, M, K, w)
+    out = nc.matmul_quantized_batch(ctx, q, torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda())
+    torch.cuda.synchronize()
+    ref = O.matmul_q8_0(xq, xs, w, N, M, K, nthreads=16)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
 
 def test_quantize_q8_0_matches_oracle(ctx):

@@ -300,10 +300,12 @@ def test_long_context_logits(ctx, hd, checks):
         pos = c
 
 
-@pytest.mark.parametrize("hd,wt", [(64, 2), (128, 2), (128, 12)], ids=["hd64-q4_0", "hd128-q4_0", "hd128-q4_k"])
+@pytest.mark.parametrize("hd,wt", [(64, 2), (128, 2), (128, 12), (128, 8)],
+                         ids=["hd64-q4_0", "hd128-q4_0", "hd128-q4_k", "hd128-q8_0"])
 def test_prompt_passes_match_oracle(ctx, hd, wt):
     """Prompts of 32 or more tokens on Q4_0 and Q4_K models run as MFMA prompt passes of up to
-    256 tokens (epilogues as separate kernels, attention in 64-row groups): a 300-token prompt
+    256 tokens, Q8_0 models as the same passes with their matmuls in 16-token slices of the
+    verify kernel (epilogues as separate kernels, attention in 64-row groups): a 300-token prompt
     without logits (passes of 256 + 44) and 400 more with logits (passes of 256 + 128, then the
     last 16 rows as a verify-sized pass), then a 9-row verify: every logit bit-identical to the
     oracle's after 16-token chunks, i.e. the same KV cache bits."""
@@ -370,6 +372,33 @@ def test_q6_k_head_model_logits(ctx):
     pos = 0
     for n in (1, 5, 16, 9):
         batch = nc.uniform_prompt(300 + n, n, V)
+        _, _, _, preds = gs.verify_greedy(batch, pos)
+        opreds, _, ologits = os_.verify_greedy(batch, pos, want_logits=True)
+        assert np.array_equal(preds, opreds), n
+        for i in range(n):
+            assert _same(gs.logits(i), ologits[i]), (n, i)
+        pos += n
+
+
+def test_q8_0_model_logits(ctx):
+    """A Q8_0 model (llama.cpp's Q8_0 files: every layer matrix and the untied head in Q8_0,
+    matmul_q8_0_batch inference.rs:1343-1383): fused q,k,v with RoPE, the interleaved gate,up
+    with SwiGLU + Q8_0 and the residual epilogues on the 64-row Q8_0 kernel; verify logits and
+    predictions bit-identical to the oracle at widths 1, 5, 16, 9."""
+    import nanocamelid_amd as nc
+    from tests import gguf_writer as GW
+    spec = dict(TINY, tied=0, weight_type=nc.NC_TYPE_Q8_0)
+    meta, ts = GW.read(nc.synth_gguf(**spec, seed=71).tobytes())
+    d, V = TINY["embedding_length"], TINY["vocab_size"]
+    raw = GW.random_blocks(nc.NC_TYPE_Q8_0, d * V // 32, seed=71).tobytes()
+    ts = [("output.weight", [d, V], nc.NC_TYPE_Q8_0, raw) if t[0] == "output.weight" else t for t in ts]
+    img = GW.write(meta, ts)
+    gm, om = nc.Model(ctx, data=np.frombuffer(img, np.uint8)), O.Model(data=img)
+    assert gm.config["weight_type"] == nc.NC_TYPE_Q8_0
+    gs, os_ = nc.Session(gm, 128, 16), O.Session(om, 128, 16)
+    pos = 0
+    for n in (1, 5, 16, 9):
+        batch = nc.uniform_prompt(400 + n, n, V)
         _, _, _, preds = gs.verify_greedy(batch, pos)
         opreds, _, ologits = os_.verify_greedy(batch, pos, want_logits=True)
         assert np.array_equal(preds, opreds), n

@@ -397,3 +397,68 @@ def test_q6_k_dot_float64_and_term_order():
         assert np.float32(O.q6_k_dot(blk, x, xs)) == chain(ref_order)
         differs |= bool(chain(other) != chain(ref_order))
     assert differs
+
+
+# ---------------------------------------------------------------- Q8_0 matrices (inference.rs:1343-1383)
+def q8_block(scale_bits, vals):
+    return np.concatenate([np.array([scale_bits & 0xFF, scale_bits >> 8], np.uint8),
+                           np.asarray(vals, np.int8).view(np.uint8)])
+
+
+def test_matmul_q8_0_block_dot_known_answer():
+    # q8.rs:5050-5058: a [2]*32 block scaled 2.0 against [-3]*32 scaled 0.5: dot -192, -192.0
+    w = q8_block(0x4000, [2] * 32)
+    x = np.full(32, -3, np.int8)
+    out = O.matmul_q8_0(x, np.array([0.5], np.float32), w, 1, 1, 32)
+    assert out[0, 0] == np.float32(-192.0)
+
+
+def test_matmul_q8_0_reference_fixture_vs_float64():
+    # the fixture of inference.rs:6815-6860 (q8_block helper :5399-5405): 3 tokens x 3 rows x 64
+    N, M, K = 3, 3, 64
+    x = np.array([((i * 5) % 61) - 30 for i in range(N * K)], np.int8)
+    xs = np.array([0.125 + i * 0.03125 for i in range(N * (K // 32))], np.float32)
+    blocks = []
+    for idx in range(M * (K // 32)):
+        seed = idx + 1
+        blocks.append(q8_block(0x3800 + idx, [((seed + j * 7) % 63) - 31 for j in range(32)]))
+    w = np.concatenate(blocks)
+    got = O.matmul_q8_0(x, xs, w, N, M, K)
+    blk = w.reshape(M, K // 32, 34)
+    ws = blk[:, :, :2].copy().view(np.float16)[:, :, 0].astype(np.float64)
+    q = blk[:, :, 2:].copy().view(np.int8).astype(np.float64)
+    deq = (q * ws[:, :, None]).reshape(M, K)
+    xf = x.reshape(N, K).astype(np.float64) * np.repeat(xs.reshape(N, -1).astype(np.float64), 32, axis=1)
+    ref = xf @ deq.T
+    assert np.allclose(got, ref, rtol=1e-6, atol=1e-6)
+    # batch rows equal single-token calls (the fixture's own assertion)
+    for n in range(N):
+        one = O.matmul_q8_0(x[n * K:(n + 1) * K], xs[n * 2:(n + 1) * 2], w, 1, M, K)[0]
+        assert np.array_equal(one, got[n])
+
+
+def test_matmul_q8_0_left_to_right_order():
+    # terms 2^24, 1, -2^24 in block order: left to right gives 0 (2^24 + 1 rounds back to
+    # 2^24), any other grouping or the float64 sum gives 1
+    w = np.concatenate([q8_block(0x6400, [1] * 32), q8_block(0x3C00, [1] * 32), q8_block(0x6400, [-1] * 32)])
+    x = np.concatenate([np.full(32, 32, np.int8), np.full(32, 1, np.int8), np.full(32, 32, np.int8)])
+    xs = np.array([16.0, 0.03125, 16.0], np.float32)
+    out = O.matmul_q8_0(x, xs, w, 1, 1, 96)
+    assert out[0, 0] == np.float32(0.0)
+
+
+def test_matmul_q8_0_random_vs_float64():
+    rng = np.random.default_rng(8)
+    N, M, K = 4, 24, 512
+    blk = rng.integers(-128, 128, (M, K // 32, 34), dtype=np.int16).astype(np.int8).view(np.uint8)
+    scales = rng.uniform(0.0005, 0.004, (M, K // 32)).astype(np.float16).view(np.uint16)
+    blk[:, :, 0] = scales & 0xFF
+    blk[:, :, 1] = scales >> 8
+    x = rng.integers(-127, 128, N * K, dtype=np.int8)
+    xs = rng.uniform(0.001, 0.02, N * (K // 32)).astype(np.float32)
+    got = O.matmul_q8_0(x, xs, blk.ravel(), N, M, K)
+    q = blk[:, :, 2:].copy().view(np.int8).astype(np.int64)
+    dots = np.einsum("mbj,nbj->nmb", q, x.reshape(N, K // 32, 32).astype(np.int64))
+    ref = np.einsum("mb,nb,nmb->nm", scales.view(np.float16).astype(np.float64),
+                    xs.reshape(N, -1).astype(np.float64), dots.astype(np.float64))
+    assert np.allclose(got, ref, rtol=1e-4, atol=1e-6)
