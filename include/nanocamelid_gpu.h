@@ -38,6 +38,7 @@ extern "C" {
 #define NC_TYPE_Q4_0 2
 #define NC_TYPE_Q8_0 8
 #define NC_TYPE_Q4_K 12
+#define NC_TYPE_Q5_K 13
 #define NC_TYPE_Q6_K 14
 
 typedef struct nc_ctx nc_ctx;         /* device context: device id, default stream */
@@ -93,10 +94,11 @@ int nc_ctx_set_attention(nc_ctx* ctx, int order);
  * and repacks it into the device layout.  Replaces the load-time matrix
  * construction load_q4_0_matrix / decode_q4_k_blocks (src/model.rs:1369-1401,
  * src/model.rs:1270) that feeds QuantizedMatrix (src/model.rs:294-310).
- * type: NC_TYPE_Q4_0, NC_TYPE_Q4_K, NC_TYPE_Q8_0 (matmul_q8_0_batch src/inference.rs:1343-1383;
- * batches of 1..16 tokens, more in 16-token slices) or NC_TYPE_Q6_K (the Q6_K output projection
+ * type: NC_TYPE_Q4_0, NC_TYPE_Q4_K, NC_TYPE_Q5_K (matmul_q5_k_batch src/inference.rs:2513-2640),
+ * NC_TYPE_Q8_0 (matmul_q8_0_batch src/inference.rs:1343-1383; both batches of 1..16 tokens, more
+ * in 16-token slices) or NC_TYPE_Q6_K (the Q6_K output projection
  * of llama.cpp files, matmul_q6_k_batch src/inference.rs:1882-2000; batches of 1..16 tokens).
- * cols % 32 == 0 (Q4_K, Q6_K: % 256; Q6_K: cols <= 16384). */
+ * cols % 32 == 0 (Q4_K, Q5_K, Q6_K: % 256; Q6_K: cols <= 16384). */
 int nc_qmat_upload(nc_ctx* ctx, int type, int64_t rows, int64_t cols, const void* gguf_blocks_host,
                    nc_qmat** out);
 void nc_qmat_free(nc_qmat* w);
@@ -192,8 +194,8 @@ typedef struct nc_model_config {
     int64_t context_length, embedding_length, block_count, feed_forward_length;
     int64_t head_count, head_count_kv, head_dim, rope_dimension_count, vocab_size;
     int64_t attention_output_width, kv_width;
-    int32_t weight_type;  /* GGUF type of blk.0.attn_q.weight: NC_TYPE_Q4_0, NC_TYPE_Q4_K, NC_TYPE_Q8_0 or
-                             NC_TYPE_Q6_K.
+    int32_t weight_type;  /* GGUF type of blk.0.attn_q.weight: NC_TYPE_Q4_0, NC_TYPE_Q4_K, NC_TYPE_Q5_K,
+                             NC_TYPE_Q8_0 or NC_TYPE_Q6_K.
                            Files that mix types (llama.cpp Q4_K_M) keep each matrix's own type; this
                            field names the first layer's attention-query type only. */
     int32_t tied_head;    /* 1 when the head was requantised from token_embd */
@@ -411,7 +413,8 @@ int nc_generate_speculative_stochastic(nc_session* target, nc_session* draft, co
 typedef struct nc_synth_spec {
     int32_t layers, embedding_length, head_count, head_count_kv, feed_forward_length, vocab_size;
     int32_t context_length;
-    int32_t weight_type; /* NC_TYPE_Q4_0, NC_TYPE_Q4_K or NC_TYPE_Q8_0 for layer matrices and token_embd */
+    int32_t weight_type; /* NC_TYPE_Q4_0, NC_TYPE_Q4_K, NC_TYPE_Q5_K or NC_TYPE_Q8_0 for layer matrices and
+                            token_embd */
     int32_t tied;        /* 1: no output.weight (head requantised at load) */
     int32_t norm_mode;   /* 0: norm weights 1.0; 1: N(1, 0.1) */
     float rope_freq_base, rms_norm_epsilon, weight_std;

@@ -20,12 +20,13 @@ import ctypes as C
 
 import numpy as np
 
-from ._ffi import (NC_TYPE_Q4_0, NC_TYPE_Q4_K, NC_TYPE_Q6_K, NC_TYPE_Q8_0, DecodeStats, LoadOpts, ModelConfig, NcError, SynthSpec,
+from ._ffi import (NC_TYPE_Q4_0, NC_TYPE_Q4_K, NC_TYPE_Q5_K, NC_TYPE_Q6_K, NC_TYPE_Q8_0, DecodeStats, LoadOpts, ModelConfig, NcError, SynthSpec,
                    VerifyResult, check, lib)
 
 __all__ = ["Context", "QMat", "Model", "Session", "matmul_quantized_batch", "matmul_blockdots",
            "quantize_f32_to_q8_0_batch", "synth_gguf", "uniform_prompt", "oracle_draft",
-           "generate_speculative_draft", "NcError", "NC_TYPE_Q4_0", "NC_TYPE_Q4_K", "NC_TYPE_Q8_0", "SYNTH_CONFIGS"]
+           "generate_speculative_draft", "NcError", "NC_TYPE_Q4_0", "NC_TYPE_Q4_K", "NC_TYPE_Q5_K", "NC_TYPE_Q8_0",
+           "SYNTH_CONFIGS"]
 
 
 def _u32(a):
@@ -74,7 +75,7 @@ class Context:
 
 
 class QMat:
-    """Device-resident repacked Q4_0 / Q4_K / Q8_0 / Q6_K matrix (QuantizedMatrix, src/model.rs:294-310)."""
+    """Device-resident repacked Q4_0 / Q4_K / Q5_K / Q8_0 / Q6_K matrix (QuantizedMatrix, src/model.rs:294-310)."""
 
     def __init__(self, ctx: Context, qtype: int, rows: int, cols: int, gguf_blocks: np.ndarray):
         blocks = np.ascontiguousarray(gguf_blocks, dtype=np.uint8)

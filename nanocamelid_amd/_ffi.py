@@ -18,7 +18,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libnanocamelid_hip.so")
 
 NC_OK, NC_EINVAL, NC_ENOMEM, NC_EHIP, NC_EFORMAT, NC_ERANGE = 0, -1, -2, -3, -4, -5
-NC_TYPE_F32, NC_TYPE_Q4_0, NC_TYPE_Q8_0, NC_TYPE_Q4_K, NC_TYPE_Q6_K = 0, 2, 8, 12, 14
+NC_TYPE_F32, NC_TYPE_Q4_0, NC_TYPE_Q8_0, NC_TYPE_Q4_K, NC_TYPE_Q5_K, NC_TYPE_Q6_K = 0, 2, 8, 12, 13, 14
 NC_GEMM_KERNEL_AUTO, NC_GEMM_KERNEL_DOT4, NC_GEMM_KERNEL_MFMA = 0, 1, 2
 NC_ATTN_SEQUENTIAL, NC_ATTN_SPLIT = 0, 1
 

@@ -970,8 +970,15 @@ __device__ __forceinline__ uint32_t kbyte(uint32_t w0, uint32_t w1, uint32_t w2,
     return (w >> ((i & 3) * 8)) & 0xff;
 }
 
-template <int NMAX, int S, int D>
+// Q5 = true: Q5_K super-blocks (q8.rs:1380-1397: slot 0 as Q4_K, slots 1-2 the 32 high-bit bytes,
+// slots 3-10 the nibbles), chunks of 11 x 1 KB; a sub-block's 5-bit value is its nibble plus 16
+// when bit 2*pair (low half) / 2*pair + 1 (high half) of qh[l] is set, and the term is the same
+// xs_j * (sc_j * W_j - mn_j * A_j) (matmul_q5_k_batch's x86 path, q8.rs:1551-1594).
+template <int NMAX, int S, int D, bool Q5 = false>
 __global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
+    constexpr int NSLOT = Q5 ? 11 : 9;       // 16-byte slots per super-block and lane
+    constexpr int QS = Q5 ? 3 : 1;           // first nibble slot
+    constexpr int CHUNK = NSLOT * 1024;
     constexpr int TPW = (NMAX + S - 1) / S;  // chain tokens per thread
     extern __shared__ float lds[];           // [2][S][NMAX][64] super-block terms when S > 1
     const int tile = blockIdx.x;
@@ -980,7 +987,7 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
     const int N = p.N;
     const int nsb = p.units;
     const int nb = nsb * 8;
-    const uint8_t* wt = p.w + (size_t)tile * nsb * kQ4KChunkBytes + lane * 16;
+    const uint8_t* wt = p.w + (size_t)tile * nsb * CHUNK + lane * 16;
     float acc[TPW];
 #pragma unroll
     for (int j = 0; j < TPW; j++) acc[j] = 0.0f;
@@ -988,12 +995,12 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
     // is in flight.  Loads are unconditional with clamped indices (straight-line load code
     // keeps the wait counts exact); a clamped super-block's term is never added.
     const int nrounds = (nsb + S - 1) / S;
-    uint4 rw[D][9];
+    uint4 rw[D][NSLOT];
 #define NC_K_LOAD(R, SLOT)                                                                           \
     do {                                                                                             \
         const int sb_ = min(min((R), nrounds - 1) * S + wave, nsb - 1);                              \
-        const uint8_t* c_ = wt + (size_t)sb_ * kQ4KChunkBytes;                                       \
-        _Pragma("unroll") for (int i = 0; i < 9; i++) rw[SLOT][i] = *(const uint4*)(c_ + i * 1024); \
+        const uint8_t* c_ = wt + (size_t)sb_ * CHUNK;                                                \
+        _Pragma("unroll") for (int i = 0; i < NSLOT; i++) rw[SLOT][i] = *(const uint4*)(c_ + i * 1024); \
     } while (0)
 #pragma unroll
     for (int k = 0; k < D - 1; k++) NC_K_LOAD(k, k);
@@ -1026,29 +1033,66 @@ __global__ __launch_bounds__(64 * S) void gemm_q4_k_kernel(GemmParams p) {
                 // every token of the instantiation, without branches (tokens >= N read clamped
                 // activations and are never stored)
                 float t[NMAX];
+                if constexpr (!Q5) {
 #pragma unroll
-                for (int n = 0; n < NMAX; n++) {
-                    const int nn = min(n, N - 1);
-                    sptr_i32 xw = as_scalar_i32(p.x + (size_t)nn * p.K + (size_t)sbc * 256);
-                    sptr_f32 xsp = as_scalar_f32(p.xs + (size_t)nn * nb + (size_t)sbc * 8);
-                    sptr_i32 xap = as_scalar_i32(p.xs8 + (size_t)nn * nb + (size_t)sbc * 8);
-                    float part = 0.0f;
+                    for (int n = 0; n < NMAX; n++) {
+                        const int nn = min(n, N - 1);
+                        sptr_i32 xw = as_scalar_i32(p.x + (size_t)nn * p.K + (size_t)sbc * 256);
+                        sptr_f32 xsp = as_scalar_f32(p.xs + (size_t)nn * nb + (size_t)sbc * 8);
+                        sptr_i32 xap = as_scalar_i32(p.xs8 + (size_t)nn * nb + (size_t)sbc * 8);
+                        float part = 0.0f;
+#pragma unroll
+                        for (int pr = 0; pr < 4; pr++) {
+                            const uint4 q0 = v[QS + 2 * pr], q1 = v[QS + 1 + 2 * pr];
+                            const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                            int wl = 0, wh = 0;
+#pragma unroll
+                            for (int i = 0; i < 8; i++) {
+                                wl = dot4((int)(qw[i] & 0x0F0F0F0Fu), xw[pr * 16 + i], wl);
+                                wh = dot4((int)((qw[i] >> 4) & 0x0F0F0F0Fu), xw[pr * 16 + 8 + i], wh);
+                            }
+                            // q8.rs:1372-1375: sum += xs * (sc*W - mn*A), low then high half
+                            const int jl = 2 * pr, jh = 2 * pr + 1;
+                            part = part + xsp[jl] * (sc[jl] * (float)wl - mn[jl] * (float)(xap[jl] / -8));
+                            part = part + xsp[jh] * (sc[jh] * (float)wh - mn[jh] * (float)(xap[jh] / -8));
+                        }
+                        t[n] = part;
+                    }
+                } else {
+                    // pairs outside, tokens inside: each pair's 5-bit values are built once; every
+                    // token's sum still takes its pairs in order, low then high half
+                    const uint32_t qh[8] = {v[1].x, v[1].y, v[1].z, v[1].w, v[2].x, v[2].y, v[2].z, v[2].w};
+#pragma unroll
+                    for (int n = 0; n < NMAX; n++) t[n] = 0.0f;
 #pragma unroll
                     for (int pr = 0; pr < 4; pr++) {
-                        const uint4 q0 = v[1 + 2 * pr], q1 = v[2 + 2 * pr];
+                        const uint4 q0 = v[QS + 2 * pr], q1 = v[QS + 1 + 2 * pr];
                         const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-                        int wl = 0, wh = 0;
+                        int lo[8], hi[8];
 #pragma unroll
                         for (int i = 0; i < 8; i++) {
-                            wl = dot4((int)(qw[i] & 0x0F0F0F0F), xw[pr * 16 + i], wl);
-                            wh = dot4((int)((qw[i] >> 4) & 0x0F0F0F0F), xw[pr * 16 + 8 + i], wh);
+                            // qh bytes 4i..4i+3: bit 2*pr adds 16 to the low value, 2*pr + 1 to the high
+                            lo[i] = (int)((qw[i] & 0x0F0F0F0Fu) | (((qh[i] >> (2 * pr)) & 0x01010101u) << 4));
+                            hi[i] = (int)(((qw[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * pr + 1)) & 0x01010101u) << 4));
                         }
-                        // q8.rs:1372-1375: sum += xs * (sc*W - mn*A), low then high half
                         const int jl = 2 * pr, jh = 2 * pr + 1;
-                        part = part + xsp[jl] * (sc[jl] * (float)wl - mn[jl] * (float)(xap[jl] / -8));
-                        part = part + xsp[jh] * (sc[jh] * (float)wh - mn[jh] * (float)(xap[jh] / -8));
+#pragma unroll
+                        for (int n = 0; n < NMAX; n++) {
+                            const int nn = min(n, N - 1);
+                            sptr_i32 xw = as_scalar_i32(p.x + (size_t)nn * p.K + (size_t)sbc * 256);
+                            sptr_f32 xsp = as_scalar_f32(p.xs + (size_t)nn * nb + (size_t)sbc * 8);
+                            sptr_i32 xap = as_scalar_i32(p.xs8 + (size_t)nn * nb + (size_t)sbc * 8);
+                            int wl = 0, wh = 0;
+#pragma unroll
+                            for (int i = 0; i < 8; i++) {
+                                wl = dot4(lo[i], xw[pr * 16 + i], wl);
+                                wh = dot4(hi[i], xw[pr * 16 + 8 + i], wh);
+                            }
+                            // q8.rs:1587-1590: sum += xs * (sc*W - mn*A), low then high half
+                            t[n] = t[n] + xsp[jl] * (sc[jl] * (float)wl - mn[jl] * (float)(xap[jl] / -8));
+                            t[n] = t[n] + xsp[jh] * (sc[jh] * (float)wh - mn[jh] * (float)(xap[jh] / -8));
+                        }
                     }
-                    t[n] = part;
                 }
                 if constexpr (S == 1) {
                     if (sb < nsb) {  // uniform
@@ -1452,6 +1496,14 @@ int launch_one(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
             else
                 NC_LAUNCH((gemm_q4_0_kernel<NMAX, S, D>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
         }
+    } else if (w.type == NC_TYPE_Q5_K) {
+        constexpr int D = 2;
+        const size_t lds = S > 1 ? (size_t)2 * S * NMAX * 64 * sizeof(float) : 0;
+        if (ev0)
+            hipExtLaunchKernelGGL((gemm_q4_k_kernel<NMAX, S, D, true>), dim3(p.ntiles), dim3(64 * S), lds, st, ev0,
+                                  ev1, 0, p);
+        else
+            NC_LAUNCH((gemm_q4_k_kernel<NMAX, S, D, true>), dim3(p.ntiles), dim3(64 * S), lds, st, p);
     } else {
         constexpr int D = 2;  // one super-block ahead
         const size_t lds = S > 1 ? (size_t)2 * S * NMAX * 64 * sizeof(float) : 0;
@@ -1711,7 +1763,7 @@ int launch_gemm(const QMatDev& w, const GemmParams& p0, hipStream_t st, hipEvent
     if (w.layout == LAYOUT_Q80) {
         NC_GEMM_FOR_NMAX(launch_q80, p.N, w, p, st, ev0, ev1)
     }
-    if (w.type == NC_TYPE_Q4_K) {
+    if (w.type == NC_TYPE_Q4_K || w.type == NC_TYPE_Q5_K) {
         const int nsb = (int)w.units;
         int S = nsb == 12 ? 12 : (nsb >= 8 ? 8 : 4);
         if (w.tiles * S > 4096) S = pick_waves(w.tiles);

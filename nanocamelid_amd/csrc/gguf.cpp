@@ -591,6 +591,63 @@ void quant_q4_k_block(const float* x, uint8_t* out) {
     }
 }
 
+// A valid Q5_K encoding: the Q4_K scheme with 31 levels per sub-block; the fifth bit of the
+// value of element 64*pair + 32*half + l goes to bit 2*pair + half of qh[l] (q8.rs:1380-1397).
+void quant_q5_k_block(const float* x, uint8_t* out) {
+    float scale[8], minv[8];
+    float maxs = 0.0f, maxm = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        float lo = 0.0f, hi = 0.0f;
+        for (int l = 0; l < 32; l++) {
+            lo = std::fmin(lo, x[j * 32 + l]);
+            hi = std::fmax(hi, x[j * 32 + l]);
+        }
+        scale[j] = (hi - lo) / 31.0f;
+        minv[j] = -lo;
+        maxs = std::fmax(maxs, scale[j]);
+        maxm = std::fmax(maxm, minv[j]);
+    }
+    const uint16_t dh = f32_to_f16_rne(maxs / 63.0f), mh = f32_to_f16_rne(maxm / 63.0f);
+    const float d = (float)__builtin_bit_cast(_Float16, dh), dmin = (float)__builtin_bit_cast(_Float16, mh);
+    uint8_t ls[8], lm[8];
+    for (int j = 0; j < 8; j++) {
+        int a = d > 0 ? (int)std::nearbyint(scale[j] / d) : 0;
+        int b = dmin > 0 ? (int)std::nearbyint(minv[j] / dmin) : 0;
+        ls[j] = (uint8_t)(a < 0 ? 0 : (a > 63 ? 63 : a));
+        lm[j] = (uint8_t)(b < 0 ? 0 : (b > 63 ? 63 : b));
+    }
+    uint8_t* sc = out + 4;
+    std::memset(sc, 0, 12);
+    for (int j = 0; j < 8; j++) {
+        if (j < 4) {
+            sc[j] = ls[j];
+            sc[j + 4] = lm[j];
+        } else {
+            sc[j + 4] = (uint8_t)((ls[j] & 0x0f) | ((lm[j] & 0x0f) << 4));
+            sc[j - 4] |= (uint8_t)((ls[j] >> 4) << 6);
+            sc[j] |= (uint8_t)((lm[j] >> 4) << 6);
+        }
+    }
+    out[0] = (uint8_t)(dh & 0xff);
+    out[1] = (uint8_t)(dh >> 8);
+    out[2] = (uint8_t)(mh & 0xff);
+    out[3] = (uint8_t)(mh >> 8);
+    uint8_t* qh = out + 16;
+    uint8_t* qs = out + 48;
+    std::memset(qh, 0, 32);
+    std::memset(qs, 0, 128);
+    for (int j = 0; j < 8; j++) {
+        const float sj = d * (float)ls[j], mj = dmin * (float)lm[j];
+        const int pair = j / 2, half = j % 2;
+        for (int l = 0; l < 32; l++) {
+            int q = sj > 0 ? (int)std::nearbyint((x[j * 32 + l] + mj) / sj) : 0;
+            q = q < 0 ? 0 : (q > 31 ? 31 : q);
+            qs[pair * 32 + l] |= (uint8_t)(half ? ((q & 15) << 4) : (q & 15));
+            if (q & 16) qh[l] |= (uint8_t)(1u << j);
+        }
+    }
+}
+
 }  // namespace
 
 void synth_normal_values(uint64_t seed, uint32_t tid, uint64_t start, uint64_t count, uint32_t purpose, float* out) {
@@ -659,6 +716,11 @@ int synth_write(const nc_synth_spec& s, uint8_t* dst, uint64_t size, int nthread
                 for (uint64_t b = it.b0; b < it.b1; b++) {
                     gen_values(s.seed, it.tid, b * 32, 32, s.weight_std, 0.0f, kPurposeWeight, buf.data());
                     quant_q4_0_block(buf.data(), tp + b * 18);
+                }
+            } else if (t.type == NC_TYPE_Q5_K) {
+                for (uint64_t b = it.b0; b < it.b1; b++) {
+                    gen_values(s.seed, it.tid, b * 256, 256, s.weight_std, 0.0f, kPurposeWeight, buf.data());
+                    quant_q5_k_block(buf.data(), tp + b * 176);
                 }
             } else if (t.type == NC_TYPE_Q8_0) {
                 for (uint64_t b = it.b0; b < it.b1; b++) {

@@ -85,7 +85,8 @@ struct QMatDev {
 // (lanes 32..63) of an interleaved SwiGLU matrix (half = 0 or 1), else -1.
 void repack_q4_0(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups,
                  int64_t row_off, int half);
-void repack_q4_k(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t row_off, int half);
+void repack_q4_k(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t row_off, int half,
+                 int nslot = 9);
 void repack_q4_0_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t groups, int64_t row_off,
                      int half);
 int64_t q40_r16_layout_bytes(int64_t rows, int64_t cols);

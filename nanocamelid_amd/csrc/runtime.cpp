@@ -228,16 +228,19 @@ void repack_q4_0_r16(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t
     });
 }
 
-void repack_q4_k(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t row_off, int half) {
+// Q4_K (nslot 9, 144-byte blocks) and Q5_K (nslot 11, 176-byte blocks) on 64-row tiles: per
+// (tile, super-block) nslot x [64 lanes x 16 B], slot i = bytes 16i..16i+15 of the block.
+void repack_q4_k(const uint8_t* src, int64_t rows_src, int64_t cols, uint8_t* dst, int64_t row_off, int half,
+                 int nslot) {
     const int64_t nsb = cols / 256;
     parallel_for(rows_src, 0, [&](int64_t lo, int64_t hi) {
         for (int64_t r = lo; r < hi; r++) {
             const int64_t R = dst_row(r, row_off, half);
             const int64_t t = R / 64, l = R % 64;
             for (int64_t s = 0; s < nsb; s++) {
-                const uint8_t* blk = src + (r * nsb + s) * 144;
-                uint8_t* chunk = dst + (t * nsb + s) * kQ4KChunkBytes;
-                for (int i = 0; i < 9; i++) std::memcpy(chunk + i * 1024 + l * 16, blk + i * 16, 16);
+                const uint8_t* blk = src + (r * nsb + s) * 16 * nslot;
+                uint8_t* chunk = dst + (t * nsb + s) * (int64_t)nslot * 1024;
+                for (int i = 0; i < nslot; i++) std::memcpy(chunk + i * 1024 + l * 16, blk + i * 16, 16);
             }
         }
     });
@@ -281,8 +284,8 @@ static void repack_q6_k_planes(const uint8_t* src, int64_t nblk, uint8_t* dst) {
 }
 
 static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector<Part>& parts, QMatDev& out) {
-    if (cols % 32 || ((type == NC_TYPE_Q4_K || type == NC_TYPE_Q6_K) && cols % 256))
-        return fail(NC_EINVAL, "matrix columns must be a multiple of 32 (Q4_K, Q6_K: 256)");
+    if (cols % 32 || ((type == NC_TYPE_Q4_K || type == NC_TYPE_Q5_K || type == NC_TYPE_Q6_K) && cols % 256))
+        return fail(NC_EINVAL, "matrix columns must be a multiple of 32 (Q4_K, Q5_K, Q6_K: 256)");
     if (type == NC_TYPE_Q6_K) {
         if (parts.size() != 1 || parts[0].half >= 0 || parts[0].rows != rows || cols > 16384)
             return fail(NC_EINVAL, "Q6_K: single matrices of at most 16384 columns");
@@ -345,15 +348,19 @@ static int upload_matrix(int type, int64_t rows, int64_t cols, const std::vector
     } else {
         out.tiles = (rows + 63) / 64;
         out.groups = type == NC_TYPE_Q4_0 ? (out.units + 7) / 8 : 0;
-        out.dev_bytes = type == NC_TYPE_Q4_0 ? q40_layout_bytes(rows, cols) : q4k_layout_bytes(rows, cols);
+        out.dev_bytes = type == NC_TYPE_Q4_0 ? q40_layout_bytes(rows, cols)
+                        : type == NC_TYPE_Q5_K ? q4k_layout_bytes(rows, cols) / 9 * 11
+                                               : q4k_layout_bytes(rows, cols);
     }
-    out.algo_bytes = type == NC_TYPE_Q4_0 ? rows * cols / 32 * 18 : rows * cols / 256 * 144;
+    out.algo_bytes = type == NC_TYPE_Q4_0 ? rows * cols / 32 * 18
+                     : type == NC_TYPE_Q5_K ? rows * cols / 256 * 176
+                                            : rows * cols / 256 * 144;
     std::vector<uint8_t> host(out.dev_bytes, 0);
     for (const auto& p : parts) {
         if (out.layout == LAYOUT_R16) repack_q4_0_r16(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
         else if (out.layout == LAYOUT_R16K) repack_q4_k_r16(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
         else if (type == NC_TYPE_Q4_0) repack_q4_0(p.src, p.rows, cols, host.data(), out.groups, p.row_off, p.half);
-        else repack_q4_k(p.src, p.rows, cols, host.data(), p.row_off, p.half);
+        else repack_q4_k(p.src, p.rows, cols, host.data(), p.row_off, p.half, type == NC_TYPE_Q5_K ? 11 : 9);
     }
     NC_HIP(hipMalloc((void**)&out.dev, out.dev_bytes));
     NC_HIP(hipMemcpy(out.dev, host.data(), out.dev_bytes, hipMemcpyHostToDevice));
@@ -558,9 +565,9 @@ static const GgufTensor* matrix_desc(const GgufFile& g, const std::string& name,
                                     " is not supported");
         return nullptr;
     }
-    if (t->type != NC_TYPE_Q4_0 && t->type != NC_TYPE_Q4_K && t->type != NC_TYPE_Q8_0 &&
+    if (t->type != NC_TYPE_Q4_0 && t->type != NC_TYPE_Q4_K && t->type != NC_TYPE_Q5_K && t->type != NC_TYPE_Q8_0 &&
         !(allow_q6k && t->type == NC_TYPE_Q6_K)) {
-        *err = fail(NC_EFORMAT, "tensor " + name + ": only Q4_0, Q4_K, Q8_0" + (allow_q6k ? " and Q6_K" : "") +
+        *err = fail(NC_EFORMAT, "tensor " + name + ": only Q4_0, Q4_K, Q5_K, Q8_0" + (allow_q6k ? " and Q6_K" : "") +
                                     " matrices are supported, got GGML type " + std::to_string(t->type));
         return nullptr;
     }
@@ -701,7 +708,9 @@ static int load_model(nc_ctx* ctx, const uint8_t* data, size_t size, const nc_lo
         const GgufTensor* tdn = tu ? matrix_desc(g, b + "ffn_down.weight", d, F, &e, true) : nullptr;
         if (!tdn) return e;
         const int ty = (int)tq->type;
-        const auto fusable = [](uint32_t t) { return t == NC_TYPE_Q4_0 || t == NC_TYPE_Q4_K || t == NC_TYPE_Q8_0; };
+        const auto fusable = [](uint32_t t) {
+            return t == NC_TYPE_Q4_0 || t == NC_TYPE_Q4_K || t == NC_TYPE_Q5_K || t == NC_TYPE_Q8_0;
+        };
         const auto one = [&](const GgufTensor* t, int64_t rows, int64_t cols, QMatDev& out) {
             return upload_matrix((int)t->type, rows, cols, {{g.data + t->offset, rows, 0, -1}}, out);
         };
@@ -1069,11 +1078,13 @@ static bool prompt_matrix_ok(const QMatDev& q) {
     return false;
 }
 
-// Prompt passes take every layer matrix on a prompt kernel, or Q6_K and Q8_0 ones in 16-row slices.
+// Prompt passes take every layer matrix on a prompt kernel, or Q5_K, Q6_K and Q8_0 ones in 16-row slices.
 static bool prompt_path_ok(const nc_model* m) {
     for (const LayerDev& L : m->layers)
         for (const QMatDev* q : L.all())
-            if (q->dev && !prompt_matrix_ok(*q) && q->type != NC_TYPE_Q6_K && q->type != NC_TYPE_Q8_0) return false;
+            if (q->dev && !prompt_matrix_ok(*q) && q->type != NC_TYPE_Q6_K && q->type != NC_TYPE_Q8_0 &&
+                q->type != NC_TYPE_Q5_K)
+                return false;
     return true;
 }
 
@@ -1110,7 +1121,7 @@ static int ensure_prompt_bufs(nc_session* s) {
 
 // Prompt matmul of the pass's activations (repacked first into MFMA operand order).
 // A prompt pass's matmul into rows of stride ld (default: the matrix's rows): the MFMA prompt
-// kernels, or for Q6_K and Q8_0 matrices (no prompt kernel) the verify kernel on 16-row slices.
+// kernels, or for Q5_K, Q6_K and Q8_0 matrices (no prompt kernel) the verify kernel on 16-row slices.
 static int prompt_gemm(nc_session* s, const QMatDev& w, const int8_t* xq, const float* xs, float* out, int n,
                        int ld = 0) {
     if (ld == 0) ld = (int)w.rows;
@@ -1373,8 +1384,9 @@ int nc_ctx_synchronize(nc_ctx* c) {
 
 int nc_qmat_upload(nc_ctx* ctx, int type, int64_t rows, int64_t cols, const void* blocks, nc_qmat** out) {
     if (!ctx || !blocks || !out || rows <= 0 || cols <= 0) return fail(NC_EINVAL, "nc_qmat_upload: bad arguments");
-    if (type != NC_TYPE_Q4_0 && type != NC_TYPE_Q4_K && type != NC_TYPE_Q8_0 && type != NC_TYPE_Q6_K)
-        return fail(NC_EINVAL, "nc_qmat_upload: type must be Q4_0, Q4_K, Q8_0 or Q6_K");
+    if (type != NC_TYPE_Q4_0 && type != NC_TYPE_Q4_K && type != NC_TYPE_Q5_K && type != NC_TYPE_Q8_0 &&
+        type != NC_TYPE_Q6_K)
+        return fail(NC_EINVAL, "nc_qmat_upload: type must be Q4_0, Q4_K, Q5_K, Q8_0 or Q6_K");
     NC_HIP(hipSetDevice(ctx->device));
     auto* q = new nc_qmat();
     q->ctx = ctx;
@@ -2396,8 +2408,9 @@ int nc_synth_write(const nc_synth_spec* spec, void* dst, uint64_t size, int32_t 
     if (!spec || !dst) return fail(NC_EINVAL, "null argument");
     if (spec->embedding_length % spec->head_count || spec->embedding_length % 256 || spec->feed_forward_length % 256)
         return fail(NC_EINVAL, "synth: widths must be multiples of 256");
-    if (spec->weight_type != NC_TYPE_Q4_0 && spec->weight_type != NC_TYPE_Q4_K && spec->weight_type != NC_TYPE_Q8_0)
-        return fail(NC_EINVAL, "synth: weight_type must be Q4_0, Q4_K or Q8_0");
+    if (spec->weight_type != NC_TYPE_Q4_0 && spec->weight_type != NC_TYPE_Q4_K && spec->weight_type != NC_TYPE_Q5_K &&
+        spec->weight_type != NC_TYPE_Q8_0)
+        return fail(NC_EINVAL, "synth: weight_type must be Q4_0, Q4_K, Q5_K or Q8_0");
     return synth_write(*spec, (uint8_t*)dst, size, nthreads);
 }
 

@@ -258,7 +258,7 @@ bool load_qmat(const Gguf& g, const std::string& name, int64_t rows, int64_t col
         err = "bad shape for " + name;
         return false;
     }
-    if (t->type != 2 && t->type != 12 && t->type != 8 && !(allow_q6k && t->type == 14)) {
+    if (t->type != 2 && t->type != 12 && t->type != 8 && t->type != 13 && !(allow_q6k && t->type == 14)) {
         err = "unsupported matrix type for " + name;
         return false;
     }
@@ -353,6 +353,7 @@ void matmul(const or_model* m, float* out, const int8_t* x, const float* xs, con
     if (w.type == 2) or_matmul_q4_0(out, x, xs, w.blocks.data(), N, w.rows, w.cols, m->nthreads);
     else if (w.type == 14) or_matmul_q6_k(out, x, xs, w.blocks.data(), N, w.rows, w.cols, m->nthreads);
     else if (w.type == 8) or_matmul_q8_0(out, x, xs, w.blocks.data(), N, w.rows, w.cols, m->nthreads);
+    else if (w.type == 13) or_matmul_q5_k(out, x, xs, w.blocks.data(), N, w.rows, w.cols, m->nthreads);
     else or_matmul_q4_k(out, x, xs, w.blocks.data(), N, w.rows, w.cols, m->nthreads);
 }
 

@@ -20,6 +20,8 @@
  *   or_matmul_q4_0                       : brute-force dequantised reference <= 1e-5
  *                                          (inference.rs:6028-6075) + exact block dots
  *   or_matmul_q4_k                       : dequantised reference <= 1e-4 (inference.rs:6517-6558)
+ *   or_matmul_q5_k                       : the reference's dequantised fixture <= 1e-4
+ *                                          (inference.rs:6561-6603), float64 decode, batch == single
  *   or_matmul_q8_0                       : block-dot known answer (q8.rs:5050-5058), float64
  *                                          dequantised reference, an order-fixing cancellation row
  *   or_quantize_q4_0_tied                : reconstruction error <= |d| (q8.rs:4187-4245)
@@ -69,6 +71,9 @@ void or_matmul_q4_0(float* out, const int8_t* x, const float* xs, const uint8_t*
 /* int32 per-block dots [N][M][K/32] (q8.rs:2699 for every block). */
 void or_matmul_q8_0(float* out, const int8_t* x, const float* xs, const uint8_t* w, int64_t N, int64_t M, int64_t K,
                     int nthreads);
+void or_matmul_q5_k(float* out, const int8_t* x, const float* xs, const uint8_t* w, int64_t N, int64_t M, int64_t K,
+                    int nthreads);
+float or_q5_k_dot(const uint8_t* blk, const int8_t* x, const float* xs);
 void or_matmul_q4_0_blockdots(int32_t* dots, const int8_t* x, const uint8_t* w,
                               int64_t N, int64_t M, int64_t K, int nthreads);
 /* inference.rs:2006-2132 (x86 path): w = [M][K/256][144]. */

@@ -137,6 +137,42 @@ float or_q4_k_dot(const uint8_t* blk, const int8_t* x, const float* xs8) {
     return sum;
 }
 
+// Q5_K super-block layout q8.rs:1380-1397: d(f16) dmin(f16) scales[12] qh[32] qs[128]; the
+// 5-bit value of element 64*pair + l (low half) / 64*pair + 32 + l (high half) is the nibble
+// plus 16 when bit 2*pair / 2*pair + 1 of qh[l] is set.  q8.rs:1444-1468 unpack +
+// q8.rs:1551-1594 dot_q8_scaled_preloaded (the x86 path of matmul_q5_k_batch,
+// inference.rs:2587-2640): per pair the low then the high sub-block term
+// xs_j * (sc_j * W_j - mn_j * A_j), added to a sum that starts at 0.0 per super-block.
+float or_q5_k_dot(const uint8_t* blk, const int8_t* x, const float* xs) {
+    const float d = or_f16_to_f32(load_u16(blk));
+    const float dmin = or_f16_to_f32(load_u16(blk + 2));
+    const uint8_t* scales = blk + 4;
+    const uint8_t* qh = blk + 16;
+    const uint8_t* qs = blk + 48;
+    float sum = 0.0f;
+    for (int pair = 0; pair < 4; pair++) {
+        uint8_t ls, lm, hs, hm;
+        q4k_scale_min(pair * 2, scales, &ls, &lm);
+        q4k_scale_min(pair * 2 + 1, scales, &hs, &hm);
+        const float lsc = d * (float)ls, hsc = d * (float)hs;
+        const float lmn = dmin * (float)lm, hmn = dmin * (float)hm;
+        int32_t lw = 0, la = 0, hw = 0, ha = 0;
+        for (int l = 0; l < 32; l++) {
+            const uint8_t byte = qs[pair * 32 + l];
+            const int32_t lo = (byte & 0x0f) + ((qh[l] >> (2 * pair)) & 1 ? 16 : 0);
+            const int32_t hi = (byte >> 4) + ((qh[l] >> (2 * pair + 1)) & 1 ? 16 : 0);
+            const int32_t lx = x[pair * 64 + l], hx = x[pair * 64 + 32 + l];
+            lw += lo * lx;
+            la += lx;
+            hw += hi * hx;
+            ha += hx;
+        }
+        sum += xs[pair * 2] * (lsc * (float)lw - lmn * (float)la);
+        sum += xs[pair * 2 + 1] * (hsc * (float)hw - hmn * (float)ha);
+    }
+    return sum;
+}
+
 // q8.rs:1233-1264 Q4KBlock::dequantize.
 void or_q4_k_dequantize(const uint8_t* blk, float* out) {
     float d = or_f16_to_f32(load_u16(blk));
@@ -379,6 +415,23 @@ void or_matmul_q4_0(float* out, const int8_t* x, const float* xs, const uint8_t*
                     float ws = or_f16_to_f32(load_u16(blk));
                     sum += ws * st[b] * (float)dot;
                 }
+                out[t * M + r] = sum;
+            }
+        }
+    });
+}
+
+// inference.rs:2513-2640 matmul_q5_k_batch (x86 path): per row and token, super-blocks in order,
+// each contributing or_q5_k_dot (a 0.0-started partial sum).
+void or_matmul_q5_k(float* out, const int8_t* x, const float* xs, const uint8_t* w,
+                    int64_t N, int64_t M, int64_t K, int nthreads) {
+    int64_t spr = K / 256;
+    parallel_rows(M, nthreads, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; r++) {
+            for (int64_t t = 0; t < N; t++) {
+                float sum = 0.0f;
+                for (int64_t sb = 0; sb < spr; sb++)
+                    sum += or_q5_k_dot(w + (r * spr + sb) * 176, x + t * K + sb * 256, xs + t * (K / 32) + sb * 8);
                 out[t * M + r] = sum;
             }
         }

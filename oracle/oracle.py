@@ -52,6 +52,7 @@ def lib():
         "or_matmul_q4_0": (None, [_f32p, _i8p, _f32p, _u8p, _i64, _i64, _i64, C.c_int]),
         "or_matmul_q4_0_blockdots": (None, [_i32p, _i8p, _u8p, _i64, _i64, _i64, C.c_int]),
         "or_matmul_q8_0": (None, [_f32p, _i8p, _f32p, _u8p, _i64, _i64, _i64, C.c_int]),
+        "or_matmul_q5_k": (None, [_f32p, _i8p, _f32p, _u8p, _i64, _i64, _i64, C.c_int]),
         "or_matmul_q4_k": (None, [_f32p, _i8p, _f32p, _u8p, _i64, _i64, _i64, C.c_int]),
         "or_matmul_q6_k": (None, [_f32p, _i8p, _f32p, _u8p, _i64, _i64, _i64, C.c_int]),
         "or_q6_k_dot": (C.c_float, [_u8p, _i8p, _f32p]),
@@ -168,6 +169,13 @@ def matmul_q4_0_blockdots(x_i8, w_blocks, N, M, K, nthreads=8):
 def matmul_q8_0(x_i8, x_scales, w_blocks, N, M, K, nthreads=8):
     out = np.zeros(N * M, np.float32)
     lib().or_matmul_q8_0(out, _c(x_i8, np.int8).ravel(), _c(x_scales, np.float32).ravel(),
+                         _c(w_blocks, np.uint8).ravel(), N, M, K, nthreads)
+    return out.reshape(N, M)
+
+
+def matmul_q5_k(x_i8, x_scales, w_blocks, N, M, K, nthreads=8):
+    out = np.zeros(N * M, np.float32)
+    lib().or_matmul_q5_k(out, _c(x_i8, np.int8).ravel(), _c(x_scales, np.float32).ravel(),
                          _c(w_blocks, np.uint8).ravel(), N, M, K, nthreads)
     return out.reshape(N, M)
 

@@ -38,6 +38,17 @@ def random_q4_k(M, K, seed):
     return out
 
 
+def random_q5_k(M, K, seed):
+    """Random valid Q5_K super-blocks [M, K/256, 176] (any qh / nibble bytes, small d/dmin)."""
+    rng = np.random.default_rng(seed)
+    out = rng.integers(0, 256, (M, K // 256, 176), dtype=np.uint8)
+    for o in (0, 2):
+        v = rng.uniform(1e-4, 4e-4, (M, K // 256)).astype(np.float16).view(np.uint16)
+        out[:, :, o] = v & 0xFF
+        out[:, :, o + 1] = v >> 8
+    return out
+
+
 def random_q8_0(M, K, seed):
     """Random Q8_0 blocks [M, K/32, 34]: int8 values over the full range, small f16 scales."""
     rng = np.random.default_rng(seed)

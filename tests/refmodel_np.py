@@ -28,7 +28,7 @@ import numpy as np
 _FIXED = {0: ("<B", 1), 1: ("<b", 1), 2: ("<H", 2), 3: ("<h", 2), 4: ("<I", 4), 5: ("<i", 4), 6: ("<f", 4),
           7: ("<?", 1), 10: ("<Q", 8), 11: ("<q", 8), 12: ("<d", 8)}
 # tensor types used here: (block elements, block bytes)
-_LAYOUT = {0: (1, 4), 1: (1, 2), 2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
+_LAYOUT = {0: (1, 4), 1: (1, 2), 2: (32, 18), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
 
 
 class Gguf:
@@ -99,6 +99,8 @@ class Gguf:
             v = _dequant_q8_0(b)
         elif t == 12:
             v = _dequant_q4_k(b)
+        elif t == 13:
+            v = _dequant_q5_k(b)
         elif t == 14:
             v = _dequant_q6_k(b)
         else:
@@ -119,6 +121,29 @@ def _dequant_q8_0(b):
     blk = b.reshape(-1, 34)
     d = blk[:, :2].copy().view(np.float16).astype(np.float64)
     return (blk[:, 2:].copy().view(np.int8).astype(np.float64) * d).reshape(-1)
+
+
+def _dequant_q5_k(b):
+    # GGML Q5_K: d, dmin (f16), the Q4_K 6-bit scales, qh[32], qs[128]; the value of element
+    # 64*pr + 32*half + l is the nibble plus 16 when bit 2*pr + half of qh[l] is set
+    blk = b.reshape(-1, 176)
+    d = blk[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+    dmin = blk[:, 2:4].copy().view(np.float16).astype(np.float64)[:, 0]
+    sc = blk[:, 4:16].astype(np.int64)
+    qh = blk[:, 16:48].astype(np.int64)
+    qs = blk[:, 48:].astype(np.int64)
+    out = np.zeros((blk.shape[0], 256))
+    for j in range(8):
+        if j < 4:
+            s, m = sc[:, j] & 63, sc[:, j + 4] & 63
+        else:
+            s = (sc[:, j + 4] & 0x0F) | ((sc[:, j - 4] >> 6) << 4)
+            m = (sc[:, j + 4] >> 4) | ((sc[:, j] >> 6) << 4)
+        pr, hi = divmod(j, 2)
+        byte = qs[:, pr * 32:(pr + 1) * 32]
+        q = ((byte >> 4) if hi else (byte & 0x0F)) + 16 * ((qh >> j) & 1)
+        out[:, j * 32:(j + 1) * 32] = (d * s)[:, None] * q - (dmin * m)[:, None]
+    return out.reshape(-1)
 
 
 def _dequant_q4_k(b):

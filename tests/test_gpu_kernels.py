@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.gpu_util import q8_activations, random_q4_0, random_q4_k, random_q8_0
+from tests.gpu_util import q8_activations, random_q4_0, random_q4_k, random_q5_k, random_q8_0
 
 pytestmark = pytest.mark.gpu
 
@@ -235,6 +235,24 @@ def test_q8_0_bit_exact(ctx, shape, N):
     out = nc.matmul_quantized_batch(ctx, q, torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda())
     torch.cuda.synchronize()
     ref = O.matmul_q8_0(xq, xs, w, N, M, K, nthreads=16)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [(130, 1024), (64, 3072), (4200, 256), (192, 8192)],
+                         ids=["partial-tile", "S12", "one-superblock", "S8x4"])
+@pytest.mark.parametrize("N", [1, 5, 9, 16, 21])
+def test_q5_k_bit_exact(ctx, shape, N):
+    """Q5_K matrices (matmul_q5_k_batch's x86 path, inference.rs:2513-2640) on the 64-row
+    K-quant kernel: one to many super-blocks per row, a partial last tile, 21 tokens as
+    16-token slices.  Every output bit-identical to the oracle."""
+    import nanocamelid_amd as nc
+    M, K = shape
+    w = random_q5_k(M, K, seed=M + K + N)
+    _, xq, xs = q8_activations(N, K, seed=600 + N)
+    q = nc.QMat(ctx, nc.NC_TYPE_Q5_K, M, K, w)
+    out = nc.matmul_quantized_batch(ctx, q, torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda())
+    torch.cuda.synchronize()
+    ref = O.matmul_q5_k(xq, xs, w, N, M, K, nthreads=16)
     assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
 

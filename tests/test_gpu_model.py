@@ -300,11 +300,11 @@ def test_long_context_logits(ctx, hd, checks):
         pos = c
 
 
-@pytest.mark.parametrize("hd,wt", [(64, 2), (128, 2), (128, 12), (128, 8)],
-                         ids=["hd64-q4_0", "hd128-q4_0", "hd128-q4_k", "hd128-q8_0"])
+@pytest.mark.parametrize("hd,wt", [(64, 2), (128, 2), (128, 12), (128, 8), (64, 13)],
+                         ids=["hd64-q4_0", "hd128-q4_0", "hd128-q4_k", "hd128-q8_0", "hd64-q5_k"])
 def test_prompt_passes_match_oracle(ctx, hd, wt):
     """Prompts of 32 or more tokens on Q4_0 and Q4_K models run as MFMA prompt passes of up to
-    256 tokens, Q8_0 models as the same passes with their matmuls in 16-token slices of the
+    256 tokens, Q8_0 and Q5_K models as the same passes with their matmuls in 16-token slices of the
     verify kernel (epilogues as separate kernels, attention in 64-row groups): a 300-token prompt
     without logits (passes of 256 + 44) and 400 more with logits (passes of 256 + 128, then the
     last 16 rows as a verify-sized pass), then a 9-row verify: every logit bit-identical to the
@@ -399,6 +399,28 @@ def test_q8_0_model_logits(ctx):
     pos = 0
     for n in (1, 5, 16, 9):
         batch = nc.uniform_prompt(400 + n, n, V)
+        _, _, _, preds = gs.verify_greedy(batch, pos)
+        opreds, _, ologits = os_.verify_greedy(batch, pos, want_logits=True)
+        assert np.array_equal(preds, opreds), n
+        for i in range(n):
+            assert _same(gs.logits(i), ologits[i]), (n, i)
+        pos += n
+
+
+def test_q5_k_model_logits(ctx):
+    """A Q5_K model (the layer matrices of llama.cpp's Q5_K_M files; matmul_q5_k_batch
+    inference.rs:2513-2640) and a Q4_0 output.weight: fused q,k,v, the
+    interleaved gate,up and the residual epilogues on the 64-row K-quant kernel; verify logits
+    and predictions bit-identical to the oracle at widths 1, 5, 16, 9."""
+    import nanocamelid_amd as nc
+    spec = dict(TINY, weight_type=nc.NC_TYPE_Q5_K)
+    _, gm, om = _models(ctx, spec, seed=81)
+    assert gm.config["weight_type"] == nc.NC_TYPE_Q5_K
+    gs, os_ = nc.Session(gm, 128, 16), O.Session(om, 128, 16)
+    V = TINY["vocab_size"]
+    pos = 0
+    for n in (1, 5, 16, 9):
+        batch = nc.uniform_prompt(500 + n, n, V)
         _, _, _, preds = gs.verify_greedy(batch, pos)
         opreds, _, ologits = os_.verify_greedy(batch, pos, want_logits=True)
         assert np.array_equal(preds, opreds), n

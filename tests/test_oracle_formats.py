@@ -462,3 +462,76 @@ def test_matmul_q8_0_random_vs_float64():
     ref = np.einsum("mb,nb,nmb->nm", scales.view(np.float16).astype(np.float64),
                     xs.reshape(N, -1).astype(np.float64), dots.astype(np.float64))
     assert np.allclose(got, ref, rtol=1e-4, atol=1e-6)
+
+
+# ---------------------------------------------------------------- Q5_K matrices (inference.rs:2513-2640)
+def q5_k_block(scale_bits, min_bits, seed):
+    # inference.rs:5575-5587 (k_scales :5519-5525)
+    high = [((seed + i * 11) % 256) for i in range(32)]
+    vals = [((seed + i * 3) % 16) | (((seed + i * 5) % 16) << 4) for i in range(128)]
+    return np.array([scale_bits & 0xFF, scale_bits >> 8, min_bits & 0xFF, min_bits >> 8] + k_scales(seed) + high + vals,
+                    np.uint8)
+
+
+def _dequant_q5_k_f64(blk):
+    # GGML Q5_K: value = d * sc_j * q5 - dmin * mn_j, q5 = nibble + 16 * (qh bit), sub-block j
+    d = float(np.frombuffer(blk[0:2].tobytes(), np.float16)[0])
+    dmin = float(np.frombuffer(blk[2:4].tobytes(), np.float16)[0])
+    sc = blk[4:16]
+    qh = blk[16:48]
+    qs = blk[48:176]
+    out = np.zeros(256)
+    for j in range(8):
+        if j < 4:
+            s, m = sc[j] & 63, sc[j + 4] & 63
+        else:
+            s = (sc[j + 4] & 0x0F) | ((sc[j - 4] >> 6) << 4)
+            m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4)
+        pair, half = j // 2, j % 2
+        for l in range(32):
+            q = ((qs[pair * 32 + l] >> (4 * half)) & 0x0F) + (16 if (qh[l] >> j) & 1 else 0)
+            out[pair * 64 + 32 * half + l] = d * s * q - dmin * m
+    return out
+
+
+def test_matmul_q5_k_matches_dequantized_reference():
+    # inference.rs:6561-6603: rows 2, cols 512, four fixture blocks, tolerance 1e-4
+    rows, cols = 2, 512
+    x = np.array([((i * 5) % 61) - 30 for i in range(cols)], np.int8)
+    xs = np.array([0.125 + i * 0.03125 for i in range(cols // 32)], np.float32)
+    w = np.concatenate([q5_k_block(0x3800, 0x3000, 1), q5_k_block(0x3C00, 0x3400, 2),
+                        q5_k_block(0x4000, 0x3800, 3), q5_k_block(0x4200, 0x3A00, 4)])
+    got = O.matmul_q5_k(x, xs, w, 1, rows, cols)[0]
+    deq = np.stack([np.concatenate([_dequant_q5_k_f64(w[(r * 2 + b) * 176:(r * 2 + b + 1) * 176]) for b in range(2)])
+                    for r in range(rows)])
+    ref = deq @ (x.astype(np.float64) * np.repeat(xs.astype(np.float64), 32))
+    assert np.all(np.abs(got - ref) < 1e-4)
+    # the high bit matters: the same blocks with qh cleared give a different product
+    w0 = w.copy().reshape(4, 176)
+    w0[:, 16:48] = 0
+    assert not np.allclose(O.matmul_q5_k(x, xs, w0.ravel(), 1, rows, cols)[0], got)
+
+
+def test_matmul_q5_k_batch_and_float64():
+    # inference.rs:7329-7375 fixture (3 tokens x 2 rows x 512): batch rows equal single calls;
+    # random blocks against a float64 decode
+    N, rows, cols = 3, 2, 512
+    x = np.array([((i * 5) % 61) - 30 for i in range(N * cols)], np.int8)
+    xs = np.array([0.125 + i * 0.03125 for i in range(N * (cols // 32))], np.float32)
+    w = np.concatenate([q5_k_block(0x3800 + i, 0x3000 + i, i + 1) for i in range(rows * 2)])
+    got = O.matmul_q5_k(x, xs, w, N, rows, cols)
+    for n in range(N):
+        one = O.matmul_q5_k(x[n * cols:(n + 1) * cols], xs[n * 16:(n + 1) * 16], w, 1, rows, cols)[0]
+        assert np.array_equal(one, got[n])
+    rng = np.random.default_rng(13)
+    M, K = 6, 768
+    blk = rng.integers(0, 256, (M, K // 256, 176), dtype=np.uint8)
+    for o in (0, 2):
+        v = rng.uniform(1e-4, 4e-4, (M, K // 256)).astype(np.float16).view(np.uint16)
+        blk[:, :, o], blk[:, :, o + 1] = v & 0xFF, v >> 8
+    xr = rng.integers(-127, 128, 2 * K, dtype=np.int8)
+    xsr = rng.uniform(0.001, 0.02, 2 * (K // 32)).astype(np.float32)
+    got = O.matmul_q5_k(xr, xsr, blk.ravel(), 2, M, K)
+    deq = np.stack([np.concatenate([_dequant_q5_k_f64(blk[r, b]) for b in range(K // 256)]) for r in range(M)])
+    xf = xr.reshape(2, K).astype(np.float64) * np.repeat(xsr.reshape(2, -1).astype(np.float64), 32, axis=1)
+    assert np.allclose(got, xf @ deq.T, rtol=1e-4, atol=1e-6)

@@ -30,6 +30,8 @@ SPECS = {
                      vocab_size=500, tied=1, norm_mode=1, weight_type=nc.NC_TYPE_Q4_K),
     "q8_0-untied": dict(layers=2, embedding_length=256, head_count=4, head_count_kv=2, feed_forward_length=512,
                         vocab_size=700, tied=0, norm_mode=1, weight_type=nc.NC_TYPE_Q8_0),
+    "q5_k": dict(layers=2, embedding_length=512, head_count=4, head_count_kv=2, feed_forward_length=512,
+                 vocab_size=600, tied=1, norm_mode=1, weight_type=nc.NC_TYPE_Q5_K),
     "rope-scaled": dict(layers=2, embedding_length=256, head_count=4, head_count_kv=2, feed_forward_length=512,
                         vocab_size=1000, tied=0, norm_mode=1, rope_freq_base=10000.0,
                         rope_scaling=(8.0, 64, 1.0, 4.0)),
