@@ -50,14 +50,17 @@ GEMM_KERNELS = {"auto": 0, "dot4": 1, "mfma": 2}  # NC_GEMM_KERNEL_*
 GEMM_KERNEL = "auto"
 ATTENTION_ORDERS = {"sequential": 0, "split": 1}  # NC_ATTN_*
 ATTENTION = "sequential"
+PASS_LAUNCHES = {"direct": 0, "graph": 1}  # NC_PASS_*
+PASS_LAUNCH = "direct"
 
 
 def make_ctx(nc):
-    """Device context on GPU 0 with the --gemm-kernel dot-product path and the --attention
-    summation order selected."""
+    """Device context on GPU 0 with the --gemm-kernel dot-product path, the --attention
+    summation order and the --pass-launch mode selected."""
     ctx = nc.Context(0)
     ctx.set_gemm_kernel(GEMM_KERNELS[GEMM_KERNEL])
     ctx.set_attention(ATTENTION_ORDERS[ATTENTION])
+    ctx.set_pass_launch(PASS_LAUNCHES[PASS_LAUNCH])
     return ctx
 
 
@@ -449,7 +452,7 @@ def run_config3(args):
         "data": "synthetic (random-init weights N(0,0.02) -> Q4_K / Q4_0, seeded uniform prompt)",
         "config": {"workload": f"llama-3.2-3b-q4k target + llama-3.2-1b draft, stochastic speculative sampling k={args.k} "
                                f"T=1.0, {n_prompt}-token prompt, {int(tok)} new tokens, 4096-position KV",
-                   "gemm_kernel": GEMM_KERNEL, "attention": ATTENTION,
+                   "gemm_kernel": GEMM_KERNEL, "attention": ATTENTION, "pass_launch": PASS_LAUNCH,
                    "k": args.k, "temperature": temp, "prompt_tokens": n_prompt, "tokens_emitted": int(tok),
                    "drafted": int(st.drafted), "accepted": int(st.accepted),
                    "target_verify_weight_bytes": int(tm.config["verify_weight_bytes"]),
@@ -556,7 +559,7 @@ def run_config4(args):
         "data": "synthetic (random-init weights N(0,0.02) -> Q4_0; KV cache of 8192 positions of N(0, 1) keys and "
                 "values from seeded Philox + Box-Muller streams)",
         "config": {"workload": "llama-3-70b-shape Q4_0 single k+1 verify (k=8) over an 8192-position KV cache",
-                   "gemm_kernel": GEMM_KERNEL, "attention": ATTENTION,
+                   "gemm_kernel": GEMM_KERNEL, "attention": ATTENTION, "pass_launch": PASS_LAUNCH,
                    "rows": n, "kv_positions": n_ctx, "verify_weight_bytes": int(cfg["verify_weight_bytes"]),
                    "kv_bytes_read": int(kv_bytes), "greedy_drafts_all_accepted": consistent,
                    "kv_fill_s": round(fill_s, 2), "oracle_parity": parity},
@@ -607,10 +610,14 @@ def main():
                     help="skip the extra run of the opt-in split-position attention")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB device copy (known HBM bytes) to scale rocprofv3 --pmc byte counters")
+    ap.add_argument("--pass-launch", choices=sorted(PASS_LAUNCHES), default="direct",
+                    help="verify/decode passes replayed from HIP graphs or launched kernel by kernel "
+                         "(nc_ctx_set_pass_launch)")
     args = ap.parse_args()
-    global GEMM_KERNEL, ATTENTION
+    global GEMM_KERNEL, ATTENTION, PASS_LAUNCH
     GEMM_KERNEL = args.gemm_kernel
     ATTENTION = args.attention
+    PASS_LAUNCH = args.pass_launch
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU (multi-GPU sharding is designed, not "
                                    "built); run with --gpus 1"}))
@@ -790,7 +797,7 @@ def main():
                                f" (the config's full {args.n_new}-token decode at every k, alpha: full_decode)",
                    "timed_positions": [args.n_prompt, args.n_prompt + emitted_by_steps],
                    "full_decode": full,
-                   "gemm_kernel": GEMM_KERNEL, "attention": ATTENTION,
+                   "gemm_kernel": GEMM_KERNEL, "attention": ATTENTION, "pass_launch": PASS_LAUNCH,
                    "k": args.k, "alpha": args.alpha, "prompt_tokens": args.n_prompt,
                    "tokens_emitted": int(emitted_by_steps), "drafted": int(st.drafted),
                    "accepted": int(st.accepted), "stream_equals_greedy": parity,

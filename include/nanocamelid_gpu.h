@@ -89,6 +89,22 @@ int nc_ctx_set_gemm_kernel(nc_ctx* ctx, int kernel);
 #define NC_ATTN_SPLIT 1
 int nc_ctx_set_attention(nc_ctx* ctx, int order);
 
+/* How the sessions of this context launch a verify / decode pass (nc_verify_greedy,
+ * nc_verify_stochastic, nc_forward1 and the decode loops; not prompt passes).  DIRECT (the
+ * default): every kernel is launched one by one.  GRAPH: the pass's kernels after the one that
+ * writes its positions and tokens are captured into a HIP graph on the first pass of each kind
+ * (width, head or not, dot-product path, attention variant: the attention kernels change at a few
+ * row lengths and, past 1536 positions, every 512 positions) and replayed after that, which takes
+ * the host's per-kernel launch cost off the pass.  Both run the same kernels on the same data, so
+ * results are bit-identical.  The passes of the benchmarked models are bound by the GPU, not by
+ * the launches (the 8B verify step measured 2.52 ms direct and 2.54 ms replayed, captures
+ * included), hence the default.  Passes with per-kernel or per-stage timing enabled, and models
+ * whose q, k and v are separate matrices, always launch directly.  No counterpart in the
+ * reference (its passes are CPU loops).  Set it between calls. */
+#define NC_PASS_DIRECT 0
+#define NC_PASS_GRAPH 1
+int nc_ctx_set_pass_launch(nc_ctx* ctx, int mode);
+
 /* ---------------------------------------------------------------- operator boundary */
 /* Uploads a row-major GGUF quantized matrix (rows x cols, GGUF dims [cols, rows])
  * and repacks it into the device layout.  Replaces the load-time matrix
@@ -141,6 +157,9 @@ int nc_debug_expf(nc_ctx* ctx, uint32_t first_bits, int64_t count, float* out, v
  * that runs the vocabulary's segments in parallel, 0 if from the segment-after-segment one (a
  * row whose checks failed, or a vocabulary above 262144).  Synchronises the stream. */
 int nc_debug_temperature_paths(nc_ctx* ctx, int32_t rows, int32_t* fast, void* stream);
+/* Debug hook: passes this session captured into HIP graphs and passes it replayed from them
+ * (NC_PASS_GRAPH; both stay 0 under NC_PASS_DIRECT). */
+int nc_debug_pass_graphs(nc_session* s, int64_t* captures, int64_t* replays);
 /* Per-32-block Q8_0 activation quantiser: scale = amax/127 (f32), q = round-half-away
  * (x * (1/scale)) clamped to +-127.  Replaces quantize_f32_to_q8_0_batch
  * (src/inference.rs:967-989, scalar path :991-1029).  Device pointers. */

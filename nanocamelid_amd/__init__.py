@@ -62,6 +62,11 @@ class Context:
         combined in a fixed order; equal up to f32 rounding, batch-independent)."""
         check(lib().nc_ctx_set_attention(self.h, int(order)))
 
+    def set_pass_launch(self, mode: int):
+        """How sessions launch verify and decode passes: NC_PASS_DIRECT (kernel by kernel, the
+        default) or NC_PASS_GRAPH (captured HIP graphs, replayed); results are identical."""
+        check(lib().nc_ctx_set_pass_launch(self.h, int(mode)))
+
     def close(self):
         if getattr(self, "h", None):
             lib().nc_ctx_free(self.h)
@@ -324,6 +329,12 @@ class Session:
         """Benchmark/test helper: N(0, 1) keys and values in KV rows [0, n) of every layer
         (synth_kv_values streams), so a pass at start_pos = n attends over n such positions."""
         check(lib().nc_session_fill_kv(self.h, n, seed))
+
+    def pass_graphs(self):
+        """Debug: (passes captured into HIP graphs, passes replayed from them) of this session."""
+        cap, rep = C.c_int64(0), C.c_int64(0)
+        check(lib().nc_debug_pass_graphs(self.h, C.byref(cap), C.byref(rep)))
+        return cap.value, rep.value
 
     def logits(self, row: int) -> np.ndarray:
         out = np.empty(self.vocab, np.float32)

@@ -21,6 +21,7 @@ NC_OK, NC_EINVAL, NC_ENOMEM, NC_EHIP, NC_EFORMAT, NC_ERANGE = 0, -1, -2, -3, -4,
 NC_TYPE_F32, NC_TYPE_Q4_0, NC_TYPE_Q8_0, NC_TYPE_Q4_K, NC_TYPE_Q5_K, NC_TYPE_Q6_K = 0, 2, 8, 12, 13, 14
 NC_GEMM_KERNEL_AUTO, NC_GEMM_KERNEL_DOT4, NC_GEMM_KERNEL_MFMA = 0, 1, 2
 NC_ATTN_SEQUENTIAL, NC_ATTN_SPLIT = 0, 1
+NC_PASS_DIRECT, NC_PASS_GRAPH = 0, 1
 
 
 class ModelConfig(C.Structure):
@@ -69,6 +70,7 @@ SIGNATURES = {
     "nc_ctx_synchronize": (C.c_int, [_vp]),
     "nc_ctx_set_gemm_kernel": (C.c_int, [_vp, C.c_int]),
     "nc_ctx_set_attention": (C.c_int, [_vp, C.c_int]),
+    "nc_ctx_set_pass_launch": (C.c_int, [_vp, C.c_int]),
     "nc_qmat_upload": (C.c_int, [_vp, C.c_int, _i64, _i64, _vp, C.POINTER(_vp)]),
     "nc_qmat_free": (None, [_vp]),
     "nc_qmat_device_bytes": (_i64, [_vp]),
@@ -77,6 +79,7 @@ SIGNATURES = {
     "nc_matmul_blockdots": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _vp]),
     "nc_debug_expf": (C.c_int, [_vp, C.c_uint32, _i64, _vp, _vp]),
     "nc_debug_temperature_paths": (C.c_int, [_vp, C.c_int32, _vp, _vp]),
+    "nc_debug_pass_graphs": (C.c_int, [_vp, _vp, _vp]),
     "nc_quantize_q8_0_batch": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _i64, _vp]),
     "nc_rms_norm_q8_0_batch": (C.c_int, [_vp, _vp, _vp, C.c_float, _vp, _vp, C.c_int, _i64, _vp]),
     "nc_bench_matmul": (C.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _vp]),

@@ -903,15 +903,17 @@ static int launch_attention_split(const AttnParams& a, hipStream_t st) {
     return NC_OK;
 }
 
-int launch_attention(const AttnParams& a, hipStream_t st) {
-    const int G = a.H / a.Hkv;
-    if (G > 8 || a.H % a.Hkv) return fail(NC_EINVAL, "attention: at most 8 query heads per KV head supported");
-    const int tiles = (a.max_pos + 64) / 64;
-    if (a.hd != 64 && a.hd != 128) return fail(NC_EINVAL, "attention: head_dim must be 64 or 128");
-    if (a.split) return launch_attention_split(a, st);
-    // max_pos + 1 is the longest score row of the pass
-    const int len = a.max_pos + 1;
-    const dim3 grid(a.N * a.H);
+// Kernel choice of the sequential-order attention for a pass whose longest row holds len
+// positions (the branches of launch_attention below).
+enum AttnTier {
+    AT_FUSED_1_512, AT_FUSED_3_256, AT_FUSED_4_256, AT_FUSED_5_256, AT_FUSED_3_512,  // one kernel
+    AT_PV_32_256_X1, AT_PV_4_512, AT_PV_8_512, AT_PV_16_512, AT_PV_32_512,           // scores, then
+    AT_PV_8_256, AT_PV_16_256, AT_PV_32_256,                                         // softmax + V
+    AT_TOO_LONG
+};
+
+static int attention_tier(const AttnParams& a) {
+    const int len = a.max_pos + 1;  // the longest score row of the pass
     if (len <= 1536) {
         // one kernel per pass: each (row, head) unit scores its own keys (rows up to 1536
         // positions: the units of a KV head, all on one XCD, re-read its keys from that XCD's
@@ -919,19 +921,57 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
         // positions per thread E matched to the row (fewer score slots past the row); rows of
         // at most 512 and of 1281..1536 positions on 512 threads (two waves per SIMD in the
         // score phase; measured faster there, slower for 513..1280)
+        return len <= 512 ? AT_FUSED_1_512 : len <= 768 ? AT_FUSED_3_256 : len <= 1024 ? AT_FUSED_4_256
+             : len <= 1280 ? AT_FUSED_5_256 : AT_FUSED_3_512;
+    }
+    if (len > 16384) return AT_TOO_LONG;
+    // more units than CUs on rows just past 8192 positions (a verify over an 8192-position
+    // cache): the 256-thread tier with one extra position per thread (70B shape, 9 rows x 64
+    // heads at 8201 positions)
+    if (a.N * a.H > 256 && len > 8192 && len <= 8192 + 256) return AT_PV_32_256_X1;
+    // at most one unit per CU: 512 threads, two waves per SIMD through the max, exp and sum
+    // phases (a wave issues one VALU instruction per 8 cycles at most; 2000 positions 27.2 ->
+    // 26.4 us, 8000 84.2 -> 78.4 us for one row), and the plain weighted-V loop
+    if (a.N * a.H <= 256 || len > 8192)
+        return len <= 2048 ? AT_PV_4_512 : len <= 4096 ? AT_PV_8_512 : len <= 8192 ? AT_PV_16_512 : AT_PV_32_512;
+    // more units than CUs: 256 threads, so that three units fit on a CU at once (168 VGPRs
+    // allow three waves per SIMD; at 512 threads only one unit fits and 576 units ran in three
+    // rounds), and the software-pipelined weighted-V loop, which is faster when several chains
+    // share a SIMD.  70B shape, 9 rows x 64 heads at 8101 positions: softmax + weighted V 213
+    // -> 126 us, 9 rows x 64 heads at 2001: 78 -> 51 us (both kernels)
+    return len <= 2048 ? AT_PV_8_256 : len <= 4096 ? AT_PV_16_256 : AT_PV_32_256;
+}
+
+// Score-kernel workgroups along the positions: the row's 64-position tiles rounded up to a
+// multiple of 8 (the kernel strides over the tiles and a workgroup past the last tile does
+// nothing), so that one grid serves 512 consecutive positions.
+static int score_tile_groups(const AttnParams& a) { return ((a.max_pos + 64) / 64 + 7) / 8 * 8; }
+
+int64_t attention_variant(const AttnParams& a) {
+    if (a.split) return ((int64_t)1 << 40) | (a.max_pos / kSplitChunk + 1);
+    const int tier = attention_tier(a);
+    return ((int64_t)tier << 24) | (tier >= AT_PV_32_256_X1 ? score_tile_groups(a) : 0);
+}
+
+int launch_attention(const AttnParams& a, hipStream_t st) {
+    const int G = a.H / a.Hkv;
+    if (G > 8 || a.H % a.Hkv) return fail(NC_EINVAL, "attention: at most 8 query heads per KV head supported");
+    if (a.hd != 64 && a.hd != 128) return fail(NC_EINVAL, "attention: head_dim must be 64 or 128");
+    if (a.split) return launch_attention_split(a, st);
+    const int tier = attention_tier(a);
+    if (tier == AT_TOO_LONG) return fail(NC_ERANGE, "attention: context longer than 16384 positions");
+    const dim3 grid(a.N * a.H);
+    if (tier <= AT_FUSED_3_512) {
 #define NC_FUSED(E, T)                                                                               \
     if (a.hd == 128) NC_LAUNCH((attn_fused_kernel<E, T, 128>), grid, dim3(T), 0, st, a);    \
-    else NC_LAUNCH((attn_fused_kernel<E, T, 64>), grid, dim3(T), 0, st, a);
-        if (len <= 512) {
-            NC_FUSED(1, 512)
-        } else if (len <= 768) {
-            NC_FUSED(3, 256)
-        } else if (len <= 1024) {
-            NC_FUSED(4, 256)
-        } else if (len <= 1280) {
-            NC_FUSED(5, 256)
-        } else {
-            NC_FUSED(3, 512)
+    else NC_LAUNCH((attn_fused_kernel<E, T, 64>), grid, dim3(T), 0, st, a);                 \
+    break;
+        switch (tier) {
+            case AT_FUSED_1_512: NC_FUSED(1, 512)
+            case AT_FUSED_3_256: NC_FUSED(3, 256)
+            case AT_FUSED_4_256: NC_FUSED(4, 256)
+            case AT_FUSED_5_256: NC_FUSED(5, 256)
+            default: NC_FUSED(3, 512)
         }
 #undef NC_FUSED
         NC_HIP(hipGetLastError());
@@ -942,6 +982,7 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
     // rows per block: one or two interleaved dot chains per lane; row groups are spread over
     // blockIdx.z so that every SIMD gets a short chain instead of a few SIMDs getting long ones
     const int rb = a.N >= 2 ? 2 : 1;
+    const int tiles = score_tile_groups(a);
 #define NC_SCORES(HD, RB)                                                                         \
     NC_LAUNCH((attn_scores_kernel<HD, RB>), dim3(a.Hkv, tiles, (a.N + (RB)-1) / (RB)), dim3(64 * G), 0, \
                        st, a);                                                                    \
@@ -959,43 +1000,19 @@ int launch_attention(const AttnParams& a, hipStream_t st) {
 #undef NC_SCORES_HD
 #undef NC_SCORES
     NC_HIP(hipGetLastError());
-#define NC_PV(E, T, PIPE)                                                                              \
-    if (a.hd == 128) NC_LAUNCH((attn_softmax_pv_kernel<E, T, 128, PIPE>), grid, dim3(T), 0, st, a); \
-    else NC_LAUNCH((attn_softmax_pv_kernel<E, T, 64, PIPE>), grid, dim3(T), 0, st, a);
-    if (len > 16384) return fail(NC_ERANGE, "attention: context longer than 16384 positions");
-    if (a.N * a.H > 256 && len > 8192 && len <= 8192 + 256) {
-        // more units than CUs on rows just past 8192 positions (a verify over an 8192-position
-        // cache): the 256-thread tier with one extra position per thread (70B shape, 9 rows x
-        // 64 heads at 8201 positions)
-        if (a.hd == 128) NC_LAUNCH((attn_softmax_pv_kernel<32, 256, 128, true, 1>), grid, dim3(256), 0, st, a);
-        else NC_LAUNCH((attn_softmax_pv_kernel<32, 256, 64, true, 1>), grid, dim3(256), 0, st, a);
-    } else if (a.N * a.H <= 256 || len > 8192) {
-        // at most one unit per CU: 512 threads, two waves per SIMD through the max, exp and sum
-        // phases (a wave issues one VALU instruction per 8 cycles at most; 2000 positions 27.2
-        // -> 26.4 us, 8000 84.2 -> 78.4 us for one row), and the plain weighted-V loop
-        if (len <= 2048) {
-            NC_PV(4, 512, false)
-        } else if (len <= 4096) {
-            NC_PV(8, 512, false)
-        } else if (len <= 8192) {
-            NC_PV(16, 512, false)
-        } else {
-            NC_PV(32, 512, false)
-        }
-    } else {
-        // more units than CUs: 256 threads, so that three units fit on a CU at once (168 VGPRs
-        // allow three waves per SIMD; at 512 threads only one unit fits and 576 units ran in
-        // three rounds), and the software-pipelined weighted-V loop, which is faster when
-        // several chains share a SIMD.  70B shape, 9 rows x 64 heads at 8101 positions:
-        // softmax + weighted V 213 -> 126 us, 9 rows x 64 heads at 2001: 78 -> 51 us (both
-        // kernels)
-        if (len <= 2048) {
-            NC_PV(8, 256, true)
-        } else if (len <= 4096) {
-            NC_PV(16, 256, true)
-        } else {
-            NC_PV(32, 256, true)
-        }
+#define NC_PV(E, T, PIPE, X)                                                                              \
+    if (a.hd == 128) NC_LAUNCH((attn_softmax_pv_kernel<E, T, 128, PIPE, X>), grid, dim3(T), 0, st, a); \
+    else NC_LAUNCH((attn_softmax_pv_kernel<E, T, 64, PIPE, X>), grid, dim3(T), 0, st, a);              \
+    break;
+    switch (tier) {
+        case AT_PV_32_256_X1: NC_PV(32, 256, true, 1)
+        case AT_PV_4_512: NC_PV(4, 512, false, 0)
+        case AT_PV_8_512: NC_PV(8, 512, false, 0)
+        case AT_PV_16_512: NC_PV(16, 512, false, 0)
+        case AT_PV_32_512: NC_PV(32, 512, false, 0)
+        case AT_PV_8_256: NC_PV(8, 256, true, 0)
+        case AT_PV_16_256: NC_PV(16, 256, true, 0)
+        default: NC_PV(32, 256, true, 0)
     }
 #undef NC_PV
     NC_HIP(hipGetLastError());

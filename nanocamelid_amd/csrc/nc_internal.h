@@ -177,6 +177,10 @@ struct AttnParams {
     int nchunks = 0;
 };
 int launch_attention(const AttnParams& a, hipStream_t stream);
+// Launch variant of launch_attention: passes with equal values launch the same kernels with the
+// same grids and blocks (the kernels read the rows' positions from d_pos, not from max_pos), so
+// a captured pass replays correctly at every start position of its variant.
+int64_t attention_variant(const AttnParams& a);
 
 // ---------------------------------------------------------------- prompt (prefill) path
 // Q4_0 batch matmul for any number of tokens on int8 MFMA: out[n * ld_out + row] (R16 and R64
@@ -263,6 +267,7 @@ struct nc_ctx {
     int32_t* static_scratch = nullptr;
     int gemm_kernel = NC_GEMM_KERNEL_AUTO;  // dot-product path of the quantized matmuls
     int attn_order = NC_ATTN_SEQUENTIAL;     // summation order of the verify passes' attention
+    int pass_launch = NC_PASS_DIRECT;         // NC_PASS_GRAPH: session passes replayed from HIP graphs
 };
 
 struct nc_qmat {

@@ -8,6 +8,7 @@
 #include <cstring>
 #include <memory>
 #include <thread>
+#include <unordered_map>
 
 #include "gguf.h"
 #include "nc_internal.h"
@@ -92,6 +93,9 @@ struct nc_session {
     uint32_t staged[16] = {};
     int n_staged = 0;  // staged tokens land in d_toks[0..n_staged); the rest stay as they are
     bool pending_toks = false;
+    // captured passes (everything after the pass-state kernel), by pass_graph_key
+    std::unordered_map<uint64_t, hipGraphExec_t> graphs;
+    int64_t graph_captures = 0, graph_replays = 0;
     // per-stage timing (events between the pass's stages, named as the reference's trace stages)
     bool stage_timing = false;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> stage_ev;  // first kernel's start, last kernel's end
@@ -868,25 +872,13 @@ static int stage_reserve(nc_session* s) {
 // One forward over the n tokens already in d_toks at positions start_pos..: embedding,
 // all layers (run_layer_range_batch, inference.rs:3747-4111), final norm, head and
 // per-row argmax.  Writes d_preds and logits.
-static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
+static int pass_body(nc_session* s, int n, int64_t start_pos, bool head) {
     nc_model* m = s->m;
     const nc_model_config& c = m->cfg;
     const int d = (int)c.embedding_length, aw = (int)c.attention_output_width, kw = (int)c.kv_width;
     const int F = (int)c.feed_forward_length, hd = (int)c.head_dim, Hkv = (int)c.head_count_kv;
-    if (n < 1 || n > s->max_batch) return fail(NC_ERANGE, "batch exceeds the session's max_batch");
-    if (start_pos < 0 || start_pos + n > s->max_ctx) return fail(NC_ERANGE, "batch end exceeds the session context");
     hipStream_t st = s->stream;
-    int rc = stage_reserve(s);
-    if (rc) return rc;
-    struct StageEnd {  // no stage stays open past the pass, whatever path returns
-        ~StageEnd() { t_stage_ev0 = t_stage_ev1 = nullptr; }
-    } stage_end;
-    stage_mark(s, ST_EMBED);
-    rc = launch_set_pass_state(s->d_pos, (int32_t)start_pos, s->d_toks, s->pending_toks ? s->staged : nullptr,
-                               s->pending_toks ? s->n_staged : 0, st);
-    if (rc) return rc;
-    s->pending_toks = false;
-    rc = launch_embed(m->tok_emb, s->d_toks, n, d, s->hidden, st);
+    int rc = launch_embed(m->tok_emb, s->d_toks, n, d, s->hidden, st);
     if (rc) return rc;
     const size_t layer_kv = (size_t)Hkv * s->ctx_stride * hd;
     for (int64_t li = 0; li < c.block_count; li++) {
@@ -1022,6 +1014,93 @@ static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
     if ((rc = launch_argmax_final(s->part_val, s->part_idx, n, (int)m->head.tiles, s->d_preds, st))) return rc;
     s->last_n = n;
     return NC_OK;
+}
+
+// The attention parameters of a pass that decide its launches (attention_variant).
+static AttnParams pass_attention_shape(const nc_session* s, int n, int64_t start_pos) {
+    const nc_model_config& c = s->m->cfg;
+    AttnParams a;
+    a.N = n;
+    a.H = (int)c.head_count;
+    a.Hkv = (int)c.head_count_kv;
+    a.hd = (int)c.head_dim;
+    a.max_pos = (int)(start_pos + n - 1);
+    a.split = s->ctx->attn_order == NC_ATTN_SPLIT;
+    a.nchunks = s->attn_chunks;
+    return a;
+}
+
+// Every launch of pass_body is fixed by the pass width, whether the head runs, the dot-product
+// path and the attention variant: the kernels take the start position and the tokens from
+// d_pos / d_toks, which the pass-state kernel writes before each replay.  Layers whose q, k and v
+// come from separate matrices take the start position as a kernel argument (the RoPE kernel of
+// the prompt path), so their passes always launch directly.
+static bool pass_graph_ok(const nc_session* s) {
+    if (s->ctx->pass_launch != NC_PASS_GRAPH || s->timing || s->stage_timing) return false;
+    for (const LayerDev& L : s->m->layers)
+        if (L.split_qkv) return false;
+    return true;
+}
+
+static uint64_t pass_graph_key(const nc_session* s, int n, int64_t start_pos, bool head) {
+    return (uint64_t)n | (uint64_t)head << 5 | (uint64_t)s->ctx->gemm_kernel << 6 |
+           (uint64_t)attention_variant(pass_attention_shape(s, n, start_pos)) << 8;
+}
+
+// Captured passes kept per session; past this many (contexts crossing many 512-position
+// score-grid steps) the cache starts over.
+constexpr size_t kMaxPassGraphs = 48;
+
+// pass_body as one HIP graph: captured on the first pass of its key, then replayed.  A graph
+// holds kernel nodes only (no memset or copy nodes).
+static int pass_body_graph(nc_session* s, int n, int64_t start_pos, bool head) {
+    const uint64_t key = pass_graph_key(s, n, start_pos, head);
+    auto it = s->graphs.find(key);
+    if (it == s->graphs.end()) {
+        if (s->graphs.size() >= kMaxPassGraphs) {
+            NC_HIP(hipStreamSynchronize(s->stream));
+            for (auto& g : s->graphs) NC_HIP(hipGraphExecDestroy(g.second));
+            s->graphs.clear();
+        }
+        hipGraph_t g = nullptr;
+        NC_HIP(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = pass_body(s, n, start_pos, head);
+        const hipError_t e = hipStreamEndCapture(s->stream, &g);
+        if (rc || e != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc ? rc : fail(NC_EHIP, std::string("pass capture: ") + hipGetErrorString(e));
+        }
+        hipGraphExec_t x = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (ei != hipSuccess) return fail(NC_EHIP, std::string("pass graph instantiate: ") + hipGetErrorString(ei));
+        it = s->graphs.emplace(key, x).first;
+        s->graph_captures++;
+    }
+    NC_HIP(hipGraphLaunch(it->second, s->stream));
+    s->graph_replays++;
+    s->last_n = head ? n : 0;
+    return NC_OK;
+}
+
+// One forward over the n tokens staged by upload_toks (or already in d_toks) at positions
+// start_pos..: the pass-state kernel (positions and staged tokens, by kernel arguments), then
+// pass_body, launched directly or replayed from its captured graph.
+static int run_pass(nc_session* s, int n, int64_t start_pos, bool head = true) {
+    if (n < 1 || n > s->max_batch) return fail(NC_ERANGE, "batch exceeds the session's max_batch");
+    if (start_pos < 0 || start_pos + n > s->max_ctx) return fail(NC_ERANGE, "batch end exceeds the session context");
+    int rc = stage_reserve(s);
+    if (rc) return rc;
+    struct StageEnd {  // no stage stays open past the pass, whatever path returns
+        ~StageEnd() { t_stage_ev0 = t_stage_ev1 = nullptr; }
+    } stage_end;
+    stage_mark(s, ST_EMBED);
+    rc = launch_set_pass_state(s->d_pos, (int32_t)start_pos, s->d_toks, s->pending_toks ? s->staged : nullptr,
+                               s->pending_toks ? s->n_staged : 0, s->stream);
+    if (rc) return rc;
+    s->pending_toks = false;
+    if (pass_graph_ok(s)) return pass_body_graph(s, n, start_pos, head);
+    return pass_body(s, n, start_pos, head);
 }
 
 // Stages the next pass's tokens; run_pass writes them to the device together with the
@@ -1368,6 +1447,13 @@ int nc_ctx_set_attention(nc_ctx* c, int order) {
     return NC_OK;
 }
 
+int nc_ctx_set_pass_launch(nc_ctx* c, int mode) {
+    if (!c || (mode != NC_PASS_GRAPH && mode != NC_PASS_DIRECT))
+        return fail(NC_EINVAL, "nc_ctx_set_pass_launch: unknown launch mode");
+    c->pass_launch = mode;
+    return NC_OK;
+}
+
 int nc_ctx_set_gemm_kernel(nc_ctx* c, int kernel) {
     if (!c || kernel < NC_GEMM_KERNEL_AUTO || kernel > NC_GEMM_KERNEL_MFMA)
         return fail(NC_EINVAL, "nc_ctx_set_gemm_kernel: unknown kernel");
@@ -1530,6 +1616,13 @@ int nc_debug_expf(nc_ctx* ctx, uint32_t first_bits, int64_t count, float* out, v
     return launch_expf_range(first_bits, count, out, stream ? (hipStream_t)stream : ctx->stream);
 }
 
+int nc_debug_pass_graphs(nc_session* s, int64_t* captures, int64_t* replays) {
+    if (!s || !captures || !replays) return fail(NC_EINVAL, "nc_debug_pass_graphs: null argument");
+    *captures = s->graph_captures;
+    *replays = s->graph_replays;
+    return NC_OK;
+}
+
 int nc_debug_temperature_paths(nc_ctx* ctx, int32_t rows, int32_t* fast, void* stream) {
     if (!ctx || !fast || rows < 1 || temperature_scratch_floats(rows) > ctx->tp_cap)
         return fail(NC_EINVAL, "nc_debug_temperature_paths: bad arguments");
@@ -1685,6 +1778,7 @@ void nc_session_free(nc_session* s) {
         (void)hipEventDestroy(e.first);
         (void)hipEventDestroy(e.second);
     }
+    for (auto& g : s->graphs) (void)hipGraphExecDestroy(g.second);
     for (void* p : s->allocs) (void)hipFree(p);
     for (void* p : {(void*)s->h_toks, (void*)s->h_preds, (void*)s->h_result, (void*)s->h_pos})
         if (p) (void)hipHostFree(p);

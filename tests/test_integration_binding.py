@@ -33,7 +33,7 @@ RUST_NAMES = {"i8": "i8", "u8": "u8", "i16": "i16", "u16": "u16", "i32": "i32", 
 LEFT_OUT = {"nc_generate_speculative_oracle", "nc_synth_size", "nc_synth_write", "nc_uniform_prompt",
             "nc_oracle_draft", "nc_bench_matmul", "nc_session_kernel_timing", "nc_session_timing_enable",
             "nc_debug_expf", "nc_session_fill_kv", "nc_synth_kv_values", "nc_session_stage_timing",
-            "nc_debug_temperature_paths"}
+            "nc_debug_temperature_paths", "nc_debug_pass_graphs"}
 
 
 def _strip_c_comments(text):
