@@ -1656,11 +1656,9 @@ int launch_k16(const QMatDev& w, const GemmParams& p, hipStream_t st, hipEvent_t
                 NC_LAUNCH((gemm_q4_k_ps_kernel<NMAX, QL, TPG>), grid, block, 0, st, p);
         };
         // NC_Q4K_PS=<1..4>: tuning override, plain matrices on the pair-split kernel with that many
-        // quad lanes (each width ran the Q4_K matmul tests bit-exact)
-        static const int forced = [] {
-            const char* e = getenv("NC_Q4K_PS");
-            return e ? atoi(e) : 0;
-        }();
+        // quad lanes; read at each launch, so a sweep or a test can switch it within a process
+        const char* ps_env = getenv("NC_Q4K_PS");
+        const int forced = ps_env ? atoi(ps_env) : 0;
         if (p.epi == EPI_SWIGLU_Q8) {
             if (p.ntiles % 4) return fail(NC_EINVAL, "gemm: interleaved gate,up needs whole 64-row groups");
             ps.template operator()<1, 4>();

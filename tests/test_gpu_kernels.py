@@ -200,6 +200,23 @@ def test_q4_k_wave_splits(ctx, shape, N):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("lanes", [1, 2, 3, 4])
+def test_q4_k_pair_split_override_bit_exact(ctx, lanes, monkeypatch):
+    """NC_Q4K_PS=<1..4>, the tuning override that runs plain 16-row-tile Q4_K matrices on the
+    pair-split kernel with that many quad lanes (read at each launch): outputs bit-exact at the
+    widths that kernel serves (1..9) on one quad of super-blocks, a partial last quad, a partial
+    last tile and more tiles than CUs."""
+    import nanocamelid_amd as nc
+    monkeypatch.setenv("NC_Q4K_PS", str(lanes))
+    for M, K in ((192, 1024), (130, 1280), (130, 2048), (4200, 3072)):
+        w = random_q4_k(M, K, seed=M + K + lanes)
+        for N in (1, 5, 9):
+            _, xq, xs = q8_activations(N, K, seed=600 + N + lanes)
+            out, _ = _run_gemm(ctx, nc.NC_TYPE_Q4_K, w, M, K, xq, xs)
+            ref = O.matmul_q4_k(xq, xs, w, N, M, K, nthreads=16)
+            assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (M, K, N)
+
+
 @pytest.mark.parametrize("shape", [(130, 1280), (16400, 1024)], ids=["r16k-partial-quad", "r64-large"])
 @pytest.mark.parametrize("N", [1, 5, 16])
 def test_q4_k_layouts(ctx, shape, N):
