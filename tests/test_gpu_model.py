@@ -503,6 +503,33 @@ def test_long_context_many_units(ctx):
         pos = c
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_long_prompt_many_unit_tiers_vs_oracle(ctx, hd):
+    """A 4300-token prompt on a two-layer model with 8 query heads: its prompt passes run the
+    attention of 64-row groups (512 (row, head) units) through the one-kernel tiers, then the
+    256-thread softmax tiers at up to 2048, 4096 and 8192 positions with the software-pipelined
+    weighted-V loop.  Layer 0's attention outputs feed layer 1's keys and values, so a 9-row
+    verify at 4300 whose every logit is bit-identical to the oracle's (16-token chunks) pins
+    those tiers."""
+    import nanocamelid_amd as nc
+    spec = dict(layers=2, embedding_length=8 * hd, head_count=8, head_count_kv=2, feed_forward_length=512,
+                vocab_size=1000, context_length=4400, tied=1, norm_mode=1)
+    _, gm, om = _models(ctx, spec, seed=4300 + hd)
+    n = 4300
+    prompt = nc.uniform_prompt(4300 + hd, n, 1000)
+    gs, os_ = nc.Session(gm, n + 16, 16), O.Session(om, n + 16, 16)
+    print(f"long prompt hd={hd}: {n} tokens in prompt passes", flush=True)
+    gs.prefill_pass_batch(prompt, 0, want_logits=False)
+    for i in range(0, n, 16):
+        os_.prefill_pass_batch(prompt[i:min(i + 16, n)], i)
+    batch = nc.uniform_prompt(n, 9, 1000)
+    _, _, _, preds = gs.verify_greedy(batch, n)
+    opreds, _, ologits = os_.verify_greedy(batch, n, want_logits=True)
+    assert np.array_equal(preds, opreds)
+    for i in range(9):
+        assert _same(gs.logits(i), ologits[i]), i
+
+
 def test_long_context_many_units_past_8192(ctx):
     """9 rows x 32 heads (288 units) at 8193..8201 positions take the 256-thread tier with one
     extra position per thread (its e joins the exact chain after the first 8192): every verify
