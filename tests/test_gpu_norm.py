@@ -51,7 +51,7 @@ def _rows(d, rng):
     return {k: v.astype(np.float32) for k, v in rows.items()}
 
 
-@pytest.mark.parametrize("d", [256, 512, 768, 1024, 2048, 3072, 4096, 8192])
+@pytest.mark.parametrize("d", [256, 512, 768, 1024, 1536, 2048, 3072, 4096, 5120, 6144, 8192])
 def test_rms_norm_q8_bit_exact(ctx, d):
     import nanocamelid_amd as nc
     rng = np.random.default_rng(d)
